@@ -1,0 +1,209 @@
+"""TEST INFRASTRUCTURE ONLY -- ctypes view of the C restatement in attn_oracle.c.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module,
+and only as the checker; the product path (llmplayer_amd/) never touches it.
+
+Every function wraps the C function of the same name, which cites the reference Java code it
+restates (Attention.java, KVCache.java, RoPE.java, SimdVectorOps.java, ScalarOps.java under
+/root/reference/src/main/).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libattn_oracle.so")
+_lib = None
+
+ARCH_OTHER, ARCH_GEMMA2, ARCH_GEMMA3, ARCH_GPT_OSS, ARCH_COHERE2 = 0, 1, 2, 3, 4
+ROPE_NORMAL, ROPE_NEOX = 0, 2
+
+
+def build(force: bool = False) -> str:
+    """Compile libattn_oracle.so with the committed Makefile."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-B", "-C", _HERE], check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+class _Cfg(C.Structure):
+    _fields_ = [
+        ("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("head_size", C.c_int),
+        ("rope_dim", C.c_int), ("rope_type", C.c_int), ("max_seq", C.c_int),
+        ("norm_eps", C.c_float), ("sliding_window", C.c_int),
+        ("attention_scale", C.c_float), ("softcap", C.c_float), ("arch", C.c_int),
+        ("no_rope_interval", C.c_int), ("nope_on_global", C.c_int),
+    ]
+
+
+@dataclass
+class OracleConfig:
+    """Attention hyper-parameters read by Attention.forwardFromProjections."""
+    n_heads: int
+    n_kv_heads: int
+    head_size: int
+    max_seq: int
+    rope_type: int = ROPE_NORMAL
+    rope_dim: int = 0          # 0 -> head_size
+    norm_eps: float = 1e-5
+    sliding_window: int = 0
+    attention_scale: float = 0.0
+    softcap: float = 0.0
+    arch: int = ARCH_OTHER
+    no_rope_interval: int = 0
+    nope_on_global: bool = False
+
+    def c(self) -> _Cfg:
+        return _Cfg(self.n_heads, self.n_kv_heads, self.head_size,
+                    self.rope_dim or self.head_size, self.rope_type, self.max_seq,
+                    self.norm_eps, self.sliding_window, self.attention_scale, self.softcap,
+                    self.arch, self.no_rope_interval, int(self.nope_on_global))
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_kv_heads * self.head_size
+
+
+_F = C.POINTER(C.c_float)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        build()
+        L = C.CDLL(_LIB_PATH)
+        L.orc_dot.restype = C.c_float
+        L.orc_dot.argtypes = [_F, _F, C.c_int]
+        L.orc_saxpy.argtypes = [C.c_float, _F, _F, C.c_int]
+        L.orc_softmax.argtypes = [_F, C.c_int]
+        L.orc_per_head_norm.argtypes = [_F, _F, C.c_int, C.c_int, C.c_float]
+        L.orc_rope_tables.argtypes = [C.c_int, C.c_int, C.c_float, C.c_float, _F, C.c_int, _F, _F]
+        L.orc_rope_apply_all.argtypes = [_F, C.c_int, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int]
+        L.orc_is_global_layer.restype = C.c_int
+        L.orc_is_global_layer.argtypes = [C.c_int, C.c_int]
+        L.orc_start_pos.restype = C.c_int
+        L.orc_start_pos.argtypes = [C.POINTER(_Cfg), C.c_int, C.c_int]
+        L.orc_forward_from_projections.argtypes = [
+            C.POINTER(_Cfg), _F, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int, _F, _F,
+            C.c_int, C.c_int]
+        L.orc_prefill_sequential.argtypes = [
+            C.POINTER(_Cfg), _F, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int, C.c_int,
+            _F, C.c_int]
+        L.orc_max_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_F)
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def dot(a, b) -> np.float32:
+    a, b = f32(a), f32(b)
+    return np.float32(lib().orc_dot(_p(a), _p(b), a.size))
+
+
+def saxpy(alpha, x, y) -> np.ndarray:
+    x, y = f32(x), f32(y).copy()
+    lib().orc_saxpy(float(np.float32(alpha)), _p(x), _p(y), x.size)
+    return y
+
+
+def softmax(x) -> np.ndarray:
+    x = f32(x).copy()
+    lib().orc_softmax(_p(x), x.size)
+    return x
+
+
+def per_head_norm(vec, w, n_heads, head_size, eps) -> np.ndarray:
+    vec, w = f32(vec).copy(), f32(w)
+    lib().orc_per_head_norm(_p(vec), _p(w), n_heads, head_size, float(np.float32(eps)))
+    return vec
+
+
+def rope_tables(rope_dim, max_seq, theta, linear_freq_scale=1.0, freq_factors=None):
+    half = rope_dim // 2
+    cos_t = np.zeros((max_seq, half), np.float32)
+    sin_t = np.zeros((max_seq, half), np.float32)
+    ff = f32(freq_factors) if freq_factors is not None else None
+    lib().orc_rope_tables(rope_dim, max_seq, float(np.float32(theta)),
+                          float(np.float32(linear_freq_scale)), _p(ff),
+                          0 if ff is None else ff.size, _p(cos_t), _p(sin_t))
+    return cos_t, sin_t
+
+
+def rope_apply_all(vec, n_heads, head_size, rope_dim, rope_type, cos_t, sin_t, pos):
+    vec = f32(vec).copy()
+    lib().orc_rope_apply_all(_p(vec), n_heads, head_size, rope_dim, rope_type,
+                             _p(f32(cos_t)), _p(f32(sin_t)), pos)
+    return vec
+
+
+def is_global_layer(arch, layer) -> bool:
+    return bool(lib().orc_is_global_layer(arch, layer))
+
+
+def start_pos(cfg: OracleConfig, layer, pos) -> int:
+    c = cfg.c()
+    return lib().orc_start_pos(C.byref(c), layer, pos)
+
+
+def forward_from_projections(cfg: OracleConfig, kcache, vcache, q, k, v, layer, pos,
+                             qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None,
+                             use_flash=False, n_threads=1):
+    """Runs Attention.forwardFromProjections for one layer-call.
+
+    kcache/vcache: float32 [max_seq, kvDim] (the reference layout), modified in place (the
+    new K/V rows are appended at `pos`).  Returns (out[Hq*D], q_after, k_after): q and k
+    after QK-norm and RoPE, as state.q / state.k hold them after the call."""
+    c = cfg.c()
+    q, k, v = f32(q).copy(), f32(k).copy(), f32(v)
+    assert kcache.dtype == np.float32 and kcache.flags["C_CONTIGUOUS"]
+    assert vcache.dtype == np.float32 and vcache.flags["C_CONTIGUOUS"]
+    assert kcache.size >= cfg.max_seq * cfg.kv_dim and vcache.size >= cfg.max_seq * cfg.kv_dim
+    assert 0 <= pos < cfg.max_seq
+    out = np.zeros(cfg.n_heads * cfg.head_size, np.float32)
+    att = np.zeros(cfg.n_heads * (pos + 1), np.float32)
+    lib().orc_forward_from_projections(
+        C.byref(c), _p(kcache), _p(vcache),
+        _p(f32(qnorm_w)) if qnorm_w is not None else None,
+        _p(f32(knorm_w)) if knorm_w is not None else None,
+        _p(f32(rope_cos)) if rope_cos is not None else None,
+        _p(f32(rope_sin)) if rope_sin is not None else None,
+        _p(q), _p(k), _p(v), layer, pos, _p(out), _p(att), int(use_flash), int(n_threads))
+    return out, q, k
+
+
+def prefill_sequential(cfg: OracleConfig, kcache, vcache, q, k, v, layer, pos0,
+                       qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1):
+    """P sequential single-token calls (the reference's prefill).  q: [P, Hq*D],
+    k/v: [P, kvDim].  Returns out [P, Hq*D]; the caches gain rows pos0..pos0+P-1."""
+    c = cfg.c()
+    q, k, v = f32(q), f32(k), f32(v)
+    P = q.shape[0]
+    assert pos0 + P <= cfg.max_seq
+    out = np.zeros((P, cfg.n_heads * cfg.head_size), np.float32)
+    lib().orc_prefill_sequential(
+        C.byref(c), _p(kcache), _p(vcache),
+        _p(f32(qnorm_w)) if qnorm_w is not None else None,
+        _p(f32(knorm_w)) if knorm_w is not None else None,
+        _p(f32(rope_cos)) if rope_cos is not None else None,
+        _p(f32(rope_sin)) if rope_sin is not None else None,
+        _p(q), _p(k), _p(v), layer, pos0, P, _p(out), int(n_threads))
+    return out
+
+
+def max_threads() -> int:
+    return lib().orc_max_threads()

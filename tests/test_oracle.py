@@ -1,0 +1,356 @@
+"""Pins the CPU restatement (oracle/attn_oracle.c) before it is trusted as the checker.
+
+The reference ships no tests or golden vectors for this path and its Java cannot run here,
+so each oracle function is pinned by what the mathematics fixes: closed forms, invariants,
+special cases that reduce to a textbook routine, and float64 brute force on small shapes.
+Each check is chosen so that a plausible slip (dropped FMA, wrong pair index, eps in the
+wrong place, wrong GQA mapping, off-by-one window) fails it.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import refmath as rm
+
+F32 = np.float32
+
+
+# ---------------------------------------------------------------- SimdVectorOps.dot / saxpy
+def test_dot_integer_closed_form():
+    for n in (1, 7, 8, 9, 16, 64, 100, 128, 256):
+        a = np.arange(1, n + 1, dtype=F32)
+        assert orc.dot(a, np.ones(n, F32)) == F32(n * (n + 1) / 2)
+        assert orc.dot(a, a) == F32(n * (n + 1) * (2 * n + 1) / 6)
+
+
+def test_dot_uses_fma_on_lanes_and_plain_mul_add_on_tail():
+    # x*x with x = 1 + 2^-12 is 1 + 2^-11 + 2^-24, which is not a float: a fused
+    # multiply-add keeps the 2^-24, an unfused one rounds it away (Vector.fma vs a*b+c).
+    x = F32(1 + 2.0 ** -12)
+    m = F32(-(1 + 2.0 ** -11))
+    a = np.zeros(16, F32); b = np.zeros(16, F32)
+    a[0], b[0] = m, F32(1)          # lane 0 first term
+    a[8], b[8] = x, x               # lane 0 second term -> fma keeps 2^-24
+    assert orc.dot(a, b) == F32(2.0 ** -24)
+    # tail element (index 8 of a 9-vector) uses a separate multiply and add
+    a9 = np.zeros(9, F32); b9 = np.zeros(9, F32)
+    a9[0], b9[0] = m, F32(1)
+    a9[8], b9[8] = x, x
+    assert orc.dot(a9, b9) == F32(0.0)
+
+
+def test_dot_matches_float64():
+    rng = np.random.default_rng(1)
+    for n in (64, 128, 256, 77):
+        a = rng.standard_normal(n).astype(F32)
+        b = rng.standard_normal(n).astype(F32)
+        want = float(a.astype(np.float64) @ b.astype(np.float64))
+        assert abs(float(orc.dot(a, b)) - want) < 1e-5 * n
+
+
+def test_saxpy_fused_on_lanes():
+    x = np.full(8, F32(1 + 2.0 ** -12), F32)
+    y = np.full(8, F32(-(1 + 2.0 ** -11)), F32)
+    out = orc.saxpy(F32(1 + 2.0 ** -12), x, y)
+    assert np.all(out == F32(2.0 ** -24))
+    out9 = orc.saxpy(F32(1 + 2.0 ** -12), np.full(9, x[0], F32), np.full(9, y[0], F32))
+    assert out9[8] == F32(0.0) and out9[0] == F32(2.0 ** -24)
+
+
+# ------------------------------------------------------------------------- softmax
+def test_softmax_closed_forms():
+    assert np.all(orc.softmax(np.zeros(10, F32)) == F32(0.1))
+    assert orc.softmax(np.array([3.5], F32))[0] == F32(1.0)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(1000).astype(F32) * 4
+    got = orc.softmax(x)
+    e = np.exp(x.astype(np.float64) - x.max())
+    np.testing.assert_allclose(got, e / e.sum(), rtol=2e-6, atol=1e-9)
+    assert abs(got.astype(np.float64).sum() - 1) < 1e-5
+    # argmax kept, ordering kept
+    assert np.argmax(got) == np.argmax(x)
+    assert np.all(np.diff(got[np.argsort(x)]) >= 0)
+
+
+# --------------------------------------------------------------------- QK-norm
+def test_per_head_norm_constant_vector_is_sign():
+    D = 128
+    x = np.concatenate([np.full(D, 3.0, F32), np.full(D, -0.25, F32)])
+    out = orc.per_head_norm(x, np.ones(D, F32), 2, D, 0.0)
+    np.testing.assert_allclose(out[:D], 1.0, rtol=2e-7)
+    np.testing.assert_allclose(out[D:], -1.0, rtol=2e-7)
+
+
+def test_per_head_norm_power_of_two_scale_invariance_is_exact():
+    rng = np.random.default_rng(3)
+    D = 128
+    x = rng.standard_normal(4 * D).astype(F32)
+    w = rng.uniform(0.5, 1.5, D).astype(F32)
+    base = orc.per_head_norm(x, w, 4, D, 0.0)
+    for k in (-6, -1, 3, 10):
+        assert np.array_equal(orc.per_head_norm(x * F32(2.0 ** k), w, 4, D, 0.0), base)
+
+
+def test_per_head_norm_matches_float64_with_eps_and_weights():
+    rng = np.random.default_rng(4)
+    for D, H, eps in ((128, 16, 1e-6), (256, 4, 1e-6), (64, 3, 0.5)):
+        x = (rng.standard_normal(H * D) * rng.uniform(0.01, 3, H).repeat(D)).astype(F32)
+        w = rng.uniform(0.5, 1.5, D).astype(F32)
+        got = orc.per_head_norm(x, w, H, D, eps)
+        want = rm.rms_norm_heads(x, w, H, D, eps)
+        np.testing.assert_allclose(got, want, rtol=3e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------------ RoPE
+@pytest.mark.parametrize("R,theta", [(64, 5e5), (128, 1e6), (256, 1e4), (128, 5e5)])
+def test_rope_tables_match_angle_definition(R, theta):
+    S = 2048
+    cos_t, sin_t = orc.rope_tables(R, S, theta)
+    assert np.all(cos_t[0] == 1) and np.all(sin_t[0] == 0)
+    i = np.arange(R // 2)
+    freq = (1.0 / np.power(np.float64(F32(theta)), 2.0 * i / R)).astype(F32)
+    ang = (np.arange(S, dtype=F32)[:, None] * freq[None, :]).astype(F32)
+    # float32 angle as the reference forms it, then cos/sin in double -> float
+    np.testing.assert_array_max_ulp(cos_t, np.cos(ang.astype(np.float64)).astype(F32), 1)
+    np.testing.assert_array_max_ulp(sin_t, np.sin(ang.astype(np.float64)).astype(F32), 1)
+    # pair 0 rotates by exactly `pos` radians
+    np.testing.assert_allclose(cos_t[:, 0], np.cos(np.arange(S)), atol=2e-7)
+
+
+def test_rope_linear_scale_divides_frequencies():
+    R, S = 128, 64
+    c1, s1 = orc.rope_tables(R, S * 8, 1e4)
+    c8, s8 = orc.rope_tables(R, S * 8, 1e4, linear_freq_scale=8.0)
+    # angle(pos*8, scale 8) == angle(pos, 1) up to float rounding of freq/8
+    np.testing.assert_allclose(c8[::8][:S], c1[:S], atol=2e-5)
+    np.testing.assert_allclose(s8[::8][:S], s1[:S], atol=2e-5)
+
+
+@pytest.mark.parametrize("rope_type", [0, 2])
+def test_rope_apply_identity_at_pos0_and_pairing(rope_type):
+    H, D, R = 3, 64, 64
+    cos_t, sin_t = orc.rope_tables(R, 16, 5e5)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(H * D).astype(F32)
+    assert np.array_equal(orc.rope_apply_all(x, H, D, R, rope_type, cos_t, sin_t, 0), x)
+    # one-hot on the first element of each pair lands on (cos, sin) at the partner index
+    half = R // 2
+    for i in (0, 1, 5, half - 1):
+        e = np.zeros(H * D, F32)
+        i0 = 2 * i if rope_type == 0 else i
+        i1 = 2 * i + 1 if rope_type == 0 else half + i
+        e[D + i0] = 1.0
+        out = orc.rope_apply_all(e, H, D, R, rope_type, cos_t, sin_t, 7)
+        assert out[D + i0] == cos_t[7, i] and out[D + i1] == sin_t[7, i]
+        out[D + i0] = 0; out[D + i1] = 0
+        assert not out.any()
+
+
+@pytest.mark.parametrize("rope_type", [0, 2])
+def test_rope_apply_matches_rotation_and_preserves_pair_norms(rope_type):
+    H, D, R, theta = 4, 128, 128, 1e6
+    S = 4096
+    cos_t, sin_t = orc.rope_tables(R, S, theta)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(H * D).astype(F32)
+    for pos in (1, 17, 4095):
+        got = orc.rope_apply_all(x, H, D, R, rope_type, cos_t, sin_t, pos)
+        want = rm.rope_rotate(x, H, D, R, rope_type, rm.rope_angles(R, pos, float(F32(theta))))
+        np.testing.assert_allclose(got, want, atol=3e-6)
+        # rotation back by the same angle (sin negated) recovers x
+        back = orc.rope_apply_all(got, H, D, R, rope_type, cos_t, -sin_t, pos)
+        np.testing.assert_allclose(back, x, atol=2e-6)
+        half = R // 2
+        xx = x.reshape(H, D); gg = got.reshape(H, D)
+        if rope_type == 0:
+            n0 = xx[:, 0::2] ** 2 + xx[:, 1::2] ** 2; n1 = gg[:, 0::2] ** 2 + gg[:, 1::2] ** 2
+        else:
+            n0 = xx[:, :half] ** 2 + xx[:, half:] ** 2; n1 = gg[:, :half] ** 2 + gg[:, half:] ** 2
+        np.testing.assert_allclose(n1, n0, rtol=3e-6, atol=1e-7)
+
+
+def test_partial_rope_leaves_tail_untouched():
+    H, D, R = 2, 128, 64
+    cos_t, sin_t = orc.rope_tables(R, 32, 1e4)
+    x = np.random.default_rng(7).standard_normal(H * D).astype(F32)
+    out = orc.rope_apply_all(x, H, D, R, 2, cos_t, sin_t, 9).reshape(H, D)
+    assert np.array_equal(out[:, R:], x.reshape(H, D)[:, R:])
+
+
+def test_global_layer_patterns():
+    g3 = [orc.is_global_layer(orc.ARCH_GEMMA3, l) for l in range(26)]
+    assert [l for l in range(26) if g3[l]] == [5, 11, 17, 23]
+    assert [orc.is_global_layer(orc.ARCH_GEMMA2, l) for l in range(4)] == [False, True, False, True]
+    assert [orc.is_global_layer(orc.ARCH_GPT_OSS, l) for l in range(4)] == [True, False, True, False]
+    assert [orc.is_global_layer(orc.ARCH_COHERE2, l) for l in range(8)] == [
+        False, False, False, True, False, False, False, True]
+    assert all(orc.is_global_layer(orc.ARCH_OTHER, l) for l in range(8))
+
+
+# ------------------------------------------------------------ full attention layer-call
+def _setup(cfg, pos, seed, k_scale=1.0, theta=5e5):
+    rng = np.random.default_rng(seed)
+    kv = cfg.kv_dim
+    kc = np.zeros((cfg.max_seq, kv), F32); vc = np.zeros((cfg.max_seq, kv), F32)
+    kc[:pos] = rng.standard_normal((pos, kv)).astype(F32) * F32(k_scale)
+    vc[:pos] = rng.standard_normal((pos, kv)).astype(F32)
+    q = rng.standard_normal(cfg.n_heads * cfg.head_size).astype(F32)
+    k = (rng.standard_normal(kv) * k_scale).astype(F32)
+    v = rng.standard_normal(kv).astype(F32)
+    cos_t, sin_t = orc.rope_tables(cfg.rope_dim or cfg.head_size, cfg.max_seq, theta)
+    return kc, vc, q, k, v, cos_t, sin_t
+
+
+def test_pos0_output_is_v0():
+    # DiagnosticRunner.java:367-385: at pos=0 attention output = V directly
+    cfg = orc.OracleConfig(32, 8, 64, 16)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 0, 10)
+    out, _, _ = orc.forward_from_projections(cfg, kc, vc, q, k, v, 0, 0, rope_cos=cs, rope_sin=sn)
+    want = np.repeat(v.reshape(8, 64), 4, axis=0).reshape(-1)
+    assert np.array_equal(out, want)
+
+
+def test_uniform_scores_give_mean_of_v():
+    cfg = orc.OracleConfig(24, 8, 128, 300)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 257, 11)
+    q[:] = 0
+    out, _, _ = orc.forward_from_projections(cfg, kc, vc, q, k, v, 0, 257, rope_cos=cs, rope_sin=sn)
+    mean = vc[:258].astype(np.float64).mean(axis=0).reshape(8, 128)
+    np.testing.assert_allclose(out.reshape(24, 128), np.repeat(mean, 3, axis=0), atol=2e-6)
+
+
+def test_dominant_score_selects_row_and_gqa_mapping():
+    Hq, Hkv, D = 8, 2, 64
+    cfg = orc.OracleConfig(Hq, Hkv, D, 64)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 40, 12)
+    # no RoPE so that K rows line up with q directly
+    q = np.zeros(Hq * D, F32); q[::D] = 1.0  # every head looks along dim 0
+    kc[:40] = 0; k[:] = 0
+    kc[13, 0] = 1000.0         # kv head 0 strongly prefers t=13
+    kc[29, D] = 1000.0         # kv head 1 strongly prefers t=29
+    out, _, _ = orc.forward_from_projections(cfg, kc, vc, q, k, v, 0, 40)
+    o = out.reshape(Hq, D)
+    for h in range(Hq):
+        kh = h // (Hq // Hkv)
+        t = 13 if kh == 0 else 29
+        np.testing.assert_allclose(o[h], vc[t, kh * D:(kh + 1) * D], atol=1e-5)
+
+
+def test_gqa_heads_read_their_own_kv_head():
+    Hq, Hkv, D = 12, 4, 64
+    cfg = orc.OracleConfig(Hq, Hkv, D, 32)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 20, 13)
+    for kh in range(Hkv):
+        vc[:, kh * D:(kh + 1) * D] = kh + 1
+        v[kh * D:(kh + 1) * D] = kh + 1
+    out, _, _ = orc.forward_from_projections(cfg, kc, vc, q, k, v, 0, 20, rope_cos=cs, rope_sin=sn)
+    o = out.reshape(Hq, D)
+    for h in range(Hq):
+        np.testing.assert_allclose(o[h], h // 3 + 1, rtol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(4, 1, 256, 2), (32, 8, 64, 4), (16, 8, 128, 0), (24, 8, 128, 0)])
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_layer_call_matches_float64_brute_force(shape, qk_norm):
+    Hq, Hkv, D, rtype = shape
+    pos = 63
+    cfg = orc.OracleConfig(Hq, Hkv, D, 64, rope_type=rtype, norm_eps=1e-6)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, pos, 14, k_scale=0.5, theta=1e6)
+    rng = np.random.default_rng(15)
+    qw = rng.uniform(0.5, 1.5, D).astype(F32) if qk_norm else None
+    kw = rng.uniform(0.5, 1.5, D).astype(F32) if qk_norm else None
+    kc0 = kc.copy(); vc0 = vc.copy()
+    out, q2, k2 = orc.forward_from_projections(cfg, kc, vc, q, k, v, 0, pos, qnorm_w=qw,
+                                               knorm_w=kw, rope_cos=cs, rope_sin=sn)
+    # float64 chain: norm -> rotate -> append -> softmax attention
+    qq = rm.rms_norm_heads(q, qw, Hq, D, 1e-6) if qk_norm else q.astype(np.float64)
+    kk = rm.rms_norm_heads(k, kw, Hkv, D, 1e-6) if qk_norm else k.astype(np.float64)
+    ang = rm.rope_angles(D, pos, float(F32(1e6)))
+    qq = rm.rope_rotate(qq, Hq, D, D, rtype, ang)
+    kk = rm.rope_rotate(kk, Hkv, D, D, rtype, ang)
+    np.testing.assert_allclose(q2, qq, atol=2e-5)
+    np.testing.assert_allclose(k2, kk, atol=2e-5)
+    K = kc0.astype(np.float64); V = vc0.astype(np.float64)
+    K[pos] = kk; V[pos] = v
+    want = rm.attention(qq, K, V, Hq, Hkv, D, 0, pos, 1 / np.sqrt(D))
+    rm.assert_close(out, want, atol=2e-5, rtol=1e-4, what="oracle vs fp64")
+    # append: row pos holds the rotated k / raw v bit-for-bit, nothing else changed
+    assert np.array_equal(kc[pos], k2) and np.array_equal(vc[pos], v)
+    kc[pos] = kc0[pos]; vc[pos] = vc0[pos]
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+
+
+def test_flash_equals_two_pass():
+    cfg = orc.OracleConfig(24, 8, 128, 1100)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 1023, 16, k_scale=0.5)
+    a, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 0, 1023,
+                                           rope_cos=cs, rope_sin=sn)
+    b, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 0, 1023,
+                                           rope_cos=cs, rope_sin=sn, use_flash=True)
+    np.testing.assert_allclose(a, b, atol=2e-6)
+
+
+def test_threads_do_not_change_results():
+    cfg = orc.OracleConfig(24, 8, 128, 600)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 511, 17)
+    a, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 0, 511,
+                                           rope_cos=cs, rope_sin=sn, n_threads=1)
+    b, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 0, 511,
+                                           rope_cos=cs, rope_sin=sn, n_threads=4)
+    assert np.array_equal(a, b)
+
+
+def test_softcap_matches_float64():
+    cfg = orc.OracleConfig(8, 2, 64, 100, softcap=5.0)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 80, 18, k_scale=3.0)
+    kc0 = kc.copy(); vc0 = vc.copy()
+    out, q2, k2 = orc.forward_from_projections(cfg, kc, vc, q, k, v, 0, 80)
+    K = kc0.astype(np.float64); V = vc0.astype(np.float64); K[80] = k; V[80] = v
+    want = rm.attention(q, K, V, 8, 2, 64, 0, 80, 1 / 8.0, softcap=5.0)
+    rm.assert_close(out, want, atol=2e-5, rtol=1e-4, what="softcap")
+
+
+@pytest.mark.parametrize("pos", [100, 510, 511, 512, 513, 900])
+def test_sliding_window_boundaries(pos):
+    W = 512
+    cfg = orc.OracleConfig(4, 1, 256, 1024, sliding_window=W, arch=orc.ARCH_GEMMA3)
+    start = max(0, pos - W + 1)
+    assert orc.start_pos(cfg, 0, pos) == start          # local layer
+    assert orc.start_pos(cfg, 5, pos) == 0              # global layer (5 % 6 == 5)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, pos, 19)
+    vc_poison = vc.copy(); vc_poison[:start] = 1e6       # rows outside the window
+    a, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 0, pos)
+    b, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc_poison, q, k, v, 0, pos)
+    assert np.array_equal(a, b)
+    K = kc.astype(np.float64); V = vc.astype(np.float64); K[pos] = k; V[pos] = v
+    want = rm.attention(q, K, V, 4, 1, 256, start, pos, 1 / 16.0)
+    rm.assert_close(a, want, atol=2e-5, rtol=1e-4, what="window")
+
+
+def test_nope_layer_skips_rotation():
+    cfg = orc.OracleConfig(8, 2, 64, 32, no_rope_interval=4)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 10, 20)
+    _, q3, k3 = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 3, 10,
+                                             rope_cos=cs, rope_sin=sn)
+    assert np.array_equal(q3, q) and np.array_equal(k3, k)
+    _, q2, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 2, 10,
+                                            rope_cos=cs, rope_sin=sn)
+    assert not np.array_equal(q2, q)
+
+
+def test_prefill_equals_sequential_decode_calls():
+    cfg = orc.OracleConfig(8, 2, 64, 64)
+    rng = np.random.default_rng(21)
+    P = 20
+    q = rng.standard_normal((P, 8 * 64)).astype(F32)
+    k = rng.standard_normal((P, 128)).astype(F32)
+    v = rng.standard_normal((P, 128)).astype(F32)
+    cs, sn = orc.rope_tables(64, 64, 5e5)
+    kc1 = np.zeros((64, 128), F32); vc1 = np.zeros((64, 128), F32)
+    out = orc.prefill_sequential(cfg, kc1, vc1, q, k, v, 0, 0, rope_cos=cs, rope_sin=sn)
+    kc2 = np.zeros((64, 128), F32); vc2 = np.zeros((64, 128), F32)
+    for i in range(P):
+        o, _, _ = orc.forward_from_projections(cfg, kc2, vc2, q[i], k[i], v[i], 0, i,
+                                               rope_cos=cs, rope_sin=sn)
+        assert np.array_equal(out[i], o)
+    assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
