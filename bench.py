@@ -1,0 +1,232 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X (BASELINE.json metric).
+
+A step is one decode attention layer-call (QK-norm/RoPE prep, KV append, split-K
+QK^T/softmax/PV and the log-sum-exp combine) at the Llama-3.2-3B head shape (24 query heads,
+8 KV heads, head_dim 128, fp32 KV) for one new token at position ctx-1.  Successive steps
+rotate over enough layer caches (>= 2 GiB) that every step reads its KV from HBM rather than
+the 256 MB Infinity Cache.  Inputs are synthetic N(0,1) (K x 0.5) and resident in HBM before
+the timed region.
+
+value = KV-read GB/s = (2 * ctx * Hkv * D * 4 bytes) / (time per layer-call), whole region.
+roofline.achieved = the same bytes / the split-K kernel's mean duration (HIP events around
+each launch, on the library stream the kernel runs on).
+cpu_baseline = the CPU restatement of the reference's Java attention (oracle/, parallel over
+query heads like Attention.java:343), timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBPS = 8000.0            # MI355X HBM3E peak
+HQ, HKV, D = 24, 8, 128       # Llama-3.2-3B head shape
+THETA = 500000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def kv_bytes(ctx: int) -> int:
+    return 2 * ctx * HKV * D * 4
+
+
+def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int) -> dict:
+    from llmplayer_amd import _lib
+    from llmplayer_amd import hip_forward_pass as hfp
+
+    per_layer = kv_bytes(ctx)
+    n_layers = max(1, math.ceil(rotate_bytes / per_layer))
+    c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
+    log(f"[bench] ctx {ctx}: {n_layers} layer caches x {per_layer / 2**20:.0f} MiB")
+    fp = hfp.HipForwardPass(c, ctx)
+    try:
+        rng = np.random.default_rng(2024)
+        kc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32) * np.float32(0.5)
+        vc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32)
+        for layer in range(n_layers):
+            fp.kv.write(layer, 0, kc, vc)
+        del kc, vc
+        fp.uploadQKV(rng.standard_normal(c.q_dim, dtype=np.float32),
+                     rng.standard_normal(c.kv_dim, dtype=np.float32) * np.float32(0.5),
+                     rng.standard_normal(c.kv_dim, dtype=np.float32))
+        pos = ctx - 1
+        for i in range(warmup):
+            fp.forwardAttentionPart(i % n_layers, pos, splits)
+        fp.sync()
+        h = fp.kv.handle
+        _lib.call("llmp_profile_reset", h)
+        _lib.call("llmp_profile_enable", h, 1)
+        e0, e1 = C.c_uint64(), C.c_uint64()
+        _lib.call("llmp_event_create", C.byref(e0))
+        _lib.call("llmp_event_create", C.byref(e1))
+        _lib.call("llmp_event_record", e0.value, 0)
+        for i in range(steps):
+            fp.forwardAttentionPart(i % n_layers, pos, splits)
+        _lib.call("llmp_event_record", e1.value, 0)
+        _lib.call("llmp_event_sync", e1.value)
+        ms = C.c_float()
+        _lib.call("llmp_event_elapsed_ms", C.byref(ms), e0.value, e1.value)
+        _lib.call("llmp_profile_enable", h, 0)
+        res = {}
+        for kind, name in ((_lib.LLMP_PROF_DECODE_SPLIT, "split"),
+                           (_lib.LLMP_PROF_DECODE_REDUCE, "reduce")):
+            cnt, tot = C.c_int(), C.c_double()
+            _lib.call("llmp_profile_read", h, kind, C.byref(cnt), C.byref(tot))
+            res[name] = (cnt.value, tot.value)
+        _lib.call("llmp_event_destroy", e0.value)
+        _lib.call("llmp_event_destroy", e1.value)
+    finally:
+        fp.close()
+    ms_per_step = ms.value / steps
+    split_ms = res["split"][1] / max(1, res["split"][0])
+    reduce_ms = res["reduce"][1] / res["reduce"][0] if res["reduce"][0] else 0.0
+    return {"ctx": ctx, "n_layers": n_layers, "ms_per_step": ms_per_step,
+            "us_per_layer_call": ms_per_step * 1e3,
+            "kv_read_gbps": per_layer / (ms_per_step * 1e-3) / 1e9,
+            "split_kernel_us": split_ms * 1e3, "reduce_kernel_us": reduce_ms * 1e3,
+            "split_launches": res["split"][0]}
+
+
+def cpu_baseline(ctx: int, seconds: float) -> dict:
+    """The oracle (CPU restatement of Attention.forwardFromProjections) on one layer-call of
+    the same shape, parallel over query heads; median over a bounded sample."""
+    from oracle import oracle as orc
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    threads = max(1, min(16, avail))
+    oc = orc.OracleConfig(HQ, HKV, D, ctx, rope_type=0)
+    rng = np.random.default_rng(2024)
+    kc = np.zeros((ctx, HKV * D), np.float32)
+    vc = np.zeros((ctx, HKV * D), np.float32)
+    kc[:ctx - 1] = rng.standard_normal((ctx - 1, HKV * D), dtype=np.float32) * np.float32(0.5)
+    vc[:ctx - 1] = rng.standard_normal((ctx - 1, HKV * D), dtype=np.float32)
+    q = rng.standard_normal(HQ * D, dtype=np.float32)
+    k = rng.standard_normal(HKV * D, dtype=np.float32) * np.float32(0.5)
+    v = rng.standard_normal(HKV * D, dtype=np.float32)
+    cs, sn = orc.rope_tables(D, ctx, THETA)
+    for _ in range(2):
+        orc.forward_from_projections(oc, kc, vc, q, k, v, 0, ctx - 1, rope_cos=cs, rope_sin=sn,
+                                     n_threads=threads)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        orc.forward_from_projections(oc, kc, vc, q, k, v, 0, ctx - 1, rope_cos=cs, rope_sin=sn,
+                                     n_threads=threads)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": kv_bytes(ctx) / med / 1e9, "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{len(times)} layer-calls of the C3 shape at ctx {ctx} (median "
+                      f"{med * 1e6:.0f} us/layer-call), oracle/attn_oracle.c, {threads} threads "
+                      f"over query heads",
+            "us_per_layer_call": med * 1e6}
+
+
+def traffic_from_profiles(ctx: int):
+    """HBM bytes per launch of the split kernel from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), if present."""
+    path = os.path.join(ROOT, "profiles", f"decode_split_c3_ctx{ctx}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--ctx2", type=int, default=4096, help="second context reported (0 = none)")
+    ap.add_argument("--splits", type=int, default=0, help="split-K partitions (0 = library choice)")
+    ap.add_argument("--rotate-gib", type=float, default=2.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
+              "(decode attention runs on one MI355X; multi-GPU sharding is design-only)",
+              file=sys.stderr)
+        return 2
+    with open(os.path.join(ROOT, "BASELINE.json")) as f:
+        metric = json.load(f)["metric"]
+
+    from llmplayer_amd import hip_forward_pass as hfp
+    hfp.init(0)
+    info = hfp.device_info()
+    log(f"[bench] device {info['arch']} with {info['n_cu']} CUs")
+    rot = int(args.rotate_gib * 2**30)
+    main_run = gpu_run(args.ctx, args.steps, args.warmup, args.splits, rot)
+    log(f"[bench] ctx {args.ctx}: {main_run['us_per_layer_call']:.2f} us/layer-call, "
+        f"{main_run['kv_read_gbps']:.0f} GB/s, split kernel {main_run['split_kernel_us']:.2f} us")
+    second = None
+    if args.ctx2:
+        second = gpu_run(args.ctx2, args.steps, args.warmup, args.splits, rot)
+        log(f"[bench] ctx {args.ctx2}: {second['us_per_layer_call']:.2f} us/layer-call, "
+            f"{second['kv_read_gbps']:.0f} GB/s, split kernel {second['split_kernel_us']:.2f} us")
+
+    B = kv_bytes(args.ctx)
+    achieved = B / (main_run["split_kernel_us"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic_from_profiles(args.ctx),
+                "kernel": "decode_split_kernel<128,3,16,2>",
+                "algorithmic_bytes_per_launch": B,
+                "kernel_mean_us": round(main_run["split_kernel_us"], 3)}
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU restatement ...")
+        cpu = cpu_baseline(args.ctx, args.cpu_seconds)
+        log(f"[bench] CPU: {cpu['us_per_layer_call']:.0f} us/layer-call on {cpu['cores']} threads")
+    line = {
+        "metric": metric,
+        "value": round(main_run["kv_read_gbps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_run["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic N(0,1) Q/K/V and KV cache (K x 0.5), seeded",
+        "config": {"workload": f"C3 Llama-3.2-3B decode attention, ctx {args.ctx}",
+                   "heads_q": HQ, "heads_kv": HKV, "head_dim": D, "ctx": args.ctx,
+                   "splits": args.splits or "auto", "kv_layers_rotated": main_run["n_layers"]},
+        "us_per_layer_call": round(main_run["us_per_layer_call"], 3),
+        "kv_read_pct_of_hbm_peak": round(100 * main_run["kv_read_gbps"] / PEAK_GBPS, 2),
+        "reduce_kernel_us": round(main_run["reduce_kernel_us"], 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if second is not None:
+        line[f"ctx{args.ctx2}"] = {
+            "us_per_layer_call": round(second["us_per_layer_call"], 3),
+            "kv_read_gbps": round(second["kv_read_gbps"], 1),
+            "kv_read_pct_of_hbm_peak": round(100 * second["kv_read_gbps"] / PEAK_GBPS, 2),
+            "split_kernel_us": round(second["split_kernel_us"], 3),
+            "reduce_kernel_us": round(second["reduce_kernel_us"], 3),
+            "kv_layers_rotated": second["n_layers"]}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

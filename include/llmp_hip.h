@@ -1,0 +1,170 @@
+/*
+ * llmp_hip.h -- C ABI of libllmp_hip.so, the MI355X (gfx950) attention path for LLMPlayer.
+ *
+ * The library replaces, for the attention steps of the GPU forward pass, what the reference
+ * reaches through CudaBindings / CudaContext (FFM downcalls into libcuda + NVRTC kernels):
+ * steps 2b'-5 of CudaForwardPass.forwardAttentionPart (per-head QK-norm, RoPE, KV append,
+ * scores / softmax / PV).  Paths cited below are relative to the reference tree
+ * (src/main/java21/it/denzosoft/llmplayer/... unless stated otherwise).
+ *
+ * Conventions (shaped for a Panama FFM binding, as CudaBindings.java:23-95 binds libcuda):
+ *  - every function returns an int status: LLMP_OK (0) on success, like CUDA_SUCCESS
+ *    (CudaBindings.java:15); a non-zero status carries a message readable with
+ *    llmp_last_error (per calling thread);
+ *  - device pointers, streams, events and handles are uint64_t (bound as JAVA_LONG, the way
+ *    CUdeviceptr is, CudaBindings.java:133-158); scalars are int32 / float;
+ *  - host arrays are plain pointers (FFM MemorySegment addresses);
+ *  - stream 0 means the library's own stream (created by llmp_init); launches on one stream
+ *    run in order.  A handle is single-owner and not re-entrant: calls on one handle must not
+ *    overlap (the reference keeps one GPU KV cache per forward pass, CudaForwardPass.java:407-416).
+ *  - every entry point makes the library's device current on the calling thread first, so
+ *    any Java thread may call it (HIP device selection is per thread).
+ */
+#ifndef LLMP_HIP_H
+#define LLMP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------------------- */
+#define LLMP_OK                 0
+#define LLMP_ERR_INVALID_ARG    1  /* bad size, null pointer, unsupported shape            */
+#define LLMP_ERR_OUT_OF_RANGE   2  /* layer / position outside the cache                    */
+#define LLMP_ERR_NOT_INIT       3  /* llmp_init not called                                  */
+#define LLMP_ERR_NO_DEVICE      4  /* no HIP device / wrong architecture                    */
+#define LLMP_ERR_OUT_OF_MEMORY  5  /* allocation would not fit in free HBM                  */
+#define LLMP_ERR_UNSUPPORTED    6  /* shape or mode this build has no kernel for            */
+#define LLMP_ERR_HIP            7  /* a HIP runtime call failed (message has the HIP error) */
+#define LLMP_ERR_BAD_HANDLE     8  /* unknown or destroyed handle                           */
+
+/* ---- enums ----------------------------------------------------------------------------- */
+#define LLMP_KV_F32             0  /* fp32 cache rows (KVCache.Mode.FLOAT32, KVCache.java:79) */
+
+#define LLMP_ROPE_NORMAL        0  /* pairs (2i, 2i+1)    RoPE.ROPE_TYPE_NORMAL, RoPE.java:18 */
+#define LLMP_ROPE_NEOX          2  /* pairs (i, i + R/2)  RoPE.ROPE_TYPE_NEOX,   RoPE.java:19 */
+
+#define LLMP_ROPE_SEL_NONE     -1  /* NoPE layer (Attention.java:311-320 skip)               */
+#define LLMP_ROPE_SEL_GLOBAL    0  /* Attention.rope                                         */
+#define LLMP_ROPE_SEL_LOCAL     1  /* Attention.ropeLocal (Gemma 3 local theta, Attention.java:317) */
+
+/* ---- context (replaces CudaContext.create / close, CudaContext.java:102-160) ----------- */
+
+/* Select HIP device `device`, check it is gfx950 and create the library stream. */
+int llmp_init(int device);
+/* Destroy every handle, the stream and the library's device allocations. */
+int llmp_shutdown(void);
+/* Device facts (DeviceInfo.java:1-22): compute units, total and free HBM bytes, and the
+ * architecture name (NUL-terminated, truncated to name_len). Any out pointer may be NULL. */
+int llmp_device_info(int *n_cu, int64_t *hbm_total, int64_t *hbm_free, char *name, int name_len);
+/* Copy the calling thread's last error message (NUL-terminated) into buf. */
+int llmp_last_error(char *buf, int len);
+
+/* ---- memory and streams (CudaContext.allocBuffer / writeBuffer / readBuffer /
+ *      fillBufferZero / finish, CudaContext.java:368-491, 578-628) ------------------------- */
+int llmp_malloc(uint64_t *dptr, uint64_t bytes);
+int llmp_free(uint64_t dptr);
+int llmp_memcpy_htod(uint64_t dst, const void *src, uint64_t bytes, uint64_t stream);
+int llmp_memcpy_dtoh(void *dst, uint64_t src, uint64_t bytes, uint64_t stream);
+int llmp_memcpy_dtod(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream);
+int llmp_memset_zero(uint64_t dst, uint64_t bytes, uint64_t stream);
+int llmp_stream_create(uint64_t *stream);
+int llmp_stream_destroy(uint64_t stream);
+int llmp_stream_sync(uint64_t stream);
+int llmp_event_create(uint64_t *event);
+int llmp_event_destroy(uint64_t event);
+int llmp_event_record(uint64_t event, uint64_t stream);
+int llmp_event_sync(uint64_t event);
+int llmp_event_elapsed_ms(float *ms, uint64_t start, uint64_t end);
+
+/* ---- device KV cache (CudaForwardPass.java:407-416 per-layer K/V buffers; sizing as
+ *      LLMEngine.estimateKvCache, LLMEngine.java:917-928) --------------------------------- */
+
+/* One zero-filled device pool for n_layers x {K,V}, laid out head-major
+ * [layer][K|V][kv_head][pos][head_dim].  Fails with LLMP_ERR_OUT_OF_MEMORY when the pool
+ * would not fit in free HBM.  head_dim must be 64, 128 or 256; dtype LLMP_KV_F32. */
+int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int dtype,
+                   uint64_t *handle);
+int llmp_kv_destroy(uint64_t handle);
+/* Read rows [pos0, pos0+n) of one layer into host arrays in the reference layout
+ * [pos][kvDim] (KVCache.keyLayer / valueLayer, KVCache.java:149-161).  Either out may be NULL. */
+int llmp_kv_read(uint64_t handle, int layer, int pos0, int n, float *host_k, float *host_v);
+/* Write rows [pos0, pos0+n) of one layer from host arrays in the reference layout
+ * (the inverse of llmp_kv_read; restores a saved prefix, ConversationCache.java:36-56). */
+int llmp_kv_write(uint64_t handle, int layer, int pos0, int n, const float *host_k,
+                  const float *host_v);
+/* Device addresses of one layer's K and V planes ([kv_head][pos][head_dim] fp32). */
+int llmp_kv_layer_ptrs(uint64_t handle, int layer, uint64_t *k_plane, uint64_t *v_plane);
+/* Zero the whole pool (a new conversation). */
+int llmp_kv_clear(uint64_t handle, uint64_t stream);
+
+/* ---- RoPE tables (RoPE.java:45-106; upload as CudaForwardPass.java:398-402) ------------ */
+
+/* Host helper: fill cos/sin tables [max_seq][rope_dim/2] exactly as the RoPE constructor
+ * does (non-YaRN branch, RoPE.java:80-105): freq_i = (float)(1/pow(theta, 2i/R)) / ff[i]
+ * * freqScale, angle = (float)pos * freq_i, cos = (float)cos(angle), sin = (float)sin(angle).
+ * freq_factors may be NULL; linear_freq_scale <= 1 means no scaling. */
+int llmp_rope_table(int rope_dim, int max_seq, float theta, float linear_freq_scale,
+                    const float *freq_factors, int n_freq_factors, float *cos_out,
+                    float *sin_out);
+/* Upload a table ([max_seq][half_rope] each) as the global or local table of a handle.
+ * `which` is LLMP_ROPE_SEL_GLOBAL or LLMP_ROPE_SEL_LOCAL.  The reference uploads only the
+ * global table (CudaForwardPass.java:398-402); the local one serves Gemma 3 local layers
+ * (InferenceEngine.java:58-78, Attention.java:317). */
+int llmp_rope_upload(uint64_t handle, int which, const float *cos_t, const float *sin_t,
+                     int max_seq, int half_rope);
+
+/* ---- per-layer attention configuration (ModelConfig fields read by
+ *      Attention.forwardFromProjections, Attention.java:284-367) ------------------------- */
+
+/* n_heads / n_kv_heads / head_dim: headCount, headCountKV, headSize (n_kv_heads and head_dim
+ * must equal the handle's).  rope_type: LLMP_ROPE_NORMAL / LLMP_ROPE_NEOX.  rope_sel:
+ * LLMP_ROPE_SEL_*.  window: slidingWindow (0 = none); is_global: Attention.isGlobalLayer
+ * (Attention.java:250-276) -- a global layer ignores the window.  scale: attentionScale, or
+ * <= 0 for (float)(1/sqrt(headSize)) (Attention.java:326-328).  softcap: attnLogitSoftCap
+ * (0 = off, Attention.java:352-354).  eps: normEps for QK-norm.  qnorm_w / knorm_w: host
+ * arrays of head_dim floats (RMSNorm.cacheWeights, Attention.java:53-64) or NULL for no
+ * QK-norm (both or neither).  Called once per layer at set-up; it may allocate. */
+int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, int head_dim,
+                      int rope_type, int rope_sel, int window, int is_global, float scale,
+                      float softcap, float eps, const float *qnorm_w, const float *knorm_w);
+
+/* ---- decode attention: one layer-call for one new token --------------------------------
+ * Replaces CudaForwardPass.forwardAttentionPart steps 2b'-5 (CudaForwardPass.java:1529-1570):
+ * rmsnorm_per_head (Q, K) -> rope_apply (Q, K) -> kv_cache_update -> attention_full, with the
+ * CPU semantics of Attention.forwardFromProjections (Attention.java:284-367): sliding window,
+ * local/global RoPE, soft-cap, custom scale.
+ *   q:   device fp32 [n_heads*head_dim]   raw projection (read only: unlike the reference's
+ *                                         in-place kernels, q and k are not rewritten)
+ *   k,v: device fp32 [n_kv_heads*head_dim]
+ *   out: device fp32 [n_heads*head_dim]   (gpuXb2)
+ * The K row stored at `position` is QK-norm + RoPE of k, bit-identical to the CPU path's
+ * KVCache.storeK; the V row is v.  splits: number of split-K partitions per KV head (1..1024),
+ * or <= 0 to let the library choose.  Errors: LLMP_ERR_OUT_OF_RANGE for position outside
+ * [0, max_seq) or a bad layer; LLMP_ERR_INVALID_ARG for a layer never configured. */
+int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint64_t k,
+                     uint64_t v, uint64_t out, int splits, uint64_t stream);
+
+/* ---- profiling (the reference's -Dcuda.profile section timers,
+ *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */
+#define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV) */
+#define LLMP_PROF_DECODE_REDUCE  1  /* log-sum-exp combine of the splits                    */
+#define LLMP_PROF_KINDS          2
+/* on != 0 records a HIP event pair around every launch of the handle's kernels. */
+int llmp_profile_enable(uint64_t handle, int on);
+/* Waits for recorded launches of `kind` and returns their count and summed duration (ms)
+ * since the last reset. */
+int llmp_profile_read(uint64_t handle, int kind, int *count, double *total_ms);
+int llmp_profile_reset(uint64_t handle);
+
+/* ---- utilities ---------------------------------------------------------------------------
+ * A plain device-to-device copy kernel (one 16-byte load and store per thread); used to
+ * calibrate HBM byte counters against a kernel of known traffic.  bytes % 16 == 0. */
+int llmp_copy_kernel(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLMP_HIP_H */

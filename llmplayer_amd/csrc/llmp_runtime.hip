@@ -1,0 +1,754 @@
+// C ABI of libllmp_hip.so: context, memory helpers, device KV cache manager, RoPE tables,
+// per-layer configuration, decode attention entry point and profiling hooks.
+// Declarations and reference citations: include/llmp_hip.h.
+#include "llmp_hip.h"
+#include "llmp_internal.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace llmp {
+namespace {
+
+thread_local std::string t_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_last_error = buf;
+    return code;
+}
+
+#define LLMP_HIP_CHECK(call, what)                                                         \
+    do {                                                                                   \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return fail(LLMP_ERR_HIP, "HIP error in %s: %s (%d)", what, hipGetErrorString(e_), \
+                        (int)e_);                                                          \
+    } while (0)
+
+struct LayerCfg {
+    bool configured = false;
+    int n_heads = 0;
+    int rope_type = 0;
+    int rope_sel = LLMP_ROPE_SEL_GLOBAL;
+    int window = 0;
+    int is_global = 1;
+    float scale = 0.0f;
+    float softcap = 0.0f;
+    float eps = 0.0f;
+    float* d_qnw = nullptr;
+    float* d_knw = nullptr;
+};
+
+struct RopeTable {
+    float* d_cos = nullptr;
+    float* d_sin = nullptr;
+    int max_seq = 0;
+    int half = 0;
+};
+
+struct ProfPair {
+    hipEvent_t begin, end;
+};
+
+struct KvHandle {
+    int n_layers = 0, max_seq = 0, n_kv_heads = 0, head_dim = 0, dtype = 0;
+    float* pool = nullptr;
+    size_t plane_floats = 0;  // floats of one K or V plane of one layer
+    RopeTable rope[2];
+    std::vector<LayerCfg> layers;
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    size_t part_slots = 0;    // (split, query head) slots the workspace holds
+    bool prof_on = false;
+    std::vector<ProfPair> prof_pending[LLMP_PROF_KINDS];
+    std::vector<hipEvent_t> prof_free;
+    double prof_ms[LLMP_PROF_KINDS] = {0, 0};
+    long long prof_count[LLMP_PROF_KINDS] = {0, 0};
+
+    float* k_plane(int layer) const { return pool + (size_t)(2 * layer) * plane_floats; }
+    float* v_plane(int layer) const { return pool + (size_t)(2 * layer + 1) * plane_floats; }
+};
+
+struct Global {
+    std::mutex mu;
+    bool init = false;
+    int device = -1;
+    int n_cu = 0;
+    hipStream_t stream = nullptr;
+    std::string arch;
+    uint64_t next_handle = 1;
+    std::map<uint64_t, std::unique_ptr<KvHandle>> handles;
+};
+
+Global& G() {
+    static Global g;
+    return g;
+}
+
+int ensure_init() {
+    Global& g = G();
+    if (!g.init) return fail(LLMP_ERR_NOT_INIT, "llmp_init has not been called");
+    hipError_t e = hipSetDevice(g.device);
+    if (e != hipSuccess)
+        return fail(LLMP_ERR_HIP, "HIP error in hipSetDevice: %s", hipGetErrorString(e));
+    return LLMP_OK;
+}
+
+hipStream_t pick_stream(uint64_t s) {
+    return s ? reinterpret_cast<hipStream_t>(s) : G().stream;
+}
+
+KvHandle* find_handle(uint64_t h) {
+    auto it = G().handles.find(h);
+    return it == G().handles.end() ? nullptr : it->second.get();
+}
+
+#define LLMP_GET_HANDLE(var, h)                                                   \
+    KvHandle* var = find_handle(h);                                               \
+    if (!var) return fail(LLMP_ERR_BAD_HANDLE, "unknown KV handle %llu", (unsigned long long)(h))
+
+void free_handle(KvHandle* kv) {
+    if (kv->pool) (void)hipFree(kv->pool);
+    for (auto& t : kv->rope) {
+        if (t.d_cos) (void)hipFree(t.d_cos);
+        if (t.d_sin) (void)hipFree(t.d_sin);
+    }
+    for (auto& l : kv->layers) {
+        if (l.d_qnw) (void)hipFree(l.d_qnw);
+        if (l.d_knw) (void)hipFree(l.d_knw);
+    }
+    if (kv->part_o) (void)hipFree(kv->part_o);
+    if (kv->part_ml) (void)hipFree(kv->part_ml);
+    for (auto& v : kv->prof_pending)
+        for (auto& p : v) {
+            (void)hipEventDestroy(p.begin);
+            (void)hipEventDestroy(p.end);
+        }
+    for (auto e : kv->prof_free) (void)hipEventDestroy(e);
+}
+
+int prof_event(KvHandle* kv, hipEvent_t* ev) {
+    if (!kv->prof_free.empty()) {
+        *ev = kv->prof_free.back();
+        kv->prof_free.pop_back();
+        return LLMP_OK;
+    }
+    LLMP_HIP_CHECK(hipEventCreate(ev), "hipEventCreate");
+    return LLMP_OK;
+}
+
+// Folds completed event pairs of one kind into the totals (waits for them).
+int prof_fold(KvHandle* kv, int kind) {
+    for (auto& p : kv->prof_pending[kind]) {
+        LLMP_HIP_CHECK(hipEventSynchronize(p.end), "hipEventSynchronize");
+        float ms = 0.0f;
+        LLMP_HIP_CHECK(hipEventElapsedTime(&ms, p.begin, p.end), "hipEventElapsedTime");
+        kv->prof_ms[kind] += ms;
+        kv->prof_count[kind] += 1;
+        kv->prof_free.push_back(p.begin);
+        kv->prof_free.push_back(p.end);
+    }
+    kv->prof_pending[kind].clear();
+    return LLMP_OK;
+}
+
+// Number of splits when the caller leaves the choice to the library: enough workgroups to
+// give every CU several (the chip has n_cu CUs in 8 XCDs), but never fewer than 64 rows per
+// split, where the per-workgroup prologue and merge would dominate.
+int auto_splits(int n, int n_kv_heads, int n_cu) {
+    const int target_wgs = 4 * (n_cu > 0 ? n_cu : 256);
+    int s = (target_wgs + n_kv_heads - 1) / n_kv_heads;
+    const int by_rows = n / 64 > 0 ? n / 64 : 1;
+    if (s > by_rows) s = by_rows;
+    if (s > kMaxSplits) s = kMaxSplits;
+    return s < 1 ? 1 : s;
+}
+
+}  // namespace
+}  // namespace llmp
+
+using namespace llmp;
+
+extern "C" {
+
+int llmp_init(int device) {
+    Global& g = G();
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (g.init) {
+        if (g.device == device) return LLMP_OK;
+        return fail(LLMP_ERR_INVALID_ARG, "already initialised on device %d", g.device);
+    }
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return fail(LLMP_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= count)
+        return fail(LLMP_ERR_NO_DEVICE, "device %d out of range (%d devices)", device, count);
+    LLMP_HIP_CHECK(hipSetDevice(device), "hipSetDevice");
+    hipDeviceProp_t prop;
+    LLMP_HIP_CHECK(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    std::string arch = prop.gcnArchName;
+    if (arch.rfind("gfx950", 0) != 0)
+        return fail(LLMP_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
+                    device, arch.c_str());
+    hipStream_t s = nullptr;
+    LLMP_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    g.device = device;
+    g.n_cu = prop.multiProcessorCount;
+    g.arch = arch;
+    g.stream = s;
+    g.init = true;
+    return LLMP_OK;
+}
+
+int llmp_shutdown(void) {
+    Global& g = G();
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (!g.init) return LLMP_OK;
+    (void)hipSetDevice(g.device);
+    (void)hipStreamSynchronize(g.stream);
+    for (auto& kv : g.handles) free_handle(kv.second.get());
+    g.handles.clear();
+    (void)hipStreamDestroy(g.stream);
+    g.stream = nullptr;
+    g.init = false;
+    return LLMP_OK;
+}
+
+int llmp_device_info(int* n_cu, int64_t* hbm_total, int64_t* hbm_free, char* name, int name_len) {
+    if (int rc = ensure_init()) return rc;
+    size_t fr = 0, tot = 0;
+    LLMP_HIP_CHECK(hipMemGetInfo(&fr, &tot), "hipMemGetInfo");
+    if (n_cu) *n_cu = G().n_cu;
+    if (hbm_total) *hbm_total = (int64_t)tot;
+    if (hbm_free) *hbm_free = (int64_t)fr;
+    if (name && name_len > 0) {
+        std::strncpy(name, G().arch.c_str(), (size_t)name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    return LLMP_OK;
+}
+
+int llmp_last_error(char* buf, int len) {
+    if (!buf || len <= 0) return LLMP_ERR_INVALID_ARG;
+    std::strncpy(buf, t_last_error.c_str(), (size_t)len - 1);
+    buf[len - 1] = 0;
+    return LLMP_OK;
+}
+
+// ---- memory, streams, events --------------------------------------------------------------
+int llmp_malloc(uint64_t* dptr, uint64_t bytes) {
+    if (int rc = ensure_init()) return rc;
+    if (!dptr || bytes == 0) return fail(LLMP_ERR_INVALID_ARG, "llmp_malloc: bad arguments");
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipErrorOutOfMemory)
+        return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_malloc: %llu bytes do not fit",
+                    (unsigned long long)bytes);
+    LLMP_HIP_CHECK(e, "hipMalloc");
+    *dptr = reinterpret_cast<uint64_t>(p);
+    return LLMP_OK;
+}
+
+int llmp_free(uint64_t dptr) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_HIP_CHECK(hipFree(reinterpret_cast<void*>(dptr)), "hipFree");
+    return LLMP_OK;
+}
+
+int llmp_memcpy_htod(uint64_t dst, const void* src, uint64_t bytes, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    hipStream_t s = pick_stream(stream);
+    LLMP_HIP_CHECK(hipMemcpyAsync(reinterpret_cast<void*>(dst), src, bytes, hipMemcpyHostToDevice, s),
+                   "hipMemcpyAsync(HtoD)");
+    LLMP_HIP_CHECK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return LLMP_OK;
+}
+
+int llmp_memcpy_dtoh(void* dst, uint64_t src, uint64_t bytes, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    hipStream_t s = pick_stream(stream);
+    LLMP_HIP_CHECK(hipMemcpyAsync(dst, reinterpret_cast<const void*>(src), bytes, hipMemcpyDeviceToHost, s),
+                   "hipMemcpyAsync(DtoH)");
+    LLMP_HIP_CHECK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return LLMP_OK;
+}
+
+int llmp_memcpy_dtod(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_HIP_CHECK(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src),
+                                  bytes, hipMemcpyDeviceToDevice, pick_stream(stream)),
+                   "hipMemcpyAsync(DtoD)");
+    return LLMP_OK;
+}
+
+int llmp_memset_zero(uint64_t dst, uint64_t bytes, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_HIP_CHECK(hipMemsetAsync(reinterpret_cast<void*>(dst), 0, bytes, pick_stream(stream)),
+                   "hipMemsetAsync");
+    return LLMP_OK;
+}
+
+int llmp_stream_create(uint64_t* stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!stream) return fail(LLMP_ERR_INVALID_ARG, "llmp_stream_create: null out");
+    hipStream_t s = nullptr;
+    LLMP_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    *stream = reinterpret_cast<uint64_t>(s);
+    return LLMP_OK;
+}
+
+int llmp_stream_destroy(uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!stream) return fail(LLMP_ERR_INVALID_ARG, "llmp_stream_destroy: the library stream is not destroyable");
+    LLMP_HIP_CHECK(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)), "hipStreamDestroy");
+    return LLMP_OK;
+}
+
+int llmp_stream_sync(uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_HIP_CHECK(hipStreamSynchronize(pick_stream(stream)), "hipStreamSynchronize");
+    return LLMP_OK;
+}
+
+int llmp_event_create(uint64_t* event) {
+    if (int rc = ensure_init()) return rc;
+    if (!event) return fail(LLMP_ERR_INVALID_ARG, "llmp_event_create: null out");
+    hipEvent_t e = nullptr;
+    LLMP_HIP_CHECK(hipEventCreate(&e), "hipEventCreate");
+    *event = reinterpret_cast<uint64_t>(e);
+    return LLMP_OK;
+}
+
+int llmp_event_destroy(uint64_t event) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_HIP_CHECK(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)), "hipEventDestroy");
+    return LLMP_OK;
+}
+
+int llmp_event_record(uint64_t event, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_HIP_CHECK(hipEventRecord(reinterpret_cast<hipEvent_t>(event), pick_stream(stream)),
+                   "hipEventRecord");
+    return LLMP_OK;
+}
+
+int llmp_event_sync(uint64_t event) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_HIP_CHECK(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)), "hipEventSynchronize");
+    return LLMP_OK;
+}
+
+int llmp_event_elapsed_ms(float* ms, uint64_t start, uint64_t end) {
+    if (int rc = ensure_init()) return rc;
+    if (!ms) return fail(LLMP_ERR_INVALID_ARG, "llmp_event_elapsed_ms: null out");
+    LLMP_HIP_CHECK(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                       reinterpret_cast<hipEvent_t>(end)),
+                   "hipEventElapsedTime");
+    return LLMP_OK;
+}
+
+// ---- KV cache manager ------------------------------------------------------------------------
+int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int dtype,
+                   uint64_t* handle) {
+    if (int rc = ensure_init()) return rc;
+    if (!handle) return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: null handle out");
+    if (n_layers <= 0 || max_seq <= 0 || n_kv_heads <= 0)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: n_layers=%d max_seq=%d n_kv_heads=%d",
+                    n_layers, max_seq, n_kv_heads);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: head_dim %d (supported: 64, 128, 256)",
+                    head_dim);
+    if (dtype != LLMP_KV_F32)
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: dtype %d (supported: LLMP_KV_F32)", dtype);
+    if ((long long)max_seq * head_dim >= (1LL << 31))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: max_seq*head_dim exceeds 2^31");
+    auto kv = std::make_unique<KvHandle>();
+    kv->n_layers = n_layers;
+    kv->max_seq = max_seq;
+    kv->n_kv_heads = n_kv_heads;
+    kv->head_dim = head_dim;
+    kv->dtype = dtype;
+    kv->plane_floats = (size_t)n_kv_heads * (size_t)max_seq * (size_t)head_dim;
+    const size_t bytes = 2 * (size_t)n_layers * kv->plane_floats * sizeof(float);
+    size_t fr = 0, tot = 0;
+    LLMP_HIP_CHECK(hipMemGetInfo(&fr, &tot), "hipMemGetInfo");
+    if (bytes > fr)
+        return fail(LLMP_ERR_OUT_OF_MEMORY,
+                    "llmp_kv_create: %zu bytes requested, %zu free of %zu HBM bytes", bytes, fr, tot);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipErrorOutOfMemory)
+        return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_kv_create: hipMalloc(%zu) out of memory", bytes);
+    LLMP_HIP_CHECK(e, "hipMalloc(kv pool)");
+    kv->pool = static_cast<float*>(p);
+    kv->layers.resize((size_t)n_layers);
+    hipError_t z = hipMemsetAsync(p, 0, bytes, G().stream);
+    if (z == hipSuccess) z = hipStreamSynchronize(G().stream);
+    if (z != hipSuccess) {
+        free_handle(kv.get());
+        return fail(LLMP_ERR_HIP, "HIP error in hipMemset(kv pool): %s", hipGetErrorString(z));
+    }
+    std::lock_guard<std::mutex> lk(G().mu);
+    const uint64_t id = G().next_handle++;
+    G().handles[id] = std::move(kv);
+    *handle = id;
+    return LLMP_OK;
+}
+
+int llmp_kv_destroy(uint64_t handle) {
+    if (int rc = ensure_init()) return rc;
+    std::lock_guard<std::mutex> lk(G().mu);
+    auto it = G().handles.find(handle);
+    if (it == G().handles.end())
+        return fail(LLMP_ERR_BAD_HANDLE, "unknown KV handle %llu", (unsigned long long)handle);
+    (void)hipStreamSynchronize(G().stream);
+    free_handle(it->second.get());
+    G().handles.erase(it);
+    return LLMP_OK;
+}
+
+static int check_rows(const KvHandle* kv, int layer, int pos0, int n) {
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (pos0 < 0 || n < 0 || (long long)pos0 + n > kv->max_seq)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "rows [%d, %lld) outside [0, %d)", pos0,
+                    (long long)pos0 + n, kv->max_seq);
+    return LLMP_OK;
+}
+
+int llmp_kv_read(uint64_t handle, int layer, int pos0, int n, float* host_k, float* host_v) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (int rc = check_rows(kv, layer, pos0, n)) return rc;
+    if (n == 0) return LLMP_OK;
+    const size_t D = (size_t)kv->head_dim, kv_dim = D * kv->n_kv_heads;
+    hipStream_t s = G().stream;
+    for (int which = 0; which < 2; ++which) {
+        float* host = which == 0 ? host_k : host_v;
+        if (!host) continue;
+        const float* plane = which == 0 ? kv->k_plane(layer) : kv->v_plane(layer);
+        for (int h = 0; h < kv->n_kv_heads; ++h) {
+            const float* src = plane + ((size_t)h * kv->max_seq + (size_t)pos0) * D;
+            LLMP_HIP_CHECK(hipMemcpy2DAsync(host + (size_t)h * D, kv_dim * sizeof(float), src,
+                                            D * sizeof(float), D * sizeof(float), (size_t)n,
+                                            hipMemcpyDeviceToHost, s),
+                           "hipMemcpy2DAsync(kv_read)");
+        }
+    }
+    LLMP_HIP_CHECK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return LLMP_OK;
+}
+
+int llmp_kv_write(uint64_t handle, int layer, int pos0, int n, const float* host_k,
+                  const float* host_v) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (int rc = check_rows(kv, layer, pos0, n)) return rc;
+    if (n == 0) return LLMP_OK;
+    const size_t D = (size_t)kv->head_dim, kv_dim = D * kv->n_kv_heads;
+    hipStream_t s = G().stream;
+    for (int which = 0; which < 2; ++which) {
+        const float* host = which == 0 ? host_k : host_v;
+        if (!host) continue;
+        float* plane = which == 0 ? kv->k_plane(layer) : kv->v_plane(layer);
+        for (int h = 0; h < kv->n_kv_heads; ++h) {
+            float* dst = plane + ((size_t)h * kv->max_seq + (size_t)pos0) * D;
+            LLMP_HIP_CHECK(hipMemcpy2DAsync(dst, D * sizeof(float), host + (size_t)h * D,
+                                            kv_dim * sizeof(float), D * sizeof(float), (size_t)n,
+                                            hipMemcpyHostToDevice, s),
+                           "hipMemcpy2DAsync(kv_write)");
+        }
+    }
+    LLMP_HIP_CHECK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return LLMP_OK;
+}
+
+int llmp_kv_layer_ptrs(uint64_t handle, int layer, uint64_t* k_plane, uint64_t* v_plane) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (k_plane) *k_plane = reinterpret_cast<uint64_t>(kv->k_plane(layer));
+    if (v_plane) *v_plane = reinterpret_cast<uint64_t>(kv->v_plane(layer));
+    return LLMP_OK;
+}
+
+int llmp_kv_clear(uint64_t handle, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    const size_t bytes = 2 * (size_t)kv->n_layers * kv->plane_floats * sizeof(float);
+    LLMP_HIP_CHECK(hipMemsetAsync(kv->pool, 0, bytes, pick_stream(stream)), "hipMemsetAsync(kv)");
+    return LLMP_OK;
+}
+
+// ---- RoPE ------------------------------------------------------------------------------------
+int llmp_rope_table(int rope_dim, int max_seq, float theta, float linear_freq_scale,
+                    const float* freq_factors, int n_freq_factors, float* cos_out,
+                    float* sin_out) {
+    if (rope_dim <= 0 || (rope_dim & 1) || max_seq <= 0 || !cos_out || !sin_out)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_rope_table: rope_dim=%d max_seq=%d", rope_dim,
+                    max_seq);
+    const int half = rope_dim / 2;
+    const float freq_scale = linear_freq_scale > 1.0f ? 1.0f / linear_freq_scale : 1.0f;
+    std::vector<float> freq((size_t)half);
+    for (int i = 0; i < half; ++i) {
+        const double ex = 2.0 * (double)i / (double)rope_dim;
+        float base = (float)(1.0 / std::pow((double)theta, ex));
+        if (freq_factors && i < n_freq_factors) base = base / freq_factors[i];
+        freq[(size_t)i] = base * freq_scale;
+    }
+    for (int pos = 0; pos < max_seq; ++pos) {
+        for (int i = 0; i < half; ++i) {
+            const float angle = (float)pos * freq[(size_t)i];
+            cos_out[(size_t)pos * half + i] = (float)std::cos((double)angle);
+            sin_out[(size_t)pos * half + i] = (float)std::sin((double)angle);
+        }
+    }
+    return LLMP_OK;
+}
+
+int llmp_rope_upload(uint64_t handle, int which, const float* cos_t, const float* sin_t,
+                     int max_seq, int half_rope) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (which != LLMP_ROPE_SEL_GLOBAL && which != LLMP_ROPE_SEL_LOCAL)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_rope_upload: which=%d", which);
+    if (!cos_t || !sin_t || half_rope <= 0 || 2 * half_rope > kv->head_dim || max_seq < kv->max_seq)
+        return fail(LLMP_ERR_INVALID_ARG,
+                    "llmp_rope_upload: need >= %d rows of <= %d pairs (got max_seq=%d half=%d)",
+                    kv->max_seq, kv->head_dim / 2, max_seq, half_rope);
+    RopeTable& t = kv->rope[which];
+    const size_t bytes = (size_t)kv->max_seq * half_rope * sizeof(float);
+    if (t.d_cos && (t.half != half_rope)) {
+        (void)hipFree(t.d_cos);
+        (void)hipFree(t.d_sin);
+        t.d_cos = t.d_sin = nullptr;
+    }
+    if (!t.d_cos) {
+        LLMP_HIP_CHECK(hipMalloc(&t.d_cos, bytes), "hipMalloc(rope cos)");
+        LLMP_HIP_CHECK(hipMalloc(&t.d_sin, bytes), "hipMalloc(rope sin)");
+    }
+    LLMP_HIP_CHECK(hipMemcpy(t.d_cos, cos_t, bytes, hipMemcpyHostToDevice), "hipMemcpy(rope cos)");
+    LLMP_HIP_CHECK(hipMemcpy(t.d_sin, sin_t, bytes, hipMemcpyHostToDevice), "hipMemcpy(rope sin)");
+    t.max_seq = kv->max_seq;
+    t.half = half_rope;
+    return LLMP_OK;
+}
+
+// ---- layer configuration -------------------------------------------------------------------
+int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, int head_dim,
+                      int rope_type, int rope_sel, int window, int is_global, float scale,
+                      float softcap, float eps, const float* qnorm_w, const float* knorm_w) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (n_kv_heads != kv->n_kv_heads || head_dim != kv->head_dim)
+        return fail(LLMP_ERR_INVALID_ARG,
+                    "layer %d: n_kv_heads=%d head_dim=%d differ from the cache's %d/%d", layer,
+                    n_kv_heads, head_dim, kv->n_kv_heads, kv->head_dim);
+    if (n_heads <= 0 || n_heads % n_kv_heads != 0)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d: n_heads=%d not a multiple of n_kv_heads=%d",
+                    layer, n_heads, n_kv_heads);
+    const int group = n_heads / n_kv_heads;
+    if (!decode_shape_supported(head_dim, group))
+        return fail(LLMP_ERR_UNSUPPORTED, "layer %d: no decode kernel for head_dim=%d group=%d",
+                    layer, head_dim, group);
+    if (rope_type != LLMP_ROPE_NORMAL && rope_type != LLMP_ROPE_NEOX)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d: rope_type=%d", layer, rope_type);
+    if (rope_sel != LLMP_ROPE_SEL_NONE && rope_sel != LLMP_ROPE_SEL_GLOBAL &&
+        rope_sel != LLMP_ROPE_SEL_LOCAL)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d: rope_sel=%d", layer, rope_sel);
+    if (window < 0 || softcap < 0.0f || !std::isfinite(scale) || !std::isfinite(softcap) ||
+        !std::isfinite(eps))
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d: window=%d softcap=%g", layer, window,
+                    (double)softcap);
+    if ((qnorm_w == nullptr) != (knorm_w == nullptr))
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d: QK-norm needs both weights or neither", layer);
+
+    LayerCfg& c = kv->layers[(size_t)layer];
+    const size_t wbytes = (size_t)head_dim * sizeof(float);
+    if (qnorm_w) {
+        if (!c.d_qnw) LLMP_HIP_CHECK(hipMalloc(&c.d_qnw, wbytes), "hipMalloc(qnorm)");
+        if (!c.d_knw) LLMP_HIP_CHECK(hipMalloc(&c.d_knw, wbytes), "hipMalloc(knorm)");
+        LLMP_HIP_CHECK(hipMemcpy(c.d_qnw, qnorm_w, wbytes, hipMemcpyHostToDevice), "hipMemcpy(qnorm)");
+        LLMP_HIP_CHECK(hipMemcpy(c.d_knw, knorm_w, wbytes, hipMemcpyHostToDevice), "hipMemcpy(knorm)");
+    } else {
+        if (c.d_qnw) (void)hipFree(c.d_qnw);
+        if (c.d_knw) (void)hipFree(c.d_knw);
+        c.d_qnw = c.d_knw = nullptr;
+    }
+    // Split workspace: kMaxSplits slots per query head.
+    const size_t slots = (size_t)kMaxSplits * (size_t)n_heads;
+    if (slots > kv->part_slots) {
+        if (kv->part_o) (void)hipFree(kv->part_o);
+        if (kv->part_ml) (void)hipFree(kv->part_ml);
+        kv->part_o = kv->part_ml = nullptr;
+        kv->part_slots = 0;
+        LLMP_HIP_CHECK(hipMalloc(&kv->part_o, slots * (size_t)head_dim * sizeof(float)),
+                       "hipMalloc(split outputs)");
+        LLMP_HIP_CHECK(hipMalloc(&kv->part_ml, slots * 2 * sizeof(float)), "hipMalloc(split stats)");
+        kv->part_slots = slots;
+    }
+    c.n_heads = n_heads;
+    c.rope_type = rope_type;
+    c.rope_sel = rope_sel;
+    c.window = window;
+    c.is_global = is_global;
+    c.scale = scale;
+    c.softcap = softcap;
+    c.eps = eps;
+    c.configured = true;
+    return LLMP_OK;
+}
+
+// ---- decode attention --------------------------------------------------------------------------
+int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint64_t k, uint64_t v,
+                     uint64_t out, int splits, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (position < 0 || position >= kv->max_seq)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "position %d outside [0, %d)", position, kv->max_seq);
+    const LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode: null buffer");
+    if (splits > kMaxSplits)
+        return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
+
+    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    DecodeArgs a{};
+    a.q = reinterpret_cast<const float*>(q);
+    a.k = reinterpret_cast<const float*>(k);
+    a.v = reinterpret_cast<const float*>(v);
+    a.kc = kv->k_plane(layer);
+    a.vc = kv->v_plane(layer);
+    if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
+        const RopeTable& t = kv->rope[c.rope_sel];
+        if (!t.d_cos)
+            return fail(LLMP_ERR_INVALID_ARG, "layer %d selects a RoPE table never uploaded", layer);
+        a.cos_row = t.d_cos + (size_t)position * t.half;
+        a.sin_row = t.d_sin + (size_t)position * t.half;
+        a.half_rope = t.half;
+    }
+    a.qnw = c.d_qnw;
+    a.knw = c.d_knw;
+    a.out = reinterpret_cast<float*>(out);
+    a.part_o = kv->part_o;
+    a.part_ml = kv->part_ml;
+    a.head_stride = (long long)kv->max_seq * D;
+    a.pos = position;
+    // Window start (Attention.java:330-335): local layers attend to the last `window` rows.
+    int start = 0;
+    if (c.window > 0 && !c.is_global) start = position - c.window + 1 > 0 ? position - c.window + 1 : 0;
+    a.t_start = start;
+    const int n = position + 1 - start;
+    int s = splits > 0 ? splits : auto_splits(n, Hkv, G().n_cu);
+    if (s > n) s = n;
+    // Rows per split rounded to 16 so splits start on aligned rows; then drop empty splits.
+    int rps = (n + s - 1) / s;
+    if (n >= 16 * s) rps = (rps + 15) & ~15;
+    s = (n + rps - 1) / rps;
+    a.rows_per_split = rps;
+    a.splits = s;
+    a.rope_type = c.rope_type;
+    a.eps = c.eps;
+    const float scale = c.scale > 0.0f ? c.scale : (float)(1.0 / std::sqrt((double)D));
+    const float log2e = 1.4426950408889634f;
+    if (c.softcap > 0.0f) {
+        a.qk_scale = scale;
+        a.softcap = c.softcap;
+        a.softcap_log2e = c.softcap * log2e;
+        a.inv_softcap = 1.0f / c.softcap;
+    } else {
+        a.qk_scale = scale * log2e;
+    }
+
+    hipStream_t st = pick_stream(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+    if (kv->prof_on) {
+        if (int rc = prof_event(kv, &e0)) return rc;
+        if (int rc = prof_event(kv, &e1)) return rc;
+        LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
+    }
+    LLMP_HIP_CHECK(launch_decode_split(a, D, group, Hkv, st), "decode split-K launch");
+    if (kv->prof_on) {
+        LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
+        kv->prof_pending[LLMP_PROF_DECODE_SPLIT].push_back({e0, e1});
+    }
+    if (s > 1) {
+        if (kv->prof_on) {
+            if (int rc = prof_event(kv, &e2)) return rc;
+            if (int rc = prof_event(kv, &e0)) return rc;
+            LLMP_HIP_CHECK(hipEventRecord(e2, st), "hipEventRecord");
+        }
+        LLMP_HIP_CHECK(launch_decode_reduce(a, D, group, c.n_heads, st), "decode reduce launch");
+        if (kv->prof_on) {
+            LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
+            kv->prof_pending[LLMP_PROF_DECODE_REDUCE].push_back({e2, e0});
+        }
+    }
+    if (kv->prof_on && kv->prof_pending[LLMP_PROF_DECODE_SPLIT].size() >= 4096) {
+        for (int kind = 0; kind < LLMP_PROF_KINDS; ++kind)
+            if (int rc = prof_fold(kv, kind)) return rc;
+    }
+    return LLMP_OK;
+}
+
+// ---- profiling ---------------------------------------------------------------------------------
+int llmp_profile_enable(uint64_t handle, int on) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    kv->prof_on = on != 0;
+    return LLMP_OK;
+}
+
+int llmp_profile_read(uint64_t handle, int kind, int* count, double* total_ms) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (kind < 0 || kind >= LLMP_PROF_KINDS)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_profile_read: kind %d", kind);
+    if (int rc = prof_fold(kv, kind)) return rc;
+    if (count) *count = (int)kv->prof_count[kind];
+    if (total_ms) *total_ms = kv->prof_ms[kind];
+    return LLMP_OK;
+}
+
+int llmp_profile_reset(uint64_t handle) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    for (int kind = 0; kind < LLMP_PROF_KINDS; ++kind) {
+        if (int rc = prof_fold(kv, kind)) return rc;
+        kv->prof_ms[kind] = 0.0;
+        kv->prof_count[kind] = 0;
+    }
+    return LLMP_OK;
+}
+
+// ---- utilities -----------------------------------------------------------------------------------
+int llmp_copy_kernel(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!dst || !src || bytes % 16 != 0)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_copy_kernel: needs non-null 16-byte multiples");
+    LLMP_HIP_CHECK(launch_copy(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src),
+                               (size_t)bytes, pick_stream(stream)),
+                   "copy kernel launch");
+    return LLMP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,332 @@
+"""Host-side mirror of the reference's GPU forward-pass attention section, over libllmp_hip.so.
+
+The reference's engine drives the GPU through a class found by reflection
+(InferenceEngine.tryInitForwardPass, InferenceEngine.java:119-160) whose attention half is
+`forwardAttentionPart(layer, position)` (CudaForwardPass.java:1495-1588), reached publicly
+through `forwardAttentionOnly(...)` (:1481-1488) and gated by the static
+`isSupportedForAttention(config, weights)` (:1223-1244).  HipForwardPass keeps those names and
+their meaning for the attention steps (2b'-5: QK-norm, RoPE, KV append, attention) with the
+semantics of Attention.forwardFromProjections (Attention.java:284-367): sliding window,
+local/global RoPE, soft-cap and custom scale, which the reference GPU path lacks.
+
+The Q/K/V projections, Wo and the residual are outside this path: the section takes the
+projections in device buffers (gpuQ, gpuK, gpuV) and leaves the attention output in gpuXb2,
+which is where the reference's projection and Wo kernels read and write.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import LlmpError, call
+
+_F = C.POINTER(C.c_float)
+
+# ModelArchitecture names used by the attention section.
+ARCH_LLAMA, ARCH_QWEN3, ARCH_GEMMA2, ARCH_GEMMA3 = "llama", "qwen3", "gemma2", "gemma3"
+ARCH_GPT_OSS, ARCH_COHERE2, ARCH_GEMMA4 = "gpt-oss", "cohere2", "gemma4"
+# ModelConfig.java:295-314: rope type per architecture (0 NORMAL, 2 NEOX).
+_NEOX_ARCHS = {"qwen2", "qwen3", "glm4", "phi3", "qwen3moe", "olmo2", "gpt-oss", "granitehybrid",
+               "qwen35"}
+
+
+def rope_type_for(arch: str) -> int:
+    return _lib.LLMP_ROPE_NEOX if arch in _NEOX_ARCHS else _lib.LLMP_ROPE_NORMAL
+
+
+def is_global_layer(arch: str, layer: int, sliding_window_pattern: Optional[Sequence[bool]] = None) -> bool:
+    """Attention.isGlobalLayer (Attention.java:250-276)."""
+    if arch == ARCH_GEMMA2:
+        return layer % 2 == 1
+    if arch == ARCH_GEMMA3:
+        return layer % 6 == 5
+    if arch == ARCH_GPT_OSS:
+        return layer % 2 == 0
+    if arch == ARCH_COHERE2:
+        return layer % 4 == 3
+    if arch == ARCH_GEMMA4:
+        if sliding_window_pattern is not None and layer < len(sliding_window_pattern):
+            return not sliding_window_pattern[layer]
+        return layer % 6 == 5
+    return True
+
+
+@dataclass
+class ModelConfig:
+    """The ModelConfig fields the attention section reads (ModelConfig.java:242-511)."""
+    head_count: int
+    head_count_kv: int
+    head_size: int
+    block_count: int
+    architecture: str = ARCH_LLAMA
+    rope_freq_base: float = 10000.0
+    rope_dim_count: int = 0               # 0 -> head_size
+    rope_type: Optional[int] = None       # None -> per architecture
+    rope_scaling_factor: float = 1.0      # linear scaling (InferenceEngine.java:61-64)
+    rope_freq_base_swa: float = 10000.0   # Gemma 4 SWA theta
+    norm_eps: float = 1e-5
+    sliding_window: int = 0
+    sliding_window_pattern: Optional[Sequence[bool]] = None
+    attention_scale: float = 0.0
+    attn_logit_soft_cap: float = 0.0
+    no_rope_layer_interval: int = 0
+    use_no_pe_on_global_layers: bool = False
+    use_layer_norm: bool = False
+
+    @property
+    def kv_dim(self) -> int:
+        return self.head_count_kv * self.head_size
+
+    @property
+    def q_dim(self) -> int:
+        return self.head_count * self.head_size
+
+    def resolved_rope_type(self) -> int:
+        return self.rope_type if self.rope_type is not None else rope_type_for(self.architecture)
+
+
+@dataclass
+class InferenceState:
+    """The buffers of InferenceState (InferenceState.java:11-22) the attention section touches."""
+    q: np.ndarray
+    k: np.ndarray
+    v: np.ndarray
+    xb2: np.ndarray
+
+    @classmethod
+    def create(cls, config: ModelConfig) -> "InferenceState":
+        return cls(np.zeros(config.q_dim, np.float32), np.zeros(config.kv_dim, np.float32),
+                   np.zeros(config.kv_dim, np.float32), np.zeros(config.q_dim, np.float32))
+
+
+def init(device: int = 0) -> None:
+    call("llmp_init", device)
+
+
+def shutdown() -> None:
+    call("llmp_shutdown")
+
+
+def device_info() -> dict:
+    n_cu = C.c_int()
+    tot, fr = C.c_int64(), C.c_int64()
+    name = C.create_string_buffer(64)
+    call("llmp_device_info", C.byref(n_cu), C.byref(tot), C.byref(fr), name, len(name))
+    return {"n_cu": n_cu.value, "hbm_total": tot.value, "hbm_free": fr.value,
+            "arch": name.value.decode()}
+
+
+def _fp(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_F)
+
+
+def rope_table(rope_dim: int, max_seq: int, theta: float, linear_freq_scale: float = 1.0,
+               freq_factors: Optional[np.ndarray] = None):
+    """cos/sin tables [max_seq][rope_dim/2] built as the RoPE constructor builds them
+    (RoPE.java:45-106, non-YaRN branch), by the library's host helper."""
+    half = rope_dim // 2
+    cos_t = np.empty((max_seq, half), np.float32)
+    sin_t = np.empty((max_seq, half), np.float32)
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
+    call("llmp_rope_table", rope_dim, max_seq, float(theta), float(linear_freq_scale), _fp(ff),
+         0 if ff is None else ff.size, _fp(cos_t), _fp(sin_t))
+    return cos_t, sin_t
+
+
+class DeviceBuffer:
+    """A device allocation (CudaBufferManager.createBuffer analogue)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_uint64()
+        call("llmp_malloc", C.byref(p), self.nbytes)
+        self.ptr = p.value
+
+    def upload(self, arr: np.ndarray, stream: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes, (arr.nbytes, self.nbytes)
+        call("llmp_memcpy_htod", self.ptr, arr.ctypes.data, arr.nbytes, stream)
+
+    def download(self, dtype=np.float32, count: Optional[int] = None, stream: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        count = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype)
+        call("llmp_memcpy_dtoh", out.ctypes.data, self.ptr, out.nbytes, stream)
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            call("llmp_free", self.ptr)
+            self.ptr = 0
+
+
+class KvCache:
+    """Device KV cache handle (llmp_kv_*): head-major pool, reference-layout read/write."""
+
+    def __init__(self, n_layers: int, max_seq: int, n_kv_heads: int, head_dim: int):
+        h = C.c_uint64()
+        call("llmp_kv_create", n_layers, max_seq, n_kv_heads, head_dim, _lib.LLMP_KV_F32,
+             C.byref(h))
+        self.handle = h.value
+        self.n_layers, self.max_seq = n_layers, max_seq
+        self.n_kv_heads, self.head_dim = n_kv_heads, head_dim
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+    def read(self, layer: int, pos0: int, n: int):
+        k = np.empty((n, self.kv_dim), np.float32)
+        v = np.empty((n, self.kv_dim), np.float32)
+        call("llmp_kv_read", self.handle, layer, pos0, n, _fp(k), _fp(v))
+        return k, v
+
+    def write(self, layer: int, pos0: int, k: Optional[np.ndarray], v: Optional[np.ndarray]) -> None:
+        k = None if k is None else np.ascontiguousarray(k, np.float32).reshape(-1, self.kv_dim)
+        v = None if v is None else np.ascontiguousarray(v, np.float32).reshape(-1, self.kv_dim)
+        n = (k if k is not None else v).shape[0]
+        call("llmp_kv_write", self.handle, layer, pos0, n, _fp(k), _fp(v))
+
+    def layer_ptrs(self, layer: int):
+        kp, vp = C.c_uint64(), C.c_uint64()
+        call("llmp_kv_layer_ptrs", self.handle, layer, C.byref(kp), C.byref(vp))
+        return kp.value, vp.value
+
+    def clear(self, stream: int = 0) -> None:
+        call("llmp_kv_clear", self.handle, stream)
+
+    def destroy(self) -> None:
+        if self.handle:
+            call("llmp_kv_destroy", self.handle)
+            self.handle = 0
+
+
+class HipForwardPass:
+    """Attention section of a GPU-resident forward pass on MI355X.
+
+    Mirrors the CudaForwardPass constructor's attention set-up (CudaForwardPass.java:346-416:
+    RoPE table upload, per-layer zero-filled KV, QK-norm weights) and its attention API.
+    `qk_norm` holds per-layer (q_weights, k_weights) arrays of head_size floats, or None."""
+
+    def __init__(self, config: ModelConfig, max_seq_len: int,
+                 qk_norm: Optional[Sequence[Optional[tuple]]] = None, device: int = 0):
+        if not HipForwardPass.isSupportedForAttention(config):
+            raise LlmpError("HipForwardPass", 6, "configuration not supported by the HIP attention path")
+        init(device)
+        self.config = config
+        self.max_seq_len = max_seq_len
+        c = config
+        self.kv = KvCache(c.block_count, max_seq_len, c.head_count_kv, c.head_size)
+        rope_dim = c.rope_dim_count or c.head_size
+        # InferenceEngine.java:58-78: global table with linear scaling; local table for
+        # Gemma 3 (theta 10000) and Gemma 4 (SWA theta) when a sliding window exists.
+        linear = c.rope_scaling_factor if c.rope_scaling_factor > 1.0 else 1.0
+        cos_g, sin_g = rope_table(rope_dim, max_seq_len, c.rope_freq_base, linear)
+        call("llmp_rope_upload", self.kv.handle, _lib.LLMP_ROPE_SEL_GLOBAL, _fp(cos_g), _fp(sin_g),
+             max_seq_len, rope_dim // 2)
+        self.has_local_rope = False
+        if c.sliding_window > 0 and c.architecture in (ARCH_GEMMA3, ARCH_GEMMA4):
+            theta_l = 10000.0 if c.architecture == ARCH_GEMMA3 else c.rope_freq_base_swa
+            cos_l, sin_l = rope_table(rope_dim, max_seq_len, theta_l)
+            call("llmp_rope_upload", self.kv.handle, _lib.LLMP_ROPE_SEL_LOCAL, _fp(cos_l),
+                 _fp(sin_l), max_seq_len, rope_dim // 2)
+            self.has_local_rope = True
+        for layer in range(c.block_count):
+            w = qk_norm[layer] if qk_norm is not None else None
+            self.configure_layer(layer, w)
+        self.gpuQ = DeviceBuffer(c.q_dim * 4)
+        self.gpuK = DeviceBuffer(c.kv_dim * 4)
+        self.gpuV = DeviceBuffer(c.kv_dim * 4)
+        self.gpuXb2 = DeviceBuffer(c.q_dim * 4)
+
+    # -- reflection-contract statics -------------------------------------------------------
+    @staticmethod
+    def isSupportedForAttention(config: ModelConfig, weights=None) -> bool:
+        """CudaForwardPass.isSupportedForAttention (CudaForwardPass.java:1223-1244) rejects
+        LayerNorm models; the HIP section also needs a head shape it has a kernel for."""
+        if config.use_layer_norm:
+            return False
+        if config.head_count <= 0 or config.head_count_kv <= 0:
+            return False
+        if config.head_count % config.head_count_kv:
+            return False
+        if config.head_size not in (64, 128, 256):
+            return False
+        if config.head_count // config.head_count_kv not in (1, 2, 3, 4, 6, 8):
+            return False
+        rd = config.rope_dim_count or config.head_size
+        return rd % 2 == 0 and rd <= config.head_size
+
+    def getGpuLayerCount(self) -> int:
+        return self.config.block_count
+
+    # -- set-up ------------------------------------------------------------------------------
+    def configure_layer(self, layer: int, qk_norm: Optional[tuple]) -> None:
+        c = self.config
+        is_global = is_global_layer(c.architecture, layer, c.sliding_window_pattern)
+        irope_skip = c.no_rope_layer_interval > 0 and \
+            layer % c.no_rope_layer_interval == c.no_rope_layer_interval - 1
+        cohere_skip = c.use_no_pe_on_global_layers and is_global
+        if irope_skip or cohere_skip:
+            rope_sel = _lib.LLMP_ROPE_SEL_NONE
+        elif self.has_local_rope and not is_global:
+            rope_sel = _lib.LLMP_ROPE_SEL_LOCAL
+        else:
+            rope_sel = _lib.LLMP_ROPE_SEL_GLOBAL
+        qw = kw = None
+        if qk_norm is not None:
+            qw = np.ascontiguousarray(qk_norm[0], np.float32)
+            kw = np.ascontiguousarray(qk_norm[1], np.float32)
+            assert qw.size == c.head_size and kw.size == c.head_size
+        call("llmp_layer_config", self.kv.handle, layer, c.head_count, c.head_count_kv,
+             c.head_size, c.resolved_rope_type(), rope_sel, c.sliding_window, int(is_global),
+             float(c.attention_scale), float(c.attn_logit_soft_cap), float(c.norm_eps),
+             _fp(qw), _fp(kw))
+
+    # -- per-token API -------------------------------------------------------------------------
+    def uploadQKV(self, q: np.ndarray, k: np.ndarray, v: np.ndarray) -> None:
+        self.gpuQ.upload(np.ascontiguousarray(q, np.float32))
+        self.gpuK.upload(np.ascontiguousarray(k, np.float32))
+        self.gpuV.upload(np.ascontiguousarray(v, np.float32))
+
+    def forwardAttentionPart(self, layerIdx: int, position: int, splits: int = 0,
+                             stream: int = 0) -> None:
+        """Steps 2b'-5 on the device buffers: gpuQ/gpuK/gpuV -> KV append -> gpuXb2."""
+        call("llmp_attn_decode", self.kv.handle, layerIdx, position, self.gpuQ.ptr, self.gpuK.ptr,
+             self.gpuV.ptr, self.gpuXb2.ptr, splits, stream)
+
+    def forwardAttentionOnly(self, state: InferenceState, layerIdx: int, position: int,
+                             splits: int = 0) -> None:
+        """Attention for one layer from host projections in `state` (state.q, state.k,
+        state.v) into state.xb2 -- the contract of Attention.forwardFromProjections
+        (Attention.java:284-367) that GpuForwardPass.java:207-241 relies on."""
+        self.uploadQKV(state.q, state.k, state.v)
+        self.forwardAttentionPart(layerIdx, position, splits)
+        state.xb2[:] = self.downloadXb2()
+
+    def downloadXb2(self) -> np.ndarray:
+        return self.gpuXb2.download(np.float32, self.config.q_dim)
+
+    def sync(self, stream: int = 0) -> None:
+        call("llmp_stream_sync", stream)
+
+    def close(self) -> None:
+        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2"):
+            buf = getattr(self, b, None)
+            if buf is not None:
+                buf.free()
+        if getattr(self, "kv", None) is not None:
+            self.kv.destroy()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

@@ -1,0 +1,120 @@
+"""Seeded decode-attention cases run through both the HIP path (HipForwardPass over
+libllmp_hip.so) and the CPU oracle, with the comparison the path must pass:
+  - output: max |gpu - oracle| <= 1e-4 (and <= 1e-4 + 1e-3*|oracle| elementwise);
+  - cache: every row of the layer read back with llmp_kv_read is bit-identical to the
+    oracle's cache after its own append (KV append and position indexing are exact).
+"""
+from __future__ import annotations
+
+import sys
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+from llmplayer_amd import hip_forward_pass as hfp
+from oracle import oracle as orc
+
+ATOL = 1e-4   # max-abs bar on the attention output
+RTOL = 1e-3   # relative bar on the attention output
+
+_ORC_ARCH = {hfp.ARCH_GEMMA2: orc.ARCH_GEMMA2, hfp.ARCH_GEMMA3: orc.ARCH_GEMMA3,
+             hfp.ARCH_GPT_OSS: orc.ARCH_GPT_OSS, hfp.ARCH_COHERE2: orc.ARCH_COHERE2}
+
+
+def log(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def oracle_config(c: hfp.ModelConfig, max_seq: int) -> orc.OracleConfig:
+    return orc.OracleConfig(
+        n_heads=c.head_count, n_kv_heads=c.head_count_kv, head_size=c.head_size,
+        max_seq=max_seq, rope_type=c.resolved_rope_type(), rope_dim=c.rope_dim_count or c.head_size,
+        norm_eps=c.norm_eps, sliding_window=c.sliding_window, attention_scale=c.attention_scale,
+        softcap=c.attn_logit_soft_cap, arch=_ORC_ARCH.get(c.architecture, orc.ARCH_OTHER),
+        no_rope_interval=c.no_rope_layer_interval, nope_on_global=c.use_no_pe_on_global_layers)
+
+
+def oracle_tables(c: hfp.ModelConfig, max_seq: int, layer: int):
+    """The table Attention.java:317 selects for `layer` (None for a NoPE layer)."""
+    rd = c.rope_dim_count or c.head_size
+    is_global = hfp.is_global_layer(c.architecture, layer, c.sliding_window_pattern)
+    irope = c.no_rope_layer_interval > 0 and layer % c.no_rope_layer_interval == c.no_rope_layer_interval - 1
+    if irope or (c.use_no_pe_on_global_layers and is_global):
+        return None, None
+    if c.sliding_window > 0 and c.architecture in (hfp.ARCH_GEMMA3, hfp.ARCH_GEMMA4) and not is_global:
+        theta = 10000.0 if c.architecture == hfp.ARCH_GEMMA3 else c.rope_freq_base_swa
+        return orc.rope_tables(rd, max_seq, theta)
+    lin = c.rope_scaling_factor if c.rope_scaling_factor > 1.0 else 1.0
+    return orc.rope_tables(rd, max_seq, c.rope_freq_base, lin)
+
+
+@dataclass
+class LayerData:
+    kc: np.ndarray      # [max_seq, kvDim] oracle cache (reference layout)
+    vc: np.ndarray
+    q: np.ndarray
+    k: np.ndarray
+    v: np.ndarray
+    qk_norm: Optional[tuple] = None
+
+
+def make_layer(c: hfp.ModelConfig, max_seq: int, filled: int, seed: int, k_scale: float = 1.0,
+               qk_norm: bool = False) -> LayerData:
+    """Cache rows [0, filled) and the new token's q/k/v ~ N(0,1) (K scaled by k_scale);
+    QK-norm gammas ~ U(0.5, 1.5)."""
+    rng = np.random.default_rng(seed)
+    kv = c.kv_dim
+    kc = np.zeros((max_seq, kv), np.float32)
+    vc = np.zeros((max_seq, kv), np.float32)
+    kc[:filled] = rng.standard_normal((filled, kv), dtype=np.float32)
+    if k_scale != 1.0:
+        kc[:filled] *= np.float32(k_scale)
+    vc[:filled] = rng.standard_normal((filled, kv), dtype=np.float32)
+    q = rng.standard_normal(c.q_dim, dtype=np.float32)
+    k = rng.standard_normal(kv, dtype=np.float32) * np.float32(k_scale)
+    v = rng.standard_normal(kv, dtype=np.float32)
+    w = None
+    if qk_norm:
+        w = (rng.uniform(0.5, 1.5, c.head_size).astype(np.float32),
+             rng.uniform(0.5, 1.5, c.head_size).astype(np.float32))
+    return LayerData(kc, vc, q, k, v, w)
+
+
+def oracle_call(c: hfp.ModelConfig, max_seq: int, d: LayerData, layer: int, pos: int,
+                n_threads: int = 8):
+    """Runs the oracle on a copy of the layer's cache; returns (out, kc_after, vc_after)."""
+    oc = oracle_config(c, max_seq)
+    cs, sn = oracle_tables(c, max_seq, layer)
+    kc, vc = d.kc.copy(), d.vc.copy()
+    qw, kw = (d.qk_norm if d.qk_norm is not None else (None, None))
+    out, _, _ = orc.forward_from_projections(oc, kc, vc, d.q, d.k, d.v, layer, pos, qnorm_w=qw,
+                                             knorm_w=kw, rope_cos=cs, rope_sin=sn,
+                                             n_threads=n_threads)
+    return out, kc, vc
+
+
+def compare_out(got: np.ndarray, want: np.ndarray, what: str) -> float:
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bound = ATOL + RTOL * np.abs(want.astype(np.float64))
+    worst = float(err.max())
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert worst <= ATOL and (err <= bound).all(), (
+        f"{what}: max abs err {worst:.3e} (bar {ATOL}); "
+        f"{int((err > bound).sum())} elements above {ATOL} + {RTOL}*|ref|")
+    return worst
+
+
+def compare_cache(fp: hfp.HipForwardPass, layer: int, kc: np.ndarray, vc: np.ndarray, what: str,
+                  rows: Optional[tuple] = None) -> None:
+    lo, hi = rows if rows is not None else (0, kc.shape[0])
+    gk, gv = fp.kv.read(layer, lo, hi - lo)
+    if not np.array_equal(gk, kc[lo:hi]):
+        bad = np.argwhere(gk != kc[lo:hi])
+        raise AssertionError(f"{what}: K cache differs at {len(bad)} elements, first "
+                             f"(row {bad[0][0] + lo}, col {bad[0][1]}): "
+                             f"{gk[tuple(bad[0])]!r} vs {kc[lo:hi][tuple(bad[0])]!r}")
+    if not np.array_equal(gv, vc[lo:hi]):
+        bad = np.argwhere(gv != vc[lo:hi])
+        raise AssertionError(f"{what}: V cache differs at {len(bad)} elements, first row {bad[0][0] + lo}")

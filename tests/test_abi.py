@@ -1,0 +1,105 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol, reports errors
+through the documented codes, and its host-side helpers match the oracle.  No GPU is used:
+entry points that need a device are only called where they must fail cleanly."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from llmplayer_amd import _lib
+from llmplayer_amd import hip_forward_pass as hfp
+from oracle import oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "llmp_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\bint\s+(llmp_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for must in ("llmp_init", "llmp_shutdown", "llmp_kv_create", "llmp_kv_read", "llmp_kv_write",
+                 "llmp_rope_upload", "llmp_layer_config", "llmp_attn_decode"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_every_declared_symbol():
+    assert set(declared_functions()) == set(_lib.SIGNATURES)
+
+
+def test_error_codes_match_header():
+    text = open(HEADER).read()
+    codes = dict((name, int(val)) for name, val in
+                 re.findall(r"#define\s+(LLMP_ERR_\w+)\s+(\d+)", text))
+    assert {v: k for k, v in codes.items()} == _lib.ERR_NAMES
+
+
+def test_calls_before_init_fail_with_not_init():
+    h = C.c_uint64()
+    rc = _lib.status("llmp_kv_create", 1, 16, 1, 64, 0, C.byref(h))
+    assert rc == 3  # LLMP_ERR_NOT_INIT
+    assert "llmp_init" in _lib.last_error()
+    with pytest.raises(_lib.LlmpError) as ei:
+        _lib.call("llmp_attn_decode", 1, 0, 0, 1, 1, 1, 1, 0, 0)
+    assert ei.value.code == 3 and str(ei.value).startswith("HIP error in llmp_attn_decode: 3")
+
+
+def test_init_without_device_fails_cleanly():
+    rc = _lib.status("llmp_init", 0)
+    if rc == 0:  # a gfx950 device is present: nothing to check here
+        _lib.call("llmp_shutdown")
+        pytest.skip("a GPU is present")
+    assert rc == 4  # LLMP_ERR_NO_DEVICE
+    assert "device" in _lib.last_error()
+
+
+@pytest.mark.parametrize("R,S,theta,lin", [(64, 600, 5e5, 1.0), (128, 2048, 1e6, 1.0),
+                                           (256, 1024, 1e4, 1.0), (128, 512, 1e4, 8.0)])
+def test_rope_table_helper_is_bit_identical_to_oracle(R, S, theta, lin):
+    c1, s1 = hfp.rope_table(R, S, theta, lin)
+    c2, s2 = orc.rope_tables(R, S, theta, lin)
+    assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
+
+
+def test_rope_table_helper_freq_factors():
+    ff = np.linspace(1, 4, 32).astype(np.float32)
+    c1, s1 = hfp.rope_table(64, 100, 5e5, 1.0, ff)
+    c2, s2 = orc.rope_tables(64, 100, 5e5, 1.0, ff)
+    assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
+
+
+def test_rope_table_rejects_bad_args():
+    out = np.zeros(4, np.float32)
+    p = out.ctypes.data_as(C.POINTER(C.c_float))
+    assert _lib.status("llmp_rope_table", 3, 1, 1e4, 1.0, None, 0, p, p) == 1
+
+
+def test_is_supported_for_attention():
+    ok = hfp.ModelConfig(24, 8, 128, 28)
+    assert hfp.HipForwardPass.isSupportedForAttention(ok)
+    assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(24, 8, 128, 28, use_layer_norm=True))
+    assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(24, 8, 96, 28))
+    assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(40, 8, 128, 28))  # group 5
+    assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(24, 7, 128, 28))
+
+
+def test_global_layer_and_rope_type_host_logic_match_oracle():
+    for arch, oarch in ((hfp.ARCH_GEMMA2, orc.ARCH_GEMMA2), (hfp.ARCH_GEMMA3, orc.ARCH_GEMMA3),
+                        (hfp.ARCH_GPT_OSS, orc.ARCH_GPT_OSS), (hfp.ARCH_COHERE2, orc.ARCH_COHERE2),
+                        (hfp.ARCH_LLAMA, orc.ARCH_OTHER)):
+        for layer in range(30):
+            assert hfp.is_global_layer(arch, layer) == orc.is_global_layer(oarch, layer)
+    assert hfp.rope_type_for("llama") == 0 and hfp.rope_type_for("qwen3") == 2
+    assert hfp.rope_type_for("gemma3") == 0

@@ -1,0 +1,216 @@
+"""GPU parity of the decode attention path (libllmp_hip.so through HipForwardPass) against the
+CPU oracle on the BASELINE configurations, plus edge cases and error plumbing.
+
+Bar: attention output max-abs error <= 1e-4 (and <= 1e-4 + 1e-3*|ref| elementwise) versus the
+oracle (fp32 accumulate); the KV cache after the call is bit-identical to the oracle's (append
+and position indexing exact)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from llmplayer_amd import _lib
+from llmplayer_amd import hip_forward_pass as hfp
+from tests import decode_cases as dc
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(fp, c, max_seq, d, layer, pos, splits, what, check_cache=True, oracle=None):
+    dc.log(f"[gpu] {what}: layer={layer} pos={pos} splits={splits}")
+    fp.kv.write(layer, 0, d.kc, d.vc)
+    st = hfp.InferenceState.create(c)
+    st.q[:], st.k[:], st.v[:] = d.q, d.k, d.v
+    fp.forwardAttentionOnly(st, layer, pos, splits)
+    out, kc, vc = oracle if oracle is not None else dc.oracle_call(c, max_seq, d, layer, pos)
+    err = dc.compare_out(st.xb2, out, what)
+    if check_cache:
+        dc.compare_cache(fp, layer, kc, vc, what)
+    else:
+        dc.compare_cache(fp, layer, kc, vc, what, rows=(pos, pos + 1))
+    dc.log(f"[gpu] {what}: ok, max abs err {err:.2e}")
+    return out, kc, vc
+
+
+# --------------------------------------------------------------------------- C1: Llama-3.2-1B
+@pytest.mark.parametrize("splits", [0, 1, 3, 16, 64])
+def test_c1_llama1b_pos511(splits):
+    c = hfp.ModelConfig(32, 8, 64, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=500000.0)
+    d = dc.make_layer(c, 512, 511, seed=101)
+    with hfp.HipForwardPass(c, 512) as fp:
+        _run(fp, c, 512, d, 0, 511, splits, "C1 Llama-3.2-1B pos 511")
+
+
+# ------------------------------------------------------------ C3: Llama-3.2-3B (headline shape)
+@pytest.fixture(scope="module", params=[4096, 32768], ids=["ctx4k", "ctx32k"])
+def c3(request):
+    n = request.param
+    c = hfp.ModelConfig(24, 8, 128, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=500000.0)
+    d = dc.make_layer(c, n, n - 1, seed=303, k_scale=0.5)
+    ref = dc.oracle_call(c, n, d, 0, n - 1)
+    fp = hfp.HipForwardPass(c, n)
+    yield c, n, d, ref, fp
+    fp.close()
+
+
+@pytest.mark.parametrize("splits", [0, 8, 16, 32, 64, 128])
+def test_c3_llama3b_split_sweep(c3, splits):
+    c, n, d, ref, fp = c3
+    _run(fp, c, n, d, 0, n - 1, splits, f"C3 Llama-3.2-3B ctx {n}", check_cache=(splits == 0),
+         oracle=ref)
+
+
+# ------------------------------------------------------------------- C2: Qwen3-0.6B, QK-norm
+@pytest.mark.parametrize("n,layers", [(1024, range(28)), (4096, (0, 5, 13, 20, 27)),
+                                      (16384, (0, 13, 27))])
+def test_c2_qwen3_qknorm(n, layers):
+    c = hfp.ModelConfig(16, 8, 128, 28, architecture=hfp.ARCH_QWEN3, rope_freq_base=1e6,
+                        norm_eps=1e-6)
+    datas = {l: dc.make_layer(c, n, n - 1, seed=2000 + l, qk_norm=True) for l in layers}
+    qk = [datas[l].qk_norm if l in datas else (np.ones(128, np.float32),) * 2 for l in range(28)]
+    with hfp.HipForwardPass(c, n, qk_norm=qk) as fp:
+        for l in layers:
+            _run(fp, c, n, datas[l], l, n - 1, 0, f"C2 Qwen3-0.6B ctx {n}",
+                 check_cache=(n <= 4096))
+
+
+# ---------------------------------------------------- C4: Gemma-3-1B, MQA, window 512 / global
+def _gemma3(max_seq):
+    return hfp.ModelConfig(4, 1, 256, 6, architecture=hfp.ARCH_GEMMA3, rope_freq_base=1e6,
+                           norm_eps=1e-6, sliding_window=512)
+
+
+def test_c4_gemma3_local_and_global_layers():
+    c = _gemma3(8192)
+    datas = {l: dc.make_layer(c, 8192, 8191, seed=400 + l, qk_norm=True) for l in range(6)}
+    with hfp.HipForwardPass(c, 8192, qk_norm=[datas[l].qk_norm for l in range(6)]) as fp:
+        for l in range(6):
+            kind = "global" if l % 6 == 5 else "local W=512"
+            _run(fp, c, 8192, datas[l], l, 8191, 0, f"C4 Gemma-3-1B ctx 8192 layer {l} ({kind})")
+
+
+@pytest.mark.parametrize("pos", [0, 1, 510, 511, 512, 513, 1000])
+def test_c4_window_boundaries(pos):
+    c = _gemma3(1024)
+    d = dc.make_layer(c, 1024, pos, seed=450 + pos, qk_norm=True)
+    qk = [d.qk_norm] * 6
+    with hfp.HipForwardPass(c, 1024, qk_norm=qk) as fp:
+        _run(fp, c, 1024, d, 0, pos, 0, "C4 window boundary (local layer)")
+        _run(fp, c, 1024, d, 5, pos, 0, "C4 window boundary (global layer)")
+
+
+# ------------------------------------------------------------------------------ shapes
+SHAPES = [(8, 8, 64), (16, 8, 64), (24, 8, 64), (32, 8, 64), (48, 8, 64), (64, 8, 64),
+          (8, 8, 128), (16, 8, 128), (32, 4, 128), (48, 8, 128), (64, 8, 128),
+          (4, 4, 256), (8, 4, 256), (12, 4, 256), (16, 4, 256), (24, 4, 256), (32, 4, 256),
+          (4, 1, 256)]
+
+
+@pytest.mark.parametrize("hq,hkv,dim", SHAPES, ids=[f"{a}-{b}-{c}" for a, b, c in SHAPES])
+def test_every_supported_group_and_head_dim(hq, hkv, dim):
+    c = hfp.ModelConfig(hq, hkv, dim, 1, architecture=hfp.ARCH_QWEN3, rope_freq_base=1e6,
+                        norm_eps=1e-6)
+    d = dc.make_layer(c, 1200, 999, seed=hq * 1000 + hkv * 10 + dim, qk_norm=True)
+    with hfp.HipForwardPass(c, 1200, qk_norm=[d.qk_norm]) as fp:
+        for splits in (0, 1, 7):
+            _run(fp, c, 1200, d, 0, 999, splits, f"shape {hq}/{hkv}/{dim}")
+
+
+# ------------------------------------------------------------------------------ edge cases
+def test_pos0_output_is_v0():
+    c = hfp.ModelConfig(32, 8, 64, 1, rope_freq_base=500000.0)
+    d = dc.make_layer(c, 64, 0, seed=7)
+    with hfp.HipForwardPass(c, 64) as fp:
+        out, _, _ = _run(fp, c, 64, d, 0, 0, 0, "pos 0")
+        got = fp.downloadXb2()
+        assert np.array_equal(got, np.repeat(d.v.reshape(8, 64), 4, axis=0).reshape(-1))
+
+
+def test_last_row_of_cache_and_splits_above_rows():
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    d = dc.make_layer(c, 300, 299, seed=8)
+    with hfp.HipForwardPass(c, 300) as fp:
+        _run(fp, c, 300, d, 0, 299, 1024, "pos = max_seq-1, splits 1024 > rows")
+        _run(fp, c, 300, d, 0, 299, 299, "splits = rows - 1")
+
+
+def test_nope_layer_and_softcap_and_custom_scale():
+    c = hfp.ModelConfig(16, 4, 128, 4, architecture=hfp.ARCH_GEMMA2, rope_freq_base=1e4,
+                        attn_logit_soft_cap=50.0, attention_scale=0.125, sliding_window=300,
+                        no_rope_layer_interval=4)
+    for layer in (0, 1, 3):
+        d = dc.make_layer(c, 700, 650, seed=90 + layer, k_scale=3.0)
+        with hfp.HipForwardPass(c, 700) as fp:
+            _run(fp, c, 700, d, layer, 650, 0, f"gemma2-like layer {layer} (softcap, scale, window, NoPE)")
+
+
+def test_consecutive_decode_steps_match_sequential_oracle():
+    c = hfp.ModelConfig(16, 8, 128, 2, architecture=hfp.ARCH_QWEN3, rope_freq_base=1e6, norm_eps=1e-6)
+    rng = np.random.default_rng(55)
+    max_seq, p0, steps = 2048, 1500, 12
+    base = dc.make_layer(c, max_seq, p0, seed=56, qk_norm=True)
+    kc, vc = base.kc.copy(), base.vc.copy()
+    with hfp.HipForwardPass(c, max_seq, qk_norm=[base.qk_norm] * 2) as fp:
+        fp.kv.write(1, 0, kc, vc)
+        for i in range(steps):
+            pos = p0 + i
+            d = dc.LayerData(kc, vc, rng.standard_normal(c.q_dim, dtype=np.float32),
+                             rng.standard_normal(c.kv_dim, dtype=np.float32),
+                             rng.standard_normal(c.kv_dim, dtype=np.float32), base.qk_norm)
+            dc.log(f"[gpu] decode step {i} pos {pos}")
+            st = hfp.InferenceState.create(c)
+            st.q[:], st.k[:], st.v[:] = d.q, d.k, d.v
+            fp.forwardAttentionOnly(st, 1, pos)
+            out, kc, vc = dc.oracle_call(c, max_seq, d, 1, pos)
+            dc.compare_out(st.xb2, out, f"step {i}")
+        dc.compare_cache(fp, 1, kc, vc, "after decode steps")
+
+
+def test_error_codes():
+    c = hfp.ModelConfig(8, 2, 64, 2, rope_freq_base=1e4)
+    with hfp.HipForwardPass(c, 128) as fp:
+        h = fp.kv.handle
+        args = (fp.gpuQ.ptr, fp.gpuK.ptr, fp.gpuV.ptr, fp.gpuXb2.ptr)
+        assert _lib.status("llmp_attn_decode", h, 0, 128, *args, 0, 0) == 2   # pos >= max_seq
+        assert _lib.status("llmp_attn_decode", h, 0, -1, *args, 0, 0) == 2
+        assert _lib.status("llmp_attn_decode", h, 2, 5, *args, 0, 0) == 2     # bad layer
+        assert _lib.status("llmp_attn_decode", h, 0, 5, *args, 2000, 0) == 1  # splits > max
+        assert _lib.status("llmp_attn_decode", h + 999, 0, 5, *args, 0, 0) == 8
+        with pytest.raises(_lib.LlmpError) as ei:
+            fp.forwardAttentionPart(0, 128)
+        assert ei.value.code == 2 and "position 128" in ei.value.message
+        k = np.zeros((4, c.kv_dim), np.float32)
+        with pytest.raises(_lib.LlmpError):
+            fp.kv.write(0, 126, k, k)                                          # rows past the end
+        # a layer never configured
+        kv = hfp.KvCache(1, 16, 2, 64)
+        try:
+            assert _lib.status("llmp_attn_decode", kv.handle, 0, 1, *args, 0, 0) == 1
+        finally:
+            kv.destroy()
+        # unsupported shapes
+        hd = C.c_uint64()
+        assert _lib.status("llmp_kv_create", 1, 16, 2, 96, 0, C.byref(hd)) == 6
+        assert _lib.status("llmp_layer_config", h, 0, 10, 2, 64, 0, 0, 0, 1, 0.0, 0.0, 1e-5,
+                           None, None) == 6   # group 5 has no kernel
+        # an allocation beyond HBM is refused before touching the device
+        assert _lib.status("llmp_kv_create", 4096, 1 << 20, 64, 128, 0, C.byref(hd)) == 5
+
+
+def test_profile_counters_count_launches():
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    d = dc.make_layer(c, 4096, 4095, seed=9, k_scale=0.5)
+    with hfp.HipForwardPass(c, 4096) as fp:
+        fp.kv.write(0, 0, d.kc, d.vc)
+        fp.uploadQKV(d.q, d.k, d.v)
+        _lib.call("llmp_profile_enable", fp.kv.handle, 1)
+        for _ in range(5):
+            fp.forwardAttentionPart(0, 4095, 32)
+        cnt, ms = C.c_int(), C.c_double()
+        _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(cnt), C.byref(ms))
+        assert cnt.value == 5 and ms.value > 0
+        _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_REDUCE, C.byref(cnt), C.byref(ms))
+        assert cnt.value == 5
+        _lib.call("llmp_profile_reset", fp.kv.handle)
+        _lib.call("llmp_profile_read", fp.kv.handle, 0, C.byref(cnt), C.byref(ms))
+        assert cnt.value == 0
