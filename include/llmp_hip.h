@@ -147,6 +147,17 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
 int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint64_t k,
                      uint64_t v, uint64_t out, int splits, uint64_t stream);
 
+/* ---- graph capture (CudaContext.beginCapture / endCapture / launchGraph,
+ *      CudaContext.java:585-613): record a sequence of launches on a stream once, replay it
+ *      with one call.  Arguments (positions included) are frozen at capture time. ---------- */
+/* Start capturing the work enqueued on `stream` (0 = the library stream; capture mode
+ * "thread local").  Profiling must be off while capturing. */
+int llmp_graph_begin(uint64_t stream);
+/* Stop capturing and instantiate the graph; *graph receives an executable-graph handle. */
+int llmp_graph_end(uint64_t stream, uint64_t *graph);
+int llmp_graph_launch(uint64_t graph, uint64_t stream);
+int llmp_graph_destroy(uint64_t graph);
+
 /* ---- profiling (the reference's -Dcuda.profile section timers,
  *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */
 #define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV) */

@@ -1,0 +1,487 @@
+// Split-K flash-decoding kernels for one new token, gfx950 (CDNA4, wave64).  Included by
+// decode_attention.hip, which instantiates the shapes the library ships.
+//
+// One workgroup = (split j, KV head g): it owns rows [t_start + j*R, ...) of that KV head and
+// every query head of its GQA group (Hq/Hkv heads), so each KV byte is read from HBM once per
+// layer-call.  It also does the per-token prep of the reference's separate kernels
+// (rmsnorm_per_head, rope_apply, kv_cache_update: CudaForwardPass.java:1529-1564) for its own
+// heads.  With more than one split, a second small kernel merges the splits (log-sum-exp
+// combine); a layer-call is one or two launches.
+//
+// Bit-exactness of the appended K row: it is computed with the CPU path's float step order --
+// sum of squares in the SimdVectorOps.dot order (8 FMA lanes, lanes summed left to right,
+// SimdVectorOps.java:17-31), r = 1/(float)sqrt((double)(ss/D + eps)) (Attention.java:390),
+// x = (x*r)*w (SimdVectorOps.java:150-162), and the rotation x0*c - x1*s, x0*s + x1*c with
+// separately rounded products (RoPE.java:145-170, SimdVectorOps.java:165-186).  The library
+// is compiled with -ffp-contract=off so none of these is fused; fmaf is explicit where the
+// attention math wants a fused multiply-add.
+//
+// Streaming: the device cache is head-major [kv_head][pos][D], so a split's K (and V) rows
+// are one contiguous span.  LPR lanes share a row; lane j of a row group loads the 16-byte
+// chunks j, j+LPR, ... of the row, so one wave-wide load instruction covers RPW = 64/LPR rows
+// with LPR*16 contiguous bytes per row.  Scores are reduced across the LPR lanes of a row with
+// DPP (quad_perm, row_half_mirror, row_mirror); each row group keeps its own online-softmax
+// state (max, sum, output slice) in registers; groups and waves are merged once at the end
+// through cross-lane shuffles and LDS.  Decode is HBM-bound (Hq/(2*Hkv) flop/byte), so no
+// MFMA is used.
+#pragma once
+
+#include "llmp_internal.h"
+
+namespace llmp {
+namespace dk {
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Finite "minus infinity" for running maxima, so that exp2(m_old - m_new) never sees
+// (-inf) - (-inf).  Masked scores use a true -inf, which exp2 maps to 0.
+constexpr float kNegBig = -1.0e30f;
+
+// DPP controls (CDNA3/CDNA4 ISA): quad_perm, row_half_mirror, row_mirror.
+constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRowMirror = 0x140;      // lane i <- lane 15-i within each row of 16
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <- lane 7-i within each half row
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the LPR consecutive lanes that share a row.  Every lane ends with the same value
+// (each step adds the same two operands, in either order).
+template <int LPR>
+__device__ __forceinline__ float row_group_sum(float x) {
+    static_assert(LPR == 4 || LPR == 8 || LPR == 16, "rows are shared by 4, 8 or 16 lanes");
+    x = x + dpp<kDppQuadXor1>(x);
+    x = x + dpp<kDppQuadXor2>(x);
+    if constexpr (LPR >= 8) x = x + dpp<kDppRowHalfMirror>(x);
+    if constexpr (LPR >= 16) x = x + dpp<kDppRowMirror>(x);
+    return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef float native_f4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load; NT marks it non-temporal (streamed once, no reuse expected).
+template <bool NT>
+__device__ __forceinline__ float4 load4(const float4* p) {
+    if constexpr (NT) {
+        const native_f4 v = __builtin_nontemporal_load(reinterpret_cast<const native_f4*>(p));
+        return make_float4(v.x, v.y, v.z, v.w);
+    } else {
+        return *p;
+    }
+}
+
+template <int D, int EPL>
+struct Frag {
+    static constexpr int LPR = D / EPL;   // lanes per row
+    static constexpr int RPW = 64 / LPR;  // rows per wave-wide load
+    static constexpr int C4 = EPL / 4;    // 16-byte chunks per lane per row
+    // Dimension held by lane j (within its row group) at element e.
+    static __device__ __forceinline__ int dim(int j, int e) {
+        return (e >> 2) * (LPR * 4) + j * 4 + (e & 3);
+    }
+};
+
+// Online-softmax update of one row group with U rows: s = (q . K_t) in the log2 domain,
+// masked rows get -inf; o and l are rescaled once per call.
+template <int D, int G, int EPL, int U>
+__device__ __forceinline__ void accumulate_rows(const float (&qr)[G][EPL],
+                                                const float4 (&kf)[U][EPL / 4],
+                                                const float4 (&vf)[U][EPL / 4],
+                                                const bool (&valid)[U], float (&m)[G],
+                                                float (&l)[G], float (&o)[G][EPL],
+                                                const DecodeArgs& a) {
+    using F = Frag<D, EPL>;
+    float s[U][G];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < F::C4; ++c) {
+                acc = __builtin_fmaf(qr[h][4 * c + 0], kf[u][c].x, acc);
+                acc = __builtin_fmaf(qr[h][4 * c + 1], kf[u][c].y, acc);
+                acc = __builtin_fmaf(qr[h][4 * c + 2], kf[u][c].z, acc);
+                acc = __builtin_fmaf(qr[h][4 * c + 3], kf[u][c].w, acc);
+            }
+            s[u][h] = row_group_sum<F::LPR>(acc);
+        }
+    }
+    if (a.softcap > 0.0f) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int h = 0; h < G; ++h) s[u][h] = a.softcap_log2e * tanhf(s[u][h] * a.inv_softcap);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float mx = m[h];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            s[u][h] = valid[u] ? s[u][h] : -__builtin_inff();
+            mx = fmaxf(mx, s[u][h]);
+        }
+        const float alpha = fast_exp2(m[h] - mx);
+        m[h] = mx;
+        float lsum = l[h] * alpha;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[h][e] = o[h][e] * alpha;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float p = fast_exp2(s[u][h] - mx);
+            lsum = lsum + p;
+#pragma unroll
+            for (int c = 0; c < F::C4; ++c) {
+                o[h][4 * c + 0] = __builtin_fmaf(p, vf[u][c].x, o[h][4 * c + 0]);
+                o[h][4 * c + 1] = __builtin_fmaf(p, vf[u][c].y, o[h][4 * c + 1]);
+                o[h][4 * c + 2] = __builtin_fmaf(p, vf[u][c].z, o[h][4 * c + 2]);
+                o[h][4 * c + 3] = __builtin_fmaf(p, vf[u][c].w, o[h][4 * c + 3]);
+            }
+        }
+        l[h] = lsum;
+    }
+}
+
+// Exact prep of `nh` heads staged in LDS (x: nh*D floats): QK-norm with weights w0 for heads
+// < n_w0 and w1 for the others, then RoPE.  Must be called by the whole workgroup.
+template <int D, int NTHR>
+__device__ void prep_heads_lds(float* x, int nh, int n_w0, const float* w0, const float* w1,
+                               float* s_acc, float* s_r, const DecodeArgs& a, int tid) {
+    if (a.qnw != nullptr) {
+        if (tid < nh * 8) {
+            const int hh = tid >> 3, ln = tid & 7;
+            const float* xh = x + hh * D;
+            float acc = 0.0f;
+            for (int i = ln; i < D; i += 8) acc = __builtin_fmaf(xh[i], xh[i], acc);
+            s_acc[tid] = acc;
+        }
+        __syncthreads();
+        if (tid < nh) {
+            const float* ac = s_acc + tid * 8;
+            float ss = ac[0];
+#pragma unroll
+            for (int ln = 1; ln < 8; ++ln) ss = ss + ac[ln];
+            float t = ss / (float)D;
+            t = t + a.eps;
+            const float r = (float)__builtin_sqrt((double)t);
+            s_r[tid] = 1.0f / r;
+        }
+        __syncthreads();
+        for (int i = tid; i < nh * D; i += NTHR) {
+            const int hh = i / D;
+            const float* w = (hh < n_w0) ? w0 : w1;
+            const float xs = x[i] * s_r[hh];
+            x[i] = xs * w[i - hh * D];
+        }
+        __syncthreads();
+    }
+    if (a.cos_row != nullptr) {
+        const int half = a.half_rope;
+        for (int idx = tid; idx < nh * half; idx += NTHR) {
+            const int hh = idx / half, i = idx - hh * half;
+            float* xh = x + hh * D;
+            const int i0 = (a.rope_type == 0) ? 2 * i : i;
+            const int i1 = (a.rope_type == 0) ? 2 * i + 1 : half + i;
+            const float c = a.cos_row[i], sn = a.sin_row[i];
+            const float v0 = xh[i0], v1 = xh[i1];
+            const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
+            xh[i0] = t0 - t1;
+            xh[i1] = t2 + t3;
+        }
+        __syncthreads();
+    }
+}
+
+// Rotation of the lane's own q slice in registers (no QK-norm; NORMAL pairs sit inside one
+// 16-byte chunk, NEOX pairs (i, i+D/2) in chunks c and c+C4/2 of the same lane).
+template <int D, int G, int EPL>
+__device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const DecodeArgs& a) {
+    using F = Frag<D, EPL>;
+    const int half = a.half_rope;
+    if (a.rope_type == 0) {
+#pragma unroll
+        for (int c = 0; c < F::C4; ++c) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                // Pairs at or beyond half_rope (partial RoPE) keep their values.
+                const int i = (c * F::LPR * 4 + j * 4) / 2 + p;
+                const bool rot = i < half;
+                const int ii = rot ? i : 0;
+                const float cs = a.cos_row[ii], sn = a.sin_row[ii];
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float v0 = qr[h][4 * c + 2 * p], v1 = qr[h][4 * c + 2 * p + 1];
+                    const float t0 = v0 * cs, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * cs;
+                    const float r0 = t0 - t1, r1 = t2 + t3;
+                    qr[h][4 * c + 2 * p] = rot ? r0 : v0;
+                    qr[h][4 * c + 2 * p + 1] = rot ? r1 : v1;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < F::C4 / 2; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = c * F::LPR * 4 + j * 4 + e;  // < D/2 = half
+                const float cs = a.cos_row[i], sn = a.sin_row[i];
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const float v0 = qr[h][4 * c + e], v1 = qr[h][4 * (c + F::C4 / 2) + e];
+                    const float t0 = v0 * cs, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * cs;
+                    qr[h][4 * c + e] = t0 - t1;
+                    qr[h][4 * (c + F::C4 / 2) + e] = t2 + t3;
+                }
+            }
+        }
+    }
+}
+
+template <int D, int G, int EPL, int U, int WAVES, bool NT>
+__global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) {
+    using F = Frag<D, EPL>;
+    constexpr int NTHR = WAVES * 64;
+    constexpr int LPR = F::LPR, RPW = F::RPW, C4 = F::C4;
+    constexpr int ROWS_WAVE = U * RPW;
+    constexpr int ROWS_BLOCK = WAVES * ROWS_WAVE;
+
+    // s_x: G query heads then the group's K head (post norm and RoPE).
+    __shared__ float s_x[(G + 1) * D];
+    __shared__ float s_v[D];
+    __shared__ float s_acc[(G + 1) * 8];
+    __shared__ float s_r[G + 1];
+    __shared__ float s_m[WAVES * G];
+    __shared__ float s_l[WAVES * G];
+    __shared__ float s_o[WAVES * G * D];
+
+    const int tid = threadIdx.x;
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int h0 = kvh * G;
+    const int row_begin = a.t_start + split * a.rows_per_split;
+    const int row_end = min(row_begin + a.rows_per_split, a.pos + 1);
+    const bool has_pos = (row_end == a.pos + 1);
+    const int cache_end = has_pos ? a.pos : row_end;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int grp = lane / LPR, j = lane - grp * LPR;
+
+    float* kplane = a.kc + (long long)kvh * a.head_stride;
+    float* vplane = a.vc + (long long)kvh * a.head_stride;
+
+    // 1. Query slice of this lane, pre-scaled (log2 domain unless soft-capping).  Without
+    //    QK-norm and with pairs inside a lane, q is loaded and rotated in registers, with no
+    //    barrier ahead of the first KV loads; otherwise it goes through the exact LDS path.
+    float qr[G][EPL];
+    const bool reg_prologue =
+        a.qnw == nullptr && (a.cos_row == nullptr || a.rope_type == 0 || 2 * a.half_rope == D);
+    if (reg_prologue) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int c = 0; c < C4; ++c) {
+                const float4 x =
+                    reinterpret_cast<const float4*>(a.q + (h0 + h) * D)[c * LPR + j];
+                qr[h][4 * c + 0] = x.x;
+                qr[h][4 * c + 1] = x.y;
+                qr[h][4 * c + 2] = x.z;
+                qr[h][4 * c + 3] = x.w;
+            }
+        if (a.cos_row != nullptr) rope_registers<D, G, EPL>(qr, j, a);
+    } else {
+        for (int i = tid; i < G * D; i += NTHR) s_x[i] = a.q[h0 * D + i];
+        __syncthreads();
+        prep_heads_lds<D, NTHR>(s_x, G, G, a.qnw, a.knw, s_acc, s_r, a, tid);
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) qr[h][e] = s_x[h * D + F::dim(j, e)];
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) qr[h][e] = qr[h][e] * a.qk_scale;
+
+    float m[G], l[G], o[G][EPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        m[h] = kNegBig;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[h][e] = 0.0f;
+    }
+
+    // 2. Stream the cached rows [row_begin, cache_end).
+    for (int base = row_begin + wave * ROWS_WAVE; base < cache_end; base += ROWS_BLOCK) {
+        float4 kf[U][C4], vf[U][C4];
+        bool valid[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = base + u * RPW + grp;
+            valid[u] = t < cache_end;
+            const int tt = valid[u] ? t : cache_end - 1;  // in-bounds address for masked rows
+            const float4* kp = reinterpret_cast<const float4*>(kplane + (long long)tt * D) + j;
+            const float4* vp = reinterpret_cast<const float4*>(vplane + (long long)tt * D) + j;
+#pragma unroll
+            for (int c = 0; c < C4; ++c) kf[u][c] = load4<NT>(kp + c * LPR);
+#pragma unroll
+            for (int c = 0; c < C4; ++c) vf[u][c] = load4<NT>(vp + c * LPR);
+        }
+        accumulate_rows<D, G, EPL, U>(qr, kf, vf, valid, m, l, o, a);
+    }
+
+    // 3. The split that owns row `pos`: prepare k exactly, append K/V (KVCache.storeK/storeV),
+    //    and take row `pos` from LDS (row group 0 of wave 0).
+    if (has_pos) {
+        for (int i = tid; i < D; i += NTHR) {
+            s_x[G * D + i] = a.k[kvh * D + i];
+            s_v[i] = a.v[kvh * D + i];
+        }
+        __syncthreads();
+        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, a.qnw, a.knw, s_acc, s_r, a, tid);
+        for (int i = tid; i < D; i += NTHR) {
+            kplane[(long long)a.pos * D + i] = s_x[G * D + i];
+            vplane[(long long)a.pos * D + i] = s_v[i];
+        }
+        if (wave == 0) {
+            float4 kf[1][C4], vf[1][C4];
+            bool valid[1] = {grp == 0};
+#pragma unroll
+            for (int c = 0; c < C4; ++c) {
+                const int d0 = c * LPR * 4 + j * 4;
+                kf[0][c] = make_float4(s_x[G * D + d0], s_x[G * D + d0 + 1], s_x[G * D + d0 + 2],
+                                       s_x[G * D + d0 + 3]);
+                vf[0][c] = make_float4(s_v[d0], s_v[d0 + 1], s_v[d0 + 2], s_v[d0 + 3]);
+            }
+            accumulate_rows<D, G, EPL, 1>(qr, kf, vf, valid, m, l, o, a);
+        }
+    }
+
+    // 4. Merge the row groups of each wave (lanes j, j+LPR, ...), then the waves via LDS.
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float mw = m[h];
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off));
+        const float sc = fast_exp2(m[h] - mw);
+        float lw = l[h] * sc;
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) lw = lw + __shfl_xor(lw, off);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float x = o[h][e] * sc;
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) x = x + __shfl_xor(x, off);
+            o[h][e] = x;
+        }
+        m[h] = mw;
+        l[h] = lw;
+    }
+    if (grp == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) s_o[(wave * G + h) * D + F::dim(j, e)] = o[h][e];
+            if (j == 0) {
+                s_m[wave * G + h] = m[h];
+                s_l[wave * G + h] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+
+    for (int idx = tid; idx < G * D; idx += NTHR) {
+        const int h = idx / D, d = idx - h * D;
+        float M = s_m[h];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w * G + h]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float sc = fast_exp2(s_m[w * G + h] - M);
+            L = __builtin_fmaf(s_l[w * G + h], sc, L);
+            O = __builtin_fmaf(s_o[(w * G + h) * D + d], sc, O);
+        }
+        if (a.splits == 1) {
+            a.out[(h0 + h) * D + d] = O / L;
+        } else {
+            const long long slot = ((long long)kvh * a.splits + split) * G + h;
+            a.part_o[slot * D + d] = O;
+            if (d == 0) {
+                a.part_ml[2 * slot] = M;
+                a.part_ml[2 * slot + 1] = L;
+            }
+        }
+    }
+}
+
+// Combine of the splits: one block per query head; thread (column c, split group p) owns float4 column c of the head's output for the
+// splits p, p+NP, ...  Every load of a thread is issued up front (one memory round trip),
+// the per-group maxima and sums are merged through LDS.
+constexpr int kReduceThreads = 256;
+
+template <int D>
+__global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArgs a, int G) {
+    constexpr int NC = D / 4;                 // float4 columns
+    constexpr int NP = kReduceThreads / NC;   // split groups
+    __shared__ float s_m[NP], s_l[NP];
+    __shared__ float4 s_o[NP][NC];
+    const int hq = blockIdx.x;
+    const int kvh = hq / G, h = hq - kvh * G;
+    const int tid = threadIdx.x;
+    const int c = tid % NC, p = tid / NC;
+    const int S = a.splits;
+    const long long slot0 = (long long)kvh * S * G + h;  // slot of split j: slot0 + j*G
+
+    // Online merge over this thread's splits (loads are independent of the running max).
+    float m = kNegBig, l = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int jj = p; jj < S; jj += NP) {
+        const long long slot = slot0 + (long long)jj * G;
+        const float mj = a.part_ml[2 * slot], lj = a.part_ml[2 * slot + 1];
+        const float4 oj = reinterpret_cast<const float4*>(a.part_o + slot * D)[c];
+        const float mn = fmaxf(m, mj);
+        const float so = fast_exp2(m - mn), sj = fast_exp2(mj - mn);
+        l = __builtin_fmaf(l, so, lj * sj);
+        o.x = __builtin_fmaf(o.x, so, oj.x * sj);
+        o.y = __builtin_fmaf(o.y, so, oj.y * sj);
+        o.z = __builtin_fmaf(o.z, so, oj.z * sj);
+        o.w = __builtin_fmaf(o.w, so, oj.w * sj);
+        m = mn;
+    }
+    if (c == 0) {
+        s_m[p] = m;
+        s_l[p] = l;
+    }
+    s_o[p][c] = o;
+    __syncthreads();
+    if (p == 0) {
+        float M = s_m[0];
+        for (int q = 1; q < NP; ++q) M = fmaxf(M, s_m[q]);
+        float L = 0.0f;
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < NP; ++q) {
+            const float sc = fast_exp2(s_m[q] - M);
+            L = __builtin_fmaf(s_l[q], sc, L);
+            const float4 x = s_o[q][c];
+            O.x = __builtin_fmaf(x.x, sc, O.x);
+            O.y = __builtin_fmaf(x.y, sc, O.y);
+            O.z = __builtin_fmaf(x.z, sc, O.z);
+            O.w = __builtin_fmaf(x.w, sc, O.w);
+        }
+        const float inv = 1.0f / L;
+        O.x = O.x * inv;
+        O.y = O.y * inv;
+        O.z = O.z * inv;
+        O.w = O.w * inv;
+        reinterpret_cast<float4*>(a.out + (long long)hq * D)[c] = O;
+    }
+}
+
+}  // namespace dk
+}  // namespace llmp

@@ -40,9 +40,10 @@ struct DecodeArgs {
 };
 
 // Launches the split-K kernel for head_dim D and GQA group G = Hq/Hkv on grid
-// (splits, Hkv).  Returns hipErrorInvalidValue for an unsupported (D, G).
+// (splits, Hkv) with `waves` (4 or 8) waves per workgroup.  Returns hipErrorInvalidValue for
+// an unsupported shape.  With splits > 1, launch_decode_reduce must follow.
 hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads,
-                               hipStream_t stream);
+                               int waves, hipStream_t stream);
 // Launches the log-sum-exp combine of the splits: one block per query head.
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,
                                 hipStream_t stream);

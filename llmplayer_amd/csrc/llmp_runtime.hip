@@ -165,16 +165,25 @@ int prof_fold(KvHandle* kv, int kind) {
     return LLMP_OK;
 }
 
-// Number of splits when the caller leaves the choice to the library: enough workgroups to
-// give every CU several (the chip has n_cu CUs in 8 XCDs), but never fewer than 64 rows per
-// split, where the per-workgroup prologue and merge would dominate.
-int auto_splits(int n, int n_kv_heads, int n_cu) {
-    const int target_wgs = 4 * (n_cu > 0 ? n_cu : 256);
-    int s = (target_wgs + n_kv_heads - 1) / n_kv_heads;
-    const int by_rows = n / 64 > 0 ? n / 64 : 1;
+// Number of splits when the caller leaves the choice to the library, from sweeps over the
+// BASELINE shapes on MI355X (256 CUs in 8 XCDs): about one workgroup per CU, at least 32 rows
+// per split (below that the per-workgroup prologue and merge dominate) and at most 128 splits
+// per KV head.  Very long splits (>= 1024 rows) run 8-wave workgroups on 3/4 as many splits:
+// fewer concurrent KV streams, each read by more waves, keep HBM closer to its peak.
+void auto_launch(int n, int n_kv_heads, int n_cu, int* splits, int* waves) {
+    const int cu = n_cu > 0 ? n_cu : 256;
+    int s = (cu + n_kv_heads - 1) / n_kv_heads;
+    const int by_rows = n / 32 > 0 ? n / 32 : 1;
     if (s > by_rows) s = by_rows;
-    if (s > kMaxSplits) s = kMaxSplits;
-    return s < 1 ? 1 : s;
+    if (s > 128) s = 128;
+    if (s < 1) s = 1;
+    int w = 4;
+    if (n / s >= 1024) {
+        w = 8;
+        s = (3 * s + 3) / 4;
+    }
+    *splits = s;
+    *waves = w;
 }
 
 }  // namespace
@@ -628,6 +637,8 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
     if (!c.configured)
         return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
     if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode: null buffer");
+    if ((q | k | v | out) & 15)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode: q/k/v/out must be 16-byte aligned");
     if (splits > kMaxSplits)
         return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
 
@@ -658,7 +669,9 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
     if (c.window > 0 && !c.is_global) start = position - c.window + 1 > 0 ? position - c.window + 1 : 0;
     a.t_start = start;
     const int n = position + 1 - start;
-    int s = splits > 0 ? splits : auto_splits(n, Hkv, G().n_cu);
+    int s = splits, waves = 4;
+    if (s <= 0) auto_launch(n, Hkv, G().n_cu, &s, &waves);
+    else if (n / s >= 1024) waves = 8;
     if (s > n) s = n;
     // Rows per split rounded to 16 so splits start on aligned rows; then drop empty splits.
     int rps = (n + s - 1) / s;
@@ -686,7 +699,7 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
         if (int rc = prof_event(kv, &e1)) return rc;
         LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
     }
-    LLMP_HIP_CHECK(launch_decode_split(a, D, group, Hkv, st), "decode split-K launch");
+    LLMP_HIP_CHECK(launch_decode_split(a, D, group, Hkv, waves, st), "decode split-K launch");
     if (kv->prof_on) {
         LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
         kv->prof_pending[LLMP_PROF_DECODE_SPLIT].push_back({e0, e1});
@@ -707,6 +720,45 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
         for (int kind = 0; kind < LLMP_PROF_KINDS; ++kind)
             if (int rc = prof_fold(kv, kind)) return rc;
     }
+    return LLMP_OK;
+}
+
+// ---- graph capture ---------------------------------------------------------------------------------
+int llmp_graph_begin(uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    for (auto& kv : G().handles)
+        if (kv.second->prof_on)
+            return fail(LLMP_ERR_INVALID_ARG, "llmp_graph_begin: turn profiling off before capturing");
+    LLMP_HIP_CHECK(hipStreamBeginCapture(pick_stream(stream), hipStreamCaptureModeThreadLocal),
+                   "hipStreamBeginCapture");
+    return LLMP_OK;
+}
+
+int llmp_graph_end(uint64_t stream, uint64_t* graph) {
+    if (int rc = ensure_init()) return rc;
+    if (!graph) return fail(LLMP_ERR_INVALID_ARG, "llmp_graph_end: null out");
+    hipGraph_t g = nullptr;
+    LLMP_HIP_CHECK(hipStreamEndCapture(pick_stream(stream), &g), "hipStreamEndCapture");
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    LLMP_HIP_CHECK(e, "hipGraphInstantiate");
+    *graph = reinterpret_cast<uint64_t>(ge);
+    return LLMP_OK;
+}
+
+int llmp_graph_launch(uint64_t graph, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    if (!graph) return fail(LLMP_ERR_INVALID_ARG, "llmp_graph_launch: null graph");
+    LLMP_HIP_CHECK(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph), pick_stream(stream)),
+                   "hipGraphLaunch");
+    return LLMP_OK;
+}
+
+int llmp_graph_destroy(uint64_t graph) {
+    if (int rc = ensure_init()) return rc;
+    if (!graph) return fail(LLMP_ERR_INVALID_ARG, "llmp_graph_destroy: null graph");
+    LLMP_HIP_CHECK(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph)), "hipGraphExecDestroy");
     return LLMP_OK;
 }
 

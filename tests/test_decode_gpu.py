@@ -53,8 +53,9 @@ def c3(request):
     fp.close()
 
 
-@pytest.mark.parametrize("splits", [0, 8, 16, 32, 64, 128])
+@pytest.mark.parametrize("splits", [0, 8, 16, 32, 64, 128, 1000])
 def test_c3_llama3b_split_sweep(c3, splits):
+    # 8..32 splits at ctx 32768 run 8-wave workgroups (>= 1024 rows per split), the rest 4.
     c, n, d, ref, fp = c3
     _run(fp, c, n, d, 0, n - 1, splits, f"C3 Llama-3.2-3B ctx {n}", check_cache=(splits == 0),
          oracle=ref)
@@ -205,12 +206,47 @@ def test_profile_counters_count_launches():
         fp.uploadQKV(d.q, d.k, d.v)
         _lib.call("llmp_profile_enable", fp.kv.handle, 1)
         for _ in range(5):
-            fp.forwardAttentionPart(0, 4095, 32)
+            fp.forwardAttentionPart(0, 4095, 32)     # split kernel + combine kernel
+        for _ in range(3):
+            fp.forwardAttentionPart(0, 4095, 1)      # one split: no combine kernel
         cnt, ms = C.c_int(), C.c_double()
         _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(cnt), C.byref(ms))
-        assert cnt.value == 5 and ms.value > 0
+        assert cnt.value == 8 and ms.value > 0
         _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_REDUCE, C.byref(cnt), C.byref(ms))
         assert cnt.value == 5
         _lib.call("llmp_profile_reset", fp.kv.handle)
         _lib.call("llmp_profile_read", fp.kv.handle, 0, C.byref(cnt), C.byref(ms))
         assert cnt.value == 0
+
+
+@pytest.mark.parametrize("splits", [0, 1, 1000])
+def test_graph_replay_matches_eager(splits):
+    """Decode calls captured into a HIP graph (llmp_graph_*) give the eager results on every
+    replay, with other eager work and synchronisations between replays."""
+    c = hfp.ModelConfig(24, 8, 128, 3, rope_freq_base=500000.0)
+    d = dc.make_layer(c, 4096, 4095, seed=77, k_scale=0.5)
+    with hfp.HipForwardPass(c, 4096) as fp:
+        for layer in range(3):
+            fp.kv.write(layer, 0, d.kc, d.vc)
+        fp.uploadQKV(d.q, d.k, d.v)
+        fp.forwardAttentionPart(0, 4095, splits)
+        eager = fp.downloadXb2()
+        out, _, _ = dc.oracle_call(c, 4096, d, 0, 4095)
+        dc.compare_out(eager, out, "eager before capture")
+        g = C.c_uint64()
+        _lib.call("llmp_graph_begin", 0)
+        fp.forwardAttentionPart(1, 4095, splits)
+        fp.forwardAttentionPart(0, 4095, splits)
+        _lib.call("llmp_graph_end", 0, C.byref(g))
+        try:
+            for rep in range(4):
+                dc.log(f"[gpu] graph replay {rep} splits={splits}")
+                fp.forwardAttentionPart(2, 4095, splits)       # eager work between replays
+                fp.sync()
+                _lib.call("llmp_graph_launch", g.value, 0)
+                fp.sync()
+                got = fp.downloadXb2()
+                assert np.array_equal(got, eager), f"replay {rep} differs from eager"
+        finally:
+            _lib.call("llmp_graph_destroy", g.value)
+        dc.compare_cache(fp, 0, *dc.oracle_call(c, 4096, d, 0, 4095)[1:], "cache after replays")
