@@ -64,6 +64,7 @@ def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int) -
                      rng.standard_normal(c.kv_dim, dtype=np.float32))
         pos = ctx - 1
         h = fp.kv.handle
+        plan = fp.decodePlan(0, pos, splits)
         for i in range(warmup):
             fp.forwardAttentionPart(i % n_layers, pos, splits)
         fp.sync()
@@ -117,7 +118,7 @@ def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int) -
             "us_per_layer_call": ms_per_step * 1e3,
             "kv_read_gbps": per_layer / (ms_per_step * 1e-3) / 1e9,
             "split_kernel_us": split_ms * 1e3, "reduce_kernel_us": reduce_ms * 1e3,
-            "split_launches": res["split"][0]}
+            "split_launches": res["split"][0], "plan": plan}
 
 
 def cpu_baseline(ctx: int, seconds: float) -> dict:
@@ -158,6 +159,53 @@ def cpu_baseline(ctx: int, seconds: float) -> dict:
             "us_per_layer_call": med * 1e6}
 
 
+def copy_calibration(mib: int) -> int:
+    """A kernel of known traffic: mib MiB read and mib MiB written per launch."""
+    from llmplayer_amd import _lib
+    from llmplayer_amd.hip_forward_pass import DeviceBuffer
+    n = mib * 2**20
+    src, dst = DeviceBuffer(n), DeviceBuffer(n)
+    for _ in range(5):
+        _lib.call("llmp_copy_kernel", dst.ptr, src.ptr, n, 0)
+    _lib.call("llmp_stream_sync", 0)
+    src.free()
+    dst.free()
+    log(f"[bench] copy calibration: 5 launches x {mib} MiB read + {mib} MiB written")
+    return 0
+
+
+def profile_workload(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int) -> int:
+    """Eager layer-calls only (the decode kernels as rocprofv3 sees them one by one)."""
+    from llmplayer_amd import hip_forward_pass as hfp
+    per_layer = kv_bytes(ctx)
+    n_layers = max(1, math.ceil(rotate_bytes / per_layer))
+    c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
+    fp = hfp.HipForwardPass(c, ctx)
+    try:
+        rng = np.random.default_rng(2024)
+        kc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32) * np.float32(0.5)
+        vc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32)
+        for layer in range(n_layers):
+            fp.kv.write(layer, 0, kc, vc)
+        fp.uploadQKV(rng.standard_normal(c.q_dim, dtype=np.float32),
+                     rng.standard_normal(c.kv_dim, dtype=np.float32) * np.float32(0.5),
+                     rng.standard_normal(c.kv_dim, dtype=np.float32))
+        plan = fp.decodePlan(0, ctx - 1, splits)
+        for i in range(warmup + steps):
+            fp.forwardAttentionPart(i % n_layers, ctx - 1, splits)
+        fp.sync()
+    finally:
+        fp.close()
+    log(f"[bench] profile workload: ctx {ctx}, {warmup}+{steps} eager layer-calls over "
+        f"{n_layers} layer caches, plan {plan}")
+    return 0
+
+
+def kernel_name(plan: dict) -> str:
+    """The split kernel instantiation the library launches for the C3 shape (D=128, G=3)."""
+    return f"decode_split_kernel<128, 3, 8, 2, {plan['waves']}, true>"
+
+
 def traffic_from_profiles(ctx: int):
     """HBM bytes per launch of the split kernel from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), if present."""
@@ -165,7 +213,7 @@ def traffic_from_profiles(ctx: int):
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        return json.load(f).get("hbm_bytes_per_launch")  # FETCH+WRITE, copy-calibrated
 
 
 def main() -> int:
@@ -179,6 +227,12 @@ def main() -> int:
     ap.add_argument("--rotate-gib", type=float, default=2.0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-workload", action="store_true",
+                    help="for rocprofv3: only the warm-up and K eager layer-calls at --ctx "
+                         "(no graph replay, no second context, no CPU baseline), then exit")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="for rocprofv3 PMC calibration: 5 launches of the library's plain "
+                         "copy kernel over MIB MiB, then exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -190,6 +244,11 @@ def main() -> int:
 
     from llmplayer_amd import hip_forward_pass as hfp
     hfp.init(0)
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
+    if args.profile_workload:
+        return profile_workload(args.ctx, args.steps, args.warmup, args.splits,
+                                int(args.rotate_gib * 2**30))
     info = hfp.device_info()
     log(f"[bench] device {info['arch']} with {info['n_cu']} CUs")
     rot = int(args.rotate_gib * 2**30)
@@ -206,7 +265,7 @@ def main() -> int:
     achieved = B / (main_run["split_kernel_us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic_from_profiles(args.ctx),
-                "kernel": "decode_split_kernel<128,3,16,2>",
+                "kernel": kernel_name(main_run["plan"]),
                 "algorithmic_bytes_per_launch": B,
                 "kernel_mean_us": round(main_run["split_kernel_us"], 3)}
     cpu = None
@@ -229,7 +288,8 @@ def main() -> int:
         "data": "synthetic N(0,1) Q/K/V and KV cache (K x 0.5), seeded",
         "config": {"workload": f"C3 Llama-3.2-3B decode attention, ctx {args.ctx}",
                    "heads_q": HQ, "heads_kv": HKV, "head_dim": D, "ctx": args.ctx,
-                   "splits": args.splits or "auto", "kv_layers_rotated": main_run["n_layers"]},
+                   "splits": main_run["plan"]["splits"], "waves": main_run["plan"]["waves"],
+                   "kv_layers_rotated": main_run["n_layers"]},
         "us_per_layer_call": round(main_run["us_per_layer_call"], 3),
         "kv_read_pct_of_hbm_peak": round(100 * main_run["kv_read_gbps"] / PEAK_GBPS, 2),
         "reduce_kernel_us": round(main_run["reduce_kernel_us"], 3),

@@ -147,6 +147,11 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
 int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint64_t k,
                      uint64_t v, uint64_t out, int splits, uint64_t stream);
 
+/* Launch plan llmp_attn_decode would use for this call: splits per KV head, waves per
+ * workgroup (4 or 8), rows per split and the first attended position.  Any out may be NULL. */
+int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int *out_splits,
+                     int *out_waves, int *out_rows_per_split, int *out_start);
+
 /* ---- graph capture (CudaContext.beginCapture / endCapture / launchGraph,
  *      CudaContext.java:585-613): record a sequence of launches on a stream once, replay it
  *      with one call.  Arguments (positions included) are frozen at capture time. ---------- */

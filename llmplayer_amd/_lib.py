@@ -61,6 +61,8 @@ SIGNATURES = {
     "llmp_layer_config": [_u64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
                           _f32, _pf, _pf],
     "llmp_attn_decode": [_u64, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
+    "llmp_decode_plan": [_u64, _i32, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32),
+                         C.POINTER(_i32), C.POINTER(_i32)],
     "llmp_graph_begin": [_u64],
     "llmp_graph_end": [_u64, _pu64],
     "llmp_graph_launch": [_u64, _u64],

@@ -186,6 +186,35 @@ void auto_launch(int n, int n_kv_heads, int n_cu, int* splits, int* waves) {
     *waves = w;
 }
 
+struct Plan {
+    int start;           // first attended position
+    int n;               // attended rows
+    int splits;          // split-K partitions per KV head
+    int rows_per_split;
+    int waves;           // waves per workgroup
+};
+
+// Launch plan of one decode call: window start (Attention.java:330-335: local layers attend
+// to the last `window` rows), splits and workgroup size.
+Plan make_plan(const LayerCfg& c, int position, int splits_req, int n_kv_heads) {
+    Plan p{};
+    p.start = 0;
+    if (c.window > 0 && !c.is_global) p.start = position - c.window + 1 > 0 ? position - c.window + 1 : 0;
+    p.n = position + 1 - p.start;
+    int s = splits_req, waves = 4;
+    if (s <= 0) auto_launch(p.n, n_kv_heads, G().n_cu, &s, &waves);
+    else if (p.n / s >= 1024) waves = 8;
+    if (s > p.n) s = p.n;
+    // Rows per split rounded to 16 so splits start on aligned rows; then drop empty splits.
+    int rps = (p.n + s - 1) / s;
+    if (p.n >= 16 * s) rps = (rps + 15) & ~15;
+    s = (p.n + rps - 1) / rps;
+    p.splits = s;
+    p.rows_per_split = rps;
+    p.waves = waves;
+    return p;
+}
+
 }  // namespace
 }  // namespace llmp
 
@@ -643,6 +672,8 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
         return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
 
     const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    const Plan plan = make_plan(c, position, splits, Hkv);
+    const int s = plan.splits, waves = plan.waves;
     DecodeArgs a{};
     a.q = reinterpret_cast<const float*>(q);
     a.k = reinterpret_cast<const float*>(k);
@@ -664,20 +695,8 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
     a.part_ml = kv->part_ml;
     a.head_stride = (long long)kv->max_seq * D;
     a.pos = position;
-    // Window start (Attention.java:330-335): local layers attend to the last `window` rows.
-    int start = 0;
-    if (c.window > 0 && !c.is_global) start = position - c.window + 1 > 0 ? position - c.window + 1 : 0;
-    a.t_start = start;
-    const int n = position + 1 - start;
-    int s = splits, waves = 4;
-    if (s <= 0) auto_launch(n, Hkv, G().n_cu, &s, &waves);
-    else if (n / s >= 1024) waves = 8;
-    if (s > n) s = n;
-    // Rows per split rounded to 16 so splits start on aligned rows; then drop empty splits.
-    int rps = (n + s - 1) / s;
-    if (n >= 16 * s) rps = (rps + 15) & ~15;
-    s = (n + rps - 1) / rps;
-    a.rows_per_split = rps;
+    a.t_start = plan.start;
+    a.rows_per_split = plan.rows_per_split;
     a.splits = s;
     a.rope_type = c.rope_type;
     a.eps = c.eps;
@@ -720,6 +739,27 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
         for (int kind = 0; kind < LLMP_PROF_KINDS; ++kind)
             if (int rc = prof_fold(kv, kind)) return rc;
     }
+    return LLMP_OK;
+}
+
+int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* out_splits,
+                     int* out_waves, int* out_rows_per_split, int* out_start) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (position < 0 || position >= kv->max_seq)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "position %d outside [0, %d)", position, kv->max_seq);
+    const LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    if (splits > kMaxSplits)
+        return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
+    const Plan p = make_plan(c, position, splits, kv->n_kv_heads);
+    if (out_splits) *out_splits = p.splits;
+    if (out_waves) *out_waves = p.waves;
+    if (out_rows_per_split) *out_rows_per_split = p.rows_per_split;
+    if (out_start) *out_start = p.start;
     return LLMP_OK;
 }
 

@@ -311,6 +311,14 @@ class HipForwardPass:
         self.forwardAttentionPart(layerIdx, position, splits)
         state.xb2[:] = self.downloadXb2()
 
+    def decodePlan(self, layerIdx: int, position: int, splits: int = 0) -> dict:
+        """The launch llmp_attn_decode would make for this call."""
+        sp, wv, rps, st = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        call("llmp_decode_plan", self.kv.handle, layerIdx, position, splits, C.byref(sp),
+             C.byref(wv), C.byref(rps), C.byref(st))
+        return {"splits": sp.value, "waves": wv.value, "rows_per_split": rps.value,
+                "start": st.value}
+
     def downloadXb2(self) -> np.ndarray:
         return self.gpuXb2.download(np.float32, self.config.q_dim)
 
