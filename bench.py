@@ -121,6 +121,72 @@ def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int) -
             "split_launches": res["split"][0], "plan": plan}
 
 
+def prefill_run(P: int, steps: int) -> dict:
+    """C5: prefill attention of P prompt tokens (Llama-3.2-1B shape 32/8/64, bf16 Q/K/V
+    N(0,1), causal) in one llmp_attn_prefill call (exact K/V append + MFMA attention).
+    Timed as a graph replay of `steps` calls; per-kernel means from an eager profiled pass."""
+    from llmplayer_amd import _lib
+    from llmplayer_amd import hip_forward_pass as hfp
+    c = hfp.ModelConfig(32, 8, 64, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
+    fp = hfp.HipForwardPass(c, P)
+    bufs = []
+    try:
+        rng = np.random.default_rng(5)
+        arrs = [hfp.to_bf16(rng.standard_normal((P, n), dtype=np.float32))
+                for n in (c.q_dim, c.kv_dim, c.kv_dim)]
+        for a in arrs:
+            b = hfp.DeviceBuffer(a.nbytes)
+            b.upload(a)
+            bufs.append(b)
+        out = hfp.DeviceBuffer(P * c.q_dim * 4)
+        bufs.append(out)
+        args = (fp.kv.handle, 0, 0, P, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, out.ptr, 0)
+        for _ in range(3):
+            _lib.call("llmp_attn_prefill", *args)
+        g = C.c_uint64()
+        _lib.call("llmp_graph_begin", 0)
+        for _ in range(steps):
+            _lib.call("llmp_attn_prefill", *args)
+        _lib.call("llmp_graph_end", 0, C.byref(g))
+        _lib.call("llmp_graph_launch", g.value, 0)
+        _lib.call("llmp_stream_sync", 0)
+        e0, e1 = C.c_uint64(), C.c_uint64()
+        _lib.call("llmp_event_create", C.byref(e0))
+        _lib.call("llmp_event_create", C.byref(e1))
+        _lib.call("llmp_event_record", e0.value, 0)
+        _lib.call("llmp_graph_launch", g.value, 0)
+        _lib.call("llmp_event_record", e1.value, 0)
+        _lib.call("llmp_event_sync", e1.value)
+        ms = C.c_float()
+        _lib.call("llmp_event_elapsed_ms", C.byref(ms), e0.value, e1.value)
+        _lib.call("llmp_graph_destroy", g.value)
+        _lib.call("llmp_event_destroy", e0.value)
+        _lib.call("llmp_event_destroy", e1.value)
+        h = fp.kv.handle
+        _lib.call("llmp_profile_reset", h)
+        _lib.call("llmp_profile_enable", h, 1)
+        for _ in range(steps):
+            _lib.call("llmp_attn_prefill", *args)
+        _lib.call("llmp_profile_enable", h, 0)
+        res = {}
+        for kind, name in ((_lib.LLMP_PROF_PREFILL_APPEND, "append"),
+                           (_lib.LLMP_PROF_PREFILL_ATTN, "attn")):
+            cnt, tot = C.c_int(), C.c_double()
+            _lib.call("llmp_profile_read", h, kind, C.byref(cnt), C.byref(tot))
+            res[name] = tot.value / max(1, cnt.value) * 1e3
+    finally:
+        for b in bufs:
+            b.free()
+        fp.close()
+    us = ms.value / steps * 1e3
+    flops = 4.0 * c.head_count * c.head_size * P * (P + 1) / 2   # causal QK^T + PV
+    return {"P": P, "us_per_call": round(us, 2), "attn_kernel_us": round(res["attn"], 2),
+            "append_kernel_us": round(res["append"], 2),
+            "causal_tflops": round(flops / (us * 1e-6) / 1e12, 2),
+            "attn_kernel_causal_tflops": round(flops / (res["attn"] * 1e-6) / 1e12, 2),
+            "mfma_tflops_bf16x3": round(3 * flops / (res["attn"] * 1e-6) / 1e12, 2)}
+
+
 def cpu_baseline(ctx: int, seconds: float) -> dict:
     """The oracle (CPU restatement of Attention.forwardFromProjections) on one layer-call of
     the same shape, parallel over query heads; median over a bounded sample."""
@@ -227,6 +293,8 @@ def main() -> int:
     ap.add_argument("--rotate-gib", type=float, default=2.0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", dest="prefill", action="store_false",
+                    help="skip the C5 prefill measurement")
     ap.add_argument("--profile-workload", action="store_true",
                     help="for rocprofv3: only the warm-up and K eager layer-calls at --ctx "
                          "(no graph replay, no second context, no CPU baseline), then exit")
@@ -261,6 +329,13 @@ def main() -> int:
         log(f"[bench] ctx {args.ctx2}: {second['us_per_layer_call']:.2f} us/layer-call, "
             f"{second['kv_read_gbps']:.0f} GB/s, split kernel {second['split_kernel_us']:.2f} us")
 
+    prefill = []
+    if args.prefill:
+        for P in (512, 2048):
+            r = prefill_run(P, 20)
+            log(f"[bench] prefill C5 P={P}: {r['us_per_call']:.1f} us/call, attention kernel "
+                f"{r['attn_kernel_us']:.1f} us ({r['attn_kernel_causal_tflops']:.1f} causal TFLOP/s)")
+            prefill.append(r)
     B = kv_bytes(args.ctx)
     achieved = B / (main_run["split_kernel_us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
@@ -306,6 +381,8 @@ def main() -> int:
             "reduce_kernel_us": round(second["reduce_kernel_us"], 3),
             "us_per_layer_call_eager": round(second["us_per_layer_call_eager"], 3),
             "kv_layers_rotated": second["n_layers"]}
+    if prefill:
+        line["prefill_c5_llama1b"] = prefill
     print(json.dumps(line), flush=True)
     return 0
 

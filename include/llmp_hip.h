@@ -163,11 +163,28 @@ int llmp_graph_end(uint64_t stream, uint64_t *graph);
 int llmp_graph_launch(uint64_t graph, uint64_t stream);
 int llmp_graph_destroy(uint64_t graph);
 
+/* ---- prefill attention: n_tokens prompt tokens in one call --------------------------------
+ * The reference runs a prompt as n_tokens sequential single-token forwards
+ * (InferenceEngine.prefill, InferenceEngine.java:374-381; LLMEngine.java:478-480); this call
+ * computes the same attention outputs and cache rows for positions pos0 .. pos0+n_tokens-1:
+ *   q:   device bf16 [n_tokens][n_heads*head_dim]
+ *   k,v: device bf16 [n_tokens][n_kv_heads*head_dim]
+ *   out: device fp32 [n_tokens][n_heads*head_dim] (16-byte aligned)
+ * K/V rows are appended exactly as n_tokens llmp_attn_decode calls would write them (inputs
+ * widened to fp32, QK-norm and RoPE in the CPU path's float order).  Token i attends causally
+ * to rows [start(pos0+i), pos0+i] (start from the layer's sliding window), on MFMA with bf16
+ * hi/lo split operands and fp32 accumulation.  Rows before pos0 must already be in the cache.
+ * NEOX partial RoPE (rotated dims < head_dim) is LLMP_ERR_UNSUPPORTED here. */
+int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
+                      uint64_t k, uint64_t v, uint64_t out, uint64_t stream);
+
 /* ---- profiling (the reference's -Dcuda.profile section timers,
  *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */
 #define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV) */
 #define LLMP_PROF_DECODE_REDUCE  1  /* log-sum-exp combine of the splits                    */
-#define LLMP_PROF_KINDS          2
+#define LLMP_PROF_PREFILL_APPEND 2  /* prefill: exact K/V append of the prompt tokens       */
+#define LLMP_PROF_PREFILL_ATTN   3  /* prefill: MFMA causal attention                       */
+#define LLMP_PROF_KINDS          4
 /* on != 0 records a HIP event pair around every launch of the handle's kernels. */
 int llmp_profile_enable(uint64_t handle, int on);
 /* Waits for recorded launches of `kind` and returns their count and summed duration (ms)

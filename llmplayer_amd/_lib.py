@@ -24,6 +24,7 @@ LLMP_KV_F32 = 0
 LLMP_ROPE_NORMAL, LLMP_ROPE_NEOX = 0, 2
 LLMP_ROPE_SEL_NONE, LLMP_ROPE_SEL_GLOBAL, LLMP_ROPE_SEL_LOCAL = -1, 0, 1
 LLMP_PROF_DECODE_SPLIT, LLMP_PROF_DECODE_REDUCE = 0, 1
+LLMP_PROF_PREFILL_APPEND, LLMP_PROF_PREFILL_ATTN = 2, 3
 
 _u64, _i32, _f32 = C.c_uint64, C.c_int, C.c_float
 _pu64 = C.POINTER(C.c_uint64)
@@ -61,6 +62,7 @@ SIGNATURES = {
     "llmp_layer_config": [_u64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
                           _f32, _pf, _pf],
     "llmp_attn_decode": [_u64, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
+    "llmp_attn_prefill": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64],
     "llmp_decode_plan": [_u64, _i32, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32),
                          C.POINTER(_i32), C.POINTER(_i32)],
     "llmp_graph_begin": [_u64],

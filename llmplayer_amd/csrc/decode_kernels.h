@@ -147,47 +147,63 @@ __device__ __forceinline__ void accumulate_rows(const float (&qr)[G][EPL],
     }
 }
 
-// Exact prep of `nh` heads staged in LDS (x: nh*D floats): QK-norm with weights w0 for heads
-// < n_w0 and w1 for the others, then RoPE.  Must be called by the whole workgroup.
+// Per-token prep parameters shared by the decode and prefill kernels.
+struct HeadPrep {
+    const float* qnw;      // QK-norm weights for query heads [D] or nullptr (no QK-norm)
+    const float* knw;      // QK-norm weights for key heads [D]
+    float eps;
+    const float* cos_row;  // RoPE row of the token's position, or nullptr (NoPE)
+    const float* sin_row;
+    int half_rope;
+    int rope_type;         // 0 NORMAL, 2 NEOX
+};
+
+__device__ __forceinline__ HeadPrep head_prep(const DecodeArgs& a) {
+    return HeadPrep{a.qnw, a.knw, a.eps, a.cos_row, a.sin_row, a.half_rope, a.rope_type};
+}
+
+// Exact prep of `nh` heads staged in LDS (x: nh*D floats): QK-norm with weights p.qnw for
+// heads < n_w0 and p.knw for the others, then RoPE.  Must be called by the whole workgroup
+// (NTHR threads).
 template <int D, int NTHR>
-__device__ void prep_heads_lds(float* x, int nh, int n_w0, const float* w0, const float* w1,
-                               float* s_acc, float* s_r, const DecodeArgs& a, int tid) {
-    if (a.qnw != nullptr) {
-        if (tid < nh * 8) {
-            const int hh = tid >> 3, ln = tid & 7;
+__device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* s_r,
+                               const HeadPrep& p, int tid) {
+    if (p.qnw != nullptr) {
+        for (int t = tid; t < nh * 8; t += NTHR) {
+            const int hh = t >> 3, ln = t & 7;
             const float* xh = x + hh * D;
             float acc = 0.0f;
             for (int i = ln; i < D; i += 8) acc = __builtin_fmaf(xh[i], xh[i], acc);
-            s_acc[tid] = acc;
+            s_acc[t] = acc;
         }
         __syncthreads();
-        if (tid < nh) {
-            const float* ac = s_acc + tid * 8;
+        for (int t = tid; t < nh; t += NTHR) {
+            const float* ac = s_acc + t * 8;
             float ss = ac[0];
 #pragma unroll
             for (int ln = 1; ln < 8; ++ln) ss = ss + ac[ln];
-            float t = ss / (float)D;
-            t = t + a.eps;
-            const float r = (float)__builtin_sqrt((double)t);
-            s_r[tid] = 1.0f / r;
+            float v = ss / (float)D;
+            v = v + p.eps;
+            const float r = (float)__builtin_sqrt((double)v);
+            s_r[t] = 1.0f / r;
         }
         __syncthreads();
         for (int i = tid; i < nh * D; i += NTHR) {
             const int hh = i / D;
-            const float* w = (hh < n_w0) ? w0 : w1;
+            const float* w = (hh < n_w0) ? p.qnw : p.knw;
             const float xs = x[i] * s_r[hh];
             x[i] = xs * w[i - hh * D];
         }
         __syncthreads();
     }
-    if (a.cos_row != nullptr) {
-        const int half = a.half_rope;
+    if (p.cos_row != nullptr) {
+        const int half = p.half_rope;
         for (int idx = tid; idx < nh * half; idx += NTHR) {
             const int hh = idx / half, i = idx - hh * half;
             float* xh = x + hh * D;
-            const int i0 = (a.rope_type == 0) ? 2 * i : i;
-            const int i1 = (a.rope_type == 0) ? 2 * i + 1 : half + i;
-            const float c = a.cos_row[i], sn = a.sin_row[i];
+            const int i0 = (p.rope_type == 0) ? 2 * i : i;
+            const int i1 = (p.rope_type == 0) ? 2 * i + 1 : half + i;
+            const float c = p.cos_row[i], sn = p.sin_row[i];
             const float v0 = xh[i0], v1 = xh[i1];
             const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
             xh[i0] = t0 - t1;
@@ -295,7 +311,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     } else {
         for (int i = tid; i < G * D; i += NTHR) s_x[i] = a.q[h0 * D + i];
         __syncthreads();
-        prep_heads_lds<D, NTHR>(s_x, G, G, a.qnw, a.knw, s_acc, s_r, a, tid);
+        prep_heads_lds<D, NTHR>(s_x, G, G, s_acc, s_r, head_prep(a), tid);
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -342,7 +358,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             s_v[i] = a.v[kvh * D + i];
         }
         __syncthreads();
-        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, a.qnw, a.knw, s_acc, s_r, a, tid);
+        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, head_prep(a), tid);
         for (int i = tid; i < D; i += NTHR) {
             kplane[(long long)a.pos * D + i] = s_x[G * D + i];
             vplane[(long long)a.pos * D + i] = s_v[i];

@@ -50,6 +50,15 @@ hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, in
 // True when a decode kernel exists for (head_dim, group).
 bool decode_shape_supported(int head_dim, int group);
 
+namespace pk {
+struct PrefillArgs;
+}
+// Prefill: exact K/V append of all prompt tokens (one workgroup per token), then the MFMA
+// causal attention.  Both return hipErrorInvalidValue for an unsupported shape.
+hipError_t launch_prefill_append(const pk::PrefillArgs& a, int head_dim, hipStream_t stream);
+hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group,
+                               hipStream_t stream);
+
 // Plain 16-byte-per-thread copy kernel.
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);
 

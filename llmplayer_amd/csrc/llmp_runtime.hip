@@ -3,6 +3,7 @@
 // Declarations and reference citations: include/llmp_hip.h.
 #include "llmp_hip.h"
 #include "llmp_internal.h"
+#include "prefill_kernels.h"
 
 #include <cmath>
 #include <cstdarg>
@@ -75,8 +76,8 @@ struct KvHandle {
     bool prof_on = false;
     std::vector<ProfPair> prof_pending[LLMP_PROF_KINDS];
     std::vector<hipEvent_t> prof_free;
-    double prof_ms[LLMP_PROF_KINDS] = {0, 0};
-    long long prof_count[LLMP_PROF_KINDS] = {0, 0};
+    double prof_ms[LLMP_PROF_KINDS] = {};
+    long long prof_count[LLMP_PROF_KINDS] = {};
 
     float* k_plane(int layer) const { return pool + (size_t)(2 * layer) * plane_floats; }
     float* v_plane(int layer) const { return pool + (size_t)(2 * layer + 1) * plane_floats; }
@@ -760,6 +761,81 @@ int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* 
     if (out_waves) *out_waves = p.waves;
     if (out_rows_per_split) *out_rows_per_split = p.rows_per_split;
     if (out_start) *out_start = p.start;
+    return LLMP_OK;
+}
+
+// ---- prefill attention -------------------------------------------------------------------------
+int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q, uint64_t k,
+                      uint64_t v, uint64_t out, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (n_tokens <= 0 || pos0 < 0 || (long long)pos0 + n_tokens > kv->max_seq)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "prefill rows [%d, %lld) outside [0, %d)", pos0,
+                    (long long)pos0 + n_tokens, kv->max_seq);
+    const LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: null buffer");
+    if ((q | k | v) & 1 || out & 15)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: misaligned q/k/v (2 B) or out (16 B)");
+    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    pk::PrefillArgs a{};
+    a.q = reinterpret_cast<const unsigned short*>(q);
+    a.k = reinterpret_cast<const unsigned short*>(k);
+    a.v = reinterpret_cast<const unsigned short*>(v);
+    a.kc = kv->k_plane(layer);
+    a.vc = kv->v_plane(layer);
+    a.head_stride = (long long)kv->max_seq * D;
+    if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
+        const RopeTable& t = kv->rope[c.rope_sel];
+        if (!t.d_cos)
+            return fail(LLMP_ERR_INVALID_ARG, "layer %d selects a RoPE table never uploaded", layer);
+        if (c.rope_type == LLMP_ROPE_NEOX && 2 * t.half != D)
+            return fail(LLMP_ERR_UNSUPPORTED, "prefill: NEOX partial RoPE (%d of %d dims)", 2 * t.half, D);
+        a.cos_t = t.d_cos;
+        a.sin_t = t.d_sin;
+        a.half_rope = t.half;
+    }
+    a.qnw = c.d_qnw;
+    a.knw = c.d_knw;
+    a.out = reinterpret_cast<float*>(out);
+    a.pos0 = pos0;
+    a.P = n_tokens;
+    a.Hq = c.n_heads;
+    a.Hkv = Hkv;
+    a.rope_type = c.rope_type;
+    a.window = (c.window > 0 && !c.is_global) ? c.window : 0;
+    a.eps = c.eps;
+    const float scale = c.scale > 0.0f ? c.scale : (float)(1.0 / std::sqrt((double)D));
+    const float log2e = 1.4426950408889634f;
+    if (c.softcap > 0.0f) {
+        a.qk_scale = scale;
+        a.softcap = c.softcap;
+        a.softcap_log2e = c.softcap * log2e;
+        a.inv_softcap = 1.0f / c.softcap;
+    } else {
+        a.qk_scale = scale * log2e;
+    }
+    hipStream_t st = pick_stream(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr, e3 = nullptr;
+    if (kv->prof_on) {
+        for (hipEvent_t* e : {&e0, &e1, &e2, &e3})
+            if (int rc = prof_event(kv, e)) return rc;
+        LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
+    }
+    LLMP_HIP_CHECK(launch_prefill_append(a, D, st), "prefill append launch");
+    if (kv->prof_on) {
+        LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
+        kv->prof_pending[LLMP_PROF_PREFILL_APPEND].push_back({e0, e1});
+        LLMP_HIP_CHECK(hipEventRecord(e2, st), "hipEventRecord");
+    }
+    LLMP_HIP_CHECK(launch_prefill_attn(a, D, group, st), "prefill attention launch");
+    if (kv->prof_on) {
+        LLMP_HIP_CHECK(hipEventRecord(e3, st), "hipEventRecord");
+        kv->prof_pending[LLMP_PROF_PREFILL_ATTN].push_back({e2, e3});
+    }
     return LLMP_OK;
 }
 

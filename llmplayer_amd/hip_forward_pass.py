@@ -127,6 +127,18 @@ def _fp(a: Optional[np.ndarray]):
     return a.ctypes.data_as(_F)
 
 
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), round to nearest even."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def from_bf16(b: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32 (exact)."""
+    return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
 def rope_table(rope_dim: int, max_seq: int, theta: float, linear_freq_scale: float = 1.0,
                freq_factors: Optional[np.ndarray] = None):
     """cos/sin tables [max_seq][rope_dim/2] built as the RoPE constructor builds them
@@ -310,6 +322,30 @@ class HipForwardPass:
         self.uploadQKV(state.q, state.k, state.v)
         self.forwardAttentionPart(layerIdx, position, splits)
         state.xb2[:] = self.downloadXb2()
+
+    def prefill(self, layerIdx: int, pos0: int, q_bf16: np.ndarray, k_bf16: np.ndarray,
+                v_bf16: np.ndarray) -> np.ndarray:
+        """Attention for a prompt of P tokens at positions pos0..pos0+P-1 in one call (the
+        reference runs P sequential forwards, InferenceEngine.java:374-381).  Inputs are bf16
+        bit patterns (uint16) [P, Hq*D] / [P, kvDim]; returns fp32 [P, Hq*D]."""
+        c = self.config
+        q16 = np.ascontiguousarray(q_bf16, np.uint16).reshape(-1, c.q_dim)
+        k16 = np.ascontiguousarray(k_bf16, np.uint16).reshape(-1, c.kv_dim)
+        v16 = np.ascontiguousarray(v_bf16, np.uint16).reshape(-1, c.kv_dim)
+        P = q16.shape[0]
+        assert k16.shape[0] == P and v16.shape[0] == P
+        bq, bk, bv = DeviceBuffer(q16.nbytes), DeviceBuffer(k16.nbytes), DeviceBuffer(v16.nbytes)
+        bo = DeviceBuffer(P * c.q_dim * 4)
+        try:
+            bq.upload(q16)
+            bk.upload(k16)
+            bv.upload(v16)
+            call("llmp_attn_prefill", self.kv.handle, layerIdx, pos0, P, bq.ptr, bk.ptr, bv.ptr,
+                 bo.ptr, 0)
+            return bo.download(np.float32, P * c.q_dim).reshape(P, c.q_dim)
+        finally:
+            for b in (bq, bk, bv, bo):
+                b.free()
 
     def decodePlan(self, layerIdx: int, position: int, splits: int = 0) -> dict:
         """The launch llmp_attn_decode would make for this call."""
