@@ -147,6 +147,16 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
 int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint64_t k,
                      uint64_t v, uint64_t out, int splits, uint64_t stream);
 
+/* The same layer-call with the position read from device memory when the kernels run:
+ * d_position points to an int32 holding the position (the reference's tokenParams[0],
+ * CudaForwardPass.java:138-141, written per token by uploadXAndUpdateParams, :1283-1292).
+ * The launch is planned for the longest step of the layer (position max_seq-1), so one
+ * capture of this call (llmp_graph_*) replays correctly at every position: the kernels derive
+ * the window, rows per split and the splits actually used from the device value.  A device
+ * position outside [0, max_seq) makes the call a no-op (nothing is read or written). */
+int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uint64_t q,
+                            uint64_t k, uint64_t v, uint64_t out, int splits, uint64_t stream);
+
 /* Launch plan llmp_attn_decode would use for this call: splits per KV head, waves per
  * workgroup (4 or 8), rows per split and the first attended position.  Any out may be NULL. */
 int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int *out_splits,

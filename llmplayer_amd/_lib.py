@@ -62,6 +62,7 @@ SIGNATURES = {
     "llmp_layer_config": [_u64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
                           _f32, _pf, _pf],
     "llmp_attn_decode": [_u64, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
+    "llmp_attn_decode_devpos": [_u64, _i32, _u64, _u64, _u64, _u64, _u64, _i32, _u64],
     "llmp_attn_prefill": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64],
     "llmp_decode_plan": [_u64, _i32, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32),
                          C.POINTER(_i32), C.POINTER(_i32)],

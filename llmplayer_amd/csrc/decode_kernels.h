@@ -158,8 +158,16 @@ struct HeadPrep {
     int rope_type;         // 0 NORMAL, 2 NEOX
 };
 
-__device__ __forceinline__ HeadPrep head_prep(const DecodeArgs& a) {
-    return HeadPrep{a.qnw, a.knw, a.eps, a.cos_row, a.sin_row, a.half_rope, a.rope_type};
+__device__ __forceinline__ HeadPrep head_prep(const DecodeArgs& a, int pos) {
+    const long long row = (long long)pos * a.half_rope;
+    return HeadPrep{a.qnw, a.knw, a.eps, a.cos_t ? a.cos_t + row : nullptr,
+                    a.sin_t ? a.sin_t + row : nullptr, a.half_rope, a.rope_type};
+}
+
+// Position of this step: the host value, or the device word (read once per thread; all
+// threads read the same value).
+__device__ __forceinline__ int step_position(const DecodeArgs& a) {
+    return a.d_pos != nullptr ? *a.d_pos : a.pos;
 }
 
 // Exact prep of `nh` heads staged in LDS (x: nh*D floats): QK-norm with weights p.qnw for
@@ -216,7 +224,7 @@ __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* 
 // Rotation of the lane's own q slice in registers (no QK-norm; NORMAL pairs sit inside one
 // 16-byte chunk, NEOX pairs (i, i+D/2) in chunks c and c+C4/2 of the same lane).
 template <int D, int G, int EPL>
-__device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const DecodeArgs& a) {
+__device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const HeadPrep& a) {
     using F = Frag<D, EPL>;
     const int half = a.half_rope;
     if (a.rope_type == 0) {
@@ -279,10 +287,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
     const int h0 = kvh * G;
-    const int row_begin = a.t_start + split * a.rows_per_split;
-    const int row_end = min(row_begin + a.rows_per_split, a.pos + 1);
-    const bool has_pos = (row_end == a.pos + 1);
-    const int cache_end = has_pos ? a.pos : row_end;
+    // Step plan from the position (host value or device word).  A device position outside
+    // the cache leaves everything untouched; splits beyond the rows of this step exit.
+    const int pos = step_position(a);
+    if (pos < 0 || pos >= a.max_seq) return;
+    const StepPlan sp = plan_step(pos, a.window, a.splits);
+    if (split >= sp.splits) return;
+    const HeadPrep hp = head_prep(a, pos);
+    const int row_begin = sp.start + split * sp.rows_per_split;
+    const int row_end = min(row_begin + sp.rows_per_split, pos + 1);
+    const bool has_pos = (row_end == pos + 1);
+    const int cache_end = has_pos ? pos : row_end;
     const int wave = tid >> 6, lane = tid & 63;
     const int grp = lane / LPR, j = lane - grp * LPR;
 
@@ -294,7 +309,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     //    barrier ahead of the first KV loads; otherwise it goes through the exact LDS path.
     float qr[G][EPL];
     const bool reg_prologue =
-        a.qnw == nullptr && (a.cos_row == nullptr || a.rope_type == 0 || 2 * a.half_rope == D);
+        a.qnw == nullptr && (a.cos_t == nullptr || a.rope_type == 0 || 2 * a.half_rope == D);
     if (reg_prologue) {
 #pragma unroll
         for (int h = 0; h < G; ++h)
@@ -307,11 +322,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
                 qr[h][4 * c + 2] = x.z;
                 qr[h][4 * c + 3] = x.w;
             }
-        if (a.cos_row != nullptr) rope_registers<D, G, EPL>(qr, j, a);
+        if (hp.cos_row != nullptr) rope_registers<D, G, EPL>(qr, j, hp);
     } else {
         for (int i = tid; i < G * D; i += NTHR) s_x[i] = a.q[h0 * D + i];
         __syncthreads();
-        prep_heads_lds<D, NTHR>(s_x, G, G, s_acc, s_r, head_prep(a), tid);
+        prep_heads_lds<D, NTHR>(s_x, G, G, s_acc, s_r, hp, tid);
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -358,10 +373,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             s_v[i] = a.v[kvh * D + i];
         }
         __syncthreads();
-        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, head_prep(a), tid);
+        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, hp, tid);
         for (int i = tid; i < D; i += NTHR) {
-            kplane[(long long)a.pos * D + i] = s_x[G * D + i];
-            vplane[(long long)a.pos * D + i] = s_v[i];
+            kplane[(long long)pos * D + i] = s_x[G * D + i];
+            vplane[(long long)pos * D + i] = s_v[i];
         }
         if (wave == 0) {
             float4 kf[1][C4], vf[1][C4];
@@ -422,10 +437,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             L = __builtin_fmaf(s_l[w * G + h], sc, L);
             O = __builtin_fmaf(s_o[(w * G + h) * D + d], sc, O);
         }
-        if (a.splits == 1) {
+        if (sp.splits == 1) {
             a.out[(h0 + h) * D + d] = O / L;
         } else {
-            const long long slot = ((long long)kvh * a.splits + split) * G + h;
+            const long long slot = ((long long)kvh * sp.splits + split) * G + h;
             a.part_o[slot * D + d] = O;
             if (d == 0) {
                 a.part_ml[2 * slot] = M;
@@ -450,7 +465,10 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
     const int kvh = hq / G, h = hq - kvh * G;
     const int tid = threadIdx.x;
     const int c = tid % NC, p = tid / NC;
-    const int S = a.splits;
+    const int pos = step_position(a);
+    if (pos < 0 || pos >= a.max_seq) return;
+    const int S = plan_step(pos, a.window, a.splits).splits;
+    if (S == 1) return;   // the split kernel wrote the output directly
     const long long slot0 = (long long)kvh * S * G + h;  // slot of split j: slot0 + j*G
 
     // Online merge over this thread's splits (loads are independent of the running max).

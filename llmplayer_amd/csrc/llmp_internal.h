@@ -11,25 +11,29 @@ namespace llmp {
 // Largest number of split-K partitions per KV head a decode call may use.
 constexpr int kMaxSplits = 1024;
 
-// Arguments of one split-K decode launch.  All pointers are device pointers.
+// Arguments of one split-K decode launch.  All pointers are device pointers.  The kernels
+// derive the step plan (window start, rows per split, effective splits, RoPE row) from the
+// position, which comes from `pos` or, when d_pos is set, from device memory at run time (a
+// captured graph then replays at whatever position the caller stored there).
 struct DecodeArgs {
     const float* q;        // [Hq*D] raw query projection
     const float* k;        // [Hkv*D] raw key projection
     const float* v;        // [Hkv*D] value projection
     float* kc;             // layer K plane [Hkv][max_seq][D]
     float* vc;             // layer V plane [Hkv][max_seq][D]
-    const float* cos_row;  // RoPE table row of `pos` (half_rope floats) or nullptr (NoPE)
-    const float* sin_row;
+    const float* cos_t;    // RoPE table [max_seq][half_rope] or nullptr (NoPE)
+    const float* sin_t;
     const float* qnw;      // QK-norm weights [D] or nullptr
     const float* knw;
-    float* out;            // [Hq*D] final output (written directly when splits == 1)
+    float* out;            // [Hq*D] final output (written directly when one split runs)
     float* part_o;         // [Hkv][splits][G][D] unnormalised split outputs
     float* part_ml;        // [Hkv][splits][G][2] split (max, sum) in the log2 domain
+    const int* d_pos;      // device position (tokenParams[0]) or nullptr to use `pos`
     long long head_stride; // floats between consecutive KV heads of a plane (max_seq*D)
-    int pos;               // position of the new token (row appended)
-    int t_start;           // first attended position
-    int rows_per_split;    // rows of [t_start, pos] per split
-    int splits;            // number of splits per KV head
+    int pos;               // position of the new token (row appended) when d_pos is null
+    int max_seq;           // cache rows; a device position outside [0, max_seq) is a no-op
+    int window;            // > 0: attend to the last `window` rows; 0: all rows
+    int splits;            // grid size: most splits per KV head (fewer run for short rows)
     int half_rope;         // rotated pairs per head
     int rope_type;         // 0 NORMAL, 2 NEOX
     float eps;             // QK-norm epsilon
@@ -38,6 +42,24 @@ struct DecodeArgs {
     float softcap_log2e;   // softcap * log2(e)
     float inv_softcap;     // 1 / softcap
 };
+
+// Step plan shared by host and kernels: window start, attended rows, rows per split (rounded
+// to 16 once there are at least 16 per split) and the splits that end up non-empty.
+struct StepPlan {
+    int start, n, rows_per_split, splits;
+};
+__host__ __device__ inline StepPlan plan_step(int pos, int window, int max_splits) {
+    StepPlan p;
+    p.start = (window > 0 && pos - window + 1 > 0) ? pos - window + 1 : 0;
+    p.n = pos + 1 - p.start;
+    int s = max_splits < p.n ? max_splits : p.n;
+    if (s < 1) s = 1;
+    int rps = (p.n + s - 1) / s;
+    if (p.n >= 16 * s) rps = (rps + 15) & ~15;
+    p.rows_per_split = rps;
+    p.splits = (p.n + rps - 1) / rps;
+    return p;
+}
 
 // Launches the split-K kernel for head_dim D and GQA group G = Hq/Hkv on grid
 // (splits, Hkv) with `waves` (4 or 8) waves per workgroup.  Returns hipErrorInvalidValue for

@@ -195,25 +195,109 @@ struct Plan {
     int waves;           // waves per workgroup
 };
 
-// Launch plan of one decode call: window start (Attention.java:330-335: local layers attend
-// to the last `window` rows), splits and workgroup size.
+// Attention window of a layer (Attention.java:330-335): local layers attend to the last
+// `window` rows, global layers to all of them.
+int layer_window(const LayerCfg& c) { return (c.window > 0 && !c.is_global) ? c.window : 0; }
+
+// Launch plan of one decode call at `position`: splits and workgroup size (auto_launch unless
+// the caller fixed the splits), then the kernels' own step plan (plan_step).
 Plan make_plan(const LayerCfg& c, int position, int splits_req, int n_kv_heads) {
-    Plan p{};
-    p.start = 0;
-    if (c.window > 0 && !c.is_global) p.start = position - c.window + 1 > 0 ? position - c.window + 1 : 0;
-    p.n = position + 1 - p.start;
+    const int window = layer_window(c);
+    const StepPlan full = plan_step(position, window, 1);
     int s = splits_req, waves = 4;
-    if (s <= 0) auto_launch(p.n, n_kv_heads, G().n_cu, &s, &waves);
-    else if (p.n / s >= 1024) waves = 8;
-    if (s > p.n) s = p.n;
-    // Rows per split rounded to 16 so splits start on aligned rows; then drop empty splits.
-    int rps = (p.n + s - 1) / s;
-    if (p.n >= 16 * s) rps = (rps + 15) & ~15;
-    s = (p.n + rps - 1) / rps;
-    p.splits = s;
-    p.rows_per_split = rps;
-    p.waves = waves;
-    return p;
+    if (s <= 0) auto_launch(full.n, n_kv_heads, G().n_cu, &s, &waves);
+    else if (full.n / s >= 1024) waves = 8;
+    const StepPlan sp = plan_step(position, window, s);
+    return Plan{sp.start, sp.n, sp.splits, sp.rows_per_split, waves};
+}
+
+// Enqueues one decode layer-call.  With d_pos == nullptr the step runs at `position`;
+// otherwise the kernels read the position from device memory when they run, and the launch
+// is planned for the longest step the layer can take (position = max_seq - 1).
+int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint64_t q,
+                   uint64_t k, uint64_t v, uint64_t out, int splits, uint64_t stream) {
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (position < 0 || position >= kv->max_seq)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "position %d outside [0, %d)", position, kv->max_seq);
+    const LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "decode: null buffer");
+    if ((q | k | v | out) & 15)
+        return fail(LLMP_ERR_INVALID_ARG, "decode: q/k/v/out must be 16-byte aligned");
+    if (splits > kMaxSplits)
+        return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
+
+    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    const Plan plan = make_plan(c, position, splits, Hkv);
+    DecodeArgs a{};
+    a.q = reinterpret_cast<const float*>(q);
+    a.k = reinterpret_cast<const float*>(k);
+    a.v = reinterpret_cast<const float*>(v);
+    a.kc = kv->k_plane(layer);
+    a.vc = kv->v_plane(layer);
+    if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
+        const RopeTable& t = kv->rope[c.rope_sel];
+        if (!t.d_cos)
+            return fail(LLMP_ERR_INVALID_ARG, "layer %d selects a RoPE table never uploaded", layer);
+        a.cos_t = t.d_cos;
+        a.sin_t = t.d_sin;
+        a.half_rope = t.half;
+    }
+    a.qnw = c.d_qnw;
+    a.knw = c.d_knw;
+    a.out = reinterpret_cast<float*>(out);
+    a.part_o = kv->part_o;
+    a.part_ml = kv->part_ml;
+    a.d_pos = d_pos;
+    a.head_stride = (long long)kv->max_seq * D;
+    a.pos = position;
+    a.max_seq = kv->max_seq;
+    a.window = layer_window(c);
+    a.splits = plan.splits;
+    a.rope_type = c.rope_type;
+    a.eps = c.eps;
+    const float scale = c.scale > 0.0f ? c.scale : (float)(1.0 / std::sqrt((double)D));
+    const float log2e = 1.4426950408889634f;
+    if (c.softcap > 0.0f) {
+        a.qk_scale = scale;
+        a.softcap = c.softcap;
+        a.softcap_log2e = c.softcap * log2e;
+        a.inv_softcap = 1.0f / c.softcap;
+    } else {
+        a.qk_scale = scale * log2e;
+    }
+
+    hipStream_t st = pick_stream(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+    if (kv->prof_on) {
+        if (int rc = prof_event(kv, &e0)) return rc;
+        if (int rc = prof_event(kv, &e1)) return rc;
+        LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
+    }
+    LLMP_HIP_CHECK(launch_decode_split(a, D, group, Hkv, plan.waves, st), "decode split-K launch");
+    if (kv->prof_on) {
+        LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
+        kv->prof_pending[LLMP_PROF_DECODE_SPLIT].push_back({e0, e1});
+    }
+    if (plan.splits > 1) {
+        if (kv->prof_on) {
+            if (int rc = prof_event(kv, &e2)) return rc;
+            if (int rc = prof_event(kv, &e0)) return rc;
+            LLMP_HIP_CHECK(hipEventRecord(e2, st), "hipEventRecord");
+        }
+        LLMP_HIP_CHECK(launch_decode_reduce(a, D, group, c.n_heads, st), "decode reduce launch");
+        if (kv->prof_on) {
+            LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
+            kv->prof_pending[LLMP_PROF_DECODE_REDUCE].push_back({e2, e0});
+        }
+    }
+    if (kv->prof_on && kv->prof_pending[LLMP_PROF_DECODE_SPLIT].size() >= 4096) {
+        for (int kind = 0; kind < LLMP_PROF_KINDS; ++kind)
+            if (int rc = prof_fold(kv, kind)) return rc;
+    }
+    return LLMP_OK;
 }
 
 }  // namespace
@@ -659,88 +743,17 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
                      uint64_t out, int splits, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    if (layer < 0 || layer >= kv->n_layers)
-        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
-    if (position < 0 || position >= kv->max_seq)
-        return fail(LLMP_ERR_OUT_OF_RANGE, "position %d outside [0, %d)", position, kv->max_seq);
-    const LayerCfg& c = kv->layers[(size_t)layer];
-    if (!c.configured)
-        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
-    if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode: null buffer");
-    if ((q | k | v | out) & 15)
-        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode: q/k/v/out must be 16-byte aligned");
-    if (splits > kMaxSplits)
-        return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
+    return enqueue_decode(kv, layer, position, nullptr, q, k, v, out, splits, stream);
+}
 
-    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
-    const Plan plan = make_plan(c, position, splits, Hkv);
-    const int s = plan.splits, waves = plan.waves;
-    DecodeArgs a{};
-    a.q = reinterpret_cast<const float*>(q);
-    a.k = reinterpret_cast<const float*>(k);
-    a.v = reinterpret_cast<const float*>(v);
-    a.kc = kv->k_plane(layer);
-    a.vc = kv->v_plane(layer);
-    if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
-        const RopeTable& t = kv->rope[c.rope_sel];
-        if (!t.d_cos)
-            return fail(LLMP_ERR_INVALID_ARG, "layer %d selects a RoPE table never uploaded", layer);
-        a.cos_row = t.d_cos + (size_t)position * t.half;
-        a.sin_row = t.d_sin + (size_t)position * t.half;
-        a.half_rope = t.half;
-    }
-    a.qnw = c.d_qnw;
-    a.knw = c.d_knw;
-    a.out = reinterpret_cast<float*>(out);
-    a.part_o = kv->part_o;
-    a.part_ml = kv->part_ml;
-    a.head_stride = (long long)kv->max_seq * D;
-    a.pos = position;
-    a.t_start = plan.start;
-    a.rows_per_split = plan.rows_per_split;
-    a.splits = s;
-    a.rope_type = c.rope_type;
-    a.eps = c.eps;
-    const float scale = c.scale > 0.0f ? c.scale : (float)(1.0 / std::sqrt((double)D));
-    const float log2e = 1.4426950408889634f;
-    if (c.softcap > 0.0f) {
-        a.qk_scale = scale;
-        a.softcap = c.softcap;
-        a.softcap_log2e = c.softcap * log2e;
-        a.inv_softcap = 1.0f / c.softcap;
-    } else {
-        a.qk_scale = scale * log2e;
-    }
-
-    hipStream_t st = pick_stream(stream);
-    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
-    if (kv->prof_on) {
-        if (int rc = prof_event(kv, &e0)) return rc;
-        if (int rc = prof_event(kv, &e1)) return rc;
-        LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
-    }
-    LLMP_HIP_CHECK(launch_decode_split(a, D, group, Hkv, waves, st), "decode split-K launch");
-    if (kv->prof_on) {
-        LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
-        kv->prof_pending[LLMP_PROF_DECODE_SPLIT].push_back({e0, e1});
-    }
-    if (s > 1) {
-        if (kv->prof_on) {
-            if (int rc = prof_event(kv, &e2)) return rc;
-            if (int rc = prof_event(kv, &e0)) return rc;
-            LLMP_HIP_CHECK(hipEventRecord(e2, st), "hipEventRecord");
-        }
-        LLMP_HIP_CHECK(launch_decode_reduce(a, D, group, c.n_heads, st), "decode reduce launch");
-        if (kv->prof_on) {
-            LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
-            kv->prof_pending[LLMP_PROF_DECODE_REDUCE].push_back({e2, e0});
-        }
-    }
-    if (kv->prof_on && kv->prof_pending[LLMP_PROF_DECODE_SPLIT].size() >= 4096) {
-        for (int kind = 0; kind < LLMP_PROF_KINDS; ++kind)
-            if (int rc = prof_fold(kv, kind)) return rc;
-    }
-    return LLMP_OK;
+int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uint64_t q,
+                            uint64_t k, uint64_t v, uint64_t out, int splits, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (!d_position || (d_position & 3))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode_devpos: null or misaligned position word");
+    return enqueue_decode(kv, layer, kv->max_seq - 1, reinterpret_cast<const int*>(d_position), q,
+                          k, v, out, splits, stream);
 }
 
 int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* out_splits,

@@ -257,6 +257,8 @@ class HipForwardPass:
         self.gpuK = DeviceBuffer(c.kv_dim * 4)
         self.gpuV = DeviceBuffer(c.kv_dim * 4)
         self.gpuXb2 = DeviceBuffer(c.q_dim * 4)
+        # [position, position + 1] as int32 (CudaForwardPass.gpuTokenParams, :138-141)
+        self.gpuTokenParams = DeviceBuffer(8)
 
     # -- reflection-contract statics -------------------------------------------------------
     @staticmethod
@@ -314,6 +316,18 @@ class HipForwardPass:
         call("llmp_attn_decode", self.kv.handle, layerIdx, position, self.gpuQ.ptr, self.gpuK.ptr,
              self.gpuV.ptr, self.gpuXb2.ptr, splits, stream)
 
+    def updateTokenParams(self, position: int) -> None:
+        """Store [position, position+1] in device memory (CudaForwardPass.updateTokenParams /
+        uploadXAndUpdateParams, CudaForwardPass.java:1283-1292), for graph-captured calls."""
+        self.gpuTokenParams.upload(np.array([position, position + 1], np.int32))
+
+    def forwardAttentionPartDevicePosition(self, layerIdx: int, splits: int = 0,
+                                           stream: int = 0) -> None:
+        """Steps 2b'-5 at the position held in gpuTokenParams, read when the kernels run
+        (capturable once and replayed per token, like the reference's graph mode)."""
+        call("llmp_attn_decode_devpos", self.kv.handle, layerIdx, self.gpuTokenParams.ptr,
+             self.gpuQ.ptr, self.gpuK.ptr, self.gpuV.ptr, self.gpuXb2.ptr, splits, stream)
+
     def forwardAttentionOnly(self, state: InferenceState, layerIdx: int, position: int,
                              splits: int = 0) -> None:
         """Attention for one layer from host projections in `state` (state.q, state.k,
@@ -362,7 +376,7 @@ class HipForwardPass:
         call("llmp_stream_sync", stream)
 
     def close(self) -> None:
-        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2"):
+        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2", "gpuTokenParams"):
             buf = getattr(self, b, None)
             if buf is not None:
                 buf.free()

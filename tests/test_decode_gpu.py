@@ -250,3 +250,80 @@ def test_graph_replay_matches_eager(splits):
         finally:
             _lib.call("llmp_graph_destroy", g.value)
         dc.compare_cache(fp, 0, *dc.oracle_call(c, 4096, d, 0, 4095)[1:], "cache after replays")
+
+
+# ------------------------------------------------- device-side position (reference graph mode)
+def test_device_position_matches_oracle_and_host_position():
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    d = dc.make_layer(c, 4096, 3000, seed=88, k_scale=0.5)
+    out, kc, vc = dc.oracle_call(c, 4096, d, 0, 3000)
+    with hfp.HipForwardPass(c, 4096) as fp:
+        fp.kv.write(0, 0, d.kc, d.vc)
+        fp.uploadQKV(d.q, d.k, d.v)
+        fp.updateTokenParams(3000)
+        dc.log("[gpu] device-position decode at 3000")
+        fp.forwardAttentionPartDevicePosition(0)
+        dc.compare_out(fp.downloadXb2(), out, "device position")
+        dc.compare_cache(fp, 0, kc, vc, "device position")
+
+
+def test_graph_of_device_position_decode_replays_across_tokens():
+    """One capture of two layers' decode calls replayed for 10 consecutive tokens: the
+    positions and q/k/v change between replays (uploaded outside the graph, as the reference's
+    uploadXAndUpdateParams does before cuGraphLaunch)."""
+    c = hfp.ModelConfig(16, 8, 128, 2, architecture=hfp.ARCH_QWEN3, rope_freq_base=1e6,
+                        norm_eps=1e-6)
+    max_seq, p0, steps = 2048, 1000, 10
+    rng = np.random.default_rng(89)
+    base = [dc.make_layer(c, max_seq, p0, seed=90 + l, qk_norm=True) for l in range(2)]
+    caches = [(b.kc.copy(), b.vc.copy()) for b in base]
+    with hfp.HipForwardPass(c, max_seq, qk_norm=[b.qk_norm for b in base]) as fp:
+        for l in range(2):
+            fp.kv.write(l, 0, *caches[l])
+        outs = [hfp.DeviceBuffer(c.q_dim * 4) for _ in range(2)]
+        g = C.c_uint64()
+        _lib.call("llmp_graph_begin", 0)
+        for l in range(2):
+            _lib.call("llmp_attn_decode_devpos", fp.kv.handle, l, fp.gpuTokenParams.ptr,
+                      fp.gpuQ.ptr, fp.gpuK.ptr, fp.gpuV.ptr, outs[l].ptr, 0, 0)
+        _lib.call("llmp_graph_end", 0, C.byref(g))
+        try:
+            for i in range(steps):
+                pos = p0 + i
+                q = rng.standard_normal(c.q_dim, dtype=np.float32)
+                k = rng.standard_normal(c.kv_dim, dtype=np.float32)
+                v = rng.standard_normal(c.kv_dim, dtype=np.float32)
+                fp.uploadQKV(q, k, v)
+                fp.updateTokenParams(pos)
+                dc.log(f"[gpu] graph replay at position {pos}")
+                _lib.call("llmp_graph_launch", g.value, 0)
+                fp.sync()
+                for l in range(2):
+                    d = dc.LayerData(caches[l][0], caches[l][1], q, k, v, base[l].qk_norm)
+                    want, kc, vc = dc.oracle_call(c, max_seq, d, l, pos)
+                    caches[l] = (kc, vc)
+                    dc.compare_out(outs[l].download(np.float32, c.q_dim), want,
+                                   f"graph replay layer {l} pos {pos}")
+        finally:
+            _lib.call("llmp_graph_destroy", g.value)
+            for b in outs:
+                b.free()
+        for l in range(2):
+            dc.compare_cache(fp, l, *caches[l], f"cache layer {l} after graph replays")
+
+
+def test_device_position_outside_cache_is_a_no_op():
+    c = hfp.ModelConfig(8, 2, 64, 1, rope_freq_base=1e4)
+    d = dc.make_layer(c, 64, 63, seed=91)
+    with hfp.HipForwardPass(c, 64) as fp:
+        fp.kv.write(0, 0, d.kc, d.vc)
+        fp.uploadQKV(d.q, d.k, d.v)
+        sentinel = np.full(c.q_dim, 7.0, np.float32)
+        fp.gpuXb2.upload(sentinel)
+        for bad in (64, 1000, -1):
+            fp.updateTokenParams(bad)
+            fp.forwardAttentionPartDevicePosition(0, splits=4)
+            fp.sync()
+            assert np.array_equal(fp.downloadXb2(), sentinel)
+        k_after, v_after = fp.kv.read(0, 0, 64)
+        assert np.array_equal(k_after, d.kc) and np.array_equal(v_after, d.vc)
