@@ -39,26 +39,41 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def kv_bytes(ctx: int) -> int:
-    return 2 * ctx * HKV * D * 4
+def kv_bytes(ctx: int, q8: bool = False) -> int:
+    """K and V bytes one layer-call reads: fp32 rows, or Q8_0 quants plus a 4-byte scale per
+    32 values (1.125 bytes per value)."""
+    return 2 * ctx * HKV * (D + D // 32 * 4) if q8 else 2 * ctx * HKV * D * 4
 
 
-def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int) -> dict:
+def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int,
+            q8: bool = False) -> dict:
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
 
-    per_layer = kv_bytes(ctx)
+    per_layer = kv_bytes(ctx, q8)
     n_layers = max(1, math.ceil(rotate_bytes / per_layer))
     c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
-    log(f"[bench] ctx {ctx}: {n_layers} layer caches x {per_layer / 2**20:.0f} MiB")
-    fp = hfp.HipForwardPass(c, ctx)
+    log(f"[bench] ctx {ctx}{' Q8_0' if q8 else ''}: {n_layers} layer caches x "
+        f"{per_layer / 2**20:.0f} MiB")
+    fp = hfp.HipForwardPass(c, ctx, kv_dtype=_lib.LLMP_KV_Q8_0 if q8 else _lib.LLMP_KV_F32)
     try:
         rng = np.random.default_rng(2024)
-        kc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32) * np.float32(0.5)
-        vc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32)
-        for layer in range(n_layers):
-            fp.kv.write(layer, 0, kc, vc)
-        del kc, vc
+        if q8:
+            # Synthetic Q8_0 rows: uniform quants, scales of N(0,0.5)-sized blocks (~max/127).
+            kq = rng.integers(-127, 128, (ctx - 1, c.kv_dim), dtype=np.int8)
+            vq = rng.integers(-127, 128, (ctx - 1, c.kv_dim), dtype=np.int8)
+            ks = np.full((ctx - 1, c.kv_dim // 32), 1.2 / 127, np.float32)
+            vs = np.full((ctx - 1, c.kv_dim // 32), 2.4 / 127, np.float32)
+            for layer in range(n_layers):
+                fp.kv.write_q8(layer, 0, kq, ks, vq, vs)
+                log(f"[bench] Q8_0 layer cache {layer + 1}/{n_layers} filled")
+            del kq, vq, ks, vs
+        else:
+            kc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32) * np.float32(0.5)
+            vc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32)
+            for layer in range(n_layers):
+                fp.kv.write(layer, 0, kc, vc)
+            del kc, vc
         fp.uploadQKV(rng.standard_normal(c.q_dim, dtype=np.float32),
                      rng.standard_normal(c.kv_dim, dtype=np.float32) * np.float32(0.5),
                      rng.standard_normal(c.kv_dim, dtype=np.float32))
@@ -275,7 +290,8 @@ def kernel_name(plan: dict) -> str:
 def traffic_from_profiles(ctx: int):
     """HBM bytes per launch of the split kernel from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), if present."""
-    path = os.path.join(ROOT, "profiles", f"decode_split_c3_ctx{ctx}_traffic.json")
+    tag = f"{ctx // 1024}k" if ctx % 1024 == 0 else str(ctx)
+    path = os.path.join(ROOT, "profiles", f"decode_split_c3_ctx{tag}_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -293,6 +309,8 @@ def main() -> int:
     ap.add_argument("--rotate-gib", type=float, default=2.0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-q8", dest="q8", action="store_false",
+                    help="skip the Q8_0-cache decode measurement")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="skip the C5 prefill measurement")
     ap.add_argument("--profile-workload", action="store_true",
@@ -328,6 +346,12 @@ def main() -> int:
         second = gpu_run(args.ctx2, args.steps, args.warmup, args.splits, rot)
         log(f"[bench] ctx {args.ctx2}: {second['us_per_layer_call']:.2f} us/layer-call, "
             f"{second['kv_read_gbps']:.0f} GB/s, split kernel {second['split_kernel_us']:.2f} us")
+
+    q8_run = None
+    if args.q8:
+        q8_run = gpu_run(args.ctx, args.steps, args.warmup, args.splits, rot, q8=True)
+        log(f"[bench] ctx {args.ctx} Q8_0: {q8_run['us_per_layer_call']:.2f} us/layer-call, "
+            f"{q8_run['kv_read_gbps']:.0f} GB/s, split kernel {q8_run['split_kernel_us']:.2f} us")
 
     prefill = []
     if args.prefill:
@@ -381,6 +405,19 @@ def main() -> int:
             "reduce_kernel_us": round(second["reduce_kernel_us"], 3),
             "us_per_layer_call_eager": round(second["us_per_layer_call_eager"], 3),
             "kv_layers_rotated": second["n_layers"]}
+    if q8_run is not None:
+        bq = kv_bytes(args.ctx, True)
+        line["q8_0_kv"] = {
+            "workload": f"C3 decode attention over a Q8_0 cache, ctx {args.ctx}",
+            "us_per_layer_call": round(q8_run["us_per_layer_call"], 3),
+            "kv_read_gbps": round(q8_run["kv_read_gbps"], 1),
+            "split_kernel_us": round(q8_run["split_kernel_us"], 3),
+            "split_kernel_gbps": round(bq / (q8_run["split_kernel_us"] * 1e-6) / 1e9, 1),
+            "reduce_kernel_us": round(q8_run["reduce_kernel_us"], 3),
+            "algorithmic_bytes_per_launch": bq,
+            "splits": q8_run["plan"]["splits"], "waves": q8_run["plan"]["waves"],
+            "speedup_vs_f32_cache": round(main_run["us_per_layer_call"] /
+                                          q8_run["us_per_layer_call"], 3)}
     if prefill:
         line["prefill_c5_llama1b"] = prefill
     print(json.dumps(line), flush=True)

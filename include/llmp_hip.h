@@ -42,6 +42,13 @@ extern "C" {
 
 /* ---- enums ----------------------------------------------------------------------------- */
 #define LLMP_KV_F32             0  /* fp32 cache rows (KVCache.Mode.FLOAT32, KVCache.java:79) */
+#define LLMP_KV_Q8_0            1  /* int8 quants + fp32 scale per 32 values (KVCache.Mode.Q8_0,
+                                      KVCache.java:11-28, 79; 1.125 bytes per value); the
+                                      appended row rounds half up like quantizeBlocksScalar
+                                      (KVCache.java:218-243)                                  */
+#define LLMP_KV_Q8_0_TRUNC      2  /* the same format, appended rows truncated toward zero like
+                                      SimdQ8KvOps.quantize (SimdQ8KvOps.java:86-117), the
+                                      contract the JVM runs on 8-lane (AVX2) hosts            */
 
 #define LLMP_ROPE_NORMAL        0  /* pairs (2i, 2i+1)    RoPE.ROPE_TYPE_NORMAL, RoPE.java:18 */
 #define LLMP_ROPE_NEOX          2  /* pairs (i, i + R/2)  RoPE.ROPE_TYPE_NEOX,   RoPE.java:19 */
@@ -82,20 +89,32 @@ int llmp_event_elapsed_ms(float *ms, uint64_t start, uint64_t end);
 /* ---- device KV cache (CudaForwardPass.java:407-416 per-layer K/V buffers; sizing as
  *      LLMEngine.estimateKvCache, LLMEngine.java:917-928) --------------------------------- */
 
-/* One zero-filled device pool for n_layers x {K,V}, laid out head-major
- * [layer][K|V][kv_head][pos][head_dim].  Fails with LLMP_ERR_OUT_OF_MEMORY when the pool
- * would not fit in free HBM.  head_dim must be 64, 128 or 256; dtype LLMP_KV_F32. */
+/* One zero-filled device pool for n_layers x {K,V}, laid out head-major.  LLMP_KV_F32:
+ * [layer][K|V][kv_head][pos][head_dim] fp32.  LLMP_KV_Q8_0(_TRUNC): per layer the K quants
+ * [kv_head][pos][head_dim] int8, K scales [kv_head][pos][head_dim/32] fp32, then the same for
+ * V.  Fails with LLMP_ERR_OUT_OF_MEMORY when the pool would not fit in free HBM.  head_dim must
+ * be 64, 128 or 256. */
 int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int dtype,
                    uint64_t *handle);
 int llmp_kv_destroy(uint64_t handle);
 /* Read rows [pos0, pos0+n) of one layer into host arrays in the reference layout
- * [pos][kvDim] (KVCache.keyLayer / valueLayer, KVCache.java:149-161).  Either out may be NULL. */
+ * [pos][kvDim] (KVCache.keyLayer / valueLayer, KVCache.java:149-161).  Either out may be NULL.
+ * fp32 caches only (LLMP_ERR_UNSUPPORTED on a Q8_0 cache: use llmp_kv_read_q8). */
 int llmp_kv_read(uint64_t handle, int layer, int pos0, int n, float *host_k, float *host_v);
 /* Write rows [pos0, pos0+n) of one layer from host arrays in the reference layout
  * (the inverse of llmp_kv_read; restores a saved prefix, ConversationCache.java:36-56). */
 int llmp_kv_write(uint64_t handle, int layer, int pos0, int n, const float *host_k,
                   const float *host_v);
-/* Device addresses of one layer's K and V planes ([kv_head][pos][head_dim] fp32). */
+/* Q8_0 caches: rows [pos0, pos0+n) of one layer in the reference's Q8_0 layout
+ * (KVCache.keyQuants / keyScales, KVCache.java:91-94): quants [pos][kvDim] int8 and scales
+ * [pos][kvDim/32] fp32, for K and V.  Any out may be NULL. */
+int llmp_kv_read_q8(uint64_t handle, int layer, int pos0, int n, int8_t *k_quants,
+                    float *k_scales, int8_t *v_quants, float *v_scales);
+/* The inverse of llmp_kv_read_q8. */
+int llmp_kv_write_q8(uint64_t handle, int layer, int pos0, int n, const int8_t *k_quants,
+                     const float *k_scales, const int8_t *v_quants, const float *v_scales);
+/* Device addresses of one layer's K and V planes ([kv_head][pos][head_dim] fp32, or the quant
+ * planes of a Q8_0 cache). */
 int llmp_kv_layer_ptrs(uint64_t handle, int layer, uint64_t *k_plane, uint64_t *v_plane);
 /* Zero the whole pool (a new conversation). */
 int llmp_kv_clear(uint64_t handle, uint64_t stream);

@@ -20,7 +20,7 @@ ERR_NAMES = {
     4: "LLMP_ERR_NO_DEVICE", 5: "LLMP_ERR_OUT_OF_MEMORY", 6: "LLMP_ERR_UNSUPPORTED",
     7: "LLMP_ERR_HIP", 8: "LLMP_ERR_BAD_HANDLE",
 }
-LLMP_KV_F32 = 0
+LLMP_KV_F32, LLMP_KV_Q8_0, LLMP_KV_Q8_0_TRUNC = 0, 1, 2
 LLMP_ROPE_NORMAL, LLMP_ROPE_NEOX = 0, 2
 LLMP_ROPE_SEL_NONE, LLMP_ROPE_SEL_GLOBAL, LLMP_ROPE_SEL_LOCAL = -1, 0, 1
 LLMP_PROF_DECODE_SPLIT, LLMP_PROF_DECODE_REDUCE = 0, 1
@@ -55,6 +55,8 @@ SIGNATURES = {
     "llmp_kv_destroy": [_u64],
     "llmp_kv_read": [_u64, _i32, _i32, _i32, _pf, _pf],
     "llmp_kv_write": [_u64, _i32, _i32, _i32, _pf, _pf],
+    "llmp_kv_read_q8": [_u64, _i32, _i32, _i32, C.POINTER(C.c_int8), _pf, C.POINTER(C.c_int8), _pf],
+    "llmp_kv_write_q8": [_u64, _i32, _i32, _i32, C.POINTER(C.c_int8), _pf, C.POINTER(C.c_int8), _pf],
     "llmp_kv_layer_ptrs": [_u64, _i32, _pu64, _pu64],
     "llmp_kv_clear": [_u64, _u64],
     "llmp_rope_table": [_i32, _i32, _f32, _f32, _pf, _i32, _pf, _pf],

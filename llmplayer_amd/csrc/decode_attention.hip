@@ -16,36 +16,50 @@ constexpr Tune pick(int D, int G) {
     return Tune{(D == 256 || (G > 4 && D / 8 > 16)) ? 16 : 8, (G > 4) ? 1 : 2, true};
 }
 
-template <int D, int G, int W>
+template <int D, int G, int W, bool Q8>
 hipError_t launch_dgw(const DecodeArgs& a, int n_kv_heads, hipStream_t stream) {
     constexpr Tune t = pick(D, G);
-    hipLaunchKernelGGL((dk::decode_split_kernel<D, G, t.epl, t.unroll, W, t.nt>),
+    // Q8_0 rows are read as 16 quants per lane (D/16 lanes per row).
+    constexpr int EPL = Q8 ? 16 : t.epl;
+    constexpr int UNROLL = Q8 ? (G > 4 ? 1 : 2) : t.unroll;
+    hipLaunchKernelGGL((dk::decode_split_kernel<D, G, EPL, UNROLL, W, t.nt, Q8>),
                        dim3(a.splits, n_kv_heads), dim3(W * 64), 0, stream, a);
     return hipGetLastError();
 }
 
-// 8-wave workgroups except for head_dim 256 with more than 4 query heads per KV head, whose
-// register footprint leaves no room for two 8-wave workgroups per CU.
-template <int D, int G>
+// 8-wave workgroups except where more than 4 query heads per KV head hold 16 elements per
+// lane (head_dim 256, or any Q8_0 cache): that register footprint leaves no room for them.
+template <int D, int G, bool Q8>
 hipError_t launch_dg(const DecodeArgs& a, int n_kv_heads, int waves, hipStream_t stream) {
-    if constexpr (D == 256 && G > 4) {
-        return launch_dgw<D, G, 4>(a, n_kv_heads, stream);
+    if constexpr ((D == 256 || Q8) && G > 4) {
+        return launch_dgw<D, G, 4, Q8>(a, n_kv_heads, stream);
     } else {
-        return waves == 8 ? launch_dgw<D, G, 8>(a, n_kv_heads, stream)
-                          : launch_dgw<D, G, 4>(a, n_kv_heads, stream);
+        return waves == 8 ? launch_dgw<D, G, 8, Q8>(a, n_kv_heads, stream)
+                          : launch_dgw<D, G, 4, Q8>(a, n_kv_heads, stream);
     }
 }
 
-template <int D>
+template <int D, bool Q8>
 hipError_t launch_d(const DecodeArgs& a, int group, int n_kv_heads, int waves,
                     hipStream_t stream) {
     switch (group) {
-    case 1: return launch_dg<D, 1>(a, n_kv_heads, waves, stream);
-    case 2: return launch_dg<D, 2>(a, n_kv_heads, waves, stream);
-    case 3: return launch_dg<D, 3>(a, n_kv_heads, waves, stream);
-    case 4: return launch_dg<D, 4>(a, n_kv_heads, waves, stream);
-    case 6: return launch_dg<D, 6>(a, n_kv_heads, waves, stream);
-    case 8: return launch_dg<D, 8>(a, n_kv_heads, waves, stream);
+    case 1: return launch_dg<D, 1, Q8>(a, n_kv_heads, waves, stream);
+    case 2: return launch_dg<D, 2, Q8>(a, n_kv_heads, waves, stream);
+    case 3: return launch_dg<D, 3, Q8>(a, n_kv_heads, waves, stream);
+    case 4: return launch_dg<D, 4, Q8>(a, n_kv_heads, waves, stream);
+    case 6: return launch_dg<D, 6, Q8>(a, n_kv_heads, waves, stream);
+    case 8: return launch_dg<D, 8, Q8>(a, n_kv_heads, waves, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <bool Q8>
+hipError_t launch_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads, int waves,
+                        hipStream_t stream) {
+    switch (head_dim) {
+    case 64: return launch_d<64, Q8>(a, group, n_kv_heads, waves, stream);
+    case 128: return launch_d<128, Q8>(a, group, n_kv_heads, waves, stream);
+    case 256: return launch_d<256, Q8>(a, group, n_kv_heads, waves, stream);
     default: return hipErrorInvalidValue;
     }
 }
@@ -66,14 +80,10 @@ bool decode_shape_supported(int head_dim, int group) {
 }
 
 hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads,
-                               int waves, hipStream_t stream) {
+                               int waves, bool q8, hipStream_t stream) {
     if (waves != 4 && waves != 8) return hipErrorInvalidValue;
-    switch (head_dim) {
-    case 64: return launch_d<64>(a, group, n_kv_heads, waves, stream);
-    case 128: return launch_d<128>(a, group, n_kv_heads, waves, stream);
-    case 256: return launch_d<256>(a, group, n_kv_heads, waves, stream);
-    default: return hipErrorInvalidValue;
-    }
+    return q8 ? launch_split<true>(a, head_dim, group, n_kv_heads, waves, stream)
+              : launch_split<false>(a, head_dim, group, n_kv_heads, waves, stream);
 }
 
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,

@@ -35,6 +35,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Finite "minus infinity" for running maxima, so that exp2(m_old - m_new) never sees
 // (-inf) - (-inf).  Masked scores use a true -inf, which exp2 maps to 0.
 constexpr float kNegBig = -1.0e30f;
+// Lazy rescaling: a running max is only raised (and o, l rescaled) once some lane of the wave
+// sees a score more than this many log2 units above it, so exp2(s - m) stays <= 2^8 and the
+// rescale multiplies are skipped on most trips.  O/L is unchanged: both use the same max.
+constexpr float kLazyMargin = 8.0f;
 
 // DPP controls (CDNA3/CDNA4 ISA): quad_perm, row_half_mirror, row_mirror.
 constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
@@ -75,16 +79,132 @@ __device__ __forceinline__ float4 load4(const float4* p) {
     }
 }
 
-template <int D, int EPL>
+// Lane layout of a K/V row.  fp32 rows: lane j of a row group holds the 16-byte chunks
+// j, j+LPR, ... (LPR*16 contiguous bytes per wave-wide load).  Q8_0 rows (CONTIG): lane j
+// holds the 16 contiguous quants 16j..16j+15, i.e. half of one 32-value scale block.
+template <int D, int EPL, bool CONTIG = false>
 struct Frag {
     static constexpr int LPR = D / EPL;   // lanes per row
     static constexpr int RPW = 64 / LPR;  // rows per wave-wide load
-    static constexpr int C4 = EPL / 4;    // 16-byte chunks per lane per row
+    static constexpr int C4 = EPL / 4;    // 16-byte fp32 chunks per lane per row
     // Dimension held by lane j (within its row group) at element e.
     static __device__ __forceinline__ int dim(int j, int e) {
-        return (e >> 2) * (LPR * 4) + j * 4 + (e & 3);
+        return CONTIG ? j * EPL + e : (e >> 2) * (LPR * 4) + j * 4 + (e & 3);
     }
 };
+
+typedef unsigned int native_u4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 load_u4(const uint4* p) {
+    if constexpr (NT) {
+        const native_u4 v = __builtin_nontemporal_load(reinterpret_cast<const native_u4*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *p;
+    }
+}
+
+// 16 signed bytes -> floats.
+__device__ __forceinline__ void unpack_q8(const uint4& w, float (&f)[16]) {
+    const unsigned d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) f[4 * i + b] = (float)(int)(signed char)(d[i] >> (8 * b));
+}
+
+// Online-softmax update of one row group over U Q8_0 rows: s = scale_k * (q . quants_k),
+// o += (p * scale_v) * quants_v (KVCache.dotK / saxpyV in Q8_0 mode, KVCache.java:187-210).
+template <int D, int G, int U, bool LAZY = false>
+__device__ __forceinline__ void accumulate_rows_q8(const float (&qr)[G][16],
+                                                   const float (&kq)[U][16], const float (&ksc)[U],
+                                                   const float (&vq)[U][16], const float (&vsc)[U],
+                                                   const bool (&valid)[U], float (&m)[G],
+                                                   float (&l)[G], float (&o)[G][16],
+                                                   const DecodeArgs& a) {
+    constexpr int LPR = D / 16;
+    float s[U][G];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc = __builtin_fmaf(qr[h][e], kq[u][e], acc);
+            s[u][h] = row_group_sum<LPR>(acc * ksc[u]);
+        }
+    }
+    if (a.softcap > 0.0f) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int h = 0; h < G; ++h) s[u][h] = a.softcap_log2e * tanhf(s[u][h] * a.inv_softcap);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        float mx = m[h];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            s[u][h] = valid[u] ? s[u][h] : -__builtin_inff();
+            mx = fmaxf(mx, s[u][h]);
+        }
+        float lsum = l[h];
+        if (!LAZY || __any(mx > m[h] + kLazyMargin)) {
+            const float alpha = fast_exp2(m[h] - mx);
+            m[h] = mx;
+            lsum = lsum * alpha;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[h][e] = o[h][e] * alpha;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float p = fast_exp2(s[u][h] - m[h]);
+            lsum = lsum + p;
+            const float w = p * vsc[u];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[h][e] = __builtin_fmaf(w, vq[u][e], o[h][e]);
+        }
+        l[h] = lsum;
+    }
+}
+
+// Math.round(float): nearest int, ties toward +infinity (exact for |y| < 2^22).
+__device__ __forceinline__ int round_half_up(float y) {
+    float r = floorf(y);
+    const float frac = y - r;
+    if (frac >= 0.5f) r = r + 1.0f;
+    return (int)r;
+}
+
+// Q8_0 quantisation of one row of D fp32 values staged in LDS: per 32-value block
+// scale = maxAbs/127, quant = clamp(r(x * (1/scale)), -128, 127), where r rounds half up
+// (KVCache.quantizeBlocksScalar, KVCache.java:218-243) or truncates toward zero when `trunc`
+// is set (SimdQ8KvOps.quantize on 8-lane hosts, SimdQ8KvOps.java:86-117).  Whole workgroup;
+// results in LDS (q: D bytes, sc: D/32 floats).
+template <int D, int NTHR>
+__device__ void quantize_row_lds(const float* x, signed char* q, float* sc, float* s_inv, int tid,
+                                 bool trunc) {
+    for (int b = tid; b < D / 32; b += NTHR) {
+        float mx = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            const float v = x[32 * b + i];
+            const float av = v >= 0.0f ? v : -v;
+            mx = av > mx ? av : mx;
+        }
+        const float scale = mx / 127.0f;
+        sc[b] = scale;
+        s_inv[b] = scale != 0.0f ? 1.0f / scale : 0.0f;
+    }
+    __syncthreads();
+    for (int i = tid; i < D; i += NTHR) {
+        const float y = x[i] * s_inv[i / 32];
+        int v = trunc ? (int)y : round_half_up(y);   // |y| <= 127.x: the cast is in range
+        v = v > 127 ? 127 : (v < -128 ? -128 : v);
+        q[i] = (signed char)v;
+    }
+    __syncthreads();
+}
 
 // Online-softmax update of one row group with U rows: s = (q . K_t) in the log2 domain,
 // masked rows get -inf; o and l are rescaled once per call.
@@ -223,9 +343,9 @@ __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* 
 
 // Rotation of the lane's own q slice in registers (no QK-norm; NORMAL pairs sit inside one
 // 16-byte chunk, NEOX pairs (i, i+D/2) in chunks c and c+C4/2 of the same lane).
-template <int D, int G, int EPL>
+template <int D, int G, int EPL, bool CONTIG = false>
 __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const HeadPrep& a) {
-    using F = Frag<D, EPL>;
+    using F = Frag<D, EPL, CONTIG>;
     const int half = a.half_rope;
     if (a.rope_type == 0) {
 #pragma unroll
@@ -233,7 +353,7 @@ __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 // Pairs at or beyond half_rope (partial RoPE) keep their values.
-                const int i = (c * F::LPR * 4 + j * 4) / 2 + p;
+                const int i = F::dim(j, 4 * c + 2 * p) / 2;
                 const bool rot = i < half;
                 const int ii = rot ? i : 0;
                 const float cs = a.cos_row[ii], sn = a.sin_row[ii];
@@ -247,7 +367,7 @@ __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const
                 }
             }
         }
-    } else {
+    } else if constexpr (!CONTIG) {  // NEOX, fp32 layout: dims i, i + D/2 in chunks c, c + C4/2
 #pragma unroll
         for (int c = 0; c < F::C4 / 2; ++c) {
 #pragma unroll
@@ -266,9 +386,12 @@ __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const
     }
 }
 
-template <int D, int G, int EPL, int U, int WAVES, bool NT>
+template <int D, int G, int EPL, int U, int WAVES, bool NT, bool Q8 = false, int VAR = 0>
 __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) {
-    using F = Frag<D, EPL>;
+    constexpr bool LAZY = (VAR & 1) != 0;   // Q8_0: lazy rescaling
+    constexpr bool PF = (VAR & 2) != 0;     // Q8_0: next trip's rows loaded before this trip's math
+    static_assert(!Q8 || EPL == 16, "Q8_0 rows are read 16 quants per lane");
+    using F = Frag<D, EPL, Q8>;
     constexpr int NTHR = WAVES * 64;
     constexpr int LPR = F::LPR, RPW = F::RPW, C4 = F::C4;
     constexpr int ROWS_WAVE = U * RPW;
@@ -298,31 +421,27 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     const int row_end = min(row_begin + sp.rows_per_split, pos + 1);
     const bool has_pos = (row_end == pos + 1);
     const int cache_end = has_pos ? pos : row_end;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int grp = lane / LPR, j = lane - grp * LPR;
-
-    float* kplane = a.kc + (long long)kvh * a.head_stride;
-    float* vplane = a.vc + (long long)kvh * a.head_stride;
 
     // 1. Query slice of this lane, pre-scaled (log2 domain unless soft-capping).  Without
-    //    QK-norm and with pairs inside a lane, q is loaded and rotated in registers, with no
-    //    barrier ahead of the first KV loads; otherwise it goes through the exact LDS path.
+    //    QK-norm and with RoPE pairs inside a lane, q is loaded and rotated in registers, with
+    //    no barrier ahead of the first KV loads; otherwise it goes through the exact LDS path.
+    const int wave = tid >> 6, lane = tid & 63;
+    const int grp = lane / LPR, j = lane - grp * LPR;
     float qr[G][EPL];
-    const bool reg_prologue =
-        a.qnw == nullptr && (a.cos_t == nullptr || a.rope_type == 0 || 2 * a.half_rope == D);
+    const bool pairs_in_lane = a.rope_type == 0 || (!Q8 && 2 * a.half_rope == D);
+    const bool reg_prologue = a.qnw == nullptr && (a.cos_t == nullptr || pairs_in_lane);
     if (reg_prologue) {
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
             for (int c = 0; c < C4; ++c) {
-                const float4 x =
-                    reinterpret_cast<const float4*>(a.q + (h0 + h) * D)[c * LPR + j];
+                const float4 x = *reinterpret_cast<const float4*>(a.q + (h0 + h) * D + F::dim(j, 4 * c));
                 qr[h][4 * c + 0] = x.x;
                 qr[h][4 * c + 1] = x.y;
                 qr[h][4 * c + 2] = x.z;
                 qr[h][4 * c + 3] = x.w;
             }
-        if (hp.cos_row != nullptr) rope_registers<D, G, EPL>(qr, j, hp);
+        if (hp.cos_row != nullptr) rope_registers<D, G, EPL, Q8>(qr, j, hp);
     } else {
         for (int i = tid; i < G * D; i += NTHR) s_x[i] = a.q[h0 * D + i];
         __syncthreads();
@@ -347,26 +466,89 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     }
 
     // 2. Stream the cached rows [row_begin, cache_end).
-    for (int base = row_begin + wave * ROWS_WAVE; base < cache_end; base += ROWS_BLOCK) {
-        float4 kf[U][C4], vf[U][C4];
-        bool valid[U];
+    if constexpr (!Q8) {
+        const float* kplane = a.kc + (long long)kvh * a.head_stride;
+        const float* vplane = a.vc + (long long)kvh * a.head_stride;
+        for (int base = row_begin + wave * ROWS_WAVE; base < cache_end; base += ROWS_BLOCK) {
+            float4 kf[U][C4], vf[U][C4];
+            bool valid[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = base + u * RPW + grp;
-            valid[u] = t < cache_end;
-            const int tt = valid[u] ? t : cache_end - 1;  // in-bounds address for masked rows
-            const float4* kp = reinterpret_cast<const float4*>(kplane + (long long)tt * D) + j;
-            const float4* vp = reinterpret_cast<const float4*>(vplane + (long long)tt * D) + j;
+            for (int u = 0; u < U; ++u) {
+                const int t = base + u * RPW + grp;
+                valid[u] = t < cache_end;
+                const int tt = valid[u] ? t : cache_end - 1;  // in-bounds address, masked row
+                const float4* kp = reinterpret_cast<const float4*>(kplane + (long long)tt * D) + j;
+                const float4* vp = reinterpret_cast<const float4*>(vplane + (long long)tt * D) + j;
 #pragma unroll
-            for (int c = 0; c < C4; ++c) kf[u][c] = load4<NT>(kp + c * LPR);
+                for (int c = 0; c < C4; ++c) kf[u][c] = load4<NT>(kp + c * LPR);
 #pragma unroll
-            for (int c = 0; c < C4; ++c) vf[u][c] = load4<NT>(vp + c * LPR);
+                for (int c = 0; c < C4; ++c) vf[u][c] = load4<NT>(vp + c * LPR);
+            }
+            accumulate_rows<D, G, EPL, U>(qr, kf, vf, valid, m, l, o, a);
         }
-        accumulate_rows<D, G, EPL, U>(qr, kf, vf, valid, m, l, o, a);
+    } else {
+        const signed char* kqp = a.kq + (long long)kvh * a.head_stride;
+        const signed char* vqp = a.vq + (long long)kvh * a.head_stride;
+        const float* ksp = a.ks + (long long)kvh * (a.head_stride / 32);
+        const float* vsp = a.vs + (long long)kvh * (a.head_stride / 32);
+        struct Rows {
+            uint4 kw[U], vw[U];
+            float ksc[U], vsc[U];
+            bool valid[U];
+        };
+        // Rows base + u*RPW + grp of this lane group (masked past cache_end, clamped address).
+        auto load_rows = [&](int base, Rows& r) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int t = base + u * RPW + grp;
+                r.valid[u] = t < cache_end;
+                const int tt = r.valid[u] ? t : cache_end - 1;
+                r.kw[u] = load_u4<NT>(reinterpret_cast<const uint4*>(kqp + (long long)tt * D) + j);
+                r.vw[u] = load_u4<NT>(reinterpret_cast<const uint4*>(vqp + (long long)tt * D) + j);
+                r.ksc[u] = ksp[(long long)tt * (D / 32) + (j >> 1)];
+                r.vsc[u] = vsp[(long long)tt * (D / 32) + (j >> 1)];
+            }
+        };
+        auto consume = [&](const Rows& r) {
+            float kq[U][16], vq[U][16];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                unpack_q8(r.kw[u], kq[u]);
+                unpack_q8(r.vw[u], vq[u]);
+            }
+            accumulate_rows_q8<D, G, U, LAZY>(qr, kq, r.ksc, vq, r.vsc, r.valid, m, l, o, a);
+        };
+        int base = row_begin + wave * ROWS_WAVE;
+        if constexpr (PF) {
+            // Two row buffers in turn: the loads of trip i+1 are in flight during trip i's math.
+            Rows ra, rb;
+            if (base < cache_end) {
+                load_rows(base, ra);
+                while (true) {
+                    base += ROWS_BLOCK;
+                    const bool more_b = base < cache_end;
+                    if (more_b) load_rows(base, rb);
+                    consume(ra);
+                    if (!more_b) break;
+                    base += ROWS_BLOCK;
+                    const bool more_a = base < cache_end;
+                    if (more_a) load_rows(base, ra);
+                    consume(rb);
+                    if (!more_a) break;
+                }
+            }
+        } else {
+            for (; base < cache_end; base += ROWS_BLOCK) {
+                Rows r;
+                load_rows(base, r);
+                consume(r);
+            }
+        }
     }
 
-    // 3. The split that owns row `pos`: prepare k exactly, append K/V (KVCache.storeK/storeV),
-    //    and take row `pos` from LDS (row group 0 of wave 0).
+    // 3. The split that owns row `pos`: prepare k exactly, append K/V (KVCache.storeK/storeV:
+    //    the exact fp32 rows, or their Q8_0 quantisation), and take row `pos` from LDS as the
+    //    cache now holds it (row group 0 of wave 0).
     if (has_pos) {
         for (int i = tid; i < D; i += NTHR) {
             s_x[G * D + i] = a.k[kvh * D + i];
@@ -374,21 +556,54 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
         }
         __syncthreads();
         prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, hp, tid);
-        for (int i = tid; i < D; i += NTHR) {
-            kplane[(long long)pos * D + i] = s_x[G * D + i];
-            vplane[(long long)pos * D + i] = s_v[i];
-        }
-        if (wave == 0) {
-            float4 kf[1][C4], vf[1][C4];
-            bool valid[1] = {grp == 0};
-#pragma unroll
-            for (int c = 0; c < C4; ++c) {
-                const int d0 = c * LPR * 4 + j * 4;
-                kf[0][c] = make_float4(s_x[G * D + d0], s_x[G * D + d0 + 1], s_x[G * D + d0 + 2],
-                                       s_x[G * D + d0 + 3]);
-                vf[0][c] = make_float4(s_v[d0], s_v[d0 + 1], s_v[d0 + 2], s_v[d0 + 3]);
+        if constexpr (!Q8) {
+            float* kplane = a.kc + (long long)kvh * a.head_stride;
+            float* vplane = a.vc + (long long)kvh * a.head_stride;
+            for (int i = tid; i < D; i += NTHR) {
+                kplane[(long long)pos * D + i] = s_x[G * D + i];
+                vplane[(long long)pos * D + i] = s_v[i];
             }
-            accumulate_rows<D, G, EPL, 1>(qr, kf, vf, valid, m, l, o, a);
+            if (wave == 0) {
+                float4 kf[1][C4], vf[1][C4];
+                bool valid[1] = {grp == 0};
+#pragma unroll
+                for (int c = 0; c < C4; ++c) {
+                    const int d0 = F::dim(j, 4 * c);
+                    kf[0][c] = make_float4(s_x[G * D + d0], s_x[G * D + d0 + 1],
+                                           s_x[G * D + d0 + 2], s_x[G * D + d0 + 3]);
+                    vf[0][c] = make_float4(s_v[d0], s_v[d0 + 1], s_v[d0 + 2], s_v[d0 + 3]);
+                }
+                accumulate_rows<D, G, EPL, 1>(qr, kf, vf, valid, m, l, o, a);
+            }
+        } else {
+            __shared__ signed char s_kq[D], s_vq[D];
+            __shared__ float s_ks[D / 32], s_vs[D / 32], s_inv[D / 32];
+            quantize_row_lds<D, NTHR>(s_x + G * D, s_kq, s_ks, s_inv, tid, a.q8_trunc != 0);
+            quantize_row_lds<D, NTHR>(s_v, s_vq, s_vs, s_inv, tid, a.q8_trunc != 0);
+            signed char* kqp = a.kq + (long long)kvh * a.head_stride + (long long)pos * D;
+            signed char* vqp = a.vq + (long long)kvh * a.head_stride + (long long)pos * D;
+            float* ksp = a.ks + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
+            float* vsp = a.vs + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
+            for (int i = tid; i < D; i += NTHR) {
+                kqp[i] = s_kq[i];
+                vqp[i] = s_vq[i];
+            }
+            for (int b = tid; b < D / 32; b += NTHR) {
+                ksp[b] = s_ks[b];
+                vsp[b] = s_vs[b];
+            }
+            if (wave == 0) {
+                float kq[1][16], vq[1][16], ksc[1], vsc[1];
+                bool valid[1] = {grp == 0};
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    kq[0][e] = (float)s_kq[16 * j + e];
+                    vq[0][e] = (float)s_vq[16 * j + e];
+                }
+                ksc[0] = s_ks[j >> 1];
+                vsc[0] = s_vs[j >> 1];
+                accumulate_rows_q8<D, G, 1>(qr, kq, ksc, vq, vsc, valid, m, l, o, a);
+            }
         }
     }
 

@@ -19,8 +19,12 @@ struct DecodeArgs {
     const float* q;        // [Hq*D] raw query projection
     const float* k;        // [Hkv*D] raw key projection
     const float* v;        // [Hkv*D] value projection
-    float* kc;             // layer K plane [Hkv][max_seq][D]
-    float* vc;             // layer V plane [Hkv][max_seq][D]
+    float* kc;             // fp32 cache: layer K plane [Hkv][max_seq][D]
+    float* vc;             // fp32 cache: layer V plane [Hkv][max_seq][D]
+    signed char* kq;       // Q8_0 cache: K quants [Hkv][max_seq][D]
+    float* ks;             // Q8_0 cache: K block scales [Hkv][max_seq][D/32]
+    signed char* vq;
+    float* vs;
     const float* cos_t;    // RoPE table [max_seq][half_rope] or nullptr (NoPE)
     const float* sin_t;
     const float* qnw;      // QK-norm weights [D] or nullptr
@@ -36,6 +40,7 @@ struct DecodeArgs {
     int splits;            // grid size: most splits per KV head (fewer run for short rows)
     int half_rope;         // rotated pairs per head
     int rope_type;         // 0 NORMAL, 2 NEOX
+    int q8_trunc;          // Q8_0 append: 1 = truncate (8-lane SIMD contract), 0 = round half up
     float eps;             // QK-norm epsilon
     float qk_scale;        // factor folded into q: scale*log2(e), or scale when soft-capping
     float softcap;         // 0 = off
@@ -62,10 +67,11 @@ __host__ __device__ inline StepPlan plan_step(int pos, int window, int max_split
 }
 
 // Launches the split-K kernel for head_dim D and GQA group G = Hq/Hkv on grid
-// (splits, Hkv) with `waves` (4 or 8) waves per workgroup.  Returns hipErrorInvalidValue for
-// an unsupported shape.  With splits > 1, launch_decode_reduce must follow.
+// (splits, Hkv) with `waves` (4 or 8) waves per workgroup, over an fp32 (q8 = false) or
+// Q8_0 (q8 = true) cache.  Returns hipErrorInvalidValue for an unsupported shape.  With
+// splits > 1, launch_decode_reduce must follow.
 hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads,
-                               int waves, hipStream_t stream);
+                               int waves, bool q8, hipStream_t stream);
 // Launches the log-sum-exp combine of the splits: one block per query head.
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,
                                 hipStream_t stream);

@@ -79,8 +79,33 @@ struct KvHandle {
     double prof_ms[LLMP_PROF_KINDS] = {};
     long long prof_count[LLMP_PROF_KINDS] = {};
 
+    // fp32 pool: [layer][K|V][kv_head][pos][D].
     float* k_plane(int layer) const { return pool + (size_t)(2 * layer) * plane_floats; }
     float* v_plane(int layer) const { return pool + (size_t)(2 * layer + 1) * plane_floats; }
+    // Q8_0 pool, per layer: K quants, K scales, V quants, V scales, each section padded to
+    // 256 bytes so every quant row is 16-byte aligned for the wide loads.
+    bool q8() const { return dtype == LLMP_KV_Q8_0 || dtype == LLMP_KV_Q8_0_TRUNC; }
+    static size_t pad256(size_t b) { return (b + 255) & ~(size_t)255; }
+    size_t q8_quant_bytes() const { return pad256(plane_floats); }
+    size_t q8_scale_bytes() const { return pad256(plane_floats / 32 * sizeof(float)); }
+    size_t q8_layer_bytes() const { return 2 * (q8_quant_bytes() + q8_scale_bytes()); }
+    char* q8_layer(int layer) const {
+        return reinterpret_cast<char*>(pool) + (size_t)layer * q8_layer_bytes();
+    }
+    signed char* kq(int layer) const { return reinterpret_cast<signed char*>(q8_layer(layer)); }
+    float* ks(int layer) const {
+        return reinterpret_cast<float*>(q8_layer(layer) + q8_quant_bytes());
+    }
+    signed char* vq(int layer) const {
+        return reinterpret_cast<signed char*>(q8_layer(layer) + q8_quant_bytes() + q8_scale_bytes());
+    }
+    float* vs(int layer) const {
+        return reinterpret_cast<float*>(q8_layer(layer) + 2 * q8_quant_bytes() + q8_scale_bytes());
+    }
+    size_t pool_bytes() const {
+        return q8() ? (size_t)n_layers * q8_layer_bytes()
+                    : 2 * (size_t)n_layers * plane_floats * sizeof(float);
+    }
 };
 
 struct Global {
@@ -235,8 +260,16 @@ int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint
     a.q = reinterpret_cast<const float*>(q);
     a.k = reinterpret_cast<const float*>(k);
     a.v = reinterpret_cast<const float*>(v);
-    a.kc = kv->k_plane(layer);
-    a.vc = kv->v_plane(layer);
+    if (kv->q8()) {
+        a.kq = kv->kq(layer);
+        a.ks = kv->ks(layer);
+        a.vq = kv->vq(layer);
+        a.vs = kv->vs(layer);
+        a.q8_trunc = kv->dtype == LLMP_KV_Q8_0_TRUNC;
+    } else {
+        a.kc = kv->k_plane(layer);
+        a.vc = kv->v_plane(layer);
+    }
     if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
         const RopeTable& t = kv->rope[c.rope_sel];
         if (!t.d_cos)
@@ -276,7 +309,8 @@ int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint
         if (int rc = prof_event(kv, &e1)) return rc;
         LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
     }
-    LLMP_HIP_CHECK(launch_decode_split(a, D, group, Hkv, plan.waves, st), "decode split-K launch");
+    LLMP_HIP_CHECK(launch_decode_split(a, D, group, Hkv, plan.waves, kv->q8(), st),
+                   "decode split-K launch");
     if (kv->prof_on) {
         LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
         kv->prof_pending[LLMP_PROF_DECODE_SPLIT].push_back({e0, e1});
@@ -494,8 +528,10 @@ int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int 
     if (head_dim != 64 && head_dim != 128 && head_dim != 256)
         return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: head_dim %d (supported: 64, 128, 256)",
                     head_dim);
-    if (dtype != LLMP_KV_F32)
-        return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: dtype %d (supported: LLMP_KV_F32)", dtype);
+    if (dtype != LLMP_KV_F32 && dtype != LLMP_KV_Q8_0 && dtype != LLMP_KV_Q8_0_TRUNC)
+        return fail(LLMP_ERR_UNSUPPORTED,
+                    "llmp_kv_create: dtype %d (LLMP_KV_F32, LLMP_KV_Q8_0 or LLMP_KV_Q8_0_TRUNC)",
+                    dtype);
     if ((long long)max_seq * head_dim >= (1LL << 31))
         return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: max_seq*head_dim exceeds 2^31");
     auto kv = std::make_unique<KvHandle>();
@@ -505,7 +541,7 @@ int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int 
     kv->head_dim = head_dim;
     kv->dtype = dtype;
     kv->plane_floats = (size_t)n_kv_heads * (size_t)max_seq * (size_t)head_dim;
-    const size_t bytes = 2 * (size_t)n_layers * kv->plane_floats * sizeof(float);
+    const size_t bytes = kv->pool_bytes();
     size_t fr = 0, tot = 0;
     LLMP_HIP_CHECK(hipMemGetInfo(&fr, &tot), "hipMemGetInfo");
     if (bytes > fr)
@@ -552,26 +588,46 @@ static int check_rows(const KvHandle* kv, int layer, int pos0, int n) {
     return LLMP_OK;
 }
 
+// Copies between rows [pos0, pos0+n) of one head-major device plane (per KV head, rows of
+// `row` bytes) and a host array in the reference layout [pos][n_kv_heads * row bytes].  The
+// host side is re-laid out through a head-major staging buffer so that each head moves as one
+// contiguous copy (narrow pitched copies, e.g. the 16-byte scale rows of a Q8_0 cache, are
+// otherwise moved row by row).
+static int copy_plane(KvHandle* kv, void* dev_plane, size_t row, int pos0, int n, void* host,
+                      bool to_host) {
+    const size_t H = (size_t)kv->n_kv_heads, host_row = row * H, span = row * (size_t)n;
+    std::vector<char> stage(span * H);
+    char* hp = static_cast<char*>(host);
+    if (!to_host)
+        for (size_t t = 0; t < (size_t)n; ++t)
+            for (size_t h = 0; h < H; ++h)
+                std::memcpy(stage.data() + h * span + t * row, hp + t * host_row + h * row, row);
+    for (size_t h = 0; h < H; ++h) {
+        char* dev = static_cast<char*>(dev_plane) + (h * (size_t)kv->max_seq + (size_t)pos0) * row;
+        hipError_t e = to_host ? hipMemcpyAsync(stage.data() + h * span, dev, span,
+                                                hipMemcpyDeviceToHost, G().stream)
+                               : hipMemcpyAsync(dev, stage.data() + h * span, span,
+                                                hipMemcpyHostToDevice, G().stream);
+        LLMP_HIP_CHECK(e, "hipMemcpyAsync(kv plane)");
+    }
+    // The staging buffer is released on return: every copy from or into it must be done.
+    LLMP_HIP_CHECK(hipStreamSynchronize(G().stream), "hipStreamSynchronize");
+    if (to_host)
+        for (size_t t = 0; t < (size_t)n; ++t)
+            for (size_t h = 0; h < H; ++h)
+                std::memcpy(hp + t * host_row + h * row, stage.data() + h * span + t * row, row);
+    return LLMP_OK;
+}
+
 int llmp_kv_read(uint64_t handle, int layer, int pos0, int n, float* host_k, float* host_v) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
+    if (kv->q8()) return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_read: Q8_0 cache (use llmp_kv_read_q8)");
     if (int rc = check_rows(kv, layer, pos0, n)) return rc;
     if (n == 0) return LLMP_OK;
-    const size_t D = (size_t)kv->head_dim, kv_dim = D * kv->n_kv_heads;
-    hipStream_t s = G().stream;
-    for (int which = 0; which < 2; ++which) {
-        float* host = which == 0 ? host_k : host_v;
-        if (!host) continue;
-        const float* plane = which == 0 ? kv->k_plane(layer) : kv->v_plane(layer);
-        for (int h = 0; h < kv->n_kv_heads; ++h) {
-            const float* src = plane + ((size_t)h * kv->max_seq + (size_t)pos0) * D;
-            LLMP_HIP_CHECK(hipMemcpy2DAsync(host + (size_t)h * D, kv_dim * sizeof(float), src,
-                                            D * sizeof(float), D * sizeof(float), (size_t)n,
-                                            hipMemcpyDeviceToHost, s),
-                           "hipMemcpy2DAsync(kv_read)");
-        }
-    }
-    LLMP_HIP_CHECK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    const size_t row = (size_t)kv->head_dim * sizeof(float);
+    if (host_k) if (int rc = copy_plane(kv, kv->k_plane(layer), row, pos0, n, host_k, true)) return rc;
+    if (host_v) if (int rc = copy_plane(kv, kv->v_plane(layer), row, pos0, n, host_v, true)) return rc;
     return LLMP_OK;
 }
 
@@ -579,23 +635,49 @@ int llmp_kv_write(uint64_t handle, int layer, int pos0, int n, const float* host
                   const float* host_v) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
+    if (kv->q8()) return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_write: Q8_0 cache (use llmp_kv_write_q8)");
     if (int rc = check_rows(kv, layer, pos0, n)) return rc;
     if (n == 0) return LLMP_OK;
-    const size_t D = (size_t)kv->head_dim, kv_dim = D * kv->n_kv_heads;
-    hipStream_t s = G().stream;
-    for (int which = 0; which < 2; ++which) {
-        const float* host = which == 0 ? host_k : host_v;
-        if (!host) continue;
-        float* plane = which == 0 ? kv->k_plane(layer) : kv->v_plane(layer);
-        for (int h = 0; h < kv->n_kv_heads; ++h) {
-            float* dst = plane + ((size_t)h * kv->max_seq + (size_t)pos0) * D;
-            LLMP_HIP_CHECK(hipMemcpy2DAsync(dst, D * sizeof(float), host + (size_t)h * D,
-                                            kv_dim * sizeof(float), D * sizeof(float), (size_t)n,
-                                            hipMemcpyHostToDevice, s),
-                           "hipMemcpy2DAsync(kv_write)");
-        }
-    }
-    LLMP_HIP_CHECK(hipStreamSynchronize(s), "hipStreamSynchronize");
+    const size_t row = (size_t)kv->head_dim * sizeof(float);
+    if (host_k)
+        if (int rc = copy_plane(kv, kv->k_plane(layer), row, pos0, n, const_cast<float*>(host_k), false))
+            return rc;
+    if (host_v)
+        if (int rc = copy_plane(kv, kv->v_plane(layer), row, pos0, n, const_cast<float*>(host_v), false))
+            return rc;
+    return LLMP_OK;
+}
+
+int llmp_kv_read_q8(uint64_t handle, int layer, int pos0, int n, int8_t* k_quants,
+                    float* k_scales, int8_t* v_quants, float* v_scales) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (!kv->q8()) return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_read_q8: not a Q8_0 cache");
+    if (int rc = check_rows(kv, layer, pos0, n)) return rc;
+    if (n == 0) return LLMP_OK;
+    const size_t qrow = (size_t)kv->head_dim, srow = (size_t)kv->head_dim / 32 * sizeof(float);
+    if (k_quants) if (int rc = copy_plane(kv, kv->kq(layer), qrow, pos0, n, k_quants, true)) return rc;
+    if (k_scales) if (int rc = copy_plane(kv, kv->ks(layer), srow, pos0, n, k_scales, true)) return rc;
+    if (v_quants) if (int rc = copy_plane(kv, kv->vq(layer), qrow, pos0, n, v_quants, true)) return rc;
+    if (v_scales) if (int rc = copy_plane(kv, kv->vs(layer), srow, pos0, n, v_scales, true)) return rc;
+    return LLMP_OK;
+}
+
+int llmp_kv_write_q8(uint64_t handle, int layer, int pos0, int n, const int8_t* k_quants,
+                     const float* k_scales, const int8_t* v_quants, const float* v_scales) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (!kv->q8()) return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_write_q8: not a Q8_0 cache");
+    if (int rc = check_rows(kv, layer, pos0, n)) return rc;
+    if (n == 0) return LLMP_OK;
+    const size_t qrow = (size_t)kv->head_dim, srow = (size_t)kv->head_dim / 32 * sizeof(float);
+    auto cp = [&](void* plane, size_t row, const void* host) {
+        return copy_plane(kv, plane, row, pos0, n, const_cast<void*>(host), false);
+    };
+    if (k_quants) if (int rc = cp(kv->kq(layer), qrow, k_quants)) return rc;
+    if (k_scales) if (int rc = cp(kv->ks(layer), srow, k_scales)) return rc;
+    if (v_quants) if (int rc = cp(kv->vq(layer), qrow, v_quants)) return rc;
+    if (v_scales) if (int rc = cp(kv->vs(layer), srow, v_scales)) return rc;
     return LLMP_OK;
 }
 
@@ -604,16 +686,20 @@ int llmp_kv_layer_ptrs(uint64_t handle, int layer, uint64_t* k_plane, uint64_t* 
     LLMP_GET_HANDLE(kv, handle);
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
-    if (k_plane) *k_plane = reinterpret_cast<uint64_t>(kv->k_plane(layer));
-    if (v_plane) *v_plane = reinterpret_cast<uint64_t>(kv->v_plane(layer));
+    if (k_plane)
+        *k_plane = kv->q8() ? reinterpret_cast<uint64_t>(kv->kq(layer))
+                            : reinterpret_cast<uint64_t>(kv->k_plane(layer));
+    if (v_plane)
+        *v_plane = kv->q8() ? reinterpret_cast<uint64_t>(kv->vq(layer))
+                            : reinterpret_cast<uint64_t>(kv->v_plane(layer));
     return LLMP_OK;
 }
 
 int llmp_kv_clear(uint64_t handle, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    const size_t bytes = 2 * (size_t)kv->n_layers * kv->plane_floats * sizeof(float);
-    LLMP_HIP_CHECK(hipMemsetAsync(kv->pool, 0, bytes, pick_stream(stream)), "hipMemsetAsync(kv)");
+    LLMP_HIP_CHECK(hipMemsetAsync(kv->pool, 0, kv->pool_bytes(), pick_stream(stream)),
+                   "hipMemsetAsync(kv)");
     return LLMP_OK;
 }
 
@@ -791,6 +877,8 @@ int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64
     if (!c.configured)
         return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
     if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: null buffer");
+    if (kv->q8())
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_attn_prefill: Q8_0 cache (decode steps only)");
     if ((q | k | v) & 1 || out & 15)
         return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: misaligned q/k/v (2 B) or out (16 B)");
     const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;

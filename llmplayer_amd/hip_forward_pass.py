@@ -127,6 +127,13 @@ def _fp(a: Optional[np.ndarray]):
     return a.ctypes.data_as(_F)
 
 
+def _i8p(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.dtype == np.int8 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.POINTER(C.c_int8))
+
+
 def to_bf16(x: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bit patterns (uint16), round to nearest even."""
     u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
@@ -180,15 +187,45 @@ class DeviceBuffer:
 
 
 class KvCache:
-    """Device KV cache handle (llmp_kv_*): head-major pool, reference-layout read/write."""
+    """Device KV cache handle (llmp_kv_*): head-major pool, reference-layout read/write.
 
-    def __init__(self, n_layers: int, max_seq: int, n_kv_heads: int, head_dim: int):
+    dtype LLMP_KV_F32 (KVCache.Mode.FLOAT32), or LLMP_KV_Q8_0 / LLMP_KV_Q8_0_TRUNC
+    (KVCache.Mode.Q8_0: int8 quants and one fp32 scale per 32 values, KVCache.java:11-28; new
+    rows rounded half up like quantizeBlocksScalar, or truncated like SimdQ8KvOps on 8-lane
+    hosts)."""
+
+    def __init__(self, n_layers: int, max_seq: int, n_kv_heads: int, head_dim: int,
+                 dtype: int = _lib.LLMP_KV_F32):
         h = C.c_uint64()
-        call("llmp_kv_create", n_layers, max_seq, n_kv_heads, head_dim, _lib.LLMP_KV_F32,
-             C.byref(h))
+        call("llmp_kv_create", n_layers, max_seq, n_kv_heads, head_dim, dtype, C.byref(h))
         self.handle = h.value
+        self.dtype = dtype
         self.n_layers, self.max_seq = n_layers, max_seq
         self.n_kv_heads, self.head_dim = n_kv_heads, head_dim
+
+    @property
+    def is_q8(self) -> bool:
+        return self.dtype in (_lib.LLMP_KV_Q8_0, _lib.LLMP_KV_Q8_0_TRUNC)
+
+    def read_q8(self, layer: int, pos0: int, n: int):
+        """(k_quants, k_scales, v_quants, v_scales) in the reference layout
+        (KVCache.keyQuants [pos][kvDim], keyScales [pos][kvDim/32])."""
+        kq = np.empty((n, self.kv_dim), np.int8)
+        vq = np.empty((n, self.kv_dim), np.int8)
+        ks = np.empty((n, self.kv_dim // 32), np.float32)
+        vs = np.empty((n, self.kv_dim // 32), np.float32)
+        call("llmp_kv_read_q8", self.handle, layer, pos0, n, _i8p(kq), _fp(ks), _i8p(vq), _fp(vs))
+        return kq, ks, vq, vs
+
+    def write_q8(self, layer: int, pos0: int, kq, ks, vq, vs) -> None:
+        kq = np.ascontiguousarray(kq, np.int8).reshape(-1, self.kv_dim)
+        vq = np.ascontiguousarray(vq, np.int8).reshape(-1, self.kv_dim)
+        ks = np.ascontiguousarray(ks, np.float32).reshape(-1, self.kv_dim // 32)
+        vs = np.ascontiguousarray(vs, np.float32).reshape(-1, self.kv_dim // 32)
+        n = kq.shape[0]
+        if not (vq.shape[0] == ks.shape[0] == vs.shape[0] == n):
+            raise ValueError("write_q8: quants and scales disagree on the row count")
+        call("llmp_kv_write_q8", self.handle, layer, pos0, n, _i8p(kq), _fp(ks), _i8p(vq), _fp(vs))
 
     @property
     def kv_dim(self) -> int:
@@ -228,14 +265,15 @@ class HipForwardPass:
     `qk_norm` holds per-layer (q_weights, k_weights) arrays of head_size floats, or None."""
 
     def __init__(self, config: ModelConfig, max_seq_len: int,
-                 qk_norm: Optional[Sequence[Optional[tuple]]] = None, device: int = 0):
+                 qk_norm: Optional[Sequence[Optional[tuple]]] = None, device: int = 0,
+                 kv_dtype: int = _lib.LLMP_KV_F32):
         if not HipForwardPass.isSupportedForAttention(config):
             raise LlmpError("HipForwardPass", 6, "configuration not supported by the HIP attention path")
         init(device)
         self.config = config
         self.max_seq_len = max_seq_len
         c = config
-        self.kv = KvCache(c.block_count, max_seq_len, c.head_count_kv, c.head_size)
+        self.kv = KvCache(c.block_count, max_seq_len, c.head_count_kv, c.head_size, kv_dtype)
         rope_dim = c.rope_dim_count or c.head_size
         # InferenceEngine.java:58-78: global table with linear scaling; local table for
         # Gemma 3 (theta 10000) and Gemma 4 (SWA theta) when a sliding window exists.

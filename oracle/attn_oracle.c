@@ -199,6 +199,142 @@ void orc_kv_store(float *cache_layer, int pos, const float *x, int kv_dim)
     memcpy(cache_layer + (size_t)pos * kv_dim, x, sizeof(float) * (size_t)kv_dim);
 }
 
+/* ---- KVCache Q8_0 mode (KVCache.java:11-28, 218-282) -----------------------------------
+ * Blocks of 32 values with one fp32 scale each.  The JVM picks one of two contracts at class
+ * load (KVCache.loadQ8Ops, KVCache.java:54-62): SimdQ8KvOps when the Vector API is present
+ * and its preferred float species has exactly 8 lanes (AVX2 hosts, SimdQ8KvOps.java:27-33),
+ * otherwise the scalar one (quantizeBlocksScalar / dotQ8BlockScalar / saxpyQ8BlockScalar).
+ * ORC_Q8_SCALAR restates the scalar contract (round half up); ORC_Q8_SIMD8 restates the
+ * 8-lane one (truncating quantize, FMA lanes in dot and saxpy, SimdQ8KvOps.java:37-117). */
+#define ORC_Q8_BLOCK 32
+#define ORC_Q8_SCALAR 1
+#define ORC_Q8_SIMD8 2
+
+/* Math.round(float): the closest int, ties toward positive infinity.  floor(y) and y - floor(y)
+ * are exact for |y| < 2^22, which covers every quantized value (|y| <= 127.x). */
+int orc_round_half_up(float y)
+{
+    float r = floorf(y);
+    float frac = y - r;
+    if (frac >= 0.5f) r = r + 1.0f;
+    return (int)r;
+}
+
+/* quantizeBlocksScalar (KVCache.java:218-243). */
+void orc_q8_quantize(const float *src, int n, int8_t *dst, float *scales)
+{
+    int blocks = n / ORC_Q8_BLOCK;
+    for (int b = 0; b < blocks; b++) {
+        const float *x = src + (size_t)b * ORC_Q8_BLOCK;
+        float max_abs = 0.0f;
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+            float a = x[i] >= 0 ? x[i] : -x[i];
+            if (a > max_abs) max_abs = a;
+        }
+        float scale = max_abs / 127.0f;
+        float inv = scale != 0.0f ? 1.0f / scale : 0.0f;
+        scales[b] = scale;
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+            float y = x[i] * inv;
+            int q = orc_round_half_up(y);
+            if (q > 127) q = 127;
+            else if (q < -128) q = -128;
+            dst[(size_t)b * ORC_Q8_BLOCK + i] = (int8_t)q;
+        }
+    }
+}
+
+/* dotQ8BlockScalar (KVCache.java:252-267): per block a sequential unfused sum, then * scale. */
+float orc_q8_dot(const float *q, const int8_t *kq, const float *ks, int n)
+{
+    int blocks = n / ORC_Q8_BLOCK;
+    float total = 0.0f;
+    for (int b = 0; b < blocks; b++) {
+        float acc = 0.0f;
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+            float p = q[b * ORC_Q8_BLOCK + i] * (float)kq[b * ORC_Q8_BLOCK + i];
+            acc = acc + p;
+        }
+        float t = acc * ks[b];
+        total = total + t;
+    }
+    return total;
+}
+
+/* saxpyQ8BlockScalar (KVCache.java:269-282): out += (weight*scale) * quant, unfused. */
+void orc_q8_saxpy(float weight, const int8_t *vq, const float *vs, float *out, int n)
+{
+    int blocks = n / ORC_Q8_BLOCK;
+    for (int b = 0; b < blocks; b++) {
+        float w = weight * vs[b];
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+            float p = w * (float)vq[b * ORC_Q8_BLOCK + i];
+            out[b * ORC_Q8_BLOCK + i] = out[b * ORC_Q8_BLOCK + i] + p;
+        }
+    }
+}
+
+/* SimdQ8KvOps.quantize (SimdQ8KvOps.java:86-117): block max of |x| (order-free), the same
+ * scale and inverse as the scalar path, then F2I, i.e. truncation toward zero, and a clamp to
+ * [-128, 127]. */
+void orc_q8_quantize_simd8(const float *src, int n, int8_t *dst, float *scales)
+{
+    int blocks = n / ORC_Q8_BLOCK;
+    for (int b = 0; b < blocks; b++) {
+        const float *x = src + (size_t)b * ORC_Q8_BLOCK;
+        float max_abs = 0.0f;
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+            float a = fabsf(x[i]);
+            if (a > max_abs) max_abs = a;
+        }
+        float scale = max_abs / 127.0f;
+        float inv = scale != 0.0f ? 1.0f / scale : 0.0f;
+        scales[b] = scale;
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+            float y = x[i] * inv;
+            int q = (int)y;                       /* |y| <= 127.x: in range, toward zero */
+            if (q > 127) q = 127;
+            else if (q < -128) q = -128;
+            dst[(size_t)b * ORC_Q8_BLOCK + i] = (int8_t)q;
+        }
+    }
+}
+
+/* SimdQ8KvOps.dot (SimdQ8KvOps.java:37-63): per block, 8 lanes each FMA-accumulate the
+ * elements i = l (mod 8) in chunk order; the lanes are summed (left to right, the order the
+ * restatement fixes for reduceLanes(ADD)), multiplied by the scale and added to the total. */
+float orc_q8_dot_simd8(const float *q, const int8_t *kq, const float *ks, int n)
+{
+    int blocks = n / ORC_Q8_BLOCK;
+    float total = 0.0f;
+    for (int b = 0; b < blocks; b++) {
+        float lane[ORC_LANES] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int c = 0; c < ORC_Q8_BLOCK; c += ORC_LANES)
+            for (int l = 0; l < ORC_LANES; l++) {
+                int i = b * ORC_Q8_BLOCK + c + l;
+                lane[l] = fmaf((float)kq[i], q[i], lane[l]);
+            }
+        float sum = lane[0];
+        for (int l = 1; l < ORC_LANES; l++) sum = sum + lane[l];
+        float t = sum * ks[b];
+        total = total + t;
+    }
+    return total;
+}
+
+/* SimdQ8KvOps.saxpy (SimdQ8KvOps.java:66-84): out = fma(quant, weight*scale, out). */
+void orc_q8_saxpy_simd8(float weight, const int8_t *vq, const float *vs, float *out, int n)
+{
+    int blocks = n / ORC_Q8_BLOCK;
+    for (int b = 0; b < blocks; b++) {
+        float w = weight * vs[b];
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) {
+            int j = b * ORC_Q8_BLOCK + i;
+            out[j] = fmaf((float)vq[j], w, out[j]);
+        }
+    }
+}
+
 /* First attended position (Attention.java:330-335). */
 int orc_start_pos(const orc_cfg *c, int layer, int pos)
 {
@@ -209,18 +345,44 @@ int orc_start_pos(const orc_cfg *c, int layer, int pos)
     return 0;
 }
 
-/* Attention.forwardFromProjections (Attention.java:284-367), optional bias omitted (absent
- * from every configuration this build covers).  q and k are modified in place exactly as
- * state.q / state.k are; the K/V rows are appended at `pos`; out = xb2[Hq*D].
- * use_flash != 0 selects the online-softmax loop of Attention.forward (Attention.java:161-207).
- * kcache/vcache are one layer's [max_seq][kvDim] arrays.  rope_cos/rope_sin are the table
- * the layer selects (global or local, Attention.java:317); NULL skips RoPE (NoPE layer). */
-void orc_forward_from_projections(const orc_cfg *c, float *kcache, float *vcache,
-                                  const float *qnorm_w, const float *knorm_w,
-                                  const float *rope_cos, const float *rope_sin,
-                                  float *q, float *k, const float *v,
-                                  int layer, int pos, float *out, float *att_scratch,
-                                  int use_flash, int n_threads)
+/* A layer's cache in either KVCache mode: FLOAT32 rows [max_seq][kvDim], or Q8_0 quants
+ * [max_seq][kvDim] with scales [max_seq][kvDim/32] (KVCache.java:86-94). */
+typedef struct {
+    float *kf, *vf;          /* FLOAT32 mode */
+    int8_t *kq, *vq;         /* Q8_0 mode    */
+    float *ks, *vs;
+} orc_layer_cache;
+
+static float cache_dot(const orc_layer_cache *kv, int q8, int t, int kv_dim, int off,
+                       const float *q, int D)
+{
+    if (!q8) return orc_dot(q, kv->kf + (size_t)t * kv_dim + off, D);
+    size_t base = (size_t)t * kv_dim + off;
+    if (q8 == ORC_Q8_SIMD8)
+        return orc_q8_dot_simd8(q, kv->kq + base, kv->ks + base / ORC_Q8_BLOCK, D);
+    return orc_q8_dot(q, kv->kq + base, kv->ks + base / ORC_Q8_BLOCK, D);
+}
+
+static void cache_saxpy(const orc_layer_cache *kv, int q8, int t, int kv_dim, int off, float a,
+                        float *out, int D)
+{
+    if (!q8) {
+        orc_saxpy(a, kv->vf + (size_t)t * kv_dim + off, out, D);
+        return;
+    }
+    size_t base = (size_t)t * kv_dim + off;
+    if (q8 == ORC_Q8_SIMD8)
+        orc_q8_saxpy_simd8(a, kv->vq + base, kv->vs + base / ORC_Q8_BLOCK, out, D);
+    else
+        orc_q8_saxpy(a, kv->vq + base, kv->vs + base / ORC_Q8_BLOCK, out, D);
+}
+
+/* Attention.forwardFromProjections (Attention.java:284-367) over a cache in either mode
+ * (KVCache.storeK/storeV/dotK/saxpyV, KVCache.java:164-210). */
+static void forward_impl(const orc_cfg *c, const orc_layer_cache *kv, int q8,
+                         const float *qnorm_w, const float *knorm_w, const float *rope_cos,
+                         const float *rope_sin, float *q, float *k, const float *v, int layer,
+                         int pos, float *out, float *att_scratch, int use_flash, int n_threads)
 {
     const int Hq = c->n_heads, Hkv = c->n_kv_heads, D = c->head_size;
     const int kv_dim = Hkv * D;
@@ -237,8 +399,16 @@ void orc_forward_from_projections(const orc_cfg *c, float *kcache, float *vcache
         orc_rope_apply_all(q, Hq, D, c->rope_dim, c->rope_type, rope_cos, rope_sin, pos);
         orc_rope_apply_all(k, Hkv, D, c->rope_dim, c->rope_type, rope_cos, rope_sin, pos);
     }
-    orc_kv_store(kcache, pos, k, kv_dim);
-    orc_kv_store(vcache, pos, v, kv_dim);
+    if (!q8) {
+        orc_kv_store(kv->kf, pos, k, kv_dim);
+        orc_kv_store(kv->vf, pos, v, kv_dim);
+    } else {
+        size_t base = (size_t)pos * kv_dim;
+        void (*quant)(const float *, int, int8_t *, float *) =
+            q8 == ORC_Q8_SIMD8 ? orc_q8_quantize_simd8 : orc_q8_quantize;
+        quant(k, kv_dim, kv->kq + base, kv->ks + base / ORC_Q8_BLOCK);
+        quant(v, kv_dim, kv->vq + base, kv->vs + base / ORC_Q8_BLOCK);
+    }
 
     float scale = c->attention_scale > 0.0f ? c->attention_scale
                                             : (float)(1.0 / sqrt((double)D));
@@ -258,7 +428,7 @@ void orc_forward_from_projections(const orc_cfg *c, float *kcache, float *vcache
             float max_score = -INFINITY;
             float sum_exp = 0.0f;
             for (int t = start; t <= pos; t++) {
-                float score = orc_dot(qh, kcache + (size_t)t * kv_dim + kv_off, D);
+                float score = cache_dot(kv, q8, t, kv_dim, kv_off, qh, D);
                 float s = score * scale;
                 if (softcap > 0.0f) {
                     float r = s / softcap;
@@ -271,7 +441,7 @@ void orc_forward_from_projections(const orc_cfg *c, float *kcache, float *vcache
                 float scale_new = (float)exp((double)(s - new_max));
                 if (scale_old != 1.0f)
                     for (int i = 0; i < D; i++) oh[i] = oh[i] * scale_old;
-                orc_saxpy(scale_new, vcache + (size_t)t * kv_dim + kv_off, oh, D);
+                cache_saxpy(kv, q8, t, kv_dim, kv_off, scale_new, oh, D);
                 float m = sum_exp * scale_old;
                 sum_exp = m + scale_new;
                 max_score = new_max;
@@ -283,7 +453,7 @@ void orc_forward_from_projections(const orc_cfg *c, float *kcache, float *vcache
         } else {
             float *att = att_scratch + (size_t)h * seq_len;
             for (int t = start; t <= pos; t++) {
-                float score = orc_dot(qh, kcache + (size_t)t * kv_dim + kv_off, D);
+                float score = cache_dot(kv, q8, t, kv_dim, kv_off, qh, D);
                 float s = score * scale;
                 if (softcap > 0.0f) {
                     float r = s / softcap;
@@ -293,9 +463,42 @@ void orc_forward_from_projections(const orc_cfg *c, float *kcache, float *vcache
             }
             orc_softmax(att, seq_len);
             for (int t = start; t <= pos; t++)
-                orc_saxpy(att[t - start], vcache + (size_t)t * kv_dim + kv_off, oh, D);
+                cache_saxpy(kv, q8, t, kv_dim, kv_off, att[t - start], oh, D);
         }
     }
+}
+
+/* Attention.forwardFromProjections (Attention.java:284-367), optional bias omitted (absent
+ * from every configuration this build covers).  q and k are modified in place exactly as
+ * state.q / state.k are; the K/V rows are appended at `pos`; out = xb2[Hq*D].
+ * use_flash != 0 selects the online-softmax loop of Attention.forward (Attention.java:161-207).
+ * kcache/vcache are one layer's FLOAT32 [max_seq][kvDim] arrays.  rope_cos/rope_sin are the
+ * table the layer selects (global or local, Attention.java:317); NULL skips RoPE (NoPE). */
+void orc_forward_from_projections(const orc_cfg *c, float *kcache, float *vcache,
+                                  const float *qnorm_w, const float *knorm_w,
+                                  const float *rope_cos, const float *rope_sin,
+                                  float *q, float *k, const float *v,
+                                  int layer, int pos, float *out, float *att_scratch,
+                                  int use_flash, int n_threads)
+{
+    orc_layer_cache kv = {kcache, vcache, NULL, NULL, NULL, NULL};
+    forward_impl(c, &kv, 0, qnorm_w, knorm_w, rope_cos, rope_sin, q, k, v, layer, pos, out,
+                 att_scratch, use_flash, n_threads);
+}
+
+/* The same layer-call over a Q8_0 cache (KVCache Mode.Q8_0): quants [max_seq][kvDim],
+ * scales [max_seq][kvDim/32] for K and V. */
+void orc_forward_from_projections_q8(const orc_cfg *c, int8_t *kq, float *ks, int8_t *vq,
+                                     float *vs, const float *qnorm_w, const float *knorm_w,
+                                     const float *rope_cos, const float *rope_sin, float *q,
+                                     float *k, const float *v, int layer, int pos, float *out,
+                                     float *att_scratch, int use_flash, int n_threads,
+                                     int q8_mode)
+{
+    orc_layer_cache kv = {NULL, NULL, kq, vq, ks, vs};
+    int mode = q8_mode == ORC_Q8_SIMD8 ? ORC_Q8_SIMD8 : ORC_Q8_SCALAR;
+    forward_impl(c, &kv, mode, qnorm_w, knorm_w, rope_cos, rope_sin, q, k, v, layer, pos, out,
+                 att_scratch, use_flash, n_threads);
 }
 
 /* The reference has no batched prefill: the prompt runs as P sequential single-token

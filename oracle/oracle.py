@@ -95,6 +95,20 @@ def lib():
             C.POINTER(_Cfg), _F, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int, C.c_int,
             _F, C.c_int]
         L.orc_max_threads.restype = C.c_int
+        _I8 = C.POINTER(C.c_int8)
+        L.orc_round_half_up.restype = C.c_int
+        L.orc_round_half_up.argtypes = [C.c_float]
+        L.orc_q8_quantize.argtypes = [_F, C.c_int, _I8, _F]
+        L.orc_q8_dot.restype = C.c_float
+        L.orc_q8_dot.argtypes = [_F, _I8, _F, C.c_int]
+        L.orc_q8_saxpy.argtypes = [C.c_float, _I8, _F, _F, C.c_int]
+        L.orc_q8_quantize_simd8.argtypes = [_F, C.c_int, _I8, _F]
+        L.orc_q8_dot_simd8.restype = C.c_float
+        L.orc_q8_dot_simd8.argtypes = [_F, _I8, _F, C.c_int]
+        L.orc_q8_saxpy_simd8.argtypes = [C.c_float, _I8, _F, _F, C.c_int]
+        L.orc_forward_from_projections_q8.argtypes = [
+            C.POINTER(_Cfg), _I8, _F, _I8, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int, _F,
+            _F, C.c_int, C.c_int, C.c_int]
         _lib = L
     return _lib
 
@@ -203,6 +217,72 @@ def prefill_sequential(cfg: OracleConfig, kcache, vcache, q, k, v, layer, pos0,
         _p(f32(rope_sin)) if rope_sin is not None else None,
         _p(q), _p(k), _p(v), layer, pos0, P, _p(out), int(n_threads))
     return out
+
+
+def _pi8(a):
+    assert a.dtype == np.int8 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.POINTER(C.c_int8))
+
+
+def round_half_up(y) -> int:
+    return lib().orc_round_half_up(float(np.float32(y)))
+
+
+# The two Q8_0 contracts the JVM chooses between (KVCache.loadQ8Ops, KVCache.java:54-62).
+Q8_SCALAR = 1   # quantizeBlocksScalar / dotQ8BlockScalar / saxpyQ8BlockScalar
+Q8_SIMD8 = 2    # SimdQ8KvOps on an 8-lane float species (AVX2): truncating quantize, FMA lanes
+
+
+def q8_quantize(x, mode=Q8_SCALAR):
+    """Returns (int8 quants[n], fp32 scales[n/32]) (quantizeBlocksScalar, or
+    SimdQ8KvOps.quantize for Q8_SIMD8)."""
+    x = f32(x)
+    q = np.zeros(x.size, np.int8)
+    sc = np.zeros(x.size // 32, np.float32)
+    fn = lib().orc_q8_quantize_simd8 if mode == Q8_SIMD8 else lib().orc_q8_quantize
+    fn(_p(x), x.size, _pi8(q), _p(sc))
+    return q, sc
+
+
+def q8_dot(q, kq, ks, mode=Q8_SCALAR) -> np.float32:
+    q = f32(q)
+    fn = lib().orc_q8_dot_simd8 if mode == Q8_SIMD8 else lib().orc_q8_dot
+    return np.float32(fn(_p(q), _pi8(np.ascontiguousarray(kq, np.int8)), _p(f32(ks)), q.size))
+
+
+def q8_saxpy(w, vq, vs, out, mode=Q8_SCALAR):
+    out = f32(out).copy()
+    fn = lib().orc_q8_saxpy_simd8 if mode == Q8_SIMD8 else lib().orc_q8_saxpy
+    fn(float(np.float32(w)), _pi8(np.ascontiguousarray(vq, np.int8)), _p(f32(vs)), _p(out),
+       out.size)
+    return out
+
+
+def forward_from_projections_q8(cfg: OracleConfig, kq, ks, vq, vs, q, k, v, layer, pos,
+                                qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None,
+                                use_flash=False, n_threads=1, mode=Q8_SCALAR):
+    """Attention.forwardFromProjections over a Q8_0 cache.  kq/vq: int8 [max_seq, kvDim],
+    ks/vs: float32 [max_seq, kvDim/32], modified in place (row `pos` is quantized and
+    stored).  `mode` selects the JVM's Q8_0 contract.  Returns (out, q_after, k_after)."""
+    c = cfg.c()
+    q, k, v = f32(q).copy(), f32(k).copy(), f32(v)
+    for a in (kq, vq):
+        assert a.dtype == np.int8 and a.flags["C_CONTIGUOUS"] and a.size >= cfg.max_seq * cfg.kv_dim
+    for a in (ks, vs):
+        assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+        assert a.size >= cfg.max_seq * cfg.kv_dim // 32
+    assert 0 <= pos < cfg.max_seq
+    out = np.zeros(cfg.n_heads * cfg.head_size, np.float32)
+    att = np.zeros(cfg.n_heads * (pos + 1), np.float32)
+    lib().orc_forward_from_projections_q8(
+        C.byref(c), _pi8(kq), _p(ks), _pi8(vq), _p(vs),
+        _p(f32(qnorm_w)) if qnorm_w is not None else None,
+        _p(f32(knorm_w)) if knorm_w is not None else None,
+        _p(f32(rope_cos)) if rope_cos is not None else None,
+        _p(f32(rope_sin)) if rope_sin is not None else None,
+        _p(q), _p(k), _p(v), layer, pos, _p(out), _p(att), int(use_flash), int(n_threads),
+        int(mode))
+    return out, q, k
 
 
 def max_threads() -> int:

@@ -118,3 +118,61 @@ def compare_cache(fp: hfp.HipForwardPass, layer: int, kc: np.ndarray, vc: np.nda
     if not np.array_equal(gv, vc[lo:hi]):
         bad = np.argwhere(gv != vc[lo:hi])
         raise AssertionError(f"{what}: V cache differs at {len(bad)} elements, first row {bad[0][0] + lo}")
+
+
+# ------------------------------------------------------------------- Q8_0 cache (KVCache.Mode.Q8_0)
+@dataclass
+class LayerDataQ8:
+    kq: np.ndarray      # [max_seq, kvDim] int8 (KVCache.keyQuants layout)
+    ks: np.ndarray      # [max_seq, kvDim/32] fp32 (KVCache.keyScales layout)
+    vq: np.ndarray
+    vs: np.ndarray
+    q: np.ndarray
+    k: np.ndarray
+    v: np.ndarray
+    qk_norm: Optional[tuple] = None
+
+
+def quantize_rows(x: np.ndarray, mode: int = orc.Q8_SCALAR):
+    """Rows [n, kvDim] -> (quants [n, kvDim] int8, scales [n, kvDim/32]) by the oracle's
+    quantizer for `mode` (blocks of 32 never straddle rows: kvDim is a multiple of 32)."""
+    n, kv = x.shape
+    q, s = orc.q8_quantize(x.reshape(-1), mode)
+    return q.reshape(n, kv), s.reshape(n, kv // 32)
+
+
+def make_layer_q8(c: hfp.ModelConfig, max_seq: int, filled: int, seed: int, k_scale: float = 1.0,
+                  qk_norm: bool = False, mode: int = orc.Q8_SCALAR) -> LayerDataQ8:
+    """make_layer's rows [0, filled) quantized to Q8_0; rows beyond stay zero."""
+    d = make_layer(c, max_seq, filled, seed, k_scale, qk_norm)
+    kq, ks = quantize_rows(d.kc, mode)
+    vq, vs = quantize_rows(d.vc, mode)
+    return LayerDataQ8(kq, ks, vq, vs, d.q, d.k, d.v, d.qk_norm)
+
+
+def oracle_call_q8(c: hfp.ModelConfig, max_seq: int, d: LayerDataQ8, layer: int, pos: int,
+                   n_threads: int = 8, mode: int = orc.Q8_SCALAR):
+    """The oracle over copies of the Q8_0 cache; returns (out, (kq, ks, vq, vs) after)."""
+    oc = oracle_config(c, max_seq)
+    cs, sn = oracle_tables(c, max_seq, layer)
+    kq, ks, vq, vs = d.kq.copy(), d.ks.copy(), d.vq.copy(), d.vs.copy()
+    qw, kw = (d.qk_norm if d.qk_norm is not None else (None, None))
+    out, _, _ = orc.forward_from_projections_q8(oc, kq, ks, vq, vs, d.q, d.k, d.v, layer, pos,
+                                                qnorm_w=qw, knorm_w=kw, rope_cos=cs, rope_sin=sn,
+                                                n_threads=n_threads, mode=mode)
+    return out, (kq, ks, vq, vs)
+
+
+def compare_cache_q8(fp: hfp.HipForwardPass, layer: int, want: tuple, what: str,
+                     rows: Optional[tuple] = None) -> None:
+    """Quants and scales read back with llmp_kv_read_q8 bit-identical to the oracle's."""
+    lo, hi = rows if rows is not None else (0, want[0].shape[0])
+    got = fp.kv.read_q8(layer, lo, hi - lo)
+    for name, g, w in zip(("K quants", "K scales", "V quants", "V scales"), got, want):
+        w = w[lo:hi]
+        if not np.array_equal(g.view(np.uint8) if g.dtype == np.int8 else g.view(np.uint32),
+                              w.view(np.uint8) if w.dtype == np.int8 else w.view(np.uint32)):
+            bad = np.argwhere(g != w)
+            first = tuple(bad[0]) if len(bad) else (0, 0)
+            raise AssertionError(f"{what}: {name} differ at {len(bad)} elements, first "
+                                 f"(row {first[0] + lo}, col {first[1]}): {g[first]!r} vs {w[first]!r}")

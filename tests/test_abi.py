@@ -46,6 +46,14 @@ def test_error_codes_match_header():
     assert {v: k for k, v in codes.items()} == _lib.ERR_NAMES
 
 
+def test_constants_match_header():
+    text = open(HEADER).read()
+    defs = dict((name, int(val)) for name, val in re.findall(r"#define\s+(LLMP_\w+)\s+(-?\d+)", text))
+    for name in ("LLMP_KV_F32", "LLMP_KV_Q8_0", "LLMP_KV_Q8_0_TRUNC", "LLMP_ROPE_NORMAL", "LLMP_ROPE_NEOX",
+                 "LLMP_ROPE_SEL_NONE", "LLMP_ROPE_SEL_GLOBAL", "LLMP_ROPE_SEL_LOCAL"):
+        assert getattr(_lib, name) == defs[name], name
+
+
 def test_calls_before_init_fail_with_not_init():
     h = C.c_uint64()
     rc = _lib.status("llmp_kv_create", 1, 16, 1, 64, 0, C.byref(h))

@@ -354,3 +354,192 @@ def test_prefill_equals_sequential_decode_calls():
                                                rope_cos=cs, rope_sin=sn)
         assert np.array_equal(out[i], o)
     assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
+
+
+# ----------------------------------------------------------------- Q8_0 KV cache mode
+def _round_half_up_f64(y):
+    """Math.round(float): floor(y + 0.5) computed exactly in float64."""
+    return np.floor(np.float64(np.float32(y)) + 0.5)
+
+
+def test_q8_round_half_up_matches_exact_definition():
+    edges = [0.0, 0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -127.5, 0.49999997, -0.49999997,
+             0.50000006, -0.50000006, 1e-30, -1e-30, 127.0, -128.0, 3.4999998, -3.4999998]
+    for y in edges:
+        assert orc.round_half_up(y) == _round_half_up_f64(y), y
+    rng = np.random.default_rng(30)
+    ys = np.concatenate([rng.uniform(-130, 130, 4000), np.arange(-128, 128) + 0.5]).astype(F32)
+    got = np.array([orc.round_half_up(y) for y in ys])
+    assert np.array_equal(got, _round_half_up_f64(ys))
+
+
+def test_q8_quantize_closed_form_and_round_trip():
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal(256) * rng.uniform(0.01, 10, 8).repeat(32)).astype(F32)
+    q, sc = orc.q8_quantize(x)
+    xb = x.reshape(8, 32)
+    want_scale = (np.abs(xb).max(axis=1) / F32(127.0)).astype(F32)     # IEEE float32 division
+    assert np.array_equal(sc, want_scale)
+    inv = (F32(1.0) / want_scale).astype(F32)
+    y = (xb * inv[:, None]).astype(F32)
+    want_q = np.clip(_round_half_up_f64(y), -128, 127).astype(np.int8).reshape(-1)
+    assert np.array_equal(q, want_q)
+    # every block reaches +-127 at its largest |x|; dequantisation error <= scale/2 (+ulp)
+    assert np.all(np.abs(q.reshape(8, 32)).max(axis=1) == 127)
+    deq = q.reshape(8, 32).astype(np.float64) * sc[:, None]
+    assert np.all(np.abs(deq - xb) <= sc[:, None] * 0.5 * (1 + 1e-5))
+    # an all-zero block has scale 0 and zero quants
+    q0, s0 = orc.q8_quantize(np.zeros(32, F32))
+    assert s0[0] == 0 and not q0.any()
+
+
+def test_q8_dot_and_saxpy_match_float64_on_dequantised_values():
+    rng = np.random.default_rng(32)
+    for D in (64, 128, 256):
+        k = rng.standard_normal(D).astype(F32)
+        qv = rng.standard_normal(D).astype(F32)
+        kq, ks = orc.q8_quantize(k)
+        deq = kq.astype(np.float64) * np.repeat(ks, 32)
+        assert abs(float(orc.q8_dot(qv, kq, ks)) - float(qv.astype(np.float64) @ deq)) < 1e-4
+        out0 = rng.standard_normal(D).astype(F32)
+        got = orc.q8_saxpy(0.37, kq, ks, out0)
+        np.testing.assert_allclose(got, out0 + np.float32(0.37) * deq, atol=2e-6)
+        # per-block unfused order: the scalar path's exact float result
+        acc = np.float32(0)
+        for b in range(D // 32):
+            a = np.float32(0)
+            for i in range(32):
+                a = np.float32(a + np.float32(qv[32 * b + i] * np.float32(kq[32 * b + i])))
+            acc = np.float32(acc + np.float32(a * ks[b]))
+        assert orc.q8_dot(qv, kq, ks) == acc
+
+
+@pytest.mark.parametrize("shape", [(32, 8, 64), (24, 8, 128), (4, 1, 256)])
+def test_q8_layer_call_matches_float64_on_dequantised_cache(shape):
+    Hq, Hkv, D = shape
+    S, pos = 80, 70
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0)
+    rng = np.random.default_rng(33)
+    kv = Hkv * D
+    kf = rng.standard_normal((S, kv)).astype(F32)
+    vf = rng.standard_normal((S, kv)).astype(F32)
+    kq = np.zeros((S, kv), np.int8); vq = np.zeros((S, kv), np.int8)
+    ks = np.zeros((S, kv // 32), F32); vs = np.zeros((S, kv // 32), F32)
+    for t in range(pos):
+        kq[t], ks[t] = orc.q8_quantize(kf[t])
+        vq[t], vs[t] = orc.q8_quantize(vf[t])
+    q = rng.standard_normal(Hq * D).astype(F32)
+    k = rng.standard_normal(kv).astype(F32)
+    v = rng.standard_normal(kv).astype(F32)
+    cs, sn = orc.rope_tables(D, S, 5e5)
+    kq0, ks0, vq0, vs0 = kq.copy(), ks.copy(), vq.copy(), vs.copy()
+    out, q2, k2 = orc.forward_from_projections_q8(cfg, kq, ks, vq, vs, q, k, v, 0, pos,
+                                                  rope_cos=cs, rope_sin=sn)
+    # the appended row is the quantisation of the rotated k and of v
+    qk_row, sk_row = orc.q8_quantize(k2)
+    qv_row, sv_row = orc.q8_quantize(v)
+    assert np.array_equal(kq[pos], qk_row) and np.array_equal(ks[pos], sk_row)
+    assert np.array_equal(vq[pos], qv_row) and np.array_equal(vs[pos], sv_row)
+    kq[pos] = kq0[pos]; ks[pos] = ks0[pos]; vq[pos] = vq0[pos]; vs[pos] = vs0[pos]
+    assert np.array_equal(kq, kq0) and np.array_equal(vs, vs0)
+    K = (kq0.astype(np.float64).reshape(S, -1, 32) * ks0[:, :, None]).reshape(S, kv)
+    V = (vq0.astype(np.float64).reshape(S, -1, 32) * vs0[:, :, None]).reshape(S, kv)
+    K[pos] = (qk_row.astype(np.float64).reshape(-1, 32) * sk_row[:, None]).reshape(-1)
+    V[pos] = (qv_row.astype(np.float64).reshape(-1, 32) * sv_row[:, None]).reshape(-1)
+    want = rm.attention(q2, K, V, Hq, Hkv, D, 0, pos, 1 / np.sqrt(D))
+    rm.assert_close(out, want, atol=2e-5, rtol=1e-4, what="q8 layer-call")
+    b, _, _ = orc.forward_from_projections_q8(cfg, kq0.copy(), ks0.copy(), vq0.copy(), vs0.copy(),
+                                              q, k, v, 0, pos, rope_cos=cs, rope_sin=sn,
+                                              use_flash=True)
+    np.testing.assert_allclose(out, b, atol=2e-6)
+
+
+# ----------------------------------------- Q8_0, the 8-lane SimdQ8KvOps contract (AVX2 hosts)
+def _fma32(a, b, c):
+    """float32 fma: a*b + c exact in float64 (a is an int8 quant or a product of <= 32
+    significant bits, magnitudes kept moderate by the callers), rounded once to float32."""
+    return np.float32(np.float64(a) * np.float64(b) + np.float64(c))
+
+
+def test_q8_simd8_quantize_truncates_toward_zero():
+    rng = np.random.default_rng(40)
+    x = (rng.standard_normal(512) * rng.uniform(0.01, 10, 16).repeat(32)).astype(F32)
+    q, sc = orc.q8_quantize(x, orc.Q8_SIMD8)
+    qs, scs = orc.q8_quantize(x)
+    assert np.array_equal(sc, scs)                                   # same scale as the scalar path
+    inv = (F32(1.0) / sc).astype(F32)
+    y = (x.reshape(16, 32) * inv[:, None]).astype(F32)
+    assert np.array_equal(q, np.clip(np.trunc(y), -128, 127).astype(np.int8).reshape(-1))
+    assert (q != qs).any()                                           # the contracts differ
+    # hand cases: scale 1 (max 127), so y = x exactly
+    blk = np.array([127.0, -127.0, 2.7, -2.7, 0.5, -0.5, 126.99, -126.99] + [0.0] * 24, F32)
+    qb, sb = orc.q8_quantize(blk, orc.Q8_SIMD8)
+    assert sb[0] == 1.0 and list(qb[:8]) == [127, -127, 2, -2, 0, 0, 126, -126]
+    qr, _ = orc.q8_quantize(blk)
+    assert list(qr[:8]) == [127, -127, 3, -3, 1, 0, 127, -127]       # Math.round: ties up
+
+
+def test_q8_simd8_dot_and_saxpy_follow_lane_fma_order():
+    rng = np.random.default_rng(41)
+    for D in (64, 128, 256):
+        qv = rng.standard_normal(D).astype(F32)
+        kq = rng.integers(-128, 128, D).astype(np.int8)
+        ks = rng.uniform(0.001, 0.05, D // 32).astype(F32)
+        total = F32(0)
+        for b in range(D // 32):
+            lane = [F32(0)] * 8
+            for c in range(0, 32, 8):
+                for l in range(8):
+                    i = 32 * b + c + l
+                    lane[l] = _fma32(kq[i], qv[i], lane[l])
+            s = lane[0]
+            for l in range(1, 8):
+                s = F32(s + lane[l])
+            total = F32(total + F32(s * ks[b]))
+        assert orc.q8_dot(qv, kq, ks, orc.Q8_SIMD8) == total
+        out0 = rng.standard_normal(D).astype(F32)
+        got = orc.q8_saxpy(0.37, kq, ks, out0, orc.Q8_SIMD8)
+        w = np.repeat((F32(0.37) * ks).astype(F32), 32)
+        want = np.array([_fma32(kq[i], w[i], out0[i]) for i in range(D)], F32)
+        assert np.array_equal(got, want)
+    # FMA witness: lane 0 sees quant -3 x q 1 (chunk 0), then quant 3 x q (1 + 2^-23)
+    # (chunk 1).  Fused: 3*(1 + 2^-23) - 3 = 3*2^-23 exactly; an unfused product rounds
+    # 3 + 3*2^-23 to a multiple of 2^-22 first, leaving 2^-22 or 2^-21.
+    qv = np.zeros(32, F32)
+    kq = np.zeros(32, np.int8)
+    qv[0], kq[0] = 1.0, -3
+    qv[8], kq[8] = F32(1 + 2.0 ** -23), 3
+    assert orc.q8_dot(qv, kq, np.ones(1, F32), orc.Q8_SIMD8) == F32(3 * 2.0 ** -23)
+    assert orc.q8_dot(qv, kq, np.ones(1, F32)) != F32(3 * 2.0 ** -23)   # scalar: unfused
+
+
+def test_q8_simd8_layer_call():
+    Hq, Hkv, D, S, pos = 24, 8, 128, 80, 70
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0)
+    rng = np.random.default_rng(42)
+    kv = Hkv * D
+    kq = np.zeros((S, kv), np.int8); vq = np.zeros((S, kv), np.int8)
+    ks = np.zeros((S, kv // 32), F32); vs = np.zeros((S, kv // 32), F32)
+    for t in range(pos):
+        kq[t], ks[t] = orc.q8_quantize(rng.standard_normal(kv).astype(F32), orc.Q8_SIMD8)
+        vq[t], vs[t] = orc.q8_quantize(rng.standard_normal(kv).astype(F32), orc.Q8_SIMD8)
+    q = rng.standard_normal(Hq * D).astype(F32)
+    k = rng.standard_normal(kv).astype(F32)
+    v = rng.standard_normal(kv).astype(F32)
+    cs, sn = orc.rope_tables(D, S, 5e5)
+    kq0, ks0, vq0, vs0 = kq.copy(), ks.copy(), vq.copy(), vs.copy()
+    out, q2, k2 = orc.forward_from_projections_q8(cfg, kq, ks, vq, vs, q, k, v, 0, pos,
+                                                  rope_cos=cs, rope_sin=sn, mode=orc.Q8_SIMD8)
+    qk_row, sk_row = orc.q8_quantize(k2, orc.Q8_SIMD8)
+    qv_row, sv_row = orc.q8_quantize(v, orc.Q8_SIMD8)
+    assert np.array_equal(kq[pos], qk_row) and np.array_equal(ks[pos], sk_row)
+    assert np.array_equal(vq[pos], qv_row) and np.array_equal(vs[pos], sv_row)
+    K = (kq.astype(np.float64).reshape(S, -1, 32) * ks[:, :, None]).reshape(S, kv)
+    V = (vq.astype(np.float64).reshape(S, -1, 32) * vs[:, :, None]).reshape(S, kv)
+    want = rm.attention(q2, K, V, Hq, Hkv, D, 0, pos, 1 / np.sqrt(D))
+    rm.assert_close(out, want, atol=2e-5, rtol=1e-4, what="q8 simd8 layer-call")
+    # the scalar contract stores a different row for the same input
+    kq1, ks1, vq1, vs1 = kq0.copy(), ks0.copy(), vq0.copy(), vs0.copy()
+    orc.forward_from_projections_q8(cfg, kq1, ks1, vq1, vs1, q, k, v, 0, pos, rope_cos=cs,
+                                    rope_sin=sn)
+    assert not np.array_equal(kq1[pos], kq[pos])
