@@ -45,6 +45,24 @@ def kv_bytes(ctx: int, q8: bool = False) -> int:
     return 2 * ctx * HKV * (D + D // 32 * 4) if q8 else 2 * ctx * HKV * D * 4
 
 
+def fill_caches(fp, c, ctx: int, n_layers: int, q8: bool, rng) -> None:
+    """Rows [0, ctx-1) of every rotated layer cache: N(0,1) fp32 rows (K x 0.5), or synthetic
+    Q8_0 rows (uniform quants, block scales of the size N(0,1) blocks give, ~max/127)."""
+    if q8:
+        kq = rng.integers(-127, 128, (ctx - 1, c.kv_dim), dtype=np.int8)
+        vq = rng.integers(-127, 128, (ctx - 1, c.kv_dim), dtype=np.int8)
+        ks = np.full((ctx - 1, c.kv_dim // 32), 1.2 / 127, np.float32)
+        vs = np.full((ctx - 1, c.kv_dim // 32), 2.4 / 127, np.float32)
+        for layer in range(n_layers):
+            fp.kv.write_q8(layer, 0, kq, ks, vq, vs)
+            log(f"[bench] Q8_0 layer cache {layer + 1}/{n_layers} filled")
+    else:
+        kc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32) * np.float32(0.5)
+        vc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32)
+        for layer in range(n_layers):
+            fp.kv.write(layer, 0, kc, vc)
+
+
 def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int,
             q8: bool = False) -> dict:
     from llmplayer_amd import _lib
@@ -58,22 +76,7 @@ def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int,
     fp = hfp.HipForwardPass(c, ctx, kv_dtype=_lib.LLMP_KV_Q8_0 if q8 else _lib.LLMP_KV_F32)
     try:
         rng = np.random.default_rng(2024)
-        if q8:
-            # Synthetic Q8_0 rows: uniform quants, scales of N(0,0.5)-sized blocks (~max/127).
-            kq = rng.integers(-127, 128, (ctx - 1, c.kv_dim), dtype=np.int8)
-            vq = rng.integers(-127, 128, (ctx - 1, c.kv_dim), dtype=np.int8)
-            ks = np.full((ctx - 1, c.kv_dim // 32), 1.2 / 127, np.float32)
-            vs = np.full((ctx - 1, c.kv_dim // 32), 2.4 / 127, np.float32)
-            for layer in range(n_layers):
-                fp.kv.write_q8(layer, 0, kq, ks, vq, vs)
-                log(f"[bench] Q8_0 layer cache {layer + 1}/{n_layers} filled")
-            del kq, vq, ks, vs
-        else:
-            kc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32) * np.float32(0.5)
-            vc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32)
-            for layer in range(n_layers):
-                fp.kv.write(layer, 0, kc, vc)
-            del kc, vc
+        fill_caches(fp, c, ctx, n_layers, q8, rng)
         fp.uploadQKV(rng.standard_normal(c.q_dim, dtype=np.float32),
                      rng.standard_normal(c.kv_dim, dtype=np.float32) * np.float32(0.5),
                      rng.standard_normal(c.kv_dim, dtype=np.float32))
@@ -255,19 +258,18 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
-def profile_workload(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int) -> int:
+def profile_workload(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int,
+                     q8: bool = False) -> int:
     """Eager layer-calls only (the decode kernels as rocprofv3 sees them one by one)."""
+    from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
-    per_layer = kv_bytes(ctx)
+    per_layer = kv_bytes(ctx, q8)
     n_layers = max(1, math.ceil(rotate_bytes / per_layer))
     c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
-    fp = hfp.HipForwardPass(c, ctx)
+    fp = hfp.HipForwardPass(c, ctx, kv_dtype=_lib.LLMP_KV_Q8_0 if q8 else _lib.LLMP_KV_F32)
     try:
         rng = np.random.default_rng(2024)
-        kc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32) * np.float32(0.5)
-        vc = rng.standard_normal((ctx - 1, c.kv_dim), dtype=np.float32)
-        for layer in range(n_layers):
-            fp.kv.write(layer, 0, kc, vc)
+        fill_caches(fp, c, ctx, n_layers, q8, rng)
         fp.uploadQKV(rng.standard_normal(c.q_dim, dtype=np.float32),
                      rng.standard_normal(c.kv_dim, dtype=np.float32) * np.float32(0.5),
                      rng.standard_normal(c.kv_dim, dtype=np.float32))
@@ -277,8 +279,15 @@ def profile_workload(ctx: int, steps: int, warmup: int, splits: int, rotate_byte
         fp.sync()
     finally:
         fp.close()
-    log(f"[bench] profile workload: ctx {ctx}, {warmup}+{steps} eager layer-calls over "
-        f"{n_layers} layer caches, plan {plan}")
+    log(f"[bench] profile workload: ctx {ctx}{' Q8_0' if q8 else ''}, {warmup}+{steps} eager "
+        f"layer-calls over {n_layers} layer caches, plan {plan}")
+    return 0
+
+
+def profile_prefill(P: int, steps: int) -> int:
+    """C5 prefill calls only (append + attention kernels as rocprofv3 sees them)."""
+    r = prefill_run(P, steps)
+    log(f"[bench] profile prefill: P={P}, {r}")
     return 0
 
 
@@ -316,6 +325,10 @@ def main() -> int:
     ap.add_argument("--profile-workload", action="store_true",
                     help="for rocprofv3: only the warm-up and K eager layer-calls at --ctx "
                          "(no graph replay, no second context, no CPU baseline), then exit")
+    ap.add_argument("--kv", choices=("f32", "q8"), default="f32",
+                    help="KV cache of --profile-workload")
+    ap.add_argument("--profile-prefill", type=int, default=0, metavar="P",
+                    help="for rocprofv3: C5 prefill of P tokens (K graph + K eager calls), then exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="for rocprofv3 PMC calibration: 5 launches of the library's plain "
                          "copy kernel over MIB MiB, then exit")
@@ -334,7 +347,9 @@ def main() -> int:
         return copy_calibration(args.copy_calibration)
     if args.profile_workload:
         return profile_workload(args.ctx, args.steps, args.warmup, args.splits,
-                                int(args.rotate_gib * 2**30))
+                                int(args.rotate_gib * 2**30), q8=args.kv == "q8")
+    if args.profile_prefill:
+        return profile_prefill(args.profile_prefill, args.steps)
     info = hfp.device_info()
     log(f"[bench] device {info['arch']} with {info['n_cu']} CUs")
     rot = int(args.rotate_gib * 2**30)
@@ -347,11 +362,13 @@ def main() -> int:
         log(f"[bench] ctx {args.ctx2}: {second['us_per_layer_call']:.2f} us/layer-call, "
             f"{second['kv_read_gbps']:.0f} GB/s, split kernel {second['split_kernel_us']:.2f} us")
 
-    q8_run = None
+    q8_runs = []
     if args.q8:
-        q8_run = gpu_run(args.ctx, args.steps, args.warmup, args.splits, rot, q8=True)
-        log(f"[bench] ctx {args.ctx} Q8_0: {q8_run['us_per_layer_call']:.2f} us/layer-call, "
-            f"{q8_run['kv_read_gbps']:.0f} GB/s, split kernel {q8_run['split_kernel_us']:.2f} us")
+        for ctx in [args.ctx] + ([args.ctx2] if args.ctx2 else []):
+            r = gpu_run(ctx, args.steps, args.warmup, args.splits, rot, q8=True)
+            log(f"[bench] ctx {ctx} Q8_0: {r['us_per_layer_call']:.2f} us/layer-call, "
+                f"{r['kv_read_gbps']:.0f} GB/s, split kernel {r['split_kernel_us']:.2f} us")
+            q8_runs.append(r)
 
     prefill = []
     if args.prefill:
@@ -405,19 +422,23 @@ def main() -> int:
             "reduce_kernel_us": round(second["reduce_kernel_us"], 3),
             "us_per_layer_call_eager": round(second["us_per_layer_call_eager"], 3),
             "kv_layers_rotated": second["n_layers"]}
-    if q8_run is not None:
-        bq = kv_bytes(args.ctx, True)
-        line["q8_0_kv"] = {
-            "workload": f"C3 decode attention over a Q8_0 cache, ctx {args.ctx}",
-            "us_per_layer_call": round(q8_run["us_per_layer_call"], 3),
-            "kv_read_gbps": round(q8_run["kv_read_gbps"], 1),
-            "split_kernel_us": round(q8_run["split_kernel_us"], 3),
-            "split_kernel_gbps": round(bq / (q8_run["split_kernel_us"] * 1e-6) / 1e9, 1),
-            "reduce_kernel_us": round(q8_run["reduce_kernel_us"], 3),
-            "algorithmic_bytes_per_launch": bq,
-            "splits": q8_run["plan"]["splits"], "waves": q8_run["plan"]["waves"],
-            "speedup_vs_f32_cache": round(main_run["us_per_layer_call"] /
-                                          q8_run["us_per_layer_call"], 3)}
+    if q8_runs:
+        f32_us = {args.ctx: main_run["us_per_layer_call"]}
+        if second is not None:
+            f32_us[args.ctx2] = second["us_per_layer_call"]
+        line["q8_0_kv"] = []
+        for r in q8_runs:
+            bq = kv_bytes(r["ctx"], True)
+            line["q8_0_kv"].append({
+                "workload": f"C3 decode attention over a Q8_0 cache, ctx {r['ctx']}",
+                "us_per_layer_call": round(r["us_per_layer_call"], 3),
+                "kv_read_gbps": round(r["kv_read_gbps"], 1),
+                "split_kernel_us": round(r["split_kernel_us"], 3),
+                "split_kernel_gbps": round(bq / (r["split_kernel_us"] * 1e-6) / 1e9, 1),
+                "reduce_kernel_us": round(r["reduce_kernel_us"], 3),
+                "algorithmic_bytes_per_launch": bq,
+                "splits": r["plan"]["splits"], "waves": r["plan"]["waves"],
+                "speedup_vs_f32_cache": round(f32_us[r["ctx"]] / r["us_per_layer_call"], 3)})
     if prefill:
         line["prefill_c5_llama1b"] = prefill
     print(json.dumps(line), flush=True)

@@ -76,6 +76,7 @@ int llmp_free(uint64_t dptr);
 int llmp_memcpy_htod(uint64_t dst, const void *src, uint64_t bytes, uint64_t stream);
 int llmp_memcpy_dtoh(void *dst, uint64_t src, uint64_t bytes, uint64_t stream);
 int llmp_memcpy_dtod(uint64_t dst, uint64_t src, uint64_t bytes, uint64_t stream);
+/* Zero `bytes` of device memory (hipMemsetAsync: not for use inside a graph capture). */
 int llmp_memset_zero(uint64_t dst, uint64_t bytes, uint64_t stream);
 int llmp_stream_create(uint64_t *stream);
 int llmp_stream_destroy(uint64_t stream);
@@ -116,7 +117,8 @@ int llmp_kv_write_q8(uint64_t handle, int layer, int pos0, int n, const int8_t *
 /* Device addresses of one layer's K and V planes ([kv_head][pos][head_dim] fp32, or the quant
  * planes of a Q8_0 cache). */
 int llmp_kv_layer_ptrs(uint64_t handle, int layer, uint64_t *k_plane, uint64_t *v_plane);
-/* Zero the whole pool (a new conversation). */
+/* Zero the whole pool (a new conversation; hipMemsetAsync: not for use inside a graph
+ * capture). */
 int llmp_kv_clear(uint64_t handle, uint64_t stream);
 
 /* ---- RoPE tables (RoPE.java:45-106; upload as CudaForwardPass.java:398-402) ------------ */

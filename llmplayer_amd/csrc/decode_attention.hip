@@ -16,52 +16,60 @@ constexpr Tune pick(int D, int G) {
     return Tune{(D == 256 || (G > 4 && D / 8 > 16)) ? 16 : 8, (G > 4) ? 1 : 2, true};
 }
 
+// The kernel instance for one shape, and the waves per workgroup it runs with.
+struct SplitKernel {
+    const void* fn;
+    int waves;
+};
+
 template <int D, int G, int W, bool Q8>
-hipError_t launch_dgw(const DecodeArgs& a, int n_kv_heads, hipStream_t stream) {
+SplitKernel kernel_dgw() {
     constexpr Tune t = pick(D, G);
     // Q8_0 rows are read as 16 quants per lane (D/16 lanes per row).
     constexpr int EPL = Q8 ? 16 : t.epl;
     constexpr int UNROLL = Q8 ? (G > 4 ? 1 : 2) : t.unroll;
-    hipLaunchKernelGGL((dk::decode_split_kernel<D, G, EPL, UNROLL, W, t.nt, Q8>),
-                       dim3(a.splits, n_kv_heads), dim3(W * 64), 0, stream, a);
-    return hipGetLastError();
+    return SplitKernel{
+        reinterpret_cast<const void*>(&dk::decode_split_kernel<D, G, EPL, UNROLL, W, t.nt, Q8>), W};
 }
 
 // 8-wave workgroups except where more than 4 query heads per KV head hold 16 elements per
 // lane (head_dim 256, or any Q8_0 cache): that register footprint leaves no room for them.
 template <int D, int G, bool Q8>
-hipError_t launch_dg(const DecodeArgs& a, int n_kv_heads, int waves, hipStream_t stream) {
+SplitKernel kernel_dg(int waves) {
     if constexpr ((D == 256 || Q8) && G > 4) {
-        return launch_dgw<D, G, 4, Q8>(a, n_kv_heads, stream);
+        return kernel_dgw<D, G, 4, Q8>();
     } else {
-        return waves == 8 ? launch_dgw<D, G, 8, Q8>(a, n_kv_heads, stream)
-                          : launch_dgw<D, G, 4, Q8>(a, n_kv_heads, stream);
+        return waves == 8 ? kernel_dgw<D, G, 8, Q8>() : kernel_dgw<D, G, 4, Q8>();
     }
 }
 
 template <int D, bool Q8>
-hipError_t launch_d(const DecodeArgs& a, int group, int n_kv_heads, int waves,
-                    hipStream_t stream) {
+SplitKernel kernel_d(int group, int waves) {
     switch (group) {
-    case 1: return launch_dg<D, 1, Q8>(a, n_kv_heads, waves, stream);
-    case 2: return launch_dg<D, 2, Q8>(a, n_kv_heads, waves, stream);
-    case 3: return launch_dg<D, 3, Q8>(a, n_kv_heads, waves, stream);
-    case 4: return launch_dg<D, 4, Q8>(a, n_kv_heads, waves, stream);
-    case 6: return launch_dg<D, 6, Q8>(a, n_kv_heads, waves, stream);
-    case 8: return launch_dg<D, 8, Q8>(a, n_kv_heads, waves, stream);
-    default: return hipErrorInvalidValue;
+    case 1: return kernel_dg<D, 1, Q8>(waves);
+    case 2: return kernel_dg<D, 2, Q8>(waves);
+    case 3: return kernel_dg<D, 3, Q8>(waves);
+    case 4: return kernel_dg<D, 4, Q8>(waves);
+    case 6: return kernel_dg<D, 6, Q8>(waves);
+    case 8: return kernel_dg<D, 8, Q8>(waves);
+    default: return SplitKernel{nullptr, 0};
     }
 }
 
 template <bool Q8>
-hipError_t launch_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads, int waves,
-                        hipStream_t stream) {
+SplitKernel kernel_split(int head_dim, int group, int waves) {
     switch (head_dim) {
-    case 64: return launch_d<64, Q8>(a, group, n_kv_heads, waves, stream);
-    case 128: return launch_d<128, Q8>(a, group, n_kv_heads, waves, stream);
-    case 256: return launch_d<256, Q8>(a, group, n_kv_heads, waves, stream);
-    default: return hipErrorInvalidValue;
+    case 64: return kernel_d<64, Q8>(group, waves);
+    case 128: return kernel_d<128, Q8>(group, waves);
+    case 256: return kernel_d<256, Q8>(group, waves);
+    default: return SplitKernel{nullptr, 0};
     }
+}
+
+SplitKernel resolve_split(int head_dim, int group, int waves, bool q8) {
+    if (waves != 4 && waves != 8) return SplitKernel{nullptr, 0};
+    return q8 ? kernel_split<true>(head_dim, group, waves)
+              : kernel_split<false>(head_dim, group, waves);
 }
 
 __global__ void copy_kernel(float4* __restrict__ dst, const float4* __restrict__ src, size_t n) {
@@ -79,11 +87,26 @@ bool decode_shape_supported(int head_dim, int group) {
     return d_ok && g_ok;
 }
 
+int decode_split_waves(int head_dim, int group, int waves, bool q8) {
+    return resolve_split(head_dim, group, waves, q8).waves;
+}
+
+int decode_split_blocks_per_cu(int head_dim, int group, int waves, bool q8) {
+    const SplitKernel k = resolve_split(head_dim, group, waves, q8);
+    if (!k.fn) return 0;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k.fn, k.waves * 64, 0) != hipSuccess)
+        return 0;
+    return n;
+}
+
 hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads,
                                int waves, bool q8, hipStream_t stream) {
-    if (waves != 4 && waves != 8) return hipErrorInvalidValue;
-    return q8 ? launch_split<true>(a, head_dim, group, n_kv_heads, waves, stream)
-              : launch_split<false>(a, head_dim, group, n_kv_heads, waves, stream);
+    const SplitKernel k = resolve_split(head_dim, group, waves, q8);
+    if (!k.fn) return hipErrorInvalidValue;
+    DecodeArgs args = a;
+    void* params[] = {&args};
+    return hipLaunchKernel(k.fn, dim3(a.splits, n_kv_heads), dim3(k.waves * 64), params, 0, stream);
 }
 
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,

@@ -208,7 +208,7 @@ __device__ void quantize_row_lds(const float* x, signed char* q, float* sc, floa
 
 // Online-softmax update of one row group with U rows: s = (q . K_t) in the log2 domain,
 // masked rows get -inf; o and l are rescaled once per call.
-template <int D, int G, int EPL, int U>
+template <int D, int G, int EPL, int U, bool LAZY = false>
 __device__ __forceinline__ void accumulate_rows(const float (&qr)[G][EPL],
                                                 const float4 (&kf)[U][EPL / 4],
                                                 const float4 (&vf)[U][EPL / 4],
@@ -246,14 +246,17 @@ __device__ __forceinline__ void accumulate_rows(const float (&qr)[G][EPL],
             s[u][h] = valid[u] ? s[u][h] : -__builtin_inff();
             mx = fmaxf(mx, s[u][h]);
         }
-        const float alpha = fast_exp2(m[h] - mx);
-        m[h] = mx;
-        float lsum = l[h] * alpha;
+        float lsum = l[h];
+        if (!LAZY || __any(mx > m[h] + kLazyMargin)) {
+            const float alpha = fast_exp2(m[h] - mx);
+            m[h] = mx;
+            lsum = lsum * alpha;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) o[h][e] = o[h][e] * alpha;
+            for (int e = 0; e < EPL; ++e) o[h][e] = o[h][e] * alpha;
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const float p = fast_exp2(s[u][h] - mx);
+            const float p = fast_exp2(s[u][h] - m[h]);
             lsum = lsum + p;
 #pragma unroll
             for (int c = 0; c < F::C4; ++c) {
@@ -386,10 +389,8 @@ __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const
     }
 }
 
-template <int D, int G, int EPL, int U, int WAVES, bool NT, bool Q8 = false, int VAR = 0>
+template <int D, int G, int EPL, int U, int WAVES, bool NT, bool Q8 = false, bool LAZY = Q8>
 __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) {
-    constexpr bool LAZY = (VAR & 1) != 0;   // Q8_0: lazy rescaling
-    constexpr bool PF = (VAR & 2) != 0;     // Q8_0: next trip's rows loaded before this trip's math
     static_assert(!Q8 || EPL == 16, "Q8_0 rows are read 16 quants per lane");
     using F = Frag<D, EPL, Q8>;
     constexpr int NTHR = WAVES * 64;
@@ -484,7 +485,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
 #pragma unroll
                 for (int c = 0; c < C4; ++c) vf[u][c] = load4<NT>(vp + c * LPR);
             }
-            accumulate_rows<D, G, EPL, U>(qr, kf, vf, valid, m, l, o, a);
+            accumulate_rows<D, G, EPL, U, LAZY>(qr, kf, vf, valid, m, l, o, a);
         }
     } else {
         const signed char* kqp = a.kq + (long long)kvh * a.head_stride;
@@ -518,31 +519,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             }
             accumulate_rows_q8<D, G, U, LAZY>(qr, kq, r.ksc, vq, r.vsc, r.valid, m, l, o, a);
         };
-        int base = row_begin + wave * ROWS_WAVE;
-        if constexpr (PF) {
-            // Two row buffers in turn: the loads of trip i+1 are in flight during trip i's math.
-            Rows ra, rb;
-            if (base < cache_end) {
-                load_rows(base, ra);
-                while (true) {
-                    base += ROWS_BLOCK;
-                    const bool more_b = base < cache_end;
-                    if (more_b) load_rows(base, rb);
-                    consume(ra);
-                    if (!more_b) break;
-                    base += ROWS_BLOCK;
-                    const bool more_a = base < cache_end;
-                    if (more_a) load_rows(base, ra);
-                    consume(rb);
-                    if (!more_a) break;
-                }
-            }
-        } else {
-            for (; base < cache_end; base += ROWS_BLOCK) {
-                Rows r;
-                load_rows(base, r);
-                consume(r);
-            }
+        for (int base = row_begin + wave * ROWS_WAVE; base < cache_end; base += ROWS_BLOCK) {
+            Rows r;
+            load_rows(base, r);
+            consume(r);
         }
     }
 

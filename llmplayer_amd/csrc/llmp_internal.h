@@ -67,11 +67,16 @@ __host__ __device__ inline StepPlan plan_step(int pos, int window, int max_split
 }
 
 // Launches the split-K kernel for head_dim D and GQA group G = Hq/Hkv on grid
-// (splits, Hkv) with `waves` (4 or 8) waves per workgroup, over an fp32 (q8 = false) or
-// Q8_0 (q8 = true) cache.  Returns hipErrorInvalidValue for an unsupported shape.  With
-// splits > 1, launch_decode_reduce must follow.
+// (splits, Hkv) with `waves` (4 or 8) waves per workgroup requested, over an fp32
+// (q8 = false) or Q8_0 (q8 = true) cache.  Returns hipErrorInvalidValue for an unsupported
+// shape.  With splits > 1, launch_decode_reduce must follow.
 hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads,
                                int waves, bool q8, hipStream_t stream);
+// Waves per workgroup the split kernel actually runs with for a request of `waves` (some
+// shapes only ship 4-wave workgroups); 0 for an unsupported shape.
+int decode_split_waves(int head_dim, int group, int waves, bool q8);
+// Workgroups of that kernel resident per CU at once (registers and LDS), 0 on error.
+int decode_split_blocks_per_cu(int head_dim, int group, int waves, bool q8);
 // Launches the log-sum-exp combine of the splits: one block per query head.
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,
                                 hipStream_t stream);

@@ -196,20 +196,35 @@ int prof_fold(KvHandle* kv, int kind) {
 // per split (below that the per-workgroup prologue and merge dominate) and at most 128 splits
 // per KV head.  Very long splits (>= 1024 rows) run 8-wave workgroups on 3/4 as many splits:
 // fewer concurrent KV streams, each read by more waves, keep HBM closer to its peak.
-void auto_launch(int n, int n_kv_heads, int n_cu, int* splits, int* waves) {
+// Default launch shape of a decode step over n attended rows.
+//  - fp32 cache (tuned on MI355X): about one workgroup per CU (at least 32 rows per split, at
+//    most 128 splits per KV head); 8-wave workgroups at 3/4 of those splits once a split has
+//    1024 rows or more.
+//  - Q8_0 cache: its rows are 3.6x shorter and its math per byte higher, so the kernel is
+//    bound by issue and latency: 4-wave workgroups, as many per CU as stay resident at once
+//    (one full round over the chip, no tail), and at least 160 rows per split so that each
+//    workgroup's fixed prologue and merge stay small next to its streaming (measured on
+//    MI355X at the Llama-3.2-3B shape: 96 splits best at 32k rows, 24 at 4k).
+void auto_launch(int n, int n_kv_heads, int n_cu, int head_dim, int group, bool q8, int* splits,
+                 int* waves) {
     const int cu = n_cu > 0 ? n_cu : 256;
-    int s = (cu + n_kv_heads - 1) / n_kv_heads;
-    const int by_rows = n / 32 > 0 ? n / 32 : 1;
+    const int min_rows = q8 ? 160 : 32;
+    const int by_rows = n / min_rows > 0 ? n / min_rows : 1;
+    int per_cu = 1, w = 4;
+    if (q8) {
+        per_cu = decode_split_blocks_per_cu(head_dim, group, 4, true);
+        if (per_cu < 1) per_cu = 1;
+    }
+    int s = (per_cu * cu + n_kv_heads - 1) / n_kv_heads;
     if (s > by_rows) s = by_rows;
     if (s > 128) s = 128;
     if (s < 1) s = 1;
-    int w = 4;
-    if (n / s >= 1024) {
+    if (!q8 && n / s >= 1024) {
         w = 8;
         s = (3 * s + 3) / 4;
     }
     *splits = s;
-    *waves = w;
+    *waves = decode_split_waves(head_dim, group, w, q8);
 }
 
 struct Plan {
@@ -226,12 +241,16 @@ int layer_window(const LayerCfg& c) { return (c.window > 0 && !c.is_global) ? c.
 
 // Launch plan of one decode call at `position`: splits and workgroup size (auto_launch unless
 // the caller fixed the splits), then the kernels' own step plan (plan_step).
-Plan make_plan(const LayerCfg& c, int position, int splits_req, int n_kv_heads) {
+Plan make_plan(const KvHandle* kv, const LayerCfg& c, int position, int splits_req) {
     const int window = layer_window(c);
     const StepPlan full = plan_step(position, window, 1);
+    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    const bool q8 = kv->q8();
     int s = splits_req, waves = 4;
-    if (s <= 0) auto_launch(full.n, n_kv_heads, G().n_cu, &s, &waves);
-    else if (full.n / s >= 1024) waves = 8;
+    if (s <= 0)
+        auto_launch(full.n, Hkv, G().n_cu, D, group, q8, &s, &waves);
+    else
+        waves = decode_split_waves(D, group, (!q8 && full.n / s >= 1024) ? 8 : 4, q8);
     const StepPlan sp = plan_step(position, window, s);
     return Plan{sp.start, sp.n, sp.splits, sp.rows_per_split, waves};
 }
@@ -255,7 +274,7 @@ int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint
         return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
 
     const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
-    const Plan plan = make_plan(c, position, splits, Hkv);
+    const Plan plan = make_plan(kv, c, position, splits);
     DecodeArgs a{};
     a.q = reinterpret_cast<const float*>(q);
     a.k = reinterpret_cast<const float*>(k);
@@ -855,7 +874,7 @@ int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* 
         return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
     if (splits > kMaxSplits)
         return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
-    const Plan p = make_plan(c, position, splits, kv->n_kv_heads);
+    const Plan p = make_plan(kv, c, position, splits);
     if (out_splits) *out_splits = p.splits;
     if (out_waves) *out_waves = p.waves;
     if (out_rows_per_split) *out_rows_per_split = p.rows_per_split;
