@@ -205,7 +205,10 @@ int llmp_graph_destroy(uint64_t graph);
  * widened to fp32, QK-norm and RoPE in the CPU path's float order).  Token i attends causally
  * to rows [start(pos0+i), pos0+i] (start from the layer's sliding window), on MFMA with bf16
  * hi/lo split operands and fp32 accumulation.  Rows before pos0 must already be in the cache.
- * NEOX partial RoPE (rotated dims < head_dim) is LLMP_ERR_UNSUPPORTED here. */
+ * NEOX partial RoPE (rotated dims < head_dim) and Q8_0 caches are LLMP_ERR_UNSUPPORTED here.
+ * The handle keeps a workspace for the key tiles a call attends (bf16 hi/lo images of K and
+ * V: about 9 bytes per key, KV head and head_dim element); a call that needs more than any
+ * earlier call grows it (hipMalloc, so such a call cannot be captured in a graph). */
 int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                       uint64_t k, uint64_t v, uint64_t out, uint64_t stream);
 
@@ -214,7 +217,7 @@ int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64
 #define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV) */
 #define LLMP_PROF_DECODE_REDUCE  1  /* log-sum-exp combine of the splits                    */
 #define LLMP_PROF_PREFILL_APPEND 2  /* prefill: exact K/V append of the prompt tokens       */
-#define LLMP_PROF_PREFILL_ATTN   3  /* prefill: MFMA causal attention                       */
+#define LLMP_PROF_PREFILL_ATTN   3  /* prefill: key-tile images + MFMA causal attention      */
 #define LLMP_PROF_KINDS          4
 /* on != 0 records a HIP event pair around every launch of the handle's kernels. */
 int llmp_profile_enable(uint64_t handle, int on);

@@ -86,11 +86,18 @@ bool decode_shape_supported(int head_dim, int group);
 namespace pk {
 struct PrefillArgs;
 }
-// Prefill: exact K/V append of all prompt tokens (one workgroup per token), then the MFMA
-// causal attention.  Both return hipErrorInvalidValue for an unsupported shape.
+// Prefill, three launches: exact K/V append of all prompt tokens (one workgroup per token);
+// tile images (the bf16 hi/lo split of key tiles [tile0, tile0 + n_tiles) of every KV head,
+// V transposed) into `ws`; the MFMA causal attention over those images.  All return
+// hipErrorInvalidValue for an unsupported shape.
 hipError_t launch_prefill_append(const pk::PrefillArgs& a, int head_dim, hipStream_t stream);
-hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group,
-                               hipStream_t stream);
+hipError_t launch_prefill_tiles(const pk::PrefillArgs& a, int head_dim, void* ws, int tile0,
+                                int n_tiles, int row_end, hipStream_t stream);
+hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group, const void* ws,
+                               int tile0, int n_tiles, int n_cu, hipStream_t stream);
+// Keys per tile and bytes per tile image (per KV head) for head_dim; 0 if unsupported.
+int prefill_tile_keys(int head_dim);
+size_t prefill_tile_bytes(int head_dim);
 
 // Plain 16-byte-per-thread copy kernel.
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);

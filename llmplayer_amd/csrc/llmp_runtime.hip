@@ -70,6 +70,8 @@ struct KvHandle {
     size_t plane_floats = 0;  // floats of one K or V plane of one layer
     RopeTable rope[2];
     std::vector<LayerCfg> layers;
+    void* prefill_ws = nullptr;   // prefill tile images (grown on demand)
+    size_t prefill_ws_bytes = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
     size_t part_slots = 0;    // (split, query head) slots the workspace holds
@@ -158,6 +160,7 @@ void free_handle(KvHandle* kv) {
     }
     if (kv->part_o) (void)hipFree(kv->part_o);
     if (kv->part_ml) (void)hipFree(kv->part_ml);
+    if (kv->prefill_ws) (void)hipFree(kv->prefill_ws);
     for (auto& v : kv->prof_pending)
         for (auto& p : v) {
             (void)hipEventDestroy(p.begin);
@@ -939,6 +942,27 @@ int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64
         a.qk_scale = scale * log2e;
     }
     hipStream_t st = pick_stream(stream);
+    // Key tiles any query of this call attends: from the first query's window start (or 0) to
+    // the last prompt row.  Their images live in the handle's workspace, grown when a call
+    // needs more (a growth synchronises the device; the size only depends on the row range).
+    const int TK = prefill_tile_keys(D);
+    const int kbeg_min = a.window > 0 ? std::max(0, pos0 - a.window + 1) : 0;
+    const int tile0 = kbeg_min / TK, tile_last = (pos0 + n_tokens - 1) / TK;
+    const int n_tiles = tile_last - tile0 + 1;
+    const size_t ws_bytes = (size_t)Hkv * (size_t)n_tiles * prefill_tile_bytes(D);
+    if (ws_bytes > kv->prefill_ws_bytes) {
+        if (kv->prefill_ws) {
+            LLMP_HIP_CHECK(hipStreamSynchronize(st), "hipStreamSynchronize");
+            (void)hipFree(kv->prefill_ws);
+            kv->prefill_ws = nullptr;
+            kv->prefill_ws_bytes = 0;
+        }
+        hipError_t e = hipMalloc(&kv->prefill_ws, ws_bytes);
+        if (e == hipErrorOutOfMemory)
+            return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_attn_prefill: %zu-byte tile workspace", ws_bytes);
+        LLMP_HIP_CHECK(e, "hipMalloc(prefill workspace)");
+        kv->prefill_ws_bytes = ws_bytes;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr, e3 = nullptr;
     if (kv->prof_on) {
         for (hipEvent_t* e : {&e0, &e1, &e2, &e3})
@@ -951,7 +975,10 @@ int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64
         kv->prof_pending[LLMP_PROF_PREFILL_APPEND].push_back({e0, e1});
         LLMP_HIP_CHECK(hipEventRecord(e2, st), "hipEventRecord");
     }
-    LLMP_HIP_CHECK(launch_prefill_attn(a, D, group, st), "prefill attention launch");
+    LLMP_HIP_CHECK(launch_prefill_tiles(a, D, kv->prefill_ws, tile0, n_tiles, pos0 + n_tokens, st),
+                   "prefill tile launch");
+    LLMP_HIP_CHECK(launch_prefill_attn(a, D, group, kv->prefill_ws, tile0, n_tiles, G().n_cu, st),
+                   "prefill attention launch");
     if (kv->prof_on) {
         LLMP_HIP_CHECK(hipEventRecord(e3, st), "hipEventRecord");
         kv->prof_pending[LLMP_PROF_PREFILL_ATTN].push_back({e2, e3});

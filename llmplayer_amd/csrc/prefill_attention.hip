@@ -5,30 +5,55 @@ namespace llmp {
 namespace {
 
 constexpr int kAppendThreads = 256;
+constexpr int kTileThreads = 256;
 
-// Position sub-blocks of 16 per workgroup: about 8 waves (G heads x NB sub-blocks).
-constexpr int pick_nb(int G) { return G >= 8 ? 1 : (8 / G > 0 ? 8 / G : 1); }
+// Launch shape of the attention kernel: one query head per wave (HPW 1, measured best at the
+// C5 shape: each wave's K/V fragments feed its MFMAs while occupancy stays at 4 waves/SIMD),
+// 16*NB query tokens per workgroup, at most 8 waves.  NB_BIG is used when the grid then still
+// holds two workgroups per CU, else NB_BIG/2 (short prompts).
+constexpr int nb_big(int G) { return G >= 8 ? 1 : (8 / G >= 4 ? 4 : 8 / G); }
 
-template <int D, int G>
-hipError_t launch_attn_dg(const pk::PrefillArgs& a, hipStream_t stream) {
-    constexpr int NB = pick_nb(G);
-    const int blocks = (a.P + 16 * NB - 1) / (16 * NB);
-    hipLaunchKernelGGL((pk::prefill_attn_kernel<D, G, NB>), dim3(blocks, a.Hkv), dim3(G * NB * 64),
-                       0, stream, a);
+template <int D, int G, int NB>
+hipError_t launch_attn_dgn(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
+                           hipStream_t stream) {
+    const int items = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
+    hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, 1>), dim3(items), dim3(G * NB * 64),
+                       0, stream, a, ws, tile0, n_tiles);
     return hipGetLastError();
 }
 
+template <int D, int G>
+hipError_t launch_attn_dg(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
+                          int n_cu, hipStream_t stream) {
+    constexpr int NB = nb_big(G);
+    const int items_big = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
+    if constexpr (NB > 1) {
+        if (items_big < 2 * n_cu)
+            return launch_attn_dgn<D, G, NB / 2>(a, ws, tile0, n_tiles, stream);
+    }
+    return launch_attn_dgn<D, G, NB>(a, ws, tile0, n_tiles, stream);
+}
+
 template <int D>
-hipError_t launch_attn_d(const pk::PrefillArgs& a, int group, hipStream_t stream) {
+hipError_t launch_attn_d(const pk::PrefillArgs& a, int group, const uint4* ws, int tile0,
+                         int n_tiles, int n_cu, hipStream_t stream) {
     switch (group) {
-    case 1: return launch_attn_dg<D, 1>(a, stream);
-    case 2: return launch_attn_dg<D, 2>(a, stream);
-    case 3: return launch_attn_dg<D, 3>(a, stream);
-    case 4: return launch_attn_dg<D, 4>(a, stream);
-    case 6: return launch_attn_dg<D, 6>(a, stream);
-    case 8: return launch_attn_dg<D, 8>(a, stream);
+    case 1: return launch_attn_dg<D, 1>(a, ws, tile0, n_tiles, n_cu, stream);
+    case 2: return launch_attn_dg<D, 2>(a, ws, tile0, n_tiles, n_cu, stream);
+    case 3: return launch_attn_dg<D, 3>(a, ws, tile0, n_tiles, n_cu, stream);
+    case 4: return launch_attn_dg<D, 4>(a, ws, tile0, n_tiles, n_cu, stream);
+    case 6: return launch_attn_dg<D, 6>(a, ws, tile0, n_tiles, n_cu, stream);
+    case 8: return launch_attn_dg<D, 8>(a, ws, tile0, n_tiles, n_cu, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+template <int D>
+hipError_t launch_tiles_d(const pk::PrefillArgs& a, uint4* ws, int tile0, int n_tiles,
+                          int row_end, hipStream_t stream) {
+    hipLaunchKernelGGL((pk::prefill_tile_kernel<D, kTileThreads>), dim3(n_tiles, a.Hkv),
+                       dim3(kTileThreads), 0, stream, a, ws, tile0, n_tiles, row_end);
+    return hipGetLastError();
 }
 
 template <int D>
@@ -50,12 +75,42 @@ hipError_t launch_prefill_append(const pk::PrefillArgs& a, int head_dim, hipStre
     }
 }
 
-hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group,
-                               hipStream_t stream) {
+int prefill_tile_keys(int head_dim) {
     switch (head_dim) {
-    case 64: return launch_attn_d<64>(a, group, stream);
-    case 128: return launch_attn_d<128>(a, group, stream);
-    case 256: return launch_attn_d<256>(a, group, stream);
+    case 64: return pk::TileLds<64>::TK;
+    case 128: return pk::TileLds<128>::TK;
+    case 256: return pk::TileLds<256>::TK;
+    default: return 0;
+    }
+}
+
+size_t prefill_tile_bytes(int head_dim) {
+    switch (head_dim) {
+    case 64: return sizeof(pk::TileLds<64>);
+    case 128: return sizeof(pk::TileLds<128>);
+    case 256: return sizeof(pk::TileLds<256>);
+    default: return 0;
+    }
+}
+
+hipError_t launch_prefill_tiles(const pk::PrefillArgs& a, int head_dim, void* ws, int tile0,
+                                int n_tiles, int row_end, hipStream_t stream) {
+    uint4* w = static_cast<uint4*>(ws);
+    switch (head_dim) {
+    case 64: return launch_tiles_d<64>(a, w, tile0, n_tiles, row_end, stream);
+    case 128: return launch_tiles_d<128>(a, w, tile0, n_tiles, row_end, stream);
+    case 256: return launch_tiles_d<256>(a, w, tile0, n_tiles, row_end, stream);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group, const void* ws,
+                               int tile0, int n_tiles, int n_cu, hipStream_t stream) {
+    const uint4* w = static_cast<const uint4*>(ws);
+    switch (head_dim) {
+    case 64: return launch_attn_d<64>(a, group, w, tile0, n_tiles, n_cu, stream);
+    case 128: return launch_attn_d<128>(a, group, w, tile0, n_tiles, n_cu, stream);
+    case 256: return launch_attn_d<256>(a, group, w, tile0, n_tiles, n_cu, stream);
     default: return hipErrorInvalidValue;
     }
 }

@@ -3,16 +3,20 @@
 // The reference has no batched prefill: the prompt runs as P sequential single-token forwards
 // (LLMEngine.java:478-480, InferenceEngine.prefill at InferenceEngine.java:374-381), so query i
 // attends to rows [start(i), pos0+i] of a cache that already holds rows < pos0+i.  This path
-// computes the same result in two launches:
+// computes the same result in three launches:
 //
 //  1. prefill_append_kernel: one workgroup per token widens its bf16 k/v to fp32, applies the
 //     exact QK-norm + RoPE of the decode path and writes the K/V rows (bit-identical to P
 //     appends by the CPU path).
-//  2. prefill_attn_kernel: causal flash attention on MFMA.  A workgroup owns one KV head and
+//  2. prefill_tile_kernel: once per (key tile, KV head), the bf16 hi/lo split of the tile's K
+//     rows and of its V rows (transposed) into a workspace image laid out like the LDS tile.
+//  3. prefill_attn2_kernel: causal flash attention on MFMA.  A workgroup owns one KV head and
 //     16*NB query positions of all G query heads of that KV head; each wave owns 16 positions
-//     of one query head.  Per 64-key tile (staged in LDS as bf16 hi/lo, V transposed) a wave
-//     computes S^T = K Q^T and O^T += V^T P^T with v_mfma_f32_16x16x32_bf16 and an online
-//     softmax in the accumulator layout.
+//     of HPW query heads.  Tile images stream into two LDS buffers (tile i+2 is fetched into
+//     registers while tile i is consumed); per 64-key tile a wave computes S^T = K Q^T and
+//     O^T += V^T P^T with v_mfma_f32_16x16x32_bf16 and an online softmax in the accumulator
+//     layout.  Workgroups are ranked by key count and dispatched heaviest-first in the first
+//     half of the grid, lightest-first in the second, so co-resident workgroups balance.
 //
 // Precision: Q and K are post-RoPE fp32 (not bf16), so each operand is split into
 // hi = bf16(x) and lo = bf16(x - hi), and a product uses three MFMAs (hi*hi + hi*lo + lo*hi):
@@ -66,18 +70,6 @@ struct PrefillArgs {
 __device__ __forceinline__ float bf16_to_f32(unsigned short b) {
     return __uint_as_float((unsigned)b << 16);
 }
-// Round-to-nearest-even fp32 -> bf16 (finite inputs).
-__device__ __forceinline__ unsigned short f32_to_bf16(float f) {
-    unsigned u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (unsigned short)(u >> 16);
-}
-// x = hi + lo with hi, lo bf16 (x - hi is exact in fp32).
-__device__ __forceinline__ void split_bf16(float x, unsigned short& hi, unsigned short& lo) {
-    hi = f32_to_bf16(x);
-    lo = f32_to_bf16(x - bf16_to_f32(hi));
-}
-
 // ---- 1. exact K/V append, one workgroup per token --------------------------------------------
 template <int D, int NTHR>
 __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
@@ -104,10 +96,10 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
     }
 }
 
-// ---- 2. MFMA flash attention -------------------------------------------------------------------
+// ---- LDS tile layout (also the workspace image of a tile) -------------------------------------
 // LDS tile: K hi/lo [TK keys][D + 8] bf16 (row padding spreads banks), V^T hi/lo [D][TK + 8].
 template <int D>
-struct TileLds {
+struct alignas(16) TileLds {
     static constexpr int TK = tile_keys<D>();
     static constexpr int KP = D + 8;   // K row pitch (bf16 elements; 16-byte multiple)
     static constexpr int VP = TK + 8;  // V^T row pitch (8-byte multiple)
@@ -117,225 +109,365 @@ struct TileLds {
     unsigned short vl[D * VP];
 };
 
-template <int D, int G, int NB>
-__global__ __launch_bounds__(G * NB * 64) void prefill_attn_kernel(PrefillArgs a) {
-    constexpr int NTHR = G * NB * 64;
-    constexpr int KS = D / 32;   // MFMA k-steps over the head dimension
-    constexpr int DT = D / 16;   // 16-dim output tiles
-    constexpr int TK = TileLds<D>::TK;
-    constexpr int NKT = TK / 16;  // 16-key sub-tiles per tile
-    constexpr int NC = TK / 32;   // 32-key MFMA steps of P V per tile
-    __shared__ TileLds<D> t;
+// ---- 2. Tile images ----------------------------------------------------------------------------
+// The bf16 hi/lo split of a key tile does not depend on the query block, so it is done once per
+// (tile, KV head) into a workspace image laid out exactly like TileLds.
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ unsigned pack_bf16(float x, float y) {
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{x, y}, bf16x2));
+}
+// Split of two values: hi = bf16(x), lo = bf16(x - hi), packed in pairs.
+__device__ __forceinline__ void split_pair(float x, float y, unsigned& hi, unsigned& lo) {
+    hi = pack_bf16(x, y);
+    const float hx = __uint_as_float(hi << 16), hy = __uint_as_float(hi & 0xFFFF0000u);
+    lo = pack_bf16(x - hx, y - hy);
+}
+
+template <int D>
+constexpr int tile_img_u4() { return (int)(sizeof(TileLds<D>) / 16); }
+
+// Image of keys [tau*TK, tau*TK + TK) of KV head blockIdx.y, tau = tile0 + blockIdx.x, at
+// ws[(kvh * n_tiles + blockIdx.x) * tile_img_u4<D>()].  Rows at or past row_end (never attended)
+// repeat row row_end - 1 so that every staged value is finite.
+template <int D, int NTHR>
+__global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4* ws, int tile0,
+                                                            int n_tiles, int row_end) {
+    using T = TileLds<D>;
+    constexpr int TK = T::TK;
+    __shared__ T t;
+    const int tid = threadIdx.x, kvh = blockIdx.y;
+    const int r0 = (tile0 + (int)blockIdx.x) * TK;
+    const float* kplane = a.kc + (long long)kvh * a.head_stride;
+    const float* vplane = a.vc + (long long)kvh * a.head_stride;
+    // Thread work item: rows r, r+1 and dims 4*c4 .. 4*c4+3.
+    for (int e = tid; e < (TK / 2) * (D / 4); e += NTHR) {
+        const int rp = e / (D / 4), c4 = e - rp * (D / 4);
+        const int r = 2 * rp;
+        const int row0 = min(r0 + r, row_end - 1), row1 = min(r0 + r + 1, row_end - 1);
+        const float4 k0 = reinterpret_cast<const float4*>(kplane + (long long)row0 * D)[c4];
+        const float4 k1 = reinterpret_cast<const float4*>(kplane + (long long)row1 * D)[c4];
+        const float4 v0 = reinterpret_cast<const float4*>(vplane + (long long)row0 * D)[c4];
+        const float4 v1 = reinterpret_cast<const float4*>(vplane + (long long)row1 * D)[c4];
+        unsigned h0, l0, h1, l1;
+        // K rows (row-major): dims (4c4, 4c4+1) and (4c4+2, 4c4+3) of rows r and r+1.
+        split_pair(k0.x, k0.y, h0, l0);
+        split_pair(k0.z, k0.w, h1, l1);
+        *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
+        split_pair(k1.x, k1.y, h0, l0);
+        split_pair(k1.z, k1.w, h1, l1);
+        *reinterpret_cast<uint2*>(&t.kh[(r + 1) * T::KP + 4 * c4]) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(&t.kl[(r + 1) * T::KP + 4 * c4]) = make_uint2(l0, l1);
+        // V^T: for each of the 4 dims, the pair of rows (r, r+1).
+        const float va[4] = {v0.x, v0.y, v0.z, v0.w}, vb[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            split_pair(va[u], vb[u], h0, l0);
+            const int d = 4 * c4 + u;
+            *reinterpret_cast<unsigned*>(&t.vh[d * T::VP + r]) = h0;
+            *reinterpret_cast<unsigned*>(&t.vl[d * T::VP + r]) = l0;
+        }
+    }
+    __syncthreads();
+    const uint4* src = reinterpret_cast<const uint4*>(&t);
+    uint4* dst = ws + ((size_t)kvh * n_tiles + blockIdx.x) * tile_img_u4<D>();
+    for (int i = tid; i < tile_img_u4<D>(); i += NTHR) dst[i] = src[i];
+}
+
+// ---- 3. Double-buffered MFMA attention ------------------------------------------------------
+// Query fragment of one lane for MFMA B operands: dims 32*s + 8*grp + j of query token qi
+// (clamped into range), head hq, widened from bf16, QK-normed, rotated, scaled, then split.
+template <int D>
+__device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int hq, int qpos,
+                                               int grp, bf16x8 (&qh)[D / 32],
+                                               bf16x8 (&ql)[D / 32]) {
+    constexpr int KS = D / 32;
+    float qf[KS][8];
+    const unsigned short* qp = a.q + (long long)qi * a.Hq * D + (long long)hq * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qf[s][j] = bf16_to_f32(qp[32 * s + 8 * grp + j]);
+    if (a.qnw != nullptr) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(qf[s][j], qf[s][j], ss);
+        ss = ss + __shfl_xor(ss, 16);
+        ss = ss + __shfl_xor(ss, 32);
+        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qf[s][j] = (qf[s][j] * r) * a.qnw[32 * s + 8 * grp + j];
+    }
+    if (a.cos_t != nullptr) {
+        const float* cr = a.cos_t + (long long)qpos * a.half_rope;
+        const float* sr = a.sin_t + (long long)qpos * a.half_rope;
+        if (a.rope_type == 0) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const int i = (32 * s + 8 * grp + j) / 2;
+                    const bool rot = i < a.half_rope;
+                    const float c = cr[rot ? i : 0], sn = sr[rot ? i : 0];
+                    const float v0 = qf[s][j], v1 = qf[s][j + 1];
+                    const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
+                    qf[s][j] = rot ? t0 - t1 : v0;
+                    qf[s][j + 1] = rot ? t2 + t3 : v1;
+                }
+        } else {  // NEOX with half_rope == D/2: partner dims sit KS/2 k-steps apart
+#pragma unroll
+            for (int s = 0; s < KS / 2; ++s)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int i = 32 * s + 8 * grp + j;
+                    const float c = cr[i], sn = sr[i];
+                    const float v0 = qf[s][j], v1 = qf[s + KS / 2][j];
+                    const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
+                    qf[s][j] = t0 - t1;
+                    qf[s + KS / 2][j] = t2 + t3;
+                }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        unsigned hh[4], ll[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            split_pair(qf[s][2 * j] * a.qk_scale, qf[s][2 * j + 1] * a.qk_scale, hh[j], ll[j]);
+        qh[s] = __builtin_bit_cast(bf16x8, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+        ql[s] = __builtin_bit_cast(bf16x8, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+    }
+}
+
+// Copies of a tile image between global memory, registers and LDS: thread tid moves 16-byte
+// chunks tid, tid + NTHR, ...
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+template <int PER, int NTHR, int IMG>
+__device__ __forceinline__ void img_load(u32x4 (&stage)[PER], const uint4* src, int tid) {
+    const u32x4* s = reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int idx = tid + r * NTHR;
+        stage[r] = s[idx < IMG ? idx : IMG - 1];   // chunks past the image: a valid duplicate
+    }
+}
+template <int PER, int NTHR, int IMG>
+__device__ __forceinline__ void img_store(const u32x4 (&stage)[PER], void* dst, int tid) {
+    u32x4* d = static_cast<u32x4*>(dst);
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int idx = tid + r * NTHR;
+        if (r + 1 < PER || idx < IMG) d[idx] = stage[r];
+    }
+}
+
+// Workgroup: KV head blockIdx.y, query tokens [i0, i0 + 16*NB) of its G query heads.  Wave:
+// 16 tokens (sub-block sb) x HPW query heads (head group hg), so each K/V fragment read from
+// LDS feeds HPW heads' MFMAs.  Tiles [tile0, tile0 + n_tiles) of the layer are in `ws`.
+template <int D, int G, int NB, int HPW, int ORDER = 0>
+__global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(PrefillArgs a,
+                                                                            const uint4* ws,
+                                                                            int tile0, int n_tiles) {
+    using T = TileLds<D>;
+    constexpr int HG = G / HPW;
+    constexpr int NTHR = HG * NB * 64;
+    constexpr int KS = D / 32, DT = D / 16, TK = T::TK, NKT = TK / 16, NC = TK / 32;
+    constexpr int IMG = tile_img_u4<D>();
+    constexpr int PER = (IMG + NTHR - 1) / NTHR;
+    static_assert(G % HPW == 0, "heads per wave must divide the group");
+    __shared__ T buf[2];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int col = lane & 15, grp = lane >> 4;     // query column, lane group (k / row quad)
-    const int kvh = blockIdx.y;
-    // Heavy (late) query blocks first: the causal key range grows with the block index.
-    const int nblk = gridDim.x;
-    const int blk = nblk - 1 - (int)blockIdx.x;
-    const int i0 = blk * 16 * NB;                    // first token of the block
-    const int sb = wave / G, h = wave - sb * G;      // sub-block, query head within the group
-    const int hq = kvh * G + h;
-    const int qi = i0 + 16 * sb + col;               // token index of this lane's query
+    const int col = lane & 15, grp = lane >> 4;
+    const int nblk = (a.P + 16 * NB - 1) / (16 * NB);
+    int kvh, blk;
+    if constexpr (ORDER == 0) {
+        kvh = blockIdx.y;
+        blk = nblk - 1 - (int)blockIdx.x;            // heavy (late) query blocks first
+    } else {
+        // 1-D grid of nblk*Hkv items ranked by key count (rank r: block nblk-1-r/Hkv, head
+        // r%Hkv).  The first half of the grid takes ranks heaviest-first, the second half
+        // lightest-first, so the two workgroups a CU holds at once carry about equal total work.
+        const int n = nblk * a.Hkv, L = (int)blockIdx.x, half = (n + 1) / 2;
+        const int r = L < half ? L : n - 1 - (L - half);
+        kvh = r % a.Hkv;
+        blk = nblk - 1 - r / a.Hkv;
+    }
+    const int i0 = blk * 16 * NB;
+    const int sb = wave / HG, hg = wave - sb * HG;
+    const int qi = i0 + 16 * sb + col;
     const bool q_ok = qi < a.P;
     const int qpos = a.pos0 + (q_ok ? qi : a.P - 1);
     const int qstart = a.window > 0 ? max(0, qpos - a.window + 1) : 0;
 
-    // Query fragment: dims 32*s + 8*grp + j of token qi, head hq, fp32 -> norm -> RoPE -> scale.
-    float qf[KS][8];
-    {
-        const unsigned short* qp = a.q + (long long)(q_ok ? qi : a.P - 1) * a.Hq * D + (long long)hq * D;
+    bf16x8 qh[HPW][KS], ql[HPW][KS];
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qf[s][j] = bf16_to_f32(qp[32 * s + 8 * grp + j]);
-        if (a.qnw != nullptr) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(qf[s][j], qf[s][j], ss);
-            ss = ss + __shfl_xor(ss, 16);
-            ss = ss + __shfl_xor(ss, 32);
-            const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
-#pragma unroll
-            for (int s = 0; s < KS; ++s)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qf[s][j] = (qf[s][j] * r) * a.qnw[32 * s + 8 * grp + j];
-        }
-        if (a.cos_t != nullptr) {
-            const float* cr = a.cos_t + (long long)qpos * a.half_rope;
-            const float* sr = a.sin_t + (long long)qpos * a.half_rope;
-            if (a.rope_type == 0) {
-#pragma unroll
-                for (int s = 0; s < KS; ++s)
-#pragma unroll
-                    for (int j = 0; j < 8; j += 2) {
-                        const int i = (32 * s + 8 * grp + j) / 2;
-                        const bool rot = i < a.half_rope;
-                        const float c = cr[rot ? i : 0], sn = sr[rot ? i : 0];
-                        const float v0 = qf[s][j], v1 = qf[s][j + 1];
-                        const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
-                        qf[s][j] = rot ? t0 - t1 : v0;
-                        qf[s][j + 1] = rot ? t2 + t3 : v1;
-                    }
-            } else {  // NEOX with half_rope == D/2: partner dims sit KS/2 k-steps apart
-#pragma unroll
-                for (int s = 0; s < KS / 2; ++s)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int i = 32 * s + 8 * grp + j;
-                        const float c = cr[i], sn = sr[i];
-                        const float v0 = qf[s][j], v1 = qf[s + KS / 2][j];
-                        const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
-                        qf[s][j] = t0 - t1;
-                        qf[s + KS / 2][j] = t2 + t3;
-                    }
-            }
-        }
-    }
-    bf16x8 qh[KS], ql[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-        short8 hh, ll;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            unsigned short hi, lo;
-            split_bf16(qf[s][j] * a.qk_scale, hi, lo);
-            hh[j] = (short)hi;
-            ll[j] = (short)lo;
-        }
-        qh[s] = __builtin_bit_cast(bf16x8, hh);
-        ql[s] = __builtin_bit_cast(bf16x8, ll);
-    }
+    for (int hh = 0; hh < HPW; ++hh)
+        query_fragment<D>(a, q_ok ? qi : a.P - 1, kvh * G + hg * HPW + hh, qpos, grp, qh[hh], ql[hh]);
 
-    // Key range of the workgroup: up to its last query, from its first query's window start.
+    // Key range of the workgroup and of this wave's 16 queries.
     const int last_tok = min(i0 + 16 * NB, a.P) - 1;
     const int kend = a.pos0 + last_tok + 1;
-    const int kbeg = a.window > 0 ? max(0, a.pos0 + i0 - a.window + 1) & ~15 : 0;
-    const float* kplane = a.kc + (long long)kvh * a.head_stride;
-    const float* vplane = a.vc + (long long)kvh * a.head_stride;
+    const int kbeg = a.window > 0 ? max(0, a.pos0 + i0 - a.window + 1) : 0;
+    const int t_first = kbeg / TK, t_last = (kend - 1) / TK;
+    const int w_lo = a.pos0 + i0 + 16 * sb;           // first query position of the wave
+    const bool w_full = i0 + 16 * sb + 15 < a.P;
+    const int w_start_max = a.window > 0 ? max(0, w_lo + 15 - a.window + 1) : 0;
 
-    floatx4 o[DT];
+    const uint4* img = ws + (size_t)kvh * n_tiles * IMG;
+    u32x4 stage[PER];
+    floatx4 o[HPW][DT];
+    float m[HPW], l[HPW];
 #pragma unroll
-    for (int d = 0; d < DT; ++d) o[d] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m = kNegBig, l = 0.0f;
-
-    for (int t0 = kbeg; t0 < kend; t0 += TK) {
-        // Stage the tile: fp32 rows -> bf16 hi/lo; K row-major, V transposed.  Rows past kend
-        // (never attended) are clamped to a valid row.
-        __syncthreads();
-        for (int e = tid; e < TK * D / 4; e += NTHR) {
-            const int r = e / (D / 4), c4 = e - r * (D / 4);
-            const int row = min(t0 + r, kend - 1);
-            const float4 kx = reinterpret_cast<const float4*>(kplane + (long long)row * D)[c4];
-            const float4 vx = reinterpret_cast<const float4*>(vplane + (long long)row * D)[c4];
-            const float kk[4] = {kx.x, kx.y, kx.z, kx.w};
-            const float vv[4] = {vx.x, vx.y, vx.z, vx.w};
+    for (int hh = 0; hh < HPW; ++hh) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int d = 4 * c4 + u;
-                unsigned short hi, lo;
-                split_bf16(kk[u], hi, lo);
-                t.kh[r * TileLds<D>::KP + d] = hi;
-                t.kl[r * TileLds<D>::KP + d] = lo;
-                split_bf16(vv[u], hi, lo);
-                t.vh[d * TileLds<D>::VP + r] = hi;
-                t.vl[d * TileLds<D>::VP + r] = lo;
-            }
-        }
-        __syncthreads();
+        for (int d = 0; d < DT; ++d) o[hh][d] = floatx4{0.f, 0.f, 0.f, 0.f};
+        m[hh] = kNegBig;
+        l[hh] = 0.0f;
+    }
 
-        // S^T = K Q^T for the 16-key sub-tiles: lane holds keys 4*grp+j of sub-tile kt.
-        floatx4 st[NKT];
+    img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
+    img_store<PER, NTHR, IMG>(stage, &buf[0], tid);
+    if (t_first + 1 <= t_last)
+        img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first + 1 - tile0) * IMG, tid);
+    __syncthreads();
+    for (int tile = t_first; tile <= t_last; ++tile) {
+        const T& t = buf[(tile - t_first) & 1];
+        const int t0 = tile * TK;
+        // S^T = K Q^T per 16-key sub-tile: lane holds keys 4*grp + j of sub-tile kt.
+        floatx4 st[HPW][NKT];
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt) {
-            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+            floatx4 acc[HPW];
+#pragma unroll
+            for (int hh = 0; hh < HPW; ++hh) acc[hh] = floatx4{0.f, 0.f, 0.f, 0.f};
             const int krow = kt * 16 + col;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                const bf16x8 kh = *reinterpret_cast<const bf16x8*>(
-                    &t.kh[krow * TileLds<D>::KP + 32 * s + 8 * grp]);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8*>(
-                    &t.kl[krow * TileLds<D>::KP + 32 * s + 8 * grp]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[s], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[s], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[s], acc, 0, 0, 0);
+                const bf16x8 kh = *reinterpret_cast<const bf16x8*>(&t.kh[krow * T::KP + 32 * s + 8 * grp]);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8*>(&t.kl[krow * T::KP + 32 * s + 8 * grp]);
+#pragma unroll
+                for (int hh = 0; hh < HPW; ++hh) {
+                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[hh][s], acc[hh], 0, 0, 0);
+                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[hh][s], acc[hh], 0, 0, 0);
+                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[hh][s], acc[hh], 0, 0, 0);
+                }
             }
-            st[kt] = acc;
+#pragma unroll
+            for (int hh = 0; hh < HPW; ++hh) st[hh][kt] = acc[hh];
         }
-        // Mask (causal, window, past kend), soft-cap, tile max.
-        float mt = kNegBig;
+        // Soft-cap; causal/window/range mask only on tiles that cross a boundary of this wave.
+        if (a.softcap > 0.0f) {
 #pragma unroll
-        for (int kt = 0; kt < NKT; ++kt)
+            for (int hh = 0; hh < HPW; ++hh)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int key = t0 + kt * 16 + 4 * grp + j;
-                float sv = st[kt][j];
-                if (a.softcap > 0.0f) sv = a.softcap_log2e * tanhf(sv * a.inv_softcap);
-                const bool ok = q_ok && key <= qpos && key >= qstart && key < kend;
-                sv = ok ? sv : -__builtin_inff();
-                st[kt][j] = sv;
-                mt = fmaxf(mt, sv);
-            }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float mn = fmaxf(m, mt);
-        const float alpha = dk::fast_exp2(m - mn);
-        m = mn;
-        l = l * alpha;
+                for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int d = 0; d < DT; ++d) o[d] = o[d] * alpha;
-        // P = exp2(S - m), split for the B operand in the key order described above.
-        bf16x8 ph[NC], pl[NC];
+                    for (int j = 0; j < 4; ++j)
+                        st[hh][kt][j] = a.softcap_log2e * tanhf(st[hh][kt][j] * a.inv_softcap);
+        }
+        const bool interior = w_full && t0 + TK - 1 <= w_lo && t0 >= w_start_max;
+        if (!interior) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            short8 hh, ll;
-#pragma unroll
-            for (int half = 0; half < 2; ++half)
+            for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float p = dk::fast_exp2(st[2 * c + half][j] - mn);
-                    l = l + p;
-                    unsigned short hi, lo;
-                    split_bf16(p, hi, lo);
-                    hh[4 * half + j] = (short)hi;
-                    ll[4 * half + j] = (short)lo;
+                    const int key = t0 + kt * 16 + 4 * grp + j;
+                    const bool ok = q_ok && key <= qpos && key >= qstart && key < kend;
+#pragma unroll
+                    for (int hh = 0; hh < HPW; ++hh)
+                        st[hh][kt][j] = ok ? st[hh][kt][j] : -__builtin_inff();
                 }
-            ph[c] = __builtin_bit_cast(bf16x8, hh);
-            pl[c] = __builtin_bit_cast(bf16x8, ll);
         }
-        // O^T += V^T P^T: A operand = V^T rows (dims), keys {32c+4grp..+3, 32c+16+4grp..+3}.
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            const int dim = d * 16 + col;
+        for (int hh = 0; hh < HPW; ++hh) {
+            float mt = kNegBig;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const int k0 = 32 * c + 4 * grp;   // 4 keys (8 bytes) at k0 and at k0 + 16
-                const unsigned short* vhr = &t.vh[dim * TileLds<D>::VP + k0];
-                const unsigned short* vlr = &t.vl[dim * TileLds<D>::VP + k0];
-                const uint2 h0 = *reinterpret_cast<const uint2*>(vhr);
-                const uint2 h1 = *reinterpret_cast<const uint2*>(vhr + 16);
-                const uint2 l0 = *reinterpret_cast<const uint2*>(vlr);
-                const uint2 l1 = *reinterpret_cast<const uint2*>(vlr + 16);
-                const bf16x8 vh = __builtin_bit_cast(bf16x8, make_uint4(h0.x, h0.y, h1.x, h1.y));
-                const bf16x8 vl = __builtin_bit_cast(bf16x8, make_uint4(l0.x, l0.y, l1.x, l1.y));
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[c], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[c], o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[c], o[d], 0, 0, 0);
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) mt = fmaxf(mt, st[hh][kt][j]);
+            mt = fmaxf(mt, __shfl_xor(mt, 16));
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float mn = fmaxf(m[hh], mt);
+            const float alpha = dk::fast_exp2(m[hh] - mn);
+            m[hh] = mn;
+            l[hh] = l[hh] * alpha;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) o[hh][d] = o[hh][d] * alpha;
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float p = dk::fast_exp2(st[hh][kt][j] - mn);
+                    l[hh] = l[hh] + p;
+                    st[hh][kt][j] = p;
+                }
+        }
+        // O^T += V^T P^T: B operand = P in the key order {32c+4grp..+3, 32c+16+4grp..+3}.
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            bf16x8 ph[HPW], pl[HPW];
+#pragma unroll
+            for (int hh = 0; hh < HPW; ++hh) {
+                unsigned h0, l0, h1, l1, h2, l2, h3, l3;
+                split_pair(st[hh][2 * c][0], st[hh][2 * c][1], h0, l0);
+                split_pair(st[hh][2 * c][2], st[hh][2 * c][3], h1, l1);
+                split_pair(st[hh][2 * c + 1][0], st[hh][2 * c + 1][1], h2, l2);
+                split_pair(st[hh][2 * c + 1][2], st[hh][2 * c + 1][3], h3, l3);
+                ph[hh] = __builtin_bit_cast(bf16x8, make_uint4(h0, h1, h2, h3));
+                pl[hh] = __builtin_bit_cast(bf16x8, make_uint4(l0, l1, l2, l3));
+            }
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                const int dim = d * 16 + col;
+                const int k0 = 32 * c + 4 * grp;
+                const unsigned short* vhr = &t.vh[dim * T::VP + k0];
+                const unsigned short* vlr = &t.vl[dim * T::VP + k0];
+                const uint2 a0 = *reinterpret_cast<const uint2*>(vhr);
+                const uint2 a1 = *reinterpret_cast<const uint2*>(vhr + 16);
+                const uint2 b0 = *reinterpret_cast<const uint2*>(vlr);
+                const uint2 b1 = *reinterpret_cast<const uint2*>(vlr + 16);
+                const bf16x8 vh = __builtin_bit_cast(bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y));
+                const bf16x8 vl = __builtin_bit_cast(bf16x8, make_uint4(b0.x, b0.y, b1.x, b1.y));
+#pragma unroll
+                for (int hh = 0; hh < HPW; ++hh) {
+                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[hh], o[hh][d], 0, 0, 0);
+                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[hh], o[hh][d], 0, 0, 0);
+                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[hh], o[hh][d], 0, 0, 0);
+                }
             }
         }
+        // Next buffer: tile+1 (already in registers) to LDS, tile+2 loads in flight.  The
+        // buffer written here was last read before the previous iteration's barrier.
+        if (tile + 1 <= t_last) {
+            img_store<PER, NTHR, IMG>(stage, &buf[(tile + 1 - t_first) & 1], tid);
+            if (tile + 2 <= t_last)
+                img_load<PER, NTHR, IMG>(stage, img + (size_t)(tile + 2 - tile0) * IMG, tid);
+        }
+        __syncthreads();
     }
-    // Row sums live in 4 lane groups; o[d] lane holds dims d*16 + 4*grp + j of query col.
-    l = l + __shfl_xor(l, 16);
-    l = l + __shfl_xor(l, 32);
-    if (q_ok) {
-        const float inv = 1.0f / l;
-        float* op = a.out + (long long)qi * a.Hq * D + (long long)hq * D;
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            float4 r = make_float4(o[d][0] * inv, o[d][1] * inv, o[d][2] * inv, o[d][3] * inv);
-            reinterpret_cast<float4*>(op + d * 16 + 4 * grp)[0] = r;
+    for (int hh = 0; hh < HPW; ++hh) {
+        float lt = l[hh] + __shfl_xor(l[hh], 16);
+        lt = lt + __shfl_xor(lt, 32);
+        if (q_ok) {
+            const float inv = 1.0f / lt;
+            float* op = a.out + (long long)qi * a.Hq * D + (long long)(kvh * G + hg * HPW + hh) * D;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                const float4 r = make_float4(o[hh][d][0] * inv, o[hh][d][1] * inv,
+                                             o[hh][d][2] * inv, o[hh][d][3] * inv);
+                reinterpret_cast<float4*>(op + d * 16 + 4 * grp)[0] = r;
+            }
         }
     }
 }
