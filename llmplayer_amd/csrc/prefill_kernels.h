@@ -97,12 +97,15 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
 }
 
 // ---- LDS tile layout (also the workspace image of a tile) -------------------------------------
-// LDS tile: K hi/lo [TK keys][D + 8] bf16 (row padding spreads banks), V^T hi/lo [D][TK + 8].
+// LDS tile: K hi/lo [TK keys][D + 8] bf16, V^T hi/lo [D][TK + 4] (row padding spreads banks).
 template <int D>
 struct alignas(16) TileLds {
     static constexpr int TK = tile_keys<D>();
     static constexpr int KP = D + 8;   // K row pitch (bf16 elements; 16-byte multiple)
-    static constexpr int VP = TK + 8;  // V^T row pitch (8-byte multiple)
+    // V^T row pitch: 8-byte multiple with an odd number of 8-byte units beyond a 32-dword
+    // multiple (TK + 4 bf16 = 2*(TK/2 + 2) dwords), so the 16 dims of a lane row-group's 8-byte
+    // reads fall on 16 distinct bank pairs.
+    static constexpr int VP = TK + 4;
     unsigned short kh[TK * KP];
     unsigned short kl[TK * KP];
     unsigned short vh[D * VP];
