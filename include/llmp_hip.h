@@ -152,6 +152,13 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
                       int rope_type, int rope_sel, int window, int is_global, float scale,
                       float softcap, float eps, const float *qnorm_w, const float *knorm_w);
 
+/* Attention sinks of a layer (GPT-OSS, Qwen3MoEInferenceEngine.java:88-95, 295, 309-313):
+ * sinks[n_heads] host fp32 logits in the units of the scaled scores.  Each one joins its
+ * query head's softmax max and denominator and takes no value (softmaxWithSink,
+ * Qwen3MoEInferenceEngine.java:562-575); decode and prefill apply them.  NULL removes them; a
+ * later llmp_layer_config with another head count removes them too.  May allocate. */
+int llmp_layer_sinks(uint64_t handle, int layer, const float *sinks);
+
 /* ---- decode attention: one layer-call for one new token --------------------------------
  * Replaces CudaForwardPass.forwardAttentionPart steps 2b'-5 (CudaForwardPass.java:1529-1570):
  * rmsnorm_per_head (Q, K) -> rope_apply (Q, K) -> kv_cache_update -> attention_full, with the
@@ -177,6 +184,15 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
  * position outside [0, max_seq) makes the call a no-op (nothing is read or written). */
 int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uint64_t q,
                             uint64_t k, uint64_t v, uint64_t out, int splits, uint64_t stream);
+
+/* llmp_attn_decode (d_position == 0) or llmp_attn_decode_devpos (d_position != 0, `position`
+ * unused) with an optional output gate: gate, when non-zero, is a device fp32 [n_heads *
+ * head_dim] array and out = attention * sigmoid(gate), sigmoid(x) = 1/(1 + exp(-x)) (the
+ * Qwen3.5 attention output gate, Qwen35InferenceEngine.java:580-583, 628-630; on the reference
+ * GPU a separate sigmoid-multiply launch, Qwen35CudaForwardPass.java:1136-1137). */
+int llmp_attn_decode_ex(uint64_t handle, int layer, int position, uint64_t d_position,
+                        uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
+                        int splits, uint64_t stream);
 
 /* Launch plan llmp_attn_decode would use for this call: splits per KV head, waves per
  * workgroup (4 or 8), rows per split and the first attended position.  Any out may be NULL. */
@@ -211,6 +227,10 @@ int llmp_graph_destroy(uint64_t graph);
  * earlier call grows it (hipMalloc, so such a call cannot be captured in a graph). */
 int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                       uint64_t k, uint64_t v, uint64_t out, uint64_t stream);
+/* llmp_attn_prefill with an optional output gate (device fp32 [n_tokens][n_heads*head_dim],
+ * 0 = none): out = attention * sigmoid(gate), as llmp_attn_decode_ex applies it. */
+int llmp_attn_prefill_ex(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
+                         uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);
 
 /* ---- profiling (the reference's -Dcuda.profile section timers,
  *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */

@@ -65,7 +65,10 @@ SIGNATURES = {
                           _f32, _pf, _pf],
     "llmp_attn_decode": [_u64, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
     "llmp_attn_decode_devpos": [_u64, _i32, _u64, _u64, _u64, _u64, _u64, _i32, _u64],
+    "llmp_attn_decode_ex": [_u64, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64, _i32, _u64],
+    "llmp_layer_sinks": [_u64, _i32, _pf],
     "llmp_attn_prefill": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64],
+    "llmp_attn_prefill_ex": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64],
     "llmp_decode_plan": [_u64, _i32, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32),
                          C.POINTER(_i32), C.POINTER(_i32)],
     "llmp_graph_begin": [_u64],

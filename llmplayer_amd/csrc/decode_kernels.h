@@ -40,6 +40,7 @@ constexpr float kNegBig = -1.0e30f;
 // rescale multiplies are skipped on most trips.  O/L is unchanged: both use the same max.
 constexpr float kLazyMargin = 8.0f;
 
+
 // DPP controls (CDNA3/CDNA4 ISA): quad_perm, row_half_mirror, row_mirror.
 constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
@@ -65,6 +66,27 @@ __device__ __forceinline__ float row_group_sum(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Final normalisation of one output element of query head hq from its merged (max M,
+// sum L, unnormalised O) in the log2 domain: an attention sink (log2-domain logit) joins the
+// max and the sum with no value (softmaxWithSink, Qwen3MoEInferenceEngine.java:562-575), then
+// the optional output gate multiplies by sigmoid(gate) (Qwen35InferenceEngine.java:580-583).
+__device__ __forceinline__ float finish_output(float M, float L, float O, const float* sinks,
+                                               const float* gate, int hq, long long gate_idx) {
+    if (sinks != nullptr) {
+        const float sk = sinks[hq];
+        const float Mn = fmaxf(M, sk);
+        const float f = fast_exp2(M - Mn);
+        O = O * f;
+        L = __builtin_fmaf(L, f, fast_exp2(sk - Mn));
+    }
+    float r = O / L;
+    if (gate != nullptr) {
+        const float e = expf(-gate[gate_idx]);
+        r = r * (1.0f / (1.0f + e));
+    }
+    return r;
+}
 
 typedef float native_f4 __attribute__((ext_vector_type(4)));
 
@@ -633,7 +655,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             O = __builtin_fmaf(s_o[(w * G + h) * D + d], sc, O);
         }
         if (sp.splits == 1) {
-            a.out[(h0 + h) * D + d] = O / L;
+            a.out[(h0 + h) * D + d] =
+                finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
         } else {
             const long long slot = ((long long)kvh * sp.splits + split) * G + h;
             a.part_o[slot * D + d] = O;
@@ -703,11 +726,11 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
             O.z = __builtin_fmaf(x.z, sc, O.z);
             O.w = __builtin_fmaf(x.w, sc, O.w);
         }
-        const float inv = 1.0f / L;
-        O.x = O.x * inv;
-        O.y = O.y * inv;
-        O.z = O.z * inv;
-        O.w = O.w * inv;
+        const long long g0 = (long long)hq * D + 4 * c;
+        O.x = finish_output(M, L, O.x, a.sinks, a.gate, hq, g0);
+        O.y = finish_output(M, L, O.y, a.sinks, a.gate, hq, g0 + 1);
+        O.z = finish_output(M, L, O.z, a.sinks, a.gate, hq, g0 + 2);
+        O.w = finish_output(M, L, O.w, a.sinks, a.gate, hq, g0 + 3);
         reinterpret_cast<float4*>(a.out + (long long)hq * D)[c] = O;
     }
 }

@@ -29,6 +29,8 @@ struct DecodeArgs {
     const float* sin_t;
     const float* qnw;      // QK-norm weights [D] or nullptr
     const float* knw;
+    const float* sinks;    // [Hq] attention-sink logits times log2(e), or nullptr
+    const float* gate;     // [Hq*D] output gate (out *= sigmoid(gate)), or nullptr
     float* out;            // [Hq*D] final output (written directly when one split runs)
     float* part_o;         // [Hkv][splits][G][D] unnormalised split outputs
     float* part_ml;        // [Hkv][splits][G][2] split (max, sum) in the log2 domain

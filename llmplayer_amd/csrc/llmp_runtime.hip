@@ -51,6 +51,7 @@ struct LayerCfg {
     float eps = 0.0f;
     float* d_qnw = nullptr;
     float* d_knw = nullptr;
+    float* d_sinks = nullptr;   // [n_heads] sink logits times log2(e) (llmp_layer_sinks)
 };
 
 struct RopeTable {
@@ -157,6 +158,7 @@ void free_handle(KvHandle* kv) {
     for (auto& l : kv->layers) {
         if (l.d_qnw) (void)hipFree(l.d_qnw);
         if (l.d_knw) (void)hipFree(l.d_knw);
+        if (l.d_sinks) (void)hipFree(l.d_sinks);
     }
     if (kv->part_o) (void)hipFree(kv->part_o);
     if (kv->part_ml) (void)hipFree(kv->part_ml);
@@ -262,7 +264,8 @@ Plan make_plan(const KvHandle* kv, const LayerCfg& c, int position, int splits_r
 // otherwise the kernels read the position from device memory when they run, and the launch
 // is planned for the longest step the layer can take (position = max_seq - 1).
 int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint64_t q,
-                   uint64_t k, uint64_t v, uint64_t out, int splits, uint64_t stream) {
+                   uint64_t k, uint64_t v, uint64_t gate, uint64_t out, int splits,
+                   uint64_t stream) {
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
     if (position < 0 || position >= kv->max_seq)
@@ -273,6 +276,7 @@ int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint
     if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "decode: null buffer");
     if ((q | k | v | out) & 15)
         return fail(LLMP_ERR_INVALID_ARG, "decode: q/k/v/out must be 16-byte aligned");
+    if (gate & 3) return fail(LLMP_ERR_INVALID_ARG, "decode: gate must be 4-byte aligned");
     if (splits > kMaxSplits)
         return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
 
@@ -302,6 +306,8 @@ int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint
     }
     a.qnw = c.d_qnw;
     a.knw = c.d_knw;
+    a.sinks = c.d_sinks;
+    a.gate = reinterpret_cast<const float*>(gate);
     a.out = reinterpret_cast<float*>(out);
     a.part_o = kv->part_o;
     a.part_ml = kv->part_ml;
@@ -834,6 +840,10 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
         LLMP_HIP_CHECK(hipMalloc(&kv->part_ml, slots * 2 * sizeof(float)), "hipMalloc(split stats)");
         kv->part_slots = slots;
     }
+    if (c.d_sinks && c.n_heads != n_heads) {   // sinks are per query head: a new count drops them
+        (void)hipFree(c.d_sinks);
+        c.d_sinks = nullptr;
+    }
     c.n_heads = n_heads;
     c.rope_type = rope_type;
     c.rope_sel = rope_sel;
@@ -851,7 +861,7 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
                      uint64_t out, int splits, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    return enqueue_decode(kv, layer, position, nullptr, q, k, v, out, splits, stream);
+    return enqueue_decode(kv, layer, position, nullptr, q, k, v, 0, out, splits, stream);
 }
 
 int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uint64_t q,
@@ -861,7 +871,47 @@ int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uin
     if (!d_position || (d_position & 3))
         return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode_devpos: null or misaligned position word");
     return enqueue_decode(kv, layer, kv->max_seq - 1, reinterpret_cast<const int*>(d_position), q,
-                          k, v, out, splits, stream);
+                          k, v, 0, out, splits, stream);
+}
+
+int llmp_attn_decode_ex(uint64_t handle, int layer, int position, uint64_t d_position,
+                        uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
+                        int splits, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (d_position & 3)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode_ex: misaligned position word");
+    if (d_position)
+        return enqueue_decode(kv, layer, kv->max_seq - 1, reinterpret_cast<const int*>(d_position),
+                              q, k, v, gate, out, splits, stream);
+    return enqueue_decode(kv, layer, position, nullptr, q, k, v, gate, out, splits, stream);
+}
+
+int llmp_layer_sinks(uint64_t handle, int layer, const float* sinks) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    if (!sinks) {
+        if (c.d_sinks) (void)hipFree(c.d_sinks);
+        c.d_sinks = nullptr;
+        return LLMP_OK;
+    }
+    // The kernels keep scores in the log2 domain (scale folded with log2(e)): so do the sinks.
+    std::vector<float> l2((size_t)c.n_heads);
+    for (int h = 0; h < c.n_heads; ++h) {
+        if (!std::isfinite(sinks[h]))
+            return fail(LLMP_ERR_INVALID_ARG, "layer %d: sink %d is not finite", layer, h);
+        l2[(size_t)h] = (float)((double)sinks[h] * 1.4426950408889634);
+    }
+    if (!c.d_sinks)
+        LLMP_HIP_CHECK(hipMalloc(&c.d_sinks, l2.size() * sizeof(float)), "hipMalloc(sinks)");
+    LLMP_HIP_CHECK(hipMemcpy(c.d_sinks, l2.data(), l2.size() * sizeof(float), hipMemcpyHostToDevice),
+                   "hipMemcpy(sinks)");
+    return LLMP_OK;
 }
 
 int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* out_splits,
@@ -886,10 +936,25 @@ int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* 
 }
 
 // ---- prefill attention -------------------------------------------------------------------------
+static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint64_t q,
+                           uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);
+
 int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q, uint64_t k,
                       uint64_t v, uint64_t out, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
+    return enqueue_prefill(kv, layer, pos0, n_tokens, q, k, v, 0, out, stream);
+}
+
+int llmp_attn_prefill_ex(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
+                         uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    return enqueue_prefill(kv, layer, pos0, n_tokens, q, k, v, gate, out, stream);
+}
+
+static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint64_t q,
+                           uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream) {
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
     if (n_tokens <= 0 || pos0 < 0 || (long long)pos0 + n_tokens > kv->max_seq)
@@ -901,8 +966,9 @@ int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64
     if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: null buffer");
     if (kv->q8())
         return fail(LLMP_ERR_UNSUPPORTED, "llmp_attn_prefill: Q8_0 cache (decode steps only)");
-    if ((q | k | v) & 1 || out & 15)
-        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: misaligned q/k/v (2 B) or out (16 B)");
+    if ((q | k | v) & 1 || out & 15 || gate & 3)
+        return fail(LLMP_ERR_INVALID_ARG,
+                    "llmp_attn_prefill: misaligned q/k/v (2 B), gate (4 B) or out (16 B)");
     const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
     pk::PrefillArgs a{};
     a.q = reinterpret_cast<const unsigned short*>(q);
@@ -923,6 +989,8 @@ int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64
     }
     a.qnw = c.d_qnw;
     a.knw = c.d_knw;
+    a.sinks = c.d_sinks;
+    a.gate = reinterpret_cast<const float*>(gate);
     a.out = reinterpret_cast<float*>(out);
     a.pos0 = pos0;
     a.P = n_tokens;

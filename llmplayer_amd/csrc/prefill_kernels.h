@@ -58,6 +58,8 @@ struct PrefillArgs {
     const float* sin_t;
     const float* qnw;         // QK-norm weights or nullptr
     const float* knw;
+    const float* sinks;       // [Hq] attention-sink logits times log2(e), or nullptr
+    const float* gate;        // fp32 [P][Hq*D] output gate, or nullptr
     float* out;               // fp32 [P][Hq*D]
     int pos0, P, Hq, Hkv;
     int half_rope, rope_type;
@@ -463,13 +465,18 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
         float lt = l[hh] + __shfl_xor(l[hh], 16);
         lt = lt + __shfl_xor(lt, 32);
         if (q_ok) {
-            const float inv = 1.0f / lt;
-            float* op = a.out + (long long)qi * a.Hq * D + (long long)(kvh * G + hg * HPW + hh) * D;
+            const int hq = kvh * G + hg * HPW + hh;
+            const long long row = (long long)qi * a.Hq * D + (long long)hq * D;
+            float* op = a.out + row;
 #pragma unroll
             for (int d = 0; d < DT; ++d) {
-                const float4 r = make_float4(o[hh][d][0] * inv, o[hh][d][1] * inv,
-                                             o[hh][d][2] * inv, o[hh][d][3] * inv);
-                reinterpret_cast<float4*>(op + d * 16 + 4 * grp)[0] = r;
+                const int d0 = d * 16 + 4 * grp;
+                float4 r;
+                r.x = dk::finish_output(m[hh], lt, o[hh][d][0], a.sinks, a.gate, hq, row + d0);
+                r.y = dk::finish_output(m[hh], lt, o[hh][d][1], a.sinks, a.gate, hq, row + d0 + 1);
+                r.z = dk::finish_output(m[hh], lt, o[hh][d][2], a.sinks, a.gate, hq, row + d0 + 2);
+                r.w = dk::finish_output(m[hh], lt, o[hh][d][3], a.sinks, a.gate, hq, row + d0 + 3);
+                reinterpret_cast<float4*>(op + d0)[0] = r;
             }
         }
     }

@@ -38,8 +38,13 @@ def rope_type_for(arch: str) -> int:
     return _lib.LLMP_ROPE_NEOX if arch in _NEOX_ARCHS else _lib.LLMP_ROPE_NORMAL
 
 
-def is_global_layer(arch: str, layer: int, sliding_window_pattern: Optional[Sequence[bool]] = None) -> bool:
-    """Attention.isGlobalLayer (Attention.java:250-276)."""
+def is_global_layer(arch: str, layer: int, sliding_window_pattern: Optional[Sequence[bool]] = None,
+                    expert_count: int = 0) -> bool:
+    """Attention.isGlobalLayer (Attention.java:250-276).  GPT-OSS with experts runs on the
+    Qwen3MoE engine instead (LLMEngine.java:144), which windows the even layers
+    (Qwen3MoEInferenceEngine.java:280-286) where Attention.isGlobalLayer makes them global."""
+    if arch == ARCH_GPT_OSS and expert_count > 0:
+        return layer % 2 == 1
     if arch == ARCH_GEMMA2:
         return layer % 2 == 1
     if arch == ARCH_GEMMA3:
@@ -76,6 +81,7 @@ class ModelConfig:
     no_rope_layer_interval: int = 0
     use_no_pe_on_global_layers: bool = False
     use_layer_norm: bool = False
+    expert_count: int = 0                 # > 0 for MoE models (selects the Qwen3MoE engine rules)
 
     @property
     def kv_dim(self) -> int:
@@ -266,7 +272,8 @@ class HipForwardPass:
 
     def __init__(self, config: ModelConfig, max_seq_len: int,
                  qk_norm: Optional[Sequence[Optional[tuple]]] = None, device: int = 0,
-                 kv_dtype: int = _lib.LLMP_KV_F32):
+                 kv_dtype: int = _lib.LLMP_KV_F32,
+                 sinks: Optional[Sequence[Optional[np.ndarray]]] = None):
         if not HipForwardPass.isSupportedForAttention(config):
             raise LlmpError("HipForwardPass", 6, "configuration not supported by the HIP attention path")
         init(device)
@@ -291,10 +298,13 @@ class HipForwardPass:
         for layer in range(c.block_count):
             w = qk_norm[layer] if qk_norm is not None else None
             self.configure_layer(layer, w)
+            if sinks is not None and sinks[layer] is not None:
+                self.set_sinks(layer, sinks[layer])
         self.gpuQ = DeviceBuffer(c.q_dim * 4)
         self.gpuK = DeviceBuffer(c.kv_dim * 4)
         self.gpuV = DeviceBuffer(c.kv_dim * 4)
         self.gpuXb2 = DeviceBuffer(c.q_dim * 4)
+        self.gpuGate = DeviceBuffer(c.q_dim * 4)   # attention output gate (Qwen3.5)
         # [position, position + 1] as int32 (CudaForwardPass.gpuTokenParams, :138-141)
         self.gpuTokenParams = DeviceBuffer(8)
 
@@ -322,7 +332,7 @@ class HipForwardPass:
     # -- set-up ------------------------------------------------------------------------------
     def configure_layer(self, layer: int, qk_norm: Optional[tuple]) -> None:
         c = self.config
-        is_global = is_global_layer(c.architecture, layer, c.sliding_window_pattern)
+        is_global = is_global_layer(c.architecture, layer, c.sliding_window_pattern, c.expert_count)
         irope_skip = c.no_rope_layer_interval > 0 and \
             layer % c.no_rope_layer_interval == c.no_rope_layer_interval - 1
         cohere_skip = c.use_no_pe_on_global_layers and is_global
@@ -342,15 +352,35 @@ class HipForwardPass:
              float(c.attention_scale), float(c.attn_logit_soft_cap), float(c.norm_eps),
              _fp(qw), _fp(kw))
 
+    def set_sinks(self, layer: int, sinks: Optional[np.ndarray]) -> None:
+        """Per-query-head attention-sink logits of a layer (GPT-OSS attn_sinks,
+        Qwen3MoEInferenceEngine.java:88-95), or None to remove them."""
+        if sinks is None:
+            call("llmp_layer_sinks", self.kv.handle, layer, None)
+            return
+        s = np.ascontiguousarray(sinks, np.float32).reshape(-1)
+        if s.size != self.config.head_count:
+            raise ValueError(f"sinks: {s.size} values for {self.config.head_count} heads")
+        call("llmp_layer_sinks", self.kv.handle, layer, _fp(s))
+
     # -- per-token API -------------------------------------------------------------------------
     def uploadQKV(self, q: np.ndarray, k: np.ndarray, v: np.ndarray) -> None:
         self.gpuQ.upload(np.ascontiguousarray(q, np.float32))
         self.gpuK.upload(np.ascontiguousarray(k, np.float32))
         self.gpuV.upload(np.ascontiguousarray(v, np.float32))
 
+    def uploadGate(self, gate: np.ndarray) -> None:
+        """Attention output gate for the next gated call (Qwen3.5 attnGate, [Hq*D])."""
+        self.gpuGate.upload(np.ascontiguousarray(gate, np.float32).reshape(self.config.q_dim))
+
     def forwardAttentionPart(self, layerIdx: int, position: int, splits: int = 0,
-                             stream: int = 0) -> None:
-        """Steps 2b'-5 on the device buffers: gpuQ/gpuK/gpuV -> KV append -> gpuXb2."""
+                             stream: int = 0, gated: bool = False) -> None:
+        """Steps 2b'-5 on the device buffers: gpuQ/gpuK/gpuV -> KV append -> gpuXb2 (times
+        sigmoid(gpuGate) when gated, Qwen35InferenceEngine.java:580-583)."""
+        if gated:
+            call("llmp_attn_decode_ex", self.kv.handle, layerIdx, position, 0, self.gpuQ.ptr,
+                 self.gpuK.ptr, self.gpuV.ptr, self.gpuGate.ptr, self.gpuXb2.ptr, splits, stream)
+            return
         call("llmp_attn_decode", self.kv.handle, layerIdx, position, self.gpuQ.ptr, self.gpuK.ptr,
              self.gpuV.ptr, self.gpuXb2.ptr, splits, stream)
 
@@ -367,19 +397,23 @@ class HipForwardPass:
              self.gpuQ.ptr, self.gpuK.ptr, self.gpuV.ptr, self.gpuXb2.ptr, splits, stream)
 
     def forwardAttentionOnly(self, state: InferenceState, layerIdx: int, position: int,
-                             splits: int = 0) -> None:
+                             splits: int = 0, gate: Optional[np.ndarray] = None) -> None:
         """Attention for one layer from host projections in `state` (state.q, state.k,
         state.v) into state.xb2 -- the contract of Attention.forwardFromProjections
-        (Attention.java:284-367) that GpuForwardPass.java:207-241 relies on."""
+        (Attention.java:284-367) that GpuForwardPass.java:207-241 relies on.  `gate` applies
+        the Qwen3.5 output gate."""
         self.uploadQKV(state.q, state.k, state.v)
-        self.forwardAttentionPart(layerIdx, position, splits)
+        if gate is not None:
+            self.uploadGate(gate)
+        self.forwardAttentionPart(layerIdx, position, splits, gated=gate is not None)
         state.xb2[:] = self.downloadXb2()
 
     def prefill(self, layerIdx: int, pos0: int, q_bf16: np.ndarray, k_bf16: np.ndarray,
-                v_bf16: np.ndarray) -> np.ndarray:
+                v_bf16: np.ndarray, gate: Optional[np.ndarray] = None) -> np.ndarray:
         """Attention for a prompt of P tokens at positions pos0..pos0+P-1 in one call (the
         reference runs P sequential forwards, InferenceEngine.java:374-381).  Inputs are bf16
-        bit patterns (uint16) [P, Hq*D] / [P, kvDim]; returns fp32 [P, Hq*D]."""
+        bit patterns (uint16) [P, Hq*D] / [P, kvDim]; returns fp32 [P, Hq*D].  `gate`
+        ([P, Hq*D] fp32) applies the Qwen3.5 output gate."""
         c = self.config
         q16 = np.ascontiguousarray(q_bf16, np.uint16).reshape(-1, c.q_dim)
         k16 = np.ascontiguousarray(k_bf16, np.uint16).reshape(-1, c.kv_dim)
@@ -388,15 +422,23 @@ class HipForwardPass:
         assert k16.shape[0] == P and v16.shape[0] == P
         bq, bk, bv = DeviceBuffer(q16.nbytes), DeviceBuffer(k16.nbytes), DeviceBuffer(v16.nbytes)
         bo = DeviceBuffer(P * c.q_dim * 4)
+        bufs = [bq, bk, bv, bo]
         try:
             bq.upload(q16)
             bk.upload(k16)
             bv.upload(v16)
-            call("llmp_attn_prefill", self.kv.handle, layerIdx, pos0, P, bq.ptr, bk.ptr, bv.ptr,
-                 bo.ptr, 0)
+            gptr = 0
+            if gate is not None:
+                g = np.ascontiguousarray(gate, np.float32).reshape(P, c.q_dim)
+                bg = DeviceBuffer(g.nbytes)
+                bufs.append(bg)
+                bg.upload(g)
+                gptr = bg.ptr
+            call("llmp_attn_prefill_ex", self.kv.handle, layerIdx, pos0, P, bq.ptr, bk.ptr,
+                 bv.ptr, gptr, bo.ptr, 0)
             return bo.download(np.float32, P * c.q_dim).reshape(P, c.q_dim)
         finally:
-            for b in (bq, bk, bv, bo):
+            for b in bufs:
                 b.free()
 
     def decodePlan(self, layerIdx: int, position: int, splits: int = 0) -> dict:
@@ -414,7 +456,7 @@ class HipForwardPass:
         call("llmp_stream_sync", stream)
 
     def close(self) -> None:
-        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2", "gpuTokenParams"):
+        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2", "gpuGate", "gpuTokenParams"):
             buf = getattr(self, b, None)
             if buf is not None:
                 buf.free()

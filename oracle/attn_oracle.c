@@ -90,6 +90,35 @@ void orc_softmax(float *x, int n)
         x[i] = x[i] * inv;
 }
 
+/* Qwen3MoEInferenceEngine.softmaxWithSink (Qwen3MoEInferenceEngine.java:562-575): the sink
+ * logit joins the max and the denominator, and gets no weight of its own. */
+void orc_softmax_with_sink(float *x, int n, float sink)
+{
+    float maxv = sink;
+    for (int i = 0; i < n; i++)
+        if (x[i] > maxv) maxv = x[i];
+    float sum = (float)exp((double)(sink - maxv));
+    for (int i = 0; i < n; i++) {
+        float d = x[i] - maxv;
+        x[i] = (float)exp((double)d);
+        sum = sum + x[i];
+    }
+    float inv = 1.0f / sum;
+    for (int i = 0; i < n; i++)
+        x[i] = x[i] * inv;
+}
+
+/* Qwen3.5 attention output gate (Qwen35InferenceEngine.java:580-583, sigmoid at :628-630):
+ * out[i] *= 1/(1 + (float)exp(-gate[i])). */
+void orc_sigmoid_gate(float *out, const float *gate, int n)
+{
+    for (int i = 0; i < n; i++) {
+        float e = (float)exp((double)(-gate[i]));
+        float sg = 1.0f / (1.0f + e);
+        out[i] = out[i] * sg;
+    }
+}
+
 /* Attention.applyPerHeadNorm (Attention.java:384-394) with SimdVectorOps.scaleWeighted
  * (SimdVectorOps.java:150-162): ss = dot(x,x); r = 1/(float)sqrt(ss/D + eps); x = (x*r)*w. */
 void orc_per_head_norm(float *vec, const float *w, int n_heads, int head_size, float eps)
@@ -162,7 +191,7 @@ void orc_rope_apply_all(float *vec, int n_heads, int head_size, int rope_dim, in
 
 /* Architecture ids for Attention.isGlobalLayer (Attention.java:250-276). */
 enum { ORC_ARCH_OTHER = 0, ORC_ARCH_GEMMA2 = 1, ORC_ARCH_GEMMA3 = 2, ORC_ARCH_GPT_OSS = 3,
-       ORC_ARCH_COHERE2 = 4 };
+       ORC_ARCH_COHERE2 = 4, ORC_ARCH_GPT_OSS_MOE = 5 };
 
 int orc_is_global_layer(int arch, int layer)
 {
@@ -170,6 +199,9 @@ int orc_is_global_layer(int arch, int layer)
     case ORC_ARCH_GEMMA2: return layer % 2 == 1;
     case ORC_ARCH_GEMMA3: return layer % 6 == 5;
     case ORC_ARCH_GPT_OSS: return layer % 2 == 0;
+    /* GPT-OSS with experts on the Qwen3MoE engine: even layers windowed
+     * (Qwen3MoEInferenceEngine.java:280-286; engine choice LLMEngine.java:144). */
+    case ORC_ARCH_GPT_OSS_MOE: return layer % 2 == 1;
     case ORC_ARCH_COHERE2: return layer % 4 == 3;
     default: return 1;
     }
@@ -191,6 +223,7 @@ typedef struct {
     int arch;             /* ORC_ARCH_* */
     int no_rope_interval; /* noRopeLayerInterval, 0 = off */
     int nope_on_global;   /* useNoPeOnGlobalLayers */
+    const float *sinks;   /* per query head attention-sink logits (GPT-OSS), NULL = none */
 } orc_cfg;
 
 /* KVCache.storeK / storeV (KVCache.java:164-179), FLOAT32 mode: cache[layer][pos*kvDim + j]. */
@@ -424,7 +457,7 @@ static void forward_impl(const orc_cfg *c, const orc_layer_cache *kv, int q8,
         int kv_off = (h / kv_mul) * D;
         const float *qh = q + (size_t)h * D;
         float *oh = out + (size_t)h * D;
-        if (use_flash) {
+        if (use_flash && !c->sinks) {
             float max_score = -INFINITY;
             float sum_exp = 0.0f;
             for (int t = start; t <= pos; t++) {
@@ -461,7 +494,10 @@ static void forward_impl(const orc_cfg *c, const orc_layer_cache *kv, int q8,
                 }
                 att[t - start] = s;
             }
-            orc_softmax(att, seq_len);
+            if (c->sinks)
+                orc_softmax_with_sink(att, seq_len, c->sinks[h]);
+            else
+                orc_softmax(att, seq_len);
             for (int t = start; t <= pos; t++)
                 cache_saxpy(kv, q8, t, kv_dim, kv_off, att[t - start], oh, D);
         }

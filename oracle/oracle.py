@@ -15,12 +15,13 @@ import subprocess
 from dataclasses import dataclass
 
 import numpy as np
+from typing import Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libattn_oracle.so")
 _lib = None
 
-ARCH_OTHER, ARCH_GEMMA2, ARCH_GEMMA3, ARCH_GPT_OSS, ARCH_COHERE2 = 0, 1, 2, 3, 4
+ARCH_OTHER, ARCH_GEMMA2, ARCH_GEMMA3, ARCH_GPT_OSS, ARCH_COHERE2, ARCH_GPT_OSS_MOE = 0, 1, 2, 3, 4, 5
 ROPE_NORMAL, ROPE_NEOX = 0, 2
 
 
@@ -38,6 +39,7 @@ class _Cfg(C.Structure):
         ("norm_eps", C.c_float), ("sliding_window", C.c_int),
         ("attention_scale", C.c_float), ("softcap", C.c_float), ("arch", C.c_int),
         ("no_rope_interval", C.c_int), ("nope_on_global", C.c_int),
+        ("sinks", C.POINTER(C.c_float)),
     ]
 
 
@@ -57,12 +59,18 @@ class OracleConfig:
     arch: int = ARCH_OTHER
     no_rope_interval: int = 0
     nope_on_global: bool = False
+    sinks: Optional[np.ndarray] = None   # [n_heads] attention-sink logits (GPT-OSS)
 
     def c(self) -> _Cfg:
+        sinks = None
+        if self.sinks is not None:
+            self._sinks_keep = np.ascontiguousarray(self.sinks, np.float32)
+            assert self._sinks_keep.size == self.n_heads
+            sinks = self._sinks_keep.ctypes.data_as(C.POINTER(C.c_float))
         return _Cfg(self.n_heads, self.n_kv_heads, self.head_size,
                     self.rope_dim or self.head_size, self.rope_type, self.max_seq,
                     self.norm_eps, self.sliding_window, self.attention_scale, self.softcap,
-                    self.arch, self.no_rope_interval, int(self.nope_on_global))
+                    self.arch, self.no_rope_interval, int(self.nope_on_global), sinks)
 
     @property
     def kv_dim(self) -> int:
@@ -81,6 +89,8 @@ def lib():
         L.orc_dot.argtypes = [_F, _F, C.c_int]
         L.orc_saxpy.argtypes = [C.c_float, _F, _F, C.c_int]
         L.orc_softmax.argtypes = [_F, C.c_int]
+        L.orc_softmax_with_sink.argtypes = [_F, C.c_int, C.c_float]
+        L.orc_sigmoid_gate.argtypes = [_F, _F, C.c_int]
         L.orc_per_head_norm.argtypes = [_F, _F, C.c_int, C.c_int, C.c_float]
         L.orc_rope_tables.argtypes = [C.c_int, C.c_int, C.c_float, C.c_float, _F, C.c_int, _F, _F]
         L.orc_rope_apply_all.argtypes = [_F, C.c_int, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int]
@@ -141,6 +151,21 @@ def softmax(x) -> np.ndarray:
     return x
 
 
+def softmax_with_sink(x, sink) -> np.ndarray:
+    """Qwen3MoEInferenceEngine.softmaxWithSink."""
+    x = f32(x).copy()
+    lib().orc_softmax_with_sink(_p(x), x.size, float(np.float32(sink)))
+    return x
+
+
+def sigmoid_gate(out, gate) -> np.ndarray:
+    """out * sigmoid(gate) as the Qwen3.5 attention output gate computes it."""
+    out, gate = f32(out).copy(), f32(gate)
+    assert out.size == gate.size
+    lib().orc_sigmoid_gate(_p(out), _p(gate), out.size)
+    return out
+
+
 def per_head_norm(vec, w, n_heads, head_size, eps) -> np.ndarray:
     vec, w = f32(vec).copy(), f32(w)
     lib().orc_per_head_norm(_p(vec), _p(w), n_heads, head_size, float(np.float32(eps)))
@@ -176,12 +201,13 @@ def start_pos(cfg: OracleConfig, layer, pos) -> int:
 
 def forward_from_projections(cfg: OracleConfig, kcache, vcache, q, k, v, layer, pos,
                              qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None,
-                             use_flash=False, n_threads=1):
+                             use_flash=False, n_threads=1, gate=None):
     """Runs Attention.forwardFromProjections for one layer-call.
 
     kcache/vcache: float32 [max_seq, kvDim] (the reference layout), modified in place (the
     new K/V rows are appended at `pos`).  Returns (out[Hq*D], q_after, k_after): q and k
-    after QK-norm and RoPE, as state.q / state.k hold them after the call."""
+    after QK-norm and RoPE, as state.q / state.k hold them after the call.  cfg.sinks selects
+    GPT-OSS's sink softmax; `gate` ([Hq*D]) applies the Qwen3.5 output gate to out."""
     c = cfg.c()
     q, k, v = f32(q).copy(), f32(k).copy(), f32(v)
     assert kcache.dtype == np.float32 and kcache.flags["C_CONTIGUOUS"]
@@ -197,13 +223,17 @@ def forward_from_projections(cfg: OracleConfig, kcache, vcache, q, k, v, layer, 
         _p(f32(rope_cos)) if rope_cos is not None else None,
         _p(f32(rope_sin)) if rope_sin is not None else None,
         _p(q), _p(k), _p(v), layer, pos, _p(out), _p(att), int(use_flash), int(n_threads))
+    if gate is not None:
+        out = sigmoid_gate(out, gate)
     return out, q, k
 
 
 def prefill_sequential(cfg: OracleConfig, kcache, vcache, q, k, v, layer, pos0,
-                       qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1):
+                       qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1,
+                       gate=None):
     """P sequential single-token calls (the reference's prefill).  q: [P, Hq*D],
-    k/v: [P, kvDim].  Returns out [P, Hq*D]; the caches gain rows pos0..pos0+P-1."""
+    k/v: [P, kvDim].  Returns out [P, Hq*D]; the caches gain rows pos0..pos0+P-1.
+    `gate` ([P, Hq*D]) applies the Qwen3.5 output gate to each token's output."""
     c = cfg.c()
     q, k, v = f32(q), f32(k), f32(v)
     P = q.shape[0]
@@ -216,6 +246,8 @@ def prefill_sequential(cfg: OracleConfig, kcache, vcache, q, k, v, layer, pos0,
         _p(f32(rope_cos)) if rope_cos is not None else None,
         _p(f32(rope_sin)) if rope_sin is not None else None,
         _p(q), _p(k), _p(v), layer, pos0, P, _p(out), int(n_threads))
+    if gate is not None:
+        out = sigmoid_gate(out.reshape(-1), f32(gate).reshape(-1)).reshape(out.shape)
     return out
 
 
@@ -260,7 +292,7 @@ def q8_saxpy(w, vq, vs, out, mode=Q8_SCALAR):
 
 def forward_from_projections_q8(cfg: OracleConfig, kq, ks, vq, vs, q, k, v, layer, pos,
                                 qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None,
-                                use_flash=False, n_threads=1, mode=Q8_SCALAR):
+                                use_flash=False, n_threads=1, mode=Q8_SCALAR, gate=None):
     """Attention.forwardFromProjections over a Q8_0 cache.  kq/vq: int8 [max_seq, kvDim],
     ks/vs: float32 [max_seq, kvDim/32], modified in place (row `pos` is quantized and
     stored).  `mode` selects the JVM's Q8_0 contract.  Returns (out, q_after, k_after)."""
@@ -282,6 +314,8 @@ def forward_from_projections_q8(cfg: OracleConfig, kq, ks, vq, vs, q, k, v, laye
         _p(f32(rope_sin)) if rope_sin is not None else None,
         _p(q), _p(k), _p(v), layer, pos, _p(out), _p(att), int(use_flash), int(n_threads),
         int(mode))
+    if gate is not None:
+        out = sigmoid_gate(out, gate)
     return out, q, k
 
 

@@ -27,13 +27,17 @@ def log(msg: str) -> None:
     sys.stdout.flush()
 
 
-def oracle_config(c: hfp.ModelConfig, max_seq: int) -> orc.OracleConfig:
+def oracle_config(c: hfp.ModelConfig, max_seq: int, sinks=None) -> orc.OracleConfig:
+    arch = _ORC_ARCH.get(c.architecture, orc.ARCH_OTHER)
+    if c.architecture == hfp.ARCH_GPT_OSS and c.expert_count > 0:
+        arch = orc.ARCH_GPT_OSS_MOE
     return orc.OracleConfig(
         n_heads=c.head_count, n_kv_heads=c.head_count_kv, head_size=c.head_size,
         max_seq=max_seq, rope_type=c.resolved_rope_type(), rope_dim=c.rope_dim_count or c.head_size,
         norm_eps=c.norm_eps, sliding_window=c.sliding_window, attention_scale=c.attention_scale,
-        softcap=c.attn_logit_soft_cap, arch=_ORC_ARCH.get(c.architecture, orc.ARCH_OTHER),
-        no_rope_interval=c.no_rope_layer_interval, nope_on_global=c.use_no_pe_on_global_layers)
+        softcap=c.attn_logit_soft_cap, arch=arch,
+        no_rope_interval=c.no_rope_layer_interval, nope_on_global=c.use_no_pe_on_global_layers,
+        sinks=sinks)
 
 
 def oracle_tables(c: hfp.ModelConfig, max_seq: int, layer: int):
@@ -83,15 +87,15 @@ def make_layer(c: hfp.ModelConfig, max_seq: int, filled: int, seed: int, k_scale
 
 
 def oracle_call(c: hfp.ModelConfig, max_seq: int, d: LayerData, layer: int, pos: int,
-                n_threads: int = 8):
+                n_threads: int = 8, sinks=None, gate=None):
     """Runs the oracle on a copy of the layer's cache; returns (out, kc_after, vc_after)."""
-    oc = oracle_config(c, max_seq)
+    oc = oracle_config(c, max_seq, sinks)
     cs, sn = oracle_tables(c, max_seq, layer)
     kc, vc = d.kc.copy(), d.vc.copy()
     qw, kw = (d.qk_norm if d.qk_norm is not None else (None, None))
     out, _, _ = orc.forward_from_projections(oc, kc, vc, d.q, d.k, d.v, layer, pos, qnorm_w=qw,
                                              knorm_w=kw, rope_cos=cs, rope_sin=sn,
-                                             n_threads=n_threads)
+                                             n_threads=n_threads, gate=gate)
     return out, kc, vc
 
 
@@ -151,15 +155,15 @@ def make_layer_q8(c: hfp.ModelConfig, max_seq: int, filled: int, seed: int, k_sc
 
 
 def oracle_call_q8(c: hfp.ModelConfig, max_seq: int, d: LayerDataQ8, layer: int, pos: int,
-                   n_threads: int = 8, mode: int = orc.Q8_SCALAR):
+                   n_threads: int = 8, mode: int = orc.Q8_SCALAR, sinks=None, gate=None):
     """The oracle over copies of the Q8_0 cache; returns (out, (kq, ks, vq, vs) after)."""
-    oc = oracle_config(c, max_seq)
+    oc = oracle_config(c, max_seq, sinks)
     cs, sn = oracle_tables(c, max_seq, layer)
     kq, ks, vq, vs = d.kq.copy(), d.ks.copy(), d.vq.copy(), d.vs.copy()
     qw, kw = (d.qk_norm if d.qk_norm is not None else (None, None))
     out, _, _ = orc.forward_from_projections_q8(oc, kq, ks, vq, vs, d.q, d.k, d.v, layer, pos,
                                                 qnorm_w=qw, knorm_w=kw, rope_cos=cs, rope_sin=sn,
-                                                n_threads=n_threads, mode=mode)
+                                                n_threads=n_threads, mode=mode, gate=gate)
     return out, (kq, ks, vq, vs)
 
 

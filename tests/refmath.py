@@ -44,9 +44,10 @@ def rope_rotate(x, n_heads, head_size, rope_dim, rope_type, angles):
 
 
 def attention(q, kcache, vcache, n_heads, n_kv_heads, head_size, start, pos, scale,
-              softcap=0.0):
+              softcap=0.0, sinks=None):
     """out_h = softmax_t(s_t) . V_t over t in [start, pos], s_t = scale * q_h.K_t (soft-capped
-    as c*tanh(s/c) when softcap > 0); kv head of query head h is h // (Hq/Hkv)."""
+    as c*tanh(s/c) when softcap > 0); kv head of query head h is h // (Hq/Hkv).  With sinks,
+    head h's softmax has one more logit sinks[h] that takes no value (a denominator term)."""
     q = np.asarray(q, np.float64).reshape(n_heads, head_size)
     kv_dim = n_kv_heads * head_size
     K = np.asarray(kcache, np.float64).reshape(-1, kv_dim)[start:pos + 1]
@@ -60,8 +61,13 @@ def attention(q, kcache, vcache, n_heads, n_kv_heads, head_size, start, pos, sca
         s = Kh @ q[h] * scale
         if softcap > 0:
             s = softcap * np.tanh(s / softcap)
-        p = np.exp(s - s.max())
-        p /= p.sum()
+        if sinks is None:
+            p = np.exp(s - s.max())
+            p /= p.sum()
+        else:
+            mx = max(s.max(), float(sinks[h]))
+            p = np.exp(s - mx)
+            p /= p.sum() + np.exp(float(sinks[h]) - mx)
         out[h] = p @ Vh
     return out.reshape(-1)
 

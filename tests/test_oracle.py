@@ -543,3 +543,96 @@ def test_q8_simd8_layer_call():
     orc.forward_from_projections_q8(cfg, kq1, ks1, vq1, vs1, q, k, v, 0, pos, rope_cos=cs,
                                     rope_sin=sn)
     assert not np.array_equal(kq1[pos], kq[pos])
+
+
+# ------------------------------------------- attention variants: GPT-OSS sinks, Qwen3.5 gate
+def test_softmax_with_sink_closed_forms():
+    x = np.array([0.0, 0.0, 0.0, 0.0], F32)
+    for sink in (-3.0, 0.0, 2.0):
+        got = orc.softmax_with_sink(x, sink)
+        want = 1.0 / (4.0 + np.exp(sink))
+        np.testing.assert_allclose(got, np.full(4, want), rtol=2e-7)
+    # a very negative sink is the plain softmax, bit for bit (same max, same sum order)
+    rng = np.random.default_rng(50)
+    y = rng.standard_normal(300).astype(F32) * F32(3)
+    assert np.array_equal(orc.softmax_with_sink(y, -1e30), orc.softmax(y))
+    # a dominant sink takes (almost) all the mass; weights keep their ratios
+    z = orc.softmax_with_sink(y, 60.0)
+    assert z.sum() < 1e-15 and np.all(z >= 0)
+    w = orc.softmax_with_sink(y, 1.5)
+    e = np.exp(y.astype(np.float64) - max(y.max(), 1.5))
+    np.testing.assert_allclose(w, e / (e.sum() + np.exp(1.5 - max(y.max(), 1.5))), rtol=2e-6)
+
+
+@pytest.mark.parametrize("shape", [(24, 8, 128), (32, 8, 64), (8, 8, 64)])
+def test_sinks_layer_call_matches_float64(shape):
+    Hq, Hkv, D = shape
+    pos = 90
+    rng = np.random.default_rng(51)
+    sinks = rng.uniform(-2, 4, Hq).astype(F32)
+    cfg = orc.OracleConfig(Hq, Hkv, D, 128, sinks=sinks, attention_scale=0.11)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, pos, 52, k_scale=0.5)
+    kc0, vc0 = kc.copy(), vc.copy()
+    out, q2, k2 = orc.forward_from_projections(cfg, kc, vc, q, k, v, 0, pos, rope_cos=cs,
+                                               rope_sin=sn)
+    K = kc0.astype(np.float64); V = vc0.astype(np.float64)
+    K[pos] = k2; V[pos] = v
+    want = rm.attention(q2, K, V, Hq, Hkv, D, 0, pos, float(F32(0.11)), sinks=sinks)
+    rm.assert_close(out, want, atol=2e-6, rtol=1e-5, what="sinks vs fp64")
+    # the sinks shrink every head's weights: without them the output differs
+    cfg0 = orc.OracleConfig(Hq, Hkv, D, 128, attention_scale=0.11)
+    out0, _, _ = orc.forward_from_projections(cfg0, kc0.copy(), vc0.copy(), q, k, v, 0, pos,
+                                              rope_cos=cs, rope_sin=sn)
+    assert np.abs(out - out0).max() > 1e-3
+    # q = 0: every score is 0, so head h's output is sum(V) / (n + exp(sink_h))
+    cfgz = orc.OracleConfig(Hq, Hkv, D, 128, sinks=sinks)
+    outz, _, _ = orc.forward_from_projections(cfgz, kc0.copy(), vc0.copy(), np.zeros_like(q), k,
+                                              v, 0, pos)
+    Vh = V.reshape(-1, Hkv, D)[:pos + 1].sum(0)
+    g = Hq // Hkv
+    wantz = np.stack([Vh[h // g] / (pos + 1 + np.exp(float(sinks[h]))) for h in range(Hq)])
+    np.testing.assert_allclose(outz.reshape(Hq, D), wantz, atol=2e-6)
+    # the flash loop has no sink form in the reference: with sinks the two-pass path runs
+    b, _, _ = orc.forward_from_projections(cfg, kc0.copy(), vc0.copy(), q, k, v, 0, pos,
+                                           rope_cos=cs, rope_sin=sn, use_flash=True)
+    assert np.array_equal(b, out)
+
+
+def test_sigmoid_gate_closed_forms():
+    rng = np.random.default_rng(53)
+    out = rng.standard_normal(512).astype(F32)
+    assert np.array_equal(orc.sigmoid_gate(out, np.zeros(512, F32)), out * F32(0.5))
+    assert np.array_equal(orc.sigmoid_gate(out, np.full(512, 200.0, F32)), out)
+    assert not orc.sigmoid_gate(out, np.full(512, -200.0, F32)).any()
+    g = rng.uniform(-8, 8, 512).astype(F32)
+    want = out.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    np.testing.assert_allclose(orc.sigmoid_gate(out, g), want, rtol=3e-7, atol=1e-30)
+
+
+def test_gated_layer_call_is_gate_times_plain_output():
+    cfg = orc.OracleConfig(16, 4, 128, 64, rope_type=orc.ROPE_NEOX, norm_eps=1e-6)
+    kc, vc, q, k, v, cs, sn = _setup(cfg, 40, 54, theta=1e7)
+    gate = np.random.default_rng(55).uniform(-4, 4, 16 * 128).astype(F32)
+    a, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 0, 40,
+                                           rope_cos=cs, rope_sin=sn)
+    b, _, _ = orc.forward_from_projections(cfg, kc.copy(), vc.copy(), q, k, v, 0, 40,
+                                           rope_cos=cs, rope_sin=sn, gate=gate)
+    assert np.array_equal(b, orc.sigmoid_gate(a, gate))
+    np.testing.assert_allclose(b, a.astype(np.float64) / (1 + np.exp(-gate.astype(np.float64))),
+                               rtol=1e-6, atol=1e-30)
+
+
+def test_gptoss_moe_engine_windows_even_layers():
+    # Qwen3MoEInferenceEngine.java:280-286: even layers attend to the last W rows, odd layers
+    # to all; Attention.isGlobalLayer's GPT-OSS rule is the opposite.
+    moe = orc.OracleConfig(8, 2, 64, 600, sliding_window=128, arch=orc.ARCH_GPT_OSS_MOE)
+    att = orc.OracleConfig(8, 2, 64, 600, sliding_window=128, arch=orc.ARCH_GPT_OSS)
+    for layer in range(4):
+        even = layer % 2 == 0
+        assert orc.start_pos(moe, layer, 500) == (373 if even else 0)
+        assert orc.start_pos(att, layer, 500) == (0 if even else 373)
+        assert orc.start_pos(moe, layer, 100) == 0
+    from llmplayer_amd import hip_forward_pass as hfp
+    for layer in range(4):
+        assert hfp.is_global_layer(hfp.ARCH_GPT_OSS, layer, expert_count=32) == (layer % 2 == 1)
+        assert hfp.is_global_layer(hfp.ARCH_GPT_OSS, layer) == (layer % 2 == 0)
