@@ -148,33 +148,56 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     const int r0 = (tile0 + (int)blockIdx.x) * TK;
     const float* kplane = a.kc + (long long)kvh * a.head_stride;
     const float* vplane = a.vc + (long long)kvh * a.head_stride;
-    // Thread work item: rows r, r+1 and dims 4*c4 .. 4*c4+3.
-    for (int e = tid; e < (TK / 2) * (D / 4); e += NTHR) {
-        const int rp = e / (D / 4), c4 = e - rp * (D / 4);
-        const int r = 2 * rp;
-        const int row0 = min(r0 + r, row_end - 1), row1 = min(r0 + r + 1, row_end - 1);
-        const float4 k0 = reinterpret_cast<const float4*>(kplane + (long long)row0 * D)[c4];
-        const float4 k1 = reinterpret_cast<const float4*>(kplane + (long long)row1 * D)[c4];
-        const float4 v0 = reinterpret_cast<const float4*>(vplane + (long long)row0 * D)[c4];
-        const float4 v1 = reinterpret_cast<const float4*>(vplane + (long long)row1 * D)[c4];
+    // K rows: work item (row r, dims 4*c4 .. 4*c4+3), c4 fastest across lanes, so the loads
+    // are row-contiguous and the 8-byte stores of 16 lanes cover the 32 banks once.
+    // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), rq fastest across lanes: each
+    // dim row gets the 4 keys as one 8-byte store, and 16 lanes' stores cover the 32 banks.
+    // Every global load of a thread is issued before any of its math (one memory round trip).
+    constexpr int KI = TK * (D / 4) / NTHR, VI = (TK / 4) * (D / 4) / NTHR;
+    static_assert(KI * NTHR == TK * (D / 4) && VI * NTHR == (TK / 4) * (D / 4),
+                  "tile work must divide evenly over the threads");
+    float4 kx[KI], vx[VI][4];
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+        const int e = tid + i * NTHR;
+        const int r = e / (D / 4), c4 = e - r * (D / 4);
+        kx[i] = reinterpret_cast<const float4*>(kplane + (long long)min(r0 + r, row_end - 1) * D)[c4];
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+        const int e = tid + i * NTHR;
+        const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            vx[i][j] = reinterpret_cast<const float4*>(
+                vplane + (long long)min(r0 + 4 * rq + j, row_end - 1) * D)[c4];
+    }
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+        const int e = tid + i * NTHR;
+        const int r = e / (D / 4), c4 = e - r * (D / 4);
         unsigned h0, l0, h1, l1;
-        // K rows (row-major): dims (4c4, 4c4+1) and (4c4+2, 4c4+3) of rows r and r+1.
-        split_pair(k0.x, k0.y, h0, l0);
-        split_pair(k0.z, k0.w, h1, l1);
+        split_pair(kx[i].x, kx[i].y, h0, l0);
+        split_pair(kx[i].z, kx[i].w, h1, l1);
         *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
         *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
-        split_pair(k1.x, k1.y, h0, l0);
-        split_pair(k1.z, k1.w, h1, l1);
-        *reinterpret_cast<uint2*>(&t.kh[(r + 1) * T::KP + 4 * c4]) = make_uint2(h0, h1);
-        *reinterpret_cast<uint2*>(&t.kl[(r + 1) * T::KP + 4 * c4]) = make_uint2(l0, l1);
-        // V^T: for each of the 4 dims, the pair of rows (r, r+1).
-        const float va[4] = {v0.x, v0.y, v0.z, v0.w}, vb[4] = {v1.x, v1.y, v1.z, v1.w};
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+        const int e = tid + i * NTHR;
+        const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
+        const float vv[4][4] = {{vx[i][0].x, vx[i][0].y, vx[i][0].z, vx[i][0].w},
+                                {vx[i][1].x, vx[i][1].y, vx[i][1].z, vx[i][1].w},
+                                {vx[i][2].x, vx[i][2].y, vx[i][2].z, vx[i][2].w},
+                                {vx[i][3].x, vx[i][3].y, vx[i][3].z, vx[i][3].w}};   // [key][dim]
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            split_pair(va[u], vb[u], h0, l0);
+            unsigned h0, l0, h1, l1;
+            split_pair(vv[0][u], vv[1][u], h0, l0);
+            split_pair(vv[2][u], vv[3][u], h1, l1);
             const int d = 4 * c4 + u;
-            *reinterpret_cast<unsigned*>(&t.vh[d * T::VP + r]) = h0;
-            *reinterpret_cast<unsigned*>(&t.vl[d * T::VP + r]) = l0;
+            *reinterpret_cast<uint2*>(&t.vh[d * T::VP + 4 * rq]) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(&t.vl[d * T::VP + 4 * rq]) = make_uint2(l0, l1);
         }
     }
     __syncthreads();
