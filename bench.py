@@ -205,6 +205,62 @@ def prefill_run(P: int, steps: int) -> dict:
             "mfma_tflops_bf16x3": round(3 * flops / (res["attn"] * 1e-6) / 1e12, 2)}
 
 
+def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int) -> dict:
+    """Speculative verification at the C3 shape: K draft tokens at positions ctx-K..ctx-1 in
+    one llmp_attn_prefill call over a (ctx-K)-row cache (the reference runs K sequential
+    forwards, LLMEngine.java:1019-1033).  Layer caches rotate over >= 2 GiB; graph replay."""
+    from llmplayer_amd import _lib
+    from llmplayer_amd import hip_forward_pass as hfp
+    per_layer = kv_bytes(ctx)
+    n_layers = max(1, math.ceil(rotate_bytes / per_layer))
+    c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
+    fp = hfp.HipForwardPass(c, ctx)
+    bufs = []
+    try:
+        rng = np.random.default_rng(7)
+        fill_caches(fp, c, ctx - K + 1, n_layers, False, rng)
+        arrs = [hfp.to_bf16(rng.standard_normal((K, n), dtype=np.float32))
+                for n in (c.q_dim, c.kv_dim, c.kv_dim)]
+        for arr in arrs:
+            b = hfp.DeviceBuffer(arr.nbytes)
+            b.upload(arr)
+            bufs.append(b)
+        out = hfp.DeviceBuffer(K * c.q_dim * 4)
+        bufs.append(out)
+        pos0 = ctx - K
+        call = lambda layer: _lib.call("llmp_attn_prefill", fp.kv.handle, layer, pos0, K,
+                                       bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, out.ptr, 0)
+        for i in range(n_layers):
+            call(i)
+        _lib.call("llmp_stream_sync", 0)
+        g = C.c_uint64()
+        _lib.call("llmp_graph_begin", 0)
+        for i in range(steps):
+            call(i % n_layers)
+        _lib.call("llmp_graph_end", 0, C.byref(g))
+        _lib.call("llmp_graph_launch", g.value, 0)
+        _lib.call("llmp_stream_sync", 0)
+        e0, e1 = C.c_uint64(), C.c_uint64()
+        _lib.call("llmp_event_create", C.byref(e0))
+        _lib.call("llmp_event_create", C.byref(e1))
+        _lib.call("llmp_event_record", e0.value, 0)
+        _lib.call("llmp_graph_launch", g.value, 0)
+        _lib.call("llmp_event_record", e1.value, 0)
+        _lib.call("llmp_event_sync", e1.value)
+        ms = C.c_float()
+        _lib.call("llmp_event_elapsed_ms", C.byref(ms), e0.value, e1.value)
+        _lib.call("llmp_graph_destroy", g.value)
+        _lib.call("llmp_event_destroy", e0.value)
+        _lib.call("llmp_event_destroy", e1.value)
+    finally:
+        for b in bufs:
+            b.free()
+        fp.close()
+    us = ms.value / steps * 1e3
+    return {"K": K, "ctx": ctx, "us_per_call": round(us, 2),
+            "kv_read_gbps": round(kv_bytes(ctx - K) / (us * 1e-6) / 1e9, 1)}
+
+
 def cpu_baseline(ctx: int, seconds: float) -> dict:
     """The oracle (CPU restatement of Attention.forwardFromProjections) on one layer-call of
     the same shape, parallel over query heads; median over a bounded sample."""
@@ -318,6 +374,8 @@ def main() -> int:
     ap.add_argument("--rotate-gib", type=float, default=2.0)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-verify", dest="verify", action="store_false",
+                    help="skip the speculative-verification (K draft tokens) measurement")
     ap.add_argument("--no-q8", dest="q8", action="store_false",
                     help="skip the Q8_0-cache decode measurement")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
@@ -369,6 +427,16 @@ def main() -> int:
             log(f"[bench] ctx {ctx} Q8_0: {r['us_per_layer_call']:.2f} us/layer-call, "
                 f"{r['kv_read_gbps']:.0f} GB/s, split kernel {r['split_kernel_us']:.2f} us")
             q8_runs.append(r)
+
+    verify = []
+    if args.verify:
+        for K in (4, 8, 16):
+            r = verify_run(args.ctx, K, 100, rot)
+            r["decode_calls_us"] = round(K * main_run["us_per_layer_call"], 2)
+            r["speedup_vs_k_decode_calls"] = round(r["decode_calls_us"] / r["us_per_call"], 2)
+            log(f"[bench] verify K={K} at ctx {args.ctx}: {r['us_per_call']:.1f} us/call "
+                f"({r['speedup_vs_k_decode_calls']:.2f}x vs {K} decode calls)")
+            verify.append(r)
 
     prefill = []
     if args.prefill:
@@ -441,6 +509,8 @@ def main() -> int:
                 "speedup_vs_f32_cache": round(f32_us[r["ctx"]] / r["us_per_layer_call"], 3)})
     if prefill:
         line["prefill_c5_llama1b"] = prefill
+    if verify:
+        line["speculative_verify_c3"] = verify
     print(json.dumps(line), flush=True)
     return 0
 

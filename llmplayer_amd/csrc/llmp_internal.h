@@ -96,7 +96,13 @@ hipError_t launch_prefill_append(const pk::PrefillArgs& a, int head_dim, hipStre
 hipError_t launch_prefill_tiles(const pk::PrefillArgs& a, int head_dim, void* ws, int tile0,
                                 int n_tiles, int row_end, hipStream_t stream);
 hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group, const void* ws,
-                               int tile0, int n_tiles, int n_cu, hipStream_t stream);
+                               int tile0, int n_tiles, int n_cu, int ksplit, hipStream_t stream);
+// Key splits of a prefill call (1 unless the query blocks alone leave CUs idle: short prompts
+// after a long cached prefix, speculative verification); ksplit > 1 writes partials to
+// a.part_o / a.part_ml ([ksplit][P][Hq][D] and [..][2] floats) and adds a combine launch.
+constexpr int kMaxPrefillSplits = 64;
+int prefill_key_splits(int P, int pos0, int window, int n_kv_heads, int group, int head_dim,
+                       int n_cu);
 // Keys per tile and bytes per tile image (per KV head) for head_dim; 0 if unsupported.
 int prefill_tile_keys(int head_dim);
 size_t prefill_tile_bytes(int head_dim);

@@ -73,6 +73,8 @@ struct KvHandle {
     std::vector<LayerCfg> layers;
     void* prefill_ws = nullptr;   // prefill tile images (grown on demand)
     size_t prefill_ws_bytes = 0;
+    float* prefill_part = nullptr;   // prefill split-K partials (grown on demand)
+    size_t prefill_part_bytes = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
     size_t part_slots = 0;    // (split, query head) slots the workspace holds
@@ -163,6 +165,7 @@ void free_handle(KvHandle* kv) {
     if (kv->part_o) (void)hipFree(kv->part_o);
     if (kv->part_ml) (void)hipFree(kv->part_ml);
     if (kv->prefill_ws) (void)hipFree(kv->prefill_ws);
+    if (kv->prefill_part) (void)hipFree(kv->prefill_part);
     for (auto& v : kv->prof_pending)
         for (auto& p : v) {
             (void)hipEventDestroy(p.begin);
@@ -1017,7 +1020,9 @@ static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint
     const int kbeg_min = a.window > 0 ? std::max(0, pos0 - a.window + 1) : 0;
     const int tile0 = kbeg_min / TK, tile_last = (pos0 + n_tokens - 1) / TK;
     const int n_tiles = tile_last - tile0 + 1;
-    const size_t ws_bytes = (size_t)Hkv * (size_t)n_tiles * prefill_tile_bytes(D);
+    const int ksplit = prefill_key_splits(n_tokens, pos0, a.window, Hkv, group, D, G().n_cu);
+    const size_t ws_bytes =
+        ksplit == 1 ? (size_t)Hkv * (size_t)n_tiles * prefill_tile_bytes(D) : 0;
     if (ws_bytes > kv->prefill_ws_bytes) {
         if (kv->prefill_ws) {
             LLMP_HIP_CHECK(hipStreamSynchronize(st), "hipStreamSynchronize");
@@ -1031,6 +1036,27 @@ static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint
         LLMP_HIP_CHECK(e, "hipMalloc(prefill workspace)");
         kv->prefill_ws_bytes = ws_bytes;
     }
+    // Key splits (short prompts after a long prefix) and their partials buffer.
+    if (ksplit > 1) {
+        const size_t part_bytes =
+            (size_t)ksplit * (size_t)n_tokens * (size_t)c.n_heads * (size_t)(D + 2) * sizeof(float);
+        if (part_bytes > kv->prefill_part_bytes) {
+            if (kv->prefill_part) {
+                LLMP_HIP_CHECK(hipStreamSynchronize(st), "hipStreamSynchronize");
+                (void)hipFree(kv->prefill_part);
+                kv->prefill_part = nullptr;
+                kv->prefill_part_bytes = 0;
+            }
+            hipError_t e = hipMalloc(&kv->prefill_part, part_bytes);
+            if (e == hipErrorOutOfMemory)
+                return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_attn_prefill: %zu-byte split workspace",
+                            part_bytes);
+            LLMP_HIP_CHECK(e, "hipMalloc(prefill partials)");
+            kv->prefill_part_bytes = part_bytes;
+        }
+        a.part_o = kv->prefill_part;
+        a.part_ml = kv->prefill_part + (size_t)ksplit * n_tokens * c.n_heads * D;
+    }
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr, e3 = nullptr;
     if (kv->prof_on) {
         for (hipEvent_t* e : {&e0, &e1, &e2, &e3})
@@ -1043,9 +1069,11 @@ static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint
         kv->prof_pending[LLMP_PROF_PREFILL_APPEND].push_back({e0, e1});
         LLMP_HIP_CHECK(hipEventRecord(e2, st), "hipEventRecord");
     }
-    LLMP_HIP_CHECK(launch_prefill_tiles(a, D, kv->prefill_ws, tile0, n_tiles, pos0 + n_tokens, st),
-                   "prefill tile launch");
-    LLMP_HIP_CHECK(launch_prefill_attn(a, D, group, kv->prefill_ws, tile0, n_tiles, G().n_cu, st),
+    if (ksplit == 1)   // split launches stage straight from the cache (no images)
+        LLMP_HIP_CHECK(launch_prefill_tiles(a, D, kv->prefill_ws, tile0, n_tiles, pos0 + n_tokens, st),
+                       "prefill tile launch");
+    LLMP_HIP_CHECK(launch_prefill_attn(a, D, group, kv->prefill_ws, tile0, n_tiles, G().n_cu,
+                                       ksplit, st),
                    "prefill attention launch");
     if (kv->prof_on) {
         LLMP_HIP_CHECK(hipEventRecord(e3, st), "hipEventRecord");

@@ -1,6 +1,8 @@
 // Instantiation and dispatch of the prefill kernels (prefill_kernels.h).
 #include "prefill_kernels.h"
 
+#include <algorithm>
+
 namespace llmp {
 namespace {
 
@@ -13,39 +15,59 @@ constexpr int kTileThreads = 256;
 // holds two workgroups per CU, else NB_BIG/2 (short prompts).
 constexpr int nb_big(int G) { return G >= 8 ? 1 : (8 / G >= 4 ? 4 : 8 / G); }
 
+// Workgroups per key split: query blocks of 16*NB tokens times KV heads.
+inline int prefill_items(int P, int Hkv, int NB) { return ((P + 16 * NB - 1) / (16 * NB)) * Hkv; }
+
+// Query blocks per workgroup the launch uses for P tokens and group size G (see launch_attn_dg).
+inline int prefill_nb(int P, int Hkv, int G, int n_cu) {
+    const int nb = nb_big(G);
+    return (nb > 1 && prefill_items(P, Hkv, nb) < 2 * n_cu) ? nb / 2 : nb;
+}
+
 template <int D, int G, int NB>
 hipError_t launch_attn_dgn(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
-                           hipStream_t stream) {
+                           int ksplit, hipStream_t stream) {
     const int items = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
-    hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, 1>), dim3(items), dim3(G * NB * 64),
-                       0, stream, a, ws, tile0, n_tiles);
+    if (ksplit > 1)   // few query blocks: stage from the fp32 cache, no tile images
+        hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, true>), dim3(items, ksplit),
+                           dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
+    else
+        hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, false>), dim3(items, ksplit),
+                           dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
     return hipGetLastError();
 }
 
 template <int D, int G>
 hipError_t launch_attn_dg(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
-                          int n_cu, hipStream_t stream) {
+                          int n_cu, int ksplit, hipStream_t stream) {
     constexpr int NB = nb_big(G);
-    const int items_big = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
     if constexpr (NB > 1) {
-        if (items_big < 2 * n_cu)
-            return launch_attn_dgn<D, G, NB / 2>(a, ws, tile0, n_tiles, stream);
+        if (prefill_items(a.P, a.Hkv, NB) < 2 * n_cu)
+            return launch_attn_dgn<D, G, NB / 2>(a, ws, tile0, n_tiles, ksplit, stream);
     }
-    return launch_attn_dgn<D, G, NB>(a, ws, tile0, n_tiles, stream);
+    return launch_attn_dgn<D, G, NB>(a, ws, tile0, n_tiles, ksplit, stream);
 }
 
 template <int D>
 hipError_t launch_attn_d(const pk::PrefillArgs& a, int group, const uint4* ws, int tile0,
-                         int n_tiles, int n_cu, hipStream_t stream) {
+                         int n_tiles, int n_cu, int ksplit, hipStream_t stream) {
     switch (group) {
-    case 1: return launch_attn_dg<D, 1>(a, ws, tile0, n_tiles, n_cu, stream);
-    case 2: return launch_attn_dg<D, 2>(a, ws, tile0, n_tiles, n_cu, stream);
-    case 3: return launch_attn_dg<D, 3>(a, ws, tile0, n_tiles, n_cu, stream);
-    case 4: return launch_attn_dg<D, 4>(a, ws, tile0, n_tiles, n_cu, stream);
-    case 6: return launch_attn_dg<D, 6>(a, ws, tile0, n_tiles, n_cu, stream);
-    case 8: return launch_attn_dg<D, 8>(a, ws, tile0, n_tiles, n_cu, stream);
+    case 1: return launch_attn_dg<D, 1>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+    case 2: return launch_attn_dg<D, 2>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+    case 3: return launch_attn_dg<D, 3>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+    case 4: return launch_attn_dg<D, 4>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+    case 6: return launch_attn_dg<D, 6>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+    case 8: return launch_attn_dg<D, 8>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+template <int D>
+hipError_t launch_combine_d(const pk::PrefillArgs& a, int ksplit, hipStream_t stream) {
+    const long long threads = (long long)a.P * a.Hq * (D / 4);
+    hipLaunchKernelGGL((pk::prefill_combine_kernel<D>), dim3((unsigned)((threads + 255) / 256)),
+                       dim3(256), 0, stream, a, ksplit);
+    return hipGetLastError();
 }
 
 template <int D>
@@ -104,14 +126,36 @@ hipError_t launch_prefill_tiles(const pk::PrefillArgs& a, int head_dim, void* ws
     }
 }
 
+int prefill_key_splits(int P, int pos0, int window, int n_kv_heads, int group, int head_dim,
+                       int n_cu) {
+    const int TK = prefill_tile_keys(head_dim);
+    if (TK <= 0 || group <= 0) return 1;
+    const int items = prefill_items(P, n_kv_heads, prefill_nb(P, n_kv_heads, group, n_cu));
+    if (items >= n_cu) return 1;
+    // Key tiles of the last query (the heaviest workgroup's range, up to one block's spread).
+    const int last = pos0 + P - 1;
+    const int kbeg = window > 0 ? std::max(0, last - window + 1) : 0;
+    const int tiles = last / TK - kbeg / TK + 1;
+    int ks = (2 * n_cu + items - 1) / items;          // about two workgroups per CU
+    ks = std::min(ks, std::max(1, tiles / 2));        // at least two tiles per split
+    return std::max(1, std::min(ks, kMaxPrefillSplits));
+}
+
 hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group, const void* ws,
-                               int tile0, int n_tiles, int n_cu, hipStream_t stream) {
+                               int tile0, int n_tiles, int n_cu, int ksplit, hipStream_t stream) {
     const uint4* w = static_cast<const uint4*>(ws);
+    hipError_t e;
     switch (head_dim) {
-    case 64: return launch_attn_d<64>(a, group, w, tile0, n_tiles, n_cu, stream);
-    case 128: return launch_attn_d<128>(a, group, w, tile0, n_tiles, n_cu, stream);
-    case 256: return launch_attn_d<256>(a, group, w, tile0, n_tiles, n_cu, stream);
+    case 64: e = launch_attn_d<64>(a, group, w, tile0, n_tiles, n_cu, ksplit, stream); break;
+    case 128: e = launch_attn_d<128>(a, group, w, tile0, n_tiles, n_cu, ksplit, stream); break;
+    case 256: e = launch_attn_d<256>(a, group, w, tile0, n_tiles, n_cu, ksplit, stream); break;
     default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess || ksplit <= 1) return e;
+    switch (head_dim) {
+    case 64: return launch_combine_d<64>(a, ksplit, stream);
+    case 128: return launch_combine_d<128>(a, ksplit, stream);
+    default: return launch_combine_d<256>(a, ksplit, stream);
     }
 }
 

@@ -61,6 +61,8 @@ struct PrefillArgs {
     const float* sinks;       // [Hq] attention-sink logits times log2(e), or nullptr
     const float* gate;        // fp32 [P][Hq*D] output gate, or nullptr
     float* out;               // fp32 [P][Hq*D]
+    float* part_o;            // split-K partials [ksplit][P][Hq][D] (ksplit > 1)
+    float* part_ml;           // split-K (max, sum) [ksplit][P][Hq][2]
     int pos0, P, Hq, Hkv;
     int half_rope, rope_type;
     int window;               // > 0: attend to the last `window` rows (local layer)
@@ -298,13 +300,85 @@ __device__ __forceinline__ void img_store(const u32x4 (&stage)[PER], void* dst, 
     }
 }
 
+// Direct staging from the fp32 cache (short prompts after a long prefix, where each key tile
+// feeds only a few workgroups and building images first would re-convert the whole prefix on
+// every call).  K: items (row, 4-dim chunk) with the chunk fastest; V: items (4 keys, 4-dim
+// chunk) with the keys fastest, stored transposed as 8-byte runs.  Rows at or past row_lim
+// repeat row row_lim (never attended, finite).
+template <int D, int NTHR>
+struct RawTile {
+    static constexpr int TK = TileLds<D>::TK;
+    static constexpr int NK = TK * (D / 4), NV = (TK / 4) * (D / 4);
+    static constexpr int KI = (NK + NTHR - 1) / NTHR, VI = (NV + NTHR - 1) / NTHR;
+};
+
+template <int D, int NTHR, int KI, int VI>
+__device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4],
+                                         const float* kplane, const float* vplane, int t0,
+                                         int row_lim, int tid) {
+    using R = RawTile<D, NTHR>;
+    static_assert(KI == R::KI && VI == R::VI, "staging register counts");
+#pragma unroll
+    for (int i = 0; i < R::KI; ++i) {
+        const int e = min(tid + i * NTHR, R::NK - 1);
+        const int r = e / (D / 4), c4 = e - r * (D / 4);
+        kx[i] = reinterpret_cast<const floatx4*>(kplane + (long long)min(t0 + r, row_lim) * D)[c4];
+    }
+#pragma unroll
+    for (int i = 0; i < R::VI; ++i) {
+        const int e = min(tid + i * NTHR, R::NV - 1);
+        const int c4 = e / (R::TK / 4), rq = e - c4 * (R::TK / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            vx[i][j] = reinterpret_cast<const floatx4*>(
+                vplane + (long long)min(t0 + 4 * rq + j, row_lim) * D)[c4];
+    }
+}
+
+template <int D, int NTHR, int KI, int VI>
+__device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4 (&vx)[VI][4],
+                                          TileLds<D>& t, int tid) {
+    using R = RawTile<D, NTHR>;
+    static_assert(KI == R::KI && VI == R::VI, "staging register counts");
+    using T = TileLds<D>;
+#pragma unroll
+    for (int i = 0; i < R::KI; ++i) {
+        const int e = tid + i * NTHR;
+        if (i + 1 < R::KI || e < R::NK) {
+            const int r = e / (D / 4), c4 = e - r * (D / 4);
+            unsigned h0, l0, h1, l1;
+            split_pair(kx[i][0], kx[i][1], h0, l0);
+            split_pair(kx[i][2], kx[i][3], h1, l1);
+            *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R::VI; ++i) {
+        const int e = tid + i * NTHR;
+        if (i + 1 < R::VI || e < R::NV) {
+            const int c4 = e / (R::TK / 4), rq = e - c4 * (R::TK / 4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                unsigned h0, l0, h1, l1;
+                split_pair(vx[i][0][u], vx[i][1][u], h0, l0);
+                split_pair(vx[i][2][u], vx[i][3][u], h1, l1);
+                const int d = 4 * c4 + u;
+                *reinterpret_cast<uint2*>(&t.vh[d * T::VP + 4 * rq]) = make_uint2(h0, h1);
+                *reinterpret_cast<uint2*>(&t.vl[d * T::VP + 4 * rq]) = make_uint2(l0, l1);
+            }
+        }
+    }
+}
+
 // Workgroup: KV head blockIdx.y, query tokens [i0, i0 + 16*NB) of its G query heads.  Wave:
 // 16 tokens (sub-block sb) x HPW query heads (head group hg), so each K/V fragment read from
 // LDS feeds HPW heads' MFMAs.  Tiles [tile0, tile0 + n_tiles) of the layer are in `ws`.
-template <int D, int G, int NB, int HPW, int ORDER = 0>
+template <int D, int G, int NB, int HPW, bool DIRECT = false>
 __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(PrefillArgs a,
                                                                             const uint4* ws,
-                                                                            int tile0, int n_tiles) {
+                                                                            int tile0, int n_tiles,
+                                                                            int ksplit) {
     using T = TileLds<D>;
     constexpr int HG = G / HPW;
     constexpr int NTHR = HG * NB * 64;
@@ -317,19 +391,15 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int col = lane & 15, grp = lane >> 4;
     const int nblk = (a.P + 16 * NB - 1) / (16 * NB);
-    int kvh, blk;
-    if constexpr (ORDER == 0) {
-        kvh = blockIdx.y;
-        blk = nblk - 1 - (int)blockIdx.x;            // heavy (late) query blocks first
-    } else {
-        // 1-D grid of nblk*Hkv items ranked by key count (rank r: block nblk-1-r/Hkv, head
-        // r%Hkv).  The first half of the grid takes ranks heaviest-first, the second half
-        // lightest-first, so the two workgroups a CU holds at once carry about equal total work.
-        const int n = nblk * a.Hkv, L = (int)blockIdx.x, half = (n + 1) / 2;
-        const int r = L < half ? L : n - 1 - (L - half);
-        kvh = r % a.Hkv;
-        blk = nblk - 1 - r / a.Hkv;
-    }
+    // Grid x: nblk*Hkv items ranked by key count (rank r: block nblk-1-r/Hkv, head r%Hkv).
+    // The first half of the grid takes ranks heaviest-first, the second half lightest-first,
+    // so the two workgroups a CU holds at once carry about equal total work.  Grid y: split
+    // of the item's key tiles (ksplit > 1 writes partials for prefill_combine_kernel).
+    const int n_items = nblk * a.Hkv, L = (int)blockIdx.x, half = (n_items + 1) / 2;
+    const int rank = L < half ? L : n_items - 1 - (L - half);
+    const int kvh = rank % a.Hkv;
+    const int blk = nblk - 1 - rank / a.Hkv;
+    const int ks = blockIdx.y;
     const int i0 = blk * 16 * NB;
     const int sb = wave / HG, hg = wave - sb * HG;
     const int qi = i0 + 16 * sb + col;
@@ -346,13 +416,19 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
     const int last_tok = min(i0 + 16 * NB, a.P) - 1;
     const int kend = a.pos0 + last_tok + 1;
     const int kbeg = a.window > 0 ? max(0, a.pos0 + i0 - a.window + 1) : 0;
-    const int t_first = kbeg / TK, t_last = (kend - 1) / TK;
+    const int t_all0 = kbeg / TK, t_all1 = (kend - 1) / TK;
+    const int per = (t_all1 - t_all0 + ksplit) / ksplit;            // tiles per split
+    const int t_first = t_all0 + ks * per, t_last = min(t_all1, t_first + per - 1);
     const int w_lo = a.pos0 + i0 + 16 * sb;           // first query position of the wave
     const bool w_full = i0 + 16 * sb + 15 < a.P;
     const int w_start_max = a.window > 0 ? max(0, w_lo + 15 - a.window + 1) : 0;
 
     const uint4* img = ws + (size_t)kvh * n_tiles * IMG;
-    u32x4 stage[PER];
+    const float* kplane = a.kc + (long long)kvh * a.head_stride;
+    const float* vplane = a.vc + (long long)kvh * a.head_stride;
+    using RT = RawTile<D, NTHR>;
+    u32x4 stage[DIRECT ? 1 : PER];
+    floatx4 kx[RT::KI], vx[RT::VI][4];   // used by DIRECT staging only
     floatx4 o[HPW][DT];
     float m[HPW], l[HPW];
 #pragma unroll
@@ -363,11 +439,20 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
         l[hh] = 0.0f;
     }
 
-    img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
-    img_store<PER, NTHR, IMG>(stage, &buf[0], tid);
-    if (t_first + 1 <= t_last)
-        img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first + 1 - tile0) * IMG, tid);
-    __syncthreads();
+    if (t_first <= t_last) {   // a split past the item's last tile has no keys (neutral partial)
+        if constexpr (DIRECT) {
+            raw_load<D, NTHR, RT::KI, RT::VI>(kx, vx, kplane, vplane, t_first * TK, kend - 1, tid);
+            raw_store<D, NTHR, RT::KI, RT::VI>(kx, vx, buf[0], tid);
+            if (t_first + 1 <= t_last)
+                raw_load<D, NTHR, RT::KI, RT::VI>(kx, vx, kplane, vplane, (t_first + 1) * TK, kend - 1, tid);
+        } else {
+            img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
+            img_store<PER, NTHR, IMG>(stage, &buf[0], tid);
+            if (t_first + 1 <= t_last)
+                img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first + 1 - tile0) * IMG, tid);
+        }
+        __syncthreads();
+    }
     for (int tile = t_first; tile <= t_last; ++tile) {
         const T& t = buf[(tile - t_first) & 1];
         const int t0 = tile * TK;
@@ -477,9 +562,15 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
         // Next buffer: tile+1 (already in registers) to LDS, tile+2 loads in flight.  The
         // buffer written here was last read before the previous iteration's barrier.
         if (tile + 1 <= t_last) {
-            img_store<PER, NTHR, IMG>(stage, &buf[(tile + 1 - t_first) & 1], tid);
-            if (tile + 2 <= t_last)
-                img_load<PER, NTHR, IMG>(stage, img + (size_t)(tile + 2 - tile0) * IMG, tid);
+            if constexpr (DIRECT) {
+                raw_store<D, NTHR, RT::KI, RT::VI>(kx, vx, buf[(tile + 1 - t_first) & 1], tid);
+                if (tile + 2 <= t_last)
+                    raw_load<D, NTHR, RT::KI, RT::VI>(kx, vx, kplane, vplane, (tile + 2) * TK, kend - 1, tid);
+            } else {
+                img_store<PER, NTHR, IMG>(stage, &buf[(tile + 1 - t_first) & 1], tid);
+                if (tile + 2 <= t_last)
+                    img_load<PER, NTHR, IMG>(stage, img + (size_t)(tile + 2 - tile0) * IMG, tid);
+            }
         }
         __syncthreads();
     }
@@ -487,7 +578,16 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
     for (int hh = 0; hh < HPW; ++hh) {
         float lt = l[hh] + __shfl_xor(l[hh], 16);
         lt = lt + __shfl_xor(lt, 32);
-        if (q_ok) {
+        if (q_ok && ksplit > 1) {
+            // Unnormalised partial of split ks: o for this lane's dims, (max, sum) per row.
+            const int hq = kvh * G + hg * HPW + hh;
+            const long long slot = ((long long)ks * a.P + qi) * a.Hq + hq;
+#pragma unroll
+            for (int d = 0; d < DT; ++d)
+                *reinterpret_cast<float4*>(a.part_o + slot * D + d * 16 + 4 * grp) =
+                    make_float4(o[hh][d][0], o[hh][d][1], o[hh][d][2], o[hh][d][3]);
+            if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * slot) = make_float2(m[hh], lt);
+        } else if (q_ok) {
             const int hq = kvh * G + hg * HPW + hh;
             const long long row = (long long)qi * a.Hq * D + (long long)hq * D;
             float* op = a.out + row;
@@ -503,6 +603,43 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
             }
         }
     }
+}
+
+
+// ---- 4. Split-K combine -------------------------------------------------------------------------
+// One thread per float4 column of one (token, query head) row: the log-sum-exp merge of the
+// ksplit partials (as decode_reduce_kernel does), then sinks and the output gate.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a, int ksplit) {
+    constexpr int NC = D / 4;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long rows = (long long)a.P * a.Hq;
+    if (idx >= rows * NC) return;
+    const long long row = idx / NC;                 // token * Hq + head
+    const int c = (int)(idx - row * NC);
+    const int hq = (int)(row % a.Hq);
+    float m = kNegBig, l = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < ksplit; ++s) {
+        const long long slot = (long long)s * rows + row;
+        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * slot);
+        const float4 x = reinterpret_cast<const float4*>(a.part_o + slot * D)[c];
+        const float mn = fmaxf(m, ml.x);
+        const float so = dk::fast_exp2(m - mn), sx = dk::fast_exp2(ml.x - mn);
+        l = __builtin_fmaf(l, so, ml.y * sx);
+        o.x = __builtin_fmaf(o.x, so, x.x * sx);
+        o.y = __builtin_fmaf(o.y, so, x.y * sx);
+        o.z = __builtin_fmaf(o.z, so, x.z * sx);
+        o.w = __builtin_fmaf(o.w, so, x.w * sx);
+        m = mn;
+    }
+    const long long g0 = row * D + 4 * c;
+    float4 r;
+    r.x = dk::finish_output(m, l, o.x, a.sinks, a.gate, hq, g0);
+    r.y = dk::finish_output(m, l, o.y, a.sinks, a.gate, hq, g0 + 1);
+    r.z = dk::finish_output(m, l, o.z, a.sinks, a.gate, hq, g0 + 2);
+    r.w = dk::finish_output(m, l, o.w, a.sinks, a.gate, hq, g0 + 3);
+    reinterpret_cast<float4*>(a.out + row * D)[c] = r;
 }
 
 }  // namespace pk

@@ -127,3 +127,29 @@ def test_prefill_error_codes():
         assert _lib.status("llmp_attn_prefill", h, 0, 0, 0, b, b, b, b, 0) == 2    # no tokens
         assert _lib.status("llmp_attn_prefill", h, 1, 0, 4, b, b, b, b, 0) == 2    # bad layer
         assert _lib.status("llmp_attn_prefill", h, 0, 0, 4, b, b, b, b + 4, 0) == 1  # misaligned out
+
+
+# ------------------------------------- short chunks after a long prefix (split-K over key tiles)
+@pytest.mark.parametrize("P", [1, 4, 8, 16])
+def test_speculative_verification_shape_c3(P):
+    """K draft tokens verified in one call after a 4000-token prefix (LLMEngine.java:1019-1033
+    runs them as K sequential forwards); the launch splits the prefix's key tiles."""
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    _run_prefill_case(c, 4000 + P + 2, 0, 4000, P, seed=900 + P, k_scale=0.5, decode_steps=2,
+                      what=f"spec-verify C3 P={P} after 4000")
+
+
+def test_chunked_prefill_after_long_prefix_c5():
+    c = hfp.ModelConfig(32, 8, 64, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=500000.0)
+    _run_prefill_case(c, 8200, 0, 8000, 100, seed=901, decode_steps=1,
+                      what="C5 shape: 100 tokens after 8000")
+
+
+def test_chunk_after_prefix_with_window_and_qknorm():
+    c = hfp.ModelConfig(4, 1, 256, 6, architecture=hfp.ARCH_GEMMA3, rope_freq_base=1e6,
+                        norm_eps=1e-6, sliding_window=512)
+    rng = np.random.default_rng(902)
+    qk = (rng.uniform(0.5, 1.5, 256).astype(np.float32), rng.uniform(0.5, 1.5, 256).astype(np.float32))
+    for layer in (0, 5):   # local (window 512) and global
+        _run_prefill_case(c, 3100, layer, 3000, 64, seed=903 + layer, qk=qk, decode_steps=1,
+                          what=f"gemma3 chunk after 3000, layer {layer}")
