@@ -385,6 +385,8 @@ def main() -> int:
                          "(no graph replay, no second context, no CPU baseline), then exit")
     ap.add_argument("--kv", choices=("f32", "q8"), default="f32",
                     help="KV cache of --profile-workload")
+    ap.add_argument("--profile-verify", type=int, default=0, metavar="K",
+                    help="for rocprofv3: speculative verification of K tokens at --ctx, then exit")
     ap.add_argument("--profile-prefill", type=int, default=0, metavar="P",
                     help="for rocprofv3: C5 prefill of P tokens (K graph + K eager calls), then exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -408,6 +410,10 @@ def main() -> int:
                                 int(args.rotate_gib * 2**30), q8=args.kv == "q8")
     if args.profile_prefill:
         return profile_prefill(args.profile_prefill, args.steps)
+    if args.profile_verify:
+        r = verify_run(args.ctx, args.profile_verify, args.steps, int(args.rotate_gib * 2**30))
+        log(f"[bench] profile verify: {r}")
+        return 0
     info = hfp.device_info()
     log(f"[bench] device {info['arch']} with {info['n_cu']} CUs")
     rot = int(args.rotate_gib * 2**30)

@@ -64,9 +64,8 @@ hipError_t launch_attn_d(const pk::PrefillArgs& a, int group, const uint4* ws, i
 
 template <int D>
 hipError_t launch_combine_d(const pk::PrefillArgs& a, int ksplit, hipStream_t stream) {
-    const long long threads = (long long)a.P * a.Hq * (D / 4);
-    hipLaunchKernelGGL((pk::prefill_combine_kernel<D>), dim3((unsigned)((threads + 255) / 256)),
-                       dim3(256), 0, stream, a, ksplit);
+    hipLaunchKernelGGL((pk::prefill_combine_kernel<D>), dim3((unsigned)(a.P * a.Hq)),
+                       dim3(pk::kCombineThreads), 0, stream, a, ksplit);
     return hipGetLastError();
 }
 

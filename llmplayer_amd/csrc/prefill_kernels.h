@@ -152,8 +152,9 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     const float* vplane = a.vc + (long long)kvh * a.head_stride;
     // K rows: work item (row r, dims 4*c4 .. 4*c4+3), c4 fastest across lanes, so the loads
     // are row-contiguous and the 8-byte stores of 16 lanes cover the 32 banks once.
-    // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), rq fastest across lanes: each
-    // dim row gets the 4 keys as one 8-byte store, and 16 lanes' stores cover the 32 banks.
+    // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), c4 fastest across lanes so
+    // that each load instruction reads whole rows; each dim row gets the 4 keys as one 8-byte
+    // store.
     // Every global load of a thread is issued before any of its math (one memory round trip).
     constexpr int KI = TK * (D / 4) / NTHR, VI = (TK / 4) * (D / 4) / NTHR;
     static_assert(KI * NTHR == TK * (D / 4) && VI * NTHR == (TK / 4) * (D / 4),
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
         const int e = tid + i * NTHR;
-        const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
+        const int rq = e / (D / 4), c4 = e - rq * (D / 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             vx[i][j] = reinterpret_cast<const float4*>(
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
         const int e = tid + i * NTHR;
-        const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
+        const int rq = e / (D / 4), c4 = e - rq * (D / 4);
         const float vv[4][4] = {{vx[i][0].x, vx[i][0].y, vx[i][0].z, vx[i][0].w},
                                 {vx[i][1].x, vx[i][1].y, vx[i][1].z, vx[i][1].w},
                                 {vx[i][2].x, vx[i][2].y, vx[i][2].z, vx[i][2].w},
@@ -302,8 +303,8 @@ __device__ __forceinline__ void img_store(const u32x4 (&stage)[PER], void* dst, 
 
 // Direct staging from the fp32 cache (short prompts after a long prefix, where each key tile
 // feeds only a few workgroups and building images first would re-convert the whole prefix on
-// every call).  K: items (row, 4-dim chunk) with the chunk fastest; V: items (4 keys, 4-dim
-// chunk) with the keys fastest, stored transposed as 8-byte runs.  Rows at or past row_lim
+// every call).  K: items (row, 4-dim chunk); V: items (4 keys, 4-dim chunk), stored transposed
+// as 8-byte runs; the chunk index runs fastest across lanes so every load reads whole rows.  Rows at or past row_lim
 // repeat row row_lim (never attended, finite).
 template <int D, int NTHR>
 struct RawTile {
@@ -327,7 +328,7 @@ __device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4]
 #pragma unroll
     for (int i = 0; i < R::VI; ++i) {
         const int e = min(tid + i * NTHR, R::NV - 1);
-        const int c4 = e / (R::TK / 4), rq = e - c4 * (R::TK / 4);
+        const int rq = e / (D / 4), c4 = e - rq * (D / 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             vx[i][j] = reinterpret_cast<const floatx4*>(
@@ -357,7 +358,7 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
     for (int i = 0; i < R::VI; ++i) {
         const int e = tid + i * NTHR;
         if (i + 1 < R::VI || e < R::NV) {
-            const int c4 = e / (R::TK / 4), rq = e - c4 * (R::TK / 4);
+            const int rq = e / (D / 4), c4 = e - rq * (D / 4);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 unsigned h0, l0, h1, l1;
@@ -607,20 +608,26 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
 
 
 // ---- 4. Split-K combine -------------------------------------------------------------------------
-// One thread per float4 column of one (token, query head) row: the log-sum-exp merge of the
-// ksplit partials (as decode_reduce_kernel does), then sinks and the output gate.
+// One block per (token, query head) row.  Thread (column c, split group p) owns float4 column
+// c of the row for the splits p, p + NP, ...; its loads are independent of the running max,
+// so they are all in flight together.  The NP group results merge through LDS, then sinks and
+// the output gate apply (the same merge as decode_reduce_kernel).
+constexpr int kCombineThreads = 256;
+
 template <int D>
-__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a, int ksplit) {
-    constexpr int NC = D / 4;
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+__global__ __launch_bounds__(kCombineThreads) void prefill_combine_kernel(PrefillArgs a,
+                                                                          int ksplit) {
+    constexpr int NC = D / 4, NP = kCombineThreads / NC;
+    __shared__ float s_m[NP], s_l[NP];
+    __shared__ float4 s_o[NP][NC];
     const long long rows = (long long)a.P * a.Hq;
-    if (idx >= rows * NC) return;
-    const long long row = idx / NC;                 // token * Hq + head
-    const int c = (int)(idx - row * NC);
+    const long long row = blockIdx.x;                 // token * Hq + head
+    const int tid = threadIdx.x, c = tid % NC, p = tid / NC;
     const int hq = (int)(row % a.Hq);
     float m = kNegBig, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < ksplit; ++s) {
+#pragma unroll 4
+    for (int s = p; s < ksplit; s += NP) {
         const long long slot = (long long)s * rows + row;
         const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + 2 * slot);
         const float4 x = reinterpret_cast<const float4*>(a.part_o + slot * D)[c];
@@ -633,13 +640,34 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a, int
         o.w = __builtin_fmaf(o.w, so, x.w * sx);
         m = mn;
     }
-    const long long g0 = row * D + 4 * c;
-    float4 r;
-    r.x = dk::finish_output(m, l, o.x, a.sinks, a.gate, hq, g0);
-    r.y = dk::finish_output(m, l, o.y, a.sinks, a.gate, hq, g0 + 1);
-    r.z = dk::finish_output(m, l, o.z, a.sinks, a.gate, hq, g0 + 2);
-    r.w = dk::finish_output(m, l, o.w, a.sinks, a.gate, hq, g0 + 3);
-    reinterpret_cast<float4*>(a.out + row * D)[c] = r;
+    if (c == 0) {
+        s_m[p] = m;
+        s_l[p] = l;
+    }
+    s_o[p][c] = o;
+    __syncthreads();
+    if (p == 0) {
+        float M = s_m[0];
+        for (int q = 1; q < NP; ++q) M = fmaxf(M, s_m[q]);
+        float L = 0.0f;
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < NP; ++q) {
+            const float sc = dk::fast_exp2(s_m[q] - M);
+            L = __builtin_fmaf(s_l[q], sc, L);
+            const float4 x = s_o[q][c];
+            O.x = __builtin_fmaf(x.x, sc, O.x);
+            O.y = __builtin_fmaf(x.y, sc, O.y);
+            O.z = __builtin_fmaf(x.z, sc, O.z);
+            O.w = __builtin_fmaf(x.w, sc, O.w);
+        }
+        const long long g0 = row * D + 4 * c;
+        float4 r;
+        r.x = dk::finish_output(M, L, O.x, a.sinks, a.gate, hq, g0);
+        r.y = dk::finish_output(M, L, O.y, a.sinks, a.gate, hq, g0 + 1);
+        r.z = dk::finish_output(M, L, O.z, a.sinks, a.gate, hq, g0 + 2);
+        r.w = dk::finish_output(M, L, O.w, a.sinks, a.gate, hq, g0 + 3);
+        reinterpret_cast<float4*>(a.out + row * D)[c] = r;
+    }
 }
 
 }  // namespace pk
