@@ -67,6 +67,28 @@ __device__ __forceinline__ float row_group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// One step of a cross-lane reduction over the lanes of equal residue mod OFF (OFF a power of
+// two, 4..32), all in VGPRs: offsets 16 and 32 exchange whole rows / half-waves with the
+// gfx950 permlane swaps (the pair's two values come back in both lanes, combined in the same
+// order there); smaller offsets rotate the 16-lane row by OFF with DPP, which pairs lanes of
+// the same residue, so steps OFF, 2*OFF, ..., 8 leave the residue class's total in every lane.
+template <int OFF, bool MAX>
+__device__ __forceinline__ float lane_step(float x) {
+    static_assert(OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "offset 4, 8, 16 or 32");
+    float a, b;
+    if constexpr (OFF >= 16) {
+        const unsigned u = __builtin_bit_cast(unsigned, x);
+        const auto r = OFF == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                                 : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        a = __builtin_bit_cast(float, (unsigned)r[0]);
+        b = __builtin_bit_cast(float, (unsigned)r[1]);
+    } else {
+        a = x;
+        b = dpp<0x120 + OFF>(x);  // row_ror:OFF
+    }
+    return MAX ? fmaxf(a, b) : a + b;
+}
+
 // Final normalisation of one output element of query head hq from its merged (max M,
 // sum L, unnormalised O) in the log2 domain: an attention sink (log2-domain logit) joins the
 // max and the sum with no value (softmaxWithSink, Qwen3MoEInferenceEngine.java:562-575), then
@@ -613,17 +635,20 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         float mw = m[h];
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off));
+        if constexpr (LPR <= 4) mw = lane_step<4, true>(mw);
+        if constexpr (LPR <= 8) mw = lane_step<8, true>(mw);
+        mw = lane_step<32, true>(lane_step<16, true>(mw));
         const float sc = fast_exp2(m[h] - mw);
         float lw = l[h] * sc;
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1) lw = lw + __shfl_xor(lw, off);
+        if constexpr (LPR <= 4) lw = lane_step<4, false>(lw);
+        if constexpr (LPR <= 8) lw = lane_step<8, false>(lw);
+        lw = lane_step<32, false>(lane_step<16, false>(lw));
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             float x = o[h][e] * sc;
-#pragma unroll
-            for (int off = LPR; off < 64; off <<= 1) x = x + __shfl_xor(x, off);
+            if constexpr (LPR <= 4) x = lane_step<4, false>(x);
+            if constexpr (LPR <= 8) x = lane_step<8, false>(x);
+            x = lane_step<32, false>(lane_step<16, false>(x));
             o[h][e] = x;
         }
         m[h] = mw;
