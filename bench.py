@@ -139,14 +139,15 @@ def gpu_run(ctx: int, steps: int, warmup: int, splits: int, rotate_bytes: int,
             "split_launches": res["split"][0], "plan": plan}
 
 
-def prefill_run(P: int, steps: int) -> dict:
+def prefill_run(P: int, steps: int, q8: bool = False) -> dict:
     """C5: prefill attention of P prompt tokens (Llama-3.2-1B shape 32/8/64, bf16 Q/K/V
-    N(0,1), causal) in one llmp_attn_prefill call (exact K/V append + MFMA attention).
-    Timed as a graph replay of `steps` calls; per-kernel means from an eager profiled pass."""
+    N(0,1), causal) in one llmp_attn_prefill call (exact K/V append + MFMA attention), over
+    an fp32 or a Q8_0 cache.  Timed as a graph replay of `steps` calls; per-kernel means from
+    an eager profiled pass."""
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
     c = hfp.ModelConfig(32, 8, 64, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
-    fp = hfp.HipForwardPass(c, P)
+    fp = hfp.HipForwardPass(c, P, kv_dtype=_lib.LLMP_KV_Q8_0 if q8 else _lib.LLMP_KV_F32)
     bufs = []
     try:
         rng = np.random.default_rng(5)
@@ -205,20 +206,21 @@ def prefill_run(P: int, steps: int) -> dict:
             "mfma_tflops_bf16x3": round(3 * flops / (res["attn"] * 1e-6) / 1e12, 2)}
 
 
-def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int) -> dict:
+def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int, q8: bool = False) -> dict:
     """Speculative verification at the C3 shape: K draft tokens at positions ctx-K..ctx-1 in
-    one llmp_attn_prefill call over a (ctx-K)-row cache (the reference runs K sequential
-    forwards, LLMEngine.java:1019-1033).  Layer caches rotate over >= 2 GiB; graph replay."""
+    one llmp_attn_prefill call over a (ctx-K)-row fp32 or Q8_0 cache (the reference runs K
+    sequential forwards, LLMEngine.java:1019-1033).  Layer caches rotate over >= 2 GiB; graph
+    replay."""
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
-    per_layer = kv_bytes(ctx)
+    per_layer = kv_bytes(ctx, q8)
     n_layers = max(1, math.ceil(rotate_bytes / per_layer))
     c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
-    fp = hfp.HipForwardPass(c, ctx)
+    fp = hfp.HipForwardPass(c, ctx, kv_dtype=_lib.LLMP_KV_Q8_0 if q8 else _lib.LLMP_KV_F32)
     bufs = []
     try:
         rng = np.random.default_rng(7)
-        fill_caches(fp, c, ctx - K + 1, n_layers, False, rng)
+        fill_caches(fp, c, ctx - K + 1, n_layers, q8, rng)
         arrs = [hfp.to_bf16(rng.standard_normal((K, n), dtype=np.float32))
                 for n in (c.q_dim, c.kv_dim, c.kv_dim)]
         for arr in arrs:
@@ -258,7 +260,7 @@ def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int) -> dict:
         fp.close()
     us = ms.value / steps * 1e3
     return {"K": K, "ctx": ctx, "us_per_call": round(us, 2),
-            "kv_read_gbps": round(kv_bytes(ctx - K) / (us * 1e-6) / 1e9, 1)}
+            "kv_read_gbps": round(kv_bytes(ctx - K, q8) / (us * 1e-6) / 1e9, 1)}
 
 
 def cpu_baseline(ctx: int, seconds: float) -> dict:
@@ -451,6 +453,21 @@ def main() -> int:
             log(f"[bench] prefill C5 P={P}: {r['us_per_call']:.1f} us/call, attention kernel "
                 f"{r['attn_kernel_us']:.1f} us ({r['attn_kernel_causal_tflops']:.1f} causal TFLOP/s)")
             prefill.append(r)
+
+    # Prefill and verification over a Q8_0 cache (quantising append, dequantising staging).
+    q8_prefill = q8_verify = None
+    if args.q8 and args.prefill:
+        q8_prefill = prefill_run(2048, 20, q8=True)
+        log(f"[bench] prefill C5 P=2048 Q8_0: {q8_prefill['us_per_call']:.1f} us/call, attention "
+            f"{q8_prefill['attn_kernel_us']:.1f} us, append {q8_prefill['append_kernel_us']:.1f} us")
+    if args.q8 and args.verify:
+        q8_verify = verify_run(args.ctx, 16, 100, rot, q8=True)
+        q8_dec = [r for r in q8_runs if r["ctx"] == args.ctx]
+        if q8_dec:
+            q8_verify["decode_calls_us"] = round(16 * q8_dec[0]["us_per_layer_call"], 2)
+            q8_verify["speedup_vs_k_decode_calls"] = round(
+                q8_verify["decode_calls_us"] / q8_verify["us_per_call"], 2)
+        log(f"[bench] verify K=16 at ctx {args.ctx} Q8_0: {q8_verify['us_per_call']:.1f} us/call")
     B = kv_bytes(args.ctx)
     achieved = B / (main_run["split_kernel_us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
@@ -517,6 +534,10 @@ def main() -> int:
         line["prefill_c5_llama1b"] = prefill
     if verify:
         line["speculative_verify_c3"] = verify
+    if q8_prefill is not None:
+        line["q8_0_prefill_c5_llama1b"] = q8_prefill
+    if q8_verify is not None:
+        line["q8_0_speculative_verify_c3"] = q8_verify
     print(json.dumps(line), flush=True)
     return 0
 

@@ -221,7 +221,10 @@ int llmp_graph_destroy(uint64_t graph);
  * widened to fp32, QK-norm and RoPE in the CPU path's float order).  Token i attends causally
  * to rows [start(pos0+i), pos0+i] (start from the layer's sliding window), on MFMA with bf16
  * hi/lo split operands and fp32 accumulation.  Rows before pos0 must already be in the cache.
- * NEOX partial RoPE (rotated dims < head_dim) and Q8_0 caches are LLMP_ERR_UNSUPPORTED here.
+ * Over a Q8_0 cache each new row is quantised exactly as a decode append quantises it (under
+ * the handle's contract) and attention reads every row dequantised (quant * block scale), as
+ * the reference's sequential forwards over KVCache Mode.Q8_0 do.
+ * NEOX partial RoPE (rotated dims < head_dim) is LLMP_ERR_UNSUPPORTED here.
  * The handle keeps a workspace for the key tiles a call attends (bf16 hi/lo images of K and
  * V: about 9 bytes per key, KV head and head_dim element); a call that needs more than any
  * earlier call grows it (hipMalloc, so such a call cannot be captured in a graph). */

@@ -221,32 +221,40 @@ __device__ __forceinline__ int round_half_up(float y) {
     return (int)r;
 }
 
-// Q8_0 quantisation of one row of D fp32 values staged in LDS: per 32-value block
-// scale = maxAbs/127, quant = clamp(r(x * (1/scale)), -128, 127), where r rounds half up
-// (KVCache.quantizeBlocksScalar, KVCache.java:218-243) or truncates toward zero when `trunc`
-// is set (SimdQ8KvOps.quantize on 8-lane hosts, SimdQ8KvOps.java:86-117).  Whole workgroup;
+// Q8_0 quantisation (KVCache.quantizeBlocksScalar, KVCache.java:218-243; SimdQ8KvOps.quantize,
+// SimdQ8KvOps.java:86-117): per 32-value block scale = maxAbs/127, and each value becomes
+// clamp(r(x * (1/scale)), -128, 127), where r rounds half up, or truncates toward zero when
+// `trunc` is set (the 8-lane SIMD contract).  A zero block has inverse scale 0.
+__device__ __forceinline__ float q8_block_scale(const float* x) {
+    float mx = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        const float v = x[i];
+        const float av = v >= 0.0f ? v : -v;
+        mx = av > mx ? av : mx;
+    }
+    return mx / 127.0f;
+}
+__device__ __forceinline__ float q8_inv_scale(float scale) {
+    return scale != 0.0f ? 1.0f / scale : 0.0f;
+}
+__device__ __forceinline__ int q8_code(float x, float inv, bool trunc) {
+    const float y = x * inv;
+    int v = trunc ? (int)y : round_half_up(y);   // |y| <= 127.x: the cast is in range
+    return v > 127 ? 127 : (v < -128 ? -128 : v);
+}
+
+// Q8_0 quantisation of one row of D fp32 values staged in LDS, by the whole workgroup;
 // results in LDS (q: D bytes, sc: D/32 floats).
 template <int D, int NTHR>
 __device__ void quantize_row_lds(const float* x, signed char* q, float* sc, float* s_inv, int tid,
                                  bool trunc) {
     for (int b = tid; b < D / 32; b += NTHR) {
-        float mx = 0.0f;
-        for (int i = 0; i < 32; ++i) {
-            const float v = x[32 * b + i];
-            const float av = v >= 0.0f ? v : -v;
-            mx = av > mx ? av : mx;
-        }
-        const float scale = mx / 127.0f;
+        const float scale = q8_block_scale(x + 32 * b);
         sc[b] = scale;
-        s_inv[b] = scale != 0.0f ? 1.0f / scale : 0.0f;
+        s_inv[b] = q8_inv_scale(scale);
     }
     __syncthreads();
-    for (int i = tid; i < D; i += NTHR) {
-        const float y = x[i] * s_inv[i / 32];
-        int v = trunc ? (int)y : round_half_up(y);   // |y| <= 127.x: the cast is in range
-        v = v > 127 ? 127 : (v < -128 ? -128 : v);
-        q[i] = (signed char)v;
-    }
+    for (int i = tid; i < D; i += NTHR) q[i] = (signed char)q8_code(x[i], s_inv[i / 32], trunc);
     __syncthreads();
 }
 

@@ -967,8 +967,6 @@ static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint
     if (!c.configured)
         return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
     if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: null buffer");
-    if (kv->q8())
-        return fail(LLMP_ERR_UNSUPPORTED, "llmp_attn_prefill: Q8_0 cache (decode steps only)");
     if ((q | k | v) & 1 || out & 15 || gate & 3)
         return fail(LLMP_ERR_INVALID_ARG,
                     "llmp_attn_prefill: misaligned q/k/v (2 B), gate (4 B) or out (16 B)");
@@ -977,8 +975,16 @@ static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint
     a.q = reinterpret_cast<const unsigned short*>(q);
     a.k = reinterpret_cast<const unsigned short*>(k);
     a.v = reinterpret_cast<const unsigned short*>(v);
-    a.kc = kv->k_plane(layer);
-    a.vc = kv->v_plane(layer);
+    if (kv->q8()) {
+        a.kq = kv->kq(layer);
+        a.ks = kv->ks(layer);
+        a.vq = kv->vq(layer);
+        a.vs = kv->vs(layer);
+        a.q8_trunc = kv->dtype == LLMP_KV_Q8_0_TRUNC;
+    } else {
+        a.kc = kv->k_plane(layer);
+        a.vc = kv->v_plane(layer);
+    }
     a.head_stride = (long long)kv->max_seq * D;
     if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
         const RopeTable& t = kv->rope[c.rope_sel];

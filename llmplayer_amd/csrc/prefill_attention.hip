@@ -28,7 +28,10 @@ template <int D, int G, int NB>
 hipError_t launch_attn_dgn(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
                            int ksplit, hipStream_t stream) {
     const int items = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
-    if (ksplit > 1)   // few query blocks: stage from the fp32 cache, no tile images
+    if (ksplit > 1 && a.kq != nullptr)   // few query blocks: stage from the cache, no images
+        hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, true, true>), dim3(items, ksplit),
+                           dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
+    else if (ksplit > 1)
         hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, true>), dim3(items, ksplit),
                            dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
     else
@@ -72,14 +75,18 @@ hipError_t launch_combine_d(const pk::PrefillArgs& a, int ksplit, hipStream_t st
 template <int D>
 hipError_t launch_tiles_d(const pk::PrefillArgs& a, uint4* ws, int tile0, int n_tiles,
                           int row_end, hipStream_t stream) {
-    hipLaunchKernelGGL((pk::prefill_tile_kernel<D, kTileThreads>), dim3(n_tiles, a.Hkv),
-                       dim3(kTileThreads), 0, stream, a, ws, tile0, n_tiles, row_end);
+    if (a.kq != nullptr)
+        hipLaunchKernelGGL((pk::prefill_tile_kernel<D, kTileThreads, true>), dim3(n_tiles, a.Hkv),
+                           dim3(kTileThreads), 0, stream, a, ws, tile0, n_tiles, row_end);
+    else
+        hipLaunchKernelGGL((pk::prefill_tile_kernel<D, kTileThreads, false>), dim3(n_tiles, a.Hkv),
+                           dim3(kTileThreads), 0, stream, a, ws, tile0, n_tiles, row_end);
     return hipGetLastError();
 }
 
 template <int D>
 hipError_t launch_append_d(const pk::PrefillArgs& a, hipStream_t stream) {
-    const size_t lds = (size_t)a.Hkv * (D + 9) * sizeof(float);
+    const size_t lds = pk::prefill_append_lds(a.Hkv, D, a.kq != nullptr);
     hipLaunchKernelGGL((pk::prefill_append_kernel<D, kAppendThreads>), dim3(a.P),
                        dim3(kAppendThreads), lds, stream, a);
     return hipGetLastError();

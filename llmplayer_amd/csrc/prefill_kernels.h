@@ -51,9 +51,14 @@ struct PrefillArgs {
     const unsigned short* q;  // bf16 bits [P][Hq*D]
     const unsigned short* k;  // bf16 bits [P][Hkv*D]
     const unsigned short* v;  // bf16 bits [P][Hkv*D]
-    float* kc;                // layer K plane [Hkv][max_seq][D]
+    float* kc;                // fp32 cache: layer K plane [Hkv][max_seq][D]
     float* vc;
-    long long head_stride;    // max_seq*D
+    signed char* kq;          // Q8_0 cache (when set): K quants [Hkv][max_seq][D]
+    float* ks;                // Q8_0 cache: K block scales [Hkv][max_seq][D/32]
+    signed char* vq;
+    float* vs;
+    long long head_stride;    // max_seq*D (elements of one KV head's rows)
+    int q8_trunc;             // Q8_0 append: 1 = truncate (8-lane SIMD contract), 0 = round half up
     const float* cos_t;       // RoPE table [max_seq][half] or nullptr (NoPE)
     const float* sin_t;
     const float* qnw;         // QK-norm weights or nullptr
@@ -75,6 +80,7 @@ __device__ __forceinline__ float bf16_to_f32(unsigned short b) {
     return __uint_as_float((unsigned)b << 16);
 }
 // ---- 1. exact K/V append, one workgroup per token --------------------------------------------
+// LDS floats: Hkv*(D + 9), plus Hkv*D + 2*Hkv*D/32 over a Q8_0 cache (see prefill_append_lds).
 template <int D, int NTHR>
 __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
     extern __shared__ float s_dyn[];
@@ -92,12 +98,51 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
                     a.rope_type};
     if (a.qnw == nullptr) hp.qnw = hp.knw = nullptr;
     dk::prep_heads_lds<D, NTHR>(s_k, a.Hkv, 0, s_acc, s_r, hp, tid);
-    for (int e = tid; e < kvd; e += NTHR) {
-        const int h = e / D, d = e - h * D;
-        const long long off = (long long)h * a.head_stride + (long long)pos * D + d;
-        a.kc[off] = s_k[e];
-        a.vc[off] = bf16_to_f32(a.v[(long long)i * kvd + e]);
+    if (a.kq == nullptr) {
+        for (int e = tid; e < kvd; e += NTHR) {
+            const int h = e / D, d = e - h * D;
+            const long long off = (long long)h * a.head_stride + (long long)pos * D + d;
+            a.kc[off] = s_k[e];
+            a.vc[off] = bf16_to_f32(a.v[(long long)i * kvd + e]);
+        }
+        return;
     }
+    // Q8_0: the K and V rows are quantised block by block exactly like a decode append
+    // (KVCache.storeK/storeV over a Q8_0 cache, KVCache.java:164-179).  Blocks [0, nb) are K's,
+    // [nb, 2nb) V's; 4 consecutive codes are stored as one 32-bit word.
+    float* s_v = s_r + a.Hkv;              // Hkv*D
+    float* s_inv = s_v + kvd;              // 2*Hkv*D/32
+    for (int e = tid; e < kvd; e += NTHR) s_v[e] = bf16_to_f32(a.v[(long long)i * kvd + e]);
+    __syncthreads();
+    const int nb = kvd / 32, bph = D / 32;
+    for (int b = tid; b < 2 * nb; b += NTHR) {
+        const bool is_v = b >= nb;
+        const int bb = is_v ? b - nb : b, h = bb / bph;
+        const float scale = dk::q8_block_scale((is_v ? s_v : s_k) + 32 * bb);
+        s_inv[b] = dk::q8_inv_scale(scale);
+        (is_v ? a.vs : a.ks)[(long long)h * (a.head_stride / 32) + (long long)pos * bph +
+                             (bb - h * bph)] = scale;
+    }
+    __syncthreads();
+    const bool trunc = a.q8_trunc != 0;
+    for (int w = tid; w < 2 * kvd / 4; w += NTHR) {
+        const bool is_v = w >= kvd / 4;
+        const int e = 4 * (is_v ? w - kvd / 4 : w), h = e / D, d = e - h * D;
+        const float* x = (is_v ? s_v : s_k) + e;
+        const float inv = s_inv[(is_v ? nb : 0) + e / 32];
+        unsigned word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            word |= (unsigned)(dk::q8_code(x[j], inv, trunc) & 0xFF) << (8 * j);
+        *reinterpret_cast<unsigned*>((is_v ? a.vq : a.kq) + (long long)h * a.head_stride +
+                                     (long long)pos * D + d) = word;
+    }
+}
+
+// Dynamic LDS bytes of prefill_append_kernel.
+inline size_t prefill_append_lds(int Hkv, int D, bool q8) {
+    const size_t f = (size_t)Hkv * (D + 9) + (q8 ? (size_t)Hkv * D + 2 * (size_t)Hkv * D / 32 : 0);
+    return f * sizeof(float);
 }
 
 // ---- LDS tile layout (also the workspace image of a tile) -------------------------------------
@@ -137,10 +182,60 @@ __device__ __forceinline__ void split_pair(float x, float y, unsigned& hi, unsig
 template <int D>
 constexpr int tile_img_u4() { return (int)(sizeof(TileLds<D>) / 16); }
 
+// One KV head's rows in the cache: fp32 rows (f), or Q8_0 quants (q) and block scales (s).
+struct HeadRows {
+    const float* f;
+    const signed char* q;
+    const float* s;
+};
+template <bool Q8>
+__device__ __forceinline__ HeadRows head_rows(float* f, signed char* q, float* s,
+                                              const PrefillArgs& a, int kvh) {
+    if constexpr (Q8)
+        return {nullptr, q + (long long)kvh * a.head_stride, s + (long long)kvh * (a.head_stride / 32)};
+    else
+        return {f + (long long)kvh * a.head_stride, nullptr, nullptr};
+}
+template <bool Q8>
+__device__ __forceinline__ HeadRows k_rows(const PrefillArgs& a, int kvh) {
+    return head_rows<Q8>(a.kc, a.kq, a.ks, a, kvh);
+}
+template <bool Q8>
+__device__ __forceinline__ HeadRows v_rows(const PrefillArgs& a, int kvh) {
+    return head_rows<Q8>(a.vc, a.vq, a.vs, a, kvh);
+}
+
+// Dims 4*c4 .. 4*c4+3 of row r, as loaded: fp32 values, or for Q8_0 the four quants (one
+// 32-bit word, bit pattern in element 0) and their block's scale (element 1).  chunk_values
+// turns a loaded chunk into fp32 values (quant * scale), so loads can be issued before any
+// of the arithmetic.
+template <int D, bool Q8>
+__device__ __forceinline__ floatx4 load_chunk(const HeadRows& h, int r, int c4) {
+    if constexpr (Q8) {
+        const unsigned w = *reinterpret_cast<const unsigned*>(h.q + (long long)r * D + 4 * c4);
+        return floatx4{__builtin_bit_cast(float, w), h.s[(long long)r * (D / 32) + (c4 >> 3)],
+                       0.0f, 0.0f};
+    } else {
+        return reinterpret_cast<const floatx4*>(h.f + (long long)r * D)[c4];
+    }
+}
+template <bool Q8>
+__device__ __forceinline__ floatx4 chunk_values(floatx4 x) {
+    if constexpr (Q8) {
+        const unsigned w = __builtin_bit_cast(unsigned, x[0]);
+        const float sc = x[1];
+        return floatx4{(float)(signed char)(w & 0xFF) * sc, (float)(signed char)((w >> 8) & 0xFF) * sc,
+                       (float)(signed char)((w >> 16) & 0xFF) * sc, (float)(signed char)(w >> 24) * sc};
+    } else {
+        return x;
+    }
+}
+
 // Image of keys [tau*TK, tau*TK + TK) of KV head blockIdx.y, tau = tile0 + blockIdx.x, at
-// ws[(kvh * n_tiles + blockIdx.x) * tile_img_u4<D>()].  Rows at or past row_end (never attended)
-// repeat row row_end - 1 so that every staged value is finite.
-template <int D, int NTHR>
+// ws[(kvh * n_tiles + blockIdx.x) * tile_img_u4<D>()], from fp32 or (Q8) dequantised Q8_0 rows.
+// Rows at or past row_end (never attended) repeat row row_end - 1 so that every staged value
+// is finite.
+template <int D, int NTHR, bool Q8>
 __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4* ws, int tile0,
                                                             int n_tiles, int row_end) {
     using T = TileLds<D>;
@@ -148,8 +243,7 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     __shared__ T t;
     const int tid = threadIdx.x, kvh = blockIdx.y;
     const int r0 = (tile0 + (int)blockIdx.x) * TK;
-    const float* kplane = a.kc + (long long)kvh * a.head_stride;
-    const float* vplane = a.vc + (long long)kvh * a.head_stride;
+    const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);
     // K rows: work item (row r, dims 4*c4 .. 4*c4+3), c4 fastest across lanes, so the loads
     // are row-contiguous and the 8-byte stores of 16 lanes cover the 32 banks once.
     // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), c4 fastest across lanes so
@@ -159,29 +253,28 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     constexpr int KI = TK * (D / 4) / NTHR, VI = (TK / 4) * (D / 4) / NTHR;
     static_assert(KI * NTHR == TK * (D / 4) && VI * NTHR == (TK / 4) * (D / 4),
                   "tile work must divide evenly over the threads");
-    float4 kx[KI], vx[VI][4];
+    floatx4 kx[KI], vx[VI][4];
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
         const int e = tid + i * NTHR;
         const int r = e / (D / 4), c4 = e - r * (D / 4);
-        kx[i] = reinterpret_cast<const float4*>(kplane + (long long)min(r0 + r, row_end - 1) * D)[c4];
+        kx[i] = load_chunk<D, Q8>(kr, min(r0 + r, row_end - 1), c4);
     }
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
         const int e = tid + i * NTHR;
         const int rq = e / (D / 4), c4 = e - rq * (D / 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            vx[i][j] = reinterpret_cast<const float4*>(
-                vplane + (long long)min(r0 + 4 * rq + j, row_end - 1) * D)[c4];
+        for (int j = 0; j < 4; ++j) vx[i][j] = load_chunk<D, Q8>(vr, min(r0 + 4 * rq + j, row_end - 1), c4);
     }
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
         const int e = tid + i * NTHR;
         const int r = e / (D / 4), c4 = e - r * (D / 4);
+        const floatx4 x = chunk_values<Q8>(kx[i]);
         unsigned h0, l0, h1, l1;
-        split_pair(kx[i].x, kx[i].y, h0, l0);
-        split_pair(kx[i].z, kx[i].w, h1, l1);
+        split_pair(x[0], x[1], h0, l0);
+        split_pair(x[2], x[3], h1, l1);
         *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
         *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
     }
@@ -189,10 +282,8 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     for (int i = 0; i < VI; ++i) {
         const int e = tid + i * NTHR;
         const int rq = e / (D / 4), c4 = e - rq * (D / 4);
-        const float vv[4][4] = {{vx[i][0].x, vx[i][0].y, vx[i][0].z, vx[i][0].w},
-                                {vx[i][1].x, vx[i][1].y, vx[i][1].z, vx[i][1].w},
-                                {vx[i][2].x, vx[i][2].y, vx[i][2].z, vx[i][2].w},
-                                {vx[i][3].x, vx[i][3].y, vx[i][3].z, vx[i][3].w}};   // [key][dim]
+        const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]), chunk_values<Q8>(vx[i][1]),
+                               chunk_values<Q8>(vx[i][2]), chunk_values<Q8>(vx[i][3])};   // [key][dim]
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             unsigned h0, l0, h1, l1;
@@ -313,9 +404,9 @@ struct RawTile {
     static constexpr int KI = (NK + NTHR - 1) / NTHR, VI = (NV + NTHR - 1) / NTHR;
 };
 
-template <int D, int NTHR, int KI, int VI>
+template <int D, int NTHR, int KI, int VI, bool Q8>
 __device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4],
-                                         const float* kplane, const float* vplane, int t0,
+                                         const HeadRows& kr, const HeadRows& vr, int t0,
                                          int row_lim, int tid) {
     using R = RawTile<D, NTHR>;
     static_assert(KI == R::KI && VI == R::VI, "staging register counts");
@@ -323,20 +414,18 @@ __device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4]
     for (int i = 0; i < R::KI; ++i) {
         const int e = min(tid + i * NTHR, R::NK - 1);
         const int r = e / (D / 4), c4 = e - r * (D / 4);
-        kx[i] = reinterpret_cast<const floatx4*>(kplane + (long long)min(t0 + r, row_lim) * D)[c4];
+        kx[i] = load_chunk<D, Q8>(kr, min(t0 + r, row_lim), c4);
     }
 #pragma unroll
     for (int i = 0; i < R::VI; ++i) {
         const int e = min(tid + i * NTHR, R::NV - 1);
         const int rq = e / (D / 4), c4 = e - rq * (D / 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            vx[i][j] = reinterpret_cast<const floatx4*>(
-                vplane + (long long)min(t0 + 4 * rq + j, row_lim) * D)[c4];
+        for (int j = 0; j < 4; ++j) vx[i][j] = load_chunk<D, Q8>(vr, min(t0 + 4 * rq + j, row_lim), c4);
     }
 }
 
-template <int D, int NTHR, int KI, int VI>
+template <int D, int NTHR, int KI, int VI, bool Q8>
 __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4 (&vx)[VI][4],
                                           TileLds<D>& t, int tid) {
     using R = RawTile<D, NTHR>;
@@ -347,9 +436,10 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
         const int e = tid + i * NTHR;
         if (i + 1 < R::KI || e < R::NK) {
             const int r = e / (D / 4), c4 = e - r * (D / 4);
+            const floatx4 x = chunk_values<Q8>(kx[i]);
             unsigned h0, l0, h1, l1;
-            split_pair(kx[i][0], kx[i][1], h0, l0);
-            split_pair(kx[i][2], kx[i][3], h1, l1);
+            split_pair(x[0], x[1], h0, l0);
+            split_pair(x[2], x[3], h1, l1);
             *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
             *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
         }
@@ -359,11 +449,13 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
         const int e = tid + i * NTHR;
         if (i + 1 < R::VI || e < R::NV) {
             const int rq = e / (D / 4), c4 = e - rq * (D / 4);
+            const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]), chunk_values<Q8>(vx[i][1]),
+                                   chunk_values<Q8>(vx[i][2]), chunk_values<Q8>(vx[i][3])};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 unsigned h0, l0, h1, l1;
-                split_pair(vx[i][0][u], vx[i][1][u], h0, l0);
-                split_pair(vx[i][2][u], vx[i][3][u], h1, l1);
+                split_pair(vv[0][u], vv[1][u], h0, l0);
+                split_pair(vv[2][u], vv[3][u], h1, l1);
                 const int d = 4 * c4 + u;
                 *reinterpret_cast<uint2*>(&t.vh[d * T::VP + 4 * rq]) = make_uint2(h0, h1);
                 *reinterpret_cast<uint2*>(&t.vl[d * T::VP + 4 * rq]) = make_uint2(l0, l1);
@@ -375,7 +467,7 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
 // Workgroup: KV head blockIdx.y, query tokens [i0, i0 + 16*NB) of its G query heads.  Wave:
 // 16 tokens (sub-block sb) x HPW query heads (head group hg), so each K/V fragment read from
 // LDS feeds HPW heads' MFMAs.  Tiles [tile0, tile0 + n_tiles) of the layer are in `ws`.
-template <int D, int G, int NB, int HPW, bool DIRECT = false>
+template <int D, int G, int NB, int HPW, bool DIRECT = false, bool Q8 = false>
 __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(PrefillArgs a,
                                                                             const uint4* ws,
                                                                             int tile0, int n_tiles,
@@ -425,8 +517,7 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
     const int w_start_max = a.window > 0 ? max(0, w_lo + 15 - a.window + 1) : 0;
 
     const uint4* img = ws + (size_t)kvh * n_tiles * IMG;
-    const float* kplane = a.kc + (long long)kvh * a.head_stride;
-    const float* vplane = a.vc + (long long)kvh * a.head_stride;
+    const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);   // DIRECT staging
     using RT = RawTile<D, NTHR>;
     u32x4 stage[DIRECT ? 1 : PER];
     floatx4 kx[RT::KI], vx[RT::VI][4];   // used by DIRECT staging only
@@ -442,10 +533,10 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
 
     if (t_first <= t_last) {   // a split past the item's last tile has no keys (neutral partial)
         if constexpr (DIRECT) {
-            raw_load<D, NTHR, RT::KI, RT::VI>(kx, vx, kplane, vplane, t_first * TK, kend - 1, tid);
-            raw_store<D, NTHR, RT::KI, RT::VI>(kx, vx, buf[0], tid);
+            raw_load<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, kr, vr, t_first * TK, kend - 1, tid);
+            raw_store<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, buf[0], tid);
             if (t_first + 1 <= t_last)
-                raw_load<D, NTHR, RT::KI, RT::VI>(kx, vx, kplane, vplane, (t_first + 1) * TK, kend - 1, tid);
+                raw_load<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, kr, vr, (t_first + 1) * TK, kend - 1, tid);
         } else {
             img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
             img_store<PER, NTHR, IMG>(stage, &buf[0], tid);
@@ -564,9 +655,9 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
         // buffer written here was last read before the previous iteration's barrier.
         if (tile + 1 <= t_last) {
             if constexpr (DIRECT) {
-                raw_store<D, NTHR, RT::KI, RT::VI>(kx, vx, buf[(tile + 1 - t_first) & 1], tid);
+                raw_store<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, buf[(tile + 1 - t_first) & 1], tid);
                 if (tile + 2 <= t_last)
-                    raw_load<D, NTHR, RT::KI, RT::VI>(kx, vx, kplane, vplane, (tile + 2) * TK, kend - 1, tid);
+                    raw_load<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, kr, vr, (tile + 2) * TK, kend - 1, tid);
             } else {
                 img_store<PER, NTHR, IMG>(stage, &buf[(tile + 1 - t_first) & 1], tid);
                 if (tile + 2 <= t_last)

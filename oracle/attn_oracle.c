@@ -564,6 +564,33 @@ void orc_prefill_sequential(const orc_cfg *c, float *kcache, float *vcache,
     free(att);
 }
 
+/* The same P sequential single-token forwards over a Q8_0 cache (KVCache Mode.Q8_0): each
+ * token's K/V rows are quantised as they are appended (KVCache.storeK/storeV) and later
+ * tokens attend to the quantised rows.  q8_mode selects the JVM's contract. */
+void orc_prefill_sequential_q8(const orc_cfg *c, int8_t *kq, float *ks, int8_t *vq, float *vs,
+                               const float *qnorm_w, const float *knorm_w,
+                               const float *rope_cos, const float *rope_sin,
+                               const float *q, const float *k, const float *v,
+                               int layer, int pos0, int n_tokens, float *out, int n_threads,
+                               int q8_mode)
+{
+    const int qdim = c->n_heads * c->head_size;
+    const int kv_dim = c->n_kv_heads * c->head_size;
+    float *qb = (float *)malloc(sizeof(float) * (size_t)qdim);
+    float *kb = (float *)malloc(sizeof(float) * (size_t)kv_dim);
+    float *att = (float *)malloc(sizeof(float) * (size_t)c->n_heads * (size_t)(pos0 + n_tokens));
+    for (int i = 0; i < n_tokens; i++) {
+        memcpy(qb, q + (size_t)i * qdim, sizeof(float) * (size_t)qdim);
+        memcpy(kb, k + (size_t)i * kv_dim, sizeof(float) * (size_t)kv_dim);
+        orc_forward_from_projections_q8(c, kq, ks, vq, vs, qnorm_w, knorm_w, rope_cos, rope_sin,
+                                        qb, kb, v + (size_t)i * kv_dim, layer, pos0 + i,
+                                        out + (size_t)i * qdim, att, 0, n_threads, q8_mode);
+    }
+    free(qb);
+    free(kb);
+    free(att);
+}
+
 int orc_max_threads(void)
 {
 #ifdef _OPENMP

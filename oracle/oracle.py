@@ -119,6 +119,9 @@ def lib():
         L.orc_forward_from_projections_q8.argtypes = [
             C.POINTER(_Cfg), _I8, _F, _I8, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int, _F,
             _F, C.c_int, C.c_int, C.c_int]
+        L.orc_prefill_sequential_q8.argtypes = [
+            C.POINTER(_Cfg), _I8, _F, _I8, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int,
+            C.c_int, _F, C.c_int, C.c_int]
         _lib = L
     return _lib
 
@@ -287,6 +290,34 @@ def q8_saxpy(w, vq, vs, out, mode=Q8_SCALAR):
     fn = lib().orc_q8_saxpy_simd8 if mode == Q8_SIMD8 else lib().orc_q8_saxpy
     fn(float(np.float32(w)), _pi8(np.ascontiguousarray(vq, np.int8)), _p(f32(vs)), _p(out),
        out.size)
+    return out
+
+
+def prefill_sequential_q8(cfg: OracleConfig, kq, ks, vq, vs, q, k, v, layer, pos0,
+                          qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1,
+                          mode=Q8_SCALAR, gate=None):
+    """prefill_sequential over a Q8_0 cache (kq/vq int8 [max_seq, kvDim], ks/vs fp32
+    [max_seq, kvDim/32], modified in place: rows pos0..pos0+P-1 are quantised as each token
+    appends them).  Returns out [P, Hq*D]."""
+    c = cfg.c()
+    q, k, v = f32(q), f32(k), f32(v)
+    P = q.shape[0]
+    assert pos0 + P <= cfg.max_seq
+    for a in (kq, vq):
+        assert a.dtype == np.int8 and a.flags["C_CONTIGUOUS"] and a.size >= cfg.max_seq * cfg.kv_dim
+    for a in (ks, vs):
+        assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+        assert a.size >= cfg.max_seq * cfg.kv_dim // 32
+    out = np.zeros((P, cfg.n_heads * cfg.head_size), np.float32)
+    lib().orc_prefill_sequential_q8(
+        C.byref(c), _pi8(kq), _p(ks), _pi8(vq), _p(vs),
+        _p(f32(qnorm_w)) if qnorm_w is not None else None,
+        _p(f32(knorm_w)) if knorm_w is not None else None,
+        _p(f32(rope_cos)) if rope_cos is not None else None,
+        _p(f32(rope_sin)) if rope_sin is not None else None,
+        _p(q), _p(k), _p(v), layer, pos0, P, _p(out), int(n_threads), int(mode))
+    if gate is not None:
+        out = sigmoid_gate(out.reshape(-1), f32(gate).reshape(-1)).reshape(out.shape)
     return out
 
 

@@ -179,7 +179,7 @@ def test_q8_consecutive_steps_and_device_position(mode):
         dc.compare_cache_q8(fp, 0, cache, "Q8 after decode steps")
 
 
-def test_q8_unsupported_entry_points_and_layout(mode):
+def test_q8_cache_rejects_fp32_row_access_and_round_trips_layout(mode):
     c = hfp.ModelConfig(8, 2, 64, 2, rope_freq_base=1e4)
     with _open(c, 64, mode) as fp:
         h = fp.kv.handle
@@ -187,8 +187,6 @@ def test_q8_unsupported_entry_points_and_layout(mode):
         kp = k.ctypes.data_as(C.POINTER(C.c_float))
         assert _lib.status("llmp_kv_read", h, 0, 0, 4, kp, kp) == 6
         assert _lib.status("llmp_kv_write", h, 0, 0, 4, kp, None) == 6
-        b = fp.gpuXb2.ptr
-        assert _lib.status("llmp_attn_prefill", h, 0, 0, 4, b, b, b, b, 0) == 6
         assert _lib.status("llmp_kv_read_q8", h, 0, 62, 4, None, None, None, None) == 2
         # Round trip of both layers' quants and scales through the reference layout.
         rng = np.random.default_rng(1)

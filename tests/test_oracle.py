@@ -461,6 +461,77 @@ def _fma32(a, b, c):
     return np.float32(np.float64(a) * np.float64(b) + np.float64(c))
 
 
+def _q8_prefill_setup(Hq, Hkv, D, S, pos0, P, mode, seed):
+    """A Q8_0 cache with rows [0, pos0) quantised under `mode`, plus P tokens of q/k/v."""
+    rng = np.random.default_rng(seed)
+    kv = Hkv * D
+    kq = np.zeros((S, kv), np.int8); vq = np.zeros((S, kv), np.int8)
+    ks = np.zeros((S, kv // 32), F32); vs = np.zeros((S, kv // 32), F32)
+    for t in range(pos0):
+        kq[t], ks[t] = orc.q8_quantize(rng.standard_normal(kv).astype(F32), mode)
+        vq[t], vs[t] = orc.q8_quantize(rng.standard_normal(kv).astype(F32), mode)
+    q = rng.standard_normal((P, Hq * D)).astype(F32)
+    k = rng.standard_normal((P, kv)).astype(F32)
+    v = rng.standard_normal((P, kv)).astype(F32)
+    return kq, ks, vq, vs, q, k, v
+
+
+def _dequant(quants, scales):
+    n, kv = quants.shape
+    return (quants.astype(np.float64).reshape(n, -1, 32) * scales[:, :, None]).reshape(n, kv)
+
+
+@pytest.mark.parametrize("mode", [orc.Q8_SCALAR, orc.Q8_SIMD8])
+def test_q8_prefill_first_token_output_is_its_dequantised_v(mode):
+    # one attended row: weight 1, so out = scale * quant of the row just appended, exactly
+    Hq, Hkv, D, S = 8, 2, 64, 16
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0)
+    kq, ks, vq, vs, q, k, v = _q8_prefill_setup(Hq, Hkv, D, S, 0, 1, mode, 50)
+    cs, sn = orc.rope_tables(D, S, 5e5)
+    out = orc.prefill_sequential_q8(cfg, kq, ks, vq, vs, q, k, v, 0, 0, rope_cos=cs,
+                                    rope_sin=sn, mode=mode)
+    qv, sv = orc.q8_quantize(v[0], mode)
+    row = (qv.astype(F32).reshape(-1, 32) * sv[:, None]).reshape(Hkv, D)
+    assert np.array_equal(out.reshape(Hq, D), np.repeat(row, Hq // Hkv, axis=0))
+
+
+@pytest.mark.parametrize("mode", [orc.Q8_SCALAR, orc.Q8_SIMD8])
+def test_q8_prefill_appends_quantised_rotated_rows_at_their_positions(mode):
+    Hq, Hkv, D, S, pos0, P = 8, 2, 64, 40, 9, 12
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0)
+    kq, ks, vq, vs, q, k, v = _q8_prefill_setup(Hq, Hkv, D, S, pos0, P, mode, 51)
+    before = [a.copy() for a in (kq, ks, vq, vs)]
+    cs, sn = orc.rope_tables(D, S, 5e5)
+    orc.prefill_sequential_q8(cfg, kq, ks, vq, vs, q, k, v, 0, pos0, rope_cos=cs, rope_sin=sn,
+                              mode=mode)
+    for i in range(P):
+        kr = orc.rope_apply_all(k[i], Hkv, D, D, 0, cs, sn, pos0 + i)
+        want_kq, want_ks = orc.q8_quantize(kr, mode)
+        want_vq, want_vs = orc.q8_quantize(v[i], mode)
+        assert np.array_equal(kq[pos0 + i], want_kq) and np.array_equal(ks[pos0 + i], want_ks)
+        assert np.array_equal(vq[pos0 + i], want_vq) and np.array_equal(vs[pos0 + i], want_vs)
+    for a, b in zip((kq, ks, vq, vs), before):   # rows outside [pos0, pos0 + P) untouched
+        assert np.array_equal(a[:pos0], b[:pos0]) and np.array_equal(a[pos0 + P:], b[pos0 + P:])
+
+
+@pytest.mark.parametrize("mode", [orc.Q8_SCALAR, orc.Q8_SIMD8])
+def test_q8_prefill_uniform_scores_average_each_tokens_causal_rows(mode):
+    # q = 0: every score is 0, so token i's output is the mean of dequantised V rows
+    # 0 .. pos0 + i (its own row included, later rows excluded)
+    Hq, Hkv, D, S, pos0, P = 6, 2, 64, 48, 17, 9
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0)
+    kq, ks, vq, vs, q, k, v = _q8_prefill_setup(Hq, Hkv, D, S, pos0, P, mode, 52)
+    q[:] = 0
+    cs, sn = orc.rope_tables(D, S, 5e5)
+    out = orc.prefill_sequential_q8(cfg, kq, ks, vq, vs, q, k, v, 0, pos0, rope_cos=cs,
+                                    rope_sin=sn, mode=mode)
+    V = _dequant(vq, vs)
+    for i in range(P):
+        mean = V[:pos0 + i + 1].mean(axis=0).reshape(Hkv, D)
+        np.testing.assert_allclose(out[i].reshape(Hq, D), np.repeat(mean, Hq // Hkv, axis=0),
+                                   atol=2e-6)
+
+
 def test_q8_simd8_quantize_truncates_toward_zero():
     rng = np.random.default_rng(40)
     x = (rng.standard_normal(512) * rng.uniform(0.01, 10, 16).repeat(32)).astype(F32)
