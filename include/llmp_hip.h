@@ -94,7 +94,8 @@ int llmp_event_elapsed_ms(float *ms, uint64_t start, uint64_t end);
  * [layer][K|V][kv_head][pos][head_dim] fp32.  LLMP_KV_Q8_0(_TRUNC): per layer the K quants
  * [kv_head][pos][head_dim] int8, K scales [kv_head][pos][head_dim/32] fp32, then the same for
  * V.  Fails with LLMP_ERR_OUT_OF_MEMORY when the pool would not fit in free HBM.  head_dim must
- * be 64, 128 or 256. */
+ * be 64, 128, 256 or 512 (512: fp32 caches and decode only, the full-attention layers of
+ * Gemma 4, whose two head sizes take one handle each). */
 int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int dtype,
                    uint64_t *handle);
 int llmp_kv_destroy(uint64_t handle);
@@ -159,6 +160,19 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
  * later llmp_layer_config with another head count removes them too.  May allocate. */
 int llmp_layer_sinks(uint64_t handle, int layer, const float *sinks);
 
+/* Norm order of a layer (Gemma 4, Gemma4InferenceEngine.java:318-355).  Bits:
+ *   LLMP_NORM_SEQUENTIAL  the K-norm sums squares one value at a time, unfused (RMSNorm.apply
+ *                         with offsets, RMSNorm.java:24-35) instead of SimdVectorOps.dot's
+ *                         8-lane FMA order; the appended K row follows it bit for bit.
+ *   LLMP_NORM_V           the V row is RMS-normalised without weights before it is stored
+ *                         (RMSNorm.applyNoScale, RMSNorm.java:40-50), in the sequential order.
+ * 0 (the default) is the Attention.forwardFromProjections behaviour.  Decode and prefill apply
+ * both; the query's norm (never stored) keeps the fast order, a difference far inside the
+ * output tolerance. */
+#define LLMP_NORM_SEQUENTIAL 1
+#define LLMP_NORM_V          2
+int llmp_layer_norm_mode(uint64_t handle, int layer, int mode);
+
 /* ---- decode attention: one layer-call for one new token --------------------------------
  * Replaces CudaForwardPass.forwardAttentionPart steps 2b'-5 (CudaForwardPass.java:1529-1570):
  * rmsnorm_per_head (Q, K) -> rope_apply (Q, K) -> kv_cache_update -> attention_full, with the
@@ -193,6 +207,15 @@ int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uin
 int llmp_attn_decode_ex(uint64_t handle, int layer, int position, uint64_t d_position,
                         uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
                         int splits, uint64_t stream);
+
+/* Decode for a shared-KV layer (Gemma 4: the last sharedKvLayers layers reuse the cache of an
+ * earlier layer of the same type and compute no K/V, Gemma4InferenceEngine.java:171-180,
+ * 336-366): `layer`'s configuration (heads, window, RoPE, q-norm, scale, sinks) over the rows
+ * of `src_layer`'s cache in the same handle, which must already hold row `position`; nothing
+ * is appended.  position / d_position and gate as in llmp_attn_decode_ex. */
+int llmp_attn_decode_shared(uint64_t handle, int layer, int src_layer, int position,
+                            uint64_t d_position, uint64_t q, uint64_t gate, uint64_t out,
+                            int splits, uint64_t stream);
 
 /* Launch plan llmp_attn_decode would use for this call: splits per KV head, waves per
  * workgroup (4 or 8), rows per split and the first attended position.  Any out may be NULL. */
@@ -234,6 +257,11 @@ int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64
  * 0 = none): out = attention * sigmoid(gate), as llmp_attn_decode_ex applies it. */
 int llmp_attn_prefill_ex(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                          uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);
+/* Prefill of a shared-KV layer (llmp_attn_decode_shared for n_tokens tokens): `layer`'s
+ * configuration over src_layer's rows, which must already hold positions pos0 ..
+ * pos0+n_tokens-1 (the source layer ran the same tokens first); nothing is appended. */
+int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0, int n_tokens,
+                             uint64_t q, uint64_t gate, uint64_t out, uint64_t stream);
 
 /* ---- profiling (the reference's -Dcuda.profile section timers,
  *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */

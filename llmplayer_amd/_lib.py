@@ -23,6 +23,7 @@ ERR_NAMES = {
 LLMP_KV_F32, LLMP_KV_Q8_0, LLMP_KV_Q8_0_TRUNC = 0, 1, 2
 LLMP_ROPE_NORMAL, LLMP_ROPE_NEOX = 0, 2
 LLMP_ROPE_SEL_NONE, LLMP_ROPE_SEL_GLOBAL, LLMP_ROPE_SEL_LOCAL = -1, 0, 1
+LLMP_NORM_SEQUENTIAL, LLMP_NORM_V = 1, 2
 LLMP_PROF_DECODE_SPLIT, LLMP_PROF_DECODE_REDUCE = 0, 1
 LLMP_PROF_PREFILL_APPEND, LLMP_PROF_PREFILL_ATTN = 2, 3
 
@@ -69,6 +70,9 @@ SIGNATURES = {
     "llmp_layer_sinks": [_u64, _i32, _pf],
     "llmp_attn_prefill": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64],
     "llmp_attn_prefill_ex": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64],
+    "llmp_layer_norm_mode": [_u64, _i32, _i32],
+    "llmp_attn_decode_shared": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
+    "llmp_attn_prefill_shared": [_u64, _i32, _i32, _i32, _i32, _u64, _u64, _u64, _u64],
     "llmp_decode_plan": [_u64, _i32, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32),
                          C.POINTER(_i32), C.POINTER(_i32)],
     "llmp_graph_begin": [_u64],

@@ -1,5 +1,6 @@
 // Instantiation and dispatch of the decode kernels (decode_kernels.h) for the shapes the
-// library ships: head_dim 64/128/256 and GQA groups 1, 2, 3, 4, 6, 8.
+// library ships: head_dim 64/128/256 (fp32 and Q8_0 caches) and 512 (fp32: the full-attention
+// layers of Gemma 4), GQA groups 1, 2, 3, 4, 6, 8.
 #include "decode_kernels.h"
 
 namespace llmp {
@@ -13,7 +14,9 @@ struct Tune {
     bool nt;
 };
 constexpr Tune pick(int D, int G) {
-    return Tune{(D == 256 || (G > 4 && D / 8 > 16)) ? 16 : 8, (G > 4) ? 1 : 2, true};
+    // head_dim 512: 8 elements per lane, so a row spans the whole wave (LPR 64).
+    return Tune{D == 512 ? 8 : ((D == 256 || (G > 4 && D / 8 > 16)) ? 16 : 8), (G > 4) ? 1 : 2,
+                true};
 }
 
 // The kernel instance for one shape, and the waves per workgroup it runs with.
@@ -34,9 +37,10 @@ SplitKernel kernel_dgw() {
 
 // 8-wave workgroups except where more than 4 query heads per KV head hold 16 elements per
 // lane (head_dim 256, or any Q8_0 cache): that register footprint leaves no room for them.
+// head_dim 512 always runs 4 waves (its per-wave LDS partials would pass 128 KB at 8).
 template <int D, int G, bool Q8>
 SplitKernel kernel_dg(int waves) {
-    if constexpr ((D == 256 || Q8) && G > 4) {
+    if constexpr (((D == 256 || Q8) && G > 4) || D == 512) {
         return kernel_dgw<D, G, 4, Q8>();
     } else {
         return waves == 8 ? kernel_dgw<D, G, 8, Q8>() : kernel_dgw<D, G, 4, Q8>();
@@ -62,6 +66,9 @@ SplitKernel kernel_split(int head_dim, int group, int waves) {
     case 64: return kernel_d<64, Q8>(group, waves);
     case 128: return kernel_d<128, Q8>(group, waves);
     case 256: return kernel_d<256, Q8>(group, waves);
+    case 512:
+        if constexpr (!Q8) return kernel_d<512, false>(group, waves);
+        return SplitKernel{nullptr, 0};
     default: return SplitKernel{nullptr, 0};
     }
 }
@@ -81,7 +88,7 @@ __global__ void copy_kernel(float4* __restrict__ dst, const float4* __restrict__
 }  // namespace
 
 bool decode_shape_supported(int head_dim, int group) {
-    const bool d_ok = head_dim == 64 || head_dim == 128 || head_dim == 256;
+    const bool d_ok = head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512;
     const bool g_ok = group == 1 || group == 2 || group == 3 || group == 4 || group == 6 ||
                       group == 8;
     return d_ok && g_ok;
@@ -123,6 +130,10 @@ hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, in
         break;
     case 256:
         hipLaunchKernelGGL(dk::decode_reduce_kernel<256>, dim3(n_heads),
+                           dim3(dk::kReduceThreads), 0, stream, a, group);
+        break;
+    case 512:
+        hipLaunchKernelGGL(dk::decode_reduce_kernel<512>, dim3(n_heads),
                            dim3(dk::kReduceThreads), 0, stream, a, group);
         break;
     default: return hipErrorInvalidValue;

@@ -53,20 +53,6 @@ __device__ __forceinline__ float dpp(float x) {
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
 
-// Sum over the LPR consecutive lanes that share a row.  Every lane ends with the same value
-// (each step adds the same two operands, in either order).
-template <int LPR>
-__device__ __forceinline__ float row_group_sum(float x) {
-    static_assert(LPR == 4 || LPR == 8 || LPR == 16, "rows are shared by 4, 8 or 16 lanes");
-    x = x + dpp<kDppQuadXor1>(x);
-    x = x + dpp<kDppQuadXor2>(x);
-    if constexpr (LPR >= 8) x = x + dpp<kDppRowHalfMirror>(x);
-    if constexpr (LPR >= 16) x = x + dpp<kDppRowMirror>(x);
-    return x;
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
 // One step of a cross-lane reduction over the lanes of equal residue mod OFF (OFF a power of
 // two, 4..32), all in VGPRs: offsets 16 and 32 exchange whole rows / half-waves with the
 // gfx950 permlane swaps (the pair's two values come back in both lanes, combined in the same
@@ -88,6 +74,24 @@ __device__ __forceinline__ float lane_step(float x) {
     }
     return MAX ? fmaxf(a, b) : a + b;
 }
+
+// Sum over the LPR consecutive lanes that share a row.  Every lane ends with the same value
+// (each step adds the same two operands, in either order).
+template <int LPR>
+__device__ __forceinline__ float row_group_sum(float x) {
+    static_assert(LPR == 4 || LPR == 8 || LPR == 16 || LPR == 32 || LPR == 64,
+                  "rows are shared by 4 to 64 lanes");
+    x = x + dpp<kDppQuadXor1>(x);
+    x = x + dpp<kDppQuadXor2>(x);
+    if constexpr (LPR >= 8) x = x + dpp<kDppRowHalfMirror>(x);
+    if constexpr (LPR >= 16) x = x + dpp<kDppRowMirror>(x);
+    if constexpr (LPR >= 32) x = lane_step<16, false>(x);
+    if constexpr (LPR >= 64) x = lane_step<32, false>(x);
+    return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 
 // Final normalisation of one output element of query head hq from its merged (max M,
 // sum L, unnormalised O) in the log2 domain: an attention sink (log2-domain logit) joins the
@@ -345,13 +349,36 @@ __device__ __forceinline__ int step_position(const DecodeArgs& a) {
     return a.d_pos != nullptr ? *a.d_pos : a.pos;
 }
 
+// 1/rms of D values in the order of RMSNorm.apply with offsets (RMSNorm.java:24-35, the
+// Gemma 4 engine's QK-norm and V-norm): one thread sums the squares sequentially, unfused,
+// then r = 1/(float)sqrt(ss/D + eps).
+template <int D>
+__device__ __forceinline__ float seq_rms_inv(const float* x, float eps) {
+    float ss = 0.0f;
+    for (int i = 0; i < D; ++i) ss = ss + x[i] * x[i];
+    float v = ss / (float)D;
+    v = v + eps;
+    return 1.0f / (float)__builtin_sqrt((double)v);
+}
+
 // Exact prep of `nh` heads staged in LDS (x: nh*D floats): QK-norm with weights p.qnw for
-// heads < n_w0 and p.knw for the others, then RoPE.  Must be called by the whole workgroup
-// (NTHR threads).
+// heads < n_w0 and p.knw for the others, then RoPE.  The sum of squares follows
+// SimdVectorOps.dot's 8-lane FMA order, or with `seq` RMSNorm.apply's sequential one.  Must
+// be called by the whole workgroup (NTHR threads).
 template <int D, int NTHR>
 __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* s_r,
-                               const HeadPrep& p, int tid) {
-    if (p.qnw != nullptr) {
+                               const HeadPrep& p, int tid, bool seq = false) {
+    if (p.qnw != nullptr && seq) {
+        for (int t = tid; t < nh; t += NTHR) s_r[t] = seq_rms_inv<D>(x + t * D, p.eps);
+        __syncthreads();
+        for (int i = tid; i < nh * D; i += NTHR) {
+            const int hh = i / D;
+            const float* w = (hh < n_w0) ? p.qnw : p.knw;
+            const float xs = x[i] * s_r[hh];
+            x[i] = xs * w[i - hh * D];
+        }
+        __syncthreads();
+    } else if (p.qnw != nullptr) {
         for (int t = tid; t < nh * 8; t += NTHR) {
             const int hh = t >> 3, ln = t & 7;
             const float* xh = x + hh * D;
@@ -472,7 +499,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     const HeadPrep hp = head_prep(a, pos);
     const int row_begin = sp.start + split * sp.rows_per_split;
     const int row_end = min(row_begin + sp.rows_per_split, pos + 1);
-    const bool has_pos = (row_end == pos + 1);
+    // The split holding row `pos` appends it, unless the layer shares another layer's KV
+    // (row `pos` is then already cached and streamed like the others).
+    const bool has_pos = (row_end == pos + 1) && a.no_append == 0;
     const int cache_end = has_pos ? pos : row_end;
 
     // 1. Query slice of this lane, pre-scaled (log2 domain unless soft-capping).  Without
@@ -587,7 +616,16 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             s_v[i] = a.v[kvh * D + i];
         }
         __syncthreads();
-        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, hp, tid);
+        // Gemma 4's weightless V-norm: its sequential sum runs on another wave than the
+        // K-norm's (thread 0), and is applied after the K prep's barriers.
+        __shared__ float s_vr;
+        if (a.v_norm != 0 && tid == (NTHR > 64 ? 64 : 0)) s_vr = seq_rms_inv<D>(s_v, a.eps);
+        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, hp, tid, a.norm_seq != 0);
+        if (a.v_norm != 0) {
+            __syncthreads();
+            for (int i = tid; i < D; i += NTHR) s_v[i] = s_v[i] * s_vr;
+            __syncthreads();
+        }
         if constexpr (!Q8) {
             float* kplane = a.kc + (long long)kvh * a.head_stride;
             float* vplane = a.vc + (long long)kvh * a.head_stride;
@@ -645,18 +683,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
         float mw = m[h];
         if constexpr (LPR <= 4) mw = lane_step<4, true>(mw);
         if constexpr (LPR <= 8) mw = lane_step<8, true>(mw);
-        mw = lane_step<32, true>(lane_step<16, true>(mw));
+        if constexpr (LPR <= 16) mw = lane_step<16, true>(mw);
+        if constexpr (LPR <= 32) mw = lane_step<32, true>(mw);
         const float sc = fast_exp2(m[h] - mw);
         float lw = l[h] * sc;
         if constexpr (LPR <= 4) lw = lane_step<4, false>(lw);
         if constexpr (LPR <= 8) lw = lane_step<8, false>(lw);
-        lw = lane_step<32, false>(lane_step<16, false>(lw));
+        if constexpr (LPR <= 16) lw = lane_step<16, false>(lw);
+        if constexpr (LPR <= 32) lw = lane_step<32, false>(lw);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             float x = o[h][e] * sc;
             if constexpr (LPR <= 4) x = lane_step<4, false>(x);
             if constexpr (LPR <= 8) x = lane_step<8, false>(x);
-            x = lane_step<32, false>(lane_step<16, false>(x));
+            if constexpr (LPR <= 16) x = lane_step<16, false>(x);
+            if constexpr (LPR <= 32) x = lane_step<32, false>(x);
             o[h][e] = x;
         }
         m[h] = mw;

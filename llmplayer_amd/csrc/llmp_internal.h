@@ -43,6 +43,9 @@ struct DecodeArgs {
     int half_rope;         // rotated pairs per head
     int rope_type;         // 0 NORMAL, 2 NEOX
     int q8_trunc;          // Q8_0 append: 1 = truncate (8-lane SIMD contract), 0 = round half up
+    int norm_seq;          // 1: K-norm sums squares sequentially (RMSNorm.apply with offsets)
+    int v_norm;            // 1: the V row is RMS-normalised without weights before the append
+    int no_append;         // 1: shared-KV layer: row `pos` is already cached, k/v are unused
     float eps;             // QK-norm epsilon
     float qk_scale;        // factor folded into q: scale*log2(e), or scale when soft-capping
     float softcap;         // 0 = off

@@ -52,6 +52,7 @@ struct LayerCfg {
     float* d_qnw = nullptr;
     float* d_knw = nullptr;
     float* d_sinks = nullptr;   // [n_heads] sink logits times log2(e) (llmp_layer_sinks)
+    int norm_mode = 0;          // LLMP_NORM_* bits (llmp_layer_norm_mode)
 };
 
 struct RopeTable {
@@ -266,17 +267,27 @@ Plan make_plan(const KvHandle* kv, const LayerCfg& c, int position, int splits_r
 // Enqueues one decode layer-call.  With d_pos == nullptr the step runs at `position`;
 // otherwise the kernels read the position from device memory when they run, and the launch
 // is planned for the longest step the layer can take (position = max_seq - 1).
-int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint64_t q,
-                   uint64_t k, uint64_t v, uint64_t gate, uint64_t out, int splits,
+//
+// src_layer >= 0 is a shared-KV layer (Gemma 4): it attends to src_layer's cache rows with its
+// own configuration and appends nothing (row `position` must already be cached); k and v are
+// not read.  src_layer < 0: the layer's own cache, with the append.
+int enqueue_decode(KvHandle* kv, int layer, int src_layer, int position, const int* d_pos,
+                   uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out, int splits,
                    uint64_t stream) {
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (src_layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "source layer %d outside [0, %d)", src_layer,
+                    kv->n_layers);
+    const bool shared = src_layer >= 0;
+    const int kv_layer = shared ? src_layer : layer;
     if (position < 0 || position >= kv->max_seq)
         return fail(LLMP_ERR_OUT_OF_RANGE, "position %d outside [0, %d)", position, kv->max_seq);
     const LayerCfg& c = kv->layers[(size_t)layer];
     if (!c.configured)
         return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
-    if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "decode: null buffer");
+    if (!q || !out || (!shared && (!k || !v)))
+        return fail(LLMP_ERR_INVALID_ARG, "decode: null buffer");
     if ((q | k | v | out) & 15)
         return fail(LLMP_ERR_INVALID_ARG, "decode: q/k/v/out must be 16-byte aligned");
     if (gate & 3) return fail(LLMP_ERR_INVALID_ARG, "decode: gate must be 4-byte aligned");
@@ -290,14 +301,14 @@ int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint
     a.k = reinterpret_cast<const float*>(k);
     a.v = reinterpret_cast<const float*>(v);
     if (kv->q8()) {
-        a.kq = kv->kq(layer);
-        a.ks = kv->ks(layer);
-        a.vq = kv->vq(layer);
-        a.vs = kv->vs(layer);
+        a.kq = kv->kq(kv_layer);
+        a.ks = kv->ks(kv_layer);
+        a.vq = kv->vq(kv_layer);
+        a.vs = kv->vs(kv_layer);
         a.q8_trunc = kv->dtype == LLMP_KV_Q8_0_TRUNC;
     } else {
-        a.kc = kv->k_plane(layer);
-        a.vc = kv->v_plane(layer);
+        a.kc = kv->k_plane(kv_layer);
+        a.vc = kv->v_plane(kv_layer);
     }
     if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
         const RopeTable& t = kv->rope[c.rope_sel];
@@ -307,6 +318,9 @@ int enqueue_decode(KvHandle* kv, int layer, int position, const int* d_pos, uint
         a.sin_t = t.d_sin;
         a.half_rope = t.half;
     }
+    a.norm_seq = (c.norm_mode & LLMP_NORM_SEQUENTIAL) != 0;
+    a.v_norm = (c.norm_mode & LLMP_NORM_V) != 0;
+    a.no_append = shared;
     a.qnw = c.d_qnw;
     a.knw = c.d_knw;
     a.sinks = c.d_sinks;
@@ -556,13 +570,15 @@ int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int 
     if (n_layers <= 0 || max_seq <= 0 || n_kv_heads <= 0)
         return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: n_layers=%d max_seq=%d n_kv_heads=%d",
                     n_layers, max_seq, n_kv_heads);
-    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-        return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: head_dim %d (supported: 64, 128, 256)",
-                    head_dim);
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
+        return fail(LLMP_ERR_UNSUPPORTED,
+                    "llmp_kv_create: head_dim %d (supported: 64, 128, 256, 512)", head_dim);
     if (dtype != LLMP_KV_F32 && dtype != LLMP_KV_Q8_0 && dtype != LLMP_KV_Q8_0_TRUNC)
         return fail(LLMP_ERR_UNSUPPORTED,
                     "llmp_kv_create: dtype %d (LLMP_KV_F32, LLMP_KV_Q8_0 or LLMP_KV_Q8_0_TRUNC)",
                     dtype);
+    if (head_dim == 512 && dtype != LLMP_KV_F32)
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: head_dim 512 needs an fp32 cache");
     if ((long long)max_seq * head_dim >= (1LL << 31))
         return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: max_seq*head_dim exceeds 2^31");
     auto kv = std::make_unique<KvHandle>();
@@ -864,7 +880,7 @@ int llmp_attn_decode(uint64_t handle, int layer, int position, uint64_t q, uint6
                      uint64_t out, int splits, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    return enqueue_decode(kv, layer, position, nullptr, q, k, v, 0, out, splits, stream);
+    return enqueue_decode(kv, layer, -1, position, nullptr, q, k, v, 0, out, splits, stream);
 }
 
 int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uint64_t q,
@@ -873,7 +889,7 @@ int llmp_attn_decode_devpos(uint64_t handle, int layer, uint64_t d_position, uin
     LLMP_GET_HANDLE(kv, handle);
     if (!d_position || (d_position & 3))
         return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode_devpos: null or misaligned position word");
-    return enqueue_decode(kv, layer, kv->max_seq - 1, reinterpret_cast<const int*>(d_position), q,
+    return enqueue_decode(kv, layer, -1, kv->max_seq - 1, reinterpret_cast<const int*>(d_position), q,
                           k, v, 0, out, splits, stream);
 }
 
@@ -885,9 +901,37 @@ int llmp_attn_decode_ex(uint64_t handle, int layer, int position, uint64_t d_pos
     if (d_position & 3)
         return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode_ex: misaligned position word");
     if (d_position)
-        return enqueue_decode(kv, layer, kv->max_seq - 1, reinterpret_cast<const int*>(d_position),
+        return enqueue_decode(kv, layer, -1, kv->max_seq - 1, reinterpret_cast<const int*>(d_position),
                               q, k, v, gate, out, splits, stream);
-    return enqueue_decode(kv, layer, position, nullptr, q, k, v, gate, out, splits, stream);
+    return enqueue_decode(kv, layer, -1, position, nullptr, q, k, v, gate, out, splits, stream);
+}
+
+int llmp_attn_decode_shared(uint64_t handle, int layer, int src_layer, int position,
+                            uint64_t d_position, uint64_t q, uint64_t gate, uint64_t out,
+                            int splits, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (src_layer < 0)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "llmp_attn_decode_shared: source layer %d", src_layer);
+    if (d_position & 3)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_decode_shared: misaligned position word");
+    if (d_position)
+        return enqueue_decode(kv, layer, src_layer, kv->max_seq - 1,
+                              reinterpret_cast<const int*>(d_position), q, 0, 0, gate, out, splits,
+                              stream);
+    return enqueue_decode(kv, layer, src_layer, position, nullptr, q, 0, 0, gate, out, splits,
+                          stream);
+}
+
+int llmp_layer_norm_mode(uint64_t handle, int layer, int mode) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (mode & ~(LLMP_NORM_SEQUENTIAL | LLMP_NORM_V))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_layer_norm_mode: unknown mode bits 0x%x", mode);
+    kv->layers[(size_t)layer].norm_mode = mode;
+    return LLMP_OK;
 }
 
 int llmp_layer_sinks(uint64_t handle, int layer, const float* sinks) {
@@ -939,34 +983,56 @@ int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* 
 }
 
 // ---- prefill attention -------------------------------------------------------------------------
-static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint64_t q,
-                           uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);
+static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int n_tokens,
+                           uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
+                           uint64_t stream);
 
 int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q, uint64_t k,
                       uint64_t v, uint64_t out, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    return enqueue_prefill(kv, layer, pos0, n_tokens, q, k, v, 0, out, stream);
+    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, q, k, v, 0, out, stream);
 }
 
 int llmp_attn_prefill_ex(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                          uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    return enqueue_prefill(kv, layer, pos0, n_tokens, q, k, v, gate, out, stream);
+    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, q, k, v, gate, out, stream);
 }
 
-static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint64_t q,
-                           uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream) {
+int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0, int n_tokens,
+                             uint64_t q, uint64_t gate, uint64_t out, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (src_layer < 0)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "llmp_attn_prefill_shared: source layer %d", src_layer);
+    return enqueue_prefill(kv, layer, src_layer, pos0, n_tokens, q, 0, 0, gate, out, stream);
+}
+
+// src_layer >= 0: shared-KV layer (as in enqueue_decode): attention over src_layer's rows,
+// which must already hold the prompt's rows; no append.
+static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int n_tokens,
+                           uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
+                           uint64_t stream) {
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (src_layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "source layer %d outside [0, %d)", src_layer,
+                    kv->n_layers);
+    const bool shared = src_layer >= 0;
+    const int kv_layer = shared ? src_layer : layer;
     if (n_tokens <= 0 || pos0 < 0 || (long long)pos0 + n_tokens > kv->max_seq)
         return fail(LLMP_ERR_OUT_OF_RANGE, "prefill rows [%d, %lld) outside [0, %d)", pos0,
                     (long long)pos0 + n_tokens, kv->max_seq);
     const LayerCfg& c = kv->layers[(size_t)layer];
     if (!c.configured)
         return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
-    if (!q || !k || !v || !out) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: null buffer");
+    if (!q || !out || (!shared && (!k || !v)))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_prefill: null buffer");
+    if (prefill_tile_keys(kv->head_dim) <= 0)
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_attn_prefill: head_dim %d (decode only)",
+                    kv->head_dim);
     if ((q | k | v) & 1 || out & 15 || gate & 3)
         return fail(LLMP_ERR_INVALID_ARG,
                     "llmp_attn_prefill: misaligned q/k/v (2 B), gate (4 B) or out (16 B)");
@@ -976,15 +1042,17 @@ static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint
     a.k = reinterpret_cast<const unsigned short*>(k);
     a.v = reinterpret_cast<const unsigned short*>(v);
     if (kv->q8()) {
-        a.kq = kv->kq(layer);
-        a.ks = kv->ks(layer);
-        a.vq = kv->vq(layer);
-        a.vs = kv->vs(layer);
+        a.kq = kv->kq(kv_layer);
+        a.ks = kv->ks(kv_layer);
+        a.vq = kv->vq(kv_layer);
+        a.vs = kv->vs(kv_layer);
         a.q8_trunc = kv->dtype == LLMP_KV_Q8_0_TRUNC;
     } else {
-        a.kc = kv->k_plane(layer);
-        a.vc = kv->v_plane(layer);
+        a.kc = kv->k_plane(kv_layer);
+        a.vc = kv->v_plane(kv_layer);
     }
+    a.norm_seq = (c.norm_mode & LLMP_NORM_SEQUENTIAL) != 0;
+    a.v_norm = (c.norm_mode & LLMP_NORM_V) != 0;
     a.head_stride = (long long)kv->max_seq * D;
     if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
         const RopeTable& t = kv->rope[c.rope_sel];
@@ -1069,7 +1137,7 @@ static int enqueue_prefill(KvHandle* kv, int layer, int pos0, int n_tokens, uint
             if (int rc = prof_event(kv, e)) return rc;
         LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
     }
-    LLMP_HIP_CHECK(launch_prefill_append(a, D, st), "prefill append launch");
+    if (!shared) LLMP_HIP_CHECK(launch_prefill_append(a, D, st), "prefill append launch");
     if (kv->prof_on) {
         LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
         kv->prof_pending[LLMP_PROF_PREFILL_APPEND].push_back({e0, e1});

@@ -59,6 +59,8 @@ struct PrefillArgs {
     float* vs;
     long long head_stride;    // max_seq*D (elements of one KV head's rows)
     int q8_trunc;             // Q8_0 append: 1 = truncate (8-lane SIMD contract), 0 = round half up
+    int norm_seq;             // 1: K-norm sums squares sequentially (RMSNorm.apply with offsets)
+    int v_norm;               // 1: V rows RMS-normalised without weights before the append
     const float* cos_t;       // RoPE table [max_seq][half] or nullptr (NoPE)
     const float* sin_t;
     const float* qnw;         // QK-norm weights or nullptr
@@ -80,7 +82,8 @@ __device__ __forceinline__ float bf16_to_f32(unsigned short b) {
     return __uint_as_float((unsigned)b << 16);
 }
 // ---- 1. exact K/V append, one workgroup per token --------------------------------------------
-// LDS floats: Hkv*(D + 9), plus Hkv*D + 2*Hkv*D/32 over a Q8_0 cache (see prefill_append_lds).
+// LDS floats: Hkv*(D + 9), plus Hkv*(D + 1) + 2*Hkv*D/32 when the V rows are staged (Q8_0
+// cache or V-norm; see prefill_append_lds).
 template <int D, int NTHR>
 __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
     extern __shared__ float s_dyn[];
@@ -97,8 +100,8 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
                     a.sin_t ? a.sin_t + (long long)pos * a.half_rope : nullptr, a.half_rope,
                     a.rope_type};
     if (a.qnw == nullptr) hp.qnw = hp.knw = nullptr;
-    dk::prep_heads_lds<D, NTHR>(s_k, a.Hkv, 0, s_acc, s_r, hp, tid);
-    if (a.kq == nullptr) {
+    dk::prep_heads_lds<D, NTHR>(s_k, a.Hkv, 0, s_acc, s_r, hp, tid, a.norm_seq != 0);
+    if (a.kq == nullptr && a.v_norm == 0) {
         for (int e = tid; e < kvd; e += NTHR) {
             const int h = e / D, d = e - h * D;
             const long long off = (long long)h * a.head_stride + (long long)pos * D + d;
@@ -107,13 +110,29 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
         }
         return;
     }
+    float* s_v = s_r + a.Hkv;              // Hkv*D
+    float* s_vr = s_v + kvd;               // Hkv
+    float* s_inv = s_vr + a.Hkv;           // 2*Hkv*D/32
+    for (int e = tid; e < kvd; e += NTHR) s_v[e] = bf16_to_f32(a.v[(long long)i * kvd + e]);
+    __syncthreads();
+    if (a.v_norm != 0) {   // Gemma 4's weightless V-norm, sequential order (RMSNorm.applyNoScale)
+        for (int h = tid; h < a.Hkv; h += NTHR) s_vr[h] = dk::seq_rms_inv<D>(s_v + h * D, a.eps);
+        __syncthreads();
+        for (int e = tid; e < kvd; e += NTHR) s_v[e] = s_v[e] * s_vr[e / D];
+        __syncthreads();
+    }
+    if (a.kq == nullptr) {
+        for (int e = tid; e < kvd; e += NTHR) {
+            const int h = e / D, d = e - h * D;
+            const long long off = (long long)h * a.head_stride + (long long)pos * D + d;
+            a.kc[off] = s_k[e];
+            a.vc[off] = s_v[e];
+        }
+        return;
+    }
     // Q8_0: the K and V rows are quantised block by block exactly like a decode append
     // (KVCache.storeK/storeV over a Q8_0 cache, KVCache.java:164-179).  Blocks [0, nb) are K's,
     // [nb, 2nb) V's; 4 consecutive codes are stored as one 32-bit word.
-    float* s_v = s_r + a.Hkv;              // Hkv*D
-    float* s_inv = s_v + kvd;              // 2*Hkv*D/32
-    for (int e = tid; e < kvd; e += NTHR) s_v[e] = bf16_to_f32(a.v[(long long)i * kvd + e]);
-    __syncthreads();
     const int nb = kvd / 32, bph = D / 32;
     for (int b = tid; b < 2 * nb; b += NTHR) {
         const bool is_v = b >= nb;
@@ -139,9 +158,10 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
     }
 }
 
-// Dynamic LDS bytes of prefill_append_kernel.
-inline size_t prefill_append_lds(int Hkv, int D, bool q8) {
-    const size_t f = (size_t)Hkv * (D + 9) + (q8 ? (size_t)Hkv * D + 2 * (size_t)Hkv * D / 32 : 0);
+// Dynamic LDS bytes of prefill_append_kernel; stage_v: Q8_0 cache or V-norm.
+inline size_t prefill_append_lds(int Hkv, int D, bool stage_v) {
+    const size_t f = (size_t)Hkv * (D + 9) +
+                     (stage_v ? (size_t)Hkv * (D + 1) + 2 * (size_t)Hkv * D / 32 : 0);
     return f * sizeof(float);
 }
 

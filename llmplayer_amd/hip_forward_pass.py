@@ -82,6 +82,9 @@ class ModelConfig:
     use_no_pe_on_global_layers: bool = False
     use_layer_norm: bool = False
     expert_count: int = 0                 # > 0 for MoE models (selects the Qwen3MoE engine rules)
+    key_length: int = 0                   # Gemma 4: head size of full-attention layers (0 -> head_size)
+    shared_kv_layers: int = 0             # Gemma 4: the last N layers reuse earlier layers' KV
+    rope_freq_factors: Optional[np.ndarray] = None   # Gemma 4 full-attention RoPE factors
 
     @property
     def kv_dim(self) -> int:
@@ -462,6 +465,181 @@ class HipForwardPass:
                 buf.free()
         if getattr(self, "kv", None) is not None:
             self.kv.destroy()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+@dataclass
+class Gemma4State:
+    """The buffers of Gemma4State the attention half uses (qLarge, kLarge, vLarge, xb2Large):
+    sized for the larger head size; a layer uses the first Hq*headSize / Hkv*headSize floats."""
+    q: np.ndarray
+    k: np.ndarray
+    v: np.ndarray
+    xb2: np.ndarray
+
+
+class Gemma4HipForwardPass:
+    """Attention half of Gemma4InferenceEngine.forwardLayer (Gemma4InferenceEngine.java:
+    295-420) on MI355X.
+
+    Gemma 4 mixes sliding-window layers (head size `head_size`, RoPE theta
+    rope_freq_base_swa) and full-attention layers (head size `key_length`, theta
+    rope_freq_base with rope_freq_factors), picked by sliding_window_pattern
+    (isSwaLayer, :184-189).  Each head size gets its own KV handle.  Per-head QK-norm and the
+    weightless V-norm follow RMSNorm.apply's sequential order (llmp_layer_norm_mode), the
+    attention scale is 1.0 (:372), and the last shared_kv_layers layers compute no K/V: they
+    attend to the cache of the last own-KV layer of their type before the shared boundary
+    (kvSourceLayer, :171-180) through llmp_attn_decode_shared.  Shared layers keep a
+    configuration slot in their handle (their q-norm weights are their own); the planes of
+    that slot stay unused.  qk_norm[layer] = (q_weights, k_weights) of that layer's head size,
+    or None."""
+
+    def __init__(self, config: ModelConfig, max_seq_len: int,
+                 qk_norm: Optional[Sequence[Optional[tuple]]] = None, device: int = 0):
+        c = config
+        init(device)
+        self.config = c
+        self.max_seq_len = max_seq_len
+        self.head_swa = c.head_size
+        self.head_full = c.key_length if c.key_length > 0 else c.head_size
+        L = c.block_count
+        self.first_shared = L - c.shared_kv_layers
+        self.kv = {}        # is_swa -> KvCache
+        self.slot = []      # layer -> index inside its handle
+        counts = {True: 0, False: 0}
+        for layer in range(L):
+            t = self.isSwaLayer(layer)
+            self.slot.append(counts[t])
+            counts[t] += 1
+        rope_type = c.resolved_rope_type()
+        for t, n in counts.items():
+            if n == 0:
+                continue
+            D = self.head_size(t)
+            kv = KvCache(n, max_seq_len, c.head_count_kv, D, _lib.LLMP_KV_F32)
+            self.kv[t] = kv
+            # Gemma4InferenceEngine.java:133-139: RoPE dim = head size of the layer type.
+            theta = (c.rope_freq_base_swa or 10000.0) if t else c.rope_freq_base
+            cos_t, sin_t = rope_table(D, max_seq_len, theta, 1.0,
+                                      None if t else c.rope_freq_factors)
+            call("llmp_rope_upload", kv.handle, _lib.LLMP_ROPE_SEL_GLOBAL, _fp(cos_t), _fp(sin_t),
+                 max_seq_len, D // 2)
+        for layer in range(L):
+            t = self.isSwaLayer(layer)
+            D = self.head_size(t)
+            qw = kw = None
+            w = qk_norm[layer] if qk_norm is not None else None
+            if w is not None:
+                qw = np.ascontiguousarray(w[0], np.float32)
+                kw = np.ascontiguousarray(w[1], np.float32)
+                assert qw.size == D and kw.size == D
+            h = self.kv[t].handle
+            call("llmp_layer_config", h, self.slot[layer], c.head_count, c.head_count_kv, D,
+                 rope_type, _lib.LLMP_ROPE_SEL_GLOBAL, c.sliding_window if t else 0,
+                 int(not t), 1.0, 0.0, float(c.norm_eps), _fp(qw), _fp(kw))
+            call("llmp_layer_norm_mode", h, self.slot[layer],
+                 _lib.LLMP_NORM_SEQUENTIAL | _lib.LLMP_NORM_V)
+        Dmax = max(self.head_swa, self.head_full)
+        self.gpuQ = DeviceBuffer(c.head_count * Dmax * 4)
+        self.gpuK = DeviceBuffer(c.head_count_kv * Dmax * 4)
+        self.gpuV = DeviceBuffer(c.head_count_kv * Dmax * 4)
+        self.gpuXb2 = DeviceBuffer(c.head_count * Dmax * 4)
+
+    def isSwaLayer(self, layer: int) -> bool:
+        p = self.config.sliding_window_pattern
+        if p is not None and layer < len(p):
+            return bool(p[layer])
+        return layer % 6 != 5
+
+    def head_size(self, is_swa: bool) -> int:
+        return self.head_swa if is_swa else self.head_full
+
+    def hasOwnKv(self, layer: int) -> bool:
+        return layer < self.first_shared
+
+    def kvSourceLayer(self, layer: int) -> int:
+        if self.hasOwnKv(layer):
+            return layer
+        return self.first_shared - 2 if self.isSwaLayer(layer) else self.first_shared - 1
+
+    def createState(self) -> Gemma4State:
+        c = self.config
+        Dmax = max(self.head_swa, self.head_full)
+        return Gemma4State(np.zeros(c.head_count * Dmax, np.float32),
+                           np.zeros(c.head_count_kv * Dmax, np.float32),
+                           np.zeros(c.head_count_kv * Dmax, np.float32),
+                           np.zeros(c.head_count * Dmax, np.float32))
+
+    def kv_cache(self, layer: int):
+        """(KvCache, slot) holding `layer`'s own rows (its source layer's for shared layers)."""
+        src = self.kvSourceLayer(layer)
+        return self.kv[self.isSwaLayer(src)], self.slot[src]
+
+    def forwardAttentionOnly(self, state: Gemma4State, layer: int, position: int,
+                             splits: int = 0) -> None:
+        """Steps 2-4 of forwardLayer from the projections in state.q (and state.k, state.v for
+        layers with their own KV) into state.xb2 (the first Hq*headSize floats of each)."""
+        c = self.config
+        t = self.isSwaLayer(layer)
+        D = self.head_size(t)
+        qd, kvd = c.head_count * D, c.head_count_kv * D
+        h = self.kv[t].handle
+        self.gpuQ.upload(np.ascontiguousarray(state.q[:qd], np.float32))
+        if self.hasOwnKv(layer):
+            self.gpuK.upload(np.ascontiguousarray(state.k[:kvd], np.float32))
+            self.gpuV.upload(np.ascontiguousarray(state.v[:kvd], np.float32))
+            call("llmp_attn_decode_ex", h, self.slot[layer], position, 0, self.gpuQ.ptr,
+                 self.gpuK.ptr, self.gpuV.ptr, 0, self.gpuXb2.ptr, splits, 0)
+        else:
+            src = self.kvSourceLayer(layer)
+            call("llmp_attn_decode_shared", h, self.slot[layer], self.slot[src], position, 0,
+                 self.gpuQ.ptr, 0, self.gpuXb2.ptr, splits, 0)
+        state.xb2[:qd] = self.gpuXb2.download(np.float32, qd)
+
+    def prefill(self, layer: int, pos0: int, q_bf16: np.ndarray,
+                k_bf16: Optional[np.ndarray] = None,
+                v_bf16: Optional[np.ndarray] = None) -> np.ndarray:
+        """P tokens of one layer in one call (bf16 [P, Hq*D] / [P, Hkv*D]; k, v unused for
+        shared layers).  Sliding-window layers only: the 512-dim full-attention heads have no
+        prefill kernel (LLMP_ERR_UNSUPPORTED); the reference runs a prompt token by token."""
+        c = self.config
+        t = self.isSwaLayer(layer)
+        D = self.head_size(t)
+        qd, kvd = c.head_count * D, c.head_count_kv * D
+        q16 = np.ascontiguousarray(q_bf16, np.uint16).reshape(-1, qd)
+        P = q16.shape[0]
+        bufs = [DeviceBuffer(q16.nbytes), DeviceBuffer(P * qd * 4)]
+        try:
+            bufs[0].upload(q16)
+            h = self.kv[t].handle
+            if self.hasOwnKv(layer):
+                k16 = np.ascontiguousarray(k_bf16, np.uint16).reshape(P, kvd)
+                v16 = np.ascontiguousarray(v_bf16, np.uint16).reshape(P, kvd)
+                bk, bv = DeviceBuffer(k16.nbytes), DeviceBuffer(v16.nbytes)
+                bufs += [bk, bv]
+                bk.upload(k16)
+                bv.upload(v16)
+                call("llmp_attn_prefill_ex", h, self.slot[layer], pos0, P, bufs[0].ptr, bk.ptr,
+                     bv.ptr, 0, bufs[1].ptr, 0)
+            else:
+                call("llmp_attn_prefill_shared", h, self.slot[layer],
+                     self.slot[self.kvSourceLayer(layer)], pos0, P, bufs[0].ptr, 0, bufs[1].ptr, 0)
+            return bufs[1].download(np.float32, P * qd).reshape(P, qd)
+        finally:
+            for b in bufs:
+                b.free()
+
+    def close(self) -> None:
+        for b in (self.gpuQ, self.gpuK, self.gpuV, self.gpuXb2):
+            b.free()
+        for kv in self.kv.values():
+            kv.destroy()
+        self.kv = {}
 
     def __enter__(self):
         return self

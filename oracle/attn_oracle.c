@@ -591,6 +591,87 @@ void orc_prefill_sequential_q8(const orc_cfg *c, int8_t *kq, float *ks, int8_t *
     free(att);
 }
 
+/* ---- Gemma 4 (Gemma4InferenceEngine.java:295-420) -----------------------------------------
+ * RMSNorm.apply with offsets (RMSNorm.java:24-35): a sequential, unfused sum of squares,
+ * r = 1/(float)sqrt(ss/size + eps), x = (x*r)*w.  w == NULL is RMSNorm.applyNoScale
+ * (RMSNorm.java:40-50), x = x*r, the weightless V-norm of Gemma 4. */
+void orc_rms_norm_seq(float *x, const float *w, int size, float eps)
+{
+    float ss = 0.0f;
+    for (int i = 0; i < size; i++) {
+        float v = x[i];
+        ss += v * v;
+    }
+    ss = 1.0f / (float)sqrt((double)(ss / (float)size + eps));
+    for (int i = 0; i < size; i++) x[i] = w ? x[i] * ss * w[i] : x[i] * ss;
+}
+
+/* The attention half of Gemma4InferenceEngine.forwardLayer (Gemma4InferenceEngine.java:
+ * 300-420) for one layer: per-head QK-norm (RMSNorm.apply order) and RoPE on q; when the
+ * layer has its own KV (k, v non-NULL): K-norm, weightless V-norm, RoPE on k, store at `pos`;
+ * otherwise (shared-KV layer) the cache is the source layer's and is only read.  Scores are
+ * sequential float dots with scale 1.0, softmax as written inline there (max, (float)exp,
+ * sequential sum, multiply by 1/sum), out[i] = sum over t of att*v in increasing t.
+ * c->head_size is the layer type's head size; window applies when is_swa.  q, k, v are
+ * modified in place as qBuf/kBuf/vBuf are. */
+void orc_forward_gemma4(const orc_cfg *c, float *kcache, float *vcache, const float *qnorm_w,
+                        const float *knorm_w, const float *rope_cos, const float *rope_sin,
+                        float *q, float *k, float *v, int is_swa, int pos, float *out,
+                        float *att_scratch, int n_threads)
+{
+    const int Hq = c->n_heads, Hkv = c->n_kv_heads, D = c->head_size;
+    const int kv_dim = Hkv * D;
+    const int kv_mul = Hq / Hkv;
+    if (qnorm_w)
+        for (int h = 0; h < Hq; h++) orc_rms_norm_seq(q + (size_t)h * D, qnorm_w, D, c->norm_eps);
+    if (rope_cos && rope_sin)
+        orc_rope_apply_all(q, Hq, D, c->rope_dim, c->rope_type, rope_cos, rope_sin, pos);
+    if (k && v) {
+        if (knorm_w)
+            for (int h = 0; h < Hkv; h++) orc_rms_norm_seq(k + (size_t)h * D, knorm_w, D, c->norm_eps);
+        for (int h = 0; h < Hkv; h++) orc_rms_norm_seq(v + (size_t)h * D, NULL, D, c->norm_eps);
+        if (rope_cos && rope_sin)
+            orc_rope_apply_all(k, Hkv, D, c->rope_dim, c->rope_type, rope_cos, rope_sin, pos);
+        orc_kv_store(kcache, pos, k, kv_dim);
+        orc_kv_store(vcache, pos, v, kv_dim);
+    }
+    const int start = (is_swa && c->sliding_window > 0 && pos - c->sliding_window + 1 > 0)
+                          ? pos - c->sliding_window + 1 : 0;
+    const int n = pos + 1 - start;
+    int nt = n_threads > 0 ? n_threads : 1;
+    (void)nt;
+#pragma omp parallel for num_threads(nt) schedule(dynamic, 1)
+    for (int h = 0; h < Hq; h++) {
+        const int kvh = h / kv_mul;
+        const float *qh = q + (size_t)h * D;
+        float *att = att_scratch + (size_t)h * n;
+        for (int t = start; t <= pos; t++) {
+            const float *kt = kcache + (size_t)t * kv_dim + (size_t)kvh * D;
+            float score = 0.0f;
+            for (int i = 0; i < D; i++) score += qh[i] * kt[i];
+            att[t - start] = score * 1.0f;
+        }
+        float max_val = -INFINITY;
+        for (int t = 0; t < n; t++)
+            if (att[t] > max_val) max_val = att[t];
+        float sum = 0.0f;
+        for (int t = 0; t < n; t++) {
+            float e = (float)exp((double)(att[t] - max_val));
+            att[t] = e;
+            sum += e;
+        }
+        float inv = 1.0f / sum;
+        for (int t = 0; t < n; t++) att[t] *= inv;
+        float *oh = out + (size_t)h * D;
+        for (int i = 0; i < D; i++) {
+            float val = 0.0f;
+            for (int t = start; t <= pos; t++)
+                val += att[t - start] * vcache[(size_t)t * kv_dim + (size_t)kvh * D + i];
+            oh[i] = val;
+        }
+    }
+}
+
 int orc_max_threads(void)
 {
 #ifdef _OPENMP

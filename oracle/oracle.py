@@ -122,6 +122,10 @@ def lib():
         L.orc_prefill_sequential_q8.argtypes = [
             C.POINTER(_Cfg), _I8, _F, _I8, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int,
             C.c_int, _F, C.c_int, C.c_int]
+        L.orc_rms_norm_seq.argtypes = [_F, _F, C.c_int, C.c_float]
+        L.orc_forward_gemma4.argtypes = [
+            C.POINTER(_Cfg), _F, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int, _F, _F,
+            C.c_int]
         _lib = L
     return _lib
 
@@ -348,6 +352,39 @@ def forward_from_projections_q8(cfg: OracleConfig, kq, ks, vq, vs, q, k, v, laye
     if gate is not None:
         out = sigmoid_gate(out, gate)
     return out, q, k
+
+
+def rms_norm_seq(x, w, eps) -> np.ndarray:
+    """RMSNorm.apply with offsets / applyNoScale (w None): sequential unfused sum of squares."""
+    x = f32(x).copy()
+    lib().orc_rms_norm_seq(_p(x), _p(f32(w)) if w is not None else None, x.size, float(eps))
+    return x
+
+
+def forward_gemma4(cfg: OracleConfig, kcache, vcache, q, k, v, pos, is_swa, qnorm_w=None,
+                   knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1):
+    """Attention half of Gemma4InferenceEngine.forwardLayer over one layer's cache
+    ([max_seq, kvDim] fp32, modified in place when the layer has its own KV).  k = v = None
+    is a shared-KV layer (reads the source layer's cache, appends nothing).  cfg.head_size is
+    the layer type's head size.  Returns (out, q_after, k_after, v_after)."""
+    c = cfg.c()
+    q = f32(q).copy()
+    k = f32(k).copy() if k is not None else None
+    v = f32(v).copy() if v is not None else None
+    for a in (kcache, vcache):
+        assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"] and a.size >= cfg.max_seq * cfg.kv_dim
+    assert 0 <= pos < cfg.max_seq
+    out = np.zeros(cfg.n_heads * cfg.head_size, np.float32)
+    att = np.zeros(cfg.n_heads * (pos + 1), np.float32)
+    lib().orc_forward_gemma4(
+        C.byref(c), _p(kcache), _p(vcache),
+        _p(f32(qnorm_w)) if qnorm_w is not None else None,
+        _p(f32(knorm_w)) if knorm_w is not None else None,
+        _p(f32(rope_cos)) if rope_cos is not None else None,
+        _p(f32(rope_sin)) if rope_sin is not None else None,
+        _p(q), _p(k) if k is not None else None, _p(v) if v is not None else None,
+        int(bool(is_swa)), pos, _p(out), _p(att), int(n_threads))
+    return out, q, k, v
 
 
 def max_threads() -> int:

@@ -50,7 +50,8 @@ def test_constants_match_header():
     text = open(HEADER).read()
     defs = dict((name, int(val)) for name, val in re.findall(r"#define\s+(LLMP_\w+)\s+(-?\d+)", text))
     for name in ("LLMP_KV_F32", "LLMP_KV_Q8_0", "LLMP_KV_Q8_0_TRUNC", "LLMP_ROPE_NORMAL", "LLMP_ROPE_NEOX",
-                 "LLMP_ROPE_SEL_NONE", "LLMP_ROPE_SEL_GLOBAL", "LLMP_ROPE_SEL_LOCAL"):
+                 "LLMP_ROPE_SEL_NONE", "LLMP_ROPE_SEL_GLOBAL", "LLMP_ROPE_SEL_LOCAL",
+                 "LLMP_NORM_SEQUENTIAL", "LLMP_NORM_V"):
         assert getattr(_lib, name) == defs[name], name
 
 

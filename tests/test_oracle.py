@@ -117,6 +117,21 @@ def test_rope_tables_match_angle_definition(R, theta):
     np.testing.assert_allclose(cos_t[:, 0], np.cos(np.arange(S)), atol=2e-7)
 
 
+def test_rope_freq_factors_divide_the_base_frequency():
+    # RoPE.java:86-89: baseFreq = (float)(1/pow(theta, 2i/R)); baseFreq /= freqFactors[i] for
+    # the pairs the factor array covers; angle = (float)(pos * freq)
+    R, S, theta = 128, 600, 1e6
+    ff = np.linspace(1.0, 8.0, R // 2 - 8).astype(F32)   # shorter than R/2: tail unscaled
+    cos_t, sin_t = orc.rope_tables(R, S, theta, freq_factors=ff)
+    i = np.arange(R // 2)
+    base = (1.0 / np.power(np.float64(F32(theta)), 2.0 * i / R)).astype(F32)
+    freq = base.copy()
+    freq[:ff.size] = (base[:ff.size] / ff).astype(F32)
+    ang = (np.arange(S, dtype=F32)[:, None] * freq[None, :]).astype(F32)
+    np.testing.assert_array_max_ulp(cos_t, np.cos(ang.astype(np.float64)).astype(F32), 1)
+    np.testing.assert_array_max_ulp(sin_t, np.sin(ang.astype(np.float64)).astype(F32), 1)
+
+
 def test_rope_linear_scale_divides_frequencies():
     R, S = 128, 64
     c1, s1 = orc.rope_tables(R, S * 8, 1e4)
@@ -707,3 +722,123 @@ def test_gptoss_moe_engine_windows_even_layers():
     for layer in range(4):
         assert hfp.is_global_layer(hfp.ARCH_GPT_OSS, layer, expert_count=32) == (layer % 2 == 1)
         assert hfp.is_global_layer(hfp.ARCH_GPT_OSS, layer) == (layer % 2 == 0)
+
+
+# ----------------------------------------------------------------- Gemma 4 attention layer
+def test_rms_norm_seq_closed_forms_and_eps_inside_the_root():
+    # constant c: sum of squares D*c^2 is exact, so r = 1/(float)sqrt(c^2 + eps) exactly
+    for D, cval, eps in ((256, 3.0, 1e-6), (512, -0.75, 1e-6), (256, 2.0, 0.5)):
+        x = np.full(D, cval, F32)
+        got = orc.rms_norm_seq(x, None, eps)
+        r = F32(1.0) / F32(np.sqrt(np.float64(F32(F32(cval * cval * D) / F32(D)) + F32(eps))))
+        assert np.array_equal(got, np.full(D, F32(F32(cval) * r)))
+    # eps = 0: scaling by a power of two leaves the normalised vector bit-identical
+    rng = np.random.default_rng(70)
+    x = rng.standard_normal(512).astype(F32)
+    w = rng.uniform(0.5, 1.5, 512).astype(F32)
+    assert np.array_equal(orc.rms_norm_seq(x, w, 0.0), orc.rms_norm_seq(x * F32(8.0), w, 0.0))
+
+
+def test_rms_norm_seq_matches_float64_and_uses_the_sequential_order():
+    rng = np.random.default_rng(71)
+    differs = 0
+    for D in (256, 512):
+        for _ in range(8):
+            x = (rng.standard_normal(D) * 3).astype(F32)
+            w = rng.uniform(0.5, 1.5, D).astype(F32)
+            got = orc.rms_norm_seq(x, w, 1e-6)
+            want = rm.rms_norm_heads(x, w, 1, D, 1e-6)
+            np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-7)
+            ss = F32(0.0)                      # RMSNorm.java:26-30, one float at a time
+            for v in x:
+                ss = F32(ss + F32(v * v))
+            r = F32(1.0) / F32(np.sqrt(np.float64(F32(ss / F32(D)) + F32(1e-6))))
+            assert np.array_equal(got, (x * r) * w)
+            differs += not np.array_equal(got, orc.per_head_norm(x, w, 1, D, 1e-6))
+    assert differs > 0   # the 8-lane FMA order of SimdVectorOps gives other last bits
+
+
+def _g4_tables(D, S, theta, factors=None):
+    return orc.rope_tables(D, S, theta, freq_factors=factors)
+
+
+def _g4_float64(q, k, v, kcache, vcache, qw, kw, cs, sn, Hq, Hkv, D, pos, start, eps):
+    """Gemma 4 attention half in float64: QK-norm, V-norm, NORMAL RoPE by the tables,
+    scale-1 softmax attention over rows [start, pos] (row pos from k, v when given)."""
+    def rope(x, nh):
+        x = np.asarray(x, np.float64).reshape(nh, D).copy()
+        c, s = cs[pos].astype(np.float64), sn[pos].astype(np.float64)
+        a, b = x[:, 0::2].copy(), x[:, 1::2].copy()
+        x[:, 0::2], x[:, 1::2] = a * c - b * s, a * s + b * c
+        return x.reshape(-1)
+    qn = rope(rm.rms_norm_heads(q, qw, Hq, D, eps), Hq)
+    K = kcache.astype(np.float64).copy()
+    V = vcache.astype(np.float64).copy()
+    if k is not None:
+        K[pos] = rope(rm.rms_norm_heads(k, kw, Hkv, D, eps), Hkv)
+        V[pos] = rm.rms_norm_heads(v, np.ones(D), Hkv, D, eps)
+    return rm.attention(qn, K, V, Hq, Hkv, D, start, pos, 1.0), K[pos], V[pos]
+
+
+@pytest.mark.parametrize("D,is_swa", [(256, True), (512, False)])
+def test_gemma4_layer_matches_float64(D, is_swa):
+    Hq, Hkv, S, W, pos = 8, 2, 96, 40, 77
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0, norm_eps=1e-6, sliding_window=W)
+    rng = np.random.default_rng(72 + D)
+    kc = np.zeros((S, Hkv * D), F32); vc = np.zeros((S, Hkv * D), F32)
+    kc[:pos] = rng.standard_normal((pos, Hkv * D)).astype(F32)
+    vc[:pos] = rng.standard_normal((pos, Hkv * D)).astype(F32)
+    q = rng.standard_normal(Hq * D).astype(F32) * F32(4)
+    k = rng.standard_normal(Hkv * D).astype(F32) * F32(4)
+    v = rng.standard_normal(Hkv * D).astype(F32) * F32(4)
+    qw = rng.uniform(0.5, 1.5, D).astype(F32)
+    kw = rng.uniform(0.5, 1.5, D).astype(F32)
+    factors = None if is_swa else np.linspace(1.0, 4.0, D // 2).astype(F32)
+    cs, sn = _g4_tables(D, S, 1e4 if is_swa else 1e6, factors)
+    kc0 = kc.copy()
+    out, q2, k2, v2 = orc.forward_gemma4(cfg, kc, vc, q, k, v, pos, is_swa, qnorm_w=qw,
+                                         knorm_w=kw, rope_cos=cs, rope_sin=sn)
+    start = pos - W + 1 if is_swa else 0
+    want, krow, vrow = _g4_float64(q, k, v, kc0, vc, qw, kw, cs, sn, Hq, Hkv, D, pos, start, 1e-6)
+    rm.assert_close(out, want, atol=2e-5, rtol=1e-4, what=f"gemma4 D={D}")
+    np.testing.assert_allclose(kc[pos], krow, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(vc[pos], vrow, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(kc[pos], k2) and np.array_equal(vc[pos], v2)
+    assert np.array_equal(np.delete(kc, pos, 0), np.delete(kc0, pos, 0))
+    # the stored V row is the weightless sequential norm of v, K the weighted one then RoPE
+    for h in range(Hkv):
+        assert np.array_equal(v2[h * D:(h + 1) * D], orc.rms_norm_seq(v[h * D:(h + 1) * D], None, 1e-6))
+
+
+def test_gemma4_shared_layer_reads_the_source_cache_and_appends_nothing():
+    Hq, Hkv, D, S, pos = 4, 1, 256, 64, 50
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0, norm_eps=1e-6, sliding_window=20)
+    rng = np.random.default_rng(73)
+    kc = rng.standard_normal((S, D)).astype(F32)
+    vc = rng.standard_normal((S, D)).astype(F32)
+    q = rng.standard_normal(Hq * D).astype(F32)
+    qw = rng.uniform(0.5, 1.5, D).astype(F32)
+    cs, sn = _g4_tables(D, S, 1e4)
+    kc0, vc0 = kc.copy(), vc.copy()
+    out, _, _, _ = orc.forward_gemma4(cfg, kc, vc, q, None, None, pos, True, qnorm_w=qw,
+                                      rope_cos=cs, rope_sin=sn)
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
+    want, _, _ = _g4_float64(q, None, None, kc0, vc0, qw, None, cs, sn, Hq, Hkv, D, pos,
+                             pos - 19, 1e-6)
+    rm.assert_close(out, want, atol=2e-5, rtol=1e-4, what="gemma4 shared layer")
+
+
+@pytest.mark.parametrize("pos", [18, 19, 20, 33])
+def test_gemma4_window_boundaries_by_uniform_scores(pos):
+    # q = 0: every score is 0, so the output is the mean of V over the attended rows
+    Hq, Hkv, D, S, W = 2, 1, 256, 40, 20
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0, norm_eps=1e-6, sliding_window=W)
+    rng = np.random.default_rng(74)
+    kc = rng.standard_normal((S, D)).astype(F32)
+    vc = rng.standard_normal((S, D)).astype(F32)
+    q = np.zeros(Hq * D, F32)
+    for is_swa in (True, False):
+        out, _, _, _ = orc.forward_gemma4(cfg, kc.copy(), vc.copy(), q, None, None, pos, is_swa)
+        start = max(0, pos - W + 1) if is_swa else 0
+        mean = vc[start:pos + 1].astype(np.float64).mean(axis=0)
+        np.testing.assert_allclose(out.reshape(Hq, D), np.tile(mean, (Hq, 1)), atol=2e-6)
