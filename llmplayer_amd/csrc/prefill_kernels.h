@@ -167,9 +167,9 @@ inline size_t prefill_append_lds(int Hkv, int D, bool stage_v) {
 
 // ---- LDS tile layout (also the workspace image of a tile) -------------------------------------
 // LDS tile: K hi/lo [TK keys][D + 8] bf16, V^T hi/lo [D][TK + 4] (row padding spreads banks).
-template <int D>
+template <int D, int TKEYS = tile_keys<D>()>
 struct alignas(16) TileLds {
-    static constexpr int TK = tile_keys<D>();
+    static constexpr int TK = TKEYS;
     static constexpr int KP = D + 8;   // K row pitch (bf16 elements; 16-byte multiple)
     // V^T row pitch: 8-byte multiple with an odd number of 8-byte units beyond a 32-dword
     // multiple (TK + 4 bf16 = 2*(TK/2 + 2) dwords), so the 16 dims of a lane row-group's 8-byte
@@ -417,18 +417,23 @@ __device__ __forceinline__ void img_store(const u32x4 (&stage)[PER], void* dst, 
 // every call).  K: items (row, 4-dim chunk); V: items (4 keys, 4-dim chunk), stored transposed
 // as 8-byte runs; the chunk index runs fastest across lanes so every load reads whole rows.  Rows at or past row_lim
 // repeat row row_lim (never attended, finite).
-template <int D, int NTHR>
+// Keys per LDS tile of the direct-staging launches: 32, so two workgroups' double-buffered
+// tiles fit in a CU's 160 KB of LDS (64-key tiles of head_dim 128 take 136 KB per workgroup).
+template <int D>
+constexpr int direct_tile_keys() { return 32; }
+
+template <int D, int NTHR, int TK_ = direct_tile_keys<D>()>
 struct RawTile {
-    static constexpr int TK = TileLds<D>::TK;
+    static constexpr int TK = TK_;
     static constexpr int NK = TK * (D / 4), NV = (TK / 4) * (D / 4);
     static constexpr int KI = (NK + NTHR - 1) / NTHR, VI = (NV + NTHR - 1) / NTHR;
 };
 
-template <int D, int NTHR, int KI, int VI, bool Q8>
+template <int D, int NTHR, int KI, int VI, bool Q8, int TK = direct_tile_keys<D>()>
 __device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4],
                                          const HeadRows& kr, const HeadRows& vr, int t0,
                                          int row_lim, int tid) {
-    using R = RawTile<D, NTHR>;
+    using R = RawTile<D, NTHR, TK>;
     static_assert(KI == R::KI && VI == R::VI, "staging register counts");
 #pragma unroll
     for (int i = 0; i < R::KI; ++i) {
@@ -445,12 +450,12 @@ __device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4]
     }
 }
 
-template <int D, int NTHR, int KI, int VI, bool Q8>
+template <int D, int NTHR, int KI, int VI, bool Q8, int TK = direct_tile_keys<D>()>
 __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4 (&vx)[VI][4],
-                                          TileLds<D>& t, int tid) {
-    using R = RawTile<D, NTHR>;
+                                          TileLds<D, TK>& t, int tid) {
+    using R = RawTile<D, NTHR, TK>;
     static_assert(KI == R::KI && VI == R::VI, "staging register counts");
-    using T = TileLds<D>;
+    using T = TileLds<D, TK>;
 #pragma unroll
     for (int i = 0; i < R::KI; ++i) {
         const int e = tid + i * NTHR;
@@ -492,7 +497,7 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
                                                                             const uint4* ws,
                                                                             int tile0, int n_tiles,
                                                                             int ksplit) {
-    using T = TileLds<D>;
+    using T = TileLds<D, DIRECT ? direct_tile_keys<D>() : tile_keys<D>()>;
     constexpr int HG = G / HPW;
     constexpr int NTHR = HG * NB * 64;
     constexpr int KS = D / 32, DT = D / 16, TK = T::TK, NKT = TK / 16, NC = TK / 32;
@@ -538,7 +543,7 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
 
     const uint4* img = ws + (size_t)kvh * n_tiles * IMG;
     const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);   // DIRECT staging
-    using RT = RawTile<D, NTHR>;
+    using RT = RawTile<D, NTHR, T::TK>;
     u32x4 stage[DIRECT ? 1 : PER];
     floatx4 kx[RT::KI], vx[RT::VI][4];   // used by DIRECT staging only
     floatx4 o[HPW][DT];
@@ -553,10 +558,10 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
 
     if (t_first <= t_last) {   // a split past the item's last tile has no keys (neutral partial)
         if constexpr (DIRECT) {
-            raw_load<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, kr, vr, t_first * TK, kend - 1, tid);
-            raw_store<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, buf[0], tid);
+            raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, t_first * TK, kend - 1, tid);
+            raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, buf[0], tid);
             if (t_first + 1 <= t_last)
-                raw_load<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, kr, vr, (t_first + 1) * TK, kend - 1, tid);
+                raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (t_first + 1) * TK, kend - 1, tid);
         } else {
             img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
             img_store<PER, NTHR, IMG>(stage, &buf[0], tid);
@@ -675,9 +680,9 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
         // buffer written here was last read before the previous iteration's barrier.
         if (tile + 1 <= t_last) {
             if constexpr (DIRECT) {
-                raw_store<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, buf[(tile + 1 - t_first) & 1], tid);
+                raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, buf[(tile + 1 - t_first) & 1], tid);
                 if (tile + 2 <= t_last)
-                    raw_load<D, NTHR, RT::KI, RT::VI, Q8>(kx, vx, kr, vr, (tile + 2) * TK, kend - 1, tid);
+                    raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (tile + 2) * TK, kend - 1, tid);
             } else {
                 img_store<PER, NTHR, IMG>(stage, &buf[(tile + 1 - t_first) & 1], tid);
                 if (tile + 2 <= t_last)
