@@ -209,22 +209,7 @@ int orc_is_global_layer(int arch, int layer)
 
 /* Layer-independent attention hyper-parameters (the subset of ModelConfig read by
  * Attention.java:284-367). */
-typedef struct {
-    int n_heads;          /* headCount */
-    int n_kv_heads;       /* headCountKV */
-    int head_size;        /* headSize */
-    int rope_dim;         /* ropeDimensionCount */
-    int rope_type;        /* 0 = NORMAL, 2 = NEOX */
-    int max_seq;          /* KV cache capacity */
-    float norm_eps;       /* normEps (QK-norm) */
-    int sliding_window;   /* 0 = none */
-    float attention_scale;/* > 0 overrides 1/sqrt(headSize) */
-    float softcap;        /* attnLogitSoftCap, 0 = off */
-    int arch;             /* ORC_ARCH_* */
-    int no_rope_interval; /* noRopeLayerInterval, 0 = off */
-    int nope_on_global;   /* useNoPeOnGlobalLayers */
-    const float *sinks;   /* per query head attention-sink logits (GPT-OSS), NULL = none */
-} orc_cfg;
+#include "orc.h"
 
 /* KVCache.storeK / storeV (KVCache.java:164-179), FLOAT32 mode: cache[layer][pos*kvDim + j]. */
 void orc_kv_store(float *cache_layer, int pos, const float *x, int kv_dim)

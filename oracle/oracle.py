@@ -43,6 +43,19 @@ class _Cfg(C.Structure):
     ]
 
 
+class _BlockW(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int), ("residual_scale", C.c_float),
+        ("attn_norm", C.POINTER(C.c_float)), ("post_attn_norm", C.POINTER(C.c_float)),
+        ("wq", C.POINTER(C.c_uint8)), ("wk", C.POINTER(C.c_uint8)), ("wv", C.POINTER(C.c_uint8)),
+        ("wqkv", C.POINTER(C.c_uint8)), ("wo", C.POINTER(C.c_uint8)),
+        ("wq_type", C.c_int), ("wk_type", C.c_int), ("wv_type", C.c_int), ("wqkv_type", C.c_int),
+        ("wo_type", C.c_int),
+        ("q_bias", C.POINTER(C.c_float)), ("k_bias", C.POINTER(C.c_float)),
+        ("v_bias", C.POINTER(C.c_float)), ("o_bias", C.POINTER(C.c_float)),
+    ]
+
+
 @dataclass
 class OracleConfig:
     """Attention hyper-parameters read by Attention.forwardFromProjections."""
@@ -126,6 +139,19 @@ def lib():
         L.orc_forward_gemma4.argtypes = [
             C.POINTER(_Cfg), _F, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, C.c_int, _F, _F,
             C.c_int]
+        _U8 = C.POINTER(C.c_uint8)
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_ggml_block.restype = C.c_int
+        L.orc_ggml_block.argtypes = [C.c_int, C.POINTER(C.c_int)]
+        L.orc_dequant_row.restype = C.c_int
+        L.orc_dequant_row.argtypes = [C.c_int, _U8, C.c_int, _F]
+        L.orc_matmul.restype = C.c_int
+        L.orc_matmul.argtypes = [C.c_int, _U8, C.c_int, C.c_int, _F, _F]
+        L.orc_rmsnorm.argtypes = [_F, _F, _F, C.c_int, C.c_float]
+        L.orc_attn_block.restype = C.c_int
+        L.orc_attn_block.argtypes = [C.POINTER(_Cfg), C.POINTER(_BlockW), _F, _F, _F, _F, _F,
+                                     _F, _F, C.c_int, C.c_int, C.c_int]
         _lib = L
     return _lib
 
@@ -385,6 +411,133 @@ def forward_gemma4(cfg: OracleConfig, kcache, vcache, q, k, v, pos, is_swa, qnor
         _p(q), _p(k) if k is not None else None, _p(v) if v is not None else None,
         int(bool(is_swa)), pos, _p(out), _p(att), int(n_threads))
     return out, q, k, v
+
+
+# ---- attention half of a layer over GGUF-format projection weights ----------------------
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 14, 30
+
+
+def f16_to_f32(h: int) -> np.float32:
+    """Float16.toFloat (Float16.java:11-34)."""
+    return np.float32(lib().orc_f16_to_f32(int(h) & 0xFFFF))
+
+
+def ggml_block(t: int):
+    """(weights per block, bytes per block) of a GGMLType id (GGMLType.java:4-35)."""
+    b = C.c_int()
+    n = lib().orc_ggml_block(int(t), C.byref(b))
+    if n == 0:
+        raise ValueError(f"unsupported GGML type {t}")
+    return n, b.value
+
+
+def ggml_row_bytes(t: int, cols: int) -> int:
+    n, b = ggml_block(t)
+    assert cols % n == 0
+    return cols // n * b
+
+
+def _u8p(a):
+    assert a.dtype == np.uint8 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.POINTER(C.c_uint8))
+
+
+def dequant_rows(t: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Dequantised [rows, cols] weights exactly as the tensor class's dot() stages them."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1)
+    rb = ggml_row_bytes(t, cols)
+    assert w.size >= rows * rb
+    out = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        seg = w[r * rb:(r + 1) * rb]
+        assert lib().orc_dequant_row(int(t), _u8p(seg), cols, _p(out[r])) == 0
+    return out
+
+
+def matmul(t: int, w: np.ndarray, rows: int, cols: int, x, out=None) -> np.ndarray:
+    """FloatTensor.matmulParallel: out[row] += dot(row, x)."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1)
+    x = f32(x)
+    out = np.zeros(rows, np.float32) if out is None else f32(out).copy()
+    assert w.size >= rows * ggml_row_bytes(t, cols) and x.size >= cols
+    assert lib().orc_matmul(int(t), _u8p(w), rows, cols, _p(x), _p(out)) == 0
+    return out
+
+
+def rmsnorm(x, w, eps) -> np.ndarray:
+    """SimdVectorOps.rmsnorm."""
+    x = f32(x)
+    out = np.zeros_like(x)
+    lib().orc_rmsnorm(_p(out), _p(x), _p(f32(w)), x.size, float(eps))
+    return out
+
+
+@dataclass
+class BlockWeights:
+    """Projection weights of one layer's attention half: raw GGUF bytes (uint8) with their
+    GGMLType, fp32 norms and biases.  wqkv (merged) replaces wq/wk/wv when given."""
+    dim: int
+    wq: Optional[np.ndarray] = None
+    wk: Optional[np.ndarray] = None
+    wv: Optional[np.ndarray] = None
+    wo: Optional[np.ndarray] = None
+    wq_type: int = GGML_F32
+    wk_type: int = GGML_F32
+    wv_type: int = GGML_F32
+    wo_type: int = GGML_F32
+    wqkv: Optional[np.ndarray] = None
+    wqkv_type: int = GGML_F32
+    attn_norm: Optional[np.ndarray] = None
+    post_attn_norm: Optional[np.ndarray] = None
+    q_bias: Optional[np.ndarray] = None
+    k_bias: Optional[np.ndarray] = None
+    v_bias: Optional[np.ndarray] = None
+    o_bias: Optional[np.ndarray] = None
+    residual_scale: float = 0.0
+
+    def c(self):
+        keep = []
+
+        def fp(a):
+            if a is None:
+                return None
+            a = f32(a)
+            keep.append(a)
+            return a.ctypes.data_as(C.POINTER(C.c_float))
+
+        def up(a):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, np.uint8)
+            keep.append(a)
+            return a.ctypes.data_as(C.POINTER(C.c_uint8))
+        s = _BlockW(self.dim, float(self.residual_scale), fp(self.attn_norm),
+                    fp(self.post_attn_norm), up(self.wq), up(self.wk), up(self.wv),
+                    up(self.wqkv), up(self.wo), self.wq_type, self.wk_type, self.wv_type,
+                    self.wqkv_type, self.wo_type, fp(self.q_bias), fp(self.k_bias),
+                    fp(self.v_bias), fp(self.o_bias))
+        return s, keep
+
+
+def attn_block(cfg: OracleConfig, bw: BlockWeights, kcache, vcache, x, layer, pos,
+               qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1):
+    """The attention half of TransformerBlock.forward (pre-norm, projections, attention core,
+    Wo, post-norm, residual scale, residual add) over fp32 caches [max_seq, kvDim] (row `pos`
+    appended).  Returns the updated residual x [dim]."""
+    c = cfg.c()
+    s, keep = bw.c()
+    x = f32(x).copy()
+    assert x.size == bw.dim
+    rc = lib().orc_attn_block(
+        C.byref(c), C.byref(s), _p(kcache), _p(vcache),
+        _p(f32(qnorm_w)) if qnorm_w is not None else None,
+        _p(f32(knorm_w)) if knorm_w is not None else None,
+        _p(f32(rope_cos)) if rope_cos is not None else None,
+        _p(f32(rope_sin)) if rope_sin is not None else None,
+        _p(x), layer, pos, int(n_threads))
+    assert rc == 0, "unsupported weight type or shape"
+    del keep
+    return x
 
 
 def max_threads() -> int:

@@ -1,0 +1,148 @@
+"""Packers for the GGUF weight formats of the reference's tensor classes, written from each
+format's layout (the inverse direction of the dequantisers in oracle/block_oracle.c and of
+the library's repacking), plus the exact float32 values each packed weight stands for.
+
+Every packer takes the format's fields (scales, mins, quants) and returns (bytes [rows,
+row_bytes] uint8, dequantised values [rows, cols] float32), the values computed in float32
+in the reference's operation order (Q8_0FloatTensor, Q4_0FloatTensor, Q4_KFloatTensor and
+Q6_KFloatTensor dot()).  Random fields give test weights whose dequantised values are known
+without running the code under test."""
+import numpy as np
+
+F32 = np.float32
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 14, 30
+
+
+def _f16_bits(x):
+    return np.asarray(x, np.float16).view(np.uint16)
+
+
+def _f16_val(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(F32)
+
+
+def pack_f32(w):
+    w = np.ascontiguousarray(w, F32)
+    return w.view(np.uint8).reshape(w.shape[0], -1).copy(), w.copy()
+
+
+def pack_f16(w):
+    h = np.asarray(w, np.float16)
+    return h.view(np.uint8).reshape(h.shape[0], -1).copy(), h.astype(F32)
+
+
+def pack_bf16(w):
+    bits = (np.ascontiguousarray(w, F32).view(np.uint32) >> 16).astype(np.uint16)
+    vals = (bits.astype(np.uint32) << 16).view(F32)
+    return bits.view(np.uint8).reshape(bits.shape[0], -1).copy(), vals
+
+
+def pack_q8_0(d_bits, q):
+    """d_bits [rows, nb] fp16 scale bits, q [rows, nb*32] int8.  Block: d (2 B) + 32 int8."""
+    rows, nb = d_bits.shape
+    out = np.zeros((rows, nb, 34), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, nb, 2)
+    out[:, :, 2:] = np.asarray(q, np.int8).reshape(rows, nb, 32).view(np.uint8)
+    vals = (_f16_val(d_bits)[..., None] * q.reshape(rows, nb, 32).astype(F32)).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_q4_0(d_bits, q):
+    """q [rows, nb*32] in 0..15; byte i of a block holds element 2i (low nibble) and 2i+1
+    (high nibble), as Q4_0FloatTensor reads it."""
+    rows, nb = d_bits.shape
+    qb = np.asarray(q, np.uint8).reshape(rows, nb, 16, 2)
+    out = np.zeros((rows, nb, 18), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, nb, 2)
+    out[:, :, 2:] = qb[..., 0] | (qb[..., 1] << 4)
+    vals = ((q.reshape(rows, nb, 32).astype(np.int32) - 8).astype(F32) *
+            _f16_val(d_bits)[..., None]).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_q4_k(d_bits, dmin_bits, sc, mn, q):
+    """Super-blocks of 256: d, dmin fp16; 8 six-bit scales and mins packed in 12 bytes
+    (j < 4: bytes j and j+4 hold scale/min j in their low 6 bits and the top 2 bits of
+    scale/min j+4; byte j+8 holds the low 4 bits of scale j+4 and of min j+4); 128 bytes of
+    nibbles: byte 32g+l = element 64g+l (low) | element 64g+32+l (high).
+    sc, mn [rows, ns, 8] in 0..63; q [rows, ns*256] in 0..15."""
+    rows, ns = d_bits.shape
+    out = np.zeros((rows, ns, 144), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    out[:, :, 2:4] = np.asarray(dmin_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    sc = np.asarray(sc, np.uint8)
+    mn = np.asarray(mn, np.uint8)
+    for j in range(4):
+        out[:, :, 4 + j] = (sc[..., j] & 63) | ((sc[..., j + 4] >> 4) << 6)
+        out[:, :, 8 + j] = (mn[..., j] & 63) | ((mn[..., j + 4] >> 4) << 6)
+        out[:, :, 12 + j] = (sc[..., j + 4] & 15) | ((mn[..., j + 4] & 15) << 4)
+    qq = np.asarray(q, np.uint8).reshape(rows, ns, 4, 2, 32)   # [group][half][l]
+    out[:, :, 16:] = (qq[:, :, :, 0, :] | (qq[:, :, :, 1, :] << 4)).reshape(rows, ns, 128)
+    d = _f16_val(d_bits)[..., None, None, None]
+    dmin = _f16_val(dmin_bits)[..., None, None, None]
+    scf = sc.reshape(rows, ns, 4, 2).astype(F32)[..., None]      # sub-block 2g+half
+    mnf = mn.reshape(rows, ns, 4, 2).astype(F32)[..., None]
+    ds = (d * scf).astype(F32)
+    dm = (dmin * mnf).astype(F32)
+    vals = ((ds * qq.astype(F32)).astype(F32) - dm).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_q6_k(d_bits, sc, q):
+    """Super-blocks of 256 (210 bytes): ql[128] low nibbles, qh[64] high 2-bit pairs, 16 int8
+    scales, d fp16 at byte 208.  Element 128h + 32c + l (c = 0..3) takes its low nibble from
+    ql[64h + l] (c = 0: low, c = 2: high nibble) or ql[64h + 32 + l] (c = 1: low, c = 3:
+    high), its high two bits from bits 2c..2c+1 of qh[32h + l], and scale sc[8h + l/16 + 2c].
+    sc [rows, ns, 16] int8; q [rows, ns*256] in 0..63."""
+    rows, ns = d_bits.shape
+    qq = np.asarray(q, np.uint8).reshape(rows, ns, 2, 4, 32)    # [half][c][l]
+    out = np.zeros((rows, ns, 210), np.uint8)
+    lo = qq & 15
+    hi = qq >> 4
+    ql = np.zeros((rows, ns, 2, 64), np.uint8)
+    ql[..., 0:32] = lo[:, :, :, 0, :] | (lo[:, :, :, 2, :] << 4)
+    ql[..., 32:64] = lo[:, :, :, 1, :] | (lo[:, :, :, 3, :] << 4)
+    qh = hi[:, :, :, 0, :] | (hi[:, :, :, 1, :] << 2) | (hi[:, :, :, 2, :] << 4) | (hi[:, :, :, 3, :] << 6)
+    out[:, :, 0:128] = ql.reshape(rows, ns, 128)
+    out[:, :, 128:192] = qh.reshape(rows, ns, 64)
+    out[:, :, 192:208] = np.asarray(sc, np.int8).view(np.uint8)
+    out[:, :, 208:210] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    d = _f16_val(d_bits)
+    scv = np.asarray(sc, np.int8).astype(F32)                    # [rows, ns, 16]
+    l = np.arange(32)
+    vals = np.zeros((rows, ns, 2, 4, 32), F32)
+    for h in range(2):
+        for c in range(4):
+            si = 8 * h + l // 16 + 2 * c
+            ds = (d[..., None] * scv[:, :, si]).astype(F32)
+            vals[:, :, h, c, :] = (ds * (qq[:, :, h, c, :].astype(F32) - 32)).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def random_weights(t, rows, cols, rng, scale=0.05):
+    """Random weights of GGML type t with magnitudes around `scale`: (bytes, float32 values)."""
+    if t == GGML_F32:
+        return pack_f32(rng.standard_normal((rows, cols)).astype(F32) * F32(scale))
+    if t == GGML_F16:
+        return pack_f16(rng.standard_normal((rows, cols)).astype(F32) * F32(scale))
+    if t == GGML_BF16:
+        return pack_bf16(rng.standard_normal((rows, cols)).astype(F32) * F32(scale))
+    if t == GGML_Q8_0:
+        nb = cols // 32
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, nb)) * scale / 64)
+        return pack_q8_0(d, rng.integers(-128, 128, (rows, cols)).astype(np.int8))
+    if t == GGML_Q4_0:
+        nb = cols // 32
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, nb)) * scale / 4)
+        return pack_q4_0(d, rng.integers(0, 16, (rows, cols)))
+    if t == GGML_Q4_K:
+        ns = cols // 256
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 256)
+        dmin = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 64)
+        return pack_q4_k(d, dmin, rng.integers(0, 64, (rows, ns, 8)), rng.integers(0, 64, (rows, ns, 8)),
+                         rng.integers(0, 16, (rows, cols)))
+    if t == GGML_Q6_K:
+        ns = cols // 256
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 1024)
+        return pack_q6_k(d, rng.integers(-128, 128, (rows, ns, 16)), rng.integers(0, 64, (rows, cols)))
+    raise ValueError(t)

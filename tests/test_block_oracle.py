@@ -1,0 +1,197 @@
+"""Pins the oracle's attention-block restatement (oracle/block_oracle.c) before it is trusted.
+
+Dequantisation is checked against tests/ggml_pack.py, which packs each format from its layout
+in the opposite direction and computes the values in float32 independently; Float16 against
+numpy; the matmul and RMSNorm against float64; the whole block against a float64 chain and
+against identities a slip would break (zero output projection leaves the residual, merged
+and separate QKV agree, the bias and residual scale enter once)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests import ggml_pack as gp
+from tests import refmath as rm
+
+F32 = np.float32
+TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
+         gp.GGML_Q6_K]
+NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k"}
+
+
+def test_f16_conversion_matches_ieee_half_for_every_pattern():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = bits.view(np.float16).astype(F32)
+    got = np.array([orc.f16_to_f32(b) for b in bits], F32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
+def test_dequantised_values_match_the_packer(t):
+    rng = np.random.default_rng(80 + t)
+    rows, cols = 5, 512
+    wb, vals = gp.random_weights(t, rows, cols, rng)
+    got = orc.dequant_rows(t, wb, rows, cols)
+    assert np.array_equal(got.view(np.uint32), vals.view(np.uint32))
+
+
+def test_q4_0_nibbles_interleave_within_a_block():
+    # Q4_0FloatTensor: element 2i is the low nibble of byte i, element 2i+1 the high nibble
+    q = np.full((1, 32), 8, np.int64)
+    q[0, 5] = 9                                   # element 5: byte 2, high nibble
+    wb, _ = gp.pack_q4_0(np.array([[0x3C00]], np.uint16), q)   # d = 1.0
+    assert wb[0, 2 + 2] == (8 | (9 << 4))
+    got = orc.dequant_rows(gp.GGML_Q4_0, wb, 1, 32)[0]
+    assert got[5] == 1.0 and np.count_nonzero(got) == 1
+
+
+def test_q4_k_sub_block_scales_and_mins_are_distinct():
+    # every sub-block gets its own (scale, min), with the top bits of sub-blocks 4..7 set, so
+    # a wrong index or bit position in the 12-byte unpacking moves some value
+    sc = np.array([[[1, 2, 3, 4, 49, 50, 61, 63]]])
+    mn = np.array([[[5, 6, 7, 8, 33, 40, 52, 62]]])
+    q = np.tile(np.arange(32) % 16, 8).reshape(1, 256)
+    wb, vals = gp.pack_q4_k(np.array([[0x3C00]], np.uint16), np.array([[0x3800]], np.uint16), sc, mn, q)
+    got = orc.dequant_rows(gp.GGML_Q4_K, wb, 1, 256)[0]
+    assert np.array_equal(got, vals[0])
+    for s in range(8):
+        seg = got[32 * s:32 * s + 32]
+        # d = 1, dmin = 0.5: value = sc*q - 0.5*m
+        assert np.array_equal(seg, (sc[0, 0, s] * (np.arange(32) % 16) - 0.5 * mn[0, 0, s]).astype(F32))
+
+
+def test_q6_k_quarters_take_their_own_scales():
+    sc = np.arange(1, 17, dtype=np.int8).reshape(1, 1, 16) * np.int8(3) - np.int8(20)
+    q = np.full((1, 256), 33, np.int64)           # (q - 32) = 1: value = d * scale
+    wb, vals = gp.pack_q6_k(np.array([[0x3C00]], np.uint16), sc, q)
+    got = orc.dequant_rows(gp.GGML_Q6_K, wb, 1, 256)[0]
+    assert np.array_equal(got, vals[0])
+    for e in (0, 15, 16, 31, 32, 64, 96, 127, 128, 144, 200, 255):
+        h, r = divmod(e, 128)
+        c, l = divmod(r, 32)
+        assert got[e] == sc[0, 0, 8 * h + l // 16 + 2 * c]
+
+
+@pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
+def test_matmul_matches_float64_and_accumulates(t):
+    rng = np.random.default_rng(90 + t)
+    rows, cols = 24, 768
+    wb, vals = gp.random_weights(t, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(F32)
+    base = rng.standard_normal(rows).astype(F32)
+    got = orc.matmul(t, wb, rows, cols, x, out=base)
+    want = base.astype(np.float64) + vals.astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("t", [gp.GGML_F16, gp.GGML_BF16], ids=["f16", "bf16"])
+def test_half_precision_rows_sum_sequentially_unfused(t):
+    # FloatTensor.dot: sum += getFloat(i) * other[i], one float at a time
+    rng = np.random.default_rng(95)
+    wb, vals = gp.random_weights(t, 1, 64, rng, scale=1.0)
+    x = rng.standard_normal(64).astype(F32)
+    s = F32(0.0)
+    for w, xv in zip(vals[0], x):
+        s = F32(s + F32(w * xv))
+    assert orc.matmul(t, wb, 1, 64, x)[0] == s
+
+
+def test_rmsnorm_matches_float64_and_closed_form():
+    rng = np.random.default_rng(96)
+    x = rng.standard_normal(3072).astype(F32) * F32(5)
+    w = rng.uniform(0.5, 1.5, 3072).astype(F32)
+    got = orc.rmsnorm(x, w, 1e-5)
+    np.testing.assert_allclose(got, rm.rms_norm_heads(x, w, 1, 3072, 1e-5), rtol=2e-6, atol=1e-7)
+    c = np.full(256, 3.0, F32)                     # ss = 2304 exactly: r = 1/(float)sqrt(9 + eps)
+    r = F32(1.0) / F32(np.sqrt(np.float64(F32(F32(2304.0) / F32(256)) + F32(1e-6))))
+    assert np.array_equal(orc.rmsnorm(c, np.ones(256, F32), 1e-6), np.full(256, F32(3.0) * r))
+
+
+def _block_setup(seed, t, merged=False, post=False, bias=False, rscale=0.0):
+    Hq, Hkv, D, dim, S = 4, 2, 64, 256, 40
+    qd, kvd = Hq * D, Hkv * D
+    rng = np.random.default_rng(seed)
+    cfg = orc.OracleConfig(Hq, Hkv, D, S, rope_type=0, norm_eps=1e-5)
+    wq, vq = gp.random_weights(t, qd, dim, rng)
+    wk, vk = gp.random_weights(t, kvd, dim, rng)
+    wv, vv = gp.random_weights(t, kvd, dim, rng)
+    wo, vo = gp.random_weights(t, dim, qd, rng)
+    bw = orc.BlockWeights(dim, wo=wo, wo_type=t, residual_scale=rscale,
+                          attn_norm=rng.uniform(0.5, 1.5, dim).astype(F32))
+    if merged:
+        bw.wqkv, bw.wqkv_type = np.concatenate([wq, wk, wv]), t
+    else:
+        bw.wq, bw.wk, bw.wv = wq, wk, wv
+        bw.wq_type = bw.wk_type = bw.wv_type = t
+    if post:
+        bw.post_attn_norm = rng.uniform(0.5, 1.5, dim).astype(F32)
+    if bias:
+        bw.q_bias = rng.standard_normal(qd).astype(F32) * F32(0.1)
+        bw.k_bias = rng.standard_normal(kvd).astype(F32) * F32(0.1)
+        bw.v_bias = rng.standard_normal(kvd).astype(F32) * F32(0.1)
+        bw.o_bias = rng.standard_normal(dim).astype(F32) * F32(0.1)
+    kc = np.zeros((S, kvd), F32); vc = np.zeros((S, kvd), F32)
+    pos = 30
+    kc[:pos] = rng.standard_normal((pos, kvd)).astype(F32)
+    vc[:pos] = rng.standard_normal((pos, kvd)).astype(F32)
+    x = rng.standard_normal(dim).astype(F32) * F32(2)
+    cs, sn = orc.rope_tables(D, S, 5e5)
+    return cfg, bw, (vq, vk, vv, vo), kc, vc, x, pos, cs, sn
+
+
+@pytest.mark.parametrize("t", [gp.GGML_F32, gp.GGML_Q8_0, gp.GGML_Q4_K, gp.GGML_Q6_K],
+                         ids=["f32", "q8_0", "q4_k", "q6_k"])
+@pytest.mark.parametrize("post,bias,rscale", [(False, False, 0.0), (True, True, 0.25)],
+                         ids=["prenorm", "postnorm-bias-granite"])
+def test_attn_block_matches_float64_chain(t, post, bias, rscale):
+    cfg, bw, (vq, vk, vv, vo), kc, vc, x, pos, cs, sn = _block_setup(100 + t, t, post=post,
+                                                                    bias=bias, rscale=rscale)
+    kc0, vc0 = kc.copy(), vc.copy()
+    got = orc.attn_block(cfg, bw, kc, vc, x, 0, pos, rope_cos=cs, rope_sin=sn)
+    Hq, Hkv, D = 4, 2, 64
+    x64 = x.astype(np.float64)
+    xb = rm.rms_norm_heads(x, bw.attn_norm, 1, 256, 1e-5)
+    q = vq.astype(np.float64) @ xb
+    k = vk.astype(np.float64) @ xb
+    v = vv.astype(np.float64) @ xb
+    if bias:
+        q += bw.q_bias; k += bw.k_bias; v += bw.v_bias
+    c, s = cs[pos].astype(np.float64), sn[pos].astype(np.float64)
+
+    def rope(z, nh):
+        z = z.reshape(nh, D).copy()
+        a, b = z[:, 0::2].copy(), z[:, 1::2].copy()
+        z[:, 0::2], z[:, 1::2] = a * c - b * s, a * s + b * c
+        return z.reshape(-1)
+    K, V = kc0.astype(np.float64), vc0.astype(np.float64)
+    K[pos], V[pos] = rope(k, Hkv), v
+    att = rm.attention(rope(q, Hq), K, V, Hq, Hkv, D, 0, pos, 1 / np.sqrt(D))
+    o = vo.astype(np.float64) @ att
+    if bias:
+        o += bw.o_bias
+    if post:
+        o = rm.rms_norm_heads(o, bw.post_attn_norm, 1, 256, 1e-5)
+    if rscale > 0:
+        o *= rscale
+    np.testing.assert_allclose(got, x64 + o, rtol=1e-4, atol=2e-5)
+    np.testing.assert_allclose(kc[pos], K[pos], rtol=1e-4, atol=1e-5)
+
+
+def test_attn_block_zero_output_projection_leaves_the_residual():
+    cfg, bw, _, kc, vc, x, pos, cs, sn = _block_setup(120, gp.GGML_F32)
+    bw.wo = np.zeros_like(bw.wo)
+    assert np.array_equal(orc.attn_block(cfg, bw, kc, vc, x, 0, pos, rope_cos=cs, rope_sin=sn), x)
+    b = np.linspace(-1, 1, 256).astype(F32)
+    bw.o_bias = b
+    assert np.array_equal(orc.attn_block(cfg, bw, kc, vc, x, 0, pos + 1, rope_cos=cs, rope_sin=sn),
+                          x + b)
+
+
+def test_attn_block_merged_qkv_equals_separate_projections():
+    for t in (gp.GGML_Q4_K, gp.GGML_BF16):
+        cfg, bw, _, kc, vc, x, pos, cs, sn = _block_setup(130 + t, t)
+        cfg2, bw2, _, kc2, vc2, _, _, _, _ = _block_setup(130 + t, t, merged=True)
+        a = orc.attn_block(cfg, bw, kc, vc, x, 0, pos, rope_cos=cs, rope_sin=sn)
+        b = orc.attn_block(cfg2, bw2, kc2, vc2, x, 0, pos, rope_cos=cs, rope_sin=sn)
+        assert np.array_equal(a, b) and np.array_equal(kc, kc2)
