@@ -263,6 +263,49 @@ int llmp_attn_prefill_ex(uint64_t handle, int layer, int pos0, int n_tokens, uin
 int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0, int n_tokens,
                              uint64_t q, uint64_t gate, uint64_t out, uint64_t stream);
 
+/* ---- the attention half of a layer around the attention core ------------------------------
+ * Replaces CudaForwardPass.forwardAttentionPart steps 1-2b and 6-6c (CudaForwardPass.java:
+ * 1498-1527, 1572-1587) with the CPU path's semantics (TransformerBlock.forward's attention
+ * half and Attention.forward's projections, Attention.java:76-110, 232-238): x (the residual
+ * stream, gpuX) becomes x + rscale? * postnorm?(Wo . attention(W{q,k,v} . rmsnorm(x) + bias)
+ * + o_bias).  Projection weights keep their GGUF type; the library repacks them at upload. */
+/* GGMLType ids (GGMLType.java:4-35) with a projection kernel. */
+#define LLMP_GGML_F32    0
+#define LLMP_GGML_F16    1
+#define LLMP_GGML_Q4_0   2   /* the reference's nibble order: element 2i low, 2i+1 high      */
+#define LLMP_GGML_Q8_0   8
+#define LLMP_GGML_Q4_K  12
+#define LLMP_GGML_Q6_K  14
+#define LLMP_GGML_BF16  30
+/* Weight slots of a layer (TransformerLayerWeights): matrices are [rows][cols] in GGUF row
+ * order; vectors are fp32. */
+#define LLMP_W_ATTN_NORM      0  /* [dim] attnNorm RMSNorm weights; absent: x is copied (OLMo2) */
+#define LLMP_W_Q              1  /* [n_heads*head_dim][dim]                                     */
+#define LLMP_W_K              2  /* [n_kv_heads*head_dim][dim]                                  */
+#define LLMP_W_V              3  /* [n_kv_heads*head_dim][dim]                                  */
+#define LLMP_W_QKV            4  /* merged [q_dim + 2*kv_dim][dim] (Phi-3); replaces Q, K, V     */
+#define LLMP_W_O              5  /* [dim][n_heads*head_dim]                                     */
+#define LLMP_W_Q_BIAS         6  /* [q_dim]  (Qwen2)                                            */
+#define LLMP_W_K_BIAS         7  /* [kv_dim]                                                    */
+#define LLMP_W_V_BIAS         8  /* [kv_dim]                                                    */
+#define LLMP_W_O_BIAS         9  /* [dim]    attn_output.bias                                   */
+#define LLMP_W_POST_ATTN_NORM 10 /* [dim]    postAttnNorm (Gemma 2/3, GLM4, OLMo2)              */
+#define LLMP_W_SLOTS          11
+/* Model-wide block parameters: dim = embeddingLength (a multiple of 32, at most 16384);
+ * residual_scale = Granite's residualScale (0 = off). */
+int llmp_block_config(uint64_t handle, int dim, float residual_scale);
+/* Upload one slot of a configured layer: data = host bytes in the GGUF layout of ggml_type
+ * (rows * row_bytes; fp32 for the vectors), or NULL to clear the slot.  The weight is repacked
+ * into per-row planes on the device.  Set-up only: it allocates and synchronises. */
+int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int rows, int cols,
+                      const void *data, uint64_t nbytes);
+/* The attention half of one layer on the device residual x (fp32 [dim], updated in place):
+ * pre-norm and Q/K/V projections, the attention core of llmp_attn_decode (its K/V append,
+ * window, QK-norm, RoPE and sinks), output projection, post-norm, residual scale and add.
+ * position / d_position as in llmp_attn_decode_ex; no allocation, so it can be captured. */
+int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_position, uint64_t x,
+                    int splits, uint64_t stream);
+
 /* ---- profiling (the reference's -Dcuda.profile section timers,
  *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */
 #define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV) */

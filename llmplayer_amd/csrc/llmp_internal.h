@@ -113,4 +113,16 @@ size_t prefill_tile_bytes(int head_dim);
 // Plain 16-byte-per-thread copy kernel.
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
+namespace gk {
+struct GemvArgs;
+}
+// Weights per lane unit of a GGML type's projection kernel (0 = no kernel for that type).
+int gemv_unit(int ggml_type);
+// y = W x over one to three row segments of one GGML type (optional fused pre-RMSNorm of x,
+// optional residual epilogue); hipErrorInvalidValue for an unsupported type or shape.
+hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, hipStream_t stream);
+// x += rscale? * rmsnorm(xb, w) over dim values (one workgroup).
+hipError_t launch_post_norm_residual(const float* xb, const float* w, float eps, float rscale,
+                                     float* x, int dim, hipStream_t stream);
+
 }  // namespace llmp

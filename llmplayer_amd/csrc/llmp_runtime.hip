@@ -4,6 +4,7 @@
 #include "llmp_hip.h"
 #include "llmp_internal.h"
 #include "prefill_kernels.h"
+#include "gemv_kernels.h"
 
 #include <cmath>
 #include <cstdarg>
@@ -39,6 +40,14 @@ int fail(int code, const char* fmt, ...) {
                         (int)e_);                                                          \
     } while (0)
 
+// A projection weight or fp32 vector of a layer (llmp_layer_weight), repacked into planes.
+struct DevWeight {
+    int type = -1;
+    int rows = 0, cols = 0;
+    void* mem = nullptr;
+    gk::WPlanes planes{};
+};
+
 struct LayerCfg {
     bool configured = false;
     int n_heads = 0;
@@ -53,6 +62,7 @@ struct LayerCfg {
     float* d_knw = nullptr;
     float* d_sinks = nullptr;   // [n_heads] sink logits times log2(e) (llmp_layer_sinks)
     int norm_mode = 0;          // LLMP_NORM_* bits (llmp_layer_norm_mode)
+    DevWeight w[LLMP_W_SLOTS];  // attention-block weights (llmp_layer_weight)
 };
 
 struct RopeTable {
@@ -78,6 +88,10 @@ struct KvHandle {
     size_t prefill_part_bytes = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
+    int blk_dim = 0;                 // llmp_block_config: embedding length
+    float blk_rscale = 0.0f;         // Granite residual scale, 0 = off
+    float* blk_buf = nullptr;        // block scratch: q|k|v, attention output, Wo output
+    size_t blk_floats = 0;
     size_t part_slots = 0;    // (split, query head) slots the workspace holds
     bool prof_on = false;
     std::vector<ProfPair> prof_pending[LLMP_PROF_KINDS];
@@ -162,7 +176,10 @@ void free_handle(KvHandle* kv) {
         if (l.d_qnw) (void)hipFree(l.d_qnw);
         if (l.d_knw) (void)hipFree(l.d_knw);
         if (l.d_sinks) (void)hipFree(l.d_sinks);
+        for (auto& w : l.w)
+            if (w.mem) (void)hipFree(w.mem);
     }
+    if (kv->blk_buf) (void)hipFree(kv->blk_buf);
     if (kv->part_o) (void)hipFree(kv->part_o);
     if (kv->part_ml) (void)hipFree(kv->part_ml);
     if (kv->prefill_ws) (void)hipFree(kv->prefill_ws);
@@ -931,6 +948,266 @@ int llmp_layer_norm_mode(uint64_t handle, int layer, int mode) {
     if (mode & ~(LLMP_NORM_SEQUENTIAL | LLMP_NORM_V))
         return fail(LLMP_ERR_INVALID_ARG, "llmp_layer_norm_mode: unknown mode bits 0x%x", mode);
     kv->layers[(size_t)layer].norm_mode = mode;
+    return LLMP_OK;
+}
+
+// ---- attention block: projections around the attention core ------------------------------
+// Bytes of one row of `cols` weights in a GGML type's GGUF layout (GGMLType.java:4-35).
+static size_t ggml_row_bytes(int type, int cols) {
+    switch (type) {
+    case LLMP_GGML_F32: return (size_t)cols * 4;
+    case LLMP_GGML_F16:
+    case LLMP_GGML_BF16: return (size_t)cols * 2;
+    case LLMP_GGML_Q8_0: return (size_t)(cols / 32) * 34;
+    case LLMP_GGML_Q4_0: return (size_t)(cols / 32) * 18;
+    case LLMP_GGML_Q4_K: return (size_t)(cols / 256) * 144;
+    case LLMP_GGML_Q6_K: return (size_t)(cols / 256) * 210;
+    default: return 0;
+    }
+}
+
+static size_t pad256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Repacks GGUF rows into the planes gemv_kernels.h reads: every row's data of a plane is
+// contiguous and 16-byte chunks stay 16-byte aligned.  Returns the plane count.
+static int repack_weight(int type, int rows, int cols, const uint8_t* src, std::vector<uint8_t>& dst,
+                         size_t off[4], size_t pitch[4]) {
+    const size_t rb = ggml_row_bytes(type, cols);
+    int n = 1;
+    struct Piece { int plane; size_t src_off, len; };   // per block: bytes [src_off, +len) -> plane
+    std::vector<Piece> pieces;
+    size_t bw = 0, blk_bytes = 0;   // weights and bytes per GGUF block
+    switch (type) {
+    case LLMP_GGML_F32: case LLMP_GGML_F16: case LLMP_GGML_BF16:
+        pitch[0] = rb; break;
+    case LLMP_GGML_Q8_0:
+        n = 2; bw = 32; blk_bytes = 34; pitch[0] = (size_t)cols; pitch[1] = (size_t)cols / 32 * 2;
+        pieces = {{1, 0, 2}, {0, 2, 32}}; break;
+    case LLMP_GGML_Q4_0:
+        n = 2; bw = 32; blk_bytes = 18; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32 * 2;
+        pieces = {{1, 0, 2}, {0, 2, 16}}; break;
+    case LLMP_GGML_Q4_K:
+        n = 2; bw = 256; blk_bytes = 144; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 256 * 16;
+        pieces = {{1, 0, 16}, {0, 16, 128}}; break;
+    case LLMP_GGML_Q6_K:
+        n = 4; bw = 256; blk_bytes = 210; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 4;
+        pitch[2] = (size_t)cols / 16; pitch[3] = (size_t)cols / 256 * 2;
+        pieces = {{0, 0, 128}, {1, 128, 64}, {2, 192, 16}, {3, 208, 2}}; break;
+    default: return 0;
+    }
+    off[0] = 0;
+    for (int i = 1; i < n; ++i) off[i] = pad256(off[i - 1] + (size_t)rows * pitch[i - 1]);
+    dst.assign(pad256(off[n - 1] + (size_t)rows * pitch[n - 1]), 0);
+    if (pieces.empty()) {
+        for (int r = 0; r < rows; ++r) std::memcpy(&dst[(size_t)r * pitch[0]], src + (size_t)r * rb, rb);
+        return n;
+    }
+    const size_t nb = (size_t)cols / bw;
+    for (int r = 0; r < rows; ++r)
+        for (size_t b = 0; b < nb; ++b) {
+            const uint8_t* blk = src + (size_t)r * rb + b * blk_bytes;
+            for (const Piece& pc : pieces)
+                std::memcpy(&dst[off[pc.plane] + (size_t)r * pitch[pc.plane] + b * pc.len],
+                            blk + pc.src_off, pc.len);
+        }
+    return n;
+}
+
+int llmp_block_config(uint64_t handle, int dim, float residual_scale) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (dim <= 0 || dim > gk::kMaxGemvCols || dim % 32)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_block_config: dim %d (a multiple of 32 up to %d)",
+                    dim, gk::kMaxGemvCols);
+    if (!(residual_scale >= 0.0f) || !std::isfinite(residual_scale))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_block_config: residual scale %g", (double)residual_scale);
+    if (kv->blk_dim != 0 && kv->blk_dim != dim)
+        for (auto& l : kv->layers)
+            for (auto& w : l.w)
+                if (w.mem) return fail(LLMP_ERR_INVALID_ARG, "llmp_block_config: weights uploaded for dim %d",
+                                       kv->blk_dim);
+    kv->blk_dim = dim;
+    kv->blk_rscale = residual_scale;
+    return LLMP_OK;
+}
+
+int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int rows, int cols,
+                      const void* data, uint64_t nbytes) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (slot < 0 || slot >= LLMP_W_SLOTS)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_layer_weight: slot %d", slot);
+    LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    if (kv->blk_dim == 0)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_layer_weight: call llmp_block_config first");
+    DevWeight& w = c.w[slot];
+    if (w.mem) (void)hipFree(w.mem);
+    w = DevWeight{};
+    if (data == nullptr) return LLMP_OK;   // slot removed
+    const int D = kv->head_dim, qd = c.n_heads * D, kvd = kv->n_kv_heads * D, dim = kv->blk_dim;
+    int want_rows = 1, want_cols = 0;
+    bool vec = false;
+    switch (slot) {
+    case LLMP_W_ATTN_NORM: case LLMP_W_POST_ATTN_NORM: case LLMP_W_O_BIAS:
+        vec = true; want_cols = dim; break;
+    case LLMP_W_Q_BIAS: vec = true; want_cols = qd; break;
+    case LLMP_W_K_BIAS: case LLMP_W_V_BIAS: vec = true; want_cols = kvd; break;
+    case LLMP_W_Q: want_rows = qd; want_cols = dim; break;
+    case LLMP_W_K: case LLMP_W_V: want_rows = kvd; want_cols = dim; break;
+    case LLMP_W_QKV: want_rows = qd + 2 * kvd; want_cols = dim; break;
+    case LLMP_W_O: want_rows = dim; want_cols = qd; break;
+    }
+    if (rows != want_rows || cols != want_cols)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_layer_weight: slot %d is [%d][%d], got [%d][%d]", slot,
+                    want_rows, want_cols, rows, cols);
+    if (vec && ggml_type != LLMP_GGML_F32)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_layer_weight: slot %d takes fp32 values", slot);
+    const int unit = vec ? 1 : gemv_unit(ggml_type);
+    const size_t rb = ggml_row_bytes(ggml_type, cols);
+    if (unit == 0 || rb == 0)
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_layer_weight: GGML type %d has no kernel", ggml_type);
+    if (cols % unit || (!vec && cols > gk::kMaxGemvCols))
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_layer_weight: %d columns for GGML type %d", cols, ggml_type);
+    if (nbytes != (uint64_t)rb * (uint64_t)rows)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_layer_weight: %llu bytes, expected %llu",
+                    (unsigned long long)nbytes, (unsigned long long)rb * rows);
+    std::vector<uint8_t> packed;
+    size_t off[4] = {0, 0, 0, 0}, pitch[4] = {0, 0, 0, 0};
+    const int np = repack_weight(ggml_type, rows, cols, static_cast<const uint8_t*>(data), packed, off, pitch);
+    hipError_t e = hipMalloc(&w.mem, packed.size());
+    if (e == hipErrorOutOfMemory)
+        return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_layer_weight: %zu bytes", packed.size());
+    LLMP_HIP_CHECK(e, "hipMalloc(weight)");
+    LLMP_HIP_CHECK(hipMemcpy(w.mem, packed.data(), packed.size(), hipMemcpyHostToDevice), "hipMemcpy(weight)");
+    w.type = ggml_type;
+    w.rows = rows;
+    w.cols = cols;
+    for (int i = 0; i < np; ++i) {
+        w.planes.p[i] = static_cast<const unsigned char*>(w.mem) + off[i];
+        w.planes.pitch[i] = (long long)pitch[i];
+    }
+    // Block scratch: q | k | v, the attention output and the Wo output (kept per handle).
+    const size_t need = (size_t)(qd + 2 * kvd) + (size_t)qd + (size_t)dim + 64;
+    if (need > kv->blk_floats) {
+        LLMP_HIP_CHECK(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        if (kv->blk_buf) (void)hipFree(kv->blk_buf);
+        kv->blk_buf = nullptr;
+        kv->blk_floats = 0;
+        LLMP_HIP_CHECK(hipMalloc(&kv->blk_buf, need * sizeof(float)), "hipMalloc(block scratch)");
+        kv->blk_floats = need;
+    }
+    return LLMP_OK;
+}
+
+int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_position, uint64_t x,
+                    int splits, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    const LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    const DevWeight* W = c.w;
+    const bool merged = W[LLMP_W_QKV].mem != nullptr;
+    if (kv->blk_dim == 0 || !W[LLMP_W_O].mem ||
+        (!merged && (!W[LLMP_W_Q].mem || !W[LLMP_W_K].mem || !W[LLMP_W_V].mem)))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block: layer %d lacks projection weights", layer);
+    if (!x || (x & 3)) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block: null or misaligned x");
+    if (d_position & 3) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block: misaligned position word");
+    const int D = kv->head_dim, qd = c.n_heads * D, kvd = kv->n_kv_heads * D, dim = kv->blk_dim;
+    float* q = kv->blk_buf;
+    float* attn = q + qd + 2 * kvd;
+    float* o = attn + qd;
+    float* xp = reinterpret_cast<float*>(x);
+    hipStream_t st = pick_stream(stream);
+    auto vecp = [&](int slot) -> const float* {
+        return static_cast<const float*>(W[slot].mem);
+    };
+
+    // 1-2. Pre-norm (fused into the projection) and the Q/K/V projections with their biases.
+    gk::GemvSeg segs[3];
+    int types[3];
+    const int seg_rows[3] = {qd, kvd, kvd}, seg_off[3] = {0, qd, qd + kvd};
+    const int bias_slot[3] = {LLMP_W_Q_BIAS, LLMP_W_K_BIAS, LLMP_W_V_BIAS};
+    for (int i = 0; i < 3; ++i) {
+        const DevWeight& dw = merged ? W[LLMP_W_QKV] : W[LLMP_W_Q + i];
+        segs[i].w = dw.planes;
+        if (merged)   // rows seg_off[i].. of the merged matrix
+            for (int p = 0; p < 4; ++p)
+                if (dw.planes.p[p]) segs[i].w.p[p] = dw.planes.p[p] + (long long)seg_off[i] * dw.planes.pitch[p];
+        segs[i].rows = seg_rows[i];
+        segs[i].out_off = seg_off[i];
+        segs[i].bias = vecp(bias_slot[i]);
+        types[i] = dw.type;
+    }
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < 3; ++i) {
+        if (done[i]) continue;
+        gk::GemvArgs g{};
+        for (int k = i; k < 3; ++k)
+            if (!done[k] && types[k] == types[i]) {
+                g.seg[g.nseg++] = segs[k];
+                done[k] = true;
+            }
+        // rows of the selected segments are not contiguous in general: one launch per segment
+        // when a type change splits them, else one launch over rows [0, qd + 2 kvd)
+        if (g.nseg == 3) {
+            g.rows_total = qd + 2 * kvd;
+            g.cols = dim;
+            g.x = xp;
+            g.norm_w = vecp(LLMP_W_ATTN_NORM);
+            g.eps = c.eps;
+            g.out = q;
+            LLMP_HIP_CHECK(launch_gemv(g, types[i], st), "block Q/K/V projection launch");
+        } else {
+            for (int k = 0; k < g.nseg; ++k) {
+                gk::GemvArgs h{};
+                h.seg[0] = g.seg[k];
+                h.seg[0].out_off = 0;
+                h.nseg = 1;
+                h.rows_total = g.seg[k].rows;
+                h.cols = dim;
+                h.x = xp;
+                h.norm_w = vecp(LLMP_W_ATTN_NORM);
+                h.eps = c.eps;
+                h.out = q + g.seg[k].out_off;
+                LLMP_HIP_CHECK(launch_gemv(h, types[i], st), "block projection launch");
+            }
+        }
+    }
+    // 3-5. The attention core (QK-norm, RoPE, append, attention) into `attn`.
+    const int* dpos = reinterpret_cast<const int*>(d_position);
+    if (int rc = enqueue_decode(kv, layer, -1, d_position ? kv->max_seq - 1 : position, dpos,
+                                reinterpret_cast<uint64_t>(q), reinterpret_cast<uint64_t>(q + qd),
+                                reinterpret_cast<uint64_t>(q + qd + kvd), 0,
+                                reinterpret_cast<uint64_t>(attn), splits, stream))
+        return rc;
+    // 6. Output projection (+ bias), post-norm, residual scale and residual add.
+    gk::GemvArgs g{};
+    g.seg[0].w = W[LLMP_W_O].planes;
+    g.seg[0].rows = dim;
+    g.seg[0].bias = vecp(LLMP_W_O_BIAS);
+    g.nseg = 1;
+    g.rows_total = dim;
+    g.cols = qd;
+    g.x = attn;
+    g.eps = c.eps;
+    const float* post = vecp(LLMP_W_POST_ATTN_NORM);
+    if (post) {
+        g.out = o;
+        LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, st), "block output projection launch");
+        LLMP_HIP_CHECK(launch_post_norm_residual(o, post, c.eps, kv->blk_rscale, xp, dim, st),
+                       "block post-norm launch");
+    } else {
+        g.resid = xp;
+        g.rscale = kv->blk_rscale;
+        LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, st), "block output projection launch");
+    }
     return LLMP_OK;
 }
 

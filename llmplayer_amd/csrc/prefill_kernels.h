@@ -242,7 +242,7 @@ __device__ __forceinline__ floatx4 load_chunk(const HeadRows& h, int r, int c4) 
 template <bool Q8>
 __device__ __forceinline__ floatx4 chunk_values(floatx4 x) {
     if constexpr (Q8) {
-        const unsigned w = __builtin_bit_cast(unsigned, x[0]);
+        const unsigned w = __float_as_uint(x[0]);
         const float sc = x[1];
         return floatx4{(float)(signed char)(w & 0xFF) * sc, (float)(signed char)((w >> 8) & 0xFF) * sc,
                        (float)(signed char)((w >> 16) & 0xFF) * sc, (float)(signed char)(w >> 24) * sc};

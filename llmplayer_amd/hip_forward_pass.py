@@ -266,6 +266,32 @@ class KvCache:
             self.handle = 0
 
 
+@dataclass
+class GgufTensor:
+    """A projection weight as a GGUF file stores it: GGMLType id, [rows][cols], raw bytes."""
+    type: int
+    rows: int
+    cols: int
+    data: np.ndarray     # uint8, rows * row_bytes(type, cols)
+
+
+@dataclass
+class TransformerLayerWeights:
+    """The attention half of TransformerLayerWeights: wq/wk/wv (or merged wqkv) and wo as
+    GGUF tensors, norms and biases as fp32 arrays (None where the model has none)."""
+    wq: Optional[GgufTensor] = None
+    wk: Optional[GgufTensor] = None
+    wv: Optional[GgufTensor] = None
+    wqkv: Optional[GgufTensor] = None
+    wo: Optional[GgufTensor] = None
+    attnNorm: Optional[np.ndarray] = None
+    postAttnNorm: Optional[np.ndarray] = None
+    qBias: Optional[np.ndarray] = None
+    kBias: Optional[np.ndarray] = None
+    vBias: Optional[np.ndarray] = None
+    woBias: Optional[np.ndarray] = None
+
+
 class HipForwardPass:
     """Attention section of a GPU-resident forward pass on MI355X.
 
@@ -387,6 +413,56 @@ class HipForwardPass:
         call("llmp_attn_decode", self.kv.handle, layerIdx, position, self.gpuQ.ptr, self.gpuK.ptr,
              self.gpuV.ptr, self.gpuXb2.ptr, splits, stream)
 
+    # -- the attention half of the layer (projections + residual) --------------------------
+    def setBlockConfig(self, dim: int, residual_scale: float = 0.0) -> None:
+        """embeddingLength and Granite's residualScale (0 = off) for forwardAttentionBlock."""
+        call("llmp_block_config", self.kv.handle, dim, float(residual_scale))
+        self.dim = dim
+        if getattr(self, "gpuX", None) is None or self.gpuX.nbytes < dim * 4:
+            self.gpuX = DeviceBuffer(dim * 4)
+
+    def uploadLayerWeights(self, layer: int, lw: TransformerLayerWeights) -> None:
+        """Hands a layer's attention weights to the library (repacked on the device)."""
+        h = self.kv.handle
+
+        def put(slot, t: Optional[GgufTensor]):
+            if t is None:
+                call("llmp_layer_weight", h, layer, slot, 0, 0, 0, None, 0)
+                return
+            d = np.ascontiguousarray(t.data, np.uint8)
+            call("llmp_layer_weight", h, layer, slot, t.type, t.rows, t.cols,
+                 d.ctypes.data_as(C.c_void_p), d.nbytes)
+
+        def vec(slot, a: Optional[np.ndarray]):
+            if a is None:
+                call("llmp_layer_weight", h, layer, slot, 0, 0, 0, None, 0)
+                return
+            a = np.ascontiguousarray(a, np.float32).reshape(-1)
+            call("llmp_layer_weight", h, layer, slot, _lib.LLMP_GGML_F32, 1, a.size,
+                 a.ctypes.data_as(C.c_void_p), a.nbytes)
+        for slot, t in ((_lib.LLMP_W_Q, lw.wq), (_lib.LLMP_W_K, lw.wk), (_lib.LLMP_W_V, lw.wv),
+                        (_lib.LLMP_W_QKV, lw.wqkv), (_lib.LLMP_W_O, lw.wo)):
+            put(slot, t)
+        for slot, a in ((_lib.LLMP_W_ATTN_NORM, lw.attnNorm), (_lib.LLMP_W_POST_ATTN_NORM, lw.postAttnNorm),
+                        (_lib.LLMP_W_Q_BIAS, lw.qBias), (_lib.LLMP_W_K_BIAS, lw.kBias),
+                        (_lib.LLMP_W_V_BIAS, lw.vBias), (_lib.LLMP_W_O_BIAS, lw.woBias)):
+            vec(slot, a)
+
+    def uploadX(self, x: np.ndarray) -> None:
+        """The residual stream into gpuX (CudaForwardPass.uploadX)."""
+        self.gpuX.upload(np.ascontiguousarray(x, np.float32).reshape(self.dim))
+
+    def downloadX(self) -> np.ndarray:
+        return self.gpuX.download(np.float32, self.dim)
+
+    def forwardAttentionBlock(self, layerIdx: int, position: int, splits: int = 0,
+                              stream: int = 0, device_position: bool = False) -> None:
+        """CudaForwardPass.forwardAttentionPart steps 1-6c on gpuX: pre-norm, projections,
+        attention, output projection, post-norm and residual (gpuX holds the post-attention
+        residual afterwards).  device_position reads the position from gpuTokenParams."""
+        d = self.gpuTokenParams.ptr if device_position else 0
+        call("llmp_attn_block", self.kv.handle, layerIdx, position, d, self.gpuX.ptr, splits, stream)
+
     def updateTokenParams(self, position: int) -> None:
         """Store [position, position+1] in device memory (CudaForwardPass.updateTokenParams /
         uploadXAndUpdateParams, CudaForwardPass.java:1283-1292), for graph-captured calls."""
@@ -459,7 +535,7 @@ class HipForwardPass:
         call("llmp_stream_sync", stream)
 
     def close(self) -> None:
-        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2", "gpuGate", "gpuTokenParams"):
+        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2", "gpuGate", "gpuTokenParams", "gpuX"):
             buf = getattr(self, b, None)
             if buf is not None:
                 buf.free()

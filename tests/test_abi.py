@@ -51,7 +51,11 @@ def test_constants_match_header():
     defs = dict((name, int(val)) for name, val in re.findall(r"#define\s+(LLMP_\w+)\s+(-?\d+)", text))
     for name in ("LLMP_KV_F32", "LLMP_KV_Q8_0", "LLMP_KV_Q8_0_TRUNC", "LLMP_ROPE_NORMAL", "LLMP_ROPE_NEOX",
                  "LLMP_ROPE_SEL_NONE", "LLMP_ROPE_SEL_GLOBAL", "LLMP_ROPE_SEL_LOCAL",
-                 "LLMP_NORM_SEQUENTIAL", "LLMP_NORM_V"):
+                 "LLMP_NORM_SEQUENTIAL", "LLMP_NORM_V", "LLMP_GGML_F32", "LLMP_GGML_F16",
+                 "LLMP_GGML_Q4_0", "LLMP_GGML_Q8_0", "LLMP_GGML_Q4_K", "LLMP_GGML_Q6_K",
+                 "LLMP_GGML_BF16", "LLMP_W_ATTN_NORM", "LLMP_W_Q", "LLMP_W_K", "LLMP_W_V",
+                 "LLMP_W_QKV", "LLMP_W_O", "LLMP_W_Q_BIAS", "LLMP_W_K_BIAS", "LLMP_W_V_BIAS",
+                 "LLMP_W_O_BIAS", "LLMP_W_POST_ATTN_NORM"):
         assert getattr(_lib, name) == defs[name], name
 
 

@@ -1,0 +1,160 @@
+"""GPU parity of the attention half of a layer (llmp_attn_block: pre-norm, Q/K/V projections over
+GGUF-format weights, the attention core, output projection, post-norm, residual) against the
+oracle's restatement of TransformerBlock.forward / Attention.forward (orc.attn_block).
+
+Weights come from tests/ggml_pack.py (packed from each format's layout).  Bar: the residual
+after the block max-abs <= 1e-4 (and <= 1e-4 + 1e-3*|ref|) against the oracle; the appended
+K/V row to the same bar (the projections sum in another order than the CPU path, so the row
+is not bit-identical here; bit-exact appends are pinned by the from-projection entry points)
+and every other cache row unchanged."""
+import numpy as np
+import pytest
+
+from llmplayer_amd import _lib
+from llmplayer_amd import hip_forward_pass as hfp
+from oracle import oracle as orc
+from tests import decode_cases as dc
+from tests import ggml_pack as gp
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
+         gp.GGML_Q6_K]
+NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k"}
+
+
+def _tensor(t, rows, cols, rng, scale=0.05):
+    wb, vals = gp.random_weights(t, rows, cols, rng, scale)
+    return hfp.GgufTensor(t, rows, cols, wb.reshape(-1)), wb
+
+
+def _weights(c, dim, types, rng, merged=False, bias=False, post=False, pre=True):
+    """types: (tq, tk, tv, to).  Returns (TransformerLayerWeights, orc.BlockWeights)."""
+    qd, kvd = c.q_dim, c.kv_dim
+    tq, tk, tv, to = types
+    lw = hfp.TransformerLayerWeights()
+    bw = orc.BlockWeights(dim)
+    if merged:
+        t, wb = _tensor(tq, qd + 2 * kvd, dim, rng)
+        lw.wqkv, bw.wqkv, bw.wqkv_type = t, wb, tq
+    else:
+        lw.wq, bw.wq = _tensor(tq, qd, dim, rng)
+        lw.wk, bw.wk = _tensor(tk, kvd, dim, rng)
+        lw.wv, bw.wv = _tensor(tv, kvd, dim, rng)
+        bw.wq_type, bw.wk_type, bw.wv_type = tq, tk, tv
+    lw.wo, bw.wo = _tensor(to, dim, qd, rng)
+    bw.wo_type = to
+    if pre:
+        lw.attnNorm = bw.attn_norm = rng.uniform(0.5, 1.5, dim).astype(F32)
+    if post:
+        lw.postAttnNorm = bw.post_attn_norm = rng.uniform(0.5, 1.5, dim).astype(F32)
+    if bias:
+        lw.qBias = bw.q_bias = (rng.standard_normal(qd) * 0.1).astype(F32)
+        lw.kBias = bw.k_bias = (rng.standard_normal(kvd) * 0.1).astype(F32)
+        lw.vBias = bw.v_bias = (rng.standard_normal(kvd) * 0.1).astype(F32)
+        lw.woBias = bw.o_bias = (rng.standard_normal(dim) * 0.1).astype(F32)
+    return lw, bw
+
+
+def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=False, post=False,
+         pre=True, rscale=0.0, qk=None, splits=0, devpos=False):
+    rng = np.random.default_rng(seed)
+    lw, bw = _weights(c, dim, types, rng, merged, bias, post, pre)
+    bw.residual_scale = rscale
+    kv = c.kv_dim
+    kc = np.zeros((max_seq, kv), F32)
+    vc = np.zeros((max_seq, kv), F32)
+    kc[:pos0] = rng.standard_normal((pos0, kv)).astype(F32)
+    vc[:pos0] = rng.standard_normal((pos0, kv)).astype(F32)
+    qk_list = [qk] * c.block_count if qk is not None else None
+    oc = dc.oracle_config(c, max_seq)
+    cs, sn = dc.oracle_tables(c, max_seq, 0)
+    qw, kw = qk if qk is not None else (None, None)
+    with hfp.HipForwardPass(c, max_seq, qk_norm=qk_list) as fp:
+        fp.kv.write(0, 0, kc, vc)
+        fp.setBlockConfig(dim, rscale)
+        fp.uploadLayerWeights(0, lw)
+        worst = 0.0
+        for s in range(steps):
+            pos = pos0 + s
+            x = (rng.standard_normal(dim) * 2).astype(F32)
+            dc.log(f"[gpu] block {what}: step {s} pos {pos}")
+            fp.uploadX(x)
+            if devpos:
+                fp.updateTokenParams(pos)
+            fp.forwardAttentionBlock(0, pos, splits, device_position=devpos)
+            got = fp.downloadX()
+            want = orc.attn_block(oc, bw, kc, vc, x, 0, pos, qnorm_w=qw, knorm_w=kw, rope_cos=cs,
+                                  rope_sin=sn, n_threads=16)
+            worst = max(worst, dc.compare_out(got, want, f"block {what} pos {pos}"))
+            gk, gv = fp.kv.read(0, 0, pos + 1)
+            assert np.array_equal(gk[:pos], kc[:pos]) and np.array_equal(gv[:pos], vc[:pos])
+            dc.compare_out(gk[pos], kc[pos], f"block {what} appended K row")
+            dc.compare_out(gv[pos], vc[pos], f"block {what} appended V row")
+            # continue from the device's rows so later steps attend to the same cache
+            kc[pos], vc[pos] = gk[pos], gv[pos]
+        dc.log(f"[gpu] block {what}: ok, max abs err {worst:.2e}")
+
+
+@pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
+def test_block_every_weight_format(t):
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    _run(c, 1024, 64, 40, 2, (t, t, t, t), seed=600 + t, what=NAMES[t])
+
+
+def test_block_c3_llama3b_shape_q4_k_m_mix():
+    """C3 shape (24/8/128, dim 3072) with the Q4_K_M mix: Q4_K for q, k, o and Q6_K for v
+    (separate launches per weight type), four steps after a 2000-row prefix."""
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    _run(c, 3072, 2048, 2000, 4, (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K),
+         seed=610, what="C3 Q4_K_M")
+
+
+def test_block_merged_qkv_phi3():
+    c = hfp.ModelConfig(16, 16, 64, 1, rope_freq_base=10000.0)
+    _run(c, 1024, 64, 20, 2, (gp.GGML_F16,) * 4, seed=620, what="merged QKV f16", merged=True)
+
+
+def test_block_qwen2_biases_q8_0():
+    c = hfp.ModelConfig(12, 2, 128, 1, architecture="qwen2", rope_freq_base=1e6)   # Qwen2-1.5B shape
+    _run(c, 1536, 64, 30, 2, (gp.GGML_Q8_0,) * 4, seed=630, what="qwen2 bias q8_0", bias=True)
+
+
+def test_block_gemma_post_norm_bias_and_granite_scale():
+    c = hfp.ModelConfig(8, 4, 256, 1, architecture=hfp.ARCH_GEMMA3, rope_freq_base=1e6,
+                        norm_eps=1e-6)
+    rng = np.random.default_rng(640)
+    qk = (rng.uniform(0.5, 1.5, 256).astype(F32), rng.uniform(0.5, 1.5, 256).astype(F32))
+    _run(c, 1536, 64, 25, 2, (gp.GGML_BF16, gp.GGML_Q6_K, gp.GGML_Q6_K, gp.GGML_BF16), seed=641,
+         what="post-norm + bias + residual scale", bias=True, post=True, rscale=0.22, qk=qk)
+
+
+def test_block_olmo2_post_norm_only_and_device_position():
+    c = hfp.ModelConfig(16, 16, 128, 1, rope_freq_base=500000.0)
+    _run(c, 2048, 80, 50, 3, (gp.GGML_Q4_K,) * 4, seed=650, what="post-norm only, device position",
+         post=True, pre=False, devpos=True)
+
+
+def test_block_split_settings_agree():
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    for splits in (1, 7, 64):
+        _run(c, 3072, 600, 512, 1, (gp.GGML_Q8_0,) * 4, seed=660 + splits,
+             what=f"C3 q8_0 splits={splits}", splits=splits)
+
+
+def test_block_error_codes():
+    c = hfp.ModelConfig(8, 2, 64, 1, rope_freq_base=1e4)
+    with hfp.HipForwardPass(c, 32) as fp:
+        h = fp.kv.handle
+        assert _lib.status("llmp_layer_weight", h, 0, 1, 0, 512, 512, None, 0) == 1  # no block config
+        assert _lib.status("llmp_block_config", h, 500, 0.0) == 1                     # not a multiple of 32
+        fp.setBlockConfig(512)
+        x = fp.gpuX.ptr
+        assert _lib.status("llmp_attn_block", h, 0, 3, 0, x, 0, 0) == 1               # no weights yet
+        w = np.zeros(512 * 512 * 4, np.uint8)
+        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 128, 512, w.ctypes.data, 128 * 512 * 4) == 1  # rows != q_dim
+        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 13, 512, 512, w.ctypes.data, 512 * 176 // 256 * 512) == 6  # Q5_K: no kernel
+        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 512, 512, w.ctypes.data, 100) == 1   # byte count
+        assert _lib.status("llmp_layer_weight", h, 0, 11, 0, 1, 512, w.ctypes.data, 2048) == 1  # bad slot
+        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_ATTN_NORM, 8, 1, 512, w.ctypes.data, 2048) == 1  # vector not fp32
