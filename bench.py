@@ -263,6 +263,76 @@ def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int, q8: bool = False
             "kv_read_gbps": round(kv_bytes(ctx - K, q8) / (us * 1e-6) / 1e9, 1)}
 
 
+def synthetic_gguf(t: int, rows: int, cols: int, rng) -> np.ndarray:
+    """Random GGUF-layout bytes of type t (Q4_K or Q6_K) with finite fp16 scale fields:
+    uniform quants and scale bytes, super-block scales 2^-10 (d) and 2^-12 (dmin)."""
+    ns = cols // 256
+    if t == 12:     # Q4_K: d, dmin (fp16), 12 scale bytes, 128 nibble bytes
+        b = rng.integers(0, 256, (rows, ns, 144), dtype=np.uint8)
+        b[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -10).tobytes(), np.uint8)
+        b[:, :, 2:4] = np.frombuffer(np.float16(2.0 ** -12).tobytes(), np.uint8)
+    else:           # Q6_K: ql, qh, 16 int8 scales, d (fp16) at byte 208
+        b = rng.integers(0, 256, (rows, ns, 210), dtype=np.uint8)
+        b[:, :, 208:210] = np.frombuffer(np.float16(2.0 ** -12).tobytes(), np.uint8)
+    return b.reshape(-1)
+
+
+def block_run(ctx: int, steps: int, n_layers: int = 28) -> dict:
+    """The attention half of a C3 (Llama-3.2-3B, dim 3072) layer with the Q4_K_M weight mix
+    (Q4_K for q, k, o; Q6_K for v): pre-norm, projections, attention at ctx, output projection
+    and residual, as a graph replay over n_layers layers with their own weights and caches."""
+    from llmplayer_amd import _lib
+    from llmplayer_amd import hip_forward_pass as hfp
+    dim = 3072
+    c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=THETA)
+    fp = hfp.HipForwardPass(c, ctx)
+    try:
+        rng = np.random.default_rng(11)
+        fill_caches(fp, c, ctx, n_layers, False, rng)
+        fp.setBlockConfig(dim)
+        wbytes = 0
+        for layer in range(n_layers):
+            lw = hfp.TransformerLayerWeights(attnNorm=np.ones(dim, np.float32))
+            for name, t, rows, cols in (("wq", 12, c.q_dim, dim), ("wk", 12, c.kv_dim, dim),
+                                        ("wv", 14, c.kv_dim, dim), ("wo", 12, dim, c.q_dim)):
+                data = synthetic_gguf(t, rows, cols, rng)
+                setattr(lw, name, hfp.GgufTensor(t, rows, cols, data))
+                if layer == 0:
+                    wbytes += data.nbytes
+            fp.uploadLayerWeights(layer, lw)
+        fp.uploadX(rng.standard_normal(dim).astype(np.float32))
+        call = lambda layer: _lib.call("llmp_attn_block", fp.kv.handle, layer, ctx - 1, 0,
+                                       fp.gpuX.ptr, 0, 0)
+        for i in range(n_layers):
+            call(i)
+        _lib.call("llmp_stream_sync", 0)
+        g = C.c_uint64()
+        _lib.call("llmp_graph_begin", 0)
+        for i in range(steps):
+            call(i % n_layers)
+        _lib.call("llmp_graph_end", 0, C.byref(g))
+        _lib.call("llmp_graph_launch", g.value, 0)
+        _lib.call("llmp_stream_sync", 0)
+        e0, e1 = C.c_uint64(), C.c_uint64()
+        _lib.call("llmp_event_create", C.byref(e0))
+        _lib.call("llmp_event_create", C.byref(e1))
+        _lib.call("llmp_event_record", e0.value, 0)
+        _lib.call("llmp_graph_launch", g.value, 0)
+        _lib.call("llmp_event_record", e1.value, 0)
+        _lib.call("llmp_event_sync", e1.value)
+        ms = C.c_float()
+        _lib.call("llmp_event_elapsed_ms", C.byref(ms), e0.value, e1.value)
+        _lib.call("llmp_graph_destroy", g.value)
+        _lib.call("llmp_event_destroy", e0.value)
+        _lib.call("llmp_event_destroy", e1.value)
+    finally:
+        fp.close()
+    us = ms.value / steps * 1e3
+    return {"ctx": ctx, "weights": "Q4_K_M mix (Q4_K q/k/o, Q6_K v)", "dim": dim,
+            "us_per_layer_call": round(us, 2), "weight_bytes_per_layer": wbytes,
+            "kv_bytes_per_layer": kv_bytes(ctx), "layers_rotated": n_layers}
+
+
 def cpu_baseline(ctx: int, seconds: float) -> dict:
     """The oracle (CPU restatement of Attention.forwardFromProjections) on one layer-call of
     the same shape, parallel over query heads; median over a bounded sample."""
@@ -382,6 +452,10 @@ def main() -> int:
                     help="skip the Q8_0-cache decode measurement")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="skip the C5 prefill measurement")
+    ap.add_argument("--no-block", dest="block", action="store_false",
+                    help="skip the attention-block (projections + attention) measurement")
+    ap.add_argument("--profile-block", action="store_true",
+                    help="for rocprofv3: the attention-block graph at --ctx2 only, then exit")
     ap.add_argument("--profile-workload", action="store_true",
                     help="for rocprofv3: only the warm-up and K eager layer-calls at --ctx "
                          "(no graph replay, no second context, no CPU baseline), then exit")
@@ -412,6 +486,10 @@ def main() -> int:
                                 int(args.rotate_gib * 2**30), q8=args.kv == "q8")
     if args.profile_prefill:
         return profile_prefill(args.profile_prefill, args.steps)
+    if args.profile_block:
+        r = block_run(args.ctx2 or 4096, args.steps)
+        log(f"[bench] profile block: {r}")
+        return 0
     if args.profile_verify:
         r = verify_run(args.ctx, args.profile_verify, args.steps, int(args.rotate_gib * 2**30))
         log(f"[bench] profile verify: {r}")
@@ -453,6 +531,19 @@ def main() -> int:
             log(f"[bench] prefill C5 P={P}: {r['us_per_call']:.1f} us/call, attention kernel "
                 f"{r['attn_kernel_us']:.1f} us ({r['attn_kernel_causal_tflops']:.1f} causal TFLOP/s)")
             prefill.append(r)
+
+    block = None
+    if args.block:
+        block = block_run(args.ctx2 or 4096, 200)
+        attn_us = second["us_per_layer_call"] if second is not None else None
+        if attn_us is not None:
+            block["attention_core_us"] = round(attn_us, 2)
+            proj_us = block["us_per_layer_call"] - attn_us
+            block["projections_us"] = round(proj_us, 2)
+            if proj_us > 0:
+                block["projection_weight_gbps"] = round(block["weight_bytes_per_layer"] / (proj_us * 1e-6) / 1e9, 1)
+        log(f"[bench] attention block C3 Q4_K_M at ctx {block['ctx']}: {block['us_per_layer_call']:.1f} us/layer "
+            f"({block['weight_bytes_per_layer'] / 1e6:.1f} MB of weights)")
 
     # Prefill and verification over a Q8_0 cache (quantising append, dequantising staging).
     q8_prefill = q8_verify = None
@@ -534,6 +625,8 @@ def main() -> int:
         line["prefill_c5_llama1b"] = prefill
     if verify:
         line["speculative_verify_c3"] = verify
+    if block is not None:
+        line["attn_block_c3_q4_k_m"] = block
     if q8_prefill is not None:
         line["q8_0_prefill_c5_llama1b"] = q8_prefill
     if q8_verify is not None:

@@ -7,22 +7,12 @@ namespace {
 
 template <class F>
 hipError_t launch_f(const gk::GemvArgs& a, hipStream_t st) {
-    // Lanes per row: at least two units per lane where the row has them (units = cols/UNIT).
-    const int units = a.cols / F::UNIT;
+    // One row per wave: decode projections have a few thousand rows at most, and a workgroup
+    // per 4 rows puts every CU to work in a single round of loads.
     const size_t lds = (size_t)a.cols * sizeof(float);
-    if (units >= 128) {
-        const int g = gk::kGemvThreads / 64;
-        hipLaunchKernelGGL((gk::gemv_kernel<F, 64>), dim3((a.rows_total + g - 1) / g),
-                           dim3(gk::kGemvThreads), lds, st, a);
-    } else if (units >= 64) {
-        const int g = gk::kGemvThreads / 32;
-        hipLaunchKernelGGL((gk::gemv_kernel<F, 32>), dim3((a.rows_total + g - 1) / g),
-                           dim3(gk::kGemvThreads), lds, st, a);
-    } else {
-        const int g = gk::kGemvThreads / 16;
-        hipLaunchKernelGGL((gk::gemv_kernel<F, 16>), dim3((a.rows_total + g - 1) / g),
-                           dim3(gk::kGemvThreads), lds, st, a);
-    }
+    const int g = gk::kGemvThreads / 64;
+    hipLaunchKernelGGL((gk::gemv_kernel<F, 64>), dim3((a.rows_total + g - 1) / g),
+                       dim3(gk::kGemvThreads), lds, st, a);
     return hipGetLastError();
 }
 

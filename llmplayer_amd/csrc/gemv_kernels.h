@@ -42,7 +42,7 @@ struct GemvArgs {
     int rows_total;
     int cols;
     const float* x;        // [cols]
-    const float* norm_w;   // fused pre-norm weights [cols] (SimdVectorOps.rmsnorm), or nullptr
+    const float* norm_w;   // pre-norm weights [cols] (SimdVectorOps.rmsnorm of x), or nullptr
     float eps;
     float* out;            // [rows_total], when resid is null
     float* resid;          // Wo epilogue: resid[row] += rscale? * value (TransformerBlock residual)
@@ -63,125 +63,108 @@ __device__ __forceinline__ u32x4 ld16(const unsigned char* p) {
 }
 
 // ---- formats ---------------------------------------------------------------------------------
-// F32: plane 0 = [rows][cols] fp32.  Unit: 8 weights (two 16-byte loads).
+// A lane unit is a few bytes of one row's quants: consecutive lanes take consecutive units, so
+// a wave's weight loads are contiguous, and the x values a unit needs are 16-byte chunks that
+// consecutive lanes read from consecutive LDS addresses (no bank conflicts).
+__device__ __forceinline__ const float4& x4(const float* xs, int i) {
+    return *reinterpret_cast<const float4*>(xs + i);
+}
+__device__ __forceinline__ float dot4(float a, float b, float c, float d, const float4& x) {
+    return __builtin_fmaf(d, x.w, __builtin_fmaf(c, x.z, __builtin_fmaf(b, x.y, a * x.x)));
+}
+
+// F32: plane 0 = [rows][cols] fp32.  Unit u: weights 4u .. 4u+3 (one 16-byte load).
 struct FmtF32 {
-    static constexpr int UNIT = 8;
-    struct Raw { u32x4 a, b; };
+    static constexpr int UNIT = 4;
+    static constexpr int MAXU = 8;   // units a lane holds in registers
+    struct Raw { float4 w; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        const unsigned char* p = w.p[0] + row * w.pitch[0] + u * 32;
-        return Raw{ld16(p), ld16(p + 16)};
+        return Raw{*reinterpret_cast<const float4*>(w.p[0] + row * w.pitch[0] + u * 16)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const float* x = xs + u * 8;
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = __builtin_fmaf(__uint_as_float(r.a[i]), x[i], s);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = __builtin_fmaf(__uint_as_float(r.b[i]), x[4 + i], s);
-        return s;
+        return dot4(r.w.x, r.w.y, r.w.z, r.w.w, x4(xs, 4 * u));
     }
 };
 
-// F16 / BF16: plane 0 = [rows][cols] 16-bit.  Unit: 8 weights (one 16-byte load).
+// F16 / BF16: plane 0 = [rows][cols] 16-bit.  Unit u: weights 4u .. 4u+3 (one 8-byte load).
 template <bool BF>
 struct FmtHalf {
-    static constexpr int UNIT = 8;
-    struct Raw { u32x4 a; };
+    static constexpr int UNIT = 4;
+    static constexpr int MAXU = 16;
+    struct Raw { uint2 w; };
+    static __device__ __forceinline__ float cvt(unsigned short h) { return BF ? bf2f(h) : h2f(h); }
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        return Raw{ld16(w.p[0] + row * w.pitch[0] + u * 16)};
+        return Raw{*reinterpret_cast<const uint2*>(w.p[0] + row * w.pitch[0] + u * 8)};
     }
     static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const float* x = xs + u * 8;
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const unsigned v = r.a[i];
-            const float w0 = BF ? bf2f((unsigned short)(v & 0xFFFF)) : h2f((unsigned short)(v & 0xFFFF));
-            const float w1 = BF ? bf2f((unsigned short)(v >> 16)) : h2f((unsigned short)(v >> 16));
-            s = __builtin_fmaf(w0, x[2 * i], s);
-            s = __builtin_fmaf(w1, x[2 * i + 1], s);
-        }
-        return s;
+        return dot4(cvt((unsigned short)(r.w.x & 0xFFFF)), cvt((unsigned short)(r.w.x >> 16)),
+                    cvt((unsigned short)(r.w.y & 0xFFFF)), cvt((unsigned short)(r.w.y >> 16)),
+                    x4(xs, 4 * u));
     }
 };
 
 // Q8_0: plane 0 = quants [rows][cols] int8, plane 1 = scales [rows][cols/32] fp16.
-// Unit: one block of 32 (two 16-byte loads and its scale): d * sum(q * x).
+// Unit u: quants 4u .. 4u+3 of block u/8: d * sum(q * x).
 struct FmtQ8_0 {
-    static constexpr int UNIT = 32;
-    struct Raw { u32x4 a, b; unsigned short d; };
+    static constexpr int UNIT = 4;
+    static constexpr int MAXU = 16;
+    struct Raw { unsigned q; unsigned short d; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        const unsigned char* p = w.p[0] + row * w.pitch[0] + u * 32;
-        const unsigned short d =
-            reinterpret_cast<const unsigned short*>(w.p[1] + row * w.pitch[1])[u];
-        return Raw{ld16(p), ld16(p + 16), d};
+        return Raw{*reinterpret_cast<const unsigned*>(w.p[0] + row * w.pitch[0] + u * 4),
+                   reinterpret_cast<const unsigned short*>(w.p[1] + row * w.pitch[1])[u >> 3]};
     }
     static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const float* x = xs + u * 32;
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const unsigned v = i < 4 ? r.a[i] : r.b[i - 4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                s = __builtin_fmaf((float)(signed char)((v >> (8 * k)) & 0xFF), x[4 * i + k], s);
-        }
+        const float s = dot4((float)(signed char)(r.q & 0xFF), (float)(signed char)((r.q >> 8) & 0xFF),
+                             (float)(signed char)((r.q >> 16) & 0xFF), (float)(signed char)(r.q >> 24),
+                             x4(xs, 4 * u));
         return h2f(r.d) * s;
     }
 };
 
 // Q4_0: plane 0 = nibbles [rows][cols/2] (byte i: element 2i low, 2i+1 high, as
 // Q4_0FloatTensor reads them), plane 1 = scales [rows][cols/32] fp16.
-// Unit: one block of 32: d * sum((q - 8) * x).
+// Unit u: nibble bytes 4u .. 4u+3 = elements 8u .. 8u+7 of block u/4: d * sum((q - 8) x).
 struct FmtQ4_0 {
-    static constexpr int UNIT = 32;
-    struct Raw { u32x4 a; unsigned short d; };
+    static constexpr int UNIT = 8;
+    static constexpr int MAXU = 16;
+    struct Raw { unsigned q; unsigned short d; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        const unsigned short d =
-            reinterpret_cast<const unsigned short*>(w.p[1] + row * w.pitch[1])[u];
-        return Raw{ld16(w.p[0] + row * w.pitch[0] + u * 16), d};
+        return Raw{*reinterpret_cast<const unsigned*>(w.p[0] + row * w.pitch[0] + u * 4),
+                   reinterpret_cast<const unsigned short*>(w.p[1] + row * w.pitch[1])[u >> 2]};
     }
     static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const float* x = xs + u * 32;
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const unsigned v = r.a[i];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const unsigned b = (v >> (8 * k)) & 0xFF;
-                s = __builtin_fmaf((float)((int)(b & 15) - 8), x[8 * i + 2 * k], s);
-                s = __builtin_fmaf((float)((int)(b >> 4) - 8), x[8 * i + 2 * k + 1], s);
-            }
-        }
+        const unsigned q = r.q;
+        auto n = [&](int k) { return (float)((int)((q >> (4 * k)) & 15) - 8); };
+        const float s = dot4(n(0), n(1), n(2), n(3), x4(xs, 8 * u)) +
+                        dot4(n(4), n(5), n(6), n(7), x4(xs, 8 * u + 4));
         return h2f(r.d) * s;
     }
 };
 
 // Q4_K: plane 0 = the 128 nibble bytes of each super-block in the GGUF order (byte 32g + l:
 // element 64g + l low, 64g + 32 + l high), plane 1 = the 16-byte head of each super-block
-// (d, dmin fp16, 12 bytes of 6-bit scales and mins).  Unit: 16 nibble bytes = elements
-// 64g + 16c + i (sub-block 2g) and 64g + 32 + 16c + i (sub-block 2g + 1), i < 16:
-// d*sc*sum(q x) - dmin*m*sum(x) per sub-block half (Q4_KFloatTensor.dot's values).
+// (d, dmin fp16, 12 bytes of 6-bit scales and mins).  Unit u: nibble bytes 4u .. 4u+3 =
+// super-block sb = u/32, group g = (u%32)/8, l = 4(u%8) .. +3: elements 64g + l (sub-block
+// 2g) and 64g + 32 + l (sub-block 2g + 1); value d*sc*q - dmin*m (Q4_KFloatTensor.dot).
 struct FmtQ4_K {
-    static constexpr int UNIT = 32;
-    struct Raw { u32x4 q, h; };
+    static constexpr int UNIT = 8;
+    static constexpr int MAXU = 8;
+    struct Raw { unsigned q; u32x4 h; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        const int sb = u >> 3;
-        return Raw{ld16(w.p[0] + row * w.pitch[0] + u * 16), ld16(w.p[1] + row * w.pitch[1] + sb * 16)};
+        return Raw{*reinterpret_cast<const unsigned*>(w.p[0] + row * w.pitch[0] + u * 4),
+                   ld16(w.p[1] + row * w.pitch[1] + (u >> 5) * 16)};
     }
     static __device__ __forceinline__ int byte_of(const u32x4& v, int i) {
         return (int)((v[i >> 2] >> (8 * (i & 3))) & 0xFF);
     }
     static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const int sb = u >> 3, k = u & 7, g = k >> 1, c = k & 1;
+        const int sb = u >> 5, g = (u >> 3) & 3, l = 4 * (u & 7);
         const float d = h2f((unsigned short)(r.h[0] & 0xFFFF));
         const float dmin = h2f((unsigned short)(r.h[0] >> 16));
-        // scale/min of sub-blocks s0 = 2g and s1 = 2g + 1 (bytes 4..15 of the head)
         int sc[2], mn[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const int s = 2 * g + t;
+            const int s = 2 * g + t;   // bytes 4..15 of the head are the 12 scale bytes
             if (s < 4) {
                 sc[t] = byte_of(r.h, 4 + s) & 63;
                 mn[t] = byte_of(r.h, 8 + s) & 63;
@@ -190,17 +173,14 @@ struct FmtQ4_K {
                 mn[t] = (byte_of(r.h, 8 + s) >> 4) | ((byte_of(r.h, 4 + s) >> 6) << 4);
             }
         }
-        const float* x0 = xs + sb * 256 + g * 64 + c * 16;
-        const float* x1 = x0 + 32;
-        float s0 = 0.0f, s1 = 0.0f, t0 = 0.0f, t1 = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int b = byte_of(r.q, i);
-            s0 = __builtin_fmaf((float)(b & 15), x0[i], s0);
-            s1 = __builtin_fmaf((float)(b >> 4), x1[i], s1);
-            t0 = t0 + x0[i];
-            t1 = t1 + x1[i];
-        }
+        const unsigned q = r.q;
+        const float4& x0 = x4(xs, sb * 256 + 64 * g + l);
+        const float4& x1 = x4(xs, sb * 256 + 64 * g + 32 + l);
+        const float s0 = dot4((float)(q & 15), (float)((q >> 8) & 15), (float)((q >> 16) & 15),
+                              (float)((q >> 24) & 15), x0);
+        const float s1 = dot4((float)((q >> 4) & 15), (float)((q >> 12) & 15), (float)((q >> 20) & 15),
+                              (float)(q >> 28), x1);
+        const float t0 = (x0.x + x0.y) + (x0.z + x0.w), t1 = (x1.x + x1.y) + (x1.z + x1.w);
         const float ds0 = d * (float)sc[0], dm0 = dmin * (float)mn[0];
         const float ds1 = d * (float)sc[1], dm1 = dmin * (float)mn[1];
         return (ds0 * s0 - dm0 * t0) + (ds1 * s1 - dm1 * t1);
@@ -208,69 +188,111 @@ struct FmtQ4_K {
 };
 
 // Q6_K: plane 0 = ql (128 bytes per super-block), plane 1 = qh (64), plane 2 = scales (16
-// int8), plane 3 = d (fp16), each in the GGUF order.  Unit (h, j) of a super-block: l in
-// [16j, 16j + 16) of half h for the four quarters c, i.e. elements 128h + 32c + l, read from
-// ql[64h + l], ql[64h + 32 + l], qh[32h + l] (three 16-byte loads) with scales
-// sc[8h + j + 2c]: sum over c of d*sc*sum((q - 32) x) (Q6_KFloatTensor.dot's values).
+// int8), plane 3 = d (fp16), each in the GGUF order.  Unit u: super-block sb = u/16, half
+// h = (u%16)/8, l = 4(u%8) .. +3 for the four quarters c: elements 128h + 32c + l, from the ql
+// words at 64h + l and 64h + 32 + l and the qh word at 32h + l, scales sc[8h + l/16 + 2c]
+// (Q6_KFloatTensor.dot's values d*sc*(q - 32)).
 struct FmtQ6_K {
-    static constexpr int UNIT = 64;
-    struct Raw { u32x4 l0, l1, h; unsigned s01, s23; unsigned short d; };
+    static constexpr int UNIT = 16;
+    static constexpr int MAXU = 8;
+    struct Raw { unsigned l0, l1, qh, s01, s23; unsigned short d; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        const int sb = u >> 2, h = (u >> 1) & 1, j = u & 1;
-        const unsigned char* ql = w.p[0] + row * w.pitch[0] + sb * 128 + 64 * h + 16 * j;
-        const unsigned char* qh = w.p[1] + row * w.pitch[1] + sb * 64 + 32 * h + 16 * j;
-        const unsigned char* sc = w.p[2] + row * w.pitch[2] + sb * 16 + 8 * h;
-        const unsigned* sw = reinterpret_cast<const unsigned*>(sc);
-        const unsigned short d = reinterpret_cast<const unsigned short*>(w.p[3] + row * w.pitch[3])[sb];
-        return Raw{ld16(ql), ld16(ql + 32), ld16(qh), sw[0], sw[1], d};
-    }
-    static __device__ __forceinline__ int byte_of(const u32x4& v, int i) {
-        return (int)((v[i >> 2] >> (8 * (i & 3))) & 0xFF);
+        const int sb = u >> 4, h = (u >> 3) & 1, l = 4 * (u & 7);
+        const unsigned char* ql = w.p[0] + row * w.pitch[0] + sb * 128 + 64 * h + l;
+        const unsigned* sw =
+            reinterpret_cast<const unsigned*>(w.p[2] + row * w.pitch[2] + sb * 16 + 8 * h);
+        return Raw{*reinterpret_cast<const unsigned*>(ql), *reinterpret_cast<const unsigned*>(ql + 32),
+                   *reinterpret_cast<const unsigned*>(w.p[1] + row * w.pitch[1] + sb * 64 + 32 * h + l),
+                   sw[0], sw[1],
+                   reinterpret_cast<const unsigned short*>(w.p[3] + row * w.pitch[3])[sb]};
     }
     static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const int sb = u >> 2, h = (u >> 1) & 1, j = u & 1;
+        const int sb = u >> 4, h = (u >> 3) & 1, l = 4 * (u & 7), j = (u & 7) >> 2;   // j = l/16
         const float d = h2f(r.d);
-        // sc[8h + j + 2c], c = 0..3: bytes j, j+2 of the first word and j, j+2 of the second
-        const int scv[4] = {(signed char)((r.s01 >> (8 * j)) & 0xFF),
-                            (signed char)((r.s01 >> (8 * (j + 2))) & 0xFF),
-                            (signed char)((r.s23 >> (8 * j)) & 0xFF),
-                            (signed char)((r.s23 >> (8 * (j + 2))) & 0xFF)};
-        const float* x = xs + sb * 256 + 128 * h + 16 * j;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int a = byte_of(r.l0, i), b = byte_of(r.l1, i), hb = byte_of(r.h, i);
-            const int q0 = (a & 15) | ((hb & 3) << 4);
-            const int q1 = (b & 15) | (((hb >> 2) & 3) << 4);
-            const int q2 = (a >> 4) | (((hb >> 4) & 3) << 4);
-            const int q3 = (b >> 4) | (((hb >> 6) & 3) << 4);
-            acc[0] = __builtin_fmaf((float)(q0 - 32), x[i], acc[0]);
-            acc[1] = __builtin_fmaf((float)(q1 - 32), x[32 + i], acc[1]);
-            acc[2] = __builtin_fmaf((float)(q2 - 32), x[64 + i], acc[2]);
-            acc[3] = __builtin_fmaf((float)(q3 - 32), x[96 + i], acc[3]);
-        }
+        // sc[8h + j + 2c]: bytes j, j+2 of the first scale word (c = 0, 1), of the second (c = 2, 3)
+        const float ds[4] = {d * (float)(signed char)((r.s01 >> (8 * j)) & 0xFF),
+                             d * (float)(signed char)((r.s01 >> (8 * (j + 2))) & 0xFF),
+                             d * (float)(signed char)((r.s23 >> (8 * j)) & 0xFF),
+                             d * (float)(signed char)((r.s23 >> (8 * (j + 2))) & 0xFF)};
         float s = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) s = s + (d * (float)scv[c]) * acc[c];
+        for (int c = 0; c < 4; ++c) {
+            const unsigned lo = (c & 1) ? r.l1 : r.l0;
+            const int nib = (c >> 1) * 4;   // c = 0, 1: low nibbles; c = 2, 3: high nibbles
+            float q[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int v = (int)((lo >> (8 * t + nib)) & 15) | (int)(((r.qh >> (8 * t + 2 * c)) & 3) << 4);
+                q[t] = (float)(v - 32);
+            }
+            s = s + ds[c] * dot4(q[0], q[1], q[2], q[3], x4(xs, sb * 256 + 128 * h + 32 * c + l));
+        }
         return s;
     }
 };
 
 // ---- the kernel ------------------------------------------------------------------------------
 // Workgroup: kGemvThreads threads = kGemvThreads/LPR row groups; row group r of workgroup b
-// computes output row b*(kGemvThreads/LPR) + r.  The input is staged in LDS first (fused
-// RMSNorm when norm_w is set: 1/(float)sqrt(sum(x^2)/cols + eps), then (x*r)*w as
-// SimdVectorOps.rmsnorm forms it).
-// Dynamic LDS: cols floats.
+// computes output row b*(kGemvThreads/LPR) + r.  Each lane first issues the loads of its
+// units (up to F::MAXU, then the rest in a loop), so the weight reads are in flight while the
+// input is staged in LDS, RMS-normalised when norm_w is set (1/(float)sqrt(sum(x^2)/cols + eps),
+// then (x*r)*w as SimdVectorOps.rmsnorm forms it).  Dynamic LDS: cols floats, 16-byte aligned.
+// Dot of one row's lane units with the staged input: the first F::MAXU units come from
+// registers loaded at kernel entry, wider rows load the rest in a loop.
 template <class F, int LPR>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
-    extern __shared__ float xs[];
-    __shared__ float red[kGemvThreads / 64];
-    const int tid = threadIdx.x;
-    const int cols = a.cols;
-    if (a.norm_w != nullptr) {
-        float ss = 0.0f;
-        for (int i = tid; i < cols; i += kGemvThreads) ss = __builtin_fmaf(a.x[i], a.x[i], ss);
+__device__ __forceinline__ float row_dot(const typename F::Raw (&raw)[F::MAXU], int nu,
+                                         const GemvSeg& sg, int row, int j, int units,
+                                         const float* xs) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < F::MAXU; ++k)
+        if (k < nu) acc = acc + F::dot(raw[k], xs, j + k * LPR);
+    for (int u = j + F::MAXU * LPR; u < units; u += LPR)
+        acc = acc + F::dot(F::load(sg.w, row, u), xs, u);
+    return acc;
+}
+
+template <class F, int LPR>
+__device__ __forceinline__ void row_load(typename F::Raw (&raw)[F::MAXU], int nu, const GemvSeg& sg,
+                                         int row, int j) {
+#pragma unroll
+    for (int k = 0; k < F::MAXU; ++k)
+        if (k < nu) raw[k] = F::load(sg.w, row, j + k * LPR);
+}
+
+// Input staging: each thread copies float4 chunks c = tid, tid + 256, ... of x into LDS,
+// with the loads of up to four chunks in flight together, and sums their squares; with a
+// pre-norm, the norm weights of its first four chunks are loaded before the reduction so that
+// their latency overlaps it, then each thread scales the chunks it wrote (its own LDS values:
+// no barrier needed).  cols is a multiple of 4.  Ends with a barrier.
+__device__ __forceinline__ void stage_input(const GemvArgs& a, float* xs, int tid) {
+    constexpr int XV = 4;
+    const int cols = a.cols, n4 = cols >> 2;
+    const float4* x4g = reinterpret_cast<const float4*>(a.x);
+    const float4* w4g = reinterpret_cast<const float4*>(a.norm_w);
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+    float ss = 0.0f;
+    for (int base = tid; base < n4; base += XV * kGemvThreads) {
+        float4 xv[XV];
+#pragma unroll
+        for (int k = 0; k < XV; ++k)
+            if (base + k * kGemvThreads < n4) xv[k] = x4g[base + k * kGemvThreads];
+#pragma unroll
+        for (int k = 0; k < XV; ++k)
+            if (base + k * kGemvThreads < n4) {
+                ss = __builtin_fmaf(xv[k].x, xv[k].x, ss);
+                ss = __builtin_fmaf(xv[k].y, xv[k].y, ss);
+                ss = __builtin_fmaf(xv[k].z, xv[k].z, ss);
+                ss = __builtin_fmaf(xv[k].w, xv[k].w, ss);
+                xs4[base + k * kGemvThreads] = xv[k];
+            }
+    }
+    if (w4g != nullptr) {   // pre-attention RMSNorm (SimdVectorOps.rmsnorm's formula)
+        float4 wv[XV];
+#pragma unroll
+        for (int k = 0; k < XV; ++k)
+            if (tid + k * kGemvThreads < n4) wv[k] = w4g[tid + k * kGemvThreads];
+        __shared__ float red[kGemvThreads / 64];
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -281,42 +303,67 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
         float v = tot / (float)cols;
         v = v + a.eps;
         const float r = 1.0f / (float)__builtin_sqrt((double)v);
-        for (int i = tid; i < cols; i += kGemvThreads) xs[i] = (a.x[i] * r) * a.norm_w[i];
-    } else {
-        for (int i = tid; i < cols; i += kGemvThreads) xs[i] = a.x[i];
+#pragma unroll
+        for (int k = 0; k < XV; ++k) {
+            const int c = tid + k * kGemvThreads;
+            if (c < n4) {
+                const float4 xv = xs4[c];
+                xs4[c] = float4{(xv.x * r) * wv[k].x, (xv.y * r) * wv[k].y, (xv.z * r) * wv[k].z,
+                                (xv.w * r) * wv[k].w};
+            }
+        }
+        for (int c = tid + XV * kGemvThreads; c < n4; c += kGemvThreads) {
+            const float4 xv = xs4[c];
+            const float4 w = w4g[c];
+            xs4[c] = float4{(xv.x * r) * w.x, (xv.y * r) * w.y, (xv.z * r) * w.z, (xv.w * r) * w.w};
+        }
     }
     __syncthreads();
+}
 
+__device__ __forceinline__ void store_row(const GemvArgs& a, const GemvSeg& sg, int row_g, int row,
+                                          float acc) {
+    float v = acc;
+    if (sg.bias != nullptr) v = v + sg.bias[row];
+    if (a.resid != nullptr) {
+        if (a.rscale > 0.0f) v = v * a.rscale;
+        a.resid[row_g] = a.resid[row_g] + v;
+    } else {
+        a.out[row_g] = v;
+    }
+}
+
+__device__ __forceinline__ GemvSeg seg_of(const GemvArgs& a, int row_g) {
+    // a uniform select keeps the argument block out of scratch
+    const bool in1 = a.nseg > 1 && row_g >= a.seg[1].out_off;
+    const bool in2 = a.nseg > 2 && row_g >= a.seg[2].out_off;
+    return in2 ? a.seg[2] : (in1 ? a.seg[1] : a.seg[0]);
+}
+
+// ---- the kernels -----------------------------------------------------------------------------
+// Workgroup: kGemvThreads threads = kGemvThreads/LPR row groups; row group r of workgroup b
+// computes output row b*(kGemvThreads/LPR) + r.  Each lane first issues the loads of its
+// units (up to F::MAXU), so the weight reads are in flight while the input is staged in LDS,
+// RMS-normalised when norm_w is set (1/(float)sqrt(sum(x^2)/cols + eps), then (x*r)*w as
+// SimdVectorOps.rmsnorm forms it).  Dynamic LDS: cols floats, 16-byte aligned.
+template <class F, int LPR>
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
+    extern __shared__ float xs[];
+    const int tid = threadIdx.x;
     constexpr int GROUPS = kGemvThreads / LPR;
     const int grp = tid / LPR, j = tid - grp * LPR;
     const int row_g = blockIdx.x * GROUPS + grp;
-    if (row_g >= a.rows_total) return;
-    // segment of this row (a uniform select keeps the argument block out of scratch)
-    const bool in1 = a.nseg > 1 && row_g >= a.seg[1].out_off;
-    const bool in2 = a.nseg > 2 && row_g >= a.seg[2].out_off;
-    const GemvSeg sg = in2 ? a.seg[2] : (in1 ? a.seg[1] : a.seg[0]);
-    const int row = row_g - sg.out_off;
-    const int units = cols / F::UNIT;
-    float acc = 0.0f;
-    int u = j;
-    for (; u + LPR < units; u += 2 * LPR) {   // two units in flight per lane
-        const typename F::Raw r0 = F::load(sg.w, row, u);
-        const typename F::Raw r1 = F::load(sg.w, row, u + LPR);
-        acc = acc + F::dot(r0, xs, u);
-        acc = acc + F::dot(r1, xs, u + LPR);
-    }
-    if (u < units) acc = acc + F::dot(F::load(sg.w, row, u), xs, u);
-    acc = dk::row_group_sum<LPR>(acc);
-    if (j == 0) {
-        float v = acc;
-        if (sg.bias != nullptr) v = v + sg.bias[row];
-        if (a.resid != nullptr) {
-            if (a.rscale > 0.0f) v = v * a.rscale;
-            a.resid[row_g] = a.resid[row_g] + v;
-        } else {
-            a.out[row_g] = v;
-        }
-    }
+    const bool live = row_g < a.rows_total;
+    const GemvSeg sg = seg_of(a, row_g);
+    const int row = live ? row_g - sg.out_off : 0;
+    const int units = a.cols / F::UNIT;
+    const int nu = live ? (units - j + LPR - 1) / LPR : 0;   // units of this lane
+    typename F::Raw raw[F::MAXU];
+    row_load<F, LPR>(raw, nu, sg, row, j);
+    stage_input(a, xs, tid);
+    if (!live) return;
+    const float acc = dk::row_group_sum<LPR>(row_dot<F, LPR>(raw, nu, sg, row, j, units, xs));
+    if (j == 0) store_row(a, sg, row_g, row, acc);
 }
 
 // Post-attention norm and residual (Gemma 2/3, OLMo2: TransformerBlock.forward):

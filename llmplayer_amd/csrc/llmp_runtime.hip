@@ -1129,7 +1129,8 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
         return static_cast<const float*>(W[slot].mem);
     };
 
-    // 1-2. Pre-norm (fused into the projection) and the Q/K/V projections with their biases.
+    // 1-2. Pre-norm (fused into the projections' input staging; absent: x as is, the copy
+    //      TransformerBlock makes for OLMo2) and the Q/K/V projections with their biases.
     gk::GemvSeg segs[3];
     int types[3];
     const int seg_rows[3] = {qd, kvd, kvd}, seg_off[3] = {0, qd, qd + kvd};
@@ -1145,40 +1146,28 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
         segs[i].bias = vecp(bias_slot[i]);
         types[i] = dw.type;
     }
-    bool done[3] = {false, false, false};
-    for (int i = 0; i < 3; ++i) {
-        if (done[i]) continue;
+    // One launch per run of consecutive segments with the same type (their rows are
+    // contiguous in the q|k|v output): one launch for the usual single-type layer, two for
+    // a Q4_K_M-style mix (q, k Q4_K; v Q6_K).  (One launch over two formats measured slower:
+    // holding both formats' registers lowers occupancy more than the launch it saves.)
+    for (int i = 0; i < 3;) {
+        int n = 1;
+        while (i + n < 3 && types[i + n] == types[i]) ++n;
         gk::GemvArgs g{};
-        for (int k = i; k < 3; ++k)
-            if (!done[k] && types[k] == types[i]) {
-                g.seg[g.nseg++] = segs[k];
-                done[k] = true;
-            }
-        // rows of the selected segments are not contiguous in general: one launch per segment
-        // when a type change splits them, else one launch over rows [0, qd + 2 kvd)
-        if (g.nseg == 3) {
-            g.rows_total = qd + 2 * kvd;
-            g.cols = dim;
-            g.x = xp;
-            g.norm_w = vecp(LLMP_W_ATTN_NORM);
-            g.eps = c.eps;
-            g.out = q;
-            LLMP_HIP_CHECK(launch_gemv(g, types[i], st), "block Q/K/V projection launch");
-        } else {
-            for (int k = 0; k < g.nseg; ++k) {
-                gk::GemvArgs h{};
-                h.seg[0] = g.seg[k];
-                h.seg[0].out_off = 0;
-                h.nseg = 1;
-                h.rows_total = g.seg[k].rows;
-                h.cols = dim;
-                h.x = xp;
-                h.norm_w = vecp(LLMP_W_ATTN_NORM);
-                h.eps = c.eps;
-                h.out = q + g.seg[k].out_off;
-                LLMP_HIP_CHECK(launch_gemv(h, types[i], st), "block projection launch");
-            }
+        for (int k = 0; k < n; ++k) {
+            g.seg[k] = segs[i + k];
+            g.seg[k].out_off = segs[i + k].out_off - segs[i].out_off;
         }
+        g.nseg = n;
+        g.rows_total = 0;
+        for (int k = 0; k < n; ++k) g.rows_total += segs[i + k].rows;
+        g.cols = dim;
+        g.x = xp;
+        g.norm_w = vecp(LLMP_W_ATTN_NORM);
+        g.eps = c.eps;
+        g.out = q + segs[i].out_off;
+        LLMP_HIP_CHECK(launch_gemv(g, types[i], st), "block Q/K/V projection launch");
+        i += n;
     }
     // 3-5. The attention core (QK-norm, RoPE, append, attention) into `attn`.
     const int* dpos = reinterpret_cast<const int*>(d_position);
@@ -1196,7 +1185,6 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
     g.rows_total = dim;
     g.cols = qd;
     g.x = attn;
-    g.eps = c.eps;
     const float* post = vecp(LLMP_W_POST_ATTN_NORM);
     if (post) {
         g.out = o;
