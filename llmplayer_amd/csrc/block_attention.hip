@@ -5,15 +5,43 @@
 namespace llmp {
 namespace {
 
-template <class F>
-hipError_t launch_f(const gk::GemvArgs& a, hipStream_t st) {
-    // One row per wave: decode projections have a few thousand rows at most, and a workgroup
-    // per 4 rows puts every CU to work in a single round of loads.
-    const size_t lds = (size_t)a.cols * sizeof(float);
-    const int g = gk::kGemvThreads / 64;
-    hipLaunchKernelGGL((gk::gemv_kernel<F, 64>), dim3((a.rows_total + g - 1) / g),
+template <class F1, int NK1, class F2 = F1, int NK2 = NK1>
+hipError_t launch_nk(const gk::GemvArgs& a, hipStream_t st) {
+    const size_t lds = gk::GemvLds<F1, F2>::bytes(a.cols);
+    const int g = gk::kGemvRowsPerGroup;
+    hipLaunchKernelGGL((gk::gemv_kernel<F1, NK1, F2, NK2>), dim3((a.rows_total + g - 1) / g),
                        dim3(gk::kGemvThreads), lds, st, a);
     return hipGetLastError();
+}
+
+// One row per wave: decode projections have a few thousand rows at most, and a workgroup per
+// 4 rows puts every CU to work in a single round of loads.  NK: the unit rounds a lane holds
+// in registers (the row's rounds rounded up to 2, 4 or 8, at most the format's budget; wider
+// rows take several batches).
+template <class F>
+int nk_for(int cols) {
+    const int rounds = (cols / F::UNIT + 63) / 64;
+    return rounds <= 2 ? 2 : (rounds <= 4 || F::MAXU < 8) ? 4 : 8;
+}
+
+template <class F>
+hipError_t launch_f(const gk::GemvArgs& a, hipStream_t st) {
+    switch (nk_for<F>(a.cols)) {
+    case 2: return launch_nk<F, 2>(a, st);
+    case 4: return launch_nk<F, 4>(a, st);
+    default:
+        if constexpr (F::MAXU >= 8) return launch_nk<F, 8>(a, st);
+        return hipErrorInvalidValue;
+    }
+}
+
+// Q4_K rows (GemvSeg::fmt 0) and Q6_K rows (fmt 1) in one launch: the Q4_K_M mix of the
+// attention projections.
+template <int NK1>
+hipError_t launch_q4k_q6k(const gk::GemvArgs& a, hipStream_t st) {
+    using F2 = gk::FmtQ6_K;
+    if (nk_for<F2>(a.cols) == 2) return launch_nk<gk::FmtQ4_K, NK1, F2, 2>(a, st);
+    return launch_nk<gk::FmtQ4_K, NK1, F2, 4>(a, st);
 }
 
 }  // namespace
@@ -28,6 +56,22 @@ int gemv_unit(int ggml_type) {
     case gk::kQ4_K: return gk::FmtQ4_K::UNIT;
     case gk::kQ6_K: return gk::FmtQ6_K::UNIT;
     default: return 0;
+    }
+}
+
+bool gemv_pair_supported(int first_type, int second_type) {
+    return first_type == gk::kQ4_K && second_type == gk::kQ6_K;
+}
+
+hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_type, hipStream_t st) {
+    if (!gemv_pair_supported(first_type, second_type)) return hipErrorInvalidValue;
+    if (a.cols <= 0 || a.cols > gk::kMaxGemvCols || a.cols % 256 || a.rows_total <= 0 ||
+        a.nseg < 1 || a.nseg > 3)
+        return hipErrorInvalidValue;
+    switch (nk_for<gk::FmtQ4_K>(a.cols)) {
+    case 2: return launch_q4k_q6k<2>(a, st);
+    case 4: return launch_q4k_q6k<4>(a, st);
+    default: return launch_q4k_q6k<8>(a, st);
     }
 }
 

@@ -5,12 +5,14 @@
 // Decode is one token: y = W x is bound by the weight bytes read from HBM.  The host repacks
 // each GGUF tensor at upload into per-row planes so that every lane reads 16-byte aligned
 // chunks (see the plane list of each format below); x (fp32, at most 16384 values) is staged
-// once per workgroup in LDS, with the pre-attention RMSNorm applied while staging.  LPR lanes
-// share a row; lane j takes the row's units j, j+LPR, ... (a unit is 8 to 64 weights); the
-// LPR partial sums are reduced in registers (DPP and permlane steps).  Dequantised weights
+// once per workgroup in LDS, with the pre-attention RMSNorm applied while staging.  A wave
+// takes a row; lane j takes the row's units j, j+64, ... (a unit is 4 to 16 weights); the 64
+// partial sums are reduced in registers (DPP and permlane steps).  Dequantised weights
 // equal the reference tensor classes' values; the dot's summation order differs from the CPU
 // path's, so projections match it to a tolerance, not bit for bit.
 #pragma once
+
+#include <type_traits>
 
 #include "decode_kernels.h"
 
@@ -31,6 +33,7 @@ struct GemvSeg {
     int rows;              // rows of this segment
     int out_off;           // first output row of this segment
     const float* bias;     // [rows] added to the outputs, or nullptr
+    int fmt;               // launches over two formats: 0 = the first, 1 = the second
 };
 
 constexpr int kGemvThreads = 256;
@@ -58,65 +61,99 @@ __device__ __forceinline__ float bf2f(unsigned short b) {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ u32x4 ld16(const unsigned char* p) {
-    return *reinterpret_cast<const u32x4*>(p);
+// Row base of plane k (wave-uniform) plus a 32-bit unsigned byte offset: the loads address a
+// scalar base register plus one vector register.
+__device__ __forceinline__ const unsigned char* rp(const WPlanes& w, int k, int row) {
+    return w.p[k] + (long long)row * w.pitch[k];
+}
+template <class T>
+__device__ __forceinline__ T ldo(const unsigned char* base, unsigned off) {
+    return *reinterpret_cast<const T*>(base + off);
 }
 
 // ---- formats ---------------------------------------------------------------------------------
 // A lane unit is a few bytes of one row's quants: consecutive lanes take consecutive units, so
 // a wave's weight loads are contiguous, and the x values a unit needs are 16-byte chunks that
 // consecutive lanes read from consecutive LDS addresses (no bank conflicts).
+//
+// Each format gives UNIT (weights per unit), MAXU (unit rounds a lane may hold in registers),
+// XSUM (the dot uses the sums of the input's 4-value chunks), TAB (floats per super-block of
+// the row's decoded scale table, 0 = none), Row + load_row + build_tab (the lanes of a wave
+// load the row's per-super-block fields - lane i those of super-block i - and write the table
+// to LDS, once per row), Raw + load (one unit's quant bytes) and dot (lane j's share of the
+// row's dot product with the staged input for unit ub + j, ub a multiple of 64 and the same
+// for the whole wave: the index arithmetic splits into a scalar and a per-lane part).  The dots compute in the reference tensor classes'
+// per-element values (dequantised weight times x); their summation order is this kernel's own.
+struct Staged {
+    const float* xs;     // the input (RMS-normalised when the launch asks for it), cols floats
+    const float* xsum;   // [cols/4]: (x0 + x1) + (x2 + x3) of each 4-value chunk (XSUM formats)
+    const float* tab;    // this row's scale table (TAB formats)
+};
+
 __device__ __forceinline__ const float4& x4(const float* xs, int i) {
     return *reinterpret_cast<const float4*>(xs + i);
 }
 __device__ __forceinline__ float dot4(float a, float b, float c, float d, const float4& x) {
     return __builtin_fmaf(d, x.w, __builtin_fmaf(c, x.z, __builtin_fmaf(b, x.y, a * x.x)));
 }
+// the four bytes of v as floats (v_cvt_f32_ubyte0..3)
+__device__ __forceinline__ float byte_f(unsigned v, int t) { return (float)((v >> (8 * t)) & 0xFFu); }
+
+struct NoRow {};
 
 // F32: plane 0 = [rows][cols] fp32.  Unit u: weights 4u .. 4u+3 (one 16-byte load).
 struct FmtF32 {
-    static constexpr int UNIT = 4;
-    static constexpr int MAXU = 8;   // units a lane holds in registers
+    static constexpr int UNIT = 4, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
     struct Raw { float4 w; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        return Raw{*reinterpret_cast<const float4*>(w.p[0] + row * w.pitch[0] + u * 16)};
+        return Raw{ldo<float4>(rp(w, 0, row), (unsigned)u * 16u)};
     }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        return dot4(r.w.x, r.w.y, r.w.z, r.w.w, x4(xs, 4 * u));
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        return dot4(r.w.x, r.w.y, r.w.z, r.w.w, x4(st.xs, 4 * ub + 4 * j));
     }
 };
 
 // F16 / BF16: plane 0 = [rows][cols] 16-bit.  Unit u: weights 4u .. 4u+3 (one 8-byte load).
 template <bool BF>
 struct FmtHalf {
-    static constexpr int UNIT = 4;
-    static constexpr int MAXU = 16;
+    static constexpr int UNIT = 4, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
     struct Raw { uint2 w; };
     static __device__ __forceinline__ float cvt(unsigned short h) { return BF ? bf2f(h) : h2f(h); }
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        return Raw{*reinterpret_cast<const uint2*>(w.p[0] + row * w.pitch[0] + u * 8)};
+        return Raw{ldo<uint2>(rp(w, 0, row), (unsigned)u * 8u)};
     }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
         return dot4(cvt((unsigned short)(r.w.x & 0xFFFF)), cvt((unsigned short)(r.w.x >> 16)),
                     cvt((unsigned short)(r.w.y & 0xFFFF)), cvt((unsigned short)(r.w.y >> 16)),
-                    x4(xs, 4 * u));
+                    x4(st.xs, 4 * ub + 4 * j));
     }
 };
 
 // Q8_0: plane 0 = quants [rows][cols] int8, plane 1 = scales [rows][cols/32] fp16.
 // Unit u: quants 4u .. 4u+3 of block u/8: d * sum(q * x).
 struct FmtQ8_0 {
-    static constexpr int UNIT = 4;
-    static constexpr int MAXU = 16;
+    static constexpr int UNIT = 4, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
     struct Raw { unsigned q; unsigned short d; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        return Raw{*reinterpret_cast<const unsigned*>(w.p[0] + row * w.pitch[0] + u * 4),
-                   reinterpret_cast<const unsigned short*>(w.p[1] + row * w.pitch[1])[u >> 3]};
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u),
+                   ldo<unsigned short>(rp(w, 1, row), ((unsigned)u >> 3) * 2u)};
     }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
         const float s = dot4((float)(signed char)(r.q & 0xFF), (float)(signed char)((r.q >> 8) & 0xFF),
                              (float)(signed char)((r.q >> 16) & 0xFF), (float)(signed char)(r.q >> 24),
-                             x4(xs, 4 * u));
+                             x4(st.xs, 4 * ub + 4 * j));
         return h2f(r.d) * s;
     }
 };
@@ -125,18 +162,22 @@ struct FmtQ8_0 {
 // Q4_0FloatTensor reads them), plane 1 = scales [rows][cols/32] fp16.
 // Unit u: nibble bytes 4u .. 4u+3 = elements 8u .. 8u+7 of block u/4: d * sum((q - 8) x).
 struct FmtQ4_0 {
-    static constexpr int UNIT = 8;
-    static constexpr int MAXU = 16;
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
     struct Raw { unsigned q; unsigned short d; };
     static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        return Raw{*reinterpret_cast<const unsigned*>(w.p[0] + row * w.pitch[0] + u * 4),
-                   reinterpret_cast<const unsigned short*>(w.p[1] + row * w.pitch[1])[u >> 2]};
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u),
+                   ldo<unsigned short>(rp(w, 1, row), ((unsigned)u >> 2) * 2u)};
     }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
         const unsigned q = r.q;
         auto n = [&](int k) { return (float)((int)((q >> (4 * k)) & 15) - 8); };
-        const float s = dot4(n(0), n(1), n(2), n(3), x4(xs, 8 * u)) +
-                        dot4(n(4), n(5), n(6), n(7), x4(xs, 8 * u + 4));
+        const int i = 8 * ub + 8 * j;
+        const float s = dot4(n(0), n(1), n(2), n(3), x4(st.xs, i)) +
+                        dot4(n(4), n(5), n(6), n(7), x4(st.xs, i + 4));
         return h2f(r.d) * s;
     }
 };
@@ -145,45 +186,60 @@ struct FmtQ4_0 {
 // element 64g + l low, 64g + 32 + l high), plane 1 = the 16-byte head of each super-block
 // (d, dmin fp16, 12 bytes of 6-bit scales and mins).  Unit u: nibble bytes 4u .. 4u+3 =
 // super-block sb = u/32, group g = (u%32)/8, l = 4(u%8) .. +3: elements 64g + l (sub-block
-// 2g) and 64g + 32 + l (sub-block 2g + 1); value d*sc*q - dmin*m (Q4_KFloatTensor.dot).
+// 2g) and 64g + 32 + l (sub-block 2g + 1); value d*sc*q - dmin*m (Q4_KFloatTensor.dot), summed
+// as d*sc * sum(q x) - dmin*m * sum(x).  Table: per super-block, per sub-block s the pair
+// (d*sc_s, dmin*m_s), so a unit's four factors are one 16-byte read.
 struct FmtQ4_K {
-    static constexpr int UNIT = 8;
-    static constexpr int MAXU = 8;
-    struct Raw { unsigned q; u32x4 h; };
-    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        return Raw{*reinterpret_cast<const unsigned*>(w.p[0] + row * w.pitch[0] + u * 4),
-                   ld16(w.p[1] + row * w.pitch[1] + (u >> 5) * 16)};
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 16;
+    static constexpr bool XSUM = true;
+    struct Row { u32x4 h; };
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        return Row{ldo<u32x4>(rp(w, 1, row), (unsigned)min(j, (units >> 5) - 1) * 16u)};
     }
     static __device__ __forceinline__ int byte_of(const u32x4& v, int i) {
         return (int)((v[i >> 2] >> (8 * (i & 3))) & 0xFF);
     }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const int sb = u >> 5, g = (u >> 3) & 3, l = 4 * (u & 7);
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        if (j >= (units >> 5)) return;
         const float d = h2f((unsigned short)(r.h[0] & 0xFFFF));
         const float dmin = h2f((unsigned short)(r.h[0] >> 16));
-        int sc[2], mn[2];
+        float v[16];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int s = 2 * g + t;   // bytes 4..15 of the head are the 12 scale bytes
+        for (int s = 0; s < 8; ++s) {   // bytes 4..15 of the head are the 12 scale bytes
+            int sc, mn;
             if (s < 4) {
-                sc[t] = byte_of(r.h, 4 + s) & 63;
-                mn[t] = byte_of(r.h, 8 + s) & 63;
+                sc = byte_of(r.h, 4 + s) & 63;
+                mn = byte_of(r.h, 8 + s) & 63;
             } else {
-                sc[t] = (byte_of(r.h, 8 + s) & 15) | ((byte_of(r.h, s) >> 6) << 4);
-                mn[t] = (byte_of(r.h, 8 + s) >> 4) | ((byte_of(r.h, 4 + s) >> 6) << 4);
+                sc = (byte_of(r.h, 8 + s) & 15) | ((byte_of(r.h, s) >> 6) << 4);
+                mn = (byte_of(r.h, 8 + s) >> 4) | ((byte_of(r.h, 4 + s) >> 6) << 4);
             }
+            v[2 * s] = d * (float)sc;
+            v[2 * s + 1] = dmin * (float)mn;
         }
-        const unsigned q = r.q;
-        const float4& x0 = x4(xs, sb * 256 + 64 * g + l);
-        const float4& x1 = x4(xs, sb * 256 + 64 * g + 32 + l);
-        const float s0 = dot4((float)(q & 15), (float)((q >> 8) & 15), (float)((q >> 16) & 15),
-                              (float)((q >> 24) & 15), x0);
-        const float s1 = dot4((float)((q >> 4) & 15), (float)((q >> 12) & 15), (float)((q >> 20) & 15),
-                              (float)(q >> 28), x1);
-        const float t0 = (x0.x + x0.y) + (x0.z + x0.w), t1 = (x1.x + x1.y) + (x1.z + x1.w);
-        const float ds0 = d * (float)sc[0], dm0 = dmin * (float)mn[0];
-        const float ds1 = d * (float)sc[1], dm1 = dmin * (float)mn[1];
-        return (ds0 * s0 - dm0 * t0) + (ds1 * s1 - dm1 * t1);
+        float4* t = reinterpret_cast<float4*>(tab + j * TAB);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) t[g] = float4{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+    }
+    struct Raw { unsigned q; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        // u = ub + j: super-block ub/32 + j/32, g = (j/8)%4, l = 4(j%8)
+        const int g = (j >> 3) & 3;
+        const int i0 = 8 * ub + (j >> 5) * 256 + 64 * g + 4 * (j & 7), i1 = i0 + 32;
+        const float4& x0 = x4(st.xs, i0);
+        const float4& x1 = x4(st.xs, i1);
+        // (d*sc, dmin*m) of sub-blocks 2g, 2g+1
+        const float4 f = x4(st.tab, (ub >> 5) * TAB + (j >> 5) * TAB + 4 * g);
+        unsigned lo = r.q & 0x0F0F0F0Fu, hi = (r.q >> 4) & 0x0F0F0F0Fu;
+        // opaque to the optimiser: it would narrow the byte extracts to 4-bit fields, which
+        // lose the one-instruction byte conversions (v_cvt_f32_ubyte0..3)
+        asm("" : "+v"(lo), "+v"(hi));
+        const float p0 = dot4(byte_f(lo, 0), byte_f(lo, 1), byte_f(lo, 2), byte_f(lo, 3), x0);
+        const float p1 = dot4(byte_f(hi, 0), byte_f(hi, 1), byte_f(hi, 2), byte_f(hi, 3), x1);
+        return (f.x * p0 - f.y * st.xsum[i0 >> 2]) + (f.z * p1 - f.w * st.xsum[i1 >> 2]);
     }
 };
 
@@ -191,134 +247,107 @@ struct FmtQ4_K {
 // int8), plane 3 = d (fp16), each in the GGUF order.  Unit u: super-block sb = u/16, half
 // h = (u%16)/8, l = 4(u%8) .. +3 for the four quarters c: elements 128h + 32c + l, from the ql
 // words at 64h + l and 64h + 32 + l and the qh word at 32h + l, scales sc[8h + l/16 + 2c]
-// (Q6_KFloatTensor.dot's values d*sc*(q - 32)).
+// (Q6_KFloatTensor.dot's values d*sc*(q - 32)).  Table: per super-block the 16 products
+// d*sc[8h + i + 2c] at (2h + i)*4 + c, so a unit's four factors are one 16-byte read.  The
+// 6-bit values are assembled four at a time: byte t of (low nibbles | high bits << 4) ^ 0x20
+// is q - 32 in 6-bit two's complement, sign-extended by a bit-field extract.
 struct FmtQ6_K {
-    static constexpr int UNIT = 16;
-    static constexpr int MAXU = 8;
-    struct Raw { unsigned l0, l1, qh, s01, s23; unsigned short d; };
-    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
-        const int sb = u >> 4, h = (u >> 3) & 1, l = 4 * (u & 7);
-        const unsigned char* ql = w.p[0] + row * w.pitch[0] + sb * 128 + 64 * h + l;
-        const unsigned* sw =
-            reinterpret_cast<const unsigned*>(w.p[2] + row * w.pitch[2] + sb * 16 + 8 * h);
-        return Raw{*reinterpret_cast<const unsigned*>(ql), *reinterpret_cast<const unsigned*>(ql + 32),
-                   *reinterpret_cast<const unsigned*>(w.p[1] + row * w.pitch[1] + sb * 64 + 32 * h + l),
-                   sw[0], sw[1],
-                   reinterpret_cast<const unsigned short*>(w.p[3] + row * w.pitch[3])[sb]};
+    static constexpr int UNIT = 16, MAXU = 4, TAB = 16;
+    static constexpr bool XSUM = false;
+    struct Row { u32x4 sc; unsigned short d; };
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        const unsigned sb = (unsigned)min(j, (units >> 4) - 1);
+        return Row{ldo<u32x4>(rp(w, 2, row), sb * 16u), ldo<unsigned short>(rp(w, 3, row), sb * 2u)};
     }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* xs, int u) {
-        const int sb = u >> 4, h = (u >> 3) & 1, l = 4 * (u & 7), j = (u & 7) >> 2;   // j = l/16
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        if (j >= (units >> 4)) return;
         const float d = h2f(r.d);
-        // sc[8h + j + 2c]: bytes j, j+2 of the first scale word (c = 0, 1), of the second (c = 2, 3)
-        const float ds[4] = {d * (float)(signed char)((r.s01 >> (8 * j)) & 0xFF),
-                             d * (float)(signed char)((r.s01 >> (8 * (j + 2))) & 0xFF),
-                             d * (float)(signed char)((r.s23 >> (8 * j)) & 0xFF),
-                             d * (float)(signed char)((r.s23 >> (8 * (j + 2))) & 0xFF)};
+        float v[16];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int k = 8 * h + i + 2 * c;
+                    v[(2 * h + i) * 4 + c] = d * (float)(signed char)((r.sc[k >> 2] >> (8 * (k & 3))) & 0xFF);
+                }
+        float4* t = reinterpret_cast<float4*>(tab + j * TAB);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) t[g] = float4{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+    }
+    struct Raw { unsigned l0, l1, qh; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        const unsigned sb = (unsigned)u >> 4, h = ((unsigned)u >> 3) & 1u, l = 4u * ((unsigned)u & 7u);
+        const unsigned char* ql = rp(w, 0, row);
+        const unsigned qo = sb * 128u + 64u * h + l;
+        return Raw{ldo<unsigned>(ql, qo), ldo<unsigned>(ql, qo + 32u),
+                   ldo<unsigned>(rp(w, 1, row), sb * 64u + 32u * h + l)};
+    }
+    // the signed 6-bit field at bits 8t .. 8t+5 of v (shift left, then arithmetic shift right;
+    // the bit-field-extract builtin's result was converted as unsigned by this compiler)
+    static __device__ __forceinline__ float sx6(unsigned v, int t) {
+        return (float)((int)(v << (26 - 8 * t)) >> 26);
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        // u = ub + j: super-block ub/16 + j/16, h = (j/8)%2, l = 4(j%8), i = l/16
+        const int h = (j >> 3) & 1, l = 4 * (j & 7), i = (j & 7) >> 2;
+        const int sb = (ub >> 4) + (j >> 4);
+        const float4 f = x4(st.tab, sb * TAB + (2 * h + i) * 4);
+        const float ds[4] = {f.x, f.y, f.z, f.w};
         float s = 0.0f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const unsigned lo = (c & 1) ? r.l1 : r.l0;
-            const int nib = (c >> 1) * 4;   // c = 0, 1: low nibbles; c = 2, 3: high nibbles
-            float q[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int v = (int)((lo >> (8 * t + nib)) & 15) | (int)(((r.qh >> (8 * t + 2 * c)) & 3) << 4);
-                q[t] = (float)(v - 32);
-            }
-            s = s + ds[c] * dot4(q[0], q[1], q[2], q[3], x4(xs, sb * 256 + 128 * h + 32 * c + l));
+            const unsigned nib = (c >> 1) ? (lo >> 4) & 0x0F0F0F0Fu : lo & 0x0F0F0F0Fu;
+            const unsigned q = (nib | (((r.qh >> (2 * c)) & 0x03030303u) << 4)) ^ 0x20202020u;
+            s = s + ds[c] * dot4(sx6(q, 0), sx6(q, 1), sx6(q, 2), sx6(q, 3),
+                                 x4(st.xs, sb * 256 + 128 * h + 32 * c + l));
         }
         return s;
     }
 };
 
 // ---- the kernel ------------------------------------------------------------------------------
-// Workgroup: kGemvThreads threads = kGemvThreads/LPR row groups; row group r of workgroup b
-// computes output row b*(kGemvThreads/LPR) + r.  Each lane first issues the loads of its
-// units (up to F::MAXU, then the rest in a loop), so the weight reads are in flight while the
-// input is staged in LDS, RMS-normalised when norm_w is set (1/(float)sqrt(sum(x^2)/cols + eps),
-// then (x*r)*w as SimdVectorOps.rmsnorm forms it).  Dynamic LDS: cols floats, 16-byte aligned.
-// Dot of one row's lane units with the staged input: the first F::MAXU units come from
-// registers loaded at kernel entry, wider rows load the rest in a loop.
-template <class F, int LPR>
-__device__ __forceinline__ float row_dot(const typename F::Raw (&raw)[F::MAXU], int nu,
-                                         const GemvSeg& sg, int row, int j, int units,
-                                         const float* xs) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < F::MAXU; ++k)
-        if (k < nu) acc = acc + F::dot(raw[k], xs, j + k * LPR);
-    for (int u = j + F::MAXU * LPR; u < units; u += LPR)
-        acc = acc + F::dot(F::load(sg.w, row, u), xs, u);
-    return acc;
-}
+// One row per wave: kGemvThreads/64 rows per workgroup, row b*(kGemvThreads/64) + w for wave w
+// of workgroup b, so the row, its segment and the unit count are wave-uniform (scalar
+// registers).  Lane j takes units j, j+64, ...: NK rounds of units are held in registers (the
+// host picks NK from the row width).  Every lane issues all of its loads in one straight
+// sequence with no branch between them - the input chunks, the norm weights, the row's side
+// data, then its NK weight units (unit indices past the row clamped to its last unit, their
+// products dropped) - before it waits for any of them, so the weight reads are in flight while
+// the input is reduced and staged.  Rows wider than 64*NK units take further batches of NK
+// rounds.  Dynamic LDS (GemvLds::bytes): the staged input, its chunk sums (XSUM formats), and
+// one scale table per row of the workgroup (TAB formats).
+constexpr int kGemvRowsPerGroup = kGemvThreads / 64;
+constexpr int kStageChunks = 4;   // float4 chunks of the input per thread held in registers
 
-template <class F, int LPR>
-__device__ __forceinline__ void row_load(typename F::Raw (&raw)[F::MAXU], int nu, const GemvSeg& sg,
-                                         int row, int j) {
-#pragma unroll
-    for (int k = 0; k < F::MAXU; ++k)
-        if (k < nu) raw[k] = F::load(sg.w, row, j + k * LPR);
+// Columns rounded up to whole rounds of 64 units: the lanes past a row's last unit in its last
+// round read this padding (their products are dropped).  A launch over two formats lays out
+// the larger of each region.
+template <class F>
+__host__ __device__ constexpr int gemv_cols_padded(int cols) {
+    return (cols + 64 * F::UNIT - 1) / (64 * F::UNIT) * (64 * F::UNIT);
 }
+template <class F1, class F2 = F1>
+struct GemvLds {
+    static constexpr bool XSUM = F1::XSUM || F2::XSUM;
+    static constexpr int TAB = F1::TAB > F2::TAB ? F1::TAB : F2::TAB;
+    static __host__ __device__ constexpr int cols_padded(int cols) {
+        return gemv_cols_padded<F1>(cols) > gemv_cols_padded<F2>(cols) ? gemv_cols_padded<F1>(cols)
+                                                                        : gemv_cols_padded<F2>(cols);
+    }
+    static __host__ __device__ constexpr size_t bytes(int cols) {
+        const size_t cp = (size_t)cols_padded(cols);
+        return sizeof(float) * (cp + (XSUM ? cp / 4 : 0) + (size_t)kGemvRowsPerGroup * (cp / 256) * TAB);
+    }
+};
 
-// Input staging: each thread copies float4 chunks c = tid, tid + 256, ... of x into LDS,
-// with the loads of up to four chunks in flight together, and sums their squares; with a
-// pre-norm, the norm weights of its first four chunks are loaded before the reduction so that
-// their latency overlaps it, then each thread scales the chunks it wrote (its own LDS values:
-// no barrier needed).  cols is a multiple of 4.  Ends with a barrier.
-__device__ __forceinline__ void stage_input(const GemvArgs& a, float* xs, int tid) {
-    constexpr int XV = 4;
-    const int cols = a.cols, n4 = cols >> 2;
-    const float4* x4g = reinterpret_cast<const float4*>(a.x);
-    const float4* w4g = reinterpret_cast<const float4*>(a.norm_w);
-    float4* xs4 = reinterpret_cast<float4*>(xs);
-    float ss = 0.0f;
-    for (int base = tid; base < n4; base += XV * kGemvThreads) {
-        float4 xv[XV];
-#pragma unroll
-        for (int k = 0; k < XV; ++k)
-            if (base + k * kGemvThreads < n4) xv[k] = x4g[base + k * kGemvThreads];
-#pragma unroll
-        for (int k = 0; k < XV; ++k)
-            if (base + k * kGemvThreads < n4) {
-                ss = __builtin_fmaf(xv[k].x, xv[k].x, ss);
-                ss = __builtin_fmaf(xv[k].y, xv[k].y, ss);
-                ss = __builtin_fmaf(xv[k].z, xv[k].z, ss);
-                ss = __builtin_fmaf(xv[k].w, xv[k].w, ss);
-                xs4[base + k * kGemvThreads] = xv[k];
-            }
-    }
-    if (w4g != nullptr) {   // pre-attention RMSNorm (SimdVectorOps.rmsnorm's formula)
-        float4 wv[XV];
-#pragma unroll
-        for (int k = 0; k < XV; ++k)
-            if (tid + k * kGemvThreads < n4) wv[k] = w4g[tid + k * kGemvThreads];
-        __shared__ float red[kGemvThreads / 64];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        float tot = red[0];
-#pragma unroll
-        for (int w = 1; w < kGemvThreads / 64; ++w) tot = tot + red[w];
-        float v = tot / (float)cols;
-        v = v + a.eps;
-        const float r = 1.0f / (float)__builtin_sqrt((double)v);
-#pragma unroll
-        for (int k = 0; k < XV; ++k) {
-            const int c = tid + k * kGemvThreads;
-            if (c < n4) {
-                const float4 xv = xs4[c];
-                xs4[c] = float4{(xv.x * r) * wv[k].x, (xv.y * r) * wv[k].y, (xv.z * r) * wv[k].z,
-                                (xv.w * r) * wv[k].w};
-            }
-        }
-        for (int c = tid + XV * kGemvThreads; c < n4; c += kGemvThreads) {
-            const float4 xv = xs4[c];
-            const float4 w = w4g[c];
-            xs4[c] = float4{(xv.x * r) * w.x, (xv.y * r) * w.y, (xv.z * r) * w.z, (xv.w * r) * w.w};
-        }
-    }
-    __syncthreads();
+__device__ __forceinline__ GemvSeg seg_of(const GemvArgs& a, int row_g) {
+    // row_g is wave-uniform: the selects are scalar and the argument block stays in registers
+    const bool in1 = a.nseg > 1 && row_g >= a.seg[1].out_off;
+    const bool in2 = a.nseg > 2 && row_g >= a.seg[2].out_off;
+    return in2 ? a.seg[2] : (in1 ? a.seg[1] : a.seg[0]);
 }
 
 __device__ __forceinline__ void store_row(const GemvArgs& a, const GemvSeg& sg, int row_g, int row,
@@ -333,37 +362,153 @@ __device__ __forceinline__ void store_row(const GemvArgs& a, const GemvSeg& sg, 
     }
 }
 
-__device__ __forceinline__ GemvSeg seg_of(const GemvArgs& a, int row_g) {
-    // a uniform select keeps the argument block out of scratch
-    const bool in1 = a.nseg > 1 && row_g >= a.seg[1].out_off;
-    const bool in2 = a.nseg > 2 && row_g >= a.seg[2].out_off;
-    return in2 ? a.seg[2] : (in1 ? a.seg[1] : a.seg[0]);
+__device__ __forceinline__ float4 scale4(const float4& v, float r, const float4& w) {
+    return float4{(v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w};
 }
 
-// ---- the kernels -----------------------------------------------------------------------------
-// Workgroup: kGemvThreads threads = kGemvThreads/LPR row groups; row group r of workgroup b
-// computes output row b*(kGemvThreads/LPR) + r.  Each lane first issues the loads of its
-// units (up to F::MAXU), so the weight reads are in flight while the input is staged in LDS,
-// RMS-normalised when norm_w is set (1/(float)sqrt(sum(x^2)/cols + eps), then (x*r)*w as
-// SimdVectorOps.rmsnorm forms it).  Dynamic LDS: cols floats, 16-byte aligned.
-template <class F, int LPR>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
-    extern __shared__ float xs[];
-    const int tid = threadIdx.x;
-    constexpr int GROUPS = kGemvThreads / LPR;
-    const int grp = tid / LPR, j = tid - grp * LPR;
-    const int row_g = blockIdx.x * GROUPS + grp;
+// Units whose LDS reads the dot loop lets the scheduler hoist together: four, two for Q6_K
+// (four LDS chunks per unit).
+template <class F>
+constexpr int dot_step() { return F::UNIT == 16 ? 2 : 4; }
+
+// One row's registers: the lane's share of the row's side data and NK rounds of units.
+template <class F, int NK>
+struct RowRegs {
+    typename F::Row rw;
+    typename F::Raw raw[NK];
+};
+
+template <class F, int NK>
+__device__ __forceinline__ void row_issue(RowRegs<F, NK>& r, const GemvSeg& sg, int row, int j,
+                                          int units) {
+    r.rw = F::load_row(sg.w, row, j, units);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) r.raw[k] = F::load(sg.w, row, min(j + 64 * k, units - 1));
+}
+
+// The lane's share of the row's dot product: the NK rounds in registers, then further batches.
+template <class F, int NK>
+__device__ __forceinline__ float row_dot(RowRegs<F, NK>& r, const Staged& st, const GemvSeg& sg,
+                                         int row, int j, int units) {
+    float acc = 0.0f;
+    for (int base = 0;;) {
+        // in steps of a few units, the step loop kept rolled: the scheduler would otherwise
+        // hoist every unit's LDS reads to the top and run out of registers
+        constexpr int STEP = NK < dot_step<F>() ? NK : dot_step<F>();
+#pragma unroll 1
+        for (int h = 0; h < NK / STEP; ++h) {
+#pragma unroll
+            for (int k = 0; k < STEP; ++k) {
+                typename F::Raw rk = r.raw[k];
+#pragma unroll
+                for (int m = 1; m < NK / STEP; ++m)
+                    if (h == m) rk = r.raw[m * STEP + k];
+                const int ub = base + 64 * (h * STEP + k);
+                const float d = F::dot(rk, st, ub, j);
+                acc = acc + (ub + j < units ? d : 0.0f);
+            }
+        }
+        base += 64 * NK;
+        if (base >= units) break;   // uniform
+#pragma unroll
+        for (int k = 0; k < NK; ++k) r.raw[k] = F::load(sg.w, row, min(base + j + 64 * k, units - 1));
+    }
+    return acc;
+}
+
+// y = W x over the rows of up to three segments, with the pre-attention RMSNorm of x (norm_w
+// set: 1/(float)sqrt(sum(x^2)/cols + eps), then (x*r)*w as SimdVectorOps.rmsnorm forms it)
+// applied while x is staged in LDS.  The segments share one format, or two (F1, NK1 for
+// GemvSeg::fmt 0 and F2, NK2 for 1: each wave takes its row's path, a uniform branch).
+template <class F1, int NK1, class F2 = F1, int NK2 = NK1>
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(5)))
+void gemv_kernel(GemvArgs a) {
+    using L = GemvLds<F1, F2>;
+    constexpr bool TWO = !(std::is_same<F1, F2>::value && NK1 == NK2);
+    extern __shared__ float lds[];
+    __shared__ float red[kGemvThreads / 64];
+    const int tid = threadIdx.x, j = tid & 63, wave = tid >> 6;
+    const int row_g = __builtin_amdgcn_readfirstlane(blockIdx.x * kGemvRowsPerGroup + wave);
     const bool live = row_g < a.rows_total;
-    const GemvSeg sg = seg_of(a, row_g);
-    const int row = live ? row_g - sg.out_off : 0;
-    const int units = a.cols / F::UNIT;
-    const int nu = live ? (units - j + LPR - 1) / LPR : 0;   // units of this lane
-    typename F::Raw raw[F::MAXU];
-    row_load<F, LPR>(raw, nu, sg, row, j);
-    stage_input(a, xs, tid);
-    if (!live) return;
-    const float acc = dk::row_group_sum<LPR>(row_dot<F, LPR>(raw, nu, sg, row, j, units, xs));
-    if (j == 0) store_row(a, sg, row_g, row, acc);
+    const int row_c = live ? row_g : a.rows_total - 1;   // spare waves load a valid row
+    const GemvSeg sg = seg_of(a, row_c);
+    const int row = row_c - sg.out_off;
+    const bool second = TWO && sg.fmt != 0;
+    const int units1 = a.cols / F1::UNIT, units2 = a.cols / F2::UNIT;
+    const int n4 = a.cols >> 2;
+    const int cp = L::cols_padded(a.cols);
+    float* xs = lds;
+    float* xsum = lds + cp;
+    float* tab = xsum + (L::XSUM ? cp / 4 : 0) + wave * (cp / 256) * L::TAB;
+
+    // input chunks and norm weights (chunk c = tid + 256k, clamped to the last chunk)
+    const bool norm = a.norm_w != nullptr;
+    const float4* x4g = reinterpret_cast<const float4*>(a.x);
+    const float4* w4g = reinterpret_cast<const float4*>(norm ? a.norm_w : a.x);
+    float4 xv[kStageChunks], wv[kStageChunks];
+#pragma unroll
+    for (int k = 0; k < kStageChunks; ++k) {
+        const int c = min(tid + k * kGemvThreads, n4 - 1);
+        xv[k] = x4g[c];
+        wv[k] = w4g[c];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the input loads ahead of the weight loads
+    // the row's side data, then the weight units
+    RowRegs<F1, NK1> r1;
+    RowRegs<F2, NK2> r2;
+    if (!second) row_issue(r1, sg, row, j, units1);
+    else row_issue(r2, sg, row, j, units2);
+
+    // sum of squares of x (chunks beyond the registers: a second read, from cache)
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kStageChunks; ++k)
+        if (tid + k * kGemvThreads < n4) {
+            ss = __builtin_fmaf(xv[k].x, xv[k].x, ss);
+            ss = __builtin_fmaf(xv[k].y, xv[k].y, ss);
+            ss = __builtin_fmaf(xv[k].z, xv[k].z, ss);
+            ss = __builtin_fmaf(xv[k].w, xv[k].w, ss);
+        }
+    for (int c = tid + kStageChunks * kGemvThreads; c < n4; c += kGemvThreads) {
+        const float4 v = x4g[c];
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+    }
+    float r = 1.0f;
+    if (norm) {   // SimdVectorOps.rmsnorm's scale
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off);
+        if (j == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = red[0];
+#pragma unroll
+        for (int w = 1; w < kGemvThreads / 64; ++w) tot = tot + red[w];
+        float v = tot / (float)a.cols;
+        v = v + a.eps;
+        r = 1.0f / (float)__builtin_sqrt((double)v);
+    }
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+    auto put = [&](int c, const float4& v) {
+        xs4[c] = v;
+        if (L::XSUM) xsum[c] = (v.x + v.y) + (v.z + v.w);
+    };
+#pragma unroll
+    for (int k = 0; k < kStageChunks; ++k) {
+        const int c = tid + k * kGemvThreads;
+        if (c < n4) put(c, norm ? scale4(xv[k], r, wv[k]) : xv[k]);
+    }
+    for (int c = tid + kStageChunks * kGemvThreads; c < n4; c += kGemvThreads)
+        put(c, norm ? scale4(x4g[c], r, w4g[c]) : x4g[c]);
+    if (!second) F1::build_tab(r1.rw, tab, j, units1);
+    else F2::build_tab(r2.rw, tab, j, units2);
+    __syncthreads();
+
+    const Staged st{xs, xsum, tab};
+    float acc = !second ? row_dot(r1, st, sg, row, j, units1) : row_dot(r2, st, sg, row, j, units2);
+    acc = dk::row_group_sum<64>(acc);
+    if (live && j == 0) store_row(a, sg, row_g, row, acc);
 }
 
 // Post-attention norm and residual (Gemma 2/3, OLMo2: TransformerBlock.forward):

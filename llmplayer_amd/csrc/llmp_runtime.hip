@@ -1144,30 +1144,54 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
         segs[i].rows = seg_rows[i];
         segs[i].out_off = seg_off[i];
         segs[i].bias = vecp(bias_slot[i]);
+        segs[i].fmt = 0;
         types[i] = dw.type;
     }
-    // One launch per run of consecutive segments with the same type (their rows are
-    // contiguous in the q|k|v output): one launch for the usual single-type layer, two for
-    // a Q4_K_M-style mix (q, k Q4_K; v Q6_K).  (One launch over two formats measured slower:
-    // holding both formats' registers lowers occupancy more than the launch it saves.)
-    for (int i = 0; i < 3;) {
-        int n = 1;
-        while (i + n < 3 && types[i + n] == types[i]) ++n;
-        gk::GemvArgs g{};
-        for (int k = 0; k < n; ++k) {
-            g.seg[k] = segs[i + k];
-            g.seg[k].out_off = segs[i + k].out_off - segs[i].out_off;
+    // One launch for the three projections when they share a type or form a supported mix
+    // of two (a Q4_K_M layer: q, k Q4_K and v Q6_K; GemvSeg::fmt tells each row's format);
+    // otherwise one launch per run of consecutive segments with the same type (their rows are
+    // contiguous in the q|k|v output).
+    int t1 = types[0], t2 = -1;
+    for (int i = 1; i < 3; ++i)
+        if (types[i] != t1) {
+            if (t2 < 0) t2 = types[i];
+            else if (types[i] != t2) t2 = -2;
         }
-        g.nseg = n;
-        g.rows_total = 0;
-        for (int k = 0; k < n; ++k) g.rows_total += segs[i + k].rows;
+    if (t2 >= 0 && !gemv_pair_supported(t1, t2) && gemv_pair_supported(t2, t1)) std::swap(t1, t2);
+    if (t2 >= 0 && gemv_pair_supported(t1, t2)) {
+        gk::GemvArgs g{};
+        for (int k = 0; k < 3; ++k) {
+            g.seg[k] = segs[k];
+            g.seg[k].fmt = types[k] == t1 ? 0 : 1;
+        }
+        g.nseg = 3;
+        g.rows_total = qd + 2 * kvd;
         g.cols = dim;
         g.x = xp;
         g.norm_w = vecp(LLMP_W_ATTN_NORM);
         g.eps = c.eps;
-        g.out = q + segs[i].out_off;
-        LLMP_HIP_CHECK(launch_gemv(g, types[i], st), "block Q/K/V projection launch");
-        i += n;
+        g.out = q;
+        LLMP_HIP_CHECK(launch_gemv_pair(g, t1, t2, st), "block Q/K/V projection launch");
+    } else {
+        for (int i = 0; i < 3;) {
+            int n = 1;
+            while (i + n < 3 && types[i + n] == types[i]) ++n;
+            gk::GemvArgs g{};
+            for (int k = 0; k < n; ++k) {
+                g.seg[k] = segs[i + k];
+                g.seg[k].out_off = segs[i + k].out_off - segs[i].out_off;
+            }
+            g.nseg = n;
+            g.rows_total = 0;
+            for (int k = 0; k < n; ++k) g.rows_total += segs[i + k].rows;
+            g.cols = dim;
+            g.x = xp;
+            g.norm_w = vecp(LLMP_W_ATTN_NORM);
+            g.eps = c.eps;
+            g.out = q + segs[i].out_off;
+            LLMP_HIP_CHECK(launch_gemv(g, types[i], st), "block Q/K/V projection launch");
+            i += n;
+        }
     }
     // 3-5. The attention core (QK-norm, RoPE, append, attention) into `attn`.
     const int* dpos = reinterpret_cast<const int*>(d_position);

@@ -111,6 +111,22 @@ def test_block_c3_llama3b_shape_q4_k_m_mix():
          seed=610, what="C3 Q4_K_M")
 
 
+@pytest.mark.parametrize("dim", [1024, 2048, 4096, 8192])
+def test_block_q4_k_m_mix_widths(dim):
+    """The Q4_K + Q6_K projections in one launch at widths that take 2, 4 and 8 unit rounds in
+    registers and, at 8192, a second batch of rounds."""
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    _run(c, dim, 64, 30, 2, (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K),
+         seed=700 + dim // 1024, what=f"Q4_K_M mix dim {dim}")
+
+
+def test_block_q6_k_q4_k_mix_swapped():
+    """Q6_K for q, k and Q4_K for v (the pair in the other order, GemvSeg::fmt by type)."""
+    c = hfp.ModelConfig(16, 4, 128, 1, rope_freq_base=500000.0)
+    _run(c, 2048, 64, 21, 2, (gp.GGML_Q6_K, gp.GGML_Q6_K, gp.GGML_Q4_K, gp.GGML_Q6_K),
+         seed=720, what="Q6_K q/k + Q4_K v", bias=True)
+
+
 def test_block_merged_qkv_phi3():
     c = hfp.ModelConfig(16, 16, 64, 1, rope_freq_base=10000.0)
     _run(c, 1024, 64, 20, 2, (gp.GGML_F16,) * 4, seed=620, what="merged QKV f16", merged=True)
