@@ -277,10 +277,12 @@ def synthetic_gguf(t: int, rows: int, cols: int, rng) -> np.ndarray:
     return b.reshape(-1)
 
 
-def block_run(ctx: int, steps: int, n_layers: int = 28) -> dict:
+def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False) -> dict:
     """The attention half of a C3 (Llama-3.2-3B, dim 3072) layer with the Q4_K_M weight mix
     (Q4_K for q, k, o; Q6_K for v): pre-norm, projections, attention at ctx, output projection
-    and residual, as a graph replay over n_layers layers with their own weights and caches."""
+    and residual, as a graph replay over n_layers layers with their own weights and caches.
+    q8_input: the Q4_K projections on the Q8_1-quantised input (the reference GPU's int8
+    matvecs) instead of the fp32 input."""
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
     dim = 3072
@@ -289,7 +291,7 @@ def block_run(ctx: int, steps: int, n_layers: int = 28) -> dict:
     try:
         rng = np.random.default_rng(11)
         fill_caches(fp, c, ctx, n_layers, False, rng)
-        fp.setBlockConfig(dim)
+        fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_Q8_1 if q8_input else _lib.LLMP_INPUT_F32)
         wbytes = 0
         for layer in range(n_layers):
             lw = hfp.TransformerLayerWeights(attnNorm=np.ones(dim, np.float32))
@@ -329,6 +331,7 @@ def block_run(ctx: int, steps: int, n_layers: int = 28) -> dict:
         fp.close()
     us = ms.value / steps * 1e3
     return {"ctx": ctx, "weights": "Q4_K_M mix (Q4_K q/k/o, Q6_K v)", "dim": dim,
+            "input": "Q8_1 (int8 dot products for Q4_K)" if q8_input else "fp32",
             "us_per_layer_call": round(us, 2), "weight_bytes_per_layer": wbytes,
             "kv_bytes_per_layer": kv_bytes(ctx), "layers_rotated": n_layers}
 
@@ -454,6 +457,8 @@ def main() -> int:
                     help="skip the C5 prefill measurement")
     ap.add_argument("--no-block", dest="block", action="store_false",
                     help="skip the attention-block (projections + attention) measurement")
+    ap.add_argument("--block-q8", action="store_true",
+                    help="--profile-block: the Q8_1 input mode")
     ap.add_argument("--profile-block", action="store_true",
                     help="for rocprofv3: the attention-block graph at --ctx2 only, then exit")
     ap.add_argument("--profile-workload", action="store_true",
@@ -487,7 +492,7 @@ def main() -> int:
     if args.profile_prefill:
         return profile_prefill(args.profile_prefill, args.steps)
     if args.profile_block:
-        r = block_run(args.ctx2 or 4096, args.steps)
+        r = block_run(args.ctx2 or 4096, args.steps, q8_input=args.block_q8)
         log(f"[bench] profile block: {r}")
         return 0
     if args.profile_verify:
@@ -532,7 +537,7 @@ def main() -> int:
                 f"{r['attn_kernel_us']:.1f} us ({r['attn_kernel_causal_tflops']:.1f} causal TFLOP/s)")
             prefill.append(r)
 
-    block = None
+    block = block_q8 = None
     if args.block:
         block = block_run(args.ctx2 or 4096, 200)
         attn_us = second["us_per_layer_call"] if second is not None else None
@@ -544,6 +549,9 @@ def main() -> int:
                 block["projection_weight_gbps"] = round(block["weight_bytes_per_layer"] / (proj_us * 1e-6) / 1e9, 1)
         log(f"[bench] attention block C3 Q4_K_M at ctx {block['ctx']}: {block['us_per_layer_call']:.1f} us/layer "
             f"({block['weight_bytes_per_layer'] / 1e6:.1f} MB of weights)")
+        block_q8 = block_run(args.ctx2 or 4096, 200, q8_input=True)
+        log(f"[bench] attention block C3 Q4_K_M at ctx {block_q8['ctx']}, Q8_1 input: "
+            f"{block_q8['us_per_layer_call']:.1f} us/layer")
 
     # Prefill and verification over a Q8_0 cache (quantising append, dequantising staging).
     q8_prefill = q8_verify = None
@@ -627,6 +635,8 @@ def main() -> int:
         line["speculative_verify_c3"] = verify
     if block is not None:
         line["attn_block_c3_q4_k_m"] = block
+    if block_q8 is not None:
+        line["attn_block_c3_q4_k_m_q8_1_input"] = block_q8
     if q8_prefill is not None:
         line["q8_0_prefill_c5_llama1b"] = q8_prefill
     if q8_verify is not None:

@@ -294,6 +294,16 @@ int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0
 /* Model-wide block parameters: dim = embeddingLength (a multiple of 32, at most 16384);
  * residual_scale = Granite's residualScale (0 = off). */
 int llmp_block_config(uint64_t handle, int dim, float residual_scale);
+/* How the block's projections read their input.  LLMP_INPUT_F32 (the default): every type
+ * takes the fp32 (normalised) input, the CPU engine's arithmetic (FloatTensor.matmul).
+ * LLMP_INPUT_Q8_1: Q4_K and Q8_0 weights take a Q8_1 copy of the input (blocks of 32: scale
+ * max|x|/127, int8 quants, block sum) and exact int8 dot products, the reference GPU's
+ * default matvecs (CudaForwardPass.java:783-790 cuda.dp4a, :1998-2037; quantize_q8.cu,
+ * rmsnorm_quantize.cu, matmul_q4_k_dp4a.cu, matmul_q8_0_dp4a.cu); other types keep the fp32
+ * input, as there. */
+#define LLMP_INPUT_F32   0
+#define LLMP_INPUT_Q8_1  1
+int llmp_block_input_mode(uint64_t handle, int mode);
 /* Upload one slot of a configured layer: data = host bytes in the GGUF layout of ggml_type
  * (rows * row_bytes; fp32 for the vectors), or NULL to clear the slot.  The weight is repacked
  * into per-row planes on the device.  Set-up only: it allocates and synchronises. */

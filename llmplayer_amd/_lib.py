@@ -28,6 +28,7 @@ LLMP_GGML_F32, LLMP_GGML_F16, LLMP_GGML_Q4_0, LLMP_GGML_Q8_0 = 0, 1, 2, 8
 LLMP_GGML_Q4_K, LLMP_GGML_Q6_K, LLMP_GGML_BF16 = 12, 14, 30
 (LLMP_W_ATTN_NORM, LLMP_W_Q, LLMP_W_K, LLMP_W_V, LLMP_W_QKV, LLMP_W_O, LLMP_W_Q_BIAS, LLMP_W_K_BIAS,
  LLMP_W_V_BIAS, LLMP_W_O_BIAS, LLMP_W_POST_ATTN_NORM) = range(11)
+LLMP_INPUT_F32, LLMP_INPUT_Q8_1 = 0, 1
 LLMP_PROF_DECODE_SPLIT, LLMP_PROF_DECODE_REDUCE = 0, 1
 LLMP_PROF_PREFILL_APPEND, LLMP_PROF_PREFILL_ATTN = 2, 3
 
@@ -76,6 +77,7 @@ SIGNATURES = {
     "llmp_attn_prefill_ex": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64],
     "llmp_layer_norm_mode": [_u64, _i32, _i32],
     "llmp_block_config": [_u64, _i32, _f32],
+    "llmp_block_input_mode": [_u64, _i32],
     "llmp_layer_weight": [_u64, _i32, _i32, _i32, _i32, _i32, C.c_void_p, _u64],
     "llmp_attn_block": [_u64, _i32, _i32, _u64, _u64, _i32, _u64],
     "llmp_attn_decode_shared": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],

@@ -16,32 +16,59 @@ hipError_t launch_nk(const gk::GemvArgs& a, hipStream_t st) {
 
 // One row per wave: decode projections have a few thousand rows at most, and a workgroup per
 // 4 rows puts every CU to work in a single round of loads.  NK: the unit rounds a lane holds
-// in registers (the row's rounds rounded up to 2, 4 or 8, at most the format's budget; wider
-// rows take several batches).
+// in registers, the row's rounds rounded up to 2, 3, 4, 6 or 8 (at most the format's budget;
+// wider rows take several batches).
 template <class F>
 int nk_for(int cols) {
     const int rounds = (cols / F::UNIT + 63) / 64;
-    return rounds <= 2 ? 2 : (rounds <= 4 || F::MAXU < 8) ? 4 : 8;
+    const int nk = rounds <= 2 ? 2 : rounds <= 3 ? 3 : rounds <= 4 ? 4 : rounds <= 6 ? 6 : 8;
+    return nk > F::MAXU ? F::MAXU : nk;
 }
 
 template <class F>
 hipError_t launch_f(const gk::GemvArgs& a, hipStream_t st) {
     switch (nk_for<F>(a.cols)) {
     case 2: return launch_nk<F, 2>(a, st);
+    case 3: return launch_nk<F, 3>(a, st);
     case 4: return launch_nk<F, 4>(a, st);
     default:
-        if constexpr (F::MAXU >= 8) return launch_nk<F, 8>(a, st);
-        return hipErrorInvalidValue;
+        if constexpr (F::MAXU >= 8) {
+            if (nk_for<F>(a.cols) == 6) return launch_nk<F, 6>(a, st);
+            return launch_nk<F, 8>(a, st);
+        } else {
+            return hipErrorInvalidValue;
+        }
     }
 }
 
-// Q4_K rows (GemvSeg::fmt 0) and Q6_K rows (fmt 1) in one launch: the Q4_K_M mix of the
-// attention projections.
-template <int NK1>
+// Q4_K rows (GemvSeg::fmt 0, fp32 or Q8_1 input) and Q6_K rows (fmt 1) in one launch: the
+// Q4_K_M mix of the attention projections.
+template <class F1, int NK1>
 hipError_t launch_q4k_q6k(const gk::GemvArgs& a, hipStream_t st) {
     using F2 = gk::FmtQ6_K;
-    if (nk_for<F2>(a.cols) == 2) return launch_nk<gk::FmtQ4_K, NK1, F2, 2>(a, st);
-    return launch_nk<gk::FmtQ4_K, NK1, F2, 4>(a, st);
+    switch (nk_for<F2>(a.cols)) {
+    case 2: return launch_nk<F1, NK1, F2, 2>(a, st);
+    case 3: return launch_nk<F1, NK1, F2, 3>(a, st);
+    default: return launch_nk<F1, NK1, F2, 4>(a, st);
+    }
+}
+
+// The Q8_1-input Q4_K side holds at most 4 rounds next to Q6_K (more spills registers); its
+// rows need 4 rounds up to 4096 columns.
+template <class F1>
+hipError_t launch_pair_f(const gk::GemvArgs& a, hipStream_t st) {
+    switch (nk_for<F1>(a.cols)) {
+    case 2: return launch_q4k_q6k<F1, 2>(a, st);
+    case 3: return launch_q4k_q6k<F1, 3>(a, st);
+    case 4: return launch_q4k_q6k<F1, 4>(a, st);
+    default:
+        if constexpr (F1::Q8IN) {
+            return launch_q4k_q6k<F1, 4>(a, st);
+        } else {
+            if (nk_for<F1>(a.cols) == 6) return launch_q4k_q6k<F1, 6>(a, st);
+            return launch_q4k_q6k<F1, 8>(a, st);
+        }
+    }
 }
 
 }  // namespace
@@ -63,23 +90,22 @@ bool gemv_pair_supported(int first_type, int second_type) {
     return first_type == gk::kQ4_K && second_type == gk::kQ6_K;
 }
 
-hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_type, hipStream_t st) {
+hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_type, bool q8_input,
+                            hipStream_t st) {
     if (!gemv_pair_supported(first_type, second_type)) return hipErrorInvalidValue;
     if (a.cols <= 0 || a.cols > gk::kMaxGemvCols || a.cols % 256 || a.rows_total <= 0 ||
         a.nseg < 1 || a.nseg > 3)
         return hipErrorInvalidValue;
-    switch (nk_for<gk::FmtQ4_K>(a.cols)) {
-    case 2: return launch_q4k_q6k<2>(a, st);
-    case 4: return launch_q4k_q6k<4>(a, st);
-    default: return launch_q4k_q6k<8>(a, st);
-    }
+    return q8_input ? launch_pair_f<gk::FmtQ4_KQ8>(a, st) : launch_pair_f<gk::FmtQ4_K>(a, st);
 }
 
-hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, hipStream_t st) {
+hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipStream_t st) {
     if (a.cols <= 0 || a.cols > gk::kMaxGemvCols || a.rows_total <= 0 || a.nseg < 1 || a.nseg > 3)
         return hipErrorInvalidValue;
     const int unit = gemv_unit(ggml_type);
     if (unit == 0 || a.cols % unit) return hipErrorInvalidValue;
+    if (q8_input && ggml_type == gk::kQ4_K) return launch_f<gk::FmtQ4_KQ8>(a, st);
+    if (q8_input && ggml_type == gk::kQ8_0) return launch_f<gk::FmtQ8_0Q8>(a, st);
     switch (ggml_type) {
     case gk::kF32: return launch_f<gk::FmtF32>(a, st);
     case gk::kF16: return launch_f<gk::FmtHalf<false>>(a, st);

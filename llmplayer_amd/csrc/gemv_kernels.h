@@ -85,9 +85,12 @@ __device__ __forceinline__ T ldo(const unsigned char* base, unsigned off) {
 // for the whole wave: the index arithmetic splits into a scalar and a per-lane part).  The dots compute in the reference tensor classes'
 // per-element values (dequantised weight times x); their summation order is this kernel's own.
 struct Staged {
-    const float* xs;     // the input (RMS-normalised when the launch asks for it), cols floats
-    const float* xsum;   // [cols/4]: (x0 + x1) + (x2 + x3) of each 4-value chunk (XSUM formats)
-    const float* tab;    // this row's scale table (TAB formats)
+    const float* xs;            // the input (RMS-normalised when the launch asks for it), cols floats
+    const float* xsum;          // [cols/4]: (x0 + x1) + (x2 + x3) of each 4-value chunk (XSUM formats)
+    const float* tab;           // this row's scale table (TAB formats)
+    const unsigned char* xq;    // Q8IN formats: the input's Q8_1 quants [cols] (int8)
+    const float* xd;            //   their block scales [cols/32]
+    const float* xss;           //   and block sums [cols/32]
 };
 
 __device__ __forceinline__ const float4& x4(const float* xs, int i) {
@@ -104,7 +107,7 @@ struct NoRow {};
 // F32: plane 0 = [rows][cols] fp32.  Unit u: weights 4u .. 4u+3 (one 16-byte load).
 struct FmtF32 {
     static constexpr int UNIT = 4, MAXU = 8, TAB = 0;
-    static constexpr bool XSUM = false;
+    static constexpr bool XSUM = false, Q8IN = false;
     using Row = NoRow;
     static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
     static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
@@ -121,7 +124,7 @@ struct FmtF32 {
 template <bool BF>
 struct FmtHalf {
     static constexpr int UNIT = 4, MAXU = 8, TAB = 0;
-    static constexpr bool XSUM = false;
+    static constexpr bool XSUM = false, Q8IN = false;
     using Row = NoRow;
     static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
     static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
@@ -141,7 +144,7 @@ struct FmtHalf {
 // Unit u: quants 4u .. 4u+3 of block u/8: d * sum(q * x).
 struct FmtQ8_0 {
     static constexpr int UNIT = 4, MAXU = 8, TAB = 0;
-    static constexpr bool XSUM = false;
+    static constexpr bool XSUM = false, Q8IN = false;
     using Row = NoRow;
     static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
     static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
@@ -163,7 +166,7 @@ struct FmtQ8_0 {
 // Unit u: nibble bytes 4u .. 4u+3 = elements 8u .. 8u+7 of block u/4: d * sum((q - 8) x).
 struct FmtQ4_0 {
     static constexpr int UNIT = 8, MAXU = 8, TAB = 0;
-    static constexpr bool XSUM = false;
+    static constexpr bool XSUM = false, Q8IN = false;
     using Row = NoRow;
     static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
     static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
@@ -191,16 +194,22 @@ struct FmtQ4_0 {
 // (d*sc_s, dmin*m_s), so a unit's four factors are one 16-byte read.
 struct FmtQ4_K {
     static constexpr int UNIT = 8, MAXU = 8, TAB = 16;
-    static constexpr bool XSUM = true;
+    static constexpr bool XSUM = true, Q8IN = false;
     struct Row { u32x4 h; };
     static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
-        return Row{ldo<u32x4>(rp(w, 1, row), (unsigned)min(j, (units >> 5) - 1) * 16u)};
+        return head(w, row, j, units >> 5);
+    }
+    static __device__ __forceinline__ Row head(const WPlanes& w, int row, int j, int ns) {
+        return Row{ldo<u32x4>(rp(w, 1, row), (unsigned)min(j, ns - 1) * 16u)};
     }
     static __device__ __forceinline__ int byte_of(const u32x4& v, int i) {
         return (int)((v[i >> 2] >> (8 * (i & 3))) & 0xFF);
     }
     static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
-        if (j >= (units >> 5)) return;
+        build_tab_ns(r, tab, j, units >> 5);
+    }
+    static __device__ __forceinline__ void build_tab_ns(const Row& r, float* tab, int j, int ns) {
+        if (j >= ns) return;
         const float d = h2f((unsigned short)(r.h[0] & 0xFFFF));
         const float dmin = h2f((unsigned short)(r.h[0] >> 16));
         float v[16];
@@ -253,7 +262,7 @@ struct FmtQ4_K {
 // is q - 32 in 6-bit two's complement, sign-extended by a bit-field extract.
 struct FmtQ6_K {
     static constexpr int UNIT = 16, MAXU = 4, TAB = 16;
-    static constexpr bool XSUM = false;
+    static constexpr bool XSUM = false, Q8IN = false;
     struct Row { u32x4 sc; unsigned short d; };
     static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
         const unsigned sb = (unsigned)min(j, (units >> 4) - 1);
@@ -308,6 +317,103 @@ struct FmtQ6_K {
     }
 };
 
+// ---- Q8_1 input: the reference GPU's int8 matvecs -------------------------------------------
+// CudaForwardPass runs its Q4_K and Q8_0 projections on a Q8_1 copy of the input by default
+// (CudaForwardPass.java:783-790, 1998-2037; rmsnorm_quantize.cu, quantize_q8.cu,
+// matmul_q4_k_dp4a.cu, matmul_q8_0_dp4a.cu): per 32 values d = max|x|/127, quants rint(x*127/
+// max|x|) clamped to +-127, s = sum(x); a block's dot is an exact int8 dot product scaled in
+// float.  Here the weights keep the planes of FmtQ4_K / FmtQ8_0; a unit is 8 weight bytes,
+// and the products are v_dot4c_i32_i8.
+
+// Quantises chunk c (4 values) of the input into the Q8_1 staging.  The 8 chunks of a block
+// are held by 8 consecutive lanes (c = tid + 256k), which must all call this together: the
+// block's max and sum are butterflies over them (xor 4, 2, 1; the sum of ((x0 + x1) + (x2 +
+// x3)) per lane).  One IEEE division per lane: the group's first lane computes max/127 (the
+// block scale), the others 127/max (the quantiser's factor), which the first lane takes from
+// the second.  The reference's clamp to +-127 is never active: |x| <= max, so |x * RN(127/max)|
+// <= 127 (1 + 2^-24), which rounds to at most 127.
+__device__ __forceinline__ void put_q8(int c, const float4& v, unsigned char* xq, float* xd, float* xss) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 4));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    const bool first = (c & 7) == 0;
+    const float quo = first ? m / 127.0f : 127.0f / m;
+    const float fac = __shfl_xor(quo, 1);
+    const float inv = m > 0.0f ? (first ? fac : quo) : 0.0f;
+    auto qb = [&](float a) { return (unsigned)((int)__builtin_rintf(a * inv) & 0xFF); };
+    reinterpret_cast<unsigned*>(xq)[c] = qb(v.x) | (qb(v.y) << 8) | (qb(v.z) << 16) | (qb(v.w) << 24);
+    float s = (v.x + v.y) + (v.z + v.w);
+    s = s + __shfl_xor(s, 4);
+    s = s + __shfl_xor(s, 2);
+    s = s + __shfl_xor(s, 1);
+    if (first) {
+        xd[c >> 3] = quo;
+        xss[c >> 3] = s;
+    }
+}
+
+__device__ __forceinline__ int dot4_i8(unsigned a, unsigned b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Q4_K on a Q8_1 input (matmul_q4_k_dp4a.cu's arithmetic).  Unit u: nibble bytes 8u .. 8u+7
+// = super-block sb = u/16, group g = (u%16)/4, l = 8(u%4) .. +7: elements 64g + l (sub-block
+// 2g, low nibbles) and 64g + 32 + l (sub-block 2g + 1).  Per sub-block s the reference adds
+// ((d*sc_s)*d_x)*dp - (dmin*m_s)*s_x; the lane at l = 0 adds the min term for its sub-blocks.
+struct FmtQ4_KQ8 {
+    static constexpr int UNIT = 16, MAXU = 8, TAB = 16;
+    static constexpr bool XSUM = false, Q8IN = true;
+    using Row = FmtQ4_K::Row;
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        return FmtQ4_K::head(w, row, j, units >> 4);
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        FmtQ4_K::build_tab_ns(r, tab, j, units >> 4);
+    }
+    struct Raw { uint2 q; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<uint2>(rp(w, 0, row), (unsigned)u * 8u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const int g = (j >> 2) & 3, sb = (ub >> 4) + (j >> 4);
+        const int i0 = sb * 256 + 64 * g + 8 * (j & 3);
+        const uint2 xa = *reinterpret_cast<const uint2*>(st.xq + i0);
+        const uint2 xb = *reinterpret_cast<const uint2*>(st.xq + i0 + 32);
+        const int dp0 = dot4_i8(r.q.y & 0x0F0F0F0Fu, xa.y, dot4_i8(r.q.x & 0x0F0F0F0Fu, xa.x, 0));
+        const int dp1 = dot4_i8((r.q.y >> 4) & 0x0F0F0F0Fu, xb.y,
+                                dot4_i8((r.q.x >> 4) & 0x0F0F0F0Fu, xb.x, 0));
+        const float4 f = x4(st.tab, sb * TAB + 4 * g);   // (d*sc, dmin*m) of sub-blocks 2g, 2g+1
+        const int b0 = sb * 8 + 2 * g;
+        const float2 dx = *reinterpret_cast<const float2*>(st.xd + b0);
+        const float2 sx = *reinterpret_cast<const float2*>(st.xss + b0);
+        const float v = (f.x * dx.x) * (float)dp0 + (f.z * dx.y) * (float)dp1;
+        const float mt = (f.y * sx.x) + (f.w * sx.y);
+        return (j & 3) == 0 ? v - mt : v;
+    }
+};
+
+// Q8_0 on a Q8_1 input (matmul_q8_0_dp4a.cu's arithmetic: per block (d*d_x)*dp).  Unit u:
+// quants 8u .. 8u+7 of block u/4.
+struct FmtQ8_0Q8 {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false, Q8IN = true;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    struct Raw { uint2 q; unsigned short d; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<uint2>(rp(w, 0, row), (unsigned)u * 8u),
+                   ldo<unsigned short>(rp(w, 1, row), ((unsigned)u >> 2) * 2u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const int i = 8 * ub + 8 * j;
+        const uint2 xa = *reinterpret_cast<const uint2*>(st.xq + i);
+        const int dp = dot4_i8(r.q.y, xa.y, dot4_i8(r.q.x, xa.x, 0));
+        return (h2f(r.d) * st.xd[i >> 5]) * (float)dp;
+    }
+};
+
 // ---- the kernel ------------------------------------------------------------------------------
 // One row per wave: kGemvThreads/64 rows per workgroup, row b*(kGemvThreads/64) + w for wave w
 // of workgroup b, so the row, its segment and the unit count are wave-uniform (scalar
@@ -331,15 +437,23 @@ __host__ __device__ constexpr int gemv_cols_padded(int cols) {
 }
 template <class F1, class F2 = F1>
 struct GemvLds {
+    static constexpr bool F32X = !F1::Q8IN || !F2::Q8IN;   // some format reads the fp32 input
+    static constexpr bool Q8X = F1::Q8IN || F2::Q8IN;      // some format reads the Q8_1 input
     static constexpr bool XSUM = F1::XSUM || F2::XSUM;
     static constexpr int TAB = F1::TAB > F2::TAB ? F1::TAB : F2::TAB;
     static __host__ __device__ constexpr int cols_padded(int cols) {
         return gemv_cols_padded<F1>(cols) > gemv_cols_padded<F2>(cols) ? gemv_cols_padded<F1>(cols)
                                                                         : gemv_cols_padded<F2>(cols);
     }
+    // float offsets of the regions: xs | xsum | xq (bytes) | xd | xss | tables
+    static __host__ __device__ constexpr int off_xsum(int cp) { return F32X ? cp : 0; }
+    static __host__ __device__ constexpr int off_xq(int cp) { return off_xsum(cp) + (XSUM ? cp / 4 : 0); }
+    static __host__ __device__ constexpr int off_xd(int cp) { return off_xq(cp) + (Q8X ? cp / 4 : 0); }
+    static __host__ __device__ constexpr int off_xss(int cp) { return off_xd(cp) + (Q8X ? cp / 32 : 0); }
+    static __host__ __device__ constexpr int off_tab(int cp) { return off_xss(cp) + (Q8X ? cp / 32 : 0); }
     static __host__ __device__ constexpr size_t bytes(int cols) {
-        const size_t cp = (size_t)cols_padded(cols);
-        return sizeof(float) * (cp + (XSUM ? cp / 4 : 0) + (size_t)kGemvRowsPerGroup * (cp / 256) * TAB);
+        const int cp = cols_padded(cols);
+        return sizeof(float) * ((size_t)off_tab(cp) + (size_t)kGemvRowsPerGroup * (size_t)(cp / 256) * TAB);
     }
 };
 
@@ -369,7 +483,14 @@ __device__ __forceinline__ float4 scale4(const float4& v, float r, const float4&
 // Units whose LDS reads the dot loop lets the scheduler hoist together: four, two for Q6_K
 // (four LDS chunks per unit).
 template <class F>
-constexpr int dot_step() { return F::UNIT == 16 ? 2 : 4; }
+constexpr int dot_step() { return (F::UNIT == 16 && !F::Q8IN) ? 2 : 4; }
+// the largest divisor of NK not above dot_step
+template <class F, int NK>
+constexpr int dot_step_of() {
+    int s = dot_step<F>() < NK ? dot_step<F>() : NK;
+    while (NK % s) --s;
+    return s;
+}
 
 // One row's registers: the lane's share of the row's side data and NK rounds of units.
 template <class F, int NK>
@@ -394,7 +515,7 @@ __device__ __forceinline__ float row_dot(RowRegs<F, NK>& r, const Staged& st, co
     for (int base = 0;;) {
         // in steps of a few units, the step loop kept rolled: the scheduler would otherwise
         // hoist every unit's LDS reads to the top and run out of registers
-        constexpr int STEP = NK < dot_step<F>() ? NK : dot_step<F>();
+        constexpr int STEP = dot_step_of<F, NK>();
 #pragma unroll 1
         for (int h = 0; h < NK / STEP; ++h) {
 #pragma unroll
@@ -438,8 +559,11 @@ void gemv_kernel(GemvArgs a) {
     const int n4 = a.cols >> 2;
     const int cp = L::cols_padded(a.cols);
     float* xs = lds;
-    float* xsum = lds + cp;
-    float* tab = xsum + (L::XSUM ? cp / 4 : 0) + wave * (cp / 256) * L::TAB;
+    float* xsum = lds + L::off_xsum(cp);
+    unsigned char* xq = reinterpret_cast<unsigned char*>(lds + L::off_xq(cp));
+    float* xd = lds + L::off_xd(cp);
+    float* xss = lds + L::off_xss(cp);
+    float* tab = lds + L::off_tab(cp) + wave * (cp / 256) * L::TAB;
 
     // input chunks and norm weights (chunk c = tid + 256k, clamped to the last chunk)
     const bool norm = a.norm_w != nullptr;
@@ -490,9 +614,12 @@ void gemv_kernel(GemvArgs a) {
         r = 1.0f / (float)__builtin_sqrt((double)v);
     }
     float4* xs4 = reinterpret_cast<float4*>(xs);
-    auto put = [&](int c, const float4& v) {
-        xs4[c] = v;
-        if (L::XSUM) xsum[c] = (v.x + v.y) + (v.z + v.w);
+    auto put = [&](int c, const float4& v) {   // the 8 lanes of a Q8_1 block call together
+        if (L::F32X) {
+            xs4[c] = v;
+            if (L::XSUM) xsum[c] = (v.x + v.y) + (v.z + v.w);
+        }
+        if (L::Q8X) put_q8(c, v, xq, xd, xss);
     };
 #pragma unroll
     for (int k = 0; k < kStageChunks; ++k) {
@@ -505,7 +632,7 @@ void gemv_kernel(GemvArgs a) {
     else F2::build_tab(r2.rw, tab, j, units2);
     __syncthreads();
 
-    const Staged st{xs, xsum, tab};
+    const Staged st{xs, xsum, tab, xq, xd, xss};
     float acc = !second ? row_dot(r1, st, sg, row, j, units1) : row_dot(r2, st, sg, row, j, units2);
     acc = dk::row_group_sum<64>(acc);
     if (live && j == 0) store_row(a, sg, row_g, row, acc);

@@ -120,11 +120,13 @@ struct GemvArgs;
 int gemv_unit(int ggml_type);
 // y = W x over one to three row segments of one GGML type (optional fused pre-RMSNorm of x,
 // optional residual epilogue); hipErrorInvalidValue for an unsupported type or shape.
-hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, hipStream_t stream);
+// q8_input: Q4_K and Q8_0 rows take the Q8_1-quantised input and int8 dot products (the
+// reference GPU's default matvecs); other types are unaffected.
+hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipStream_t stream);
 // The same over segments of two types in one launch (GemvSeg::fmt 0: first_type, 1: second);
 // supported for first_type Q4_K with second_type Q6_K.
 bool gemv_pair_supported(int first_type, int second_type);
-hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_type,
+hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_type, bool q8_input,
                             hipStream_t stream);
 // x += rscale? * rmsnorm(xb, w) over dim values (one workgroup).
 hipError_t launch_post_norm_residual(const float* xb, const float* w, float eps, float rscale,

@@ -90,6 +90,7 @@ struct KvHandle {
     float* part_ml = nullptr;
     int blk_dim = 0;                 // llmp_block_config: embedding length
     float blk_rscale = 0.0f;         // Granite residual scale, 0 = off
+    int blk_input = LLMP_INPUT_F32;  // llmp_block_input_mode
     float* blk_buf = nullptr;        // block scratch: q|k|v, attention output, Wo output
     size_t blk_floats = 0;
     size_t part_slots = 0;    // (split, query head) slots the workspace holds
@@ -1031,6 +1032,15 @@ int llmp_block_config(uint64_t handle, int dim, float residual_scale) {
     return LLMP_OK;
 }
 
+int llmp_block_input_mode(uint64_t handle, int mode) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (mode != LLMP_INPUT_F32 && mode != LLMP_INPUT_Q8_1)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_block_input_mode: mode %d", mode);
+    kv->blk_input = mode;
+    return LLMP_OK;
+}
+
 int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int rows, int cols,
                       const void* data, uint64_t nbytes) {
     if (int rc = ensure_init()) return rc;
@@ -1125,6 +1135,7 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
     float* o = attn + qd;
     float* xp = reinterpret_cast<float*>(x);
     hipStream_t st = pick_stream(stream);
+    const bool q8in = kv->blk_input == LLMP_INPUT_Q8_1;
     auto vecp = [&](int slot) -> const float* {
         return static_cast<const float*>(W[slot].mem);
     };
@@ -1171,7 +1182,7 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
         g.norm_w = vecp(LLMP_W_ATTN_NORM);
         g.eps = c.eps;
         g.out = q;
-        LLMP_HIP_CHECK(launch_gemv_pair(g, t1, t2, st), "block Q/K/V projection launch");
+        LLMP_HIP_CHECK(launch_gemv_pair(g, t1, t2, q8in, st), "block Q/K/V projection launch");
     } else {
         for (int i = 0; i < 3;) {
             int n = 1;
@@ -1189,7 +1200,7 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
             g.norm_w = vecp(LLMP_W_ATTN_NORM);
             g.eps = c.eps;
             g.out = q + segs[i].out_off;
-            LLMP_HIP_CHECK(launch_gemv(g, types[i], st), "block Q/K/V projection launch");
+            LLMP_HIP_CHECK(launch_gemv(g, types[i], q8in, st), "block Q/K/V projection launch");
             i += n;
         }
     }
@@ -1212,13 +1223,13 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
     const float* post = vecp(LLMP_W_POST_ATTN_NORM);
     if (post) {
         g.out = o;
-        LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, st), "block output projection launch");
+        LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, q8in, st), "block output projection launch");
         LLMP_HIP_CHECK(launch_post_norm_residual(o, post, c.eps, kv->blk_rscale, xp, dim, st),
                        "block post-norm launch");
     } else {
         g.resid = xp;
         g.rscale = kv->blk_rscale;
-        LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, st), "block output projection launch");
+        LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, q8in, st), "block output projection launch");
     }
     return LLMP_OK;
 }

@@ -414,9 +414,14 @@ class HipForwardPass:
              self.gpuV.ptr, self.gpuXb2.ptr, splits, stream)
 
     # -- the attention half of the layer (projections + residual) --------------------------
-    def setBlockConfig(self, dim: int, residual_scale: float = 0.0) -> None:
-        """embeddingLength and Granite's residualScale (0 = off) for forwardAttentionBlock."""
+    def setBlockConfig(self, dim: int, residual_scale: float = 0.0,
+                       input_mode: int = _lib.LLMP_INPUT_F32) -> None:
+        """embeddingLength and Granite's residualScale (0 = off) for forwardAttentionBlock.
+        input_mode LLMP_INPUT_Q8_1: Q4_K / Q8_0 projections on a Q8_1 copy of the input with
+        int8 dot products (CudaForwardPass's default dp4a matvecs, CudaForwardPass.java:783-790);
+        LLMP_INPUT_F32: the CPU engine's fp32 arithmetic."""
         call("llmp_block_config", self.kv.handle, dim, float(residual_scale))
+        call("llmp_block_input_mode", self.kv.handle, int(input_mode))
         self.dim = dim
         if getattr(self, "gpuX", None) is None or self.gpuX.nbytes < dim * 4:
             self.gpuX = DeviceBuffer(dim * 4)

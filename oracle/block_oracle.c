@@ -227,6 +227,149 @@ void orc_rmsnorm(float *out, const float *x, const float *w, int size, float eps
     for (int i = 0; i < size; i++) out[i] = x[i] * ss * w[i];
 }
 
+/* ---- the reference GPU's Q8_1 input (its default "dp4a" matvecs) ----------------------------
+ * CudaForwardPass (CudaForwardPass.java:783-790: cuda.dp4a defaults to true; :1998-2037: Q4_K
+ * and Q8_0 take the int8 kernels, Q6_K stays on the fp32 one) normalises x, quantises it to
+ * Q8_1 blocks (rmsnorm_quantize.cu, quantize_q8.cu) and runs matmul_q4_k_dp4a.cu /
+ * matmul_q8_0_dp4a.cu: exact int8 dot products per 32 values, scaled in float.  The
+ * restatement fixes two reduction orders the reference leaves to its launch geometry (and to
+ * CUDA's rsqrtf): the norm's sum of squares and each block's sum, both in the library's
+ * staging order, so that the quantised bytes are the GPU's exactly. */
+
+/* The library's staged RMSNorm: 256 threads, thread t sums the squares of the 4-value chunks
+ * c = t, t+256, ... with FMAs (values in order); each 64-thread wave reduces by a butterfly
+ * (xor 32, 16, 8, 4, 2, 1); the four wave totals are added in order; r = 1/(float)sqrt((double)
+ * (ss/size + eps)); out = (x*r)*w (size a multiple of 4). */
+void orc_rmsnorm_staged(float *out, const float *x, const float *w, int size, float eps)
+{
+    float part[256], red[4];
+    const int n4 = size / 4;
+    for (int t = 0; t < 256; t++) {
+        float s = 0.0f;
+        for (int c = t; c < n4; c += 256)
+            for (int e = 0; e < 4; e++) s = fmaf(x[4 * c + e], x[4 * c + e], s);
+        part[t] = s;
+    }
+    for (int wv = 0; wv < 4; wv++) {
+        float v[64], nv[64];
+        memcpy(v, part + 64 * wv, sizeof(v));
+        for (int off = 32; off > 0; off >>= 1) {
+            for (int i = 0; i < 64; i++) nv[i] = v[i] + v[i ^ off];
+            memcpy(v, nv, sizeof(v));
+        }
+        red[wv] = v[0];
+    }
+    float tot = red[0];
+    for (int wv = 1; wv < 4; wv++) tot = tot + red[wv];
+    float v = tot / (float)size;
+    v = v + eps;
+    const float r = 1.0f / (float)sqrt((double)v);
+    for (int i = 0; i < size; i++) out[i] = (x[i] * r) * w[i];
+}
+
+/* Q8_1 blocks of 32 values (quantize_q8.cu, rmsnorm_quantize.cu): d = max|x|/127, quants
+ * rint(x * (127/max|x|)) clamped to +-127 (all 0 when max|x| = 0), s = the block's sum, here
+ * ((x0 + x1) + (x2 + x3)) per 4 values, then a butterfly over the block's 8 groups (xor 4, 2,
+ * 1).  n a multiple of 32. */
+void orc_quantize_q8_1(const float *x, int n, int8_t *q, float *d, float *s)
+{
+    for (int b = 0; b < n / 32; b++) {
+        const float *xb = x + 32 * b;
+        float m = 0.0f;
+        for (int i = 0; i < 32; i++) m = fmaxf(m, fabsf(xb[i]));
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        for (int i = 0; i < 32; i++) {
+            float r = rintf(xb[i] * inv);
+            r = r > 127.0f ? 127.0f : (r < -127.0f ? -127.0f : r);
+            q[32 * b + i] = (int8_t)r;
+        }
+        d[b] = m / 127.0f;
+        float g[8], ng[8];
+        for (int t = 0; t < 8; t++) g[t] = (xb[4 * t] + xb[4 * t + 1]) + (xb[4 * t + 2] + xb[4 * t + 3]);
+        for (int off = 4; off > 0; off >>= 1) {
+            for (int t = 0; t < 8; t++) ng[t] = g[t] + g[t ^ off];
+            memcpy(g, ng, sizeof(g));
+        }
+        s[b] = g[0];
+    }
+}
+
+/* get_scale_min_k4 of the Q4_K head's 12 scale bytes (q = head + 4): sub-block j's 6-bit
+ * scale and min. */
+static void q4k_scale_min(const uint8_t *q, int j, int *sc, int *m)
+{
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* The int8 matvecs on a Q8_1 input (q [cols], d and s [cols/32]); out[row] += the row's dot:
+ *   Q4_K (matmul_q4_k_dp4a.cu): per sub-block j of 32, ((d*sc_j)*d_x)*dp_j - (dmin*m_j)*s_x
+ *   Q8_0 (matmul_q8_0_dp4a.cu): per block, (d*d_x)*dp
+ * with dp the exact integer dot of the block's weights with the input's quants, added over
+ * the row's blocks in order (the reference adds per lane, then a warp tree).  -1 for other
+ * types. */
+int orc_matmul_q8_1(int type, const uint8_t *w, int rows, int cols, const int8_t *q,
+                    const float *d, const float *s, float *out)
+{
+    if (type == ORC_GGML_Q4_K) {
+        if (cols % 256) return -1;
+        const int ns = cols / 256;
+        for (int r = 0; r < rows; r++) {
+            float acc = 0.0f;
+            for (int b = 0; b < ns; b++) {
+                const uint8_t *blk = w + ((size_t)r * ns + b) * 144;
+                const float dd = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+                const float dmin = orc_f16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+                for (int g = 0; g < 4; g++)
+                    for (int h = 0; h < 2; h++) {   /* sub-block 2g + h: nibble h of bytes 32g .. 32g+31 */
+                        const int j = 2 * g + h, xb = b * 8 + j;
+                        int dp = 0;
+                        for (int l = 0; l < 32; l++) {
+                            const int nib = (blk[16 + 32 * g + l] >> (4 * h)) & 15;
+                            dp += nib * q[32 * xb + l];
+                        }
+                        int sc, mn;
+                        q4k_scale_min(blk + 4, j, &sc, &mn);
+                        acc += ((dd * (float)sc) * d[xb]) * (float)dp - (dmin * (float)mn) * s[xb];
+                    }
+            }
+            out[r] += acc;
+        }
+        return 0;
+    }
+    if (type == ORC_GGML_Q8_0) {
+        if (cols % 32) return -1;
+        const int nb = cols / 32;
+        for (int r = 0; r < rows; r++) {
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *blk = w + ((size_t)r * nb + b) * 34;
+                const float dd = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+                int dp = 0;
+                for (int l = 0; l < 32; l++) dp += (int)(int8_t)blk[2 + l] * q[32 * b + l];
+                acc += (dd * d[b]) * (float)dp;
+            }
+            out[r] += acc;
+        }
+        return 0;
+    }
+    return -1;
+}
+
+/* One projection in the Q8_1 mode: the int8 matvec for Q4_K / Q8_0, else the fp32 one. */
+static int matmul_mode(int q8, int type, const uint8_t *w, int rows, int cols, const float *x,
+                       const int8_t *xq, const float *xd, const float *xs, float *out)
+{
+    if (q8 && (type == ORC_GGML_Q4_K || type == ORC_GGML_Q8_0))
+        return orc_matmul_q8_1(type, w, rows, cols, xq, xd, xs, out);
+    return orc_matmul(type, w, rows, cols, x, out);
+}
+
 typedef struct {
     int dim;                     /* embeddingLength */
     float residual_scale;        /* Granite residualScale, 0 = off */
@@ -237,15 +380,18 @@ typedef struct {
     const uint8_t *wo;           /* [dim][q_dim] */
     int wq_type, wk_type, wv_type, wqkv_type, wo_type;
     const float *q_bias, *k_bias, *v_bias, *o_bias;
+    int q8_1_input;              /* 1: the reference GPU's Q8_1-input matvecs (see above) */
 } orc_block_w;
 
 /* The attention half of one layer (TransformerBlock.forward up to the residual add, with
  * Attention.forward inside it) over an fp32 cache: x [dim] is updated in place,
  * x += residual_scale? * postnorm?(Wo . attention(Wq/k/v . rmsnorm(x))).  Layer semantics
- * (QK-norm, RoPE, window, append) are orc_forward_from_projections'. */
+ * (QK-norm, RoPE, window, append) are orc_forward_from_projections'.  attn_out (or NULL)
+ * receives the attention output [q_dim], the output projection's input. */
 int orc_attn_block(const orc_cfg *c, const orc_block_w *bw, float *kcache, float *vcache,
                    const float *qnorm_w, const float *knorm_w, const float *rope_cos,
-                   const float *rope_sin, float *x, int layer, int pos, int n_threads)
+                   const float *rope_sin, float *x, int layer, int pos, int n_threads,
+                   float *attn_out)
 {
     const int dim = bw->dim, qd = c->n_heads * c->head_size, kvd = c->n_kv_heads * c->head_size;
     float *xb = (float *)calloc((size_t)dim, sizeof(float));
@@ -253,25 +399,34 @@ int orc_attn_block(const orc_cfg *c, const orc_block_w *bw, float *kcache, float
     float *xb2 = (float *)calloc((size_t)qd, sizeof(float));
     float *att = (float *)calloc((size_t)c->n_heads * (size_t)(pos + 1), sizeof(float));
     float *q = qkv, *k = qkv + qd, *v = qkv + qd + kvd;
+    const int q8 = bw->q8_1_input, xn = dim > qd ? dim : qd;
+    int8_t *xq = (int8_t *)calloc((size_t)xn, 1);
+    float *xd = (float *)calloc((size_t)xn / 32 + 1, sizeof(float));
+    float *xs = (float *)calloc((size_t)xn / 32 + 1, sizeof(float));
     int rc = 0;
-    if (bw->attn_norm)
-        orc_rmsnorm(xb, x, bw->attn_norm, dim, c->norm_eps);
-    else
-        memcpy(xb, x, sizeof(float) * (size_t)dim);
-    if (bw->wqkv) {
-        rc |= orc_matmul(bw->wqkv_type, bw->wqkv, qd + 2 * kvd, dim, xb, qkv);
+    if (bw->attn_norm) {
+        if (q8) orc_rmsnorm_staged(xb, x, bw->attn_norm, dim, c->norm_eps);
+        else orc_rmsnorm(xb, x, bw->attn_norm, dim, c->norm_eps);
     } else {
-        rc |= orc_matmul(bw->wq_type, bw->wq, qd, dim, xb, q);
-        rc |= orc_matmul(bw->wk_type, bw->wk, kvd, dim, xb, k);
-        rc |= orc_matmul(bw->wv_type, bw->wv, kvd, dim, xb, v);
+        memcpy(xb, x, sizeof(float) * (size_t)dim);
+    }
+    if (q8) orc_quantize_q8_1(xb, dim, xq, xd, xs);
+    if (bw->wqkv) {
+        rc |= matmul_mode(q8, bw->wqkv_type, bw->wqkv, qd + 2 * kvd, dim, xb, xq, xd, xs, qkv);
+    } else {
+        rc |= matmul_mode(q8, bw->wq_type, bw->wq, qd, dim, xb, xq, xd, xs, q);
+        rc |= matmul_mode(q8, bw->wk_type, bw->wk, kvd, dim, xb, xq, xd, xs, k);
+        rc |= matmul_mode(q8, bw->wv_type, bw->wv, kvd, dim, xb, xq, xd, xs, v);
     }
     if (bw->q_bias) for (int i = 0; i < qd; i++) q[i] += bw->q_bias[i];
     if (bw->k_bias) for (int i = 0; i < kvd; i++) k[i] += bw->k_bias[i];
     if (bw->v_bias) for (int i = 0; i < kvd; i++) v[i] += bw->v_bias[i];
     orc_forward_from_projections(c, kcache, vcache, qnorm_w, knorm_w, rope_cos, rope_sin, q, k, v,
                                  layer, pos, xb2, att, 0, n_threads);
+    if (attn_out) memcpy(attn_out, xb2, sizeof(float) * (size_t)qd);
     memset(xb, 0, sizeof(float) * (size_t)dim);
-    rc |= orc_matmul(bw->wo_type, bw->wo, dim, qd, xb2, xb);
+    if (q8) orc_quantize_q8_1(xb2, qd, xq, xd, xs);   /* quantizeXb2: the attention output */
+    rc |= matmul_mode(q8, bw->wo_type, bw->wo, dim, qd, xb2, xq, xd, xs, xb);
     if (bw->o_bias) for (int i = 0; i < dim; i++) xb[i] += bw->o_bias[i];
     if (bw->post_attn_norm) orc_rmsnorm(xb, xb, bw->post_attn_norm, dim, c->norm_eps);
     if (bw->residual_scale > 0.0f)
@@ -281,5 +436,8 @@ int orc_attn_block(const orc_cfg *c, const orc_block_w *bw, float *kcache, float
     free(qkv);
     free(xb2);
     free(att);
+    free(xq);
+    free(xd);
+    free(xs);
     return rc;
 }

@@ -53,6 +53,7 @@ class _BlockW(C.Structure):
         ("wo_type", C.c_int),
         ("q_bias", C.POINTER(C.c_float)), ("k_bias", C.POINTER(C.c_float)),
         ("v_bias", C.POINTER(C.c_float)), ("o_bias", C.POINTER(C.c_float)),
+        ("q8_1_input", C.c_int),
     ]
 
 
@@ -149,9 +150,14 @@ def lib():
         L.orc_matmul.restype = C.c_int
         L.orc_matmul.argtypes = [C.c_int, _U8, C.c_int, C.c_int, _F, _F]
         L.orc_rmsnorm.argtypes = [_F, _F, _F, C.c_int, C.c_float]
+        L.orc_rmsnorm_staged.argtypes = [_F, _F, _F, C.c_int, C.c_float]
+        L.orc_quantize_q8_1.argtypes = [_F, C.c_int, C.POINTER(C.c_int8), _F, _F]
+        L.orc_matmul_q8_1.restype = C.c_int
+        L.orc_matmul_q8_1.argtypes = [C.c_int, _U8, C.c_int, C.c_int, C.POINTER(C.c_int8), _F, _F,
+                                      _F]
         L.orc_attn_block.restype = C.c_int
         L.orc_attn_block.argtypes = [C.POINTER(_Cfg), C.POINTER(_BlockW), _F, _F, _F, _F, _F,
-                                     _F, _F, C.c_int, C.c_int, C.c_int]
+                                     _F, _F, C.c_int, C.c_int, C.c_int, _F]
         _lib = L
     return _lib
 
@@ -472,6 +478,38 @@ def rmsnorm(x, w, eps) -> np.ndarray:
     return out
 
 
+def rmsnorm_staged(x, w, eps) -> np.ndarray:
+    """The library's staged RMSNorm (the reduction order the Q8_1 mode quantises after)."""
+    x = f32(x)
+    out = np.zeros_like(x)
+    lib().orc_rmsnorm_staged(_p(out), _p(x), _p(f32(w)), x.size, float(eps))
+    return out
+
+
+def quantize_q8_1(x):
+    """Q8_1 blocks of 32 (quantize_q8.cu): (int8 quants [n], scales [n/32], sums [n/32])."""
+    x = f32(x)
+    assert x.size % 32 == 0
+    q = np.zeros(x.size, np.int8)
+    d = np.zeros(x.size // 32, np.float32)
+    s = np.zeros(x.size // 32, np.float32)
+    lib().orc_quantize_q8_1(_p(x), x.size, q.ctypes.data_as(C.POINTER(C.c_int8)), _p(d), _p(s))
+    return q, d, s
+
+
+def matmul_q8_1(t: int, w: np.ndarray, rows: int, cols: int, q, d, s, out=None) -> np.ndarray:
+    """The reference GPU's int8 matvec (matmul_q4_k_dp4a.cu / matmul_q8_0_dp4a.cu) on a Q8_1
+    input: out[row] += dot."""
+    w = np.ascontiguousarray(w, np.uint8).reshape(-1)
+    q = np.ascontiguousarray(q, np.int8)
+    out = np.zeros(rows, np.float32) if out is None else f32(out).copy()
+    assert w.size >= rows * ggml_row_bytes(t, cols) and q.size >= cols
+    rc = lib().orc_matmul_q8_1(int(t), _u8p(w), rows, cols, q.ctypes.data_as(C.POINTER(C.c_int8)),
+                               _p(f32(d)), _p(f32(s)), _p(out))
+    assert rc == 0, "no int8 matvec for this type"
+    return out
+
+
 @dataclass
 class BlockWeights:
     """Projection weights of one layer's attention half: raw GGUF bytes (uint8) with their
@@ -494,6 +532,7 @@ class BlockWeights:
     v_bias: Optional[np.ndarray] = None
     o_bias: Optional[np.ndarray] = None
     residual_scale: float = 0.0
+    q8_1_input: bool = False     # the reference GPU's Q8_1-input matvecs for Q4_K / Q8_0
 
     def c(self):
         keep = []
@@ -515,29 +554,32 @@ class BlockWeights:
                     fp(self.post_attn_norm), up(self.wq), up(self.wk), up(self.wv),
                     up(self.wqkv), up(self.wo), self.wq_type, self.wk_type, self.wv_type,
                     self.wqkv_type, self.wo_type, fp(self.q_bias), fp(self.k_bias),
-                    fp(self.v_bias), fp(self.o_bias))
+                    fp(self.v_bias), fp(self.o_bias), int(bool(self.q8_1_input)))
         return s, keep
 
 
 def attn_block(cfg: OracleConfig, bw: BlockWeights, kcache, vcache, x, layer, pos,
-               qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1):
+               qnorm_w=None, knorm_w=None, rope_cos=None, rope_sin=None, n_threads=1,
+               return_attn=False):
     """The attention half of TransformerBlock.forward (pre-norm, projections, attention core,
     Wo, post-norm, residual scale, residual add) over fp32 caches [max_seq, kvDim] (row `pos`
-    appended).  Returns the updated residual x [dim]."""
+    appended).  Returns the updated residual x [dim], and with return_attn also the attention
+    output [q_dim] (the output projection's input)."""
     c = cfg.c()
     s, keep = bw.c()
     x = f32(x).copy()
     assert x.size == bw.dim
+    attn = np.zeros(cfg.n_heads * cfg.head_size, np.float32)
     rc = lib().orc_attn_block(
         C.byref(c), C.byref(s), _p(kcache), _p(vcache),
         _p(f32(qnorm_w)) if qnorm_w is not None else None,
         _p(f32(knorm_w)) if knorm_w is not None else None,
         _p(f32(rope_cos)) if rope_cos is not None else None,
         _p(f32(rope_sin)) if rope_sin is not None else None,
-        _p(x), layer, pos, int(n_threads))
+        _p(x), layer, pos, int(n_threads), _p(attn))
     assert rc == 0, "unsupported weight type or shape"
     del keep
-    return x
+    return (x, attn) if return_attn else x
 
 
 def max_threads() -> int:

@@ -55,7 +55,7 @@ def test_constants_match_header():
                  "LLMP_GGML_Q4_0", "LLMP_GGML_Q8_0", "LLMP_GGML_Q4_K", "LLMP_GGML_Q6_K",
                  "LLMP_GGML_BF16", "LLMP_W_ATTN_NORM", "LLMP_W_Q", "LLMP_W_K", "LLMP_W_V",
                  "LLMP_W_QKV", "LLMP_W_O", "LLMP_W_Q_BIAS", "LLMP_W_K_BIAS", "LLMP_W_V_BIAS",
-                 "LLMP_W_O_BIAS", "LLMP_W_POST_ATTN_NORM"):
+                 "LLMP_W_O_BIAS", "LLMP_W_POST_ATTN_NORM", "LLMP_INPUT_F32", "LLMP_INPUT_Q8_1"):
         assert getattr(_lib, name) == defs[name], name
 
 

@@ -58,10 +58,11 @@ def _weights(c, dim, types, rng, merged=False, bias=False, post=False, pre=True)
 
 
 def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=False, post=False,
-         pre=True, rscale=0.0, qk=None, splits=0, devpos=False):
+         pre=True, rscale=0.0, qk=None, splits=0, devpos=False, q8=False):
     rng = np.random.default_rng(seed)
     lw, bw = _weights(c, dim, types, rng, merged, bias, post, pre)
     bw.residual_scale = rscale
+    bw.q8_1_input = q8
     kv = c.kv_dim
     kc = np.zeros((max_seq, kv), F32)
     vc = np.zeros((max_seq, kv), F32)
@@ -73,7 +74,7 @@ def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=Fal
     qw, kw = qk if qk is not None else (None, None)
     with hfp.HipForwardPass(c, max_seq, qk_norm=qk_list) as fp:
         fp.kv.write(0, 0, kc, vc)
-        fp.setBlockConfig(dim, rscale)
+        fp.setBlockConfig(dim, rscale, _lib.LLMP_INPUT_Q8_1 if q8 else _lib.LLMP_INPUT_F32)
         fp.uploadLayerWeights(0, lw)
         worst = 0.0
         for s in range(steps):
@@ -85,16 +86,46 @@ def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=Fal
                 fp.updateTokenParams(pos)
             fp.forwardAttentionBlock(0, pos, splits, device_position=devpos)
             got = fp.downloadX()
-            want = orc.attn_block(oc, bw, kc, vc, x, 0, pos, qnorm_w=qw, knorm_w=kw, rope_cos=cs,
-                                  rope_sin=sn, n_threads=16)
-            worst = max(worst, dc.compare_out(got, want, f"block {what} pos {pos}"))
+            want, attn = orc.attn_block(oc, bw, kc, vc, x, 0, pos, qnorm_w=qw, knorm_w=kw,
+                                        rope_cos=cs, rope_sin=sn, n_threads=16, return_attn=True)
             gk, gv = fp.kv.read(0, 0, pos + 1)
             assert np.array_equal(gk[:pos], kc[:pos]) and np.array_equal(gv[:pos], vc[:pos])
             dc.compare_out(gk[pos], kc[pos], f"block {what} appended K row")
             dc.compare_out(gv[pos], vc[pos], f"block {what} appended V row")
+            if q8 and bw.wo_type in (gp.GGML_Q4_K, gp.GGML_Q8_0):
+                worst = max(worst, _compare_q8_output(got, want, attn, bw, rscale,
+                                                      f"block {what} pos {pos}"))
+            else:
+                worst = max(worst, dc.compare_out(got, want, f"block {what} pos {pos}"))
             # continue from the device's rows so later steps attend to the same cache
             kc[pos], vc[pos] = gk[pos], gv[pos]
         dc.log(f"[gpu] block {what}: ok, max abs err {worst:.2e}")
+
+
+def _compare_q8_output(got, want, attn, bw, rscale, what):
+    """The residual after a Q8_1-mode block.  The attention output is computed in two orders
+    (GPU, oracle), so an element within rounding of a quantisation tie may take the other
+    int8 value ahead of the output projection; each such element j may move output i by
+    |Wo[i, j]| * d_j (its block's scale).  The bar is the usual one plus that allowance for the
+    oracle's near-tie elements (|frac(|x|*127/max) - 1/2| < 2e-3), and nothing more."""
+    qd = attn.size
+    a = attn.astype(np.float32).reshape(-1, 32)
+    m = np.abs(a).max(axis=1)
+    inv = np.where(m > 0, np.float32(127) / np.where(m > 0, m, 1), 0).astype(np.float32)
+    t = np.abs(a * inv[:, None])
+    near = (np.abs(t - np.floor(t) - 0.5) < 2e-3).reshape(-1)
+    d = np.repeat(m / np.float32(127), 32)
+    wo = orc.dequant_rows(bw.wo_type, bw.wo, bw.dim, qd).astype(np.float64)
+    allow = np.abs(wo[:, near]) @ d[near].astype(np.float64) if near.any() else np.zeros(bw.dim)
+    if rscale > 0:
+        allow = allow * rscale
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bound = dc.ATOL + dc.RTOL * np.abs(want.astype(np.float64)) + 1.01 * allow
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert (err <= bound).all(), (f"{what}: {int((err > bound).sum())} elements above the bar "
+                                  f"(max abs err {err.max():.3e}, {int(near.sum())} near-tie inputs)")
+    dc.log(f"[gpu] {what}: max abs err {err.max():.2e}, {int(near.sum())} near-tie inputs of Wo")
+    return float(err.max())
 
 
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
@@ -159,12 +190,50 @@ def test_block_split_settings_agree():
              what=f"C3 q8_0 splits={splits}", splits=splits)
 
 
+# ---- the Q8_1 input mode (the reference GPU's int8 matvecs for Q4_K and Q8_0) ----------------
+# The oracle quantises the same staged-norm floats, so the int8 operands are the GPU's; the
+# outputs differ by float summation order, and by a rare quantisation tie of the attention
+# output (computed in two orders) ahead of the output projection.
+
+@pytest.mark.parametrize("t", [gp.GGML_Q4_K, gp.GGML_Q8_0, gp.GGML_Q6_K, gp.GGML_F16],
+                         ids=["q4_k", "q8_0", "q6_k-fp32", "f16-fp32"])
+def test_block_q8_1_input_formats(t):
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    _run(c, 1024, 64, 40, 2, (t, t, t, t), seed=800 + t, what=f"q8_1 {NAMES[t]}", q8=True)
+
+
+def test_block_q8_1_c3_llama3b_q4_k_m_mix():
+    """The C3 shape with the Q4_K_M mix: Q4_K rows on the Q8_1 input and Q6_K rows on the
+    fp32 input in one launch, Wo on the quantised attention output."""
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    _run(c, 3072, 2048, 2000, 4, (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K),
+         seed=810, what="q8_1 C3 Q4_K_M", q8=True)
+
+
+@pytest.mark.parametrize("dim", [2048, 4096, 8192])
+def test_block_q8_1_widths(dim):
+    """2, 4 and 8 unit rounds of the Q8_1 Q4_K side (the pair caps it at 4: a second batch at
+    8192), Q8_0 rows at 4, 8 and 16 rounds (two batches)."""
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    _run(c, dim, 64, 30, 1, (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K),
+         seed=820 + dim // 1024, what=f"q8_1 Q4_K_M dim {dim}", q8=True)
+    _run(c, dim, 64, 30, 1, (gp.GGML_Q8_0,) * 4, seed=830 + dim // 1024,
+         what=f"q8_1 Q8_0 dim {dim}", q8=True)
+
+
+def test_block_q8_1_merged_qkv_bias_granite_scale():
+    c = hfp.ModelConfig(12, 4, 128, 1, rope_freq_base=1e6, norm_eps=1e-6)
+    _run(c, 3072, 64, 20, 2, (gp.GGML_Q8_0,) * 4, seed=840, what="q8_1 merged Q8_0",
+         merged=True, bias=True, rscale=0.3, q8=True)
+
+
 def test_block_error_codes():
     c = hfp.ModelConfig(8, 2, 64, 1, rope_freq_base=1e4)
     with hfp.HipForwardPass(c, 32) as fp:
         h = fp.kv.handle
         assert _lib.status("llmp_layer_weight", h, 0, 1, 0, 512, 512, None, 0) == 1  # no block config
         assert _lib.status("llmp_block_config", h, 500, 0.0) == 1                     # not a multiple of 32
+        assert _lib.status("llmp_block_input_mode", h, 2) == 1                        # unknown mode
         fp.setBlockConfig(512)
         x = fp.gpuX.ptr
         assert _lib.status("llmp_attn_block", h, 0, 3, 0, x, 0, 0) == 1               # no weights yet

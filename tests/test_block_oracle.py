@@ -195,3 +195,108 @@ def test_attn_block_merged_qkv_equals_separate_projections():
         a = orc.attn_block(cfg, bw, kc, vc, x, 0, pos, rope_cos=cs, rope_sin=sn)
         b = orc.attn_block(cfg2, bw2, kc2, vc2, x, 0, pos, rope_cos=cs, rope_sin=sn)
         assert np.array_equal(a, b) and np.array_equal(kc, kc2)
+
+
+# ---- the reference GPU's Q8_1-input matvecs ---------------------------------------------------
+
+def test_q8_1_quantiser_closed_forms():
+    """d = max|x|/127, quants rint(x*127/max) with ties to even and +-127 at the extremes, a
+    zero block all zero, the block sum exact on small integers."""
+    x = np.zeros(96, F32)
+    x[:32] = np.arange(-16, 16, dtype=F32)            # max 16: quants rint(x*127/16)
+    x[32:64] = 0.0                                     # zero block
+    x[64:96] = np.array([127, 2.5, 3.5, -2.5, -127] + [0.5] * 27, F32)   # max 127: inv = 1
+    q, d, s = orc.quantize_q8_1(x)
+    assert d[0] == F32(16) / F32(127) and d[1] == 0 and d[2] == 1
+    want0 = np.clip(np.rint(x[:32] * (F32(127) / F32(16))), -127, 127)
+    assert np.array_equal(q[:32], want0.astype(np.int8)) and q[0] == -127
+    assert not q[32:64].any() and s[1] == 0
+    assert list(q[64:69]) == [127, 2, 4, -2, -127] and (q[69:] == 0).all()   # 0.5 -> 0 (even)
+    assert s[0] == -16 and s[2] == F32(127 + 2.5 + 3.5 - 2.5 - 127 + 27 * 0.5)
+
+
+def test_q8_1_quantiser_against_numpy_and_its_error_bound():
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal(4096) * rng.uniform(0.1, 10, 4096)).astype(F32)
+    q, d, s = orc.quantize_q8_1(x)
+    xb = x.reshape(-1, 32)
+    m = np.abs(xb).max(axis=1)
+    assert np.array_equal(d, (m / F32(127)).astype(F32))
+    want = np.clip(np.rint(xb * (F32(127) / m)[:, None]), -127, 127).astype(np.int8).reshape(-1)
+    assert np.array_equal(q, want)
+    # reconstruction within half a step; sums within float32 rounding of the float64 sum
+    assert (np.abs(q.reshape(-1, 32) * d[:, None] - xb) <= 0.5 * d[:, None] * (1 + 1e-6)).all()
+    np.testing.assert_allclose(s, xb.astype(np.float64).sum(axis=1), rtol=1e-5, atol=1e-4)
+
+
+def test_staged_rmsnorm_matches_float64_and_the_plain_one():
+    rng = np.random.default_rng(42)
+    for n in (256, 3072, 8192):
+        x = (rng.standard_normal(n) * 2).astype(F32)
+        w = rng.uniform(0.5, 1.5, n).astype(F32)
+        got = orc.rmsnorm_staged(x, w, 1e-5)
+        x64 = x.astype(np.float64)
+        want = x64 / np.sqrt((x64 ** 2).mean() + 1e-5) * w
+        np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-7)
+        np.testing.assert_allclose(got, orc.rmsnorm(x, w, 1e-5), rtol=1e-6, atol=1e-7)
+    c = np.full(512, 3.0, F32)   # a constant vector: exact sums, r = 1/sqrt(9 + eps)
+    got = orc.rmsnorm_staged(c, np.ones(512, F32), 0.0)
+    assert np.array_equal(got, c * F32(1.0 / np.sqrt(9.0)))
+
+
+@pytest.mark.parametrize("t", [gp.GGML_Q8_0, gp.GGML_Q4_K], ids=["q8_0", "q4_k"])
+def test_q8_1_matmul_equals_the_float_matmul_on_an_exactly_quantised_input(t):
+    """On an input that Q8_1 represents exactly (x = d*q, with the block sum exact), the int8
+    matvec is the float matvec of the dequantised weights: the Q4_K min term enters through
+    the block sum, the scales through d."""
+    rng = np.random.default_rng(43 + t)
+    rows, cols = 24, 1024
+    wb, vals = gp.random_weights(t, rows, cols, rng)
+    qx = rng.integers(-127, 128, cols).astype(np.int8)
+    qx[::32] = 127                                    # each block's max is 127: d exact
+    d = (2.0 ** rng.integers(-6, 2, cols // 32)).astype(F32)
+    x = (qx.reshape(-1, 32) * d[:, None]).astype(F32).reshape(-1)
+    q, dd, s = orc.quantize_q8_1(x)
+    assert np.array_equal(q, qx) and np.array_equal(dd, d)   # powers of two: exact
+    got = orc.matmul_q8_1(t, wb, rows, cols, q, dd, s)
+    want = vals.astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-4 * np.abs(want).max())
+
+
+def test_q8_1_matmul_integer_closed_form_and_min_term():
+    """Q8_0: a row of all-ones quants with d = 1 gives (d_x)*(sum of the input's quants) per
+    block.  Q4_K: the min term is -(dmin*m)*s per sub-block, linear in the block sums."""
+    cols = 64
+    wb, _ = gp.pack_q8_0(gp._f16_bits(np.ones((1, 2))), np.ones((1, cols), np.int8))
+    q = np.arange(-32, 32).astype(np.int8)
+    d = np.array([0.5, 2.0], F32)
+    got = orc.matmul_q8_1(gp.GGML_Q8_0, wb, 1, cols, q, d, np.zeros(2, F32))
+    assert got[0] == F32(0.5 * q[:32].astype(int).sum() + 2.0 * q[32:].astype(int).sum())
+    rng = np.random.default_rng(44)
+    wb, _ = gp.random_weights(gp.GGML_Q4_K, 3, 256, rng)
+    q = rng.integers(-127, 128, 256).astype(np.int8)
+    d = np.full(8, 0.01, F32)
+    a = orc.matmul_q8_1(gp.GGML_Q4_K, wb, 3, 256, q, d, np.zeros(8, F32))
+    e = np.zeros(8, F32)
+    e[3] = 1.0
+    b = orc.matmul_q8_1(gp.GGML_Q4_K, wb, 3, 256, q, d, e)
+    dmin = np.array([gp._f16_val(wb[r, 2:4].view(np.uint16))[0] for r in range(3)], np.float64)
+    head = wb[:, 4:16]
+    m3 = head[:, 7] & 63                               # sub-block 3's min: byte 3 + 4 of the scales
+    np.testing.assert_allclose(a.astype(np.float64) - b, dmin * m3, rtol=1e-6, atol=1e-9)
+
+
+def test_attn_block_q8_1_mode_routes_only_q4_k_and_q8_0():
+    """Non-dp4a types (F16, Q6_K) take the fp32 path in the Q8_1 mode: the block then differs
+    from the fp32 mode only by the norm's summation order.  Q4_K / Q8_0 blocks move by the
+    input quantisation, within its bound."""
+    for t, tol in ((gp.GGML_F16, 2e-5), (gp.GGML_Q6_K, 2e-5), (gp.GGML_Q4_K, 3e-2), (gp.GGML_Q8_0, 3e-2)):
+        cfg, bw, _, kc, vc, x, pos, cs, sn = _block_setup(150 + t, t)
+        kc2, vc2 = kc.copy(), vc.copy()
+        a = orc.attn_block(cfg, bw, kc, vc, x, 0, pos, rope_cos=cs, rope_sin=sn)
+        bw.q8_1_input = True
+        b = orc.attn_block(cfg, bw, kc2, vc2, x, 0, pos, rope_cos=cs, rope_sin=sn)
+        err = np.abs(a - b).max() / np.abs(a - x).max()
+        assert err <= tol, (t, err)
+        if tol > 1e-3:
+            assert err > 1e-6, "the int8 path was not taken"
