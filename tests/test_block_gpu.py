@@ -58,7 +58,9 @@ def _weights(c, dim, types, rng, merged=False, bias=False, post=False, pre=True)
 
 
 def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=False, post=False,
-         pre=True, rscale=0.0, qk=None, splits=0, devpos=False, q8=False):
+         pre=True, rscale=0.0, qk=None, splits=0, devpos=False, q8=False, sinks=None, layer=0):
+    """`steps` block calls at positions pos0.. on layer `layer` of c (its window, RoPE table
+    and sinks), each checked against orc.attn_block."""
     rng = np.random.default_rng(seed)
     lw, bw = _weights(c, dim, types, rng, merged, bias, post, pre)
     bw.residual_scale = rscale
@@ -69,13 +71,14 @@ def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=Fal
     kc[:pos0] = rng.standard_normal((pos0, kv)).astype(F32)
     vc[:pos0] = rng.standard_normal((pos0, kv)).astype(F32)
     qk_list = [qk] * c.block_count if qk is not None else None
-    oc = dc.oracle_config(c, max_seq)
-    cs, sn = dc.oracle_tables(c, max_seq, 0)
+    oc = dc.oracle_config(c, max_seq, sinks)
+    cs, sn = dc.oracle_tables(c, max_seq, layer)
     qw, kw = qk if qk is not None else (None, None)
-    with hfp.HipForwardPass(c, max_seq, qk_norm=qk_list) as fp:
-        fp.kv.write(0, 0, kc, vc)
+    sink_list = [sinks] * c.block_count if sinks is not None else None
+    with hfp.HipForwardPass(c, max_seq, qk_norm=qk_list, sinks=sink_list) as fp:
+        fp.kv.write(layer, 0, kc, vc)
         fp.setBlockConfig(dim, rscale, _lib.LLMP_INPUT_Q8_1 if q8 else _lib.LLMP_INPUT_F32)
-        fp.uploadLayerWeights(0, lw)
+        fp.uploadLayerWeights(layer, lw)
         worst = 0.0
         for s in range(steps):
             pos = pos0 + s
@@ -84,11 +87,11 @@ def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=Fal
             fp.uploadX(x)
             if devpos:
                 fp.updateTokenParams(pos)
-            fp.forwardAttentionBlock(0, pos, splits, device_position=devpos)
+            fp.forwardAttentionBlock(layer, pos, splits, device_position=devpos)
             got = fp.downloadX()
-            want, attn = orc.attn_block(oc, bw, kc, vc, x, 0, pos, qnorm_w=qw, knorm_w=kw,
+            want, attn = orc.attn_block(oc, bw, kc, vc, x, layer, pos, qnorm_w=qw, knorm_w=kw,
                                         rope_cos=cs, rope_sin=sn, n_threads=16, return_attn=True)
-            gk, gv = fp.kv.read(0, 0, pos + 1)
+            gk, gv = fp.kv.read(layer, 0, pos + 1)
             assert np.array_equal(gk[:pos], kc[:pos]) and np.array_equal(gv[:pos], vc[:pos])
             dc.compare_out(gk[pos], kc[pos], f"block {what} appended K row")
             dc.compare_out(gv[pos], vc[pos], f"block {what} appended V row")
@@ -225,6 +228,33 @@ def test_block_q8_1_merged_qkv_bias_granite_scale():
     c = hfp.ModelConfig(12, 4, 128, 1, rope_freq_base=1e6, norm_eps=1e-6)
     _run(c, 3072, 64, 20, 2, (gp.GGML_Q8_0,) * 4, seed=840, what="q8_1 merged Q8_0",
          merged=True, bias=True, rscale=0.3, q8=True)
+
+
+# ---- the MoE engines' attention half (Qwen3MoEInferenceEngine.gqaAttention, :237-328) -------
+
+@pytest.mark.parametrize("layer", [0, 1], ids=["windowed", "global"])
+@pytest.mark.parametrize("q8", [False, True], ids=["f32-input", "q8_1-input"])
+def test_block_gptoss_20b_attention(layer, q8):
+    """GPT-OSS-20B's attention half: dim 2880 with q_dim 4096 (64 x 64), Q8_0 projections with
+    biases on q, k, v and o, attention sinks, the engine's window of 128 on even layers, the
+    YaRN-style scale; positions across the window edge."""
+    c = hfp.ModelConfig(64, 8, 64, 2, architecture=hfp.ARCH_GPT_OSS, rope_freq_base=150000.0,
+                        sliding_window=128, expert_count=32,
+                        attention_scale=float(np.float32(1.3 * 1.3 / 8.0)))
+    sinks = np.random.default_rng(850).uniform(-1.0, 3.0, 64).astype(np.float32)
+    _run(c, 2880, 256, 126, 3, (gp.GGML_Q8_0,) * 4, seed=851 + layer, what=f"gpt-oss layer {layer}",
+         bias=True, sinks=sinks, layer=layer, q8=q8)
+
+
+def test_block_qwen3_30b_a3b_attention():
+    """Qwen3-30B-A3B's attention half: dim 2048 with q_dim 4096 (32 x 128), 4 KV heads (GQA 8),
+    per-head QK-norm, the Q4_K_M mix."""
+    c = hfp.ModelConfig(32, 4, 128, 1, architecture=hfp.ARCH_QWEN3, rope_freq_base=1e6,
+                        norm_eps=1e-6)
+    rng = np.random.default_rng(860)
+    qk = (rng.uniform(0.5, 1.5, 128).astype(F32), rng.uniform(0.5, 1.5, 128).astype(F32))
+    _run(c, 2048, 1024, 900, 3, (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K),
+         seed=861, what="qwen3-30b-a3b", qk=qk)
 
 
 def test_block_error_codes():
