@@ -627,12 +627,16 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
                 for (int j = 0; j < 4; ++j) mt = fmaxf(mt, st[hh][kt][j]);
             mt = fmaxf(mt, __shfl_xor(mt, 16));
             mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float mn = fmaxf(m[hh], mt);
-            const float alpha = dk::fast_exp2(m[hh] - mn);
-            m[hh] = mn;
-            l[hh] = l[hh] * alpha;
+            // rescale only when some row's running max grew: otherwise alpha is exactly 1
+            if (__any(mt > m[hh])) {
+                const float mn = fmaxf(m[hh], mt);
+                const float alpha = dk::fast_exp2(m[hh] - mn);
+                m[hh] = mn;
+                l[hh] = l[hh] * alpha;
 #pragma unroll
-            for (int d = 0; d < DT; ++d) o[hh][d] = o[hh][d] * alpha;
+                for (int d = 0; d < DT; ++d) o[hh][d] = o[hh][d] * alpha;
+            }
+            const float mn = m[hh];
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
