@@ -137,6 +137,17 @@ def test_block_every_weight_format(t):
     _run(c, 1024, 64, 40, 2, (t, t, t, t), seed=600 + t, what=NAMES[t])
 
 
+WIDE = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0]
+
+
+@pytest.mark.parametrize("t", WIDE, ids=[NAMES[t] for t in WIDE])
+def test_block_weight_formats_at_width_4096(t):
+    """Rows of 4096 columns: 8 unit rounds in registers and a second batch for the 4-weight
+    unit formats (F32, F16, BF16, Q8_0), 8 rounds for Q4_0."""
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    _run(c, 4096, 64, 33, 1, (t, t, t, t), seed=900 + t, what=f"{NAMES[t]} width 4096")
+
+
 def test_block_c3_llama3b_shape_q4_k_m_mix():
     """C3 shape (24/8/128, dim 3072) with the Q4_K_M mix: Q4_K for q, k, o and Q6_K for v
     (separate launches per weight type), four steps after a 2000-row prefix."""
