@@ -28,11 +28,16 @@ struct SplitKernel {
 template <int D, int G, int W, bool Q8>
 SplitKernel kernel_dgw() {
     constexpr Tune t = pick(D, G);
-    // Q8_0 rows are read as 16 quants per lane (D/16 lanes per row).
-    constexpr int EPL = Q8 ? 16 : t.epl;
-    constexpr int UNROLL = Q8 ? (G > 4 ? 1 : 2) : t.unroll;
-    return SplitKernel{
-        reinterpret_cast<const void*>(&dk::decode_split_kernel<D, G, EPL, UNROLL, W, t.nt, Q8>), W};
+    // Q8_0 caches with up to 4 query heads per KV head: scores on the int8 matrix cores.
+    if constexpr (Q8 && G <= 4 && D <= 256) {
+        return SplitKernel{reinterpret_cast<const void*>(&dk::decode_q8_mfma_kernel<D, G, W, t.nt>), W};
+    } else {
+        // Q8_0 rows are read as 16 quants per lane (D/16 lanes per row).
+        constexpr int EPL = Q8 ? 16 : t.epl;
+        constexpr int UNROLL = Q8 ? 1 : t.unroll;
+        return SplitKernel{
+            reinterpret_cast<const void*>(&dk::decode_split_kernel<D, G, EPL, UNROLL, W, t.nt, Q8>), W};
+    }
 }
 
 // 8-wave workgroups except where more than 4 query heads per KV head hold 16 elements per

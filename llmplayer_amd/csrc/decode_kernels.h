@@ -337,6 +337,19 @@ struct HeadPrep {
     int rope_type;         // 0 NORMAL, 2 NEOX
 };
 
+// The same parameters with the weights and the RoPE row staged in LDS (pointers in the LDS
+// address space, so the prep reads them with LDS loads; a null pointer means "absent").
+typedef __attribute__((address_space(3))) const float* lds_cptr;
+struct HeadPrepLds {
+    lds_cptr qnw;
+    lds_cptr knw;
+    float eps;
+    lds_cptr cos_row;
+    lds_cptr sin_row;
+    int half_rope;
+    int rope_type;
+};
+
 __device__ __forceinline__ HeadPrep head_prep(const DecodeArgs& a, int pos) {
     const long long row = (long long)pos * a.half_rope;
     return HeadPrep{a.qnw, a.knw, a.eps, a.cos_t ? a.cos_t + row : nullptr,
@@ -365,15 +378,15 @@ __device__ __forceinline__ float seq_rms_inv(const float* x, float eps) {
 // heads < n_w0 and p.knw for the others, then RoPE.  The sum of squares follows
 // SimdVectorOps.dot's 8-lane FMA order, or with `seq` RMSNorm.apply's sequential one.  Must
 // be called by the whole workgroup (NTHR threads).
-template <int D, int NTHR>
+template <int D, int NTHR, class HP = HeadPrep>
 __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* s_r,
-                               const HeadPrep& p, int tid, bool seq = false) {
+                               const HP& p, int tid, bool seq = false) {
     if (p.qnw != nullptr && seq) {
         for (int t = tid; t < nh; t += NTHR) s_r[t] = seq_rms_inv<D>(x + t * D, p.eps);
         __syncthreads();
         for (int i = tid; i < nh * D; i += NTHR) {
             const int hh = i / D;
-            const float* w = (hh < n_w0) ? p.qnw : p.knw;
+            const auto w = (hh < n_w0) ? p.qnw : p.knw;
             const float xs = x[i] * s_r[hh];
             x[i] = xs * w[i - hh * D];
         }
@@ -400,7 +413,7 @@ __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* 
         __syncthreads();
         for (int i = tid; i < nh * D; i += NTHR) {
             const int hh = i / D;
-            const float* w = (hh < n_w0) ? p.qnw : p.knw;
+            const auto w = (hh < n_w0) ? p.qnw : p.knw;
             const float xs = x[i] * s_r[hh];
             x[i] = xs * w[i - hh * D];
         }
@@ -465,6 +478,49 @@ __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const
                 }
             }
         }
+    }
+}
+
+// The new token's K and V rows of KV head kvh, staged for the append by the whole workgroup:
+// k (sk) exactly QK-normed and rotated like the CPU path, v (sv) V-normed when the layer asks
+// for it (Gemma 4's weightless V-norm: its sequential sum runs on another wave than the
+// K-norm's thread 0, and is applied after the K prep's barriers).
+template <int D, int NTHR>
+__device__ void stage_new_row(const DecodeArgs& a, int kvh, float* sk, float* sv, float* s_acc,
+                              float* s_r, float* s_vr, const HeadPrep& hp, int tid) {
+    for (int i = tid; i < D; i += NTHR) {
+        sk[i] = a.k[kvh * D + i];
+        sv[i] = a.v[kvh * D + i];
+    }
+    __syncthreads();
+    if (a.v_norm != 0 && tid == (NTHR > 64 ? 64 : 0)) *s_vr = seq_rms_inv<D>(sv, a.eps);
+    prep_heads_lds<D, NTHR>(sk, 1, 0, s_acc, s_r, hp, tid, a.norm_seq != 0);
+    if (a.v_norm != 0) {
+        __syncthreads();
+        for (int i = tid; i < D; i += NTHR) sv[i] = sv[i] * *s_vr;
+        __syncthreads();
+    }
+}
+
+// Q8_0 append of the staged row pos (KVCache.storeK/storeV in Q8_0 mode): quantised into LDS
+// (kq/ks, vq/vs) and written to the cache.
+template <int D, int NTHR>
+__device__ void append_row_q8(const DecodeArgs& a, int kvh, int pos, const float* sk,
+                              const float* sv, signed char* kq, float* ks, signed char* vq,
+                              float* vs, float* s_inv, int tid) {
+    quantize_row_lds<D, NTHR>(sk, kq, ks, s_inv, tid, a.q8_trunc != 0);
+    quantize_row_lds<D, NTHR>(sv, vq, vs, s_inv, tid, a.q8_trunc != 0);
+    signed char* kqp = a.kq + (long long)kvh * a.head_stride + (long long)pos * D;
+    signed char* vqp = a.vq + (long long)kvh * a.head_stride + (long long)pos * D;
+    float* ksp = a.ks + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
+    float* vsp = a.vs + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
+    for (int i = tid; i < D; i += NTHR) {
+        kqp[i] = kq[i];
+        vqp[i] = vq[i];
+    }
+    for (int b = tid; b < D / 32; b += NTHR) {
+        ksp[b] = ks[b];
+        vsp[b] = vs[b];
     }
 }
 
@@ -611,21 +667,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     //    the exact fp32 rows, or their Q8_0 quantisation), and take row `pos` from LDS as the
     //    cache now holds it (row group 0 of wave 0).
     if (has_pos) {
-        for (int i = tid; i < D; i += NTHR) {
-            s_x[G * D + i] = a.k[kvh * D + i];
-            s_v[i] = a.v[kvh * D + i];
-        }
-        __syncthreads();
-        // Gemma 4's weightless V-norm: its sequential sum runs on another wave than the
-        // K-norm's (thread 0), and is applied after the K prep's barriers.
         __shared__ float s_vr;
-        if (a.v_norm != 0 && tid == (NTHR > 64 ? 64 : 0)) s_vr = seq_rms_inv<D>(s_v, a.eps);
-        prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, hp, tid, a.norm_seq != 0);
-        if (a.v_norm != 0) {
-            __syncthreads();
-            for (int i = tid; i < D; i += NTHR) s_v[i] = s_v[i] * s_vr;
-            __syncthreads();
-        }
+        stage_new_row<D, NTHR>(a, kvh, s_x + G * D, s_v, s_acc, s_r, &s_vr, hp, tid);
         if constexpr (!Q8) {
             float* kplane = a.kc + (long long)kvh * a.head_stride;
             float* vplane = a.vc + (long long)kvh * a.head_stride;
@@ -646,22 +689,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
                 accumulate_rows<D, G, EPL, 1>(qr, kf, vf, valid, m, l, o, a);
             }
         } else {
-            __shared__ signed char s_kq[D], s_vq[D];
+            __shared__ __align__(16) signed char s_kq[D], s_vq[D];
             __shared__ float s_ks[D / 32], s_vs[D / 32], s_inv[D / 32];
-            quantize_row_lds<D, NTHR>(s_x + G * D, s_kq, s_ks, s_inv, tid, a.q8_trunc != 0);
-            quantize_row_lds<D, NTHR>(s_v, s_vq, s_vs, s_inv, tid, a.q8_trunc != 0);
-            signed char* kqp = a.kq + (long long)kvh * a.head_stride + (long long)pos * D;
-            signed char* vqp = a.vq + (long long)kvh * a.head_stride + (long long)pos * D;
-            float* ksp = a.ks + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
-            float* vsp = a.vs + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
-            for (int i = tid; i < D; i += NTHR) {
-                kqp[i] = s_kq[i];
-                vqp[i] = s_vq[i];
-            }
-            for (int b = tid; b < D / 32; b += NTHR) {
-                ksp[b] = s_ks[b];
-                vsp[b] = s_vs[b];
-            }
+            append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid);
             if (wave == 0) {
                 float kq[1][16], vq[1][16], ksc[1], vsc[1];
                 bool valid[1] = {grp == 0};
@@ -737,6 +767,381 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             if (d == 0) {
                 a.part_ml[2 * slot] = M;
                 a.part_ml[2 * slot + 1] = L;
+            }
+        }
+    }
+}
+
+// ---- Q8_0 cache, scores on the matrix cores --------------------------------------------------
+// The same split-K decode over a Q8_0 cache (GQA groups of up to 4 query heads), with the
+// scores as int8 matrix products: per 16-key tile and 32-dim scale block, one
+// v_mfma_i32_16x16x32_i8 multiplies the tile's K quants (B operand, read straight from the
+// cache) by the query's int8 parts (A operand).  Each (query head, block) of the scaled query
+// is held as q = s * (Q1 + (Q2 + Q3/F)/F) with s = max|q|/127 and F = 254, Q1..Q3 int8, which
+// represents q to 2^-23 of the block maximum; the three integer dot products with the quants
+// are exact, so a score  sum_b ks_b * s_b * (D1 + (D2 + D3/F)/F)  rounds at the fp32 level of
+// KVCache.dotK in Q8_0 mode (KVCache.java:187-195).  Rows of A are (head, part) = 4*head +
+// part, so the accumulator lane (key l%16, head l/16) holds a head's three part sums for its
+// key.  The online softmax runs per 16-key tile in that layout (tile max over a DPP row); the
+// probabilities go through LDS to the V lanes, which accumulate o += (p * vscale) * quants in
+// fp32 as KVCache.saxpyV does (KVCache.java:201-210), 16 quants per lane.
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+typedef unsigned int native_u2 __attribute__((ext_vector_type(2)));
+
+constexpr float kQPartF = 254.0f;
+constexpr float kQPartInvF = 1.0f / 254.0f;
+
+template <bool NT>
+__device__ __forceinline__ uint2 load_u2(const uint2* p) {
+    if constexpr (NT) {
+        const native_u2 v = __builtin_nontemporal_load(reinterpret_cast<const native_u2*>(p));
+        return make_uint2(v.x, v.y);
+    } else {
+        return *p;
+    }
+}
+
+// The raw bytes one lane holds of a 16-key tile.
+template <int D>
+struct Q8Tile {
+    static constexpr int NB = D / 32;     // scale blocks per row
+    static constexpr int LPR = D / 16;    // V lanes per key (16 quants each)
+    static constexpr int KPL = 64 / LPR;  // keys per wave-wide V load
+    static constexpr int UV = 16 / KPL;   // V loads per tile
+    uint2 k[NB];   // K quants of key l%16, dims 32b + 8(l/16) .. +7 (MFMA B operand)
+    float ks[NB];  // K block scales of key l%16
+    uint4 v[UV];   // V quants of key u*KPL + l/LPR, dims 16(l%LPR) .. +15
+    float vs[UV];  // its V block scale
+};
+
+// Loads of keys t0 .. t0+15 (rows past `last` read row `last` and are masked by the caller).
+template <int D, bool NT>
+__device__ __forceinline__ void q8_tile_load(Q8Tile<D>& t, const signed char* kq, const float* ks,
+                                             const signed char* vq, const float* vs, int t0,
+                                             int last, int lane) {
+    using T = Q8Tile<D>;
+    const int kr = min(t0 + (lane & 15), last);
+    const signed char* krow = kq + (long long)kr * D + 8 * (lane >> 4);
+#pragma unroll
+    for (int b = 0; b < T::NB; ++b) t.k[b] = load_u2<NT>(reinterpret_cast<const uint2*>(krow + 32 * b));
+    const float* ksr = ks + (long long)kr * T::NB;
+    if constexpr (T::NB % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < T::NB / 4; ++c) {
+            const float4 x = *reinterpret_cast<const float4*>(ksr + 4 * c);
+            t.ks[4 * c + 0] = x.x;
+            t.ks[4 * c + 1] = x.y;
+            t.ks[4 * c + 2] = x.z;
+            t.ks[4 * c + 3] = x.w;
+        }
+    } else {
+        static_assert(T::NB == 2, "head_dim 64, 128 or 256");
+        const float2 x = *reinterpret_cast<const float2*>(ksr);
+        t.ks[0] = x.x;
+        t.ks[1] = x.y;
+    }
+    const int j = lane % T::LPR;
+#pragma unroll
+    for (int u = 0; u < T::UV; ++u) {
+        const int vr = min(t0 + u * T::KPL + lane / T::LPR, last);
+        t.v[u] = load_u4<NT>(reinterpret_cast<const uint4*>(vq + (long long)vr * D) + j);
+        t.vs[u] = vs[(long long)vr * T::NB + (j >> 1)];
+    }
+}
+
+// Int8 parts of the scaled query heads x ([G][D] fp32 in LDS), computed once per workgroup:
+// parts [3][G][D] bytes, block scales qs [G][NB].  Value i of a pass sits in the 32-lane group
+// that holds its whole block, so the block maximum is a cross-lane reduction.
+template <int D, int G, int NTHR>
+__device__ __forceinline__ void q8_query_split(const float* x, float qk_scale, signed char* parts,
+                                               float* qs, int tid) {
+    static_assert((G * D) % 32 == 0 && NTHR % 64 == 0, "blocks fill whole 32-lane groups");
+    for (int i0 = 0; i0 < G * D; i0 += NTHR) {
+        const int i = i0 + tid;
+        const bool in = i < G * D;
+        const float x0 = in ? x[i] * qk_scale : 0.0f;
+        float mx = fabsf(x0);
+        mx = fmaxf(mx, dpp<kDppQuadXor1>(mx));
+        mx = fmaxf(mx, dpp<kDppQuadXor2>(mx));
+        mx = fmaxf(mx, dpp<kDppRowHalfMirror>(mx));
+        mx = fmaxf(mx, dpp<kDppRowMirror>(mx));
+        mx = lane_step<16, true>(mx);
+        const float sc = mx / 127.0f;
+        const float inv = sc != 0.0f ? 1.0f / sc : 0.0f;
+        const float v = x0 * inv;
+        const float q1 = fminf(fmaxf(rintf(v), -127.0f), 127.0f);
+        const float r1 = (v - q1) * kQPartF;
+        const float q2 = fminf(fmaxf(rintf(r1), -127.0f), 127.0f);
+        const float r2 = (r1 - q2) * kQPartF;
+        const float q3 = fminf(fmaxf(rintf(r2), -127.0f), 127.0f);
+        if (in) {
+            parts[i] = (signed char)(int)q1;
+            parts[G * D + i] = (signed char)(int)q2;
+            parts[2 * G * D + i] = (signed char)(int)q3;
+            if ((i & 31) == 0) qs[i >> 5] = sc;
+        }
+    }
+}
+
+// The lane's A operands (one per 32-dim block): row l%16 = (head (l%16)/4, part l%4), dims
+// 32b + 8(l/16) .. +7.  Rows of absent heads and part 3 are zero.
+template <int D, int G>
+__device__ __forceinline__ void q8_query_operands(const signed char* parts, int lane,
+                                                  long (&aq)[D / 32]) {
+    const int row = lane & 15, h = row >> 2, part = row & 3;
+    const bool live = h < G && part < 3;
+    const signed char* src = parts + (live ? part * G * D + h * D : 0) + 8 * (lane >> 4);
+#pragma unroll
+    for (int b = 0; b < D / 32; ++b) {
+        const long w = *reinterpret_cast<const long*>(src + 32 * b);
+        aq[b] = live ? w : 0;
+    }
+}
+
+// Orders one wave's LDS writes before its later LDS reads of other lanes' data.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int D, int G, int WAVES, bool NT>
+__global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a) {
+    static_assert(G >= 1 && G <= 4, "A rows hold 4 heads x (3 parts + 1)");
+    using T = Q8Tile<D>;
+    constexpr int NB = T::NB, LPR = T::LPR, KPL = T::KPL, UV = T::UV;
+    constexpr int NTHR = WAVES * 64;
+    constexpr int TSTEP = WAVES * 16;
+
+    __shared__ float s_x[(G + 1) * D];
+    __shared__ float s_v[D];
+    __shared__ float s_acc[(G + 1) * 8];
+    __shared__ float s_r[G + 1];
+    __shared__ float s_qs[G * NB];
+    __shared__ __align__(16) signed char s_qp[3 * G * D];
+    __shared__ float4 s_p[WAVES * 16];  // per wave and key slot: p of heads 0..3
+    __shared__ float4 s_al[WAVES];      // per wave: rescale factors of heads 0..3
+    __shared__ float s_m[WAVES * G];
+    __shared__ float s_l[WAVES * G];
+    __shared__ float s_o[WAVES * G * D];
+
+    const int tid = threadIdx.x;
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int h0 = kvh * G;
+    const int pos = step_position(a);
+    if (pos < 0 || pos >= a.max_seq) return;
+    const StepPlan sp = plan_step(pos, a.window, a.splits);
+    if (split >= sp.splits) return;
+    const HeadPrep hp = head_prep(a, pos);
+    const int row_begin = sp.start + split * sp.rows_per_split;
+    const int row_end = min(row_begin + sp.rows_per_split, pos + 1);
+    const bool has_pos = (row_end == pos + 1) && a.no_append == 0;
+    const int cache_end = has_pos ? pos : row_end;
+    // The wave index is wave-uniform: from an SGPR, the tile loop's branches are scalar.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+
+    const signed char* kqp = a.kq + (long long)kvh * a.head_stride;
+    const signed char* vqp = a.vq + (long long)kvh * a.head_stride;
+    const float* ksp = a.ks + (long long)kvh * (a.head_stride / 32);
+    const float* vsp = a.vs + (long long)kvh * (a.head_stride / 32);
+    const int last = cache_end > 0 ? cache_end - 1 : 0;
+
+    // 1. The query prep's inputs are requested first and the wave's first two tiles right
+    //    after them: the load counter completes in order, so the prologue waits for its own
+    //    loads alone while the tiles stream in.
+    static_assert(D <= NTHR, "one RoPE pair and one norm weight per thread");
+    constexpr int QPT = (G * D + NTHR - 1) / NTHR;
+    float qv[QPT];
+#pragma unroll
+    for (int r = 0; r < QPT; ++r) qv[r] = a.q[h0 * D + min(tid + r * NTHR, G * D - 1)];
+    const bool rope = hp.cos_row != nullptr, qkn = hp.qnw != nullptr;
+    const int ci = min(tid, max(hp.half_rope - 1, 0));
+    const float cs = (rope ? hp.cos_row : a.q)[rope ? ci : 0];
+    const float sn = (rope ? hp.sin_row : a.q)[rope ? ci : 0];
+    const float qw = (qkn ? hp.qnw : a.q)[qkn ? tid % D : 0];
+    T ta, tb;
+    int t0 = row_begin + wave * 16;
+    q8_tile_load<D, NT>(ta, kqp, ksp, vqp, vsp, t0, last, lane);
+
+    // 2. Query heads: exact prep in LDS, the scale folded in, split into int8 parts.
+    __shared__ float s_cs[D / 2], s_sn[D / 2], s_qw[D];
+#pragma unroll
+    for (int r = 0; r < QPT; ++r)
+        if (tid + r * NTHR < G * D) s_x[tid + r * NTHR] = qv[r];
+    if (tid < hp.half_rope) {
+        s_cs[tid] = cs;
+        s_sn[tid] = sn;
+    }
+    if (tid < D) s_qw[tid] = qw;
+    __syncthreads();
+    const lds_cptr lnull = nullptr;
+    const HeadPrepLds hl{qkn ? (lds_cptr)s_qw : lnull, qkn ? (lds_cptr)s_qw : lnull, hp.eps,
+                         rope ? (lds_cptr)s_cs : lnull, rope ? (lds_cptr)s_sn : lnull,
+                         hp.half_rope, hp.rope_type};
+    prep_heads_lds<D, NTHR>(s_x, G, G, s_acc, s_r, hl, tid);
+    q8_query_split<D, G, NTHR>(s_x, a.qk_scale, s_qp, s_qs, tid);
+    __syncthreads();
+    long aq[NB];
+    q8_query_operands<D, G>(s_qp, lane, aq);
+    const int qh = lane >> 4;  // head of the lane's scores
+    float sq[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) sq[b] = qh < G ? s_qs[qh * NB + b] : 0.0f;
+
+    // 3. Stream the cached rows in 16-key tiles, one tile ahead in registers.
+    float M = kNegBig, lsum = 0.0f;
+    float o[G][16];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[h][e] = 0.0f;
+    float4* sp_w = s_p + wave * 16;
+    float* al_w = reinterpret_cast<float*>(s_al + wave);
+
+    auto consume = [&](const T& t, int base, int end) {
+        float s = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                aq[b], __builtin_bit_cast(long, t.k[b]), v4i_t{0, 0, 0, 0}, 0, 0, 0);
+            const float f = (float)d[0] + ((float)d[1] + (float)d[2] * kQPartInvF) * kQPartInvF;
+            s = __builtin_fmaf(f, t.ks[b] * sq[b], s);
+        }
+        if (a.softcap > 0.0f) s = a.softcap_log2e * tanhf(s * a.inv_softcap);
+        s = base + (lane & 15) < end ? s : -__builtin_inff();
+        float mt = fmaxf(s, dpp<kDppQuadXor1>(s));
+        mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));
+        mt = fmaxf(mt, dpp<kDppRowHalfMirror>(mt));
+        mt = fmaxf(mt, dpp<kDppRowMirror>(mt));
+        const bool rescale = __any(mt > M + kLazyMargin);
+        if (rescale) {
+            const float mn = fmaxf(M, mt);
+            const float al = fast_exp2(M - mn);
+            M = mn;
+            lsum = lsum * al;
+            if ((lane & 15) == 0) al_w[qh] = al;
+        }
+        const float p = fast_exp2(s - M);
+        lsum = lsum + p;
+        reinterpret_cast<float*>(sp_w)[(lane & 15) * 4 + qh] = p;
+        wave_lds_sync();
+        if (rescale) {
+            const float4 al4 = *reinterpret_cast<const float4*>(al_w);
+            const float al[4] = {al4.x, al4.y, al4.z, al4.w};
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[h][e] = o[h][e] * al[h];
+        }
+#pragma unroll
+        for (int u = 0; u < UV; ++u) {
+            const float4 p4 = sp_w[u * KPL + lane / LPR];
+            const float pw[4] = {p4.x, p4.y, p4.z, p4.w};
+            float w[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) w[h] = pw[h] * t.vs[u];
+            const unsigned dw[4] = {t.v[u].x, t.v[u].y, t.v[u].z, t.v[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const float vf = (float)(int)(signed char)(dw[c] >> (8 * b));
+#pragma unroll
+                    for (int h = 0; h < G; ++h)
+                        o[h][4 * c + b] = __builtin_fmaf(w[h], vf, o[h][4 * c + b]);
+                }
+        }
+        wave_lds_sync();
+    };
+
+    // Tiles in pairs, so that the loop has one exit (a break between the two halves would
+    // join the loop head with the second buffer's loads in flight, and the wait inserted
+    // there would drain the prefetch on every trip); an odd last tile follows.
+    const int ntiles = t0 < cache_end ? (cache_end - t0 + TSTEP - 1) / TSTEP : 0;
+    for (int i = 0; i + 1 < ntiles; i += 2) {
+        q8_tile_load<D, NT>(tb, kqp, ksp, vqp, vsp, t0 + TSTEP, last, lane);
+        consume(ta, t0, cache_end);
+        q8_tile_load<D, NT>(ta, kqp, ksp, vqp, vsp, t0 + 2 * TSTEP, last, lane);
+        consume(tb, t0 + TSTEP, cache_end);
+        t0 += 2 * TSTEP;
+    }
+    if (ntiles & 1) consume(ta, t0, cache_end);
+
+    // 4. The split that owns row pos appends it and takes it from LDS as a one-key tile.
+    if (has_pos) {
+        __shared__ float s_vr;
+        __shared__ __align__(16) signed char s_kq[D], s_vq[D];
+        __shared__ float s_ks[NB], s_vs[NB], s_inv[NB];
+        stage_new_row<D, NTHR>(a, kvh, s_x + G * D, s_v, s_acc, s_r, &s_vr, hp, tid);
+        append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid);
+        if (wave == 0) {
+            T t;
+            const bool k0 = (lane & 15) == 0;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                t.k[b] = k0 ? *reinterpret_cast<const uint2*>(s_kq + 32 * b + 8 * (lane >> 4))
+                            : make_uint2(0u, 0u);
+                t.ks[b] = k0 ? s_ks[b] : 0.0f;
+            }
+            const bool v0 = lane < LPR;
+            t.v[0] = v0 ? *reinterpret_cast<const uint4*>(s_vq + 16 * lane) : make_uint4(0u, 0u, 0u, 0u);
+            t.vs[0] = v0 ? s_vs[lane >> 1] : 0.0f;
+#pragma unroll
+            for (int u = 1; u < UV; ++u) {
+                t.v[u] = make_uint4(0u, 0u, 0u, 0u);
+                t.vs[u] = 0.0f;
+            }
+            consume(t, pos, pos + 1);
+        }
+    }
+
+    // 5. Merge within the wave: sums over the key slots of a head (one DPP row) and over the
+    //    V lanes of equal dims, then across waves through LDS.
+    const float L = row_group_sum<16>(lsum);
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float x = o[h][e];
+            if constexpr (LPR <= 4) x = lane_step<4, false>(x);
+            if constexpr (LPR <= 8) x = lane_step<8, false>(x);
+            if constexpr (LPR <= 16) x = lane_step<16, false>(x);
+            x = lane_step<32, false>(x);
+            o[h][e] = x;
+        }
+    if (lane < LPR) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s_o[(wave * G + h) * D + 16 * lane + e] = o[h][e];
+    }
+    if ((lane & 15) == 0 && qh < G) {
+        s_m[wave * G + qh] = M;
+        s_l[wave * G + qh] = L;
+    }
+    __syncthreads();
+
+    for (int idx = tid; idx < G * D; idx += NTHR) {
+        const int h = idx / D, d = idx - h * D;
+        float Mx = s_m[h];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) Mx = fmaxf(Mx, s_m[w * G + h]);
+        float Ls = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float sc = fast_exp2(s_m[w * G + h] - Mx);
+            Ls = __builtin_fmaf(s_l[w * G + h], sc, Ls);
+            O = __builtin_fmaf(s_o[(w * G + h) * D + d], sc, O);
+        }
+        if (sp.splits == 1) {
+            a.out[(h0 + h) * D + d] =
+                finish_output(Mx, Ls, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
+        } else {
+            const long long slot = ((long long)kvh * sp.splits + split) * G + h;
+            a.part_o[slot * D + d] = O;
+            if (d == 0) {
+                a.part_ml[2 * slot] = Mx;
+                a.part_ml[2 * slot + 1] = Ls;
             }
         }
     }
