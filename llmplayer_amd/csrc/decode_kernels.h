@@ -1147,10 +1147,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
     }
 }
 
-// Combine of the splits: one block per query head; thread (column c, split group p) owns float4 column c of the head's output for the
-// splits p, p+NP, ...  Every load of a thread is issued up front (one memory round trip),
-// the per-group maxima and sums are merged through LDS.
+// Combine of the splits: one block per query head; thread (column c, split group p) owns
+// float4 column c of the head's output for the splits p, p+NP, ...  A thread's first
+// kReduceBatch splits are loaded at once (one memory round trip), any further ones merge
+// online; the per-group maxima and sums are merged through LDS.
 constexpr int kReduceThreads = 256;
+constexpr int kReduceBatch = 12;   // splits per thread loaded up front (96 splits at head_dim 128)
 
 template <int D>
 __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArgs a, int G) {
@@ -1168,11 +1170,36 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
     if (S == 1) return;   // the split kernel wrote the output directly
     const long long slot0 = (long long)kvh * S * G + h;  // slot of split j: slot0 + j*G
 
-    // Online merge over this thread's splits (loads are independent of the running max).
+    // This thread's first kReduceBatch splits: every load issued at once (masked entries
+    // read split 0 and drop out), then one max and one weighted sum.
     float m = kNegBig, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    {
+        float mj[kReduceBatch], lj[kReduceBatch];
+        float4 oj[kReduceBatch];
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u) {
+            const int jj = p + u * NP;
+            const long long slot = slot0 + (long long)(jj < S ? jj : 0) * G;
+            mj[u] = a.part_ml[2 * slot];
+            lj[u] = a.part_ml[2 * slot + 1];
+            oj[u] = reinterpret_cast<const float4*>(a.part_o + slot * D)[c];
+        }
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u) m = fmaxf(m, p + u * NP < S ? mj[u] : kNegBig);
+#pragma unroll
+        for (int u = 0; u < kReduceBatch; ++u) {
+            const float sj = p + u * NP < S ? fast_exp2(mj[u] - m) : 0.0f;
+            l = __builtin_fmaf(lj[u], sj, l);
+            o.x = __builtin_fmaf(oj[u].x, sj, o.x);
+            o.y = __builtin_fmaf(oj[u].y, sj, o.y);
+            o.z = __builtin_fmaf(oj[u].z, sj, o.z);
+            o.w = __builtin_fmaf(oj[u].w, sj, o.w);
+        }
+    }
+    // Splits beyond the batch: online merge.
 #pragma unroll 4
-    for (int jj = p; jj < S; jj += NP) {
+    for (int jj = p + kReduceBatch * NP; jj < S; jj += NP) {
         const long long slot = slot0 + (long long)jj * G;
         const float mj = a.part_ml[2 * slot], lj = a.part_ml[2 * slot + 1];
         const float4 oj = reinterpret_cast<const float4*>(a.part_o + slot * D)[c];

@@ -109,6 +109,40 @@ def test_q8_every_group_and_head_dim(hq, hkv, dim, mode):
             _run(fp, c, 1200, d, 0, 999, splits, f"shape {hq}/{hkv}/{dim}", mode)
 
 
+RAGGED = [(8, 8, 64), (24, 8, 128), (16, 4, 256)]
+
+
+@pytest.mark.parametrize("hq,hkv,dim", RAGGED, ids=[f"{a}-{b}-{c}" for a, b, c in RAGGED])
+def test_q8_short_and_ragged_rows(hq, hkv, dim, mode):
+    """GQA groups 1, 3 and 4 (the int8-MFMA score path) at positions 0 to 100: a partial first
+    16-key tile, exact tile boundaries, and row `pos` alone in its split, at several split
+    counts."""
+    c = hfp.ModelConfig(hq, hkv, dim, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=500000.0)
+    with _open(c, 128, mode) as fp:
+        for pos in (0, 1, 15, 16, 17, 31, 32, 33, 100):
+            d = dc.make_layer_q8(c, 128, pos, seed=700 + pos, mode=mode[1])
+            for splits in (0, 1, 2, 7):
+                _run(fp, c, 128, d, 0, pos, splits, f"{hq}/{hkv}/{dim} pos {pos}", mode,
+                     check_cache=(splits == 0))
+
+
+@pytest.mark.parametrize("q_scale", [1e-3, 1.0, 30.0])
+def test_q8_query_magnitudes_and_special_blocks(q_scale, mode):
+    """The query's int8 parts (per head and 32-dim block: q = s*(Q1 + (Q2 + Q3/254)/254)) at
+    small and large magnitudes, with an all-zero block (scale 0) and a block with one dominant
+    element next to small ones (the parts must carry the small ones to fp32 precision)."""
+    c = hfp.ModelConfig(24, 8, 128, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=500000.0)
+    d = dc.make_layer_q8(c, 1024, 1000, seed=810, mode=mode[1])
+    d.q[:] *= np.float32(q_scale)
+    d.q[32:64] = 0.0                                     # head 0, block 1
+    d.q[128 + 64:128 + 96] *= np.float32(1e-3)           # head 1, block 2: small values ...
+    d.q[128 + 70] = np.float32(8.0 * q_scale)            # ... and one dominant element
+    with _open(c, 1024, mode) as fp:
+        for splits in (0, 1, 5):
+            _run(fp, c, 1024, d, 0, 1000, splits, f"q scale {q_scale}", mode,
+                 check_cache=(splits == 0))
+
+
 @pytest.mark.parametrize("rope_type,rope_dim", [(_lib.LLMP_ROPE_NEOX, 0), (_lib.LLMP_ROPE_NEOX, 64),
                                                 (_lib.LLMP_ROPE_NORMAL, 64)])
 def test_q8_neox_and_partial_rope(rope_type, rope_dim, mode):
