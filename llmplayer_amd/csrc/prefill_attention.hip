@@ -86,7 +86,7 @@ hipError_t launch_tiles_d(const pk::PrefillArgs& a, uint4* ws, int tile0, int n_
 
 template <int D>
 hipError_t launch_append_d(const pk::PrefillArgs& a, hipStream_t stream) {
-    const size_t lds = pk::prefill_append_lds(a.Hkv, D, a.kq != nullptr || a.v_norm != 0);
+    const size_t lds = pk::prefill_append_lds(a.Hkv, D);
     hipLaunchKernelGGL((pk::prefill_append_kernel<D, kAppendThreads>), dim3(a.P),
                        dim3(kAppendThreads), lds, stream, a);
     return hipGetLastError();

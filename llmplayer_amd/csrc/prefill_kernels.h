@@ -82,39 +82,43 @@ __device__ __forceinline__ float bf16_to_f32(unsigned short b) {
     return __uint_as_float((unsigned)b << 16);
 }
 // ---- 1. exact K/V append, one workgroup per token --------------------------------------------
-// LDS floats: Hkv*(D + 9), plus Hkv*(D + 1) + 2*Hkv*D/32 when the V rows are staged (Q8_0
-// cache or V-norm; see prefill_append_lds).
+// Every input of the workgroup (its K and V rows, the RoPE row, the K-norm weights) is requested
+// in one pass and staged in LDS, so the append costs one memory round trip before its stores.
+// LDS floats: Hkv*(2*D + 10) + 2*Hkv*D/32 + 2*D (prefill_append_lds).
 template <int D, int NTHR>
 __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
     extern __shared__ float s_dyn[];
-    float* s_k = s_dyn;                    // Hkv*D
-    float* s_acc = s_dyn + a.Hkv * D;      // Hkv*8
-    float* s_r = s_acc + a.Hkv * 8;        // Hkv
-    const int i = blockIdx.x, tid = threadIdx.x;
-    const int pos = a.pos0 + i;
     const int kvd = a.Hkv * D;
-    for (int e = tid; e < kvd; e += NTHR) s_k[e] = bf16_to_f32(a.k[(long long)i * kvd + e]);
-    __syncthreads();
-    dk::HeadPrep hp{a.knw, a.knw, a.eps,
-                    a.cos_t ? a.cos_t + (long long)pos * a.half_rope : nullptr,
-                    a.sin_t ? a.sin_t + (long long)pos * a.half_rope : nullptr, a.half_rope,
-                    a.rope_type};
-    if (a.qnw == nullptr) hp.qnw = hp.knw = nullptr;
-    dk::prep_heads_lds<D, NTHR>(s_k, a.Hkv, 0, s_acc, s_r, hp, tid, a.norm_seq != 0);
-    if (a.kq == nullptr && a.v_norm == 0) {
-        for (int e = tid; e < kvd; e += NTHR) {
-            const int h = e / D, d = e - h * D;
-            const long long off = (long long)h * a.head_stride + (long long)pos * D + d;
-            a.kc[off] = s_k[e];
-            a.vc[off] = bf16_to_f32(a.v[(long long)i * kvd + e]);
-        }
-        return;
-    }
+    float* s_k = s_dyn;                    // Hkv*D
+    float* s_acc = s_k + kvd;              // Hkv*8
+    float* s_r = s_acc + a.Hkv * 8;        // Hkv
     float* s_v = s_r + a.Hkv;              // Hkv*D
     float* s_vr = s_v + kvd;               // Hkv
     float* s_inv = s_vr + a.Hkv;           // 2*Hkv*D/32
-    for (int e = tid; e < kvd; e += NTHR) s_v[e] = bf16_to_f32(a.v[(long long)i * kvd + e]);
+    float* s_cs = s_inv + 2 * kvd / 32;    // D/2: cos row
+    float* s_sn = s_cs + D / 2;            // D/2: sin row
+    float* s_w = s_sn + D / 2;             // D: K-norm weights
+    const int i = blockIdx.x, tid = threadIdx.x;
+    const int pos = a.pos0 + i;
+    const bool rope = a.cos_t != nullptr, qkn = a.qnw != nullptr;
+    for (int e = tid; e < kvd; e += NTHR) {
+        s_k[e] = bf16_to_f32(a.k[(long long)i * kvd + e]);
+        s_v[e] = bf16_to_f32(a.v[(long long)i * kvd + e]);
+    }
+    if (rope) {
+        for (int e = tid; e < a.half_rope; e += NTHR) {
+            s_cs[e] = a.cos_t[(long long)pos * a.half_rope + e];
+            s_sn[e] = a.sin_t[(long long)pos * a.half_rope + e];
+        }
+    }
+    if (qkn && a.knw != nullptr)
+        for (int e = tid; e < D; e += NTHR) s_w[e] = a.knw[e];
     __syncthreads();
+    const dk::lds_cptr lnull = nullptr;
+    const dk::HeadPrepLds hp{qkn ? (dk::lds_cptr)s_w : lnull, qkn ? (dk::lds_cptr)s_w : lnull,
+                             a.eps, rope ? (dk::lds_cptr)s_cs : lnull,
+                             rope ? (dk::lds_cptr)s_sn : lnull, a.half_rope, a.rope_type};
+    dk::prep_heads_lds<D, NTHR>(s_k, a.Hkv, 0, s_acc, s_r, hp, tid, a.norm_seq != 0);
     if (a.v_norm != 0) {   // Gemma 4's weightless V-norm, sequential order (RMSNorm.applyNoScale)
         for (int h = tid; h < a.Hkv; h += NTHR) s_vr[h] = dk::seq_rms_inv<D>(s_v + h * D, a.eps);
         __syncthreads();
@@ -158,10 +162,9 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
     }
 }
 
-// Dynamic LDS bytes of prefill_append_kernel; stage_v: Q8_0 cache or V-norm.
-inline size_t prefill_append_lds(int Hkv, int D, bool stage_v) {
-    const size_t f = (size_t)Hkv * (D + 9) +
-                     (stage_v ? (size_t)Hkv * (D + 1) + 2 * (size_t)Hkv * D / 32 : 0);
+// Dynamic LDS bytes of prefill_append_kernel.
+inline size_t prefill_append_lds(int Hkv, int D) {
+    const size_t f = (size_t)Hkv * (2 * D + 10) + 2 * (size_t)Hkv * D / 32 + 2 * (size_t)D;
     return f * sizeof(float);
 }
 
