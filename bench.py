@@ -625,6 +625,9 @@ def main() -> int:
                 "kv_read_gbps": round(r["kv_read_gbps"], 1),
                 "split_kernel_us": round(r["split_kernel_us"], 3),
                 "split_kernel_gbps": round(bq / (r["split_kernel_us"] * 1e-6) / 1e9, 1),
+                "split_kernel_pct_of_hbm_peak": round(
+                    100.0 * bq / (r["split_kernel_us"] * 1e-6) / 1e9 / PEAK_GBPS, 2),
+                "kernel": f"decode_q8_mfma_kernel<128, 3, {r['plan']['waves']}, true>",
                 "reduce_kernel_us": round(r["reduce_kernel_us"], 3),
                 "algorithmic_bytes_per_launch": bq,
                 "splits": r["plan"]["splits"], "waves": r["plan"]["waves"],
