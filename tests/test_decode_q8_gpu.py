@@ -237,3 +237,41 @@ def test_q8_cache_rejects_fp32_row_access_and_round_trips_layout(mode):
             assert np.array_equal(kq0, kq[10:15]) and np.array_equal(ks0, ks[10:15])
     with hfp.HipForwardPass(c, 64) as fp:
         assert _lib.status("llmp_kv_read_q8", fp.kv.handle, 0, 0, 1, None, None, None, None) == 6
+
+
+def test_q8_graph_of_device_position_decode_replays_across_tokens(mode):
+    """One capture of a Q8_0 layer's device-position decode (the int8-MFMA score kernel, GQA
+    group 3) replayed for 8 consecutive tokens: q/k/v and the position are uploaded between
+    replays, outside the graph (uploadXAndUpdateParams before cuGraphLaunch in the
+    reference); every replay against the oracle, the cache after the last one bit-exact."""
+    c = hfp.ModelConfig(24, 8, 128, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=500000.0)
+    max_seq, p0, steps = 2048, 1500, 8
+    rng = np.random.default_rng(95)
+    d0 = dc.make_layer_q8(c, max_seq, p0, seed=96, mode=mode[1])
+    cache = (d0.kq.copy(), d0.ks.copy(), d0.vq.copy(), d0.vs.copy())
+    with _open(c, max_seq, mode) as fp:
+        fp.kv.write_q8(0, 0, *cache)
+        out = hfp.DeviceBuffer(c.q_dim * 4)
+        g = C.c_uint64()
+        _lib.call("llmp_graph_begin", 0)
+        _lib.call("llmp_attn_decode_devpos", fp.kv.handle, 0, fp.gpuTokenParams.ptr,
+                  fp.gpuQ.ptr, fp.gpuK.ptr, fp.gpuV.ptr, out.ptr, 0, 0)
+        _lib.call("llmp_graph_end", 0, C.byref(g))
+        try:
+            for i in range(steps):
+                pos = p0 + i
+                q = rng.standard_normal(c.q_dim, dtype=np.float32)
+                k = rng.standard_normal(c.kv_dim, dtype=np.float32)
+                v = rng.standard_normal(c.kv_dim, dtype=np.float32)
+                fp.uploadQKV(q, k, v)
+                fp.updateTokenParams(pos)
+                dc.log(f"[gpu] Q8 graph replay at position {pos}, mode {mode[0]}")
+                _lib.call("llmp_graph_launch", g.value, 0)
+                fp.sync()
+                d = dc.LayerDataQ8(*cache, q, k, v, None)
+                want, cache = dc.oracle_call_q8(c, max_seq, d, 0, pos, mode=mode[1])
+                dc.compare_out(out.download(np.float32, c.q_dim), want, f"Q8 graph replay pos {pos}")
+        finally:
+            _lib.call("llmp_graph_destroy", g.value)
+            out.free()
+        dc.compare_cache_q8(fp, 0, cache, "Q8 cache after graph replays")
