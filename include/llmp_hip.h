@@ -226,7 +226,12 @@ int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int *
  *      CudaContext.java:585-613): record a sequence of launches on a stream once, replay it
  *      with one call.  Arguments (positions included) are frozen at capture time. ---------- */
 /* Start capturing the work enqueued on `stream` (0 = the library stream; capture mode
- * "thread local").  Profiling must be off while capturing. */
+ * "thread local").  Profiling must be off while capturing.  A graph holds the device addresses
+ * its launches had at capture time.  Decode's split workspace is allocated once by
+ * llmp_kv_create and never moves, but set-up calls (llmp_layer_config, llmp_layer_sinks,
+ * llmp_rope_upload, llmp_layer_weight) and a prefill call that grows the handle's prefill
+ * workspace can free memory an earlier graph refers to: capture after set-up, and capture
+ * again after any of them. */
 int llmp_graph_begin(uint64_t stream);
 /* Stop capturing and instantiate the graph; *graph receives an executable-graph handle. */
 int llmp_graph_end(uint64_t stream, uint64_t *graph);
@@ -247,10 +252,11 @@ int llmp_graph_destroy(uint64_t graph);
  * Over a Q8_0 cache each new row is quantised exactly as a decode append quantises it (under
  * the handle's contract) and attention reads every row dequantised (quant * block scale), as
  * the reference's sequential forwards over KVCache Mode.Q8_0 do.
- * NEOX partial RoPE (rotated dims < head_dim) is LLMP_ERR_UNSUPPORTED here.
+ * Partial RoPE (rotated dims < head_dim, NORMAL or NEOX pairs) is applied as in decode.
  * The handle keeps a workspace for the key tiles a call attends (bf16 hi/lo images of K and
  * V: about 9 bytes per key, KV head and head_dim element); a call that needs more than any
- * earlier call grows it (hipMalloc, so such a call cannot be captured in a graph). */
+ * earlier call grows it (hipFree + hipMalloc: such a call cannot be captured in a graph, and
+ * graphs captured before it must not be replayed after it). */
 int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                       uint64_t k, uint64_t v, uint64_t out, uint64_t stream);
 /* llmp_attn_prefill with an optional output gate (device fp32 [n_tokens][n_heads*head_dim],
@@ -262,6 +268,23 @@ int llmp_attn_prefill_ex(uint64_t handle, int layer, int pos0, int n_tokens, uin
  * pos0+n_tokens-1 (the source layer ran the same tokens first); nothing is appended. */
 int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0, int n_tokens,
                              uint64_t q, uint64_t gate, uint64_t out, uint64_t stream);
+
+/* Multi-token attention on fp32 projections: the contract of the reference's own prompt and
+ * speculative-verification path, which runs the tokens as sequential fp32 forwards
+ * (InferenceEngine.prefill, InferenceEngine.java:374-381; LLMEngine.forwardBatch,
+ * LLMEngine.java:1019-1033) and stores the fp32 k/v rows (Attention.java:284-367,
+ * KVCache.java:164-179).  As llmp_attn_prefill_ex, with
+ *   q:   device fp32 [n_tokens][n_heads*head_dim]   (4-byte aligned)
+ *   k,v: device fp32 [n_tokens][n_kv_heads*head_dim]
+ * The appended rows are bit-identical to n_tokens llmp_attn_decode calls on the same fp32
+ * inputs; attention runs on the same bf16 hi/lo MFMA path (K, V and P each split, so fp32
+ * rows keep ~2^-16 relative precision per product).  gate may be 0. */
+int llmp_attn_prefill_f32(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
+                          uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);
+/* llmp_attn_prefill_shared with an fp32 q (device fp32 [n_tokens][n_heads*head_dim]). */
+int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int pos0,
+                                 int n_tokens, uint64_t q, uint64_t gate, uint64_t out,
+                                 uint64_t stream);
 
 /* ---- the attention half of a layer around the attention core ------------------------------
  * Replaces CudaForwardPass.forwardAttentionPart steps 1-2b and 6-6c (CudaForwardPass.java:

@@ -82,6 +82,8 @@ SIGNATURES = {
     "llmp_attn_block": [_u64, _i32, _i32, _u64, _u64, _i32, _u64],
     "llmp_attn_decode_shared": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
     "llmp_attn_prefill_shared": [_u64, _i32, _i32, _i32, _i32, _u64, _u64, _u64, _u64],
+    "llmp_attn_prefill_f32": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64],
+    "llmp_attn_prefill_shared_f32": [_u64, _i32, _i32, _i32, _i32, _u64, _u64, _u64, _u64],
     "llmp_decode_plan": [_u64, _i32, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32),
                          C.POINTER(_i32), C.POINTER(_i32)],
     "llmp_graph_begin": [_u64],

@@ -10,6 +10,8 @@ namespace llmp {
 
 // Largest number of split-K partitions per KV head a decode call may use.
 constexpr int kMaxSplits = 1024;
+// Largest GQA group (query heads per KV head) any decode kernel ships.
+constexpr int kMaxGroup = 8;
 
 // Arguments of one split-K decode launch.  All pointers are device pointers.  The kernels
 // derive the step plan (window start, rows per split, effective splits, RoPE row) from the

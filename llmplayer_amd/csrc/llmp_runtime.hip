@@ -158,7 +158,11 @@ hipStream_t pick_stream(uint64_t s) {
     return s ? reinterpret_cast<hipStream_t>(s) : G().stream;
 }
 
+// The handle table is shared by every thread: lookups take the same lock as create and
+// destroy.  (Calls on one handle must not overlap; different handles may be used, created and
+// destroyed from different threads.)
 KvHandle* find_handle(uint64_t h) {
+    std::lock_guard<std::mutex> lk(G().mu);
     auto it = G().handles.find(h);
     return it == G().handles.end() ? nullptr : it->second.get();
 }
@@ -438,7 +442,7 @@ int llmp_shutdown(void) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (!g.init) return LLMP_OK;
     (void)hipSetDevice(g.device);
-    (void)hipStreamSynchronize(g.stream);
+    (void)hipDeviceSynchronize();
     for (auto& kv : g.handles) free_handle(kv.second.get());
     g.handles.clear();
     (void)hipStreamDestroy(g.stream);
@@ -619,6 +623,18 @@ int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int 
     LLMP_HIP_CHECK(e, "hipMalloc(kv pool)");
     kv->pool = static_cast<float*>(p);
     kv->layers.resize((size_t)n_layers);
+    // Split workspace for every layer configuration the handle can take (kMaxSplits slots per
+    // query head, at most kMaxGroup query heads per KV head), allocated once so that its
+    // address never changes under a captured graph.
+    const size_t slots = (size_t)kMaxSplits * (size_t)kMaxGroup * (size_t)n_kv_heads;
+    hipError_t ea = hipMalloc(&kv->part_o, slots * (size_t)head_dim * sizeof(float));
+    if (ea == hipSuccess) ea = hipMalloc(&kv->part_ml, slots * 2 * sizeof(float));
+    if (ea != hipSuccess) {
+        free_handle(kv.get());
+        return fail(ea == hipErrorOutOfMemory ? LLMP_ERR_OUT_OF_MEMORY : LLMP_ERR_HIP,
+                    "llmp_kv_create: split workspace: %s", hipGetErrorString(ea));
+    }
+    kv->part_slots = slots;
     hipError_t z = hipMemsetAsync(p, 0, bytes, G().stream);
     if (z == hipSuccess) z = hipStreamSynchronize(G().stream);
     if (z != hipSuccess) {
@@ -638,7 +654,9 @@ int llmp_kv_destroy(uint64_t handle) {
     auto it = G().handles.find(handle);
     if (it == G().handles.end())
         return fail(LLMP_ERR_BAD_HANDLE, "unknown KV handle %llu", (unsigned long long)handle);
-    (void)hipStreamSynchronize(G().stream);
+    // Work on the handle's memory may sit on any stream the caller used, not only the
+    // library's: wait for the whole device before freeing.
+    (void)hipDeviceSynchronize();
     free_handle(it->second.get());
     G().handles.erase(it);
     return LLMP_OK;
@@ -853,6 +871,9 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
     if ((qnorm_w == nullptr) != (knorm_w == nullptr))
         return fail(LLMP_ERR_INVALID_ARG, "layer %d: QK-norm needs both weights or neither", layer);
 
+    if ((size_t)kMaxSplits * (size_t)n_heads > kv->part_slots)   // guarded by group <= kMaxGroup
+        return fail(LLMP_ERR_UNSUPPORTED, "layer %d: %d query heads exceed the split workspace",
+                    layer, n_heads);
     LayerCfg& c = kv->layers[(size_t)layer];
     const size_t wbytes = (size_t)head_dim * sizeof(float);
     if (qnorm_w) {
@@ -864,18 +885,6 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
         if (c.d_qnw) (void)hipFree(c.d_qnw);
         if (c.d_knw) (void)hipFree(c.d_knw);
         c.d_qnw = c.d_knw = nullptr;
-    }
-    // Split workspace: kMaxSplits slots per query head.
-    const size_t slots = (size_t)kMaxSplits * (size_t)n_heads;
-    if (slots > kv->part_slots) {
-        if (kv->part_o) (void)hipFree(kv->part_o);
-        if (kv->part_ml) (void)hipFree(kv->part_ml);
-        kv->part_o = kv->part_ml = nullptr;
-        kv->part_slots = 0;
-        LLMP_HIP_CHECK(hipMalloc(&kv->part_o, slots * (size_t)head_dim * sizeof(float)),
-                       "hipMalloc(split outputs)");
-        LLMP_HIP_CHECK(hipMalloc(&kv->part_ml, slots * 2 * sizeof(float)), "hipMalloc(split stats)");
-        kv->part_slots = slots;
     }
     if (c.d_sinks && c.n_heads != n_heads) {   // sinks are per query head: a new count drops them
         (void)hipFree(c.d_sinks);
@@ -1284,21 +1293,28 @@ int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* 
 
 // ---- prefill attention -------------------------------------------------------------------------
 static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int n_tokens,
-                           uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
-                           uint64_t stream);
+                           bool in_f32, uint64_t q, uint64_t k, uint64_t v, uint64_t gate,
+                           uint64_t out, uint64_t stream);
 
 int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q, uint64_t k,
                       uint64_t v, uint64_t out, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, q, k, v, 0, out, stream);
+    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, false, q, k, v, 0, out, stream);
 }
 
 int llmp_attn_prefill_ex(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                          uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
-    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, q, k, v, gate, out, stream);
+    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, false, q, k, v, gate, out, stream);
+}
+
+int llmp_attn_prefill_f32(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
+                          uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, true, q, k, v, gate, out, stream);
 }
 
 int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0, int n_tokens,
@@ -1307,14 +1323,26 @@ int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0
     LLMP_GET_HANDLE(kv, handle);
     if (src_layer < 0)
         return fail(LLMP_ERR_OUT_OF_RANGE, "llmp_attn_prefill_shared: source layer %d", src_layer);
-    return enqueue_prefill(kv, layer, src_layer, pos0, n_tokens, q, 0, 0, gate, out, stream);
+    return enqueue_prefill(kv, layer, src_layer, pos0, n_tokens, false, q, 0, 0, gate, out, stream);
+}
+
+int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int pos0,
+                                 int n_tokens, uint64_t q, uint64_t gate, uint64_t out,
+                                 uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (src_layer < 0)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "llmp_attn_prefill_shared_f32: source layer %d",
+                    src_layer);
+    return enqueue_prefill(kv, layer, src_layer, pos0, n_tokens, true, q, 0, 0, gate, out, stream);
 }
 
 // src_layer >= 0: shared-KV layer (as in enqueue_decode): attention over src_layer's rows,
-// which must already hold the prompt's rows; no append.
+// which must already hold the prompt's rows; no append.  in_f32: q/k/v are fp32 (the CPU
+// path's projections), else bf16 bits.
 static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int n_tokens,
-                           uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
-                           uint64_t stream) {
+                           bool in_f32, uint64_t q, uint64_t k, uint64_t v, uint64_t gate,
+                           uint64_t out, uint64_t stream) {
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
     if (src_layer >= kv->n_layers)
@@ -1333,14 +1361,16 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
     if (prefill_tile_keys(kv->head_dim) <= 0)
         return fail(LLMP_ERR_UNSUPPORTED, "llmp_attn_prefill: head_dim %d (decode only)",
                     kv->head_dim);
-    if ((q | k | v) & 1 || out & 15 || gate & 3)
+    if ((q | k | v) & (in_f32 ? 3 : 1) || out & 15 || gate & 3)
         return fail(LLMP_ERR_INVALID_ARG,
-                    "llmp_attn_prefill: misaligned q/k/v (2 B), gate (4 B) or out (16 B)");
+                    "llmp_attn_prefill: misaligned q/k/v (%d B), gate (4 B) or out (16 B)",
+                    in_f32 ? 4 : 2);
     const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
     pk::PrefillArgs a{};
-    a.q = reinterpret_cast<const unsigned short*>(q);
-    a.k = reinterpret_cast<const unsigned short*>(k);
-    a.v = reinterpret_cast<const unsigned short*>(v);
+    a.q = reinterpret_cast<const void*>(q);
+    a.k = reinterpret_cast<const void*>(k);
+    a.v = reinterpret_cast<const void*>(v);
+    a.in_f32 = in_f32 ? 1 : 0;
     if (kv->q8()) {
         a.kq = kv->kq(kv_layer);
         a.ks = kv->ks(kv_layer);
@@ -1358,8 +1388,6 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
         const RopeTable& t = kv->rope[c.rope_sel];
         if (!t.d_cos)
             return fail(LLMP_ERR_INVALID_ARG, "layer %d selects a RoPE table never uploaded", layer);
-        if (c.rope_type == LLMP_ROPE_NEOX && 2 * t.half != D)
-            return fail(LLMP_ERR_UNSUPPORTED, "prefill: NEOX partial RoPE (%d of %d dims)", 2 * t.half, D);
         a.cos_t = t.d_cos;
         a.sin_t = t.d_sin;
         a.half_rope = t.half;
@@ -1459,9 +1487,12 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
 // ---- graph capture ---------------------------------------------------------------------------------
 int llmp_graph_begin(uint64_t stream) {
     if (int rc = ensure_init()) return rc;
-    for (auto& kv : G().handles)
-        if (kv.second->prof_on)
-            return fail(LLMP_ERR_INVALID_ARG, "llmp_graph_begin: turn profiling off before capturing");
+    {
+        std::lock_guard<std::mutex> lk(G().mu);
+        for (auto& kv : G().handles)
+            if (kv.second->prof_on)
+                return fail(LLMP_ERR_INVALID_ARG, "llmp_graph_begin: turn profiling off before capturing");
+    }
     LLMP_HIP_CHECK(hipStreamBeginCapture(pick_stream(stream), hipStreamCaptureModeThreadLocal),
                    "hipStreamBeginCapture");
     return LLMP_OK;

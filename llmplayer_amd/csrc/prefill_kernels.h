@@ -5,9 +5,9 @@
 // attends to rows [start(i), pos0+i] of a cache that already holds rows < pos0+i.  This path
 // computes the same result in three launches:
 //
-//  1. prefill_append_kernel: one workgroup per token widens its bf16 k/v to fp32, applies the
-//     exact QK-norm + RoPE of the decode path and writes the K/V rows (bit-identical to P
-//     appends by the CPU path).
+//  1. prefill_append_kernel: one workgroup per token takes its k/v (fp32, or bf16 widened to
+//     fp32), applies the exact QK-norm + RoPE of the decode path and writes the K/V rows
+//     (bit-identical to P appends by the CPU path).
 //  2. prefill_tile_kernel: once per (key tile, KV head), the bf16 hi/lo split of the tile's K
 //     rows and of its V rows (transposed) into a workspace image laid out like the LDS tile.
 //  3. prefill_attn2_kernel: causal flash attention on MFMA.  A workgroup owns one KV head and
@@ -48,9 +48,10 @@ template <int D>
 constexpr int tile_keys() { return D >= 256 ? 32 : 64; }
 
 struct PrefillArgs {
-    const unsigned short* q;  // bf16 bits [P][Hq*D]
-    const unsigned short* k;  // bf16 bits [P][Hkv*D]
-    const unsigned short* v;  // bf16 bits [P][Hkv*D]
+    const void* q;            // [P][Hq*D]: bf16 bits, or fp32 when in_f32
+    const void* k;            // [P][Hkv*D]
+    const void* v;            // [P][Hkv*D]
+    int in_f32;               // 1: q/k/v are fp32 projections (the CPU path's), 0: bf16 bits
     float* kc;                // fp32 cache: layer K plane [Hkv][max_seq][D]
     float* vc;
     signed char* kq;          // Q8_0 cache (when set): K quants [Hkv][max_seq][D]
@@ -81,6 +82,11 @@ struct PrefillArgs {
 __device__ __forceinline__ float bf16_to_f32(unsigned short b) {
     return __uint_as_float((unsigned)b << 16);
 }
+// Element i of a prompt input array: fp32 as is, or bf16 bits widened to fp32 (exact).
+__device__ __forceinline__ float in_val(const void* p, long long i, int f32) {
+    return f32 ? static_cast<const float*>(p)[i]
+               : bf16_to_f32(static_cast<const unsigned short*>(p)[i]);
+}
 // ---- 1. exact K/V append, one workgroup per token --------------------------------------------
 // Every input of the workgroup (its K and V rows, the RoPE row, the K-norm weights) is requested
 // in one pass and staged in LDS, so the append costs one memory round trip before its stores.
@@ -102,8 +108,8 @@ __global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
     const int pos = a.pos0 + i;
     const bool rope = a.cos_t != nullptr, qkn = a.qnw != nullptr;
     for (int e = tid; e < kvd; e += NTHR) {
-        s_k[e] = bf16_to_f32(a.k[(long long)i * kvd + e]);
-        s_v[e] = bf16_to_f32(a.v[(long long)i * kvd + e]);
+        s_k[e] = in_val(a.k, (long long)i * kvd + e, a.in_f32);
+        s_v[e] = in_val(a.v, (long long)i * kvd + e, a.in_f32);
     }
     if (rope) {
         for (int e = tid; e < a.half_rope; e += NTHR) {
@@ -325,18 +331,31 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
 
 // ---- 3. Double-buffered MFMA attention ------------------------------------------------------
 // Query fragment of one lane for MFMA B operands: dims 32*s + 8*grp + j of query token qi
-// (clamped into range), head hq, widened from bf16, QK-normed, rotated, scaled, then split.
+// (clamped into range), head hq, as fp32 (or widened from bf16), QK-normed, rotated, scaled,
+// then split.  NEOX partners (d, d + half) usually sit in other lanes, so each element reads
+// its partner from the input and normalises it exactly as the partner's own lane does; any
+// rotated width (partial RoPE) works the same way.
 template <int D>
 __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int hq, int qpos,
                                                int grp, bf16x8 (&qh)[D / 32],
                                                bf16x8 (&ql)[D / 32]) {
     constexpr int KS = D / 32;
     float qf[KS][8];
-    const unsigned short* qp = a.q + (long long)qi * a.Hq * D + (long long)hq * D;
+    const long long q0 = (long long)qi * a.Hq * D + (long long)hq * D;
+    if (a.in_f32) {
+        const float* qp = static_cast<const float*>(a.q) + q0;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+        for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) qf[s][j] = bf16_to_f32(qp[32 * s + 8 * grp + j]);
+            for (int j = 0; j < 8; ++j) qf[s][j] = qp[32 * s + 8 * grp + j];
+    } else {
+        const unsigned short* qp = static_cast<const unsigned short*>(a.q) + q0;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qf[s][j] = bf16_to_f32(qp[32 * s + 8 * grp + j]);
+    }
+    float r = 1.0f;
     if (a.qnw != nullptr) {
         float ss = 0.0f;
 #pragma unroll
@@ -345,7 +364,7 @@ __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int
             for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(qf[s][j], qf[s][j], ss);
         ss = ss + __shfl_xor(ss, 16);
         ss = ss + __shfl_xor(ss, 32);
-        const float r = 1.0f / sqrtf(ss / (float)D + a.eps);
+        r = 1.0f / sqrtf(ss / (float)D + a.eps);
 #pragma unroll
         for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -354,30 +373,36 @@ __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int
     if (a.cos_t != nullptr) {
         const float* cr = a.cos_t + (long long)qpos * a.half_rope;
         const float* sr = a.sin_t + (long long)qpos * a.half_rope;
+        const int half = a.half_rope;
         if (a.rope_type == 0) {
 #pragma unroll
             for (int s = 0; s < KS; ++s)
 #pragma unroll
                 for (int j = 0; j < 8; j += 2) {
                     const int i = (32 * s + 8 * grp + j) / 2;
-                    const bool rot = i < a.half_rope;
+                    const bool rot = i < half;
                     const float c = cr[rot ? i : 0], sn = sr[rot ? i : 0];
                     const float v0 = qf[s][j], v1 = qf[s][j + 1];
                     const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
                     qf[s][j] = rot ? t0 - t1 : v0;
                     qf[s][j + 1] = rot ? t2 + t3 : v1;
                 }
-        } else {  // NEOX with half_rope == D/2: partner dims sit KS/2 k-steps apart
+        } else {  // NEOX: pairs (i, i + half) for i < half; dims >= 2*half keep their values
 #pragma unroll
-            for (int s = 0; s < KS / 2; ++s)
+            for (int s = 0; s < KS; ++s)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const int i = 32 * s + 8 * grp + j;
-                    const float c = cr[i], sn = sr[i];
-                    const float v0 = qf[s][j], v1 = qf[s + KS / 2][j];
-                    const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
-                    qf[s][j] = t0 - t1;
-                    qf[s + KS / 2][j] = t2 + t3;
+                    const int d = 32 * s + 8 * grp + j;
+                    if (d < 2 * half) {
+                        const bool first = d < half;
+                        const int i = first ? d : d - half, pd = first ? d + half : d - half;
+                        float pv = in_val(a.q, q0 + pd, a.in_f32);
+                        if (a.qnw != nullptr) pv = (pv * r) * a.qnw[pd];
+                        const float v0 = first ? qf[s][j] : pv, v1 = first ? pv : qf[s][j];
+                        const float c = cr[i], sn = sr[i];
+                        const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
+                        qf[s][j] = first ? t0 - t1 : t2 + t3;
+                    }
                 }
         }
     }

@@ -155,6 +155,24 @@ def from_bf16(b: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def prompt_input(x: np.ndarray, width: int, what: str):
+    """A multi-token input array as the library takes it: fp32 projections (the CPU path's own
+    values) or bf16 bit patterns (uint16).  Returns (contiguous [P, width] array, is_fp32).
+    Any other dtype is rejected rather than converted, so a caller never hands the kernels
+    reinterpreted bits."""
+    a = np.asarray(x)
+    if a.dtype == np.float32:
+        f32 = True
+    elif a.dtype == np.uint16:
+        f32 = False
+    else:
+        raise TypeError(f"{what}: dtype {a.dtype} (expected float32 projections or uint16 bf16 bits)")
+    a = np.ascontiguousarray(a)
+    if a.size % width:
+        raise ValueError(f"{what}: {a.size} values are not rows of {width}")
+    return a.reshape(-1, width), f32
+
+
 def rope_table(rope_dim: int, max_seq: int, theta: float, linear_freq_scale: float = 1.0,
                freq_factors: Optional[np.ndarray] = None):
     """cos/sin tables [max_seq][rope_dim/2] built as the RoPE constructor builds them
@@ -492,25 +510,30 @@ class HipForwardPass:
         self.forwardAttentionPart(layerIdx, position, splits, gated=gate is not None)
         state.xb2[:] = self.downloadXb2()
 
-    def prefill(self, layerIdx: int, pos0: int, q_bf16: np.ndarray, k_bf16: np.ndarray,
-                v_bf16: np.ndarray, gate: Optional[np.ndarray] = None) -> np.ndarray:
-        """Attention for a prompt of P tokens at positions pos0..pos0+P-1 in one call (the
-        reference runs P sequential forwards, InferenceEngine.java:374-381).  Inputs are bf16
-        bit patterns (uint16) [P, Hq*D] / [P, kvDim]; returns fp32 [P, Hq*D].  `gate`
-        ([P, Hq*D] fp32) applies the Qwen3.5 output gate."""
+    def prefill(self, layerIdx: int, pos0: int, q: np.ndarray, k: np.ndarray,
+                v: np.ndarray, gate: Optional[np.ndarray] = None) -> np.ndarray:
+        """Attention for P tokens at positions pos0..pos0+P-1 in one call (a prompt, or the
+        draft tokens of a speculative verification; the reference runs P sequential forwards,
+        InferenceEngine.java:374-381, LLMEngine.java:1019-1033).  Inputs [P, Hq*D] /
+        [P, kvDim] are fp32 projections (the CPU path's contract: rows bit-identical to P
+        decode appends) or bf16 bit patterns (uint16); all three share one dtype.  Returns
+        fp32 [P, Hq*D].  `gate` ([P, Hq*D] fp32) applies the Qwen3.5 output gate."""
         c = self.config
-        q16 = np.ascontiguousarray(q_bf16, np.uint16).reshape(-1, c.q_dim)
-        k16 = np.ascontiguousarray(k_bf16, np.uint16).reshape(-1, c.kv_dim)
-        v16 = np.ascontiguousarray(v_bf16, np.uint16).reshape(-1, c.kv_dim)
-        P = q16.shape[0]
-        assert k16.shape[0] == P and v16.shape[0] == P
-        bq, bk, bv = DeviceBuffer(q16.nbytes), DeviceBuffer(k16.nbytes), DeviceBuffer(v16.nbytes)
+        qa, f32 = prompt_input(q, c.q_dim, "prefill q")
+        ka, kf = prompt_input(k, c.kv_dim, "prefill k")
+        va, vf = prompt_input(v, c.kv_dim, "prefill v")
+        if not (f32 == kf == vf):
+            raise TypeError("prefill: q, k and v must share one dtype")
+        P = qa.shape[0]
+        if ka.shape[0] != P or va.shape[0] != P:
+            raise ValueError(f"prefill: {P} query rows but {ka.shape[0]} / {va.shape[0]} k / v rows")
+        bq, bk, bv = DeviceBuffer(qa.nbytes), DeviceBuffer(ka.nbytes), DeviceBuffer(va.nbytes)
         bo = DeviceBuffer(P * c.q_dim * 4)
         bufs = [bq, bk, bv, bo]
         try:
-            bq.upload(q16)
-            bk.upload(k16)
-            bv.upload(v16)
+            bq.upload(qa)
+            bk.upload(ka)
+            bv.upload(va)
             gptr = 0
             if gate is not None:
                 g = np.ascontiguousarray(gate, np.float32).reshape(P, c.q_dim)
@@ -518,8 +541,8 @@ class HipForwardPass:
                 bufs.append(bg)
                 bg.upload(g)
                 gptr = bg.ptr
-            call("llmp_attn_prefill_ex", self.kv.handle, layerIdx, pos0, P, bq.ptr, bk.ptr,
-                 bv.ptr, gptr, bo.ptr, 0)
+            call("llmp_attn_prefill_f32" if f32 else "llmp_attn_prefill_ex", self.kv.handle,
+                 layerIdx, pos0, P, bq.ptr, bk.ptr, bv.ptr, gptr, bo.ptr, 0)
             return bo.download(np.float32, P * c.q_dim).reshape(P, c.q_dim)
         finally:
             for b in bufs:
@@ -682,34 +705,38 @@ class Gemma4HipForwardPass:
                  self.gpuQ.ptr, 0, self.gpuXb2.ptr, splits, 0)
         state.xb2[:qd] = self.gpuXb2.download(np.float32, qd)
 
-    def prefill(self, layer: int, pos0: int, q_bf16: np.ndarray,
-                k_bf16: Optional[np.ndarray] = None,
-                v_bf16: Optional[np.ndarray] = None) -> np.ndarray:
-        """P tokens of one layer in one call (bf16 [P, Hq*D] / [P, Hkv*D]; k, v unused for
-        shared layers).  Sliding-window layers only: the 512-dim full-attention heads have no
-        prefill kernel (LLMP_ERR_UNSUPPORTED); the reference runs a prompt token by token."""
+    def prefill(self, layer: int, pos0: int, q: np.ndarray,
+                k: Optional[np.ndarray] = None,
+                v: Optional[np.ndarray] = None) -> np.ndarray:
+        """P tokens of one layer in one call ([P, Hq*D] / [P, Hkv*D], fp32 projections or
+        bf16 bits (uint16), one dtype for all; k, v unused for shared layers).  Sliding-window
+        layers only: the 512-dim full-attention heads have no prefill kernel
+        (LLMP_ERR_UNSUPPORTED); the reference runs a prompt token by token."""
         c = self.config
         t = self.isSwaLayer(layer)
         D = self.head_size(t)
         qd, kvd = c.head_count * D, c.head_count_kv * D
-        q16 = np.ascontiguousarray(q_bf16, np.uint16).reshape(-1, qd)
-        P = q16.shape[0]
-        bufs = [DeviceBuffer(q16.nbytes), DeviceBuffer(P * qd * 4)]
+        qa, f32 = prompt_input(q, qd, "prefill q")
+        P = qa.shape[0]
+        bufs = [DeviceBuffer(qa.nbytes), DeviceBuffer(P * qd * 4)]
         try:
-            bufs[0].upload(q16)
+            bufs[0].upload(qa)
             h = self.kv[t].handle
             if self.hasOwnKv(layer):
-                k16 = np.ascontiguousarray(k_bf16, np.uint16).reshape(P, kvd)
-                v16 = np.ascontiguousarray(v_bf16, np.uint16).reshape(P, kvd)
-                bk, bv = DeviceBuffer(k16.nbytes), DeviceBuffer(v16.nbytes)
+                ka, kf = prompt_input(k, kvd, "prefill k")
+                va, vf = prompt_input(v, kvd, "prefill v")
+                if not (f32 == kf == vf) or ka.shape[0] != P or va.shape[0] != P:
+                    raise TypeError("prefill: q, k and v must share one dtype and row count")
+                bk, bv = DeviceBuffer(ka.nbytes), DeviceBuffer(va.nbytes)
                 bufs += [bk, bv]
-                bk.upload(k16)
-                bv.upload(v16)
-                call("llmp_attn_prefill_ex", h, self.slot[layer], pos0, P, bufs[0].ptr, bk.ptr,
-                     bv.ptr, 0, bufs[1].ptr, 0)
+                bk.upload(ka)
+                bv.upload(va)
+                call("llmp_attn_prefill_f32" if f32 else "llmp_attn_prefill_ex", h,
+                     self.slot[layer], pos0, P, bufs[0].ptr, bk.ptr, bv.ptr, 0, bufs[1].ptr, 0)
             else:
-                call("llmp_attn_prefill_shared", h, self.slot[layer],
-                     self.slot[self.kvSourceLayer(layer)], pos0, P, bufs[0].ptr, 0, bufs[1].ptr, 0)
+                call("llmp_attn_prefill_shared_f32" if f32 else "llmp_attn_prefill_shared", h,
+                     self.slot[layer], self.slot[self.kvSourceLayer(layer)], pos0, P,
+                     bufs[0].ptr, 0, bufs[1].ptr, 0)
             return bufs[1].download(np.float32, P * qd).reshape(P, qd)
         finally:
             for b in bufs:

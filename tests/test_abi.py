@@ -116,3 +116,17 @@ def test_global_layer_and_rope_type_host_logic_match_oracle():
             assert hfp.is_global_layer(arch, layer) == orc.is_global_layer(oarch, layer)
     assert hfp.rope_type_for("llama") == 0 and hfp.rope_type_for("qwen3") == 2
     assert hfp.rope_type_for("gemma3") == 0
+
+
+def test_prompt_input_takes_fp32_or_bf16_bits_and_rejects_the_rest():
+    """Multi-token inputs are either fp32 projections or bf16 bit patterns; anything else
+    (float64, int arrays) raises instead of being reinterpreted."""
+    a, f32 = hfp.prompt_input(np.zeros((3, 8), np.float32), 8, "q")
+    assert f32 and a.shape == (3, 8) and a.dtype == np.float32
+    b, f32 = hfp.prompt_input(hfp.to_bf16(np.ones(16, np.float32)), 8, "q")
+    assert not f32 and b.shape == (2, 8) and b.dtype == np.uint16
+    for bad in (np.zeros(8, np.float64), np.zeros(8, np.int32), np.zeros(8, np.float16)):
+        with pytest.raises(TypeError):
+            hfp.prompt_input(bad, 8, "q")
+    with pytest.raises(ValueError):
+        hfp.prompt_input(np.zeros(9, np.float32), 8, "q")
