@@ -281,6 +281,22 @@ int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0
  * rows keep ~2^-16 relative precision per product).  gate may be 0. */
 int llmp_attn_prefill_f32(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                           uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);
+/* No counterpart in the reference.  For callers that cannot allocate device memory: code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc.  llmp_attn_prefill_f32
+ * with its workspace (the key-tile images, or the split-K partials of a short chunk after a
+ * long prefix) in a static device array of LLMP_PREFILL_STATIC_BYTES that each GPU holds until
+ * the process ends, instead of the handle's grown workspace: the call allocates and frees
+ * nothing (and records no profiling events).  A call whose workspace would exceed the array
+ * fails with LLMP_ERR_INVALID_ARG: images take Hkv * ceil(keys/TK) * tile bytes (2048 tokens at
+ * head_dim 64 with 8 KV heads: 9.2 MB; at head_dim 128: 17.8 MB), partials ksplit * n_tokens *
+ * n_heads * (head_dim + 2) * 4 bytes (16 tokens after a 32k prefix at 24/8/128: 12.8 MB).
+ * Every call on a GPU shares its one array, which keeps the last call's contents (every byte a
+ * call reads it first writes): calls that overlap in time on one GPU (other streams, other
+ * threads) race. */
+#define LLMP_PREFILL_STATIC_BYTES (32u << 20)
+int llmp_attn_prefill_f32_static(uint64_t handle, int layer, int pos0, int n_tokens,
+                                 uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
+                                 uint64_t stream);
 /* llmp_attn_prefill_shared with an fp32 q (device fp32 [n_tokens][n_heads*head_dim]). */
 int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int pos0,
                                  int n_tokens, uint64_t q, uint64_t gate, uint64_t out,

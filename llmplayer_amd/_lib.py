@@ -83,6 +83,7 @@ SIGNATURES = {
     "llmp_attn_decode_shared": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
     "llmp_attn_prefill_shared": [_u64, _i32, _i32, _i32, _i32, _u64, _u64, _u64, _u64],
     "llmp_attn_prefill_f32": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64],
+    "llmp_attn_prefill_f32_static": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64],
     "llmp_attn_prefill_shared_f32": [_u64, _i32, _i32, _i32, _i32, _u64, _u64, _u64, _u64],
     "llmp_decode_plan": [_u64, _i32, _i32, _i32, C.POINTER(_i32), C.POINTER(_i32),
                          C.POINTER(_i32), C.POINTER(_i32)],

@@ -129,11 +129,19 @@ struct KvHandle {
     }
 };
 
+// Workspace of llmp_attn_prefill_f32_static, the entry point that allocates nothing: a
+// file-scope device array each GPU holds from module load to process end.  Host code never
+// uses its name as an address (on the host it is only a stand-in symbol); llmp_init resolves
+// the device address once with hipGetSymbolAddress and every use goes through
+// Global::scratch.
+static __device__ __align__(256) unsigned char scratch[LLMP_PREFILL_STATIC_BYTES];
+
 struct Global {
     std::mutex mu;
     bool init = false;
     int device = -1;
     int n_cu = 0;
+    void* scratch = nullptr;   // device address of `scratch` on `device` (llmp_init)
     hipStream_t stream = nullptr;
     std::string arch;
     uint64_t next_handle = 1;
@@ -427,8 +435,12 @@ int llmp_init(int device) {
     if (arch.rfind("gfx950", 0) != 0)
         return fail(LLMP_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
                     device, arch.c_str());
+    void* sp = nullptr;
+    LLMP_HIP_CHECK(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!sp) return fail(LLMP_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
     hipStream_t s = nullptr;
     LLMP_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    g.scratch = sp;
     g.device = device;
     g.n_cu = prop.multiProcessorCount;
     g.arch = arch;
@@ -447,6 +459,7 @@ int llmp_shutdown(void) {
     g.handles.clear();
     (void)hipStreamDestroy(g.stream);
     g.stream = nullptr;
+    g.scratch = nullptr;
     g.init = false;
     return LLMP_OK;
 }
@@ -1294,7 +1307,7 @@ int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int* 
 // ---- prefill attention -------------------------------------------------------------------------
 static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int n_tokens,
                            bool in_f32, uint64_t q, uint64_t k, uint64_t v, uint64_t gate,
-                           uint64_t out, uint64_t stream);
+                           uint64_t out, uint64_t stream, bool use_static = false);
 
 int llmp_attn_prefill(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q, uint64_t k,
                       uint64_t v, uint64_t out, uint64_t stream) {
@@ -1315,6 +1328,14 @@ int llmp_attn_prefill_f32(uint64_t handle, int layer, int pos0, int n_tokens, ui
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
     return enqueue_prefill(kv, layer, -1, pos0, n_tokens, true, q, k, v, gate, out, stream);
+}
+
+int llmp_attn_prefill_f32_static(uint64_t handle, int layer, int pos0, int n_tokens,
+                                 uint64_t q, uint64_t k, uint64_t v, uint64_t gate, uint64_t out,
+                                 uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    return enqueue_prefill(kv, layer, -1, pos0, n_tokens, true, q, k, v, gate, out, stream, true);
 }
 
 int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0, int n_tokens,
@@ -1342,7 +1363,7 @@ int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int 
 // path's projections), else bf16 bits.
 static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int n_tokens,
                            bool in_f32, uint64_t q, uint64_t k, uint64_t v, uint64_t gate,
-                           uint64_t out, uint64_t stream) {
+                           uint64_t out, uint64_t stream, bool use_static) {
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
     if (src_layer >= kv->n_layers)
@@ -1425,6 +1446,36 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
     const int ksplit = prefill_key_splits(n_tokens, pos0, a.window, Hkv, group, D, G().n_cu);
     const size_t ws_bytes =
         ksplit == 1 ? (size_t)Hkv * (size_t)n_tiles * prefill_tile_bytes(D) : 0;
+    const size_t part_bytes =
+        ksplit > 1
+            ? (size_t)ksplit * (size_t)n_tokens * (size_t)c.n_heads * (size_t)(D + 2) * sizeof(float)
+            : 0;
+    void* ws = nullptr;
+    if (use_static) {
+        // The whole workspace (tile images, or split-K partials) in the static array: no
+        // allocation, no profiling events.
+        const size_t need = ksplit > 1 ? part_bytes : ws_bytes;
+        if (need > (size_t)LLMP_PREFILL_STATIC_BYTES)
+            return fail(LLMP_ERR_INVALID_ARG,
+                        "llmp_attn_prefill_f32_static: the call needs %zu bytes of workspace; the "
+                        "static scratch holds %u (fewer tokens per call, or llmp_attn_prefill_f32)",
+                        need, (unsigned)LLMP_PREFILL_STATIC_BYTES);
+        void* sp = G().scratch;
+        if (!sp) return fail(LLMP_ERR_NOT_INIT, "llmp_attn_prefill_f32_static: no scratch address");
+        if (ksplit > 1) {
+            a.part_o = static_cast<float*>(sp);
+            a.part_ml = a.part_o + (size_t)ksplit * n_tokens * c.n_heads * D;
+        } else {
+            ws = sp;
+        }
+        if (!shared) LLMP_HIP_CHECK(launch_prefill_append(a, D, st), "prefill append launch");
+        if (ksplit == 1)
+            LLMP_HIP_CHECK(launch_prefill_tiles(a, D, ws, tile0, n_tiles, pos0 + n_tokens, st),
+                           "prefill tile launch");
+        LLMP_HIP_CHECK(launch_prefill_attn(a, D, group, ws, tile0, n_tiles, G().n_cu, ksplit, st),
+                       "prefill attention launch");
+        return LLMP_OK;
+    }
     if (ws_bytes > kv->prefill_ws_bytes) {
         if (kv->prefill_ws) {
             LLMP_HIP_CHECK(hipStreamSynchronize(st), "hipStreamSynchronize");
@@ -1440,8 +1491,6 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
     }
     // Key splits (short prompts after a long prefix) and their partials buffer.
     if (ksplit > 1) {
-        const size_t part_bytes =
-            (size_t)ksplit * (size_t)n_tokens * (size_t)c.n_heads * (size_t)(D + 2) * sizeof(float);
         if (part_bytes > kv->prefill_part_bytes) {
             if (kv->prefill_part) {
                 LLMP_HIP_CHECK(hipStreamSynchronize(st), "hipStreamSynchronize");
