@@ -7,16 +7,19 @@ namespace llmp {
 namespace {
 
 // Per-shape tuning (measured on MI355X at the BASELINE shapes): elements of a K/V row per
-// lane (EPL), rows per lane-group per loop trip (U), non-temporal KV loads.  The number of
-// waves per workgroup is chosen per call.
+// lane (EPL), rows per lane-group per loop trip (U; the loop keeps two trips in registers, the
+// one consumed and the one prefetched), non-temporal KV loads.  The number of waves per
+// workgroup is chosen per call.
 struct Tune {
     int epl, unroll;
     bool nt;
 };
 constexpr Tune pick(int D, int G) {
-    // head_dim 512: 8 elements per lane, so a row spans the whole wave (LPR 64).
-    return Tune{D == 512 ? 8 : ((D == 256 || (G > 4 && D / 8 > 16)) ? 16 : 8), (G > 4) ? 1 : 2,
-                true};
+    // head_dim 512: 8 elements per lane, so a row spans the whole wave (LPR 64).  head_dim 256
+    // (16 elements per lane) and groups above 4 take one row per trip: two trips of two rows
+    // would not fit the register file next to the G*EPL query and output values.
+    return Tune{D == 512 ? 8 : ((D == 256 || (G > 4 && D / 8 > 16)) ? 16 : 8),
+                (G > 4 || D == 256) ? 1 : 2, true};
 }
 
 // The kernel instance for one shape, and the waves per workgroup it runs with.

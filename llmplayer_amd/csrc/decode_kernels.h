@@ -437,9 +437,39 @@ __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* 
 }
 
 // Rotation of the lane's own q slice in registers (no QK-norm; NORMAL pairs sit inside one
-// 16-byte chunk, NEOX pairs (i, i+D/2) in chunks c and c+C4/2 of the same lane).
+// 16-byte chunk, NEOX pairs (i, i+D/2) in chunks c and c+C4/2 of the same lane).  The lane's
+// EPL/2 cos/sin factors are loaded first (rope_lane_factors) so that their loads are in flight
+// with the other prologue loads, then applied (rope_registers).
+template <int D, int EPL, bool CONTIG = false>
+__device__ __forceinline__ void rope_lane_factors(float (&cs)[EPL / 2], float (&sn)[EPL / 2],
+                                                  int j, const HeadPrep& a) {
+    using F = Frag<D, EPL, CONTIG>;
+    const int half = a.half_rope;
+    if (a.rope_type == 0) {
+#pragma unroll
+        for (int c = 0; c < F::C4; ++c)
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int i = F::dim(j, 4 * c + 2 * p) / 2;
+                const int ii = i < half ? i : 0;   // pairs at or beyond half_rope keep their values
+                cs[2 * c + p] = a.cos_row[ii];
+                sn[2 * c + p] = a.sin_row[ii];
+            }
+    } else if constexpr (!CONTIG) {
+#pragma unroll
+        for (int c = 0; c < F::C4 / 2; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = c * F::LPR * 4 + j * 4 + e;   // < D/2 = half
+                cs[4 * c + e] = a.cos_row[i];
+                sn[4 * c + e] = a.sin_row[i];
+            }
+    }
+}
+
 template <int D, int G, int EPL, bool CONTIG = false>
-__device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const HeadPrep& a) {
+__device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const float (&cs)[EPL / 2],
+                                               const float (&sn)[EPL / 2], const HeadPrep& a) {
     using F = Frag<D, EPL, CONTIG>;
     const int half = a.half_rope;
     if (a.rope_type == 0) {
@@ -447,15 +477,12 @@ __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const
         for (int c = 0; c < F::C4; ++c) {
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                // Pairs at or beyond half_rope (partial RoPE) keep their values.
-                const int i = F::dim(j, 4 * c + 2 * p) / 2;
-                const bool rot = i < half;
-                const int ii = rot ? i : 0;
-                const float cs = a.cos_row[ii], sn = a.sin_row[ii];
+                const bool rot = F::dim(j, 4 * c + 2 * p) / 2 < half;
+                const float cv = cs[2 * c + p], sv = sn[2 * c + p];
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
                     const float v0 = qr[h][4 * c + 2 * p], v1 = qr[h][4 * c + 2 * p + 1];
-                    const float t0 = v0 * cs, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * cs;
+                    const float t0 = v0 * cv, t1 = v1 * sv, t2 = v0 * sv, t3 = v1 * cv;
                     const float r0 = t0 - t1, r1 = t2 + t3;
                     qr[h][4 * c + 2 * p] = rot ? r0 : v0;
                     qr[h][4 * c + 2 * p + 1] = rot ? r1 : v1;
@@ -467,12 +494,11 @@ __device__ __forceinline__ void rope_registers(float (&qr)[G][EPL], int j, const
         for (int c = 0; c < F::C4 / 2; ++c) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int i = c * F::LPR * 4 + j * 4 + e;  // < D/2 = half
-                const float cs = a.cos_row[i], sn = a.sin_row[i];
+                const float cv = cs[4 * c + e], sv = sn[4 * c + e];
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
                     const float v0 = qr[h][4 * c + e], v1 = qr[h][4 * (c + F::C4 / 2) + e];
-                    const float t0 = v0 * cs, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * cs;
+                    const float t0 = v0 * cv, t1 = v1 * sv, t2 = v0 * sv, t3 = v1 * cv;
                     qr[h][4 * c + e] = t0 - t1;
                     qr[h][4 * (c + F::C4 / 2) + e] = t2 + t3;
                 }
@@ -524,20 +550,85 @@ __device__ void append_row_q8(const DecodeArgs& a, int kvh, int pos, const float
     }
 }
 
+// Cached rows of one loop trip of a lane group: rows base + u*RPW + grp, u < U (masked past
+// cache_end, with the address clamped into the cache), as 16-byte fp32 chunks, or as 16 quants
+// and their block scale (Q8_0).
+template <int D, int EPL, int U, bool Q8>
+struct TripRows {
+    static constexpr int C4 = EPL / 4;
+    float4 k[Q8 ? 1 : U][C4], v[Q8 ? 1 : U][C4];
+    uint4 kw[Q8 ? U : 1], vw[Q8 ? U : 1];
+    float ksc[Q8 ? U : 1], vsc[Q8 ? U : 1];
+    bool valid[U];
+};
+
+template <int D, int EPL, int U, bool NT, bool Q8>
+__device__ __forceinline__ void load_trip(TripRows<D, EPL, U, Q8>& r, const DecodeArgs& a,
+                                          int kvh, int base, int cache_end, int grp, int j) {
+    using F = Frag<D, EPL, Q8>;
+    const int last = cache_end > 0 ? cache_end - 1 : 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int t = base + u * F::RPW + grp;
+        r.valid[u] = t < cache_end;
+        const long long tt = r.valid[u] ? t : last;
+        if constexpr (!Q8) {
+            const float4* kp =
+                reinterpret_cast<const float4*>(a.kc + (long long)kvh * a.head_stride + tt * D) + j;
+            const float4* vp =
+                reinterpret_cast<const float4*>(a.vc + (long long)kvh * a.head_stride + tt * D) + j;
+#pragma unroll
+            for (int c = 0; c < F::C4; ++c) r.k[u][c] = load4<NT>(kp + c * F::LPR);
+#pragma unroll
+            for (int c = 0; c < F::C4; ++c) r.v[u][c] = load4<NT>(vp + c * F::LPR);
+        } else {
+            const long long h = (long long)kvh * a.head_stride, hs = (long long)kvh * (a.head_stride / 32);
+            r.kw[u] = load_u4<NT>(reinterpret_cast<const uint4*>(a.kq + h + tt * D) + j);
+            r.vw[u] = load_u4<NT>(reinterpret_cast<const uint4*>(a.vq + h + tt * D) + j);
+            r.ksc[u] = a.ks[hs + tt * (D / 32) + (j >> 1)];
+            r.vsc[u] = a.vs[hs + tt * (D / 32) + (j >> 1)];
+        }
+    }
+}
+
+template <int D, int G, int EPL, int U, bool Q8, bool LAZY>
+__device__ __forceinline__ void consume_trip(const TripRows<D, EPL, U, Q8>& r,
+                                             const float (&qr)[G][EPL], float (&m)[G],
+                                             float (&l)[G], float (&o)[G][EPL],
+                                             const DecodeArgs& a) {
+    if constexpr (!Q8) {
+        accumulate_rows<D, G, EPL, U, LAZY>(qr, r.k, r.v, r.valid, m, l, o, a);
+    } else {
+        float kq[U][16], vq[U][16];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            unpack_q8(r.kw[u], kq[u]);
+            unpack_q8(r.vw[u], vq[u]);
+        }
+        accumulate_rows_q8<D, G, U, LAZY>(qr, kq, r.ksc, vq, r.vsc, r.valid, m, l, o, a);
+    }
+}
+
 template <int D, int G, int EPL, int U, int WAVES, bool NT, bool Q8 = false, bool LAZY = Q8>
 __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) {
     static_assert(!Q8 || EPL == 16, "Q8_0 rows are read 16 quants per lane");
     using F = Frag<D, EPL, Q8>;
+    using Trip = TripRows<D, EPL, U, Q8>;
     constexpr int NTHR = WAVES * 64;
     constexpr int LPR = F::LPR, RPW = F::RPW, C4 = F::C4;
     constexpr int ROWS_WAVE = U * RPW;
     constexpr int ROWS_BLOCK = WAVES * ROWS_WAVE;
+    constexpr int WPT = (D + NTHR - 1) / NTHR;   // per-thread elements of a D-vector
 
     // s_x: G query heads then the group's K head (post norm and RoPE).
     __shared__ float s_x[(G + 1) * D];
     __shared__ float s_v[D];
     __shared__ float s_acc[(G + 1) * 8];
     __shared__ float s_r[G + 1];
+    __shared__ float s_cs[D / 2], s_sn[D / 2], s_qw[D], s_kw[D];
+    __shared__ float s_vr;
+    __shared__ __align__(16) signed char s_kq[Q8 ? D : 16], s_vq[Q8 ? D : 16];
+    __shared__ float s_ks[D / 32], s_vs[D / 32], s_inv[D / 32];
     __shared__ float s_m[WAVES * G];
     __shared__ float s_l[WAVES * G];
     __shared__ float s_o[WAVES * G * D];
@@ -559,36 +650,123 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     // (row `pos` is then already cached and streamed like the others).
     const bool has_pos = (row_end == pos + 1) && a.no_append == 0;
     const int cache_end = has_pos ? pos : row_end;
-
-    // 1. Query slice of this lane, pre-scaled (log2 domain unless soft-capping).  Without
-    //    QK-norm and with RoPE pairs inside a lane, q is loaded and rotated in registers, with
-    //    no barrier ahead of the first KV loads; otherwise it goes through the exact LDS path.
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int grp = lane / LPR, j = lane - grp * LPR;
-    float qr[G][EPL];
+
+    // 1. Every load of the prologue is issued before any of them is waited for, then the
+    //    wave's first trip of cached rows, so the prep's memory latency overlaps the stream's:
+    //    the lane's q slice (in the streaming layout), its RoPE factors (register path), the
+    //    RoPE row and norm weights for the LDS prep, and the new k/v row (appending split).
+    //    Without QK-norm and with RoPE pairs inside a lane, q is rotated in registers;
+    //    otherwise it is prepared in LDS with the exact QK-norm order.
+    const bool rope = a.cos_t != nullptr, qkn = a.qnw != nullptr;
     const bool pairs_in_lane = a.rope_type == 0 || (!Q8 && 2 * a.half_rope == D);
-    const bool reg_prologue = a.qnw == nullptr && (a.cos_t == nullptr || pairs_in_lane);
-    if (reg_prologue) {
+    const bool reg_prologue = !qkn && (!rope || pairs_in_lane);
+    const bool lds_prep = !reg_prologue || has_pos;
+    float qr[G][EPL];
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+    for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int c = 0; c < C4; ++c) {
-                const float4 x = *reinterpret_cast<const float4*>(a.q + (h0 + h) * D + F::dim(j, 4 * c));
-                qr[h][4 * c + 0] = x.x;
-                qr[h][4 * c + 1] = x.y;
-                qr[h][4 * c + 2] = x.z;
-                qr[h][4 * c + 3] = x.w;
-            }
-        if (hp.cos_row != nullptr) rope_registers<D, G, EPL, Q8>(qr, j, hp);
-    } else {
-        for (int i = tid; i < G * D; i += NTHR) s_x[i] = a.q[h0 * D + i];
-        __syncthreads();
-        prep_heads_lds<D, NTHR>(s_x, G, G, s_acc, s_r, hp, tid);
+        for (int c = 0; c < C4; ++c) {
+            const float4 x = *reinterpret_cast<const float4*>(a.q + (h0 + h) * D + F::dim(j, 4 * c));
+            qr[h][4 * c + 0] = x.x;
+            qr[h][4 * c + 1] = x.y;
+            qr[h][4 * c + 2] = x.z;
+            qr[h][4 * c + 3] = x.w;
+        }
+    float rcs[EPL / 2], rsn[EPL / 2];
+    if (reg_prologue && rope) rope_lane_factors<D, EPL, Q8>(rcs, rsn, j, hp);
+    float cw[WPT], sw[WPT], qw[WPT], kw[WPT], kn[WPT], vn[WPT];
+    if (lds_prep) {
 #pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) qr[h][e] = s_x[h * D + F::dim(j, e)];
+        for (int r = 0; r < WPT; ++r) {
+            const int i = tid + r * NTHR;
+            const int ic = rope ? min(i, max(a.half_rope - 1, 0)) : 0;
+            cw[r] = rope ? hp.cos_row[ic] : 0.0f;
+            sw[r] = rope ? hp.sin_row[ic] : 0.0f;
+            qw[r] = qkn ? a.qnw[min(i, D - 1)] : 0.0f;
+            kw[r] = qkn ? a.knw[min(i, D - 1)] : 0.0f;
+        }
     }
+    if (has_pos) {
+#pragma unroll
+        for (int r = 0; r < WPT; ++r) {
+            const int i = min(tid + r * NTHR, D - 1);
+            kn[r] = a.k[kvh * D + i];
+            vn[r] = a.v[kvh * D + i];
+        }
+    }
+    const int first = row_begin + wave * ROWS_WAVE;
+    const int ntrips = first < cache_end ? (cache_end - first + ROWS_BLOCK - 1) / ROWS_BLOCK : 0;
+    Trip ta, tb;
+    load_trip<D, EPL, U, NT, Q8>(ta, a, kvh, first, cache_end, grp, j);
+
+    // 2. The LDS prep (one barrier for all staged inputs): q heads (LDS path) and the new K
+    //    head (appending split) normalised and rotated in the CPU path's float step order, the
+    //    V row V-normed when asked; then the append itself, before the stream.
+    if (lds_prep) {
+        if (!reg_prologue && wave == 0 && grp == 0) {
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) s_x[h * D + F::dim(j, e)] = qr[h][e];
+        }
+#pragma unroll
+        for (int r = 0; r < WPT; ++r) {
+            const int i = tid + r * NTHR;
+            if (i < a.half_rope) {
+                s_cs[i] = cw[r];
+                s_sn[i] = sw[r];
+            }
+            if (i < D) {
+                s_qw[i] = qw[r];
+                s_kw[i] = kw[r];
+                if (has_pos) {
+                    s_x[G * D + i] = kn[r];
+                    s_v[i] = vn[r];
+                }
+            }
+        }
+        __syncthreads();
+        const lds_cptr lnull = nullptr;
+        const HeadPrepLds hl{qkn ? (lds_cptr)s_qw : lnull, qkn ? (lds_cptr)s_kw : lnull, a.eps,
+                             rope ? (lds_cptr)s_cs : lnull, rope ? (lds_cptr)s_sn : lnull,
+                             a.half_rope, a.rope_type};
+        // Gemma 4's weightless V-norm: its serial sum runs on another wave than the K-norm's.
+        if (has_pos && a.v_norm != 0 && tid == (NTHR > 64 ? 64 : 0)) s_vr = seq_rms_inv<D>(s_v, a.eps);
+        const bool seq = a.norm_seq != 0;
+        if (!reg_prologue && has_pos && !seq) {
+            prep_heads_lds<D, NTHR>(s_x, G + 1, G, s_acc, s_r, hl, tid);
+        } else {
+            if (!reg_prologue) prep_heads_lds<D, NTHR>(s_x, G, G, s_acc, s_r, hl, tid);
+            if (has_pos) prep_heads_lds<D, NTHR>(s_x + G * D, 1, 0, s_acc, s_r, hl, tid, seq);
+        }
+        if (has_pos) {
+            if (a.v_norm != 0) {
+                __syncthreads();
+                for (int i = tid; i < D; i += NTHR) s_v[i] = s_v[i] * s_vr;
+                __syncthreads();
+            }
+            // KVCache.storeK/storeV: the exact fp32 rows, or their Q8_0 quantisation.
+            if constexpr (!Q8) {
+                float* kplane = a.kc + (long long)kvh * a.head_stride + (long long)pos * D;
+                float* vplane = a.vc + (long long)kvh * a.head_stride + (long long)pos * D;
+                for (int i = tid; i < D; i += NTHR) {
+                    kplane[i] = s_x[G * D + i];
+                    vplane[i] = s_v[i];
+                }
+            } else {
+                append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid);
+            }
+        }
+        if (!reg_prologue) {
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) qr[h][e] = s_x[h * D + F::dim(j, e)];
+        }
+    }
+    if (reg_prologue && rope) rope_registers<D, G, EPL, Q8>(qr, j, rcs, rsn, hp);
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
@@ -603,111 +781,48 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
         for (int e = 0; e < EPL; ++e) o[h][e] = 0.0f;
     }
 
-    // 2. Stream the cached rows [row_begin, cache_end).
-    if constexpr (!Q8) {
-        const float* kplane = a.kc + (long long)kvh * a.head_stride;
-        const float* vplane = a.vc + (long long)kvh * a.head_stride;
-        for (int base = row_begin + wave * ROWS_WAVE; base < cache_end; base += ROWS_BLOCK) {
-            float4 kf[U][C4], vf[U][C4];
-            bool valid[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int t = base + u * RPW + grp;
-                valid[u] = t < cache_end;
-                const int tt = valid[u] ? t : cache_end - 1;  // in-bounds address, masked row
-                const float4* kp = reinterpret_cast<const float4*>(kplane + (long long)tt * D) + j;
-                const float4* vp = reinterpret_cast<const float4*>(vplane + (long long)tt * D) + j;
-#pragma unroll
-                for (int c = 0; c < C4; ++c) kf[u][c] = load4<NT>(kp + c * LPR);
-#pragma unroll
-                for (int c = 0; c < C4; ++c) vf[u][c] = load4<NT>(vp + c * LPR);
-            }
-            accumulate_rows<D, G, EPL, U, LAZY>(qr, kf, vf, valid, m, l, o, a);
-        }
-    } else {
-        const signed char* kqp = a.kq + (long long)kvh * a.head_stride;
-        const signed char* vqp = a.vq + (long long)kvh * a.head_stride;
-        const float* ksp = a.ks + (long long)kvh * (a.head_stride / 32);
-        const float* vsp = a.vs + (long long)kvh * (a.head_stride / 32);
-        struct Rows {
-            uint4 kw[U], vw[U];
-            float ksc[U], vsc[U];
-            bool valid[U];
-        };
-        // Rows base + u*RPW + grp of this lane group (masked past cache_end, clamped address).
-        auto load_rows = [&](int base, Rows& r) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int t = base + u * RPW + grp;
-                r.valid[u] = t < cache_end;
-                const int tt = r.valid[u] ? t : cache_end - 1;
-                r.kw[u] = load_u4<NT>(reinterpret_cast<const uint4*>(kqp + (long long)tt * D) + j);
-                r.vw[u] = load_u4<NT>(reinterpret_cast<const uint4*>(vqp + (long long)tt * D) + j);
-                r.ksc[u] = ksp[(long long)tt * (D / 32) + (j >> 1)];
-                r.vsc[u] = vsp[(long long)tt * (D / 32) + (j >> 1)];
-            }
-        };
-        auto consume = [&](const Rows& r) {
-            float kq[U][16], vq[U][16];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                unpack_q8(r.kw[u], kq[u]);
-                unpack_q8(r.vw[u], vq[u]);
-            }
-            accumulate_rows_q8<D, G, U, LAZY>(qr, kq, r.ksc, vq, r.vsc, r.valid, m, l, o, a);
-        };
-        for (int base = row_begin + wave * ROWS_WAVE; base < cache_end; base += ROWS_BLOCK) {
-            Rows r;
-            load_rows(base, r);
-            consume(r);
-        }
+    // 3. Stream the cached rows [row_begin, cache_end), one trip prefetched in registers.  The
+    //    trips run in pairs with one exit: a branch between the two halves would join the loop
+    //    head with the second buffer's loads in flight, and the wait placed there would drain
+    //    the prefetch on every trip.  (The last pair's refill reads masked, clamped rows.)
+    int base = first;
+    for (int i = 0; i + 1 < ntrips; i += 2) {
+        load_trip<D, EPL, U, NT, Q8>(tb, a, kvh, base + ROWS_BLOCK, cache_end, grp, j);
+        consume_trip<D, G, EPL, U, Q8, LAZY>(ta, qr, m, l, o, a);
+        load_trip<D, EPL, U, NT, Q8>(ta, a, kvh, base + 2 * ROWS_BLOCK, cache_end, grp, j);
+        consume_trip<D, G, EPL, U, Q8, LAZY>(tb, qr, m, l, o, a);
+        base += 2 * ROWS_BLOCK;
     }
+    if (ntrips & 1) consume_trip<D, G, EPL, U, Q8, LAZY>(ta, qr, m, l, o, a);
 
-    // 3. The split that owns row `pos`: prepare k exactly, append K/V (KVCache.storeK/storeV:
-    //    the exact fp32 rows, or their Q8_0 quantisation), and take row `pos` from LDS as the
-    //    cache now holds it (row group 0 of wave 0).
-    if (has_pos) {
-        __shared__ float s_vr;
-        stage_new_row<D, NTHR>(a, kvh, s_x + G * D, s_v, s_acc, s_r, &s_vr, hp, tid);
+    // 4. Row `pos` as the cache now holds it, from LDS (row group 0 of wave 0).
+    if (has_pos && wave == 0) {
         if constexpr (!Q8) {
-            float* kplane = a.kc + (long long)kvh * a.head_stride;
-            float* vplane = a.vc + (long long)kvh * a.head_stride;
-            for (int i = tid; i < D; i += NTHR) {
-                kplane[(long long)pos * D + i] = s_x[G * D + i];
-                vplane[(long long)pos * D + i] = s_v[i];
-            }
-            if (wave == 0) {
-                float4 kf[1][C4], vf[1][C4];
-                bool valid[1] = {grp == 0};
+            float4 kf[1][C4], vf[1][C4];
+            bool valid[1] = {grp == 0};
 #pragma unroll
-                for (int c = 0; c < C4; ++c) {
-                    const int d0 = F::dim(j, 4 * c);
-                    kf[0][c] = make_float4(s_x[G * D + d0], s_x[G * D + d0 + 1],
-                                           s_x[G * D + d0 + 2], s_x[G * D + d0 + 3]);
-                    vf[0][c] = make_float4(s_v[d0], s_v[d0 + 1], s_v[d0 + 2], s_v[d0 + 3]);
-                }
-                accumulate_rows<D, G, EPL, 1>(qr, kf, vf, valid, m, l, o, a);
+            for (int c = 0; c < C4; ++c) {
+                const int d0 = F::dim(j, 4 * c);
+                kf[0][c] = make_float4(s_x[G * D + d0], s_x[G * D + d0 + 1], s_x[G * D + d0 + 2],
+                                       s_x[G * D + d0 + 3]);
+                vf[0][c] = make_float4(s_v[d0], s_v[d0 + 1], s_v[d0 + 2], s_v[d0 + 3]);
             }
+            accumulate_rows<D, G, EPL, 1>(qr, kf, vf, valid, m, l, o, a);
         } else {
-            __shared__ __align__(16) signed char s_kq[D], s_vq[D];
-            __shared__ float s_ks[D / 32], s_vs[D / 32], s_inv[D / 32];
-            append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid);
-            if (wave == 0) {
-                float kq[1][16], vq[1][16], ksc[1], vsc[1];
-                bool valid[1] = {grp == 0};
+            float kq[1][16], vq[1][16], ksc[1], vsc[1];
+            bool valid[1] = {grp == 0};
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    kq[0][e] = (float)s_kq[16 * j + e];
-                    vq[0][e] = (float)s_vq[16 * j + e];
-                }
-                ksc[0] = s_ks[j >> 1];
-                vsc[0] = s_vs[j >> 1];
-                accumulate_rows_q8<D, G, 1>(qr, kq, ksc, vq, vsc, valid, m, l, o, a);
+            for (int e = 0; e < 16; ++e) {
+                kq[0][e] = (float)s_kq[16 * j + e];
+                vq[0][e] = (float)s_vq[16 * j + e];
             }
+            ksc[0] = s_ks[j >> 1];
+            vsc[0] = s_vs[j >> 1];
+            accumulate_rows_q8<D, G, 1>(qr, kq, ksc, vq, vsc, valid, m, l, o, a);
         }
     }
 
-    // 4. Merge the row groups of each wave (lanes j, j+LPR, ...), then the waves via LDS.
+    // 5. Merge the row groups of each wave (lanes j, j+LPR, ...), then the waves via LDS.
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         float mw = m[h];
