@@ -538,6 +538,63 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False) 
             "kv_bytes_per_layer": kv_bytes(ctx), "layers_rotated": n_layers}
 
 
+def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28) -> dict:
+    """The attention half of a C3 Q4_K_M layer (as block_run) for K draft tokens at positions
+    ctx-K .. ctx-1 in one llmp_attn_block_batch call (projection weights read once for the K
+    tokens), against K single-token llmp_attn_block calls over the same layers; graph replays
+    over n_layers layers with their own weights and caches."""
+    from llmplayer_amd import _lib
+    from llmplayer_amd import hip_forward_pass as hfp
+    dim = 3072
+    c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=C3.theta)
+    fp = hfp.HipForwardPass(c, ctx)
+    try:
+        rng = np.random.default_rng(13)
+        kc = rng.standard_normal((ctx - K, c.kv_dim), dtype=np.float32) * np.float32(0.5)
+        vc = rng.standard_normal((ctx - K, c.kv_dim), dtype=np.float32)
+        for layer in range(n_layers):
+            fp.kv.write(layer, 0, kc, vc)
+        fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_F32)
+        wbytes = 0
+        for layer in range(n_layers):
+            lw = hfp.TransformerLayerWeights(attnNorm=np.ones(dim, np.float32))
+            for name, t, rows, cols in (("wq", 12, c.q_dim, dim), ("wk", 12, c.kv_dim, dim),
+                                        ("wv", 14, c.kv_dim, dim), ("wo", 12, dim, c.q_dim)):
+                data = synthetic_gguf(t, rows, cols, rng)
+                setattr(lw, name, hfp.GgufTensor(t, rows, cols, data))
+                if layer == 0:
+                    wbytes += data.nbytes
+            fp.uploadLayerWeights(layer, lw)
+        x = (rng.standard_normal((K, dim)) * 0.1).astype(np.float32)
+        fp.uploadXBatch(x)
+        fp.uploadX(x[0])
+        state = {"i": 0}
+
+        def batch():
+            layer = state["i"] % n_layers
+            state["i"] += 1
+            _lib.call("llmp_attn_block_batch", fp.kv.handle, layer, ctx - K, K, fp.gpuXBatch.ptr, 0)
+
+        def singles():
+            layer = state["i"] % n_layers
+            state["i"] += 1
+            for t in range(K):
+                _lib.call("llmp_attn_block", fp.kv.handle, layer, ctx - K + t, 0, fp.gpuX.ptr, 0, 0)
+        for _ in range(n_layers):
+            batch()
+        ms_b = _timed_graph(batch, steps)
+        ms_s = _timed_graph(singles, max(1, steps // 4))
+    finally:
+        fp.close()
+    us_b = ms_b / steps * 1e3
+    us_s = ms_s / max(1, steps // 4) * 1e3
+    return {"K": K, "ctx": ctx, "weights": "Q4_K_M mix (Q4_K q/k/o, Q6_K v)", "dim": dim,
+            "us_per_call": round(us_b, 2), "us_per_token": round(us_b / K, 2),
+            "single_token_blocks_us": round(us_s, 2), "speedup_vs_single_token_blocks": round(us_s / us_b, 2),
+            "weight_bytes_per_layer": wbytes, "kv_bytes_per_layer": kv_bytes(ctx - K),
+            "layers_rotated": n_layers}
+
+
 # ------------------------------------------------------------------------------ CPU baseline
 def cpu_time(shape: Shape, ctx: int, seconds: float, threads: int, layer: int = 0) -> dict:
     """The oracle (CPU restatement of Attention.forwardFromProjections) on one layer-call of
@@ -833,7 +890,7 @@ def main() -> int:
                 f"kernel {r['attn_kernel_us']} us ({r['attn_kernel_causal_tflops']} causal TFLOP/s)")
             prefill.append(r)
 
-    block = block_q8 = None
+    block = block_q8 = block_batch = None
     if args.block:
         block = block_run(args.ctx2 or 4096, 200)
         if second is not None:
@@ -846,6 +903,12 @@ def main() -> int:
         log(f"[bench] attention block C3 Q4_K_M at ctx {block['ctx']}: {block['us_per_layer_call']} us/layer")
         block_q8 = block_run(args.ctx2 or 4096, 200, q8_input=True)
         log(f"[bench] attention block, Q8_1 input: {block_q8['us_per_layer_call']} us/layer")
+        block_batch = []
+        for ctx_b, K, nl in ((4096, 4, 28), (4096, 16, 28), (32768, 4, 8), (32768, 16, 8)):
+            r = block_batch_run(ctx_b, K, 40, nl)
+            log(f"[bench] attention block, {K} tokens at ctx {ctx_b}: {r['us_per_call']} us/call "
+                f"({r['single_token_blocks_us']} us as {K} single-token blocks)")
+            block_batch.append(r)
 
     q8_prefill = q8_verify = None
     if args.q8 and args.prefill:
@@ -923,6 +986,8 @@ def main() -> int:
         line["attn_block_c3_q4_k_m"] = block
     if block_q8 is not None:
         line["attn_block_c3_q4_k_m_q8_1_input"] = block_q8
+    if block_batch:
+        line["attn_block_batch_c3_q4_k_m"] = block_batch
     if q8_prefill is not None:
         line["q8_0_prefill_c5_llama1b"] = q8_prefill
     if q8_verify is not None:

@@ -355,6 +355,21 @@ int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int r
 int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_position, uint64_t x,
                     int splits, uint64_t stream);
 
+/* The attention half of n_tokens consecutive tokens (positions pos0 .. pos0+n_tokens-1) on the
+ * device residual rows x (fp32 [n_tokens][dim], 16-byte aligned, updated in place): what
+ * n_tokens llmp_attn_block calls compute, with each projection weight read once per group of
+ * up to 16 tokens.  Replaces LLMEngine.forwardBatch's per-token attention halves
+ * (LLMEngine.java:1019-1033), batched as docs/optimization/speculative-decoding.md:120-140
+ * plans for the verification of K draft tokens.  The projections run on the matrix cores with
+ * each fp32 input split into three exact bf16 parts (fp32-accurate products, fp32 sums in
+ * another order than the CPU path); the attention is llmp_attn_prefill_f32's (the appended
+ * rows bit-identical to single-token appends of the same projections).  In the
+ * LLMP_INPUT_Q8_1 mode the tokens run one llmp_attn_block call each.  The call may grow the
+ * handle's prefill workspace, as llmp_attn_prefill_f32 does (not for use under graph capture
+ * then). */
+int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t x,
+                          uint64_t stream);
+
 /* ---- profiling (the reference's -Dcuda.profile section timers,
  *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */
 #define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV) */

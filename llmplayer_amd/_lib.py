@@ -80,6 +80,7 @@ SIGNATURES = {
     "llmp_block_input_mode": [_u64, _i32],
     "llmp_layer_weight": [_u64, _i32, _i32, _i32, _i32, _i32, C.c_void_p, _u64],
     "llmp_attn_block": [_u64, _i32, _i32, _u64, _u64, _i32, _u64],
+    "llmp_attn_block_batch": [_u64, _i32, _i32, _i32, _u64, _u64],
     "llmp_attn_decode_shared": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _i32, _u64],
     "llmp_attn_prefill_shared": [_u64, _i32, _i32, _i32, _i32, _u64, _u64, _u64, _u64],
     "llmp_attn_prefill_f32": [_u64, _i32, _i32, _i32, _u64, _u64, _u64, _u64, _u64, _u64],

@@ -119,9 +119,10 @@ hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipS
 }
 
 hipError_t launch_post_norm_residual(const float* xb, const float* w, float eps, float rscale,
-                                     float* x, int dim, hipStream_t st) {
-    hipLaunchKernelGGL(gk::post_norm_residual_kernel<gk::kPostThreads>, dim3(1), dim3(gk::kPostThreads), 0, st, xb,
-                       w, eps, rscale, x, dim);
+                                     float* x, int dim, int n_tokens, hipStream_t st) {
+    if (n_tokens < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gk::post_norm_residual_kernel<gk::kPostThreads>, dim3(n_tokens),
+                       dim3(gk::kPostThreads), 0, st, xb, w, eps, rscale, x, dim);
     return hipGetLastError();
 }
 

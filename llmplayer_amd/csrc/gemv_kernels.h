@@ -639,7 +639,8 @@ void gemv_kernel(GemvArgs a) {
 }
 
 // Post-attention norm and residual (Gemma 2/3, OLMo2: TransformerBlock.forward):
-// xb = rmsnorm(xb, w); xb *= rscale (Granite, when > 0); x += xb.  One workgroup.
+// xb = rmsnorm(xb, w); xb *= rscale (Granite, when > 0); x += xb.  One workgroup per token
+// (rows dim floats apart).
 constexpr int kPostThreads = 1024;
 template <int NTHR>
 __global__ __launch_bounds__(NTHR) void post_norm_residual_kernel(const float* xb, const float* w,
@@ -648,6 +649,8 @@ __global__ __launch_bounds__(NTHR) void post_norm_residual_kernel(const float* x
     constexpr int kPostThreads = NTHR;
     __shared__ float red[kPostThreads / 64];
     const int tid = threadIdx.x;
+    xb += (long long)blockIdx.x * dim;
+    x += (long long)blockIdx.x * dim;
     float ss = 0.0f;
     for (int i = tid; i < dim; i += kPostThreads) ss = __builtin_fmaf(xb[i], xb[i], ss);
 #pragma unroll

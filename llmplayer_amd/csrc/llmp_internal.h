@@ -12,6 +12,8 @@ namespace llmp {
 constexpr int kMaxSplits = 1024;
 // Largest GQA group (query heads per KV head) any decode kernel ships.
 constexpr int kMaxGroup = 8;
+// Tokens per launch of the token-batched projections (the MFMA's N).
+constexpr int kTokBatch = 16;
 
 // Arguments of one split-K decode launch.  All pointers are device pointers.  The kernels
 // derive the step plan (window start, rows per split, effective splits, RoPE row) from the
@@ -130,8 +132,22 @@ hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipS
 bool gemv_pair_supported(int first_type, int second_type);
 hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_type, bool q8_input,
                             hipStream_t stream);
-// x += rscale? * rmsnorm(xb, w) over dim values (one workgroup).
+// x += rscale? * rmsnorm(xb, w) over dim values, for n_tokens rows dim floats apart (one
+// workgroup per row).
 hipError_t launch_post_norm_residual(const float* xb, const float* w, float eps, float rscale,
-                                     float* x, int dim, hipStream_t stream);
+                                     float* x, int dim, int n_tokens, hipStream_t stream);
+
+namespace tk {
+struct ProjTokArgs;
+}
+// Token-batched projections on the matrix cores (proj_tok_kernels.h): the GGML types with a
+// kernel; the bytes of a staging buffer for `cols` inputs; the staging launch (pre-norm and the
+// bf16 split of n_tokens <= 16 rows x_pitch floats apart); the projection launch over the
+// staged inputs (hipErrorInvalidValue for an unsupported type or shape).
+bool proj_tok_supported(int ggml_type);
+size_t proj_tok_stage_bytes(int cols);
+hipError_t launch_proj_stage(const float* x, long long x_pitch, const float* norm_w, float eps,
+                             int cols, int n_tokens, void* stage, hipStream_t stream);
+hipError_t launch_proj_tok(tk::ProjTokArgs a, int ggml_type, const void* stage, hipStream_t stream);
 
 }  // namespace llmp

@@ -5,6 +5,7 @@
 #include "llmp_internal.h"
 #include "prefill_kernels.h"
 #include "gemv_kernels.h"
+#include "proj_tok_kernels.h"
 
 #include <cmath>
 #include <cstdarg>
@@ -93,6 +94,8 @@ struct KvHandle {
     int blk_input = LLMP_INPUT_F32;  // llmp_block_input_mode
     float* blk_buf = nullptr;        // block scratch: q|k|v, attention output, Wo output
     size_t blk_floats = 0;
+    void* blkb_buf = nullptr;        // token-batched block scratch (llmp_attn_block_batch)
+    size_t blkb_bytes = 0;
     size_t part_slots = 0;    // (split, query head) slots the workspace holds
     bool prof_on = false;
     std::vector<ProfPair> prof_pending[LLMP_PROF_KINDS];
@@ -193,6 +196,7 @@ void free_handle(KvHandle* kv) {
             if (w.mem) (void)hipFree(w.mem);
     }
     if (kv->blk_buf) (void)hipFree(kv->blk_buf);
+    if (kv->blkb_buf) (void)hipFree(kv->blkb_buf);
     if (kv->part_o) (void)hipFree(kv->part_o);
     if (kv->part_ml) (void)hipFree(kv->part_ml);
     if (kv->prefill_ws) (void)hipFree(kv->prefill_ws);
@@ -1036,6 +1040,25 @@ static int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
     return n;
 }
 
+// Byte offsets of the token-batched block scratch: the staged inputs of the larger of the two
+// projections' widths, then q, k, v, the attention output and the output projection of
+// kTokBatch tokens (each region 256-byte aligned).
+struct BatchLayout {
+    size_t q, k, v, attn, o, total;
+};
+static BatchLayout batch_layout(const KvHandle* kv, int qd, int kvd) {
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const int dim = kv->blk_dim;
+    BatchLayout L;
+    L.q = al(proj_tok_stage_bytes(dim > qd ? dim : qd));
+    L.k = L.q + al((size_t)kTokBatch * qd * sizeof(float));
+    L.v = L.k + al((size_t)kTokBatch * kvd * sizeof(float));
+    L.attn = L.v + al((size_t)kTokBatch * kvd * sizeof(float));
+    L.o = L.attn + al((size_t)kTokBatch * qd * sizeof(float));
+    L.total = L.o + al((size_t)kTokBatch * dim * sizeof(float));
+    return L;
+}
+
 int llmp_block_config(uint64_t handle, int dim, float residual_scale) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
@@ -1132,13 +1155,33 @@ int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int r
         LLMP_HIP_CHECK(hipMalloc(&kv->blk_buf, need * sizeof(float)), "hipMalloc(block scratch)");
         kv->blk_floats = need;
     }
+    // Token-batched block scratch: the staged inputs, then q, k, v, the attention output and
+    // the output projection of 16 tokens.
+    const size_t needb = batch_layout(kv, qd, kvd).total;
+    if (needb > kv->blkb_bytes) {
+        LLMP_HIP_CHECK(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        if (kv->blkb_buf) (void)hipFree(kv->blkb_buf);
+        kv->blkb_buf = nullptr;
+        kv->blkb_bytes = 0;
+        LLMP_HIP_CHECK(hipMalloc(&kv->blkb_buf, needb), "hipMalloc(batched block scratch)");
+        kv->blkb_bytes = needb;
+    }
     return LLMP_OK;
 }
+
+static int enqueue_block(KvHandle* kv, int layer, int position, uint64_t d_position, uint64_t x,
+                         int splits, uint64_t stream);
 
 int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_position, uint64_t x,
                     int splits, uint64_t stream) {
     if (int rc = ensure_init()) return rc;
     LLMP_GET_HANDLE(kv, handle);
+    return enqueue_block(kv, layer, position, d_position, x, splits, stream);
+}
+
+// One token's attention half (llmp_attn_block).
+static int enqueue_block(KvHandle* kv, int layer, int position, uint64_t d_position, uint64_t x,
+                         int splits, uint64_t stream) {
     if (layer < 0 || layer >= kv->n_layers)
         return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
     const LayerCfg& c = kv->layers[(size_t)layer];
@@ -1246,12 +1289,145 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
     if (post) {
         g.out = o;
         LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, q8in, st), "block output projection launch");
-        LLMP_HIP_CHECK(launch_post_norm_residual(o, post, c.eps, kv->blk_rscale, xp, dim, st),
+        LLMP_HIP_CHECK(launch_post_norm_residual(o, post, c.eps, kv->blk_rscale, xp, dim, 1, st),
                        "block post-norm launch");
     } else {
         g.resid = xp;
         g.rscale = kv->blk_rscale;
         LLMP_HIP_CHECK(launch_gemv(g, W[LLMP_W_O].type, q8in, st), "block output projection launch");
+    }
+    return LLMP_OK;
+}
+
+static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int n_tokens,
+                           bool in_f32, uint64_t q, uint64_t k, uint64_t v, uint64_t gate,
+                           uint64_t out, uint64_t stream, bool use_static);
+
+// The attention half of n_tokens tokens at positions pos0 .. pos0+n_tokens-1 over the rows
+// x[t][dim] (LLMEngine.forwardBatch's per-token forwards, LLMEngine.java:1019-1033, with the
+// projections batched as speculative-decoding.md:120-140 plans): per group of up to kTokBatch
+// tokens, the Q/K/V projections of all of them on the matrix cores (each weight row read once),
+// the multi-token attention on fp32 projections (the rows appended exactly as the single-token
+// decode appends them), the output projection with its residual epilogue, and the post-norm.
+// In the Q8_1 input mode the tokens run one llmp_attn_block call each (that contract's int8 dot
+// products have no batched kernel).
+int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t x,
+                          uint64_t stream) {
+    if (int rc = ensure_init()) return rc;
+    LLMP_GET_HANDLE(kv, handle);
+    if (layer < 0 || layer >= kv->n_layers)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "layer %d outside [0, %d)", layer, kv->n_layers);
+    if (n_tokens <= 0 || pos0 < 0 || (long long)pos0 + n_tokens > kv->max_seq)
+        return fail(LLMP_ERR_OUT_OF_RANGE, "llmp_attn_block_batch: rows [%d, %lld) outside [0, %d)",
+                    pos0, (long long)pos0 + n_tokens, kv->max_seq);
+    const LayerCfg& c = kv->layers[(size_t)layer];
+    if (!c.configured)
+        return fail(LLMP_ERR_INVALID_ARG, "layer %d was never configured (llmp_layer_config)", layer);
+    const DevWeight* W = c.w;
+    const bool merged = W[LLMP_W_QKV].mem != nullptr;
+    if (kv->blk_dim == 0 || !W[LLMP_W_O].mem ||
+        (!merged && (!W[LLMP_W_Q].mem || !W[LLMP_W_K].mem || !W[LLMP_W_V].mem)))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: layer %d lacks projection weights", layer);
+    if (!x || (x & 15)) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: null or misaligned x");
+    const int D = kv->head_dim, qd = c.n_heads * D, kvd = kv->n_kv_heads * D, dim = kv->blk_dim;
+    if (kv->blk_input == LLMP_INPUT_Q8_1) {
+        for (int t = 0; t < n_tokens; ++t)
+            if (int rc = enqueue_block(kv, layer, pos0 + t, 0, x + (uint64_t)t * dim * sizeof(float), 0,
+                                       stream))
+                return rc;
+        return LLMP_OK;
+    }
+    for (int i = 0; i < 3; ++i) {
+        const DevWeight& dw = merged ? W[LLMP_W_QKV] : W[LLMP_W_Q + i];
+        if (!proj_tok_supported(dw.type))
+            return fail(LLMP_ERR_UNSUPPORTED, "llmp_attn_block_batch: GGML type %d", dw.type);
+    }
+    if (!proj_tok_supported(W[LLMP_W_O].type))
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_attn_block_batch: GGML type %d", W[LLMP_W_O].type);
+    const BatchLayout L = batch_layout(kv, qd, kvd);
+    if (!kv->blkb_buf || L.total > kv->blkb_bytes)
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: layer %d weights not uploaded", layer);
+    char* base = static_cast<char*>(kv->blkb_buf);
+    void* stage = base;
+    float* qb = reinterpret_cast<float*>(base + L.q);
+    float* kb = reinterpret_cast<float*>(base + L.k);
+    float* vb = reinterpret_cast<float*>(base + L.v);
+    float* attn = reinterpret_cast<float*>(base + L.attn);
+    float* ob = reinterpret_cast<float*>(base + L.o);
+    hipStream_t st = pick_stream(stream);
+    auto vecp = [&](int slot) -> const float* { return static_cast<const float*>(W[slot].mem); };
+
+    // Q/K/V segments: outputs q [K][qd], k [K][kvd], v [K][kvd].
+    tk::TokSeg segs[3];
+    int types[3];
+    const int seg_rows[3] = {qd, kvd, kvd}, seg_off[3] = {0, qd, qd + kvd};
+    const int bias_slot[3] = {LLMP_W_Q_BIAS, LLMP_W_K_BIAS, LLMP_W_V_BIAS};
+    float* seg_out[3] = {qb, kb, vb};
+    for (int i = 0; i < 3; ++i) {
+        const DevWeight& dw = merged ? W[LLMP_W_QKV] : W[LLMP_W_Q + i];
+        segs[i].w = dw.planes;
+        if (merged)
+            for (int p = 0; p < 4; ++p)
+                if (dw.planes.p[p]) segs[i].w.p[p] = dw.planes.p[p] + (long long)seg_off[i] * dw.planes.pitch[p];
+        segs[i].rows = seg_rows[i];
+        segs[i].bias = vecp(bias_slot[i]);
+        segs[i].out = seg_out[i];
+        segs[i].out_pitch = seg_rows[i];
+        types[i] = dw.type;
+    }
+    float* xp = reinterpret_cast<float*>(x);
+    for (int t0 = 0; t0 < n_tokens; t0 += kTokBatch) {
+        const int K = n_tokens - t0 < kTokBatch ? n_tokens - t0 : kTokBatch;
+        float* xc = xp + (size_t)t0 * dim;
+        // 1-2. Pre-norm and the Q/K/V projections: one launch per run of segments of one type.
+        LLMP_HIP_CHECK(launch_proj_stage(xc, dim, vecp(LLMP_W_ATTN_NORM), c.eps, dim, K, stage, st),
+                       "batched block input staging");
+        for (int i = 0; i < 3;) {
+            int n = 1;
+            while (i + n < 3 && types[i + n] == types[i]) ++n;
+            tk::ProjTokArgs g{};
+            int off = 0;
+            for (int k = 0; k < n; ++k) {
+                g.seg[k] = segs[i + k];
+                g.seg[k].out_off = off;
+                off += segs[i + k].rows;
+            }
+            g.nseg = n;
+            g.rows_total = off;
+            g.cols = dim;
+            g.K = K;
+            LLMP_HIP_CHECK(launch_proj_tok(g, types[i], stage, st), "batched block Q/K/V projection launch");
+            i += n;
+        }
+        // 3-5. Attention of the K tokens (QK-norm, RoPE, exact appends, causal over the cache).
+        if (int rc = enqueue_prefill(kv, layer, -1, pos0 + t0, K, true, reinterpret_cast<uint64_t>(qb),
+                                     reinterpret_cast<uint64_t>(kb), reinterpret_cast<uint64_t>(vb), 0,
+                                     reinterpret_cast<uint64_t>(attn), stream, false))
+            return rc;
+        // 6. Output projection (+ bias), post-norm, residual scale and residual add.
+        LLMP_HIP_CHECK(launch_proj_stage(attn, qd, nullptr, 0.0f, qd, K, stage, st),
+                       "batched block attention staging");
+        tk::ProjTokArgs g{};
+        g.seg[0].w = W[LLMP_W_O].planes;
+        g.seg[0].rows = dim;
+        g.seg[0].bias = vecp(LLMP_W_O_BIAS);
+        g.nseg = 1;
+        g.rows_total = dim;
+        g.cols = qd;
+        g.K = K;
+        const float* post = vecp(LLMP_W_POST_ATTN_NORM);
+        if (post) {
+            g.seg[0].out = ob;
+            g.seg[0].out_pitch = dim;
+            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, stage, st), "batched block output projection launch");
+            LLMP_HIP_CHECK(launch_post_norm_residual(ob, post, c.eps, kv->blk_rscale, xc, dim, K, st),
+                           "batched block post-norm launch");
+        } else {
+            g.resid = xc;
+            g.resid_pitch = dim;
+            g.rscale = kv->blk_rscale;
+            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, stage, st), "batched block output projection launch");
+        }
     }
     return LLMP_OK;
 }

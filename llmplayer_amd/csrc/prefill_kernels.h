@@ -8,23 +8,24 @@
 //  1. prefill_append_kernel: one workgroup per token takes its k/v (fp32, or bf16 widened to
 //     fp32), applies the exact QK-norm + RoPE of the decode path and writes the K/V rows
 //     (bit-identical to P appends by the CPU path).
-//  2. prefill_tile_kernel: once per (key tile, KV head), the bf16 hi/lo split of the tile's K
+//  2. prefill_tile_kernel: once per (key tile, KV head), the fp16 hi/lo split of the tile's K
 //     rows and of its V rows (transposed) into a workspace image laid out like the LDS tile.
 //  3. prefill_attn2_kernel: causal flash attention on MFMA.  A workgroup owns one KV head and
 //     16*NB query positions of all G query heads of that KV head; each wave owns 16 positions
 //     of HPW query heads.  Tile images stream into two LDS buffers (tile i+2 is fetched into
 //     registers while tile i is consumed); per 64-key tile a wave computes S^T = K Q^T and
-//     O^T += V^T P^T with v_mfma_f32_16x16x32_bf16 and an online softmax in the accumulator
+//     O^T += V^T P^T with v_mfma_f32_16x16x32_f16 and an online softmax in the accumulator
 //     layout.  Workgroups are ranked by key count and dispatched heaviest-first in the first
 //     half of the grid, lightest-first in the second, so co-resident workgroups balance.
 //
-// Precision: Q and K are post-RoPE fp32 (not bf16), so each operand is split into
-// hi = bf16(x) and lo = bf16(x - hi), and a product uses three MFMAs (hi*hi + hi*lo + lo*hi):
-// ~2^-16 relative per term instead of bf16's 2^-9, which keeps the output within 1e-4 of the
-// fp32 CPU path.  P V uses the same split for P and for V (cache rows before pos0 may be any
-// fp32; rows written from bf16 inputs have lo = 0).
+// Precision: Q and K are post-RoPE fp32, so each operand is split into hi = fp16(x) and
+// lo = fp16(x - hi), and a product uses three MFMAs (hi*hi + hi*lo + lo*hi): ~2^-21 relative
+// per term (a bf16 split would give ~2^-16), which keeps the output within ~1e-6 of the
+// fp32 CPU path.  P V uses the same split for P and for V (rows written from bf16 inputs have
+// lo = 0 within fp16's normal range).  The split needs |x| < 65504 for the K and V rows and the
+// scaled query (the range fp16 KV caches assume); P <= 1.
 //
-// Layout facts of v_mfma_f32_16x16x32_bf16 used here (checked on MI355X): lane i holds
+// Layout facts of v_mfma_f32_16x16x32_f16 (and _bf16) used here (checked on MI355X): lane i holds
 // A[i%16][8*(i/16)+j] and B[8*(i/16)+j][i%16] (j < 8) and D[4*(i/16)+j][i%16] (j < 4).
 // S^T's D fragment (lane: query i%16, keys 4*(i/16)+j of a 16-key tile) is fed back as the B
 // operand of the P V product without moving data across lanes: the 32 keys of an MFMA step
@@ -37,13 +38,13 @@
 namespace llmp {
 namespace pk {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef short short8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr float kNegBig = dk::kNegBig;
 
-// Keys per LDS tile: 64, or 32 for head_dim 256 (keeps the bf16 hi/lo tile under 80 KB).
+// Keys per LDS tile: 64, or 32 for head_dim 256 (keeps the fp16 hi/lo tile under 80 KB).
 template <int D>
 constexpr int tile_keys() { return D >= 256 ? 32 : 64; }
 
@@ -175,13 +176,13 @@ inline size_t prefill_append_lds(int Hkv, int D) {
 }
 
 // ---- LDS tile layout (also the workspace image of a tile) -------------------------------------
-// LDS tile: K hi/lo [TK keys][D + 8] bf16, V^T hi/lo [D][TK + 4] (row padding spreads banks).
+// LDS tile: K hi/lo [TK keys][D + 8] fp16, V^T hi/lo [D][TK + 4] (row padding spreads banks).
 template <int D, int TKEYS = tile_keys<D>()>
 struct alignas(16) TileLds {
     static constexpr int TK = TKEYS;
-    static constexpr int KP = D + 8;   // K row pitch (bf16 elements; 16-byte multiple)
+    static constexpr int KP = D + 8;   // K row pitch (fp16 elements; 16-byte multiple)
     // V^T row pitch: 8-byte multiple with an odd number of 8-byte units beyond a 32-dword
-    // multiple (TK + 4 bf16 = 2*(TK/2 + 2) dwords), so the 16 dims of a lane row-group's 8-byte
+    // multiple (TK + 4 fp16 = 2*(TK/2 + 2) dwords), so the 16 dims of a lane row-group's 8-byte
     // reads fall on 16 distinct bank pairs.
     static constexpr int VP = TK + 4;
     unsigned short kh[TK * KP];
@@ -191,21 +192,22 @@ struct alignas(16) TileLds {
 };
 
 // ---- 2. Tile images ----------------------------------------------------------------------------
-// The bf16 hi/lo split of a key tile does not depend on the query block, so it is done once per
+// The fp16 hi/lo split of a key tile does not depend on the query block, so it is done once per
 // (tile, KV head) into a workspace image laid out exactly like TileLds.
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 
-// Two fp32 values -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
-__device__ __forceinline__ unsigned pack_bf16(float x, float y) {
-    return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{x, y}, bf16x2));
+// Two fp32 values -> packed fp16 (round to nearest even, v_cvt_pk_f16_f32).
+__device__ __forceinline__ unsigned pack_f16(float x, float y) {
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{x, y}, f16x2));
 }
-// Split of two values: hi = bf16(x), lo = bf16(x - hi), packed in pairs.
+// Split of two values: hi = fp16(x), lo = fp16(x - hi) (x - hi is exact in fp32), packed in
+// pairs: hi + lo holds x to ~2^-22 of |x| (or 2^-25 absolute below fp16's normal range).
 __device__ __forceinline__ void split_pair(float x, float y, unsigned& hi, unsigned& lo) {
-    hi = pack_bf16(x, y);
-    const float hx = __uint_as_float(hi << 16), hy = __uint_as_float(hi & 0xFFFF0000u);
-    lo = pack_bf16(x - hx, y - hy);
+    hi = pack_f16(x, y);
+    const f16x2 h = __builtin_bit_cast(f16x2, hi);
+    lo = pack_f16(x - (float)h[0], y - (float)h[1]);
 }
 
 template <int D>
@@ -337,8 +339,8 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
 // rotated width (partial RoPE) works the same way.
 template <int D>
 __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int hq, int qpos,
-                                               int grp, bf16x8 (&qh)[D / 32],
-                                               bf16x8 (&ql)[D / 32]) {
+                                               int grp, f16x8 (&qh)[D / 32],
+                                               f16x8 (&ql)[D / 32]) {
     constexpr int KS = D / 32;
     float qf[KS][8];
     const long long q0 = (long long)qi * a.Hq * D + (long long)hq * D;
@@ -412,8 +414,8 @@ __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             split_pair(qf[s][2 * j] * a.qk_scale, qf[s][2 * j + 1] * a.qk_scale, hh[j], ll[j]);
-        qh[s] = __builtin_bit_cast(bf16x8, make_uint4(hh[0], hh[1], hh[2], hh[3]));
-        ql[s] = __builtin_bit_cast(bf16x8, make_uint4(ll[0], ll[1], ll[2], ll[3]));
+        qh[s] = __builtin_bit_cast(f16x8, make_uint4(hh[0], hh[1], hh[2], hh[3]));
+        ql[s] = __builtin_bit_cast(f16x8, make_uint4(ll[0], ll[1], ll[2], ll[3]));
     }
 }
 
@@ -553,7 +555,7 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
     const int qpos = a.pos0 + (q_ok ? qi : a.P - 1);
     const int qstart = a.window > 0 ? max(0, qpos - a.window + 1) : 0;
 
-    bf16x8 qh[HPW][KS], ql[HPW][KS];
+    f16x8 qh[HPW][KS], ql[HPW][KS];
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh)
         query_fragment<D>(a, q_ok ? qi : a.P - 1, kvh * G + hg * HPW + hh, qpos, grp, qh[hh], ql[hh]);
@@ -611,13 +613,13 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
             const int krow = kt * 16 + col;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                const bf16x8 kh = *reinterpret_cast<const bf16x8*>(&t.kh[krow * T::KP + 32 * s + 8 * grp]);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8*>(&t.kl[krow * T::KP + 32 * s + 8 * grp]);
+                const f16x8 kh = *reinterpret_cast<const f16x8*>(&t.kh[krow * T::KP + 32 * s + 8 * grp]);
+                const f16x8 kl = *reinterpret_cast<const f16x8*>(&t.kl[krow * T::KP + 32 * s + 8 * grp]);
 #pragma unroll
                 for (int hh = 0; hh < HPW; ++hh) {
-                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[hh][s], acc[hh], 0, 0, 0);
-                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[hh][s], acc[hh], 0, 0, 0);
-                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[hh][s], acc[hh], 0, 0, 0);
+                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[hh][s], acc[hh], 0, 0, 0);
+                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[hh][s], acc[hh], 0, 0, 0);
+                    acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[hh][s], acc[hh], 0, 0, 0);
                 }
             }
 #pragma unroll
@@ -677,7 +679,7 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
         // O^T += V^T P^T: B operand = P in the key order {32c+4grp..+3, 32c+16+4grp..+3}.
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            bf16x8 ph[HPW], pl[HPW];
+            f16x8 ph[HPW], pl[HPW];
 #pragma unroll
             for (int hh = 0; hh < HPW; ++hh) {
                 unsigned h0, l0, h1, l1, h2, l2, h3, l3;
@@ -685,8 +687,8 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
                 split_pair(st[hh][2 * c][2], st[hh][2 * c][3], h1, l1);
                 split_pair(st[hh][2 * c + 1][0], st[hh][2 * c + 1][1], h2, l2);
                 split_pair(st[hh][2 * c + 1][2], st[hh][2 * c + 1][3], h3, l3);
-                ph[hh] = __builtin_bit_cast(bf16x8, make_uint4(h0, h1, h2, h3));
-                pl[hh] = __builtin_bit_cast(bf16x8, make_uint4(l0, l1, l2, l3));
+                ph[hh] = __builtin_bit_cast(f16x8, make_uint4(h0, h1, h2, h3));
+                pl[hh] = __builtin_bit_cast(f16x8, make_uint4(l0, l1, l2, l3));
             }
 #pragma unroll
             for (int d = 0; d < DT; ++d) {
@@ -698,13 +700,13 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
                 const uint2 a1 = *reinterpret_cast<const uint2*>(vhr + 16);
                 const uint2 b0 = *reinterpret_cast<const uint2*>(vlr);
                 const uint2 b1 = *reinterpret_cast<const uint2*>(vlr + 16);
-                const bf16x8 vh = __builtin_bit_cast(bf16x8, make_uint4(a0.x, a0.y, a1.x, a1.y));
-                const bf16x8 vl = __builtin_bit_cast(bf16x8, make_uint4(b0.x, b0.y, b1.x, b1.y));
+                const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(a0.x, a0.y, a1.x, a1.y));
+                const f16x8 vl = __builtin_bit_cast(f16x8, make_uint4(b0.x, b0.y, b1.x, b1.y));
 #pragma unroll
                 for (int hh = 0; hh < HPW; ++hh) {
-                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[hh], o[hh][d], 0, 0, 0);
-                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[hh], o[hh][d], 0, 0, 0);
-                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[hh], o[hh][d], 0, 0, 0);
+                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[hh], o[hh][d], 0, 0, 0);
+                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[hh], o[hh][d], 0, 0, 0);
+                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[hh], o[hh][d], 0, 0, 0);
                 }
             }
         }

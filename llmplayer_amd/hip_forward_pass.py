@@ -486,6 +486,26 @@ class HipForwardPass:
         d = self.gpuTokenParams.ptr if device_position else 0
         call("llmp_attn_block", self.kv.handle, layerIdx, position, d, self.gpuX.ptr, splits, stream)
 
+    def uploadXBatch(self, x: np.ndarray) -> None:
+        """Residual rows of n tokens, [n, dim] fp32, into gpuXBatch (for forwardAttentionBlockBatch)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.dim)
+        if getattr(self, "gpuXBatch", None) is None or self.gpuXBatch.nbytes < x.nbytes:
+            if getattr(self, "gpuXBatch", None) is not None:
+                self.gpuXBatch.free()
+            self.gpuXBatch = DeviceBuffer(x.nbytes)
+        self.gpuXBatch.upload(x)
+
+    def downloadXBatch(self, n_tokens: int) -> np.ndarray:
+        return self.gpuXBatch.download(np.float32, n_tokens * self.dim).reshape(n_tokens, self.dim)
+
+    def forwardAttentionBlockBatch(self, layerIdx: int, pos0: int, n_tokens: int,
+                                   stream: int = 0) -> None:
+        """The attention half of n_tokens tokens at positions pos0.. on gpuXBatch (the rows of
+        LLMEngine.forwardBatch's tokens, LLMEngine.java:1019-1033): what n_tokens
+        forwardAttentionBlock calls compute, each projection weight read once per 16 tokens."""
+        call("llmp_attn_block_batch", self.kv.handle, layerIdx, pos0, n_tokens,
+             self.gpuXBatch.ptr, stream)
+
     def updateTokenParams(self, position: int) -> None:
         """Store [position, position+1] in device memory (CudaForwardPass.updateTokenParams /
         uploadXAndUpdateParams, CudaForwardPass.java:1283-1292), for graph-captured calls."""
@@ -563,7 +583,8 @@ class HipForwardPass:
         call("llmp_stream_sync", stream)
 
     def close(self) -> None:
-        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2", "gpuGate", "gpuTokenParams", "gpuX"):
+        for b in ("gpuQ", "gpuK", "gpuV", "gpuXb2", "gpuGate", "gpuTokenParams", "gpuX",
+                  "gpuXBatch"):
             buf = getattr(self, b, None)
             if buf is not None:
                 buf.free()
