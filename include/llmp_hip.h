@@ -361,8 +361,8 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
  * up to 16 tokens.  Replaces LLMEngine.forwardBatch's per-token attention halves
  * (LLMEngine.java:1019-1033), batched as docs/optimization/speculative-decoding.md:120-140
  * plans for the verification of K draft tokens.  The projections run on the matrix cores with
- * each fp32 input split into three exact bf16 parts (fp32-accurate products, fp32 sums in
- * another order than the CPU path); the attention is llmp_attn_prefill_f32's (the appended
+ * each fp32 input split into two fp16 parts (fp32-accurate products, fp32 sums in another order
+ * than the CPU path; inputs below 65504); the attention is llmp_attn_prefill_f32's (the appended
  * rows bit-identical to single-token appends of the same projections).  In the
  * LLMP_INPUT_Q8_1 mode the tokens run one llmp_attn_block call each.  The call may grow the
  * handle's prefill workspace, as llmp_attn_prefill_f32 does (not for use under graph capture

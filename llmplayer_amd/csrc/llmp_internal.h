@@ -141,13 +141,11 @@ namespace tk {
 struct ProjTokArgs;
 }
 // Token-batched projections on the matrix cores (proj_tok_kernels.h): the GGML types with a
-// kernel; the bytes of a staging buffer for `cols` inputs; the staging launch (pre-norm and the
-// bf16 split of n_tokens <= 16 rows x_pitch floats apart); the projection launch over the
-// staged inputs (hipErrorInvalidValue for an unsupported type or shape).
+// kernel, the two-type pairs one launch takes (GemvSeg-like TokSeg::fmt 0 and 1), and the
+// launch (second_type < 0: one type); hipErrorInvalidValue for an unsupported type or shape.
 bool proj_tok_supported(int ggml_type);
-size_t proj_tok_stage_bytes(int cols);
-hipError_t launch_proj_stage(const float* x, long long x_pitch, const float* norm_w, float eps,
-                             int cols, int n_tokens, void* stage, hipStream_t stream);
-hipError_t launch_proj_tok(tk::ProjTokArgs a, int ggml_type, const void* stage, hipStream_t stream);
+bool proj_tok_pair_supported(int first_type, int second_type);
+hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_type,
+                           hipStream_t stream);
 
 }  // namespace llmp

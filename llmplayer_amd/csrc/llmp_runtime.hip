@@ -1040,9 +1040,8 @@ static int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
     return n;
 }
 
-// Byte offsets of the token-batched block scratch: the staged inputs of the larger of the two
-// projections' widths, then q, k, v, the attention output and the output projection of
-// kTokBatch tokens (each region 256-byte aligned).
+// Byte offsets of the token-batched block scratch: q, k, v, the attention output and the
+// output projection of kTokBatch tokens (each region 256-byte aligned).
 struct BatchLayout {
     size_t q, k, v, attn, o, total;
 };
@@ -1050,7 +1049,7 @@ static BatchLayout batch_layout(const KvHandle* kv, int qd, int kvd) {
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     const int dim = kv->blk_dim;
     BatchLayout L;
-    L.q = al(proj_tok_stage_bytes(dim > qd ? dim : qd));
+    L.q = 0;
     L.k = L.q + al((size_t)kTokBatch * qd * sizeof(float));
     L.v = L.k + al((size_t)kTokBatch * kvd * sizeof(float));
     L.attn = L.v + al((size_t)kTokBatch * kvd * sizeof(float));
@@ -1155,8 +1154,8 @@ int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int r
         LLMP_HIP_CHECK(hipMalloc(&kv->blk_buf, need * sizeof(float)), "hipMalloc(block scratch)");
         kv->blk_floats = need;
     }
-    // Token-batched block scratch: the staged inputs, then q, k, v, the attention output and
-    // the output projection of 16 tokens.
+    // Token-batched block scratch: q, k, v, the attention output and the output projection of
+    // 16 tokens.
     const size_t needb = batch_layout(kv, qd, kvd).total;
     if (needb > kv->blkb_bytes) {
         LLMP_HIP_CHECK(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -1348,7 +1347,6 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
     if (!kv->blkb_buf || L.total > kv->blkb_bytes)
         return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: layer %d weights not uploaded", layer);
     char* base = static_cast<char*>(kv->blkb_buf);
-    void* stage = base;
     float* qb = reinterpret_cast<float*>(base + L.q);
     float* kb = reinterpret_cast<float*>(base + L.k);
     float* vb = reinterpret_cast<float*>(base + L.v);
@@ -1370,34 +1368,65 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
             for (int p = 0; p < 4; ++p)
                 if (dw.planes.p[p]) segs[i].w.p[p] = dw.planes.p[p] + (long long)seg_off[i] * dw.planes.pitch[p];
         segs[i].rows = seg_rows[i];
+        segs[i].out_off = seg_off[i];
+        segs[i].fmt = 0;
         segs[i].bias = vecp(bias_slot[i]);
         segs[i].out = seg_out[i];
         segs[i].out_pitch = seg_rows[i];
         types[i] = dw.type;
     }
+    // One launch when the three share a type or form a supported pair (the Q4_K_M mix);
+    // otherwise one per run of segments of one type.
+    int t1 = types[0], t2 = -1;
+    for (int i = 1; i < 3; ++i)
+        if (types[i] != t1) {
+            if (t2 < 0) t2 = types[i];
+            else if (types[i] != t2) t2 = -2;
+        }
+    if (t2 >= 0 && !proj_tok_pair_supported(t1, t2) && proj_tok_pair_supported(t2, t1)) std::swap(t1, t2);
+    const bool paired = t2 >= 0 && proj_tok_pair_supported(t1, t2);
     float* xp = reinterpret_cast<float*>(x);
     for (int t0 = 0; t0 < n_tokens; t0 += kTokBatch) {
         const int K = n_tokens - t0 < kTokBatch ? n_tokens - t0 : kTokBatch;
         float* xc = xp + (size_t)t0 * dim;
-        // 1-2. Pre-norm and the Q/K/V projections: one launch per run of segments of one type.
-        LLMP_HIP_CHECK(launch_proj_stage(xc, dim, vecp(LLMP_W_ATTN_NORM), c.eps, dim, K, stage, st),
-                       "batched block input staging");
-        for (int i = 0; i < 3;) {
-            int n = 1;
-            while (i + n < 3 && types[i + n] == types[i]) ++n;
+        // 1-2. Pre-norm (folded into the projections) and the Q/K/V projections.
+        if (paired || t2 == -1) {
             tk::ProjTokArgs g{};
-            int off = 0;
-            for (int k = 0; k < n; ++k) {
-                g.seg[k] = segs[i + k];
-                g.seg[k].out_off = off;
-                off += segs[i + k].rows;
+            for (int k = 0; k < 3; ++k) {
+                g.seg[k] = segs[k];
+                g.seg[k].fmt = types[k] == t1 ? 0 : 1;
             }
-            g.nseg = n;
-            g.rows_total = off;
+            g.nseg = 3;
+            g.rows_total = qd + 2 * kvd;
             g.cols = dim;
             g.K = K;
-            LLMP_HIP_CHECK(launch_proj_tok(g, types[i], stage, st), "batched block Q/K/V projection launch");
-            i += n;
+            g.x = xc;
+            g.x_pitch = dim;
+            g.norm_w = vecp(LLMP_W_ATTN_NORM);
+            g.eps = c.eps;
+            LLMP_HIP_CHECK(launch_proj_tok(g, t1, paired ? t2 : -1, st), "batched block Q/K/V projection launch");
+        } else {
+            for (int i = 0; i < 3;) {
+                int n = 1;
+                while (i + n < 3 && types[i + n] == types[i]) ++n;
+                tk::ProjTokArgs g{};
+                int off = 0;
+                for (int k = 0; k < n; ++k) {
+                    g.seg[k] = segs[i + k];
+                    g.seg[k].out_off = off;
+                    off += segs[i + k].rows;
+                }
+                g.nseg = n;
+                g.rows_total = off;
+                g.cols = dim;
+                g.K = K;
+                g.x = xc;
+                g.x_pitch = dim;
+                g.norm_w = vecp(LLMP_W_ATTN_NORM);
+                g.eps = c.eps;
+                LLMP_HIP_CHECK(launch_proj_tok(g, types[i], -1, st), "batched block Q/K/V projection launch");
+                i += n;
+            }
         }
         // 3-5. Attention of the K tokens (QK-norm, RoPE, exact appends, causal over the cache).
         if (int rc = enqueue_prefill(kv, layer, -1, pos0 + t0, K, true, reinterpret_cast<uint64_t>(qb),
@@ -1405,8 +1434,6 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
                                      reinterpret_cast<uint64_t>(attn), stream, false))
             return rc;
         // 6. Output projection (+ bias), post-norm, residual scale and residual add.
-        LLMP_HIP_CHECK(launch_proj_stage(attn, qd, nullptr, 0.0f, qd, K, stage, st),
-                       "batched block attention staging");
         tk::ProjTokArgs g{};
         g.seg[0].w = W[LLMP_W_O].planes;
         g.seg[0].rows = dim;
@@ -1415,18 +1442,20 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
         g.rows_total = dim;
         g.cols = qd;
         g.K = K;
+        g.x = attn;
+        g.x_pitch = qd;
         const float* post = vecp(LLMP_W_POST_ATTN_NORM);
         if (post) {
             g.seg[0].out = ob;
             g.seg[0].out_pitch = dim;
-            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, stage, st), "batched block output projection launch");
+            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, -1, st), "batched block output projection launch");
             LLMP_HIP_CHECK(launch_post_norm_residual(ob, post, c.eps, kv->blk_rscale, xc, dim, K, st),
                            "batched block post-norm launch");
         } else {
             g.resid = xc;
             g.resid_pitch = dim;
             g.rscale = kv->blk_rscale;
-            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, stage, st), "batched block output projection launch");
+            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, -1, st), "batched block output projection launch");
         }
     }
     return LLMP_OK;
