@@ -131,6 +131,18 @@ int llmp_kv_clear(uint64_t handle, uint64_t stream);
 int llmp_rope_table(int rope_dim, int max_seq, float theta, float linear_freq_scale,
                     const float *freq_factors, int n_freq_factors, float *cos_out,
                     float *sin_out);
+/* Host helper: the YaRN branch of the RoPE constructor (RoPE.java:45-117 with YarnParams, the
+ * tables of the MoE and MLA engines, Qwen3MoEInferenceEngine.java:60-66): NTK-by-parts blend of
+ * freq_i and freq_i/scaling_factor between the correction dims of beta_fast and beta_slow
+ * (RoPE.yarnCorrDim, yarnRamp), angles and cos/sin as llmp_rope_table.  *mscale (may be NULL)
+ * receives the attention-magnitude factor; the engines scale scores by mscale^2/sqrt(headSize)
+ * (Qwen3MoEInferenceEngine.java:277-279), which llmp_layer_config takes as its custom scale.
+ * scaling_factor <= 1 builds the plain table with mscale 1.  The reference's defaults are
+ * beta_fast 32, beta_slow 1 (RoPE.YarnParams). */
+int llmp_rope_table_yarn(int rope_dim, int max_seq, float theta, const float *freq_factors,
+                         int n_freq_factors, float scaling_factor, int orig_ctx, float beta_fast,
+                         float beta_slow, float yarn_log_mul, float *cos_out, float *sin_out,
+                         float *mscale);
 /* Upload a table ([max_seq][half_rope] each) as the global or local table of a handle.
  * `which` is LLMP_ROPE_SEL_GLOBAL or LLMP_ROPE_SEL_LOCAL.  The reference uploads only the
  * global table (CudaForwardPass.java:398-402); the local one serves Gemma 3 local layers

@@ -66,6 +66,7 @@ SIGNATURES = {
     "llmp_kv_layer_ptrs": [_u64, _i32, _pu64, _pu64],
     "llmp_kv_clear": [_u64, _u64],
     "llmp_rope_table": [_i32, _i32, _f32, _f32, _pf, _i32, _pf, _pf],
+    "llmp_rope_table_yarn": [_i32, _i32, _f32, _pf, _i32, _f32, _i32, _f32, _f32, _f32, _pf, _pf, _pf],
     "llmp_rope_upload": [_u64, _i32, _pf, _pf, _i32, _i32],
     "llmp_layer_config": [_u64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
                           _f32, _pf, _pf],

@@ -829,6 +829,61 @@ int llmp_rope_table(int rope_dim, int max_seq, float theta, float linear_freq_sc
     return LLMP_OK;
 }
 
+int llmp_rope_table_yarn(int rope_dim, int max_seq, float theta, const float* freq_factors,
+                         int n_freq_factors, float scaling_factor, int orig_ctx, float beta_fast,
+                         float beta_slow, float yarn_log_mul, float* cos_out, float* sin_out,
+                         float* mscale) {
+    if (!(scaling_factor > 1.0f)) {   // RoPE.java:59: no YaRN, no linear scale
+        if (mscale) *mscale = 1.0f;
+        return llmp_rope_table(rope_dim, max_seq, theta, 1.0f, freq_factors, n_freq_factors, cos_out,
+                               sin_out);
+    }
+    if (rope_dim <= 0 || (rope_dim & 1) || max_seq <= 0 || !cos_out || !sin_out || orig_ctx <= 0 ||
+        !(beta_fast > 0.0f) || !(beta_slow > 0.0f))
+        return fail(LLMP_ERR_INVALID_ARG, "llmp_rope_table_yarn: rope_dim=%d max_seq=%d orig_ctx=%d",
+                    rope_dim, max_seq, orig_ctx);
+    const int half = rope_dim / 2;
+    const float freq_scale = 1.0f / scaling_factor;
+    const double pi = 3.141592653589793;
+    // RoPE.yarnCorrDim (RoPE.java:107-110) for both betas, floored / ceiled into [0, R/2 - 1]
+    auto corr_dim = [&](float beta) {
+        return (float)rope_dim * (float)std::log((double)orig_ctx / ((double)beta * 2.0 * pi)) /
+               (2.0f * (float)std::log((double)theta));
+    };
+    const float fl = (float)std::floor((double)corr_dim(beta_fast));
+    const float low = fl > 0.0f ? fl : 0.0f;
+    const float ce = (float)std::ceil((double)corr_dim(beta_slow));
+    const float lim = (float)rope_dim / 2.0f - 1.0f;
+    const float high = lim < ce ? lim : ce;
+    float attn_factor = 1.0f;
+    if (yarn_log_mul > 0.0f)
+        attn_factor = 0.1f * yarn_log_mul * (float)std::log((double)scaling_factor) + 1.0f;
+    if (mscale) *mscale = attn_factor * (1.0f + 0.1f * (float)std::log((double)(1.0f / freq_scale)));
+    std::vector<float> freq((size_t)half);
+    for (int i = 0; i < half; ++i) {
+        const double ex = 2.0 * (double)i / (double)rope_dim;
+        float base = (float)(1.0 / std::pow((double)theta, ex));
+        if (freq_factors && i < n_freq_factors) base = base / freq_factors[i];
+        // NTK-by-parts blend (RoPE.java:89-93, yarnRamp :113-117)
+        const float span = high - low;
+        const float y = ((float)i - low) / (span > 0.001f ? span : 0.001f);
+        const float cl = y < 0.0f ? 0.0f : (y < 1.0f ? y : 1.0f);
+        const float ramp = 1.0f - cl;
+        const float interp = freq_scale * base;
+        const float a = interp * (1.0f - ramp);
+        const float b = base * ramp;
+        freq[(size_t)i] = a + b;
+    }
+    for (int pos = 0; pos < max_seq; ++pos) {
+        for (int i = 0; i < half; ++i) {
+            const float angle = (float)pos * freq[(size_t)i];
+            cos_out[(size_t)pos * half + i] = (float)std::cos((double)angle);
+            sin_out[(size_t)pos * half + i] = (float)std::sin((double)angle);
+        }
+    }
+    return LLMP_OK;
+}
+
 int llmp_rope_upload(uint64_t handle, int which, const float* cos_t, const float* sin_t,
                      int max_seq, int half_rope) {
     if (int rc = ensure_init()) return rc;

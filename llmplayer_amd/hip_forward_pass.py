@@ -71,7 +71,10 @@ class ModelConfig:
     rope_freq_base: float = 10000.0
     rope_dim_count: int = 0               # 0 -> head_size
     rope_type: Optional[int] = None       # None -> per architecture
-    rope_scaling_factor: float = 1.0      # linear scaling (InferenceEngine.java:61-64)
+    rope_scaling_factor: float = 1.0      # linear scaling (InferenceEngine.java:61-64); YaRN
+                                          # factor in the MoE engines (Qwen3MoEInferenceEngine.java:60-66)
+    rope_orig_context_length: int = 0     # YaRN original context (ropeOrigContextLength)
+    yarn_log_multiplier: float = 0.0      # YaRN attention-factor log multiplier
     rope_freq_base_swa: float = 10000.0   # Gemma 4 SWA theta
     norm_eps: float = 1e-5
     sliding_window: int = 0
@@ -184,6 +187,22 @@ def rope_table(rope_dim: int, max_seq: int, theta: float, linear_freq_scale: flo
     call("llmp_rope_table", rope_dim, max_seq, float(theta), float(linear_freq_scale), _fp(ff),
          0 if ff is None else ff.size, _fp(cos_t), _fp(sin_t))
     return cos_t, sin_t
+
+
+def rope_table_yarn(rope_dim: int, max_seq: int, theta: float, scaling_factor: float,
+                    orig_ctx: int, yarn_log_mul: float = 0.0, beta_fast: float = 32.0,
+                    beta_slow: float = 1.0, freq_factors: Optional[np.ndarray] = None):
+    """cos/sin tables of the RoPE constructor's YaRN branch (RoPE.java:45-117) and its
+    attention-magnitude factor mscale, by the library's host helper: (cos, sin, mscale)."""
+    half = rope_dim // 2
+    cos_t = np.empty((max_seq, half), np.float32)
+    sin_t = np.empty((max_seq, half), np.float32)
+    ff = None if freq_factors is None else np.ascontiguousarray(freq_factors, np.float32)
+    ms = np.zeros(1, np.float32)
+    call("llmp_rope_table_yarn", rope_dim, max_seq, float(theta), _fp(ff), 0 if ff is None else ff.size,
+         float(scaling_factor), int(orig_ctx), float(beta_fast), float(beta_slow), float(yarn_log_mul),
+         _fp(cos_t), _fp(sin_t), _fp(ms))
+    return cos_t, sin_t, np.float32(ms[0])
 
 
 class DeviceBuffer:
@@ -330,9 +349,17 @@ class HipForwardPass:
         self.kv = KvCache(c.block_count, max_seq_len, c.head_count_kv, c.head_size, kv_dtype)
         rope_dim = c.rope_dim_count or c.head_size
         # InferenceEngine.java:58-78: global table with linear scaling; local table for
-        # Gemma 3 (theta 10000) and Gemma 4 (SWA theta) when a sliding window exists.
-        linear = c.rope_scaling_factor if c.rope_scaling_factor > 1.0 else 1.0
-        cos_g, sin_g = rope_table(rope_dim, max_seq_len, c.rope_freq_base, linear)
+        # Gemma 3 (theta 10000) and Gemma 4 (SWA theta) when a sliding window exists.  The MoE
+        # engine takes the scaling factor as YaRN's instead (Qwen3MoEInferenceEngine.java:60-66)
+        # and scales scores by mscale^2/sqrt(headSize) (:277-279).
+        self.mscale = np.float32(1.0)
+        if c.expert_count > 0 and c.rope_scaling_factor > 1.0:
+            cos_g, sin_g, self.mscale = rope_table_yarn(
+                rope_dim, max_seq_len, c.rope_freq_base, c.rope_scaling_factor,
+                c.rope_orig_context_length, c.yarn_log_multiplier)
+        else:
+            linear = c.rope_scaling_factor if c.rope_scaling_factor > 1.0 else 1.0
+            cos_g, sin_g = rope_table(rope_dim, max_seq_len, c.rope_freq_base, linear)
         call("llmp_rope_upload", self.kv.handle, _lib.LLMP_ROPE_SEL_GLOBAL, _fp(cos_g), _fp(sin_g),
              max_seq_len, rope_dim // 2)
         self.has_local_rope = False
@@ -394,10 +421,13 @@ class HipForwardPass:
             qw = np.ascontiguousarray(qk_norm[0], np.float32)
             kw = np.ascontiguousarray(qk_norm[1], np.float32)
             assert qw.size == c.head_size and kw.size == c.head_size
+        scale = float(c.attention_scale)
+        if scale <= 0.0 and self.mscale != np.float32(1.0):
+            # YaRN: mscale * mscale / (float) Math.sqrt(headSize) (Qwen3MoEInferenceEngine.java:279)
+            scale = float((self.mscale * self.mscale) / np.float32(np.sqrt(c.head_size)))
         call("llmp_layer_config", self.kv.handle, layer, c.head_count, c.head_count_kv,
              c.head_size, c.resolved_rope_type(), rope_sel, c.sliding_window, int(is_global),
-             float(c.attention_scale), float(c.attn_logit_soft_cap), float(c.norm_eps),
-             _fp(qw), _fp(kw))
+             scale, float(c.attn_logit_soft_cap), float(c.norm_eps), _fp(qw), _fp(kw))
 
     def set_sinks(self, layer: int, sinks: Optional[np.ndarray]) -> None:
         """Per-query-head attention-sink logits of a layer (GPT-OSS attn_sinks,

@@ -166,6 +166,75 @@ void orc_rope_tables(int rope_dim, int max_seq, float theta, float linear_freq_s
     free(freq);
 }
 
+/* RoPE tables, YaRN branch (RoPE.java:45-106 with YarnParams, :107-117; used by the MoE and
+ * MLA engines, Qwen3MoEInferenceEngine.java:60-66, DeepSeek2InferenceEngine.java:48), in Java's
+ * float/double steps:
+ *   freqScale = 1/s;
+ *   corrDim(beta) = R * (float)log(L / (beta*2*pi)) / (2 * (float)log(theta))  (RoPE.yarnCorrDim);
+ *   low = max(0, (float)floor(corrDim(betaFast))), high = min(R/2 - 1, (float)ceil(corrDim(betaSlow)));
+ *   attnFactor = logMul > 0 ? 0.1*logMul*(float)log(s) + 1 : 1;
+ *   mscale = attnFactor * (1 + 0.1*(float)log(1/freqScale));
+ *   ramp(i) = 1 - min(1, max(0, (i - low) / max(0.001, high - low)))  (RoPE.yarnRamp);
+ *   freq = (freqScale*base) * (1 - ramp) + base * ramp, base as in the plain branch;
+ *   angle = (float)pos * freq; cos/sin as in the plain branch.
+ * With s <= 1 the plain branch runs (no linear scale: the MoE engines pass none).  *mscale gets
+ * the attention-magnitude factor (1 without YaRN); the engines scale scores by
+ * mscale^2/sqrt(headSize) (Qwen3MoEInferenceEngine.java:277-279). */
+void orc_rope_tables_yarn(int rope_dim, int max_seq, float theta, const float *freq_factors,
+                          int n_freq_factors, float scaling_factor, int orig_ctx, float beta_fast,
+                          float beta_slow, float yarn_log_mul, float *cos_t, float *sin_t,
+                          float *mscale)
+{
+    if (!(scaling_factor > 1.0f)) {
+        orc_rope_tables(rope_dim, max_seq, theta, 1.0f, freq_factors, n_freq_factors, cos_t, sin_t);
+        if (mscale)
+            *mscale = 1.0f;
+        return;
+    }
+    int half = rope_dim / 2;
+    float freq_scale = 1.0f / scaling_factor;
+    const double pi = 3.141592653589793;   /* Math.PI */
+    float corr_low = (float)rope_dim * (float)log((double)orig_ctx / ((double)beta_fast * 2.0 * pi)) /
+                     (2.0f * (float)log((double)theta));
+    float corr_high = (float)rope_dim * (float)log((double)orig_ctx / ((double)beta_slow * 2.0 * pi)) /
+                      (2.0f * (float)log((double)theta));
+    float fl = (float)floor((double)corr_low);
+    corr_low = fl > 0.0f ? fl : 0.0f;
+    float ce = (float)ceil((double)corr_high);
+    float lim = (float)rope_dim / 2.0f - 1.0f;
+    corr_high = lim < ce ? lim : ce;
+    float attn_factor = 1.0f;
+    if (yarn_log_mul > 0.0f)
+        attn_factor = 0.1f * yarn_log_mul * (float)log((double)scaling_factor) + 1.0f;
+    float ms = attn_factor * (1.0f + 0.1f * (float)log((double)(1.0f / freq_scale)));
+    if (mscale)
+        *mscale = ms;
+    float *freq = (float *)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
+    for (int i = 0; i < half; i++) {
+        double ex = 2.0 * (double)i / (double)rope_dim;
+        float base = (float)(1.0 / pow((double)theta, ex));
+        if (freq_factors && i < n_freq_factors)
+            base = base / freq_factors[i];
+        float span = corr_high - corr_low;
+        float y = ((float)i - corr_low) / (span > 0.001f ? span : 0.001f);
+        float cl = y < 0.0f ? 0.0f : y;
+        cl = cl < 1.0f ? cl : 1.0f;
+        float ramp = 1.0f - cl;
+        float interp = freq_scale * base;
+        float a = interp * (1.0f - ramp);
+        float b = base * ramp;
+        freq[i] = a + b;
+    }
+    for (int pos = 0; pos < max_seq; pos++) {
+        for (int i = 0; i < half; i++) {
+            float angle = (float)pos * freq[i];
+            cos_t[(size_t)pos * half + i] = (float)cos((double)angle);
+            sin_t[(size_t)pos * half + i] = (float)sin((double)angle);
+        }
+    }
+    free(freq);
+}
+
 /* RoPE.applyAllHeads (RoPE.java:176-193): NORMAL pairs (2i, 2i+1) via RoPE.apply
  * (RoPE.java:145-170); NEOX pairs (i, i+R/2) via ropeNeox (SimdVectorOps.java:165-186).
  * Both compute x0' = x0*c - x1*s, x1' = x0*s + x1*c with separately rounded products. */

@@ -107,6 +107,8 @@ def lib():
         L.orc_sigmoid_gate.argtypes = [_F, _F, C.c_int]
         L.orc_per_head_norm.argtypes = [_F, _F, C.c_int, C.c_int, C.c_float]
         L.orc_rope_tables.argtypes = [C.c_int, C.c_int, C.c_float, C.c_float, _F, C.c_int, _F, _F]
+        L.orc_rope_tables_yarn.argtypes = [C.c_int, C.c_int, C.c_float, _F, C.c_int, C.c_float,
+                                           C.c_int, C.c_float, C.c_float, C.c_float, _F, _F, _F]
         L.orc_rope_apply_all.argtypes = [_F, C.c_int, C.c_int, C.c_int, C.c_int, _F, _F, C.c_int]
         L.orc_is_global_layer.restype = C.c_int
         L.orc_is_global_layer.argtypes = [C.c_int, C.c_int]
@@ -220,6 +222,23 @@ def rope_tables(rope_dim, max_seq, theta, linear_freq_scale=1.0, freq_factors=No
                           float(np.float32(linear_freq_scale)), _p(ff),
                           0 if ff is None else ff.size, _p(cos_t), _p(sin_t))
     return cos_t, sin_t
+
+
+def rope_tables_yarn(rope_dim, max_seq, theta, scaling_factor, orig_ctx, yarn_log_mul=0.0,
+                     beta_fast=32.0, beta_slow=1.0, freq_factors=None):
+    """RoPE tables of the YaRN branch (RoPE.java:45-117) and the attention-magnitude factor
+    mscale.  Returns (cos [max_seq, R/2], sin, mscale)."""
+    half = rope_dim // 2
+    cos_t = np.zeros((max_seq, half), np.float32)
+    sin_t = np.zeros((max_seq, half), np.float32)
+    ff = f32(freq_factors) if freq_factors is not None else None
+    ms = np.zeros(1, np.float32)
+    lib().orc_rope_tables_yarn(rope_dim, max_seq, float(np.float32(theta)), _p(ff),
+                               0 if ff is None else ff.size, float(np.float32(scaling_factor)),
+                               int(orig_ctx), float(np.float32(beta_fast)),
+                               float(np.float32(beta_slow)), float(np.float32(yarn_log_mul)),
+                               _p(cos_t), _p(sin_t), _p(ms))
+    return cos_t, sin_t, np.float32(ms[0])
 
 
 def rope_apply_all(vec, n_heads, head_size, rope_dim, rope_type, cos_t, sin_t, pos):

@@ -27,14 +27,25 @@ def log(msg: str) -> None:
     sys.stdout.flush()
 
 
+def _yarn(c: hfp.ModelConfig) -> bool:
+    """The MoE engines take rope_scaling_factor as YaRN's (Qwen3MoEInferenceEngine.java:60-66)."""
+    return c.expert_count > 0 and c.rope_scaling_factor > 1.0
+
+
 def oracle_config(c: hfp.ModelConfig, max_seq: int, sinks=None) -> orc.OracleConfig:
     arch = _ORC_ARCH.get(c.architecture, orc.ARCH_OTHER)
     if c.architecture == hfp.ARCH_GPT_OSS and c.expert_count > 0:
         arch = orc.ARCH_GPT_OSS_MOE
+    scale = c.attention_scale
+    if scale <= 0 and _yarn(c):   # mscale^2 / (float) sqrt(headSize), :277-279
+        _, _, ms = orc.rope_tables_yarn(c.rope_dim_count or c.head_size, 1, c.rope_freq_base,
+                                        c.rope_scaling_factor, c.rope_orig_context_length,
+                                        c.yarn_log_multiplier)
+        scale = float((ms * ms) / np.float32(np.sqrt(c.head_size)))
     return orc.OracleConfig(
         n_heads=c.head_count, n_kv_heads=c.head_count_kv, head_size=c.head_size,
         max_seq=max_seq, rope_type=c.resolved_rope_type(), rope_dim=c.rope_dim_count or c.head_size,
-        norm_eps=c.norm_eps, sliding_window=c.sliding_window, attention_scale=c.attention_scale,
+        norm_eps=c.norm_eps, sliding_window=c.sliding_window, attention_scale=scale,
         softcap=c.attn_logit_soft_cap, arch=arch,
         no_rope_interval=c.no_rope_layer_interval, nope_on_global=c.use_no_pe_on_global_layers,
         sinks=sinks)
@@ -50,6 +61,10 @@ def oracle_tables(c: hfp.ModelConfig, max_seq: int, layer: int):
     if c.sliding_window > 0 and c.architecture in (hfp.ARCH_GEMMA3, hfp.ARCH_GEMMA4) and not is_global:
         theta = 10000.0 if c.architecture == hfp.ARCH_GEMMA3 else c.rope_freq_base_swa
         return orc.rope_tables(rd, max_seq, theta)
+    if _yarn(c):
+        cs, sn, _ = orc.rope_tables_yarn(rd, max_seq, c.rope_freq_base, c.rope_scaling_factor,
+                                         c.rope_orig_context_length, c.yarn_log_multiplier)
+        return cs, sn
     lin = c.rope_scaling_factor if c.rope_scaling_factor > 1.0 else 1.0
     return orc.rope_tables(rd, max_seq, c.rope_freq_base, lin)
 

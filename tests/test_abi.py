@@ -93,6 +93,19 @@ def test_rope_table_helper_freq_factors():
     assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
 
 
+@pytest.mark.parametrize("R,S,theta,sf,L,lm", [(64, 300, 1.5e5, 32.0, 4096, 0.0),
+                                              (128, 700, 1e6, 4.0, 32768, 0.0707),
+                                              (128, 64, 1e4, 1.0, 4096, 0.1)])
+def test_rope_table_yarn_helper_is_bit_identical_to_oracle(R, S, theta, sf, L, lm):
+    c1, s1, m1 = hfp.rope_table_yarn(R, S, theta, sf, L, lm)
+    c2, s2, m2 = orc.rope_tables_yarn(R, S, theta, sf, L, lm)
+    assert np.array_equal(c1, c2) and np.array_equal(s1, s2) and m1 == m2
+    ff = np.linspace(1, 4, R // 2).astype(np.float32)
+    c1, s1, m1 = hfp.rope_table_yarn(R, S, theta, sf, L, lm, freq_factors=ff)
+    c2, s2, m2 = orc.rope_tables_yarn(R, S, theta, sf, L, lm, freq_factors=ff)
+    assert np.array_equal(c1, c2) and np.array_equal(s1, s2) and m1 == m2
+
+
 def test_rope_table_rejects_bad_args():
     out = np.zeros(4, np.float32)
     p = out.ctypes.data_as(C.POINTER(C.c_float))

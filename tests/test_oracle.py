@@ -141,6 +141,52 @@ def test_rope_linear_scale_divides_frequencies():
     np.testing.assert_allclose(s8[::8][:S], s1[:S], atol=2e-5)
 
 
+# ---- YaRN tables (RoPE.java:45-117): closed forms of the NTK-by-parts blend -----------------
+def _yarn_dims(R, theta, L, beta_fast=32.0, beta_slow=1.0):
+    """The correction dims of the YaRN paper, R*ln(L/(2*pi*beta)) / (2*ln(theta)), in float64."""
+    def corr(beta):
+        return R * np.log(L / (beta * 2 * np.pi)) / (2 * np.log(theta))
+    return max(0.0, np.floor(corr(beta_fast))), min(R / 2 - 1, np.ceil(corr(beta_slow)))
+
+
+def test_rope_yarn_factor_one_is_the_plain_table():
+    c0, s0 = orc.rope_tables(64, 300, 1.5e5)
+    c1, s1, ms = orc.rope_tables_yarn(64, 300, 1.5e5, 1.0, 4096, 0.1)
+    assert np.array_equal(c0, c1) and np.array_equal(s0, s1) and ms == 1.0
+
+
+@pytest.mark.parametrize("R,theta,s,L", [(64, 1.5e5, 32.0, 4096), (128, 1e6, 4.0, 32768),
+                                         (128, 1e4, 40.0, 4096)])
+def test_rope_yarn_blend_and_correction_dims(R, theta, s, L):
+    """Dims up to the fast correction dim keep the base frequency (bit-identical to the plain
+    table), dims from the slow one on take base/s (bit-identical to the linear-scaled table), and
+    the dims between blend linearly in the dim index."""
+    S = 64
+    cy, sy, _ = orc.rope_tables_yarn(R, S, theta, s, L)
+    c1, s1 = orc.rope_tables(R, S, theta)
+    cs, ss = orc.rope_tables(R, S, theta, linear_freq_scale=s)
+    low, high = _yarn_dims(R, theta, L)
+    i = np.arange(R // 2)
+    ext, itp = i <= low, i >= high
+    assert ext.any() and itp.any() and (~ext & ~itp).any(), (low, high)
+    assert np.array_equal(cy[:, ext], c1[:, ext]) and np.array_equal(sy[:, ext], s1[:, ext])
+    assert np.array_equal(cy[:, itp], cs[:, itp]) and np.array_equal(sy[:, itp], ss[:, itp])
+    # between: at pos 1 the angle is the frequency itself
+    base = 1.0 / np.power(np.float64(F32(theta)), 2.0 * i / R)
+    ramp = 1.0 - np.clip((i - low) / max(0.001, high - low), 0.0, 1.0)
+    want = base * ramp + base / s * (1 - ramp)
+    mid = ~ext & ~itp
+    np.testing.assert_allclose(np.arcsin(sy[1, mid].astype(np.float64)), want[mid], rtol=2e-6)
+    assert np.all(np.diff(np.arcsin(sy[1].astype(np.float64))) < 0)   # frequencies decrease
+
+
+@pytest.mark.parametrize("s,log_mul", [(32.0, 0.0), (40.0, 0.0707), (4.0, 1.0)])
+def test_rope_yarn_mscale_closed_form(s, log_mul):
+    _, _, ms = orc.rope_tables_yarn(64, 4, 1e4, s, 4096, log_mul)
+    attn = 0.1 * log_mul * np.log(s) + 1.0 if log_mul > 0 else 1.0
+    assert abs(float(ms) - attn * (1.0 + 0.1 * np.log(s))) < 2e-6
+
+
 @pytest.mark.parametrize("rope_type", [0, 2])
 def test_rope_apply_identity_at_pos0_and_pairing(rope_type):
     H, D, R = 3, 64, 64

@@ -48,6 +48,30 @@ def test_gptoss_sinks_decode_both_window_kinds(pos, splits):
             dc.compare_cache(fp, layer, kc, vc, "gpt-oss sinks cache", rows=(0, pos + 1))
 
 
+@pytest.mark.parametrize("pos", [5, 300, 3000])
+def test_gptoss_yarn_tables_and_mscale_scale(pos):
+    """GPT-OSS with its YaRN RoPE (factor 32 over a 4096-token original context) as the MoE
+    engine builds it: the host mirror makes the tables with llmp_rope_table_yarn and sets the
+    layer scale to mscale^2/sqrt(headSize) (Qwen3MoEInferenceEngine.java:60-66, 277-279); the
+    oracle builds its own (orc_rope_tables_yarn)."""
+    c = hfp.ModelConfig(64, 8, 64, 2, architecture=hfp.ARCH_GPT_OSS, rope_freq_base=150000.0,
+                        sliding_window=128, expert_count=32, rope_scaling_factor=32.0,
+                        rope_orig_context_length=4096, yarn_log_multiplier=0.0)
+    sinks = _sinks(c, 40)
+    with hfp.HipForwardPass(c, 4096, sinks=sinks) as fp:
+        assert abs(float(fp.mscale) - (1.0 + 0.1 * np.log(32.0))) < 2e-6
+        for layer in (0, 1):
+            d = dc.make_layer(c, 4096, pos, seed=400 + layer + pos)
+            dc.log(f"[gpu] gpt-oss yarn decode layer {layer} pos {pos}")
+            fp.kv.write(layer, 0, d.kc, d.vc)
+            st = hfp.InferenceState.create(c)
+            st.q[:], st.k[:], st.v[:] = d.q, d.k, d.v
+            fp.forwardAttentionOnly(st, layer, pos)
+            want, kc, vc = dc.oracle_call(c, 4096, d, layer, pos, n_threads=16, sinks=sinks[layer])
+            dc.compare_out(st.xb2, want, f"gpt-oss yarn layer {layer} pos {pos}")
+            dc.compare_cache(fp, layer, kc, vc, "gpt-oss yarn cache", rows=(0, pos + 1))
+
+
 def test_sinks_can_be_removed_and_q8_cache_and_device_position():
     c = _gptoss(window=0)
     sinks = _sinks(c, 20)
