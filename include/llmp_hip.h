@@ -94,8 +94,9 @@ int llmp_event_elapsed_ms(float *ms, uint64_t start, uint64_t end);
  * [layer][K|V][kv_head][pos][head_dim] fp32.  LLMP_KV_Q8_0(_TRUNC): per layer the K quants
  * [kv_head][pos][head_dim] int8, K scales [kv_head][pos][head_dim/32] fp32, then the same for
  * V.  Fails with LLMP_ERR_OUT_OF_MEMORY when the pool would not fit in free HBM.  head_dim must
- * be 64, 128, 256 or 512 (512: fp32 caches and decode only, the full-attention layers of
- * Gemma 4, whose two head sizes take one handle each). */
+ * be 64, 128 or 256 (any cache type, GQA groups 1-8), 96 (fp32 caches, groups 1-4: Phi-3), 80
+ * (fp32 caches, groups 1-2, decode only: Phi-2) or 512 (fp32 caches and decode only, the
+ * full-attention layers of Gemma 4, whose two head sizes take one handle each). */
 int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int dtype,
                    uint64_t *handle);
 int llmp_kv_destroy(uint64_t handle);
@@ -376,7 +377,8 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
  * each fp32 input split into two fp16 parts (fp32-accurate products, fp32 sums in another order
  * than the CPU path; inputs below 65504); the attention is llmp_attn_prefill_f32's (the appended
  * rows bit-identical to single-token appends of the same projections).  In the
- * LLMP_INPUT_Q8_1 mode the tokens run one llmp_attn_block call each.  The call may grow the
+ * LLMP_INPUT_Q8_1 mode (and at head_dim 80, which has no prefill kernel) the tokens run one
+ * llmp_attn_block call each.  The call may grow the
  * handle's prefill workspace, as llmp_attn_prefill_f32 does (not for use under graph capture
  * then). */
 int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t x,

@@ -1,6 +1,7 @@
 // Instantiation and dispatch of the decode kernels (decode_kernels.h) for the shapes the
-// library ships: head_dim 64/128/256 (fp32 and Q8_0 caches) and 512 (fp32: the full-attention
-// layers of Gemma 4), GQA groups 1, 2, 3, 4, 6, 8.
+// library ships: head_dim 64/128/256 (fp32 and Q8_0 caches) with GQA groups 1-8, 512 (fp32: the
+// full-attention layers of Gemma 4) with groups 1-8, 96 (fp32: Phi-3) with groups 1-4 and 80
+// (fp32: Phi-2) with groups 1-2.
 #include "decode_kernels.h"
 
 namespace llmp {
@@ -17,7 +18,11 @@ struct Tune {
 constexpr Tune pick(int D, int G) {
     // head_dim 512: 8 elements per lane, so a row spans the whole wave (LPR 64).  head_dim 256
     // (16 elements per lane) and groups above 4 take one row per trip: two trips of two rows
-    // would not fit the register file next to the G*EPL query and output values.
+    // would not fit the register file next to the G*EPL query and output values.  head_dim 96
+    // and 80 need a power-of-two lane count per row: 12 elements (8 lanes) and 20 (4 lanes);
+    // 80's 20 elements per lane take one row per trip.
+    if (D == 96) return Tune{12, G > 4 ? 1 : 2, true};
+    if (D == 80) return Tune{20, 1, true};
     return Tune{D == 512 ? 8 : ((D == 256 || (G > 4 && D / 8 > 16)) ? 16 : 8),
                 (G > 4 || D == 256) ? 1 : 2, true};
 }
@@ -60,11 +65,27 @@ SplitKernel kernel_d(int group, int waves) {
     switch (group) {
     case 1: return kernel_dg<D, 1, Q8>(waves);
     case 2: return kernel_dg<D, 2, Q8>(waves);
-    case 3: return kernel_dg<D, 3, Q8>(waves);
-    case 4: return kernel_dg<D, 4, Q8>(waves);
-    case 6: return kernel_dg<D, 6, Q8>(waves);
-    case 8: return kernel_dg<D, 8, Q8>(waves);
-    default: return SplitKernel{nullptr, 0};
+    default: break;
+    }
+    if constexpr (D == 80) {   // 20 elements per lane: groups beyond 2 would spill
+        return SplitKernel{nullptr, 0};
+    } else {
+        switch (group) {
+        case 3: return kernel_dg<D, 3, Q8>(waves);
+        case 4: return kernel_dg<D, 4, Q8>(waves);
+        default: break;
+        }
+    }
+    if constexpr (D == 80 || D == 96) {   // head sizes of MHA / small-group models
+        return SplitKernel{nullptr, 0};
+    } else {
+        switch (group) {
+        case 5: return kernel_dg<D, 5, Q8>(waves);
+        case 6: return kernel_dg<D, 6, Q8>(waves);
+        case 7: return kernel_dg<D, 7, Q8>(waves);
+        case 8: return kernel_dg<D, 8, Q8>(waves);
+        default: return SplitKernel{nullptr, 0};
+        }
     }
 }
 
@@ -74,8 +95,12 @@ SplitKernel kernel_split(int head_dim, int group, int waves) {
     case 64: return kernel_d<64, Q8>(group, waves);
     case 128: return kernel_d<128, Q8>(group, waves);
     case 256: return kernel_d<256, Q8>(group, waves);
-    case 512:
-        if constexpr (!Q8) return kernel_d<512, false>(group, waves);
+    case 80: case 96: case 512:   // fp32 caches only
+        if constexpr (!Q8) {
+            if (head_dim == 80) return kernel_d<80, false>(group, waves);
+            if (head_dim == 96) return kernel_d<96, false>(group, waves);
+            return kernel_d<512, false>(group, waves);
+        }
         return SplitKernel{nullptr, 0};
     default: return SplitKernel{nullptr, 0};
     }
@@ -96,10 +121,10 @@ __global__ void copy_kernel(float4* __restrict__ dst, const float4* __restrict__
 }  // namespace
 
 bool decode_shape_supported(int head_dim, int group) {
+    if (head_dim == 80) return group >= 1 && group <= 2;
+    if (head_dim == 96) return group >= 1 && group <= 4;
     const bool d_ok = head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512;
-    const bool g_ok = group == 1 || group == 2 || group == 3 || group == 4 || group == 6 ||
-                      group == 8;
-    return d_ok && g_ok;
+    return d_ok && group >= 1 && group <= 8;
 }
 
 int decode_split_waves(int head_dim, int group, int waves, bool q8) {
@@ -142,6 +167,14 @@ hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, in
         break;
     case 512:
         hipLaunchKernelGGL(dk::decode_reduce_kernel<512>, dim3(n_heads),
+                           dim3(dk::kReduceThreads), 0, stream, a, group);
+        break;
+    case 80:
+        hipLaunchKernelGGL(dk::decode_reduce_kernel<80>, dim3(n_heads),
+                           dim3(dk::kReduceThreads), 0, stream, a, group);
+        break;
+    case 96:
+        hipLaunchKernelGGL(dk::decode_reduce_kernel<96>, dim3(n_heads),
                            dim3(dk::kReduceThreads), 0, stream, a, group);
         break;
     default: return hipErrorInvalidValue;

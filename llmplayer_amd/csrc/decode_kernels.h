@@ -660,7 +660,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     //    Without QK-norm and with RoPE pairs inside a lane, q is rotated in registers;
     //    otherwise it is prepared in LDS with the exact QK-norm order.
     const bool rope = a.cos_t != nullptr, qkn = a.qnw != nullptr;
-    const bool pairs_in_lane = a.rope_type == 0 || (!Q8 && 2 * a.half_rope == D);
+    // NEOX pairs (i, i + D/2) share a lane only when the lane's chunks split evenly in halves
+    const bool pairs_in_lane = a.rope_type == 0 || (!Q8 && C4 % 2 == 0 && 2 * a.half_rope == D);
     const bool reg_prologue = !qkn && (!rope || pairs_in_lane);
     const bool lds_prep = !reg_prologue || has_pos;
     float qr[G][EPL];
@@ -1279,6 +1280,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
     const int kvh = hq / G, h = hq - kvh * G;
     const int tid = threadIdx.x;
     const int c = tid % NC, p = tid / NC;
+    const bool act = p < NP;   // NC need not divide the block: the spare threads only sync
     const int pos = step_position(a);
     if (pos < 0 || pos >= a.max_seq) return;
     const int S = plan_step(pos, a.window, a.splits).splits;
@@ -1327,11 +1329,11 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
         o.w = __builtin_fmaf(o.w, so, oj.w * sj);
         m = mn;
     }
-    if (c == 0) {
+    if (act && c == 0) {
         s_m[p] = m;
         s_l[p] = l;
     }
-    s_o[p][c] = o;
+    if (act) s_o[p][c] = o;
     __syncthreads();
     if (p == 0) {
         float M = s_m[0];

@@ -609,15 +609,16 @@ int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int 
     if (n_layers <= 0 || max_seq <= 0 || n_kv_heads <= 0)
         return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: n_layers=%d max_seq=%d n_kv_heads=%d",
                     n_layers, max_seq, n_kv_heads);
-    if (head_dim != 64 && head_dim != 128 && head_dim != 256 && head_dim != 512)
+    if (head_dim != 64 && head_dim != 80 && head_dim != 96 && head_dim != 128 && head_dim != 256 &&
+        head_dim != 512)
         return fail(LLMP_ERR_UNSUPPORTED,
-                    "llmp_kv_create: head_dim %d (supported: 64, 128, 256, 512)", head_dim);
+                    "llmp_kv_create: head_dim %d (supported: 64, 80, 96, 128, 256, 512)", head_dim);
     if (dtype != LLMP_KV_F32 && dtype != LLMP_KV_Q8_0 && dtype != LLMP_KV_Q8_0_TRUNC)
         return fail(LLMP_ERR_UNSUPPORTED,
                     "llmp_kv_create: dtype %d (LLMP_KV_F32, LLMP_KV_Q8_0 or LLMP_KV_Q8_0_TRUNC)",
                     dtype);
-    if (head_dim == 512 && dtype != LLMP_KV_F32)
-        return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: head_dim 512 needs an fp32 cache");
+    if ((head_dim == 512 || head_dim == 80 || head_dim == 96) && dtype != LLMP_KV_F32)
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_create: head_dim %d needs an fp32 cache", head_dim);
     if ((long long)max_seq * head_dim >= (1LL << 31))
         return fail(LLMP_ERR_INVALID_ARG, "llmp_kv_create: max_seq*head_dim exceeds 2^31");
     auto kv = std::make_unique<KvHandle>();
@@ -1384,7 +1385,8 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
         return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: layer %d lacks projection weights", layer);
     if (!x || (x & 15)) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: null or misaligned x");
     const int D = kv->head_dim, qd = c.n_heads * D, kvd = kv->n_kv_heads * D, dim = kv->blk_dim;
-    if (kv->blk_input == LLMP_INPUT_Q8_1) {
+    if (kv->blk_input == LLMP_INPUT_Q8_1 || prefill_tile_keys(D) <= 0) {
+        // the Q8_1 contract's int8 dot products, or a head size with decode kernels only
         for (int t = 0; t < n_tokens; ++t)
             if (int rc = enqueue_block(kv, layer, pos0 + t, 0, x + (uint64_t)t * dim * sizeof(float), 0,
                                        stream))

@@ -7,7 +7,9 @@ namespace llmp {
 namespace {
 
 constexpr int kAppendThreads = 256;
-constexpr int kTileThreads = 256;
+// Tile-image threads: the tile's K and V^T work must divide evenly (head_dim 96: 192 threads).
+template <int D>
+constexpr int tile_threads() { return D == 96 ? 192 : 256; }
 
 // Launch shape of the attention kernel: one query head per wave (HPW 1, measured best at the
 // C5 shape: each wave's K/V fragments feed its MFMAs while occupancy stays at 4 waves/SIMD),
@@ -28,10 +30,14 @@ template <int D, int G, int NB>
 hipError_t launch_attn_dgn(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
                            int ksplit, hipStream_t stream) {
     const int items = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
-    if (ksplit > 1 && a.kq != nullptr)   // few query blocks: stage from the cache, no images
+    if constexpr (D == 96) {   // fp32 caches only at head_dim 96
+        if (a.kq != nullptr) return hipErrorInvalidValue;
+    } else if (ksplit > 1 && a.kq != nullptr) {   // few query blocks: stage from the cache
         hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, true, true>), dim3(items, ksplit),
                            dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
-    else if (ksplit > 1)
+        return hipGetLastError();
+    }
+    if (ksplit > 1)
         hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, true>), dim3(items, ksplit),
                            dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
     else
@@ -59,9 +65,18 @@ hipError_t launch_attn_d(const pk::PrefillArgs& a, int group, const uint4* ws, i
     case 2: return launch_attn_dg<D, 2>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
     case 3: return launch_attn_dg<D, 3>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
     case 4: return launch_attn_dg<D, 4>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
-    case 6: return launch_attn_dg<D, 6>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
-    case 8: return launch_attn_dg<D, 8>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
-    default: return hipErrorInvalidValue;
+    default: break;
+    }
+    if constexpr (D == 96) {   // decode's head_dim-96 groups: 1-4
+        return hipErrorInvalidValue;
+    } else {
+        switch (group) {
+        case 5: return launch_attn_dg<D, 5>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+        case 6: return launch_attn_dg<D, 6>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+        case 7: return launch_attn_dg<D, 7>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+        case 8: return launch_attn_dg<D, 8>(a, ws, tile0, n_tiles, n_cu, ksplit, stream);
+        default: return hipErrorInvalidValue;
+        }
     }
 }
 
@@ -75,12 +90,16 @@ hipError_t launch_combine_d(const pk::PrefillArgs& a, int ksplit, hipStream_t st
 template <int D>
 hipError_t launch_tiles_d(const pk::PrefillArgs& a, uint4* ws, int tile0, int n_tiles,
                           int row_end, hipStream_t stream) {
-    if (a.kq != nullptr)
-        hipLaunchKernelGGL((pk::prefill_tile_kernel<D, kTileThreads, true>), dim3(n_tiles, a.Hkv),
-                           dim3(kTileThreads), 0, stream, a, ws, tile0, n_tiles, row_end);
-    else
-        hipLaunchKernelGGL((pk::prefill_tile_kernel<D, kTileThreads, false>), dim3(n_tiles, a.Hkv),
-                           dim3(kTileThreads), 0, stream, a, ws, tile0, n_tiles, row_end);
+    constexpr int NT = tile_threads<D>();
+    if constexpr (D == 96) {   // fp32 caches only at head_dim 96
+        if (a.kq != nullptr) return hipErrorInvalidValue;
+    } else if (a.kq != nullptr) {
+        hipLaunchKernelGGL((pk::prefill_tile_kernel<D, NT, true>), dim3(n_tiles, a.Hkv), dim3(NT), 0,
+                           stream, a, ws, tile0, n_tiles, row_end);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((pk::prefill_tile_kernel<D, NT, false>), dim3(n_tiles, a.Hkv), dim3(NT), 0,
+                       stream, a, ws, tile0, n_tiles, row_end);
     return hipGetLastError();
 }
 
@@ -97,6 +116,7 @@ hipError_t launch_append_d(const pk::PrefillArgs& a, hipStream_t stream) {
 hipError_t launch_prefill_append(const pk::PrefillArgs& a, int head_dim, hipStream_t stream) {
     switch (head_dim) {
     case 64: return launch_append_d<64>(a, stream);
+    case 96: return launch_append_d<96>(a, stream);
     case 128: return launch_append_d<128>(a, stream);
     case 256: return launch_append_d<256>(a, stream);
     default: return hipErrorInvalidValue;
@@ -106,6 +126,7 @@ hipError_t launch_prefill_append(const pk::PrefillArgs& a, int head_dim, hipStre
 int prefill_tile_keys(int head_dim) {
     switch (head_dim) {
     case 64: return pk::TileLds<64>::TK;
+    case 96: return pk::TileLds<96>::TK;
     case 128: return pk::TileLds<128>::TK;
     case 256: return pk::TileLds<256>::TK;
     default: return 0;
@@ -115,6 +136,7 @@ int prefill_tile_keys(int head_dim) {
 size_t prefill_tile_bytes(int head_dim) {
     switch (head_dim) {
     case 64: return sizeof(pk::TileLds<64>);
+    case 96: return sizeof(pk::TileLds<96>);
     case 128: return sizeof(pk::TileLds<128>);
     case 256: return sizeof(pk::TileLds<256>);
     default: return 0;
@@ -126,6 +148,7 @@ hipError_t launch_prefill_tiles(const pk::PrefillArgs& a, int head_dim, void* ws
     uint4* w = static_cast<uint4*>(ws);
     switch (head_dim) {
     case 64: return launch_tiles_d<64>(a, w, tile0, n_tiles, row_end, stream);
+    case 96: return launch_tiles_d<96>(a, w, tile0, n_tiles, row_end, stream);
     case 128: return launch_tiles_d<128>(a, w, tile0, n_tiles, row_end, stream);
     case 256: return launch_tiles_d<256>(a, w, tile0, n_tiles, row_end, stream);
     default: return hipErrorInvalidValue;
@@ -153,6 +176,7 @@ hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group
     hipError_t e;
     switch (head_dim) {
     case 64: e = launch_attn_d<64>(a, group, w, tile0, n_tiles, n_cu, ksplit, stream); break;
+    case 96: e = launch_attn_d<96>(a, group, w, tile0, n_tiles, n_cu, ksplit, stream); break;
     case 128: e = launch_attn_d<128>(a, group, w, tile0, n_tiles, n_cu, ksplit, stream); break;
     case 256: e = launch_attn_d<256>(a, group, w, tile0, n_tiles, n_cu, ksplit, stream); break;
     default: return hipErrorInvalidValue;
@@ -160,6 +184,7 @@ hipError_t launch_prefill_attn(const pk::PrefillArgs& a, int head_dim, int group
     if (e != hipSuccess || ksplit <= 1) return e;
     switch (head_dim) {
     case 64: return launch_combine_d<64>(a, ksplit, stream);
+    case 96: return launch_combine_d<96>(a, ksplit, stream);
     case 128: return launch_combine_d<128>(a, ksplit, stream);
     default: return launch_combine_d<256>(a, ksplit, stream);
     }

@@ -773,6 +773,7 @@ __global__ __launch_bounds__(kCombineThreads) void prefill_combine_kernel(Prefil
     const long long rows = (long long)a.P * a.Hq;
     const long long row = blockIdx.x;                 // token * Hq + head
     const int tid = threadIdx.x, c = tid % NC, p = tid / NC;
+    const bool act = p < NP;   // NC need not divide the block: the spare threads only sync
     const int hq = (int)(row % a.Hq);
     float m = kNegBig, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -790,11 +791,11 @@ __global__ __launch_bounds__(kCombineThreads) void prefill_combine_kernel(Prefil
         o.w = __builtin_fmaf(o.w, so, x.w * sx);
         m = mn;
     }
-    if (c == 0) {
+    if (act && c == 0) {
         s_m[p] = m;
         s_l[p] = l;
     }
-    s_o[p][c] = o;
+    if (act) s_o[p][c] = o;
     __syncthreads();
     if (p == 0) {
         float M = s_m[0];

@@ -393,9 +393,17 @@ class HipForwardPass:
             return False
         if config.head_count % config.head_count_kv:
             return False
-        if config.head_size not in (64, 128, 256):
-            return False
-        if config.head_count // config.head_count_kv not in (1, 2, 3, 4, 6, 8):
+        group = config.head_count // config.head_count_kv
+        if config.head_size in (64, 128, 256):
+            if not 1 <= group <= 8:
+                return False
+        elif config.head_size == 96:         # fp32 caches, groups 1-4 (Phi-3)
+            if not 1 <= group <= 4:
+                return False
+        elif config.head_size == 80:         # fp32 caches, groups 1-2, decode only (Phi-2)
+            if not 1 <= group <= 2:
+                return False
+        else:
             return False
         rd = config.rope_dim_count or config.head_size
         return rd % 2 == 0 and rd <= config.head_size

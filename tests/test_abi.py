@@ -116,9 +116,10 @@ def test_is_supported_for_attention():
     ok = hfp.ModelConfig(24, 8, 128, 28)
     assert hfp.HipForwardPass.isSupportedForAttention(ok)
     assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(24, 8, 128, 28, use_layer_norm=True))
-    assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(24, 8, 96, 28))
-    assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(40, 8, 128, 28))  # group 5
-    assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(24, 7, 128, 28))
+    for h, kv, d in ((24, 8, 96), (40, 8, 128), (28, 4, 128), (32, 32, 80), (16, 8, 80)):
+        assert hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(h, kv, d, 28)), (h, kv, d)
+    for h, kv, d in ((24, 7, 128), (36, 4, 128), (24, 4, 96), (24, 8, 80), (16, 4, 112)):
+        assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(h, kv, d, 28)), (h, kv, d)
 
 
 def test_global_layer_and_rope_type_host_logic_match_oracle():

@@ -191,9 +191,10 @@ def test_error_codes():
             kv.destroy()
         # unsupported shapes
         hd = C.c_uint64()
-        assert _lib.status("llmp_kv_create", 1, 16, 2, 96, 0, C.byref(hd)) == 6
-        assert _lib.status("llmp_layer_config", h, 0, 10, 2, 64, 0, 0, 0, 1, 0.0, 0.0, 1e-5,
-                           None, None) == 6   # group 5 has no kernel
+        assert _lib.status("llmp_kv_create", 1, 16, 2, 112, 0, C.byref(hd)) == 6
+        assert _lib.status("llmp_kv_create", 1, 16, 2, 96, 1, C.byref(hd)) == 6   # Q8_0 at 96
+        assert _lib.status("llmp_layer_config", h, 0, 18, 2, 64, 0, 0, 0, 1, 0.0, 0.0, 1e-5,
+                           None, None) == 6   # group 9 has no kernel
         # an allocation beyond HBM is refused before touching the device
         assert _lib.status("llmp_kv_create", 4096, 1 << 20, 64, 128, 0, C.byref(hd)) == 5
 
