@@ -1,0 +1,166 @@
+// Host-side layout arithmetic of the library, in plain C++ with no HIP dependency so that the
+// same code also builds with g++ under AddressSanitizer / UndefinedBehaviorSanitizer for the
+// CPU tests:
+//  - the decode step plan (window start, attended rows, rows per split), shared with the kernels;
+//  - the default split count of a decode call;
+//  - GGUF row sizes and the repacking of GGUF rows into the per-row planes the projection
+//    kernels read;
+//  - the re-layout between the reference's row-major KV arrays [pos][n_kv_heads * row] and the
+//    head-major staging the device planes use [n_kv_heads][pos][row].
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <cstring>
+#include <initializer_list>
+#include <vector>
+
+#include "llmp_hip.h"
+
+#ifdef __HIPCC__
+#define LLMP_HD __host__ __device__
+#else
+#define LLMP_HD
+#endif
+
+namespace llmp {
+
+// Step plan shared by host and kernels: window start, attended rows, rows per split (rounded
+// to 16 once there are at least 16 per split) and the splits that end up non-empty.
+struct StepPlan {
+    int start, n, rows_per_split, splits;
+};
+LLMP_HD inline StepPlan plan_step(int pos, int window, int max_splits) {
+    StepPlan p;
+    p.start = (window > 0 && pos - window + 1 > 0) ? pos - window + 1 : 0;
+    p.n = pos + 1 - p.start;
+    int s = max_splits < p.n ? max_splits : p.n;
+    if (s < 1) s = 1;
+    int rps = (p.n + s - 1) / s;
+    if (p.n >= 16 * s) rps = (rps + 15) & ~15;
+    p.rows_per_split = rps;
+    p.splits = (p.n + rps - 1) / rps;
+    return p;
+}
+
+// Default split count of a decode step over n attended rows, given the CUs and the workgroups
+// of the chosen kernel resident per CU (per_cu; 1 for fp32 caches, which aim at one workgroup
+// per CU):
+//  - fp32: at least 32 rows per split, at most 128 splits per KV head; once a split holds 1024
+//    rows or more, `wide` is set (8-wave workgroups) and 3/4 of the splits run.
+//  - Q8_0: one full round of resident workgroups over the chip, at least 160 rows per split.
+inline int default_splits(int n, int n_kv_heads, int n_cu, int per_cu, bool q8, bool* wide) {
+    const int cu = n_cu > 0 ? n_cu : 256;
+    const int min_rows = q8 ? 160 : 32;
+    const int by_rows = n / min_rows > 0 ? n / min_rows : 1;
+    if (per_cu < 1) per_cu = 1;
+    long long s = ((long long)per_cu * cu + n_kv_heads - 1) / n_kv_heads;
+    if (s > by_rows) s = by_rows;
+    if (s > 128) s = 128;
+    if (s < 1) s = 1;
+    *wide = false;
+    if (!q8 && n / s >= 1024) {
+        *wide = true;
+        s = (3 * s + 3) / 4;
+    }
+    return (int)s;
+}
+
+// Bytes of one row of `cols` weights in a GGML type's GGUF layout (GGMLType.java:4-35); 0 for
+// a type the library does not read.
+inline size_t ggml_row_bytes(int type, int cols) {
+    switch (type) {
+    case LLMP_GGML_F32: return (size_t)cols * 4;
+    case LLMP_GGML_F16:
+    case LLMP_GGML_BF16: return (size_t)cols * 2;
+    case LLMP_GGML_Q8_0: return (size_t)(cols / 32) * 34;
+    case LLMP_GGML_Q4_0: return (size_t)(cols / 32) * 18;
+    case LLMP_GGML_Q4_K: return (size_t)(cols / 256) * 144;
+    case LLMP_GGML_Q6_K: return (size_t)(cols / 256) * 210;
+    default: return 0;
+    }
+}
+
+inline size_t pad256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Repacks `rows` GGUF rows of `cols` weights (src, ggml_row_bytes(type, cols) bytes each) into
+// the planes the projection kernels read: every row's bytes of one plane are contiguous
+// (pitch[i] bytes per row) and each plane starts 256-byte aligned at off[i] in dst.  Per GGUF
+// block the pieces go to:
+//  - Q8_0: quants -> plane 0, fp16 scale -> plane 1;
+//  - Q4_0: nibbles -> plane 0, fp16 scale -> plane 1;
+//  - Q4_K: d, dmin and the 12 packed scale bytes -> plane 1, nibbles -> plane 0;
+//  - Q6_K: low nibbles -> 0, high bit pairs -> 1, int8 scales -> 2, fp16 d -> 3;
+//  - F32/F16/BF16: one plane, the rows unchanged.
+// Returns the plane count, or 0 for an unsupported type or a cols that is not a whole number
+// of blocks.
+inline int repack_weight(int type, int rows, int cols, const uint8_t* src, std::vector<uint8_t>& dst,
+                         size_t off[4], size_t pitch[4]) {
+    const size_t rb = ggml_row_bytes(type, cols);
+    if (rb == 0 || rows < 0 || cols <= 0) return 0;
+    int n = 1;
+    struct Piece { int plane; size_t src_off, len; };   // per block: bytes [src_off, +len) -> plane
+    Piece pieces[4];
+    int n_pieces = 0;
+    size_t bw = 0, blk_bytes = 0;   // weights and bytes per GGUF block
+    auto set = [&](std::initializer_list<Piece> l) {
+        for (const Piece& p : l) pieces[n_pieces++] = p;
+    };
+    switch (type) {
+    case LLMP_GGML_F32: case LLMP_GGML_F16: case LLMP_GGML_BF16:
+        pitch[0] = rb; break;
+    case LLMP_GGML_Q8_0:
+        n = 2; bw = 32; blk_bytes = 34; pitch[0] = (size_t)cols; pitch[1] = (size_t)cols / 32 * 2;
+        set({{1, 0, 2}, {0, 2, 32}}); break;
+    case LLMP_GGML_Q4_0:
+        n = 2; bw = 32; blk_bytes = 18; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32 * 2;
+        set({{1, 0, 2}, {0, 2, 16}}); break;
+    case LLMP_GGML_Q4_K:
+        n = 2; bw = 256; blk_bytes = 144; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 256 * 16;
+        set({{1, 0, 16}, {0, 16, 128}}); break;
+    case LLMP_GGML_Q6_K:
+        n = 4; bw = 256; blk_bytes = 210; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 4;
+        pitch[2] = (size_t)cols / 16; pitch[3] = (size_t)cols / 256 * 2;
+        set({{0, 0, 128}, {1, 128, 64}, {2, 192, 16}, {3, 208, 2}}); break;
+    default: return 0;
+    }
+    if (bw && cols % (int)bw) return 0;
+    off[0] = 0;
+    for (int i = 1; i < n; ++i) off[i] = pad256(off[i - 1] + (size_t)rows * pitch[i - 1]);
+    dst.assign(pad256(off[n - 1] + (size_t)rows * pitch[n - 1]), 0);
+    if (n_pieces == 0) {
+        for (int r = 0; r < rows; ++r) std::memcpy(&dst[(size_t)r * pitch[0]], src + (size_t)r * rb, rb);
+        return n;
+    }
+    const size_t nb = (size_t)cols / bw;
+    for (int r = 0; r < rows; ++r)
+        for (size_t b = 0; b < nb; ++b) {
+            const uint8_t* blk = src + (size_t)r * rb + b * blk_bytes;
+            for (int i = 0; i < n_pieces; ++i) {
+                const Piece& pc = pieces[i];
+                std::memcpy(&dst[off[pc.plane] + (size_t)r * pitch[pc.plane] + b * pc.len],
+                            blk + pc.src_off, pc.len);
+            }
+        }
+    return n;
+}
+
+// Re-layout between n rows of the reference's KV arrays, host[t][h * row + j] (t < n, h < H,
+// j < row bytes), and the head-major staging stage[h][t][row], in which each KV head's n rows
+// are one contiguous span of n * row bytes.
+inline void rows_to_heads(const void* host, void* stage, size_t H, size_t n, size_t row) {
+    const char* hp = static_cast<const char*>(host);
+    char* sp = static_cast<char*>(stage);
+    const size_t span = row * n, host_row = row * H;
+    for (size_t t = 0; t < n; ++t)
+        for (size_t h = 0; h < H; ++h) std::memcpy(sp + h * span + t * row, hp + t * host_row + h * row, row);
+}
+inline void heads_to_rows(const void* stage, void* host, size_t H, size_t n, size_t row) {
+    const char* sp = static_cast<const char*>(stage);
+    char* hp = static_cast<char*>(host);
+    const size_t span = row * n, host_row = row * H;
+    for (size_t t = 0; t < n; ++t)
+        for (size_t h = 0; h < H; ++h) std::memcpy(hp + t * host_row + h * row, sp + h * span + t * row, row);
+}
+
+}  // namespace llmp

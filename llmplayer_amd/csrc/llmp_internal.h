@@ -6,6 +6,8 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "host_layout.h"
+
 namespace llmp {
 
 // Largest number of split-K partitions per KV head a decode call may use.
@@ -56,24 +58,6 @@ struct DecodeArgs {
     float softcap_log2e;   // softcap * log2(e)
     float inv_softcap;     // 1 / softcap
 };
-
-// Step plan shared by host and kernels: window start, attended rows, rows per split (rounded
-// to 16 once there are at least 16 per split) and the splits that end up non-empty.
-struct StepPlan {
-    int start, n, rows_per_split, splits;
-};
-__host__ __device__ inline StepPlan plan_step(int pos, int window, int max_splits) {
-    StepPlan p;
-    p.start = (window > 0 && pos - window + 1 > 0) ? pos - window + 1 : 0;
-    p.n = pos + 1 - p.start;
-    int s = max_splits < p.n ? max_splits : p.n;
-    if (s < 1) s = 1;
-    int rps = (p.n + s - 1) / s;
-    if (p.n >= 16 * s) rps = (rps + 15) & ~15;
-    p.rows_per_split = rps;
-    p.splits = (p.n + rps - 1) / rps;
-    return p;
-}
 
 // Launches the split-K kernel for head_dim D and GQA group G = Hq/Hkv on grid
 // (splits, Hkv) with `waves` (4 or 8) waves per workgroup requested, over an fp32

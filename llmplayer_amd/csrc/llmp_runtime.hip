@@ -234,40 +234,21 @@ int prof_fold(KvHandle* kv, int kind) {
     return LLMP_OK;
 }
 
-// Number of splits when the caller leaves the choice to the library, from sweeps over the
-// BASELINE shapes on MI355X (256 CUs in 8 XCDs): about one workgroup per CU, at least 32 rows
-// per split (below that the per-workgroup prologue and merge dominate) and at most 128 splits
-// per KV head.  Very long splits (>= 1024 rows) run 8-wave workgroups on 3/4 as many splits:
-// fewer concurrent KV streams, each read by more waves, keep HBM closer to its peak.
-// Default launch shape of a decode step over n attended rows.
-//  - fp32 cache (tuned on MI355X): about one workgroup per CU (at least 32 rows per split, at
-//    most 128 splits per KV head); 8-wave workgroups at 3/4 of those splits once a split has
-//    1024 rows or more.
+// Default launch shape of a decode step over n attended rows (default_splits, from sweeps over
+// the BASELINE shapes on MI355X, 256 CUs in 8 XCDs):
+//  - fp32 cache: about one workgroup per CU (below 32 rows per split the per-workgroup prologue
+//    and merge dominate); very long splits (>= 1024 rows) run 8-wave workgroups on 3/4 as many
+//    splits: fewer concurrent KV streams, each read by more waves, keep HBM closer to its peak.
 //  - Q8_0 cache: its rows are 3.6x shorter and its math per byte higher, so the kernel is
 //    bound by issue and latency: 4-wave workgroups, as many per CU as stay resident at once
-//    (one full round over the chip, no tail), and at least 160 rows per split so that each
-//    workgroup's fixed prologue and merge stay small next to its streaming (measured on
-//    MI355X at the Llama-3.2-3B shape: 96 splits best at 32k rows, 24 at 4k).
+//    (one full round over the chip, no tail), at least 160 rows per split (measured on MI355X
+//    at the Llama-3.2-3B shape: 96 splits best at 32k rows, 24 at 4k).
 void auto_launch(int n, int n_kv_heads, int n_cu, int head_dim, int group, bool q8, int* splits,
                  int* waves) {
-    const int cu = n_cu > 0 ? n_cu : 256;
-    const int min_rows = q8 ? 160 : 32;
-    const int by_rows = n / min_rows > 0 ? n / min_rows : 1;
-    int per_cu = 1, w = 4;
-    if (q8) {
-        per_cu = decode_split_blocks_per_cu(head_dim, group, 4, true);
-        if (per_cu < 1) per_cu = 1;
-    }
-    int s = (per_cu * cu + n_kv_heads - 1) / n_kv_heads;
-    if (s > by_rows) s = by_rows;
-    if (s > 128) s = 128;
-    if (s < 1) s = 1;
-    if (!q8 && n / s >= 1024) {
-        w = 8;
-        s = (3 * s + 3) / 4;
-    }
-    *splits = s;
-    *waves = decode_split_waves(head_dim, group, w, q8);
+    const int per_cu = q8 ? decode_split_blocks_per_cu(head_dim, group, 4, true) : 1;
+    bool wide = false;
+    *splits = default_splits(n, n_kv_heads, n_cu, per_cu, q8, &wide);
+    *waves = decode_split_waves(head_dim, group, wide ? 8 : 4, q8);
 }
 
 struct Plan {
@@ -696,13 +677,9 @@ static int check_rows(const KvHandle* kv, int layer, int pos0, int n) {
 // otherwise moved row by row).
 static int copy_plane(KvHandle* kv, void* dev_plane, size_t row, int pos0, int n, void* host,
                       bool to_host) {
-    const size_t H = (size_t)kv->n_kv_heads, host_row = row * H, span = row * (size_t)n;
+    const size_t H = (size_t)kv->n_kv_heads, span = row * (size_t)n;
     std::vector<char> stage(span * H);
-    char* hp = static_cast<char*>(host);
-    if (!to_host)
-        for (size_t t = 0; t < (size_t)n; ++t)
-            for (size_t h = 0; h < H; ++h)
-                std::memcpy(stage.data() + h * span + t * row, hp + t * host_row + h * row, row);
+    if (!to_host) rows_to_heads(host, stage.data(), H, (size_t)n, row);
     for (size_t h = 0; h < H; ++h) {
         char* dev = static_cast<char*>(dev_plane) + (h * (size_t)kv->max_seq + (size_t)pos0) * row;
         hipError_t e = to_host ? hipMemcpyAsync(stage.data() + h * span, dev, span,
@@ -713,10 +690,7 @@ static int copy_plane(KvHandle* kv, void* dev_plane, size_t row, int pos0, int n
     }
     // The staging buffer is released on return: every copy from or into it must be done.
     LLMP_HIP_CHECK(hipStreamSynchronize(G().stream), "hipStreamSynchronize");
-    if (to_host)
-        for (size_t t = 0; t < (size_t)n; ++t)
-            for (size_t h = 0; h < H; ++h)
-                std::memcpy(hp + t * host_row + h * row, stage.data() + h * span + t * row, row);
+    if (to_host) heads_to_rows(stage.data(), host, H, (size_t)n, row);
     return LLMP_OK;
 }
 
@@ -1035,67 +1009,6 @@ int llmp_layer_norm_mode(uint64_t handle, int layer, int mode) {
 }
 
 // ---- attention block: projections around the attention core ------------------------------
-// Bytes of one row of `cols` weights in a GGML type's GGUF layout (GGMLType.java:4-35).
-static size_t ggml_row_bytes(int type, int cols) {
-    switch (type) {
-    case LLMP_GGML_F32: return (size_t)cols * 4;
-    case LLMP_GGML_F16:
-    case LLMP_GGML_BF16: return (size_t)cols * 2;
-    case LLMP_GGML_Q8_0: return (size_t)(cols / 32) * 34;
-    case LLMP_GGML_Q4_0: return (size_t)(cols / 32) * 18;
-    case LLMP_GGML_Q4_K: return (size_t)(cols / 256) * 144;
-    case LLMP_GGML_Q6_K: return (size_t)(cols / 256) * 210;
-    default: return 0;
-    }
-}
-
-static size_t pad256(size_t b) { return (b + 255) & ~(size_t)255; }
-
-// Repacks GGUF rows into the planes gemv_kernels.h reads: every row's data of a plane is
-// contiguous and 16-byte chunks stay 16-byte aligned.  Returns the plane count.
-static int repack_weight(int type, int rows, int cols, const uint8_t* src, std::vector<uint8_t>& dst,
-                         size_t off[4], size_t pitch[4]) {
-    const size_t rb = ggml_row_bytes(type, cols);
-    int n = 1;
-    struct Piece { int plane; size_t src_off, len; };   // per block: bytes [src_off, +len) -> plane
-    std::vector<Piece> pieces;
-    size_t bw = 0, blk_bytes = 0;   // weights and bytes per GGUF block
-    switch (type) {
-    case LLMP_GGML_F32: case LLMP_GGML_F16: case LLMP_GGML_BF16:
-        pitch[0] = rb; break;
-    case LLMP_GGML_Q8_0:
-        n = 2; bw = 32; blk_bytes = 34; pitch[0] = (size_t)cols; pitch[1] = (size_t)cols / 32 * 2;
-        pieces = {{1, 0, 2}, {0, 2, 32}}; break;
-    case LLMP_GGML_Q4_0:
-        n = 2; bw = 32; blk_bytes = 18; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32 * 2;
-        pieces = {{1, 0, 2}, {0, 2, 16}}; break;
-    case LLMP_GGML_Q4_K:
-        n = 2; bw = 256; blk_bytes = 144; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 256 * 16;
-        pieces = {{1, 0, 16}, {0, 16, 128}}; break;
-    case LLMP_GGML_Q6_K:
-        n = 4; bw = 256; blk_bytes = 210; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 4;
-        pitch[2] = (size_t)cols / 16; pitch[3] = (size_t)cols / 256 * 2;
-        pieces = {{0, 0, 128}, {1, 128, 64}, {2, 192, 16}, {3, 208, 2}}; break;
-    default: return 0;
-    }
-    off[0] = 0;
-    for (int i = 1; i < n; ++i) off[i] = pad256(off[i - 1] + (size_t)rows * pitch[i - 1]);
-    dst.assign(pad256(off[n - 1] + (size_t)rows * pitch[n - 1]), 0);
-    if (pieces.empty()) {
-        for (int r = 0; r < rows; ++r) std::memcpy(&dst[(size_t)r * pitch[0]], src + (size_t)r * rb, rb);
-        return n;
-    }
-    const size_t nb = (size_t)cols / bw;
-    for (int r = 0; r < rows; ++r)
-        for (size_t b = 0; b < nb; ++b) {
-            const uint8_t* blk = src + (size_t)r * rb + b * blk_bytes;
-            for (const Piece& pc : pieces)
-                std::memcpy(&dst[off[pc.plane] + (size_t)r * pitch[pc.plane] + b * pc.len],
-                            blk + pc.src_off, pc.len);
-        }
-    return n;
-}
-
 // Byte offsets of the token-batched block scratch: q, k, v, the attention output and the
 // output projection of kTokBatch tokens (each region 256-byte aligned).
 struct BatchLayout {
@@ -1188,6 +1101,8 @@ int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int r
     std::vector<uint8_t> packed;
     size_t off[4] = {0, 0, 0, 0}, pitch[4] = {0, 0, 0, 0};
     const int np = repack_weight(ggml_type, rows, cols, static_cast<const uint8_t*>(data), packed, off, pitch);
+    if (np == 0)
+        return fail(LLMP_ERR_UNSUPPORTED, "llmp_layer_weight: %d columns for GGML type %d", cols, ggml_type);
     hipError_t e = hipMalloc(&w.mem, packed.size());
     if (e == hipErrorOutOfMemory)
         return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_layer_weight: %zu bytes", packed.size());

@@ -18,7 +18,8 @@ import numpy as np
 from typing import Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libattn_oracle.so")
+# LLMP_ORACLE_LIB names another build of the same sources (the sanitizer build of the CPU tests).
+_LIB_PATH = os.environ.get("LLMP_ORACLE_LIB") or os.path.join(_HERE, "libattn_oracle.so")
 _lib = None
 
 ARCH_OTHER, ARCH_GEMMA2, ARCH_GEMMA3, ARCH_GPT_OSS, ARCH_COHERE2, ARCH_GPT_OSS_MOE = 0, 1, 2, 3, 4, 5

@@ -1,0 +1,76 @@
+// CPU driver of the library's host-side layout code (llmplayer_amd/csrc/host_layout.h), built by
+// tests/test_host_sanitize.py with g++ under AddressSanitizer and UndefinedBehaviorSanitizer.
+// It reads one command per line on stdin and answers one line per command on stdout:
+//   repack TYPE ROWS COLS IN OUT      -> "planes off0 off1 off2 off3 pitch0 pitch1 pitch2 pitch3"
+//                                        (the packed bytes are written to OUT)
+//   relayout H N ROW IN HEADS BACK    -> "ok" (rows_to_heads(IN) to HEADS, heads_to_rows back to BACK)
+//   plan POS WINDOW SPLITS            -> "start n rows_per_split splits"
+//   splits N HKV NCU PERCU Q8         -> "splits wide"
+#include <cstdio>
+#include <fstream>
+#include <iostream>
+#include <iterator>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "host_layout.h"
+
+static std::vector<uint8_t> read_file(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    return std::vector<uint8_t>(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+}
+
+static void write_file(const std::string& path, const void* p, size_t n) {
+    std::ofstream f(path, std::ios::binary);
+    f.write(static_cast<const char*>(p), (std::streamsize)n);
+}
+
+int main() {
+    std::string line;
+    while (std::getline(std::cin, line)) {
+        std::istringstream in(line);
+        std::string cmd;
+        in >> cmd;
+        if (cmd == "repack") {
+            int type, rows, cols;
+            std::string src, dst;
+            in >> type >> rows >> cols >> src >> dst;
+            // exactly the GGUF bytes, on the heap, so that any read past them is caught
+            std::vector<uint8_t> data = read_file(src);
+            std::vector<uint8_t> packed;
+            size_t off[4] = {0, 0, 0, 0}, pitch[4] = {0, 0, 0, 0};
+            const int n = llmp::repack_weight(type, rows, cols, data.data(), packed, off, pitch);
+            write_file(dst, packed.data(), packed.size());
+            std::printf("%d %zu %zu %zu %zu %zu %zu %zu %zu\n", n, off[0], off[1], off[2], off[3],
+                        pitch[0], pitch[1], pitch[2], pitch[3]);
+        } else if (cmd == "relayout") {
+            size_t H, n, row;
+            std::string src, heads, back;
+            in >> H >> n >> row >> src >> heads >> back;
+            std::vector<uint8_t> host = read_file(src);
+            std::vector<uint8_t> stage(H * n * row), again(H * n * row);
+            llmp::rows_to_heads(host.data(), stage.data(), H, n, row);
+            llmp::heads_to_rows(stage.data(), again.data(), H, n, row);
+            write_file(heads, stage.data(), stage.size());
+            write_file(back, again.data(), again.size());
+            std::printf("ok\n");
+        } else if (cmd == "plan") {
+            int pos, window, splits;
+            in >> pos >> window >> splits;
+            const llmp::StepPlan p = llmp::plan_step(pos, window, splits);
+            std::printf("%d %d %d %d\n", p.start, p.n, p.rows_per_split, p.splits);
+        } else if (cmd == "splits") {
+            int n, hkv, ncu, per_cu, q8;
+            in >> n >> hkv >> ncu >> per_cu >> q8;
+            bool wide = false;
+            const int s = llmp::default_splits(n, hkv, ncu, per_cu, q8 != 0, &wide);
+            std::printf("%d %d\n", s, wide ? 1 : 0);
+        } else if (!cmd.empty()) {
+            std::printf("unknown command %s\n", cmd.c_str());
+            return 2;
+        }
+        std::fflush(stdout);
+    }
+    return 0;
+}

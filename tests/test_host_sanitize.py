@@ -1,0 +1,197 @@
+"""The CPU code of the library and of the oracle under AddressSanitizer and
+UndefinedBehaviorSanitizer:
+
+- llmplayer_amd/csrc/host_layout.h (GGUF weight repacking, the KV re-layout between the
+  reference's [pos][n_kv_heads * row] arrays and the head-major device planes, the decode step
+  plan and the default split count), built with g++ into tests/host_layout_check.cpp and
+  checked against the GGUF block layouts, numpy transposes and the step plan's invariants;
+- the oracle (oracle/attn_oracle.c, oracle/block_oracle.c) built with the same sanitizers
+  (`make -C oracle asan`), under which tests/test_oracle.py and tests/test_block_oracle.py run
+  in a child process with the ASan runtime preloaded.
+
+Any out-of-bounds access, use after free or undefined arithmetic aborts the sanitized process,
+which fails the test."""
+import os
+import shutil
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from tests import ggml_pack as gp
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+SAN = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", "-g"]
+SAN_ENV = {"ASAN_OPTIONS": "detect_leaks=0:abort_on_error=1", "UBSAN_OPTIONS": "print_stacktrace=1"}
+
+pytestmark = pytest.mark.skipif(shutil.which("g++") is None or shutil.which("gcc") is None,
+                                reason="needs gcc/g++ with the sanitizer runtimes")
+
+
+@pytest.fixture(scope="module")
+def driver(tmp_path_factory):
+    d = tmp_path_factory.mktemp("hostsan")
+    exe = str(d / "host_layout_check")
+    subprocess.run(["g++", "-std=c++17", "-O1", *SAN, "-I", os.path.join(ROOT, "llmplayer_amd", "csrc"),
+                    "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "host_layout_check.cpp"),
+                    "-o", exe], check=True)
+    return exe, d
+
+
+def _run(exe, lines):
+    env = dict(os.environ, **SAN_ENV)
+    r = subprocess.run([exe], input="\n".join(lines) + "\n", capture_output=True, text=True, env=env,
+                       timeout=120)
+    assert r.returncode == 0, f"sanitized driver failed ({r.returncode}):\n{r.stderr[-4000:]}"
+    assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr, r.stderr[-4000:]
+    return r.stdout.splitlines()
+
+
+# GGUF block layouts (ggml's block_q8_0, block_q4_0, block_q4_K, block_q6_K), as
+# (weights per block, [(field, bytes)] in memory order), and the plane each field goes to.
+BLOCKS = {
+    gp.GGML_Q8_0: (32, [("d", 2), ("qs", 32)], {"qs": 0, "d": 1}),
+    gp.GGML_Q4_0: (32, [("d", 2), ("qs", 16)], {"qs": 0, "d": 1}),
+    gp.GGML_Q4_K: (256, [("d", 2), ("dmin", 2), ("scales", 12), ("qs", 128)],
+                   {"qs": 0, "d": 1, "dmin": 1, "scales": 1}),
+    gp.GGML_Q6_K: (256, [("ql", 128), ("qh", 64), ("scales", 16), ("d", 2)],
+                   {"ql": 0, "qh": 1, "scales": 2, "d": 3}),
+}
+DENSE = {gp.GGML_F32: 4, gp.GGML_F16: 2, gp.GGML_BF16: 2}
+
+
+def _expected_planes(t, rows, cols, raw):
+    """Per plane, the [rows][pitch] bytes: each row's bytes of every field of that plane, block
+    by block, the fields of one block in memory order."""
+    if t in DENSE:
+        return [raw.reshape(rows, cols * DENSE[t])]
+    bw, fields, plane_of = BLOCKS[t]
+    nb = cols // bw
+    blk = raw.reshape(rows, nb, sum(n for _, n in fields))
+    parts, o = {}, 0
+    for name, n in fields:
+        parts[name] = blk[:, :, o:o + n]
+        o += n
+    planes = []
+    for p in range(max(plane_of.values()) + 1):
+        sel = [parts[name] for name, _ in fields if plane_of[name] == p]
+        planes.append(np.concatenate(sel, axis=2).reshape(rows, -1))
+    return planes
+
+
+CASES = [(t, rows, cols) for t in (gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0)
+         for rows, cols in ((1, 32), (3, 96), (17, 2880))] + \
+        [(t, rows, cols) for t in (gp.GGML_Q4_K, gp.GGML_Q6_K) for rows, cols in ((1, 256), (5, 768), (33, 3072))]
+
+
+def test_repack_matches_the_gguf_block_layouts(driver):
+    exe, d = driver
+    rng = np.random.default_rng(11)
+    lines, want = [], []
+    for i, (t, rows, cols) in enumerate(CASES):
+        bw = BLOCKS[t][0] if t in BLOCKS else 1
+        row_bytes = cols * DENSE[t] if t in DENSE else cols // bw * sum(n for _, n in BLOCKS[t][1])
+        raw = rng.integers(0, 256, rows * row_bytes, dtype=np.uint8)
+        src, dst = d / f"w{i}.bin", d / f"p{i}.bin"
+        raw.tofile(src)
+        lines.append(f"repack {t} {rows} {cols} {src} {dst}")
+        want.append((raw, dst))
+    out = _run(exe, lines)
+    for (t, rows, cols), line, (raw, dst) in zip(CASES, out, want):
+        f = list(map(int, line.split()))
+        n, off, pitch = f[0], f[1:5], f[5:9]
+        planes = _expected_planes(t, rows, cols, raw)
+        assert n == len(planes), (t, rows, cols)
+        packed = np.fromfile(dst, np.uint8)
+        assert len(packed) % 256 == 0
+        end = 0
+        for p, exp in enumerate(planes):
+            assert off[p] % 256 == 0 and off[p] >= end, (t, p, off)
+            assert pitch[p] == exp.shape[1], (t, p, pitch)
+            got = packed[off[p]:off[p] + rows * pitch[p]].reshape(rows, pitch[p])
+            np.testing.assert_array_equal(got, exp, err_msg=f"type {t} plane {p}")
+            assert not packed[off[p] + rows * pitch[p]:(off[p + 1] if p + 1 < n else len(packed))].any()
+            end = off[p] + rows * pitch[p]
+
+
+def test_repack_rejects_partial_blocks_and_unknown_types(driver):
+    exe, d = driver
+    src = d / "tiny.bin"
+    np.zeros(4096, np.uint8).tofile(src)
+    out = _run(exe, [f"repack {gp.GGML_Q4_K} 1 128 {src} {d / 'x.bin'}",
+                     f"repack {gp.GGML_Q8_0} 2 48 {src} {d / 'x.bin'}",
+                     f"repack 99 1 32 {src} {d / 'x.bin'}",
+                     f"repack {gp.GGML_F32} 1 0 {src} {d / 'x.bin'}"])
+    assert [int(l.split()[0]) for l in out] == [0, 0, 0, 0]
+
+
+@pytest.mark.parametrize("H,n,row", [(1, 1, 4), (8, 37, 512), (4, 5, 16), (32, 3, 80 * 4), (2, 64, 8)])
+def test_kv_relayout_is_a_head_major_transpose(driver, H, n, row):
+    exe, d = driver
+    host = np.random.default_rng(H * n + row).integers(0, 256, (n, H * row), dtype=np.uint8)
+    src, heads, back = d / "h.bin", d / "s.bin", d / "b.bin"
+    host.tofile(src)
+    assert _run(exe, [f"relayout {H} {n} {row} {src} {heads} {back}"]) == ["ok"]
+    np.testing.assert_array_equal(np.fromfile(heads, np.uint8).reshape(H, n, row),
+                                  host.reshape(n, H, row).transpose(1, 0, 2))
+    np.testing.assert_array_equal(np.fromfile(back, np.uint8).reshape(n, H * row), host)
+
+
+def test_step_plan_invariants(driver):
+    """plan_step against its contract: the window's first row, rows that the splits cover
+    exactly once (every split non-empty), at most the requested splits, rows per split a
+    multiple of 16 once each split has 16 rows; positions up to 2^30."""
+    exe, _ = driver
+    rng = np.random.default_rng(5)
+    cases = [(0, 0, 1), (0, 0, 1024), (15, 0, 1), (16, 4, 1), (4095, 0, 32), (32767, 0, 24),
+             (8191, 1024, 64), (1023, 1024, 64), (1024, 1024, 64), (2**30, 0, 1024), (2**30, 4096, 7)]
+    cases += [(int(rng.integers(0, 1 << 20)), int(rng.choice([0, 1, 128, 4096, rng.integers(1, 9000)])),
+               int(rng.integers(1, 1025))) for _ in range(300)]
+    out = _run(exe, [f"plan {p} {w} {s}" for p, w, s in cases])
+    for (pos, window, splits), line in zip(cases, out):
+        start, n, rps, s = map(int, line.split())
+        assert start == (max(0, pos - window + 1) if window > 0 else 0)
+        assert n == pos + 1 - start
+        assert 1 <= s <= min(splits, n) and rps >= 1
+        assert (s - 1) * rps < n <= s * rps, (pos, window, splits, line)
+        if n >= 16 * min(splits, n):
+            assert rps % 16 == 0
+
+
+def test_default_splits(driver):
+    """The measured plan at the Llama-3.2-3B shape (8 KV heads, 256 CUs): fp32 at 32k rows runs
+    24 splits of 8-wave workgroups, at 4k 32 splits of 4; Q8_0 with 3 resident workgroups per CU
+    runs 96 splits at 32k. In general 1 <= splits <= 128, fp32 splits hold >= 32 rows unless there
+    is only one, Q8_0 splits >= 160, and only fp32 calls widen."""
+    exe, _ = driver
+    out = _run(exe, ["splits 32768 8 256 1 0", "splits 4096 8 256 1 0", "splits 32768 8 256 3 1"])
+    assert out == ["24 1", "32 0", "96 0"]
+    rng = np.random.default_rng(9)
+    cases = [(int(rng.integers(1, 1 << 22)), int(rng.choice([1, 2, 4, 8, 32])), int(rng.choice([0, 80, 256, 304])),
+              int(rng.integers(0, 6)), int(rng.integers(0, 2))) for _ in range(300)]
+    out = _run(exe, [f"splits {n} {h} {c} {p} {q}" for n, h, c, p, q in cases])
+    for (n, h, c, p, q), line in zip(cases, out):
+        s, wide = map(int, line.split())
+        assert 1 <= s <= 128
+        assert not (q and wide)
+        if s > 1 and not wide:
+            assert n // s >= (160 if q else 32), (n, h, c, p, q, line)
+
+
+def test_oracle_under_sanitizers(tmp_path):
+    """tests/test_oracle.py and tests/test_block_oracle.py against the sanitized oracle build."""
+    asan_dir = tmp_path / "asan"
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "asan", f"ASAN_DIR={asan_dir}"],
+                   check=True, stdout=subprocess.DEVNULL)
+    libasan = subprocess.run(["gcc", "-print-file-name=libasan.so"], capture_output=True, text=True,
+                             check=True).stdout.strip()
+    env = dict(os.environ, **SAN_ENV, LD_PRELOAD=libasan, LLMP_ORACLE_LIB=str(asan_dir / "libattn_oracle.so"))
+    r = subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider",
+                        os.path.join(ROOT, "tests", "test_oracle.py"),
+                        os.path.join(ROOT, "tests", "test_block_oracle.py")],
+                       cwd=ROOT, env=env, capture_output=True, text=True, timeout=900)
+    tail = (r.stdout[-3000:] + r.stderr[-3000:])
+    assert r.returncode == 0, tail
+    assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr, tail
+    assert " passed" in r.stdout and "failed" not in r.stdout, tail
