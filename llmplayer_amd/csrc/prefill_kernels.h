@@ -29,9 +29,11 @@
 // A[i%16][8*(i/16)+j] and B[8*(i/16)+j][i%16] (j < 8) and D[4*(i/16)+j][i%16] (j < 4).
 // S^T's D fragment (lane: query i%16, keys 4*(i/16)+j of a 16-key tile) is fed back as the B
 // operand of the P V product without moving data across lanes: the 32 keys of an MFMA step
-// are taken in the order {4q..4q+3 of tile 2c, 4q..4q+3 of tile 2c+1} (q = i/16), and V^T's A
-// operand is read from LDS in the same key order.
+// are taken in the order {4q..4q+3 of tile 2c, 4q..4q+3 of tile 2c+1} (q = i/16), and V^T is
+// stored in LDS in that key order, so its A operand is one 16-byte read.
 #pragma once
+
+#include <type_traits>
 
 #include "decode_kernels.h"
 
@@ -176,15 +178,17 @@ inline size_t prefill_append_lds(int Hkv, int D) {
 }
 
 // ---- LDS tile layout (also the workspace image of a tile) -------------------------------------
-// LDS tile: K hi/lo [TK keys][D + 8] fp16, V^T hi/lo [D][TK + 4] (row padding spreads banks).
+// LDS tile: K hi/lo [TK keys][D + 8] fp16, V^T hi/lo [D][TK + 8] (row padding spreads banks).
+// Within each 32-key chunk of a V^T row the keys are stored in the order the P V MFMA takes
+// them (vt_group_pos): the 8 keys {4q..4q+3, 16+4q..16+4q+3} a lane group q feeds to one MFMA
+// are contiguous, so a lane reads its A operand with one 16-byte load.
 template <int D, int TKEYS = tile_keys<D>()>
 struct alignas(16) TileLds {
     static constexpr int TK = TKEYS;
     static constexpr int KP = D + 8;   // K row pitch (fp16 elements; 16-byte multiple)
-    // V^T row pitch: 8-byte multiple with an odd number of 8-byte units beyond a 32-dword
-    // multiple (TK + 4 fp16 = 2*(TK/2 + 2) dwords), so the 16 dims of a lane row-group's 8-byte
-    // reads fall on 16 distinct bank pairs.
-    static constexpr int VP = TK + 4;
+    // V^T row pitch: TK + 8 fp16 = TK/2 + 4 dwords, 4 dwords past a multiple of 32 (TK is 32 or
+    // 64), so 8 consecutive dims' 16-byte reads cover the 32 banks once.
+    static constexpr int VP = TK + 8;
     unsigned short kh[TK * KP];
     unsigned short kl[TK * KP];
     unsigned short vh[D * VP];
@@ -202,16 +206,39 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ unsigned pack_f16(float x, float y) {
     return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{x, y}, f16x2));
 }
-// Split of two values: hi = fp16(x), lo = fp16(x - hi) (x - hi is exact in fp32), packed in
-// pairs: hi + lo holds x to ~2^-22 of |x| (or 2^-25 absolute below fp16's normal range).
+// Split of two values: hi = fp16(x), lo = fp16(x - hi), packed in pairs: hi + lo holds x to
+// ~2^-22 of |x| (or 2^-25 absolute below fp16's normal range).  Each lo half comes from one
+// mixed-precision FMA, hi(f16) * -1 + x(f32), which forms the difference exactly and rounds it
+// once to fp16 into its half of the register: the same bits as rounding the exact fp32
+// difference, in 3 instructions per pair instead of 6.
 __device__ __forceinline__ void split_pair(float x, float y, unsigned& hi, unsigned& lo) {
     hi = pack_f16(x, y);
-    const f16x2 h = __builtin_bit_cast(f16x2, hi);
-    lo = pack_f16(x - (float)h[0], y - (float)h[1]);
+    unsigned r;
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(hi), "v"(x));
+    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "+v"(r) : "v"(hi), "v"(y));
+    lo = r;
 }
+// True when either fp16 half of a packed lo pair is larger in magnitude than 2^-24 (fp16's
+// smallest subnormal): rows written from bf16 inputs never are.
+__device__ __forceinline__ bool lo_significant(unsigned lo) {
+    return (lo & 0x7FFFu) > 1u || ((lo >> 16) & 0x7FFFu) > 1u;
+}
+
+// Position within a 32-key chunk of V^T of the 4 keys 4*g..4*g+3 (g < 8): groups 0-3 (keys
+// 0-15) go to 8*g, groups 4-7 (keys 16-31) to 8*(g-4)+4.
+__device__ __forceinline__ int vt_group_pos(int g) { return g < 4 ? 8 * g : 8 * (g - 4) + 4; }
+// Element offset within a V^T row of the 4 keys 4*rq..4*rq+3 of a tile.
+__device__ __forceinline__ int vt_keys_off(int rq) { return 32 * (rq >> 3) + vt_group_pos(rq & 7); }
 
 template <int D>
 constexpr int tile_img_u4() { return (int)(sizeof(TileLds<D>) / 16); }
+// A tile image carries one flag in the padding of its first K row (kh[D], never read as a
+// key): nonzero when some V lo part exceeds 2^-24 in magnitude.  Where it is zero the P V
+// product drops its V-lo MFMA: the terms it would add are below 2^-24 * sum(P) / l <= 2^-24
+// of the output.  16-byte chunk and dword of the flag within the image:
+template <int D>
+constexpr int vlo_flag_chunk() { return D / 8; }
 
 // One KV head's rows in the cache: fp32 rows (f), or Q8_0 quants (q) and block scales (s).
 struct HeadRows {
@@ -277,9 +304,10 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);
     // K rows: work item (row r, dims 4*c4 .. 4*c4+3), c4 fastest across lanes, so the loads
     // are row-contiguous and the 8-byte stores of 16 lanes cover the 32 banks once.
-    // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), c4 fastest across lanes so
-    // that each load instruction reads whole rows; each dim row gets the 4 keys as one 8-byte
-    // store.
+    // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), rq fastest across lanes: each
+    // dim row gets the 4 keys as one 8-byte store, and the TK/4 lanes that share a dim chunk
+    // write one V^T row's TK keys together (no bank conflicts); a load instruction reads
+    // 64/(TK/4) consecutive 16-byte chunks of TK/4 rows.
     // Every global load of a thread is issued before any of its math (one memory round trip).
     constexpr int KI = TK * (D / 4) / NTHR, VI = (TK / 4) * (D / 4) / NTHR;
     static_assert(KI * NTHR == TK * (D / 4) && VI * NTHR == (TK / 4) * (D / 4),
@@ -294,7 +322,7 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
         const int e = tid + i * NTHR;
-        const int rq = e / (D / 4), c4 = e - rq * (D / 4);
+        const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) vx[i][j] = load_chunk<D, Q8>(vr, min(r0 + 4 * rq + j, row_end - 1), c4);
     }
@@ -309,10 +337,11 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
         *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
         *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
     }
+    bool vlo = false;
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
         const int e = tid + i * NTHR;
-        const int rq = e / (D / 4), c4 = e - rq * (D / 4);
+        const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
         const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]), chunk_values<Q8>(vx[i][1]),
                                chunk_values<Q8>(vx[i][2]), chunk_values<Q8>(vx[i][3])};   // [key][dim]
 #pragma unroll
@@ -320,15 +349,20 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
             unsigned h0, l0, h1, l1;
             split_pair(vv[0][u], vv[1][u], h0, l0);
             split_pair(vv[2][u], vv[3][u], h1, l1);
+            vlo = vlo || lo_significant(l0) || lo_significant(l1);
             const int d = 4 * c4 + u;
-            *reinterpret_cast<uint2*>(&t.vh[d * T::VP + 4 * rq]) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2*>(&t.vl[d * T::VP + 4 * rq]) = make_uint2(l0, l1);
+            *reinterpret_cast<uint2*>(&t.vh[d * T::VP + vt_keys_off(rq)]) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(&t.vl[d * T::VP + vt_keys_off(rq)]) = make_uint2(l0, l1);
         }
     }
-    __syncthreads();
+    const unsigned any_vlo = __syncthreads_or(vlo ? 1 : 0) ? 1u : 0u;
     const uint4* src = reinterpret_cast<const uint4*>(&t);
     uint4* dst = ws + ((size_t)kvh * n_tiles + blockIdx.x) * tile_img_u4<D>();
-    for (int i = tid; i < tile_img_u4<D>(); i += NTHR) dst[i] = src[i];
+    for (int i = tid; i < tile_img_u4<D>(); i += NTHR) {
+        uint4 c = src[i];
+        if (i == vlo_flag_chunk<D>()) c.x = any_vlo;
+        dst[i] = c;
+    }
 }
 
 // ---- 3. Double-buffered MFMA attention ------------------------------------------------------
@@ -364,8 +398,8 @@ __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int
         for (int s = 0; s < KS; ++s)
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(qf[s][j], qf[s][j], ss);
-        ss = ss + __shfl_xor(ss, 16);
-        ss = ss + __shfl_xor(ss, 32);
+        ss = dk::lane_step<16, false>(ss);
+        ss = dk::lane_step<32, false>(ss);
         r = 1.0f / sqrtf(ss / (float)D + a.eps);
 #pragma unroll
         for (int s = 0; s < KS; ++s)
@@ -444,9 +478,10 @@ __device__ __forceinline__ void img_store(const u32x4 (&stage)[PER], void* dst, 
 
 // Direct staging from the fp32 cache (short prompts after a long prefix, where each key tile
 // feeds only a few workgroups and building images first would re-convert the whole prefix on
-// every call).  K: items (row, 4-dim chunk); V: items (4 keys, 4-dim chunk), stored transposed
-// as 8-byte runs; the chunk index runs fastest across lanes so every load reads whole rows.  Rows at or past row_lim
-// repeat row row_lim (never attended, finite).
+// every call).  K: items (row, 4-dim chunk), the chunk index fastest across lanes so every load
+// reads whole rows; V: items (4 keys, 4-dim chunk), stored transposed as 8-byte runs, the key
+// group fastest across lanes (as in prefill_tile_kernel).  Rows at or past row_lim repeat row
+// row_lim (never attended, finite).
 // Keys per LDS tile of the direct-staging launches: 32, so two workgroups' double-buffered
 // tiles fit in a CU's 160 KB of LDS (64-key tiles of head_dim 128 take 136 KB per workgroup).
 template <int D>
@@ -474,7 +509,7 @@ __device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4]
 #pragma unroll
     for (int i = 0; i < R::VI; ++i) {
         const int e = min(tid + i * NTHR, R::NV - 1);
-        const int rq = e / (D / 4), c4 = e - rq * (D / 4);
+        const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) vx[i][j] = load_chunk<D, Q8>(vr, min(t0 + 4 * rq + j, row_lim), c4);
     }
@@ -503,7 +538,7 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
     for (int i = 0; i < R::VI; ++i) {
         const int e = tid + i * NTHR;
         if (i + 1 < R::VI || e < R::NV) {
-            const int rq = e / (D / 4), c4 = e - rq * (D / 4);
+            const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
             const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]), chunk_values<Q8>(vx[i][1]),
                                    chunk_values<Q8>(vx[i][2]), chunk_values<Q8>(vx[i][3])};
 #pragma unroll
@@ -512,8 +547,8 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
                 split_pair(vv[0][u], vv[1][u], h0, l0);
                 split_pair(vv[2][u], vv[3][u], h1, l1);
                 const int d = 4 * c4 + u;
-                *reinterpret_cast<uint2*>(&t.vh[d * T::VP + 4 * rq]) = make_uint2(h0, h1);
-                *reinterpret_cast<uint2*>(&t.vl[d * T::VP + 4 * rq]) = make_uint2(l0, l1);
+                *reinterpret_cast<uint2*>(&t.vh[d * T::VP + vt_keys_off(rq)]) = make_uint2(h0, h1);
+                *reinterpret_cast<uint2*>(&t.vl[d * T::VP + vt_keys_off(rq)]) = make_uint2(l0, l1);
             }
         }
     }
@@ -522,8 +557,16 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
 // Workgroup: KV head blockIdx.y, query tokens [i0, i0 + 16*NB) of its G query heads.  Wave:
 // 16 tokens (sub-block sb) x HPW query heads (head group hg), so each K/V fragment read from
 // LDS feeds HPW heads' MFMAs.  Tiles [tile0, tile0 + n_tiles) of the layer are in `ws`.
+// Waves per SIMD the register allocation must leave room for: head_dim 64 with image tiles
+// runs two 8-wave workgroups per CU (4 waves per SIMD, at most 128 VGPRs each); other shapes
+// are not constrained.
+template <int D, int G, bool DIRECT>
+constexpr int attn_waves_per_eu() { return (D == 64 && G >= 2 && !DIRECT) ? 4 : 1; }
+
 template <int D, int G, int NB, int HPW, bool DIRECT = false, bool Q8 = false>
-__global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(PrefillArgs a,
+__global__ __launch_bounds__((G / HPW) * NB * 64)
+__attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<D, G, DIRECT>())))
+void prefill_attn2_kernel(PrefillArgs a,
                                                                             const uint4* ws,
                                                                             int tile0, int n_tiles,
                                                                             int ksplit) {
@@ -655,8 +698,8 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) mt = fmaxf(mt, st[hh][kt][j]);
-            mt = fmaxf(mt, __shfl_xor(mt, 16));
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            mt = dk::lane_step<16, true>(mt);
+            mt = dk::lane_step<32, true>(mt);
             // rescale only when some row's running max grew: otherwise alpha is exactly 1
             if (__any(mt > m[hh])) {
                 const float mn = fmaxf(m[hh], mt);
@@ -677,6 +720,12 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
                 }
         }
         // O^T += V^T P^T: B operand = P in the key order {32c+4grp..+3, 32c+16+4grp..+3}.
+        // Tiles whose V lo parts are all within 2^-24 (rows written from bf16 inputs) skip the
+        // V-lo MFMA and its LDS reads.  Direct staging does not flag its tiles.
+        const bool tile_vlo =
+            DIRECT || __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(&t.kh[D])) != 0;
+        auto pv = [&](auto has_lo) {
+            constexpr bool HL = decltype(has_lo)::value;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             f16x8 ph[HPW], pl[HPW];
@@ -693,23 +742,24 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
 #pragma unroll
             for (int d = 0; d < DT; ++d) {
                 const int dim = d * 16 + col;
-                const int k0 = 32 * c + 4 * grp;
-                const unsigned short* vhr = &t.vh[dim * T::VP + k0];
-                const unsigned short* vlr = &t.vl[dim * T::VP + k0];
-                const uint2 a0 = *reinterpret_cast<const uint2*>(vhr);
-                const uint2 a1 = *reinterpret_cast<const uint2*>(vhr + 16);
-                const uint2 b0 = *reinterpret_cast<const uint2*>(vlr);
-                const uint2 b1 = *reinterpret_cast<const uint2*>(vlr + 16);
-                const f16x8 vh = __builtin_bit_cast(f16x8, make_uint4(a0.x, a0.y, a1.x, a1.y));
-                const f16x8 vl = __builtin_bit_cast(f16x8, make_uint4(b0.x, b0.y, b1.x, b1.y));
+                const int k0 = 32 * c + 8 * grp;   // keys {32c+4grp..+3, 32c+16+4grp..+3}
+                const f16x8 vh = *reinterpret_cast<const f16x8*>(&t.vh[dim * T::VP + k0]);
 #pragma unroll
                 for (int hh = 0; hh < HPW; ++hh) {
                     o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[hh], o[hh][d], 0, 0, 0);
                     o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[hh], o[hh][d], 0, 0, 0);
-                    o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[hh], o[hh][d], 0, 0, 0);
+                }
+                if constexpr (HL) {
+                    const f16x8 vl = *reinterpret_cast<const f16x8*>(&t.vl[dim * T::VP + k0]);
+#pragma unroll
+                    for (int hh = 0; hh < HPW; ++hh)
+                        o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[hh], o[hh][d], 0, 0, 0);
                 }
             }
         }
+        };
+        if (tile_vlo) pv(std::true_type{});
+        else pv(std::false_type{});
         // Next buffer: tile+1 (already in registers) to LDS, tile+2 loads in flight.  The
         // buffer written here was last read before the previous iteration's barrier.
         if (tile + 1 <= t_last) {
@@ -727,8 +777,8 @@ __global__ __launch_bounds__((G / HPW) * NB * 64) void prefill_attn2_kernel(Pref
     }
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
-        float lt = l[hh] + __shfl_xor(l[hh], 16);
-        lt = lt + __shfl_xor(lt, 32);
+        float lt = dk::lane_step<16, false>(l[hh]);
+        lt = dk::lane_step<32, false>(lt);
         if (q_ok && ksplit > 1) {
             // Unnormalised partial of split ks: o for this lane's dims, (max, sum) per row.
             const int hq = kvh * G + hg * HPW + hh;
