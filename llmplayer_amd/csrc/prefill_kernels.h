@@ -378,18 +378,29 @@ __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int
     constexpr int KS = D / 32;
     float qf[KS][8];
     const long long q0 = (long long)qi * a.Hq * D + (long long)hq * D;
+    // A lane's 8 elements per step are contiguous and 16-byte aligned (D is a multiple of 32):
+    // one 16-byte load per step for bf16 inputs, two for fp32.
     if (a.in_f32) {
         const float* qp = static_cast<const float*>(a.q) + q0;
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qf[s][j] = qp[32 * s + 8 * grp + j];
+        for (int s = 0; s < KS; ++s) {
+            const float4 x0 = *reinterpret_cast<const float4*>(qp + 32 * s + 8 * grp);
+            const float4 x1 = *reinterpret_cast<const float4*>(qp + 32 * s + 8 * grp + 4);
+            qf[s][0] = x0.x; qf[s][1] = x0.y; qf[s][2] = x0.z; qf[s][3] = x0.w;
+            qf[s][4] = x1.x; qf[s][5] = x1.y; qf[s][6] = x1.z; qf[s][7] = x1.w;
+        }
     } else {
         const unsigned short* qp = static_cast<const unsigned short*>(a.q) + q0;
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
+        for (int s = 0; s < KS; ++s) {
+            const uint4 w = *reinterpret_cast<const uint4*>(qp + 32 * s + 8 * grp);
+            const unsigned u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qf[s][j] = bf16_to_f32(qp[32 * s + 8 * grp + j]);
+            for (int j = 0; j < 4; ++j) {
+                qf[s][2 * j] = __uint_as_float(u[j] << 16);
+                qf[s][2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+            }
+        }
     }
     float r = 1.0f;
     if (a.qnw != nullptr) {
@@ -598,11 +609,6 @@ void prefill_attn2_kernel(PrefillArgs a,
     const int qpos = a.pos0 + (q_ok ? qi : a.P - 1);
     const int qstart = a.window > 0 ? max(0, qpos - a.window + 1) : 0;
 
-    f16x8 qh[HPW][KS], ql[HPW][KS];
-#pragma unroll
-    for (int hh = 0; hh < HPW; ++hh)
-        query_fragment<D>(a, q_ok ? qi : a.P - 1, kvh * G + hg * HPW + hh, qpos, grp, qh[hh], ql[hh]);
-
     // Key range of the workgroup and of this wave's 16 queries.
     const int last_tok = min(i0 + 16 * NB, a.P) - 1;
     const int kend = a.pos0 + last_tok + 1;
@@ -629,14 +635,25 @@ void prefill_attn2_kernel(PrefillArgs a,
         l[hh] = 0.0f;
     }
 
-    if (t_first <= t_last) {   // a split past the item's last tile has no keys (neutral partial)
-        if constexpr (DIRECT) {
+    // The first tile's loads go out before the query fragments are read and prepared, so the
+    // two memory round trips of the prologue overlap.
+    const bool has_keys = t_first <= t_last;   // a split past the item's last tile: neutral partial
+    if (has_keys) {
+        if constexpr (DIRECT)
             raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, t_first * TK, kend - 1, tid);
+        else
+            img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
+    }
+    f16x8 qh[HPW][KS], ql[HPW][KS];
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh)
+        query_fragment<D>(a, q_ok ? qi : a.P - 1, kvh * G + hg * HPW + hh, qpos, grp, qh[hh], ql[hh]);
+    if (has_keys) {
+        if constexpr (DIRECT) {
             raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, buf[0], tid);
             if (t_first + 1 <= t_last)
                 raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (t_first + 1) * TK, kend - 1, tid);
         } else {
-            img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
             img_store<PER, NTHR, IMG>(stage, &buf[0], tid);
             if (t_first + 1 <= t_last)
                 img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first + 1 - tile0) * IMG, tid);
