@@ -362,6 +362,21 @@ __device__ __forceinline__ int step_position(const DecodeArgs& a) {
     return a.d_pos != nullptr ? *a.d_pos : a.pos;
 }
 
+// Kernel arguments are read with scalar loads at their first use, and a field first used
+// after a branch (the position checks, the split's early exit) waits for another round trip
+// to the argument segment: three rounds, ~1.3 us per workgroup, measured at the Llama-3.2-3B
+// shape.  Naming every field the prologue reads at entry puts them in one round.
+__device__ __forceinline__ void load_args_now(const DecodeArgs& a) {
+    asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.kq), "s"(a.ks),
+                 "s"(a.vq), "s"(a.vs), "s"(a.cos_t), "s"(a.sin_t));
+    asm volatile("" ::"s"(a.qnw), "s"(a.knw), "s"(a.sinks), "s"(a.gate), "s"(a.out),
+                 "s"(a.part_o), "s"(a.part_ml), "s"(a.d_pos), "s"(a.head_stride));
+    asm volatile("" ::"s"(a.pos), "s"(a.max_seq), "s"(a.window), "s"(a.splits), "s"(a.half_rope),
+                 "s"(a.rope_type), "s"(a.q8_trunc), "s"(a.norm_seq), "s"(a.v_norm),
+                 "s"(a.no_append), "s"(a.eps), "s"(a.qk_scale));
+    asm volatile("" ::"s"(a.softcap), "s"(a.softcap_log2e), "s"(a.inv_softcap));
+}
+
 // 1/rms of D values in the order of RMSNorm.apply with offsets (RMSNorm.java:24-35, the
 // Gemma 4 engine's QK-norm and V-norm): one thread sums the squares sequentially, unfused,
 // then r = 1/(float)sqrt(ss/D + eps).
@@ -629,9 +644,17 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     __shared__ float s_vr;
     __shared__ __align__(16) signed char s_kq[Q8 ? D : 16], s_vq[Q8 ? D : 16];
     __shared__ float s_ks[D / 32], s_vs[D / 32], s_inv[D / 32];
-    __shared__ float s_m[WAVES * G];
-    __shared__ float s_l[WAVES * G];
-    __shared__ float s_o[WAVES * G * D];
+    // Merge of the workgroup's partial softmax states (section 5): with LDS_MERGE every row
+    // group of every wave leaves its raw (m, l, o) in LDS (NPART partials); otherwise the row
+    // groups of a wave are merged in VGPRs first (WAVES partials).
+    constexpr int NPART_LDS = WAVES * RPW;
+    constexpr bool LDS_MERGE = NPART_LDS * G * D * 4 <= 32768;
+    constexpr int NPART = LDS_MERGE ? NPART_LDS : WAVES;
+    __shared__ float s_m[NPART * G];
+    __shared__ float s_l[NPART * G];
+    __shared__ float s_w[LDS_MERGE ? NPART * G : 1];
+    __shared__ float s_ML[LDS_MERGE ? 2 * G : 1];
+    __shared__ float s_o[NPART * G * D];
 
     const int tid = threadIdx.x;
     const int split = blockIdx.x;
@@ -639,6 +662,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     const int h0 = kvh * G;
     // Step plan from the position (host value or device word).  A device position outside
     // the cache leaves everything untouched; splits beyond the rows of this step exit.
+    load_args_now(a);
     const int pos = step_position(a);
     if (pos < 0 || pos >= a.max_seq) return;
     const StepPlan sp = plan_step(pos, a.window, a.splits);
@@ -785,7 +809,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     // 3. Stream the cached rows [row_begin, cache_end), one trip prefetched in registers.  The
     //    trips run in pairs with one exit: a branch between the two halves would join the loop
     //    head with the second buffer's loads in flight, and the wait placed there would drain
-    //    the prefetch on every trip.  (The last pair's refill reads masked, clamped rows.)
+    //    the prefetch on every trip.  (The last pair's refill reads masked, clamped rows.
+    //    Peeling the last trips to skip it raised the register count by up to 40 VGPRs and cost
+    //    an occupancy step at most shapes; pointing its rows at the cache-resident query vector
+    //    measured 0.2 us faster at 4k but 0.6 us slower at 32k.)
     int base = first;
     for (int i = 0; i + 1 < ntrips; i += 2) {
         load_trip<D, EPL, U, NT, Q8>(tb, a, kvh, base + ROWS_BLOCK, cache_end, grp, j);
@@ -823,66 +850,120 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
         }
     }
 
-    // 5. Merge the row groups of each wave (lanes j, j+LPR, ...), then the waves via LDS.
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        float mw = m[h];
-        if constexpr (LPR <= 4) mw = lane_step<4, true>(mw);
-        if constexpr (LPR <= 8) mw = lane_step<8, true>(mw);
-        if constexpr (LPR <= 16) mw = lane_step<16, true>(mw);
-        if constexpr (LPR <= 32) mw = lane_step<32, true>(mw);
-        const float sc = fast_exp2(m[h] - mw);
-        float lw = l[h] * sc;
-        if constexpr (LPR <= 4) lw = lane_step<4, false>(lw);
-        if constexpr (LPR <= 8) lw = lane_step<8, false>(lw);
-        if constexpr (LPR <= 16) lw = lane_step<16, false>(lw);
-        if constexpr (LPR <= 32) lw = lane_step<32, false>(lw);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float x = o[h][e] * sc;
-            if constexpr (LPR <= 4) x = lane_step<4, false>(x);
-            if constexpr (LPR <= 8) x = lane_step<8, false>(x);
-            if constexpr (LPR <= 16) x = lane_step<16, false>(x);
-            if constexpr (LPR <= 32) x = lane_step<32, false>(x);
-            o[h][e] = x;
-        }
-        m[h] = mw;
-        l[h] = lw;
-    }
-    if (grp == 0) {
+    // 5. Merge the partial states.  LDS_MERGE: each row group writes its raw (m, l, o); the
+    //    per-(partial, head) weights 2^(m - M) are computed once, then each output element is
+    //    a weighted sum over the NPART partials.  Otherwise the row groups of each wave are
+    //    merged with lane exchanges first (the state of 8-wave workgroups and of large groups
+    //    does not fit in 32 KB of LDS).
+    if constexpr (LDS_MERGE) {
+        const int pidx = wave * RPW + grp;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) s_o[(wave * G + h) * D + F::dim(j, e)] = o[h][e];
+            for (int e = 0; e < EPL; ++e) s_o[(pidx * G + h) * D + F::dim(j, e)] = o[h][e];
             if (j == 0) {
-                s_m[wave * G + h] = m[h];
-                s_l[wave * G + h] = l[h];
+                s_m[pidx * G + h] = m[h];
+                s_l[pidx * G + h] = l[h];
             }
         }
-    }
-    __syncthreads();
-
-    for (int idx = tid; idx < G * D; idx += NTHR) {
-        const int h = idx / D, d = idx - h * D;
-        float M = s_m[h];
+        __syncthreads();
+        if (tid < NPART * G) {
+            const int h = tid % G;
+            float M = s_m[h];
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w * G + h]);
-        float L = 0.0f, O = 0.0f;
+            for (int q = 1; q < NPART; ++q) M = fmaxf(M, s_m[q * G + h]);
+            s_w[tid] = fast_exp2(s_m[tid] - M);
+            if (tid < G) {
+                float L = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            const float sc = fast_exp2(s_m[w * G + h] - M);
-            L = __builtin_fmaf(s_l[w * G + h], sc, L);
-            O = __builtin_fmaf(s_o[(w * G + h) * D + d], sc, O);
+                for (int q = 0; q < NPART; ++q)
+                    L = __builtin_fmaf(s_l[q * G + h], fast_exp2(s_m[q * G + h] - M), L);
+                s_ML[2 * h] = M;
+                s_ML[2 * h + 1] = L;
+            }
         }
-        if (sp.splits == 1) {
-            a.out[(h0 + h) * D + d] =
-                finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
-        } else {
-            const long long slot = ((long long)kvh * sp.splits + split) * G + h;
-            a.part_o[slot * D + d] = O;
-            if (d == 0) {
-                a.part_ml[2 * slot] = M;
-                a.part_ml[2 * slot + 1] = L;
+        __syncthreads();
+        for (int idx = tid; idx < G * D; idx += NTHR) {
+            const int h = idx / D, d = idx - h * D;
+            const float M = s_ML[2 * h], L = s_ML[2 * h + 1];
+            float O = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NPART; ++q)
+                O = __builtin_fmaf(s_o[(q * G + h) * D + d], s_w[q * G + h], O);
+            if (sp.splits == 1) {
+                a.out[(h0 + h) * D + d] =
+                    finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
+            } else {
+                const long long slot = ((long long)kvh * sp.splits + split) * G + h;
+                a.part_o[slot * D + d] = O;
+                if (d == 0) {
+                    a.part_ml[2 * slot] = M;
+                    a.part_ml[2 * slot + 1] = L;
+                }
+            }
+        }
+    } else {
+        // 5. Merge the row groups of each wave (lanes j, j+LPR, ...), then the waves via LDS.
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float mw = m[h];
+            if constexpr (LPR <= 4) mw = lane_step<4, true>(mw);
+            if constexpr (LPR <= 8) mw = lane_step<8, true>(mw);
+            if constexpr (LPR <= 16) mw = lane_step<16, true>(mw);
+            if constexpr (LPR <= 32) mw = lane_step<32, true>(mw);
+            const float sc = fast_exp2(m[h] - mw);
+            float lw = l[h] * sc;
+            if constexpr (LPR <= 4) lw = lane_step<4, false>(lw);
+            if constexpr (LPR <= 8) lw = lane_step<8, false>(lw);
+            if constexpr (LPR <= 16) lw = lane_step<16, false>(lw);
+            if constexpr (LPR <= 32) lw = lane_step<32, false>(lw);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                float x = o[h][e] * sc;
+                if constexpr (LPR <= 4) x = lane_step<4, false>(x);
+                if constexpr (LPR <= 8) x = lane_step<8, false>(x);
+                if constexpr (LPR <= 16) x = lane_step<16, false>(x);
+                if constexpr (LPR <= 32) x = lane_step<32, false>(x);
+                o[h][e] = x;
+            }
+            m[h] = mw;
+            l[h] = lw;
+        }
+        if (grp == 0) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) s_o[(wave * G + h) * D + F::dim(j, e)] = o[h][e];
+                if (j == 0) {
+                    s_m[wave * G + h] = m[h];
+                    s_l[wave * G + h] = l[h];
+                }
+            }
+        }
+        __syncthreads();
+
+        for (int idx = tid; idx < G * D; idx += NTHR) {
+            const int h = idx / D, d = idx - h * D;
+            float M = s_m[h];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w * G + h]);
+            float L = 0.0f, O = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const float sc = fast_exp2(s_m[w * G + h] - M);
+                L = __builtin_fmaf(s_l[w * G + h], sc, L);
+                O = __builtin_fmaf(s_o[(w * G + h) * D + d], sc, O);
+            }
+            if (sp.splits == 1) {
+                a.out[(h0 + h) * D + d] =
+                    finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
+            } else {
+                const long long slot = ((long long)kvh * sp.splits + split) * G + h;
+                a.part_o[slot * D + d] = O;
+                if (d == 0) {
+                    a.part_ml[2 * slot] = M;
+                    a.part_ml[2 * slot + 1] = L;
+                }
             }
         }
     }
@@ -1044,6 +1125,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
     const int split = blockIdx.x;
     const int kvh = blockIdx.y;
     const int h0 = kvh * G;
+    load_args_now(a);
     const int pos = step_position(a);
     if (pos < 0 || pos >= a.max_seq) return;
     const StepPlan sp = plan_step(pos, a.window, a.splits);
@@ -1172,7 +1254,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
 
     // Tiles in pairs, so that the loop has one exit (a break between the two halves would
     // join the loop head with the second buffer's loads in flight, and the wait inserted
-    // there would drain the prefetch on every trip); an odd last tile follows.
+    // there would drain the prefetch on every trip); an odd last tile follows.  (Peeling the
+    // last pair so that its unused refill is not fetched costs this kernel 20-30 VGPRs and an
+    // occupancy step at most shapes, so the refill stays.)
     const int ntiles = t0 < cache_end ? (cache_end - t0 + TSTEP - 1) / TSTEP : 0;
     for (int i = 0; i + 1 < ntiles; i += 2) {
         q8_tile_load<D, NT>(tb, kqp, ksp, vqp, vsp, t0 + TSTEP, last, lane);
@@ -1281,6 +1365,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
     const int tid = threadIdx.x;
     const int c = tid % NC, p = tid / NC;
     const bool act = p < NP;   // NC need not divide the block: the spare threads only sync
+    load_args_now(a);
     const int pos = step_position(a);
     if (pos < 0 || pos >= a.max_seq) return;
     const int S = plan_step(pos, a.window, a.splits).splits;
