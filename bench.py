@@ -790,6 +790,8 @@ def main() -> int:
                     help="--profile-block: the Q8_1 input mode")
     ap.add_argument("--profile-block", action="store_true",
                     help="for rocprofv3: the attention-block graph at --ctx2 only, then exit")
+    ap.add_argument("--profile-block-batch", type=int, default=0, metavar="K",
+                    help="for rocprofv3: the K-token attention-block graph at --ctx2 only, then exit")
     ap.add_argument("--profile-workload", action="store_true",
                     help="for rocprofv3: only the warm-up and K eager layer-calls at --ctx "
                          "(no graph replay, no second context, no CPU baseline), then exit")
@@ -838,6 +840,10 @@ def main() -> int:
     if args.profile_block:
         r = block_run(args.ctx2 or 4096, args.steps, q8_input=args.block_q8)
         log(f"[bench] profile block: {r}")
+        return 0
+    if args.profile_block_batch:
+        r = block_batch_run(args.ctx2 or 4096, args.profile_block_batch, args.steps)
+        log(f"[bench] profile block batch: {r}")
         return 0
     if args.profile_verify:
         r = verify_run(args.ctx, args.profile_verify, args.steps, rot)
