@@ -28,7 +28,7 @@ inline int prefill_nb(int P, int Hkv, int G, int n_cu) {
 
 template <int D, int G, int NB>
 hipError_t launch_attn_dgn(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
-                           int ksplit, hipStream_t stream) {
+                           int ksplit, int n_cu, hipStream_t stream) {
     const int items = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
     if constexpr (D == 96) {   // fp32 caches only at head_dim 96
         if (a.kq != nullptr) return hipErrorInvalidValue;
@@ -40,6 +40,14 @@ hipError_t launch_attn_dgn(const pk::PrefillArgs& a, const uint4* ws, int tile0,
     if (ksplit > 1)
         hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, true>), dim3(items, ksplit),
                            dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
+    else if (D == 64 && items <= n_cu)
+        // At most one workgroup per CU: two key halves per workgroup (four 64-key buffers fit
+        // at head_dim 64) double the waves on each CU and halve the heaviest block's chain.
+        // With more query blocks than CUs two workgroups share a CU and the plain kernel is
+        // faster (C5 P = 2048: 84 against 88 us; P = 512: 25.8 against 23.9 us with halves).
+        hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, false, false, D == 64 ? 2 : 1>),
+                           dim3(items, ksplit), dim3((D == 64 ? 2 : 1) * G * NB * 64), 0, stream,
+                           a, ws, tile0, n_tiles, ksplit);
     else
         hipLaunchKernelGGL((pk::prefill_attn2_kernel<D, G, NB, 1, false>), dim3(items, ksplit),
                            dim3(G * NB * 64), 0, stream, a, ws, tile0, n_tiles, ksplit);
@@ -52,9 +60,9 @@ hipError_t launch_attn_dg(const pk::PrefillArgs& a, const uint4* ws, int tile0, 
     constexpr int NB = nb_big(G);
     if constexpr (NB > 1) {
         if (prefill_items(a.P, a.Hkv, NB) < 2 * n_cu)
-            return launch_attn_dgn<D, G, NB / 2>(a, ws, tile0, n_tiles, ksplit, stream);
+            return launch_attn_dgn<D, G, NB / 2>(a, ws, tile0, n_tiles, ksplit, n_cu, stream);
     }
-    return launch_attn_dgn<D, G, NB>(a, ws, tile0, n_tiles, ksplit, stream);
+    return launch_attn_dgn<D, G, NB>(a, ws, tile0, n_tiles, ksplit, n_cu, stream);
 }
 
 template <int D>

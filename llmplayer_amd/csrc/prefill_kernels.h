@@ -574,8 +574,8 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
 template <int D, int G, bool DIRECT>
 constexpr int attn_waves_per_eu() { return (D == 64 && G >= 2 && !DIRECT) ? 4 : 1; }
 
-template <int D, int G, int NB, int HPW, bool DIRECT = false, bool Q8 = false>
-__global__ __launch_bounds__((G / HPW) * NB * 64)
+template <int D, int G, int NB, int HPW, bool DIRECT = false, bool Q8 = false, int KH = 1>
+__global__ __launch_bounds__(KH * (G / HPW) * NB * 64)
 __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<D, G, DIRECT>())))
 void prefill_attn2_kernel(PrefillArgs a,
                                                                             const uint4* ws,
@@ -583,22 +583,32 @@ void prefill_attn2_kernel(PrefillArgs a,
                                                                             int ksplit) {
     using T = TileLds<D, DIRECT ? direct_tile_keys<D>() : tile_keys<D>()>;
     constexpr int HG = G / HPW;
-    constexpr int NTHR = HG * NB * 64;
+    constexpr int WH = HG * NB;           // waves of one key half
+    constexpr int NTHR = WH * 64;         // threads of one key half (all of them when KH = 1)
     constexpr int KS = D / 32, DT = D / 16, TK = T::TK, NKT = TK / 16, NC = TK / 32;
     constexpr int IMG = tile_img_u4<D>();
     constexpr int PER = (IMG + NTHR - 1) / NTHR;
     static_assert(G % HPW == 0, "heads per wave must divide the group");
-    __shared__ T buf[2];
+    static_assert(KH == 1 || (KH == 2 && !DIRECT), "key halves stage tile images");
+    __shared__ T buf[2 * KH];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // KH = 2: two halves of WH waves each take the same queries; half 0 the first half of the
+    // item's key tiles, half 1 the second, in lockstep (one barrier per tile pair), each with
+    // its own two LDS buffers; half 1 hands its state to half 0 through LDS at the end.  The
+    // heaviest query block's chain is halved, with no partials in global memory.
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int half = KH == 2 ? wave_all / WH : 0, wave = wave_all - half * WH;
+    const int tid = threadIdx.x - half * NTHR;   // thread index within the half
     const int col = lane & 15, grp = lane >> 4;
     const int nblk = (a.P + 16 * NB - 1) / (16 * NB);
     // Grid x: nblk*Hkv items ranked by key count (rank r: block nblk-1-r/Hkv, head r%Hkv).
     // The first half of the grid takes ranks heaviest-first, the second half lightest-first,
     // so the two workgroups a CU holds at once carry about equal total work.  Grid y: split
     // of the item's key tiles (ksplit > 1 writes partials for prefill_combine_kernel).
-    const int n_items = nblk * a.Hkv, L = (int)blockIdx.x, half = (n_items + 1) / 2;
-    const int rank = L < half ? L : n_items - 1 - (L - half);
+    // With key halves a workgroup fills a CU alone: plain heaviest-first order, and the
+    // dispatcher hands each freed CU the next item.
+    const int n_items = nblk * a.Hkv, L = (int)blockIdx.x, mid = (n_items + 1) / 2;
+    const int rank = KH == 2 ? L : (L < mid ? L : n_items - 1 - (L - mid));
     const int kvh = rank % a.Hkv;
     const int blk = nblk - 1 - rank / a.Hkv;
     const int ks = blockIdx.y;
@@ -616,6 +626,11 @@ void prefill_attn2_kernel(PrefillArgs a,
     const int t_all0 = kbeg / TK, t_all1 = (kend - 1) / TK;
     const int per = (t_all1 - t_all0 + ksplit) / ksplit;            // tiles per split
     const int t_first = t_all0 + ks * per, t_last = min(t_all1, t_first + per - 1);
+    // This half's tiles [tb, tb + nh) and the workgroup's trip count n_iter (half 0's).
+    const int n_split = max(0, t_last - t_first + 1);
+    const int n_iter = KH == 2 ? (n_split + 1) / 2 : n_split;
+    const int tb = t_first + (half ? n_iter : 0);
+    const int nh = half ? n_split - n_iter : n_iter;
     const int w_lo = a.pos0 + i0 + 16 * sb;           // first query position of the wave
     const bool w_full = i0 + 16 * sb + 15 < a.P;
     const int w_start_max = a.window > 0 ? max(0, w_lo + 15 - a.window + 1) : 0;
@@ -637,12 +652,13 @@ void prefill_attn2_kernel(PrefillArgs a,
 
     // The first tile's loads go out before the query fragments are read and prepared, so the
     // two memory round trips of the prologue overlap.
-    const bool has_keys = t_first <= t_last;   // a split past the item's last tile: neutral partial
+    const bool has_keys = nh > 0;   // a split past the item's last tile: neutral partial
+    T* hbuf = buf + 2 * half;
     if (has_keys) {
         if constexpr (DIRECT)
-            raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, t_first * TK, kend - 1, tid);
+            raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, tb * TK, kend - 1, tid);
         else
-            img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first - tile0) * IMG, tid);
+            img_load<PER, NTHR, IMG>(stage, img + (size_t)(tb - tile0) * IMG, tid);
     }
     f16x8 qh[HPW][KS], ql[HPW][KS];
 #pragma unroll
@@ -650,18 +666,20 @@ void prefill_attn2_kernel(PrefillArgs a,
         query_fragment<D>(a, q_ok ? qi : a.P - 1, kvh * G + hg * HPW + hh, qpos, grp, qh[hh], ql[hh]);
     if (has_keys) {
         if constexpr (DIRECT) {
-            raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, buf[0], tid);
-            if (t_first + 1 <= t_last)
-                raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (t_first + 1) * TK, kend - 1, tid);
+            raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, hbuf[0], tid);
+            if (nh > 1)
+                raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (tb + 1) * TK, kend - 1, tid);
         } else {
-            img_store<PER, NTHR, IMG>(stage, &buf[0], tid);
-            if (t_first + 1 <= t_last)
-                img_load<PER, NTHR, IMG>(stage, img + (size_t)(t_first + 1 - tile0) * IMG, tid);
+            img_store<PER, NTHR, IMG>(stage, &hbuf[0], tid);
+            if (nh > 1) img_load<PER, NTHR, IMG>(stage, img + (size_t)(tb + 1 - tile0) * IMG, tid);
         }
-        __syncthreads();
     }
-    for (int tile = t_first; tile <= t_last; ++tile) {
-        const T& t = buf[(tile - t_first) & 1];
+    if (n_iter > 0) __syncthreads();
+    for (int it = 0; it < n_iter; ++it) {
+      // half 1 sits out the last trip when the split has an odd tile count (still at the barrier)
+      if (KH == 1 || it < nh) {
+        const int tile = tb + it;
+        const T& t = hbuf[it & 1];
         const int t0 = tile * TK;
         // S^T = K Q^T per 16-key sub-tile: lane holds keys 4*grp + j of sub-tile kt.
         floatx4 st[HPW][NKT];
@@ -779,18 +797,52 @@ void prefill_attn2_kernel(PrefillArgs a,
         else pv(std::false_type{});
         // Next buffer: tile+1 (already in registers) to LDS, tile+2 loads in flight.  The
         // buffer written here was last read before the previous iteration's barrier.
-        if (tile + 1 <= t_last) {
+        if (it + 1 < nh) {
             if constexpr (DIRECT) {
-                raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, buf[(tile + 1 - t_first) & 1], tid);
-                if (tile + 2 <= t_last)
+                raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, hbuf[(it + 1) & 1], tid);
+                if (it + 2 < nh)
                     raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (tile + 2) * TK, kend - 1, tid);
             } else {
-                img_store<PER, NTHR, IMG>(stage, &buf[(tile + 1 - t_first) & 1], tid);
-                if (tile + 2 <= t_last)
+                img_store<PER, NTHR, IMG>(stage, &hbuf[(it + 1) & 1], tid);
+                if (it + 2 < nh)
                     img_load<PER, NTHR, IMG>(stage, img + (size_t)(tile + 2 - tile0) * IMG, tid);
             }
         }
+      }
         __syncthreads();
+    }
+    if constexpr (KH == 2) {
+        // Half 1's state (m, l per lane, o) to half 0 through the tile buffers, whose last
+        // reads ended at the loop's final barrier; half 0 merges it into its own.
+        constexpr int XS = HPW * (2 + 4 * DT);   // floats per lane
+        static_assert((size_t)WH * 64 * XS * sizeof(float) <= sizeof(buf), "exchange fits the tiles");
+        float* xch = reinterpret_cast<float*>(&buf[0]) + (size_t)(wave * 64 + lane) * XS;
+        if (half == 1) {
+#pragma unroll
+            for (int hh = 0; hh < HPW; ++hh) {
+                xch[hh * (2 + 4 * DT)] = m[hh];
+                xch[hh * (2 + 4 * DT) + 1] = l[hh];
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) xch[hh * (2 + 4 * DT) + 2 + 4 * d + j] = o[hh][d][j];
+            }
+        }
+        __syncthreads();
+        if (half == 1) return;
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh) {
+            const float mb = xch[hh * (2 + 4 * DT)], lb = xch[hh * (2 + 4 * DT) + 1];
+            const float mn = fmaxf(m[hh], mb);
+            const float sa = dk::fast_exp2(m[hh] - mn), sb2 = dk::fast_exp2(mb - mn);
+            l[hh] = __builtin_fmaf(l[hh], sa, lb * sb2);
+#pragma unroll
+            for (int d = 0; d < DT; ++d)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    o[hh][d][j] = __builtin_fmaf(o[hh][d][j], sa, xch[hh * (2 + 4 * DT) + 2 + 4 * d + j] * sb2);
+            m[hh] = mn;
+        }
     }
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
