@@ -423,17 +423,35 @@ __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int
         const int half = a.half_rope;
         if (a.rope_type == 0) {
 #pragma unroll
-            for (int s = 0; s < KS; ++s)
+            for (int s = 0; s < KS; ++s) {
+                // the lane's 4 pairs are consecutive table entries: one 16-byte load each for
+                // cos and sin when all 4 rotate and the rows are 16-byte aligned
+                const int i0 = 16 * s + 4 * grp;
+                float cv[4], sv[4];
+                if ((half & 3) == 0 && i0 + 3 < half) {
+                    const float4 c4 = *reinterpret_cast<const float4*>(cr + i0);
+                    const float4 s4 = *reinterpret_cast<const float4*>(sr + i0);
+                    cv[0] = c4.x; cv[1] = c4.y; cv[2] = c4.z; cv[3] = c4.w;
+                    sv[0] = s4.x; sv[1] = s4.y; sv[2] = s4.z; sv[3] = s4.w;
+                } else {
 #pragma unroll
-                for (int j = 0; j < 8; j += 2) {
-                    const int i = (32 * s + 8 * grp + j) / 2;
-                    const bool rot = i < half;
-                    const float c = cr[rot ? i : 0], sn = sr[rot ? i : 0];
+                    for (int u = 0; u < 4; ++u) {
+                        const bool rot = i0 + u < half;
+                        cv[u] = cr[rot ? i0 + u : 0];
+                        sv[u] = sr[rot ? i0 + u : 0];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int j = 2 * u;
+                    const bool rot = i0 + u < half;
+                    const float c = cv[u], sn = sv[u];
                     const float v0 = qf[s][j], v1 = qf[s][j + 1];
                     const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
                     qf[s][j] = rot ? t0 - t1 : v0;
                     qf[s][j + 1] = rot ? t2 + t3 : v1;
                 }
+            }
         } else {  // NEOX: pairs (i, i + half) for i < half; dims >= 2*half keep their values
 #pragma unroll
             for (int s = 0; s < KS; ++s)
