@@ -266,7 +266,7 @@ int llmp_graph_destroy(uint64_t graph);
  * the handle's contract) and attention reads every row dequantised (quant * block scale), as
  * the reference's sequential forwards over KVCache Mode.Q8_0 do.
  * Partial RoPE (rotated dims < head_dim, NORMAL or NEOX pairs) is applied as in decode.
- * The handle keeps a workspace for the key tiles a call attends (bf16 hi/lo images of K and
+ * The handle keeps a workspace for the key tiles a call attends (fp16 hi/lo images of K and
  * V: about 9 bytes per key, KV head and head_dim element); a call that needs more than any
  * earlier call grows it (hipFree + hipMalloc: such a call cannot be captured in a graph, and
  * graphs captured before it must not be replayed after it). */
@@ -290,7 +290,7 @@ int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0
  *   q:   device fp32 [n_tokens][n_heads*head_dim]   (4-byte aligned)
  *   k,v: device fp32 [n_tokens][n_kv_heads*head_dim]
  * The appended rows are bit-identical to n_tokens llmp_attn_decode calls on the same fp32
- * inputs; attention runs on the same bf16 hi/lo MFMA path (K, V and P each split, so fp32
+ * inputs; attention runs on the same fp16 hi/lo MFMA path (K, V and P each split, so fp32
  * rows keep ~2^-16 relative precision per product).  gate may be 0. */
 int llmp_attn_prefill_f32(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                           uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);

@@ -80,7 +80,7 @@ namespace pk {
 struct PrefillArgs;
 }
 // Prefill, three launches: exact K/V append of all prompt tokens (one workgroup per token);
-// tile images (the bf16 hi/lo split of key tiles [tile0, tile0 + n_tiles) of every KV head,
+// tile images (the fp16 hi/lo split of key tiles [tile0, tile0 + n_tiles) of every KV head,
 // V transposed) into `ws`; the MFMA causal attention over those images.  All return
 // hipErrorInvalidValue for an unsupported shape.
 hipError_t launch_prefill_append(const pk::PrefillArgs& a, int head_dim, hipStream_t stream);
