@@ -393,25 +393,36 @@ __device__ __forceinline__ float seq_rms_inv(const float* x, float eps) {
 // heads < n_w0 and p.knw for the others, then RoPE.  The sum of squares follows
 // SimdVectorOps.dot's 8-lane FMA order, or with `seq` RMSNorm.apply's sequential one.  Must
 // be called by the whole workgroup (NTHR threads).
+//
+// Every phase loads its LDS operands before it computes: a chain that waits for each load in
+// turn costs an LDS round trip per step (head_dim 256: 32 dependent reads per partial sum).
+// The scaling and the rotation run as one pass over (head, pair) slots: slot i < half_rope is
+// the rotated pair (2i, 2i+1) (NORMAL) or (i, half_rope + i) (NEOX); every other slot is the
+// unrotated pair (2i, 2i+1), so each element is read and written once.  The float steps are
+// those of the CPU path: (x * r) * w, then x0*c - x1*s and x0*s + x1*c.
 template <int D, int NTHR, class HP = HeadPrep>
 __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* s_r,
                                const HP& p, int tid, bool seq = false) {
-    if (p.qnw != nullptr && seq) {
+    const bool norm = p.qnw != nullptr;
+    const bool rope = p.cos_row != nullptr;
+    if (norm && seq) {
         for (int t = tid; t < nh; t += NTHR) s_r[t] = seq_rms_inv<D>(x + t * D, p.eps);
         __syncthreads();
-        for (int i = tid; i < nh * D; i += NTHR) {
-            const int hh = i / D;
-            const auto w = (hh < n_w0) ? p.qnw : p.knw;
-            const float xs = x[i] * s_r[hh];
-            x[i] = xs * w[i - hh * D];
-        }
-        __syncthreads();
-    } else if (p.qnw != nullptr) {
+    } else if (norm) {
+        constexpr int NV = D / 8;                       // values per partial sum
+        constexpr int CH = NV % 8 == 0 ? 8 : NV;        // loaded ahead of their FMAs
         for (int t = tid; t < nh * 8; t += NTHR) {
             const int hh = t >> 3, ln = t & 7;
-            const float* xh = x + hh * D;
+            const float* xh = x + hh * D + ln;
             float acc = 0.0f;
-            for (int i = ln; i < D; i += 8) acc = __builtin_fmaf(xh[i], xh[i], acc);
+#pragma unroll
+            for (int k0 = 0; k0 < NV; k0 += CH) {
+                float v[CH];
+#pragma unroll
+                for (int k = 0; k < CH; ++k) v[k] = xh[8 * (k0 + k)];
+#pragma unroll
+                for (int k = 0; k < CH; ++k) acc = __builtin_fmaf(v[k], v[k], acc);
+            }
             s_acc[t] = acc;
         }
         __syncthreads();
@@ -426,29 +437,59 @@ __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* 
             s_r[t] = 1.0f / r;
         }
         __syncthreads();
-        for (int i = tid; i < nh * D; i += NTHR) {
-            const int hh = i / D;
-            const auto w = (hh < n_w0) ? p.qnw : p.knw;
-            const float xs = x[i] * s_r[hh];
-            x[i] = xs * w[i - hh * D];
-        }
-        __syncthreads();
     }
-    if (p.cos_row != nullptr) {
-        const int half = p.half_rope;
-        for (int idx = tid; idx < nh * half; idx += NTHR) {
-            const int hh = idx / half, i = idx - hh * half;
-            float* xh = x + hh * D;
-            const int i0 = (p.rope_type == 0) ? 2 * i : i;
-            const int i1 = (p.rope_type == 0) ? 2 * i + 1 : half + i;
-            const float c = p.cos_row[i], sn = p.sin_row[i];
-            const float v0 = xh[i0], v1 = xh[i1];
-            const float t0 = v0 * c, t1 = v1 * sn, t2 = v0 * sn, t3 = v1 * c;
-            xh[i0] = t0 - t1;
-            xh[i1] = t2 + t3;
+    if (!norm && !rope) return;
+    constexpr int HALF = D / 2;
+    constexpr int SL = 4;   // slots per thread per round, loaded together
+    const int n_slots = nh * HALF;
+    const int half = rope ? p.half_rope : 0;
+    const bool neox = p.rope_type != 0;
+    for (int base = tid; base < n_slots; base += SL * NTHR) {
+        float v0[SL], v1[SL], w0[SL], w1[SL], r[SL], c[SL], sn[SL];
+        int o0[SL], o1[SL];
+#pragma unroll
+        for (int k = 0; k < SL; ++k) {
+            const int slot = min(base + k * NTHR, n_slots - 1);
+            const int hh = slot / HALF, i = slot - hh * HALF;
+            const bool rot = i < half;
+            const int i0 = (rot && neox) ? i : 2 * i;
+            const int i1 = (rot && neox) ? half + i : 2 * i + 1;
+            o0[k] = hh * D + i0;
+            o1[k] = hh * D + i1;
+            v0[k] = x[o0[k]];
+            v1[k] = x[o1[k]];
+            if (norm) {
+                const auto w = (hh < n_w0) ? p.qnw : p.knw;
+                r[k] = s_r[hh];
+                w0[k] = w[i0];
+                w1[k] = w[i1];
+            }
+            if (rope) {
+                const int ic = rot ? i : 0;
+                c[k] = p.cos_row[ic];
+                sn[k] = p.sin_row[ic];
+            }
         }
-        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < SL; ++k) {
+            if (base + k * NTHR >= n_slots) break;
+            const int i = (base + k * NTHR) % HALF;
+            float a0 = v0[k], a1 = v1[k];
+            if (norm) {
+                const float xs0 = a0 * r[k], xs1 = a1 * r[k];
+                a0 = xs0 * w0[k];
+                a1 = xs1 * w1[k];
+            }
+            if (i < half) {
+                const float t0 = a0 * c[k], t1 = a1 * sn[k], t2 = a0 * sn[k], t3 = a1 * c[k];
+                a0 = t0 - t1;
+                a1 = t2 + t3;
+            }
+            x[o0[k]] = a0;
+            x[o1[k]] = a1;
+        }
     }
+    __syncthreads();
 }
 
 // Rotation of the lane's own q slice in registers (no QK-norm; NORMAL pairs sit inside one
