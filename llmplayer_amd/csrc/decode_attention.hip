@@ -152,37 +152,48 @@ hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int
     return hipLaunchKernel(k.fn, dim3(a.splits, n_kv_heads), dim3(k.waves * 64), params, 0, stream);
 }
 
+namespace {
+// Column workgroups per head for the combine: the fewest (1, 2, 4, 8) with which each thread's
+// splits fit in one batch of loads, keeping at least 4 float4 columns per workgroup.
+template <int D>
+hipError_t launch_reduce_d(const DecodeArgs& a, int group, int n_heads, hipStream_t stream) {
+    constexpr int NC = D / 4;
+    int cb = 1;
+    while (cb < 8 && NC % (2 * cb) == 0 && NC / (2 * cb) >= 4 &&
+           a.splits > dk::kReduceBatch * (dk::kReduceThreads / (NC / cb)))
+        cb *= 2;
+    const dim3 grid(n_heads, cb), block(dk::kReduceThreads);
+    switch (cb) {
+    case 1: hipLaunchKernelGGL((dk::decode_reduce_kernel<D, 1>), grid, block, 0, stream, a, group); break;
+    case 2:
+        if constexpr (NC % 2 == 0)
+            hipLaunchKernelGGL((dk::decode_reduce_kernel<D, 2>), grid, block, 0, stream, a, group);
+        break;
+    case 4:
+        if constexpr (NC % 4 == 0)
+            hipLaunchKernelGGL((dk::decode_reduce_kernel<D, 4>), grid, block, 0, stream, a, group);
+        break;
+    default:
+        if constexpr (NC % 8 == 0)
+            hipLaunchKernelGGL((dk::decode_reduce_kernel<D, 8>), grid, block, 0, stream, a, group);
+        break;
+    }
+    return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,
                                 hipStream_t stream) {
     if (a.splits > kMaxSplits) return hipErrorInvalidValue;
     switch (head_dim) {
-    case 64:
-        hipLaunchKernelGGL(dk::decode_reduce_kernel<64>, dim3(n_heads), dim3(dk::kReduceThreads),
-                           0, stream, a, group);
-        break;
-    case 128:
-        hipLaunchKernelGGL(dk::decode_reduce_kernel<128>, dim3(n_heads),
-                           dim3(dk::kReduceThreads), 0, stream, a, group);
-        break;
-    case 256:
-        hipLaunchKernelGGL(dk::decode_reduce_kernel<256>, dim3(n_heads),
-                           dim3(dk::kReduceThreads), 0, stream, a, group);
-        break;
-    case 512:
-        hipLaunchKernelGGL(dk::decode_reduce_kernel<512>, dim3(n_heads),
-                           dim3(dk::kReduceThreads), 0, stream, a, group);
-        break;
-    case 80:
-        hipLaunchKernelGGL(dk::decode_reduce_kernel<80>, dim3(n_heads),
-                           dim3(dk::kReduceThreads), 0, stream, a, group);
-        break;
-    case 96:
-        hipLaunchKernelGGL(dk::decode_reduce_kernel<96>, dim3(n_heads),
-                           dim3(dk::kReduceThreads), 0, stream, a, group);
-        break;
+    case 64: return launch_reduce_d<64>(a, group, n_heads, stream);
+    case 128: return launch_reduce_d<128>(a, group, n_heads, stream);
+    case 256: return launch_reduce_d<256>(a, group, n_heads, stream);
+    case 512: return launch_reduce_d<512>(a, group, n_heads, stream);
+    case 80: return launch_reduce_d<80>(a, group, n_heads, stream);
+    case 96: return launch_reduce_d<96>(a, group, n_heads, stream);
     default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t stream) {

@@ -1395,16 +1395,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
 constexpr int kReduceThreads = 256;
 constexpr int kReduceBatch = 12;   // splits per thread loaded up front (96 splits at head_dim 128)
 
-template <int D>
+// CB workgroups per query head (blockIdx.y), each owning D/CB of the columns: with many splits
+// per head the loads of one workgroup would take several rounds (CB is picked on the host so
+// that every thread's splits fit in one batch).
+template <int D, int CB = 1>
 __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArgs a, int G) {
-    constexpr int NC = D / 4;                 // float4 columns
+    static_assert((D / 4) % CB == 0, "whole float4 columns per workgroup");
+    constexpr int NC = D / 4 / CB;            // float4 columns of this workgroup
     constexpr int NP = kReduceThreads / NC;   // split groups
     __shared__ float s_m[NP], s_l[NP];
     __shared__ float4 s_o[NP][NC];
     const int hq = blockIdx.x;
     const int kvh = hq / G, h = hq - kvh * G;
     const int tid = threadIdx.x;
-    const int c = tid % NC, p = tid / NC;
+    const int cl = tid % NC, p = tid / NC;
+    const int c = (CB > 1 ? (int)blockIdx.y * NC : 0) + cl;   // float4 column of the head
     const bool act = p < NP;   // NC need not divide the block: the spare threads only sync
     load_args_now(a);
     const int pos = step_position(a);
@@ -1455,11 +1460,11 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
         o.w = __builtin_fmaf(o.w, so, oj.w * sj);
         m = mn;
     }
-    if (act && c == 0) {
+    if (act && cl == 0) {
         s_m[p] = m;
         s_l[p] = l;
     }
-    if (act) s_o[p][c] = o;
+    if (act) s_o[p][cl] = o;
     __syncthreads();
     if (p == 0) {
         float M = s_m[0];
@@ -1469,7 +1474,7 @@ __global__ __launch_bounds__(kReduceThreads) void decode_reduce_kernel(DecodeArg
         for (int q = 0; q < NP; ++q) {
             const float sc = fast_exp2(s_m[q] - M);
             L = __builtin_fmaf(s_l[q], sc, L);
-            const float4 x = s_o[q][c];
+            const float4 x = s_o[q][cl];
             O.x = __builtin_fmaf(x.x, sc, O.x);
             O.y = __builtin_fmaf(x.y, sc, O.y);
             O.z = __builtin_fmaf(x.z, sc, O.z);
