@@ -46,12 +46,14 @@ LLMP_HD inline StepPlan plan_step(int pos, int window, int max_splits) {
 // Default split count of a decode step over n attended rows, given the CUs and the workgroups
 // of the chosen kernel resident per CU (per_cu; 1 for fp32 caches, which aim at one workgroup
 // per CU):
-//  - fp32: at least 32 rows per split, at most 128 splits per KV head; once a split holds 1024
-//    rows or more, `wide` is set (8-wave workgroups) and 3/4 of the splits run.
+//  - fp32: at least 32 rows per split (16 where 32-row splits of all KV heads would not cover
+//    half of the CUs: few KV heads over a short window), at most 128 splits per KV head; once a
+//    split holds 1024 rows or more, `wide` is set (8-wave workgroups) and 3/4 of the splits run.
 //  - Q8_0: one full round of resident workgroups over the chip, at least 160 rows per split.
 inline int default_splits(int n, int n_kv_heads, int n_cu, int per_cu, bool q8, bool* wide) {
     const int cu = n_cu > 0 ? n_cu : 256;
-    const int min_rows = q8 ? 160 : 32;
+    int min_rows = q8 ? 160 : 32;
+    if (!q8 && 2LL * n_kv_heads * (n / 32) < cu) min_rows = 16;
     const int by_rows = n / min_rows > 0 ? n / min_rows : 1;
     if (per_cu < 1) per_cu = 1;
     long long s = ((long long)per_cu * cu + n_kv_heads - 1) / n_kv_heads;
