@@ -688,8 +688,11 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     // Merge of the workgroup's partial softmax states (section 5): with LDS_MERGE every row
     // group of every wave leaves its raw (m, l, o) in LDS (NPART partials); otherwise the row
     // groups of a wave are merged in VGPRs first (WAVES partials).
+    // The LDS budget for it is 32 KB, or 64 KB for head_dim >= 256 at 4 waves, where the VGPR
+    // count (G * EPL values of o per lane) already allows no more than 2 waves per SIMD
+    // (Gemma-3 at 8k: -1 to -2 % per layer-call against the lane-exchange merge).
     constexpr int NPART_LDS = WAVES * RPW;
-    constexpr bool LDS_MERGE = NPART_LDS * G * D * 4 <= 32768;
+    constexpr bool LDS_MERGE = NPART_LDS * G * D * 4 <= (D >= 256 && WAVES == 4 ? 65536 : 32768);
     constexpr int NPART = LDS_MERGE ? NPART_LDS : WAVES;
     __shared__ float s_m[NPART * G];
     __shared__ float s_l[NPART * G];
