@@ -602,8 +602,7 @@ void gemv_kernel(GemvArgs a) {
     }
     float r = 1.0f;
     if (norm) {   // SimdVectorOps.rmsnorm's scale
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off);
+        ss = dk::row_group_sum<64>(ss);   // pairs at lane distance 1, 2, 4, ..., 32 (DPP, permlane)
         if (j == 0) red[wave] = ss;
         __syncthreads();
         float tot = red[0];

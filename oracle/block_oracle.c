@@ -238,7 +238,7 @@ void orc_rmsnorm(float *out, const float *x, const float *w, int size, float eps
 
 /* The library's staged RMSNorm: 256 threads, thread t sums the squares of the 4-value chunks
  * c = t, t+256, ... with FMAs (values in order); each 64-thread wave reduces by a butterfly
- * (xor 32, 16, 8, 4, 2, 1); the four wave totals are added in order; r = 1/(float)sqrt((double)
+ * (xor 1, 2, 4, 8, 16, 32); the four wave totals are added in order; r = 1/(float)sqrt((double)
  * (ss/size + eps)); out = (x*r)*w (size a multiple of 4). */
 void orc_rmsnorm_staged(float *out, const float *x, const float *w, int size, float eps)
 {
@@ -253,7 +253,7 @@ void orc_rmsnorm_staged(float *out, const float *x, const float *w, int size, fl
     for (int wv = 0; wv < 4; wv++) {
         float v[64], nv[64];
         memcpy(v, part + 64 * wv, sizeof(v));
-        for (int off = 32; off > 0; off >>= 1) {
+        for (int off = 1; off < 64; off <<= 1) {
             for (int i = 0; i < 64; i++) nv[i] = v[i] + v[i ^ off];
             memcpy(v, nv, sizeof(v));
         }
