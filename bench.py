@@ -416,7 +416,9 @@ def prefill_run(P: int, steps: int, q8: bool = False, f32: bool = False) -> dict
             "attn_kernel_us": round(res["attn"], 2), "append_kernel_us": round(res["append"], 2),
             "causal_tflops": round(flops / (us * 1e-6) / 1e12, 2),
             "attn_kernel_causal_tflops": round(flops / (res["attn"] * 1e-6) / 1e12, 2),
-            "mfma_tflops_bf16x3": round(3 * flops / (res["attn"] * 1e-6) / 1e12, 2)}
+            # fp16 MFMA work issued: 3 products for QK^T (hi/lo splits), 2 for PV when the V rows
+            # are fp16-exact (bf16 rows in an fp32 cache: the V-lo product is skipped), else 3
+            "mfma_tflops_issued_f16": round((3.0 if (f32 or q8) else 2.5) * flops / (res["attn"] * 1e-6) / 1e12, 2)}
 
 
 def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int, q8: bool = False,
