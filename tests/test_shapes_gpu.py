@@ -36,9 +36,12 @@ def _config(name, layers=1):
                            rope_freq_base=s["theta"], rope_dim_count=s.get("rope_dim", 0))
 
 
-@pytest.mark.parametrize("splits", [0, 1, 7])
+@pytest.mark.parametrize("splits", [0, 1, 7, 400])
 @pytest.mark.parametrize("name", list(SHAPES))
 def test_decode_new_shapes(name, splits):
+    # 400 splits (334 effective at 1000 rows) run the combine over 2-8 column workgroups per
+    # head, including 5 and 10 float4 columns per workgroup (head_dim 80) and the per-thread
+    # online merge past the first batch of splits (head_dim 96)
     c = _config(name)
     assert hfp.HipForwardPass.isSupportedForAttention(c)
     pos = 999
