@@ -94,8 +94,12 @@ __device__ __forceinline__ float in_val(const void* p, long long i, int f32) {
 // Every input of the workgroup (its K and V rows, the RoPE row, the K-norm weights) is requested
 // in one pass and staged in LDS, so the append costs one memory round trip before its stores.
 // LDS floats: Hkv*(2*D + 10) + 2*Hkv*D/32 + 2*D (prefill_append_lds).
+// At most 64 VGPRs (8 waves per SIMD): a long prompt's workgroups then all fit on the chip at
+// once (2048 four-wave workgroups at 8 waves per SIMD), where 7 waves per SIMD left a second
+// round of workgroups behind the first.
 template <int D, int NTHR>
-__global__ __launch_bounds__(NTHR) void prefill_append_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(8)))
+void prefill_append_kernel(PrefillArgs a) {
     extern __shared__ float s_dyn[];
     const int kvd = a.Hkv * D;
     float* s_k = s_dyn;                    // Hkv*D
