@@ -153,15 +153,11 @@ hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int
 }
 
 namespace {
-// Column workgroups per head for the combine: the fewest (1, 2, 4, 8) with which each thread's
-// splits fit in one batch of loads, keeping at least 4 float4 columns per workgroup.
+// The combine over reduce_column_groups(...) column workgroups per head.
 template <int D>
 hipError_t launch_reduce_d(const DecodeArgs& a, int group, int n_heads, hipStream_t stream) {
     constexpr int NC = D / 4;
-    int cb = 1;
-    while (cb < 8 && NC % (2 * cb) == 0 && NC / (2 * cb) >= 4 &&
-           a.splits > dk::kReduceBatch * (dk::kReduceThreads / (NC / cb)))
-        cb *= 2;
+    const int cb = reduce_column_groups(D, a.splits, dk::kReduceThreads, dk::kReduceBatch);
     const dim3 grid(n_heads, cb), block(dk::kReduceThreads);
     switch (cb) {
     case 1: hipLaunchKernelGGL((dk::decode_reduce_kernel<D, 1>), grid, block, 0, stream, a, group); break;

@@ -68,6 +68,19 @@ inline int default_splits(int n, int n_kv_heads, int n_cu, int per_cu, bool q8, 
     return (int)s;
 }
 
+// Workgroups per query head of the split combine (column groups of the head's D values): the
+// fewest of 1, 2, 4, 8 with which each of the `threads` threads of a group holds at most `batch`
+// of the `splits` partials (all its loads in one round), keeping whole float4 columns and at
+// least 4 of them per group.
+inline int reduce_column_groups(int D, int splits, int threads, int batch) {
+    const int nc = D / 4;
+    int cb = 1;
+    while (cb < 8 && nc % (2 * cb) == 0 && nc / (2 * cb) >= 4 &&
+           (long long)splits > (long long)batch * (threads / (nc / cb)))
+        cb *= 2;
+    return cb;
+}
+
 // Bytes of one row of `cols` weights in a GGML type's GGUF layout (GGMLType.java:4-35); 0 for
 // a type the library does not read.
 inline size_t ggml_row_bytes(int type, int cols) {

@@ -6,6 +6,7 @@
 //   relayout H N ROW IN HEADS BACK    -> "ok" (rows_to_heads(IN) to HEADS, heads_to_rows back to BACK)
 //   plan POS WINDOW SPLITS            -> "start n rows_per_split splits"
 //   splits N HKV NCU PERCU Q8         -> "splits wide"
+//   cgroups D SPLITS THREADS BATCH    -> "column groups of the split combine"
 #include <cstdio>
 #include <fstream>
 #include <iostream>
@@ -60,6 +61,10 @@ int main() {
             in >> pos >> window >> splits;
             const llmp::StepPlan p = llmp::plan_step(pos, window, splits);
             std::printf("%d %d %d %d\n", p.start, p.n, p.rows_per_split, p.splits);
+        } else if (cmd == "cgroups") {
+            int d, splits, threads, batch;
+            in >> d >> splits >> threads >> batch;
+            std::printf("%d\n", llmp::reduce_column_groups(d, splits, threads, batch));
         } else if (cmd == "splits") {
             int n, hkv, ncu, per_cu, q8;
             in >> n >> hkv >> ncu >> per_cu >> q8;

@@ -183,6 +183,31 @@ def test_default_splits(driver):
             assert n // s >= (160 if q else (16 if few else 32)), (n, h, c, p, q, line)
 
 
+def test_combine_column_groups(driver):
+    """The combine's column workgroups per head (256 threads, 12 splits per thread in one batch):
+    the known launches (C3 at 24/96 splits and Gemma-3's 128 splits at head_dim 256 run 1 and 4
+    groups), and in general the fewest of 1/2/4/8 with which the batch covers the splits, whole
+    float4 columns and at least 4 of them per group."""
+    exe, _ = driver
+    known = [(128, 24, 1), (128, 96, 1), (128, 97, 2), (256, 128, 4), (256, 48, 1), (128, 1000, 8),
+             (80, 400, 4), (96, 400, 4), (96, 1000, 4), (64, 192, 1), (64, 193, 2), (512, 128, 8)]
+    out = _run(exe, [f"cgroups {d} {s} 256 12" for d, s, _ in known])
+    assert [int(x) for x in out] == [cb for _, _, cb in known]
+    cases = [(d, s) for d in (64, 80, 96, 128, 256, 512) for s in (1, 2, 12, 47, 48, 49, 95, 96, 97, 191, 192,
+                                                               193, 383, 384, 385, 767, 768, 769, 1024)]
+    out = _run(exe, [f"cgroups {d} {s} 256 12" for d, s in cases])
+    for (d, s), line in zip(cases, out):
+        cb = int(line)
+        nc = d // 4
+        assert cb in (1, 2, 4, 8) and nc % cb == 0, (d, s, cb)
+        assert cb == 1 or nc // cb >= 4, (d, s, cb)
+        fits = lambda g: s <= 12 * (256 // (nc // g))
+        if cb > 1:
+            assert not fits(cb // 2), (d, s, cb)          # the fewest groups
+        if not fits(cb):                                  # more groups only when it cannot split further
+            assert cb == 8 or nc % (2 * cb) or nc // (2 * cb) < 4, (d, s, cb)
+
+
 def test_oracle_under_sanitizers(tmp_path):
     """tests/test_oracle.py and tests/test_block_oracle.py against the sanitized oracle build."""
     asan_dir = tmp_path / "asan"

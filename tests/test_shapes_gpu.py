@@ -40,8 +40,7 @@ def _config(name, layers=1):
 @pytest.mark.parametrize("name", list(SHAPES))
 def test_decode_new_shapes(name, splits):
     # 400 splits (334 effective at 1000 rows) run the combine over 2-8 column workgroups per
-    # head, including 5 and 10 float4 columns per workgroup (head_dim 80) and the per-thread
-    # online merge past the first batch of splits (head_dim 96)
+    # head, including 5 and 6 float4 columns per workgroup (head_dim 80 and 96)
     c = _config(name)
     assert hfp.HipForwardPass.isSupportedForAttention(c)
     pos = 999
