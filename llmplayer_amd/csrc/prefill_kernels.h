@@ -302,7 +302,9 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
                                                             int n_tiles, int row_end) {
     using T = TileLds<D>;
     constexpr int TK = T::TK;
-    __shared__ T t;
+    // The image has the LDS tile's layout; each thread writes its converted chunks to it
+    // directly (no staging through LDS, so no copy-out pass behind a barrier).
+    T& t = *reinterpret_cast<T*>(ws + ((size_t)blockIdx.y * n_tiles + blockIdx.x) * tile_img_u4<D>());
     const int tid = threadIdx.x, kvh = blockIdx.y;
     const int r0 = (tile0 + (int)blockIdx.x) * TK;
     const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);
@@ -359,14 +361,9 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
             *reinterpret_cast<uint2*>(&t.vl[d * T::VP + vt_keys_off(rq)]) = make_uint2(l0, l1);
         }
     }
+    // The flag word sits in the padding of K row 0 (kh[D], kh[D + 1]), which no chunk covers.
     const unsigned any_vlo = __syncthreads_or(vlo ? 1 : 0) ? 1u : 0u;
-    const uint4* src = reinterpret_cast<const uint4*>(&t);
-    uint4* dst = ws + ((size_t)kvh * n_tiles + blockIdx.x) * tile_img_u4<D>();
-    for (int i = tid; i < tile_img_u4<D>(); i += NTHR) {
-        uint4 c = src[i];
-        if (i == vlo_flag_chunk<D>()) c.x = any_vlo;
-        dst[i] = c;
-    }
+    if (tid == 0) reinterpret_cast<uint4*>(&t)[vlo_flag_chunk<D>()].x = any_vlo;
 }
 
 // ---- 3. Double-buffered MFMA attention ------------------------------------------------------
