@@ -114,6 +114,34 @@ void prefill_append_kernel(PrefillArgs a) {
     const int i = blockIdx.x, tid = threadIdx.x;
     const int pos = a.pos0 + i;
     const bool rope = a.cos_t != nullptr, qkn = a.qnw != nullptr;
+    if (!qkn && a.v_norm == 0 && a.kq == nullptr) {
+        // fp32 cache, no QK-norm or V-norm: each thread rotates whole (head, pair) slots in
+        // registers, with the slot map and float steps of prep_heads_lds (no LDS, no barrier).
+        constexpr int HALF = D / 2;
+        const int half = rope ? a.half_rope : 0;
+        const bool neox = a.rope_type != 0;
+        for (int sl = tid; sl < a.Hkv * HALF; sl += NTHR) {
+            const int h = sl / HALF, p = sl - h * HALF;
+            const bool rot = p < half;
+            const int i0 = (rot && neox) ? p : 2 * p, i1 = (rot && neox) ? half + p : 2 * p + 1;
+            const long long in0 = (long long)i * kvd + (long long)h * D;
+            float k0 = in_val(a.k, in0 + i0, a.in_f32), k1 = in_val(a.k, in0 + i1, a.in_f32);
+            const float v0 = in_val(a.v, in0 + i0, a.in_f32), v1 = in_val(a.v, in0 + i1, a.in_f32);
+            if (rot) {
+                const float c = a.cos_t[(long long)pos * a.half_rope + p];
+                const float sn = a.sin_t[(long long)pos * a.half_rope + p];
+                const float t0 = k0 * c, t1 = k1 * sn, t2 = k0 * sn, t3 = k1 * c;
+                k0 = t0 - t1;
+                k1 = t2 + t3;
+            }
+            const long long off = (long long)h * a.head_stride + (long long)pos * D;
+            a.kc[off + i0] = k0;
+            a.kc[off + i1] = k1;
+            a.vc[off + i0] = v0;
+            a.vc[off + i1] = v1;
+        }
+        return;
+    }
     for (int e = tid; e < kvd; e += NTHR) {
         s_k[e] = in_val(a.k, (long long)i * kvd + e, a.in_f32);
         s_v[e] = in_val(a.v, (long long)i * kvd + e, a.in_f32);
