@@ -782,8 +782,11 @@ void prefill_attn2_kernel(PrefillArgs a,
                 for (int j = 0; j < 4; ++j) mt = fmaxf(mt, st[hh][kt][j]);
             mt = dk::lane_step<16, true>(mt);
             mt = dk::lane_step<32, true>(mt);
-            // rescale only when some row's running max grew: otherwise alpha is exactly 1
-            if (__any(mt > m[hh])) {
+            // Rescaled on every tile, with no branch: alpha is exactly 1 where the running max
+            // did not grow.  A branch on "some row grew" split the loop body into blocks the
+            // scheduler could not interleave (C5 P = 2048: 86.2 -> 84.0 us per call; 16-token
+            // verification at 32k: 72.4 -> 67.6 us).
+            {
                 const float mn = fmaxf(m[hh], mt);
                 const float alpha = dk::fast_exp2(m[hh] - mn);
                 m[hh] = mn;
