@@ -449,7 +449,9 @@ __device__ void prep_heads_lds(float* x, int nh, int n_w0, float* s_acc, float* 
         int o0[SL], o1[SL];
 #pragma unroll
         for (int k = 0; k < SL; ++k) {
-            const int slot = min(base + k * NTHR, n_slots - 1);
+            // a slot past the end re-reads this thread's own first slot (its result is dropped),
+            // so no thread reads an element another thread rewrites in this round
+            const int slot = base + k * NTHR < n_slots ? base + k * NTHR : base;
             const int hh = slot / HALF, i = slot - hh * HALF;
             const bool rot = i < half;
             const int i0 = (rot && neox) ? i : 2 * i;
