@@ -615,15 +615,21 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
 // Workgroup: KV head blockIdx.y, query tokens [i0, i0 + 16*NB) of its G query heads.  Wave:
 // 16 tokens (sub-block sb) x HPW query heads (head group hg), so each K/V fragment read from
 // LDS feeds HPW heads' MFMAs.  Tiles [tile0, tile0 + n_tiles) of the layer are in `ws`.
-// Waves per SIMD the register allocation must leave room for: head_dim 64 with image tiles
-// runs two 8-wave workgroups per CU (4 waves per SIMD, at most 128 VGPRs each); other shapes
-// are not constrained.
-template <int D, int G, bool DIRECT>
-constexpr int attn_waves_per_eu() { return (D == 64 && G >= 2 && !DIRECT) ? 4 : 1; }
+// Waves per SIMD the register allocation must leave room for: with head_dim 64 image tiles
+// as many as the LDS lets run at once (two 8-wave workgroups per CU: 4 waves per SIMD, at
+// most 128 VGPRs each; key halves: one 16-wave workgroup); other shapes are not constrained.
+template <int D, int G, int NB, int HPW, bool DIRECT, int KH>
+constexpr int attn_waves_per_eu() {
+    if (!(D == 64 && G >= 2 && !DIRECT)) return 1;
+    constexpr int waves = KH * (G / HPW) * NB;
+    constexpr int per_cu = (160 * 1024) / (2 * KH * (int)sizeof(TileLds<D>));   // LDS-bound
+    constexpr int w = per_cu * waves / 4;
+    return w < 1 ? 1 : (w > 4 ? 4 : w);
+}
 
 template <int D, int G, int NB, int HPW, bool DIRECT = false, bool Q8 = false, int KH = 1>
 __global__ __launch_bounds__(KH * (G / HPW) * NB * 64)
-__attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<D, G, DIRECT>())))
+__attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<D, G, NB, HPW, DIRECT, KH>())))
 void prefill_attn2_kernel(PrefillArgs a,
                                                                             const uint4* ws,
                                                                             int tile0, int n_tiles,
