@@ -600,17 +600,27 @@ void gemv_kernel(GemvArgs a) {
         ss = __builtin_fmaf(v.z, v.z, ss);
         ss = __builtin_fmaf(v.w, v.w, ss);
     }
-    float r = 1.0f;
-    if (norm) {   // SimdVectorOps.rmsnorm's scale
-        ss = dk::row_group_sum<64>(ss);   // pairs at lane distance 1, 2, 4, ..., 32 (DPP, permlane)
-        if (j == 0) red[wave] = ss;
-        __syncthreads();
+    // SimdVectorOps.rmsnorm's scale r from the waves' partial sums (read after a barrier).
+    auto rms_factor = [&]() {
         float tot = red[0];
 #pragma unroll
         for (int w = 1; w < kGemvThreads / 64; ++w) tot = tot + red[w];
         float v = tot / (float)a.cols;
         v = v + a.eps;
-        r = 1.0f / (float)__builtin_sqrt((double)v);
+        return 1.0f / (float)__builtin_sqrt((double)v);
+    };
+    // Without a Q8_1 staging (which quantises the normalised input itself) r multiplies each
+    // row's dot product instead: W ((x w) r) = (W (x w)) r, one rounding apart from the CPU
+    // path's (x r) w, so staging needs no barrier of its own before the dot's.
+    constexpr bool LATE_R = !L::Q8X;
+    float r = 1.0f;
+    if (norm) {
+        ss = dk::row_group_sum<64>(ss);   // pairs at lane distance 1, 2, 4, ..., 32 (DPP, permlane)
+        if (j == 0) red[wave] = ss;
+        if constexpr (!LATE_R) {
+            __syncthreads();
+            r = rms_factor();
+        }
     }
     float4* xs4 = reinterpret_cast<float4*>(xs);
     auto put = [&](int c, const float4& v) {   // the 8 lanes of a Q8_1 block call together
@@ -630,10 +640,12 @@ void gemv_kernel(GemvArgs a) {
     if (!second) F1::build_tab(r1.rw, tab, j, units1);
     else F2::build_tab(r2.rw, tab, j, units2);
     __syncthreads();
+    if (LATE_R && norm) r = rms_factor();
 
     const Staged st{xs, xsum, tab, xq, xd, xss};
     float acc = !second ? row_dot(r1, st, sg, row, j, units1) : row_dot(r2, st, sg, row, j, units2);
     acc = dk::row_group_sum<64>(acc);
+    if (LATE_R) acc = acc * r;
     if (live && j == 0) store_row(a, sg, row_g, row, acc);
 }
 
