@@ -231,7 +231,7 @@ int llmp_attn_decode_shared(uint64_t handle, int layer, int src_layer, int posit
                             int splits, uint64_t stream);
 
 /* Launch plan llmp_attn_decode would use for this call: splits per KV head, waves per
- * workgroup (4 or 8), rows per split and the first attended position.  Any out may be NULL. */
+ * workgroup (2, 4 or 8), rows per split and the first attended position.  Any out may be NULL. */
 int llmp_decode_plan(uint64_t handle, int layer, int position, int splits, int *out_splits,
                      int *out_waves, int *out_rows_per_split, int *out_start);
 

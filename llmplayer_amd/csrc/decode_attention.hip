@@ -54,11 +54,16 @@ SplitKernel kernel_dgw() {
 // 8-wave workgroups except where more than 4 query heads per KV head hold 16 elements per
 // lane (head_dim 256, or any Q8_0 cache): that register footprint leaves no room for them.
 // head_dim 512 always runs 4 waves (its per-wave LDS partials would pass 128 KB at 8).
+// head_dim 64 over an fp32 cache also has 2-wave workgroups, for splits of at most 32 rows
+// (one 16-row trip per wave; with 4 waves two of them would sit idle through the merge).
 template <int D, int G, bool Q8>
 SplitKernel kernel_dg(int waves) {
     if constexpr (((D == 256 || Q8) && G > 4) || D == 512) {
         return kernel_dgw<D, G, 4, Q8>();
     } else {
+        if constexpr (D == 64 && !Q8) {
+            if (waves == 2) return kernel_dgw<D, G, 2, Q8>();
+        }
         return waves == 8 ? kernel_dgw<D, G, 8, Q8>() : kernel_dgw<D, G, 4, Q8>();
     }
 }
@@ -110,7 +115,7 @@ SplitKernel kernel_split(int head_dim, int group, int waves) {
 }
 
 SplitKernel resolve_split(int head_dim, int group, int waves, bool q8) {
-    if (waves != 4 && waves != 8) return SplitKernel{nullptr, 0};
+    if (waves != 2 && waves != 4 && waves != 8) return SplitKernel{nullptr, 0};
     return q8 ? kernel_split<true>(head_dim, group, waves)
               : kernel_split<false>(head_dim, group, waves);
 }

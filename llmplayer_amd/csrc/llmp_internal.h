@@ -60,7 +60,7 @@ struct DecodeArgs {
 };
 
 // Launches the split-K kernel for head_dim D and GQA group G = Hq/Hkv on grid
-// (splits, Hkv) with `waves` (4 or 8) waves per workgroup requested, over an fp32
+// (splits, Hkv) with `waves` (2, 4 or 8) waves per workgroup requested, over an fp32
 // (q8 = false) or Q8_0 (q8 = true) cache.  Returns hipErrorInvalidValue for an unsupported
 // shape.  With splits > 1, launch_decode_reduce must follow.
 hipError_t launch_decode_split(const DecodeArgs& a, int head_dim, int group, int n_kv_heads,

@@ -248,7 +248,9 @@ void auto_launch(int n, int n_kv_heads, int n_cu, int head_dim, int group, bool 
     const int per_cu = q8 ? decode_split_blocks_per_cu(head_dim, group, 4, true) : 1;
     bool wide = false;
     *splits = default_splits(n, n_kv_heads, n_cu, per_cu, q8, &wide);
-    *waves = decode_split_waves(head_dim, group, wide ? 8 : 4, q8);
+    // head_dim 64 splits of at most 32 rows: 2-wave workgroups (one 16-row trip per wave)
+    const bool small = !q8 && !wide && head_dim == 64 && (n + *splits - 1) / *splits <= 32;
+    *waves = decode_split_waves(head_dim, group, wide ? 8 : (small ? 2 : 4), q8);
 }
 
 struct Plan {
