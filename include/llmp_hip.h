@@ -93,10 +93,20 @@ int llmp_event_elapsed_ms(float *ms, uint64_t start, uint64_t end);
 /* One zero-filled device pool for n_layers x {K,V}, laid out head-major.  LLMP_KV_F32:
  * [layer][K|V][kv_head][pos][head_dim] fp32.  LLMP_KV_Q8_0(_TRUNC): per layer the K quants
  * [kv_head][pos][head_dim] int8, K scales [kv_head][pos][head_dim/32] fp32, then the same for
- * V.  Fails with LLMP_ERR_OUT_OF_MEMORY when the pool would not fit in free HBM.  head_dim must
- * be 64, 128 or 256 (any cache type, GQA groups 1-8), 96 (fp32 caches, groups 1-4: Phi-3), 80
- * (fp32 caches, groups 1-2, decode only: Phi-2) or 512 (fp32 caches and decode only, the
- * full-attention layers of Gemma 4, whose two head sizes take one handle each). */
+ * V.  The pool also holds each layer's range exponents (below).  Fails with
+ * LLMP_ERR_OUT_OF_MEMORY when the pool would not fit in free HBM.  head_dim must be 64, 128 or
+ * 256 (any cache type), 96 (fp32 caches: Phi-3), 80 (fp32 caches, decode only: Phi-2) or 512
+ * (fp32 caches and decode only, the full-attention layers of Gemma 4, whose two head sizes take
+ * one handle each).  Kernels are instantiated for GQA groups 1-8 (1-4 at head_dim 96, 1-2 at 80);
+ * a larger group (GLM-4's 16 or 24 query heads per KV head) runs as several groups of its
+ * largest instantiated divisor per KV head, so every group is accepted.
+ *
+ * Range exponents: per layer and KV head, E = max(0, floor(log2 max|x|) - 14) over every K (and
+ * V) value stored since the pool was created or cleared, raised by each append and by
+ * llmp_kv_write(_q8).  The multi-token calls split rows into fp16 hi/lo parts, which hold
+ * magnitudes below 65504, and scale them by 2^-E first.  Values written through the addresses of
+ * llmp_kv_layer_ptrs are not tracked: keep them below 2^15 in magnitude, or write them with
+ * llmp_kv_write. */
 int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int dtype,
                    uint64_t *handle);
 int llmp_kv_destroy(uint64_t handle);
@@ -117,10 +127,11 @@ int llmp_kv_read_q8(uint64_t handle, int layer, int pos0, int n, int8_t *k_quant
 int llmp_kv_write_q8(uint64_t handle, int layer, int pos0, int n, const int8_t *k_quants,
                      const float *k_scales, const int8_t *v_quants, const float *v_scales);
 /* Device addresses of one layer's K and V planes ([kv_head][pos][head_dim] fp32, or the quant
- * planes of a Q8_0 cache). */
+ * planes of a Q8_0 cache).  Rows written through them do not raise the range exponents (see
+ * llmp_kv_create). */
 int llmp_kv_layer_ptrs(uint64_t handle, int layer, uint64_t *k_plane, uint64_t *v_plane);
-/* Zero the whole pool (a new conversation; hipMemsetAsync: not for use inside a graph
- * capture). */
+/* Zero the whole pool and its range exponents (a new conversation; hipMemsetAsync: not for use
+ * inside a graph capture). */
 int llmp_kv_clear(uint64_t handle, uint64_t stream);
 
 /* ---- RoPE tables (RoPE.java:45-106; upload as CudaForwardPass.java:398-402) ------------ */
@@ -290,8 +301,12 @@ int llmp_attn_prefill_shared(uint64_t handle, int layer, int src_layer, int pos0
  *   q:   device fp32 [n_tokens][n_heads*head_dim]   (4-byte aligned)
  *   k,v: device fp32 [n_tokens][n_kv_heads*head_dim]
  * The appended rows are bit-identical to n_tokens llmp_attn_decode calls on the same fp32
- * inputs; attention runs on the same fp16 hi/lo MFMA path (K, V and P each split, so fp32
- * rows keep ~2^-16 relative precision per product).  gate may be 0. */
+ * inputs; attention runs on the same fp16 hi/lo MFMA path (K, Q, V and P each split into two
+ * fp16 parts, ~2^-22 of each operand's magnitude).  Range: any finite input.  K and V rows are
+ * scaled by their layer's range exponents (llmp_kv_create) and the queries of each 16-token block
+ * by the exponent of their largest magnitude before the split, so values beyond fp16's 65504
+ * keep that precision; scores of ~1e3 and more are then resolved to ~2^-21 of their magnitude
+ * (fp32: 2^-24).  gate may be 0.  The bf16 entry points take the same path. */
 int llmp_attn_prefill_f32(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t q,
                           uint64_t k, uint64_t v, uint64_t gate, uint64_t out, uint64_t stream);
 /* No counterpart in the reference.  For callers that cannot allocate device memory: code under
@@ -375,10 +390,12 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
  * (LLMEngine.java:1019-1033), batched as docs/optimization/speculative-decoding.md:120-140
  * plans for the verification of K draft tokens.  The projections run on the matrix cores with
  * each fp32 input split into two fp16 parts (fp32-accurate products, fp32 sums in another order
- * than the CPU path; inputs below 65504); the attention is llmp_attn_prefill_f32's (the appended
- * rows bit-identical to single-token appends of the same projections).  In the
- * LLMP_INPUT_Q8_1 mode (and at head_dim 80, which has no prefill kernel) the tokens run one
- * llmp_attn_block call each.  The call may grow the
+ * than the CPU path); any finite residual is taken: the inputs of a group are scaled by a power
+ * of two that brings the largest below 2^15 (a small first kernel computes it with each token's
+ * RMSNorm factor), the outputs by its inverse.  The attention is llmp_attn_prefill_f32's (the
+ * appended rows bit-identical to single-token appends of the same projections).  In the
+ * LLMP_INPUT_Q8_1 mode, at head_dim 80 (no prefill kernel) and for layers whose fp32 or bf16
+ * weights reach 65504, the tokens run one llmp_attn_block call each.  The call may grow the
  * handle's prefill workspace, as llmp_attn_prefill_f32 does (not for use under graph capture
  * then). */
 int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t x,

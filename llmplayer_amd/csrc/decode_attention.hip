@@ -1,7 +1,8 @@
 // Instantiation and dispatch of the decode kernels (decode_kernels.h) for the shapes the
 // library ships: head_dim 64/128/256 (fp32 and Q8_0 caches) with GQA groups 1-8, 512 (fp32: the
 // full-attention layers of Gemma 4) with groups 1-8, 96 (fp32: Phi-3) with groups 1-4 and 80
-// (fp32: Phi-2) with groups 1-2.
+// (fp32: Phi-2) with groups 1-2.  Larger groups (GLM-4's 16 and 24) run as several groups of
+// one of these sizes per cached KV head (kernel_group, DecodeArgs::kv_rep).
 #include "decode_kernels.h"
 
 namespace llmp {
@@ -128,12 +129,7 @@ __global__ void copy_kernel(float4* __restrict__ dst, const float4* __restrict__
 
 }  // namespace
 
-bool decode_shape_supported(int head_dim, int group) {
-    if (head_dim == 80) return group >= 1 && group <= 2;
-    if (head_dim == 96) return group >= 1 && group <= 4;
-    const bool d_ok = head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512;
-    return d_ok && group >= 1 && group <= 8;
-}
+bool decode_shape_supported(int head_dim, int group) { return decode_group_ok(head_dim, group); }
 
 int decode_split_waves(int head_dim, int group, int waves, bool q8) {
     return resolve_split(head_dim, group, waves, q8).waves;

@@ -92,6 +92,24 @@ __device__ __forceinline__ float row_group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Range exponents of the stored rows.  The multi-token kernels split cache rows into fp16
+// hi/lo parts, which hold magnitudes below 65504; rows with larger values are scaled by 2^-E
+// first.  E(x) = max(0, floor(log2|x|) - 14), from the biased exponent: 0 for |x| < 2^15, and
+// |x| * 2^-E(x) < 2^15 for every finite x.  Every writer of cache rows raises the exponents
+// of the KV head it stores to (range[2*kvh] for K, range[2*kvh + 1] for V), so they bound
+// every row of the layer until the cache is cleared.  The atomics only run when a row holds
+// such a value.
+__device__ __forceinline__ unsigned abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+__device__ __forceinline__ int range_exp_of_bits(unsigned ab) {
+    const int e = (int)(ab >> 23) - 141;
+    return e > 0 ? e : 0;
+}
+__device__ __forceinline__ void note_range(int* range, int kvh, unsigned kbits, unsigned vbits) {
+    const int ek = range_exp_of_bits(kbits), ev = range_exp_of_bits(vbits);
+    if (ek > 0) atomicMax(range + 2 * kvh, ek);
+    if (ev > 0) atomicMax(range + 2 * kvh + 1, ev);
+}
+
 
 // Final normalisation of one output element of query head hq from its merged (max M,
 // sum L, unnormalised O) in the log2 domain: an attention sink (log2-domain logit) joins the
@@ -374,7 +392,8 @@ __device__ __forceinline__ void load_args_now(const DecodeArgs& a) {
     asm volatile("" ::"s"(a.pos), "s"(a.max_seq), "s"(a.window), "s"(a.splits), "s"(a.half_rope),
                  "s"(a.rope_type), "s"(a.q8_trunc), "s"(a.norm_seq), "s"(a.v_norm),
                  "s"(a.no_append), "s"(a.eps), "s"(a.qk_scale));
-    asm volatile("" ::"s"(a.softcap), "s"(a.softcap_log2e), "s"(a.inv_softcap));
+    asm volatile("" ::"s"(a.softcap), "s"(a.softcap_log2e), "s"(a.inv_softcap), "s"(a.range),
+                 "s"(a.kv_rep));
 }
 
 // 1/rms of D values in the order of RMSNorm.apply with offsets (RMSNorm.java:24-35, the
@@ -588,20 +607,27 @@ __device__ void stage_new_row(const DecodeArgs& a, int kvh, float* sk, float* sv
 
 // Q8_0 append of the staged row pos (KVCache.storeK/storeV in Q8_0 mode): quantised into LDS
 // (kq/ks, vq/vs) and written to the cache.
+// store: false for the workgroups of a KV head's further virtual heads (DecodeArgs::kv_rep),
+// which quantise the row for their own use and leave the cache write to the first one.
 template <int D, int NTHR>
 __device__ void append_row_q8(const DecodeArgs& a, int kvh, int pos, const float* sk,
                               const float* sv, signed char* kq, float* ks, signed char* vq,
-                              float* vs, float* s_inv, int tid) {
+                              float* vs, float* s_inv, int tid, bool store) {
     quantize_row_lds<D, NTHR>(sk, kq, ks, s_inv, tid, a.q8_trunc != 0);
     quantize_row_lds<D, NTHR>(sv, vq, vs, s_inv, tid, a.q8_trunc != 0);
+    if (!store) return;
     signed char* kqp = a.kq + (long long)kvh * a.head_stride + (long long)pos * D;
     signed char* vqp = a.vq + (long long)kvh * a.head_stride + (long long)pos * D;
     float* ksp = a.ks + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
     float* vsp = a.vs + (long long)kvh * (a.head_stride / 32) + (long long)pos * (D / 32);
+    unsigned kb = 0, vb = 0;   // the dequantised values stay within the fp32 rows' range
     for (int i = tid; i < D; i += NTHR) {
         kqp[i] = kq[i];
         vqp[i] = vq[i];
+        kb = max(kb, abs_bits(sk[i]));
+        vb = max(vb, abs_bits(sv[i]));
     }
+    note_range(a.range, kvh, kb, vb);
     for (int b = tid; b < D / 32; b += NTHR) {
         ksp[b] = ks[b];
         vsp[b] = vs[b];
@@ -704,8 +730,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
 
     const int tid = threadIdx.x;
     const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int h0 = kvh * G;
+    // Grid y runs over virtual KV heads: kv_rep of them share each cached KV head (groups of
+    // more than 8 query heads run as kv_rep groups of G), so the query heads, the partials and
+    // the grid use vkh, the cache uses kvh, and the first virtual head alone appends.
+    const int vkh = blockIdx.y;
+    const int kvh = vkh / a.kv_rep;
+    const bool store = vkh == kvh * a.kv_rep;
+    const int h0 = vkh * G;
     // Step plan from the position (host value or device word).  A device position outside
     // the cache leaves everything untouched; splits beyond the rows of this step exit.
     load_args_now(a);
@@ -820,14 +851,22 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
             }
             // KVCache.storeK/storeV: the exact fp32 rows, or their Q8_0 quantisation.
             if constexpr (!Q8) {
+              if (store) {
                 float* kplane = a.kc + (long long)kvh * a.head_stride + (long long)pos * D;
                 float* vplane = a.vc + (long long)kvh * a.head_stride + (long long)pos * D;
+                unsigned kb = 0, vb = 0;
                 for (int i = tid; i < D; i += NTHR) {
-                    kplane[i] = s_x[G * D + i];
-                    vplane[i] = s_v[i];
+                    const float kx = s_x[G * D + i], vx = s_v[i];
+                    kplane[i] = kx;
+                    vplane[i] = vx;
+                    kb = max(kb, abs_bits(kx));
+                    vb = max(vb, abs_bits(vx));
                 }
+                note_range(a.range, kvh, kb, vb);
+              }
             } else {
-                append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid);
+                append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid,
+                                       store);
             }
         }
         if (!reg_prologue) {
@@ -940,7 +979,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
                 a.out[(h0 + h) * D + d] =
                     finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
             } else {
-                const long long slot = ((long long)kvh * sp.splits + split) * G + h;
+                const long long slot = ((long long)vkh * sp.splits + split) * G + h;
                 a.part_o[slot * D + d] = O;
                 if (d == 0) {
                     a.part_ml[2 * slot] = M;
@@ -1004,7 +1043,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
                 a.out[(h0 + h) * D + d] =
                     finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
             } else {
-                const long long slot = ((long long)kvh * sp.splits + split) * G + h;
+                const long long slot = ((long long)vkh * sp.splits + split) * G + h;
                 a.part_o[slot * D + d] = O;
                 if (d == 0) {
                     a.part_ml[2 * slot] = M;
@@ -1169,8 +1208,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
 
     const int tid = threadIdx.x;
     const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int h0 = kvh * G;
+    const int vkh = blockIdx.y;          // virtual KV head (see decode_split_kernel)
+    const int kvh = vkh / a.kv_rep;
+    const bool store = vkh == kvh * a.kv_rep;
+    const int h0 = vkh * G;
     load_args_now(a);
     const int pos = step_position(a);
     if (pos < 0 || pos >= a.max_seq) return;
@@ -1319,7 +1360,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
         __shared__ __align__(16) signed char s_kq[D], s_vq[D];
         __shared__ float s_ks[NB], s_vs[NB], s_inv[NB];
         stage_new_row<D, NTHR>(a, kvh, s_x + G * D, s_v, s_acc, s_r, &s_vr, hp, tid);
-        append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid);
+        append_row_q8<D, NTHR>(a, kvh, pos, s_x + G * D, s_v, s_kq, s_ks, s_vq, s_vs, s_inv, tid, store);
         if (wave == 0) {
             T t;
             const bool k0 = (lane & 15) == 0;
@@ -1383,7 +1424,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
             a.out[(h0 + h) * D + d] =
                 finish_output(Mx, Ls, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
         } else {
-            const long long slot = ((long long)kvh * sp.splits + split) * G + h;
+            const long long slot = ((long long)vkh * sp.splits + split) * G + h;
             a.part_o[slot * D + d] = O;
             if (d == 0) {
                 a.part_ml[2 * slot] = Mx;

@@ -43,6 +43,24 @@ LLMP_HD inline StepPlan plan_step(int pos, int window, int max_splits) {
     return p;
 }
 
+// Head shapes the decode kernels are instantiated for: head_dim 64/128/256/512 with GQA groups
+// 1-8, 96 with 1-4 (Phi-3) and 80 with 1-2 (Phi-2).
+inline bool decode_group_ok(int head_dim, int group) {
+    const int limit = (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512)
+                          ? 8
+                          : (head_dim == 96 ? 4 : (head_dim == 80 ? 2 : 0));
+    return group >= 1 && group <= limit;
+}
+// The group the kernels run a layer with: `group` itself when instantiated, else its largest
+// divisor that is (a layer of G query heads per KV head then runs as G / divisor virtual KV heads
+// per cached KV head, each with `divisor` query heads); 0 when no divisor is.
+inline int kernel_group(int head_dim, int group) {
+    if (group < 1) return 0;
+    for (int g = group < 8 ? group : 8; g >= 1; --g)
+        if (group % g == 0 && decode_group_ok(head_dim, g)) return g;
+    return 0;
+}
+
 // Default split count of a decode step over n attended rows, given the CUs and the workgroups
 // of the chosen kernel resident per CU (per_cu; 1 for fp32 caches, which aim at one workgroup
 // per CU):
@@ -97,6 +115,40 @@ inline size_t ggml_row_bytes(int type, int cols) {
 }
 
 inline size_t pad256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Range exponent of a stored value, as the kernels' dk::range_exp_of_bits computes it:
+// max(0, floor(log2|x|) - 14), 0 for |x| < 2^15, so that |x| * 2^-E < 2^15 (the fp16 hi/lo
+// split of the multi-token kernels needs magnitudes below 65504).
+inline int range_exp(float x) {
+    uint32_t b;
+    std::memcpy(&b, &x, sizeof b);
+    const int e = (int)((b & 0x7FFFFFFFu) >> 23) - 141;
+    return e > 0 ? e : 0;
+}
+// Raises ek[h] / ev[h] (h < H) to the range exponents of n rows in the reference layout
+// [t][H * row] (row values per KV head); k or v may be null.
+inline void range_exp_rows(const float* k, const float* v, size_t H, size_t n, size_t row, int* ek,
+                           int* ev) {
+    for (size_t t = 0; t < n; ++t)
+        for (size_t h = 0; h < H; ++h)
+            for (size_t j = 0; j < row; ++j) {
+                const size_t i = (t * H + h) * row + j;
+                if (k) { const int e = range_exp(k[i]); if (e > ek[h]) ek[h] = e; }
+                if (v) { const int e = range_exp(v[i]); if (e > ev[h]) ev[h] = e; }
+            }
+}
+// The same for Q8_0 rows (quants [t][H * row], scales [t][H * row / 32]), over the values the
+// kernels dequantise: (float)quant * scale.
+inline void range_exp_rows_q8(const int8_t* q, const float* s, size_t H, size_t n, size_t row,
+                              int* e_out) {
+    for (size_t t = 0; t < n; ++t)
+        for (size_t h = 0; h < H; ++h)
+            for (size_t j = 0; j < row; ++j) {
+                const size_t i = (t * H + h) * row + j;
+                const int e = range_exp((float)q[i] * s[i / 32]);
+                if (e > e_out[h]) e_out[h] = e;
+            }
+}
 
 // Repacks `rows` GGUF rows of `cols` weights (src, ggml_row_bytes(type, cols) bytes each) into
 // the planes the projection kernels read: every row's bytes of one plane are contiguous

@@ -41,6 +41,8 @@ struct DecodeArgs {
     float* part_o;         // [Hkv][splits][G][D] unnormalised split outputs
     float* part_ml;        // [Hkv][splits][G][2] split (max, sum) in the log2 domain
     const int* d_pos;      // device position (tokenParams[0]) or nullptr to use `pos`
+    int* range;            // range exponents of the layer's rows [Hkv][K, V] (raised by the append)
+    int kv_rep;            // virtual KV heads per cached KV head (grid y = n_kv_heads * kv_rep)
     long long head_stride; // floats between consecutive KV heads of a plane (max_seq*D)
     int pos;               // position of the new token (row appended) when d_pos is null
     int max_seq;           // cache rows; a device position outside [0, max_seq) is a no-op
@@ -73,7 +75,8 @@ int decode_split_blocks_per_cu(int head_dim, int group, int waves, bool q8);
 // Launches the log-sum-exp combine of the splits: one block per query head.
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,
                                 hipStream_t stream);
-// True when a decode kernel exists for (head_dim, group).
+// True when a decode kernel exists for (head_dim, group) (host_layout.h decode_group_ok; larger
+// groups run through kernel_group's divisor, DecodeArgs::kv_rep).
 bool decode_shape_supported(int head_dim, int group);
 
 namespace pk {
@@ -127,6 +130,11 @@ struct ProjTokArgs;
 // Token-batched projections on the matrix cores (proj_tok_kernels.h): the GGML types with a
 // kernel, the two-type pairs one launch takes (GemvSeg-like TokSeg::fmt 0 and 1), and the
 // launch (second_type < 0: one type); hipErrorInvalidValue for an unsupported type or shape.
+// Per-token factors of a token-batched projection (tk::tok_prep_kernel): sc[2t] = the RMSNorm
+// factor r (1 without norm_w) and sc[2t + 1] = the range exponent of the largest x*w (or x),
+// for t < n_tokens (<= kTokBatch).
+hipError_t launch_tok_prep(const float* x, long long x_pitch, int cols, const float* norm_w, float eps,
+                           float* sc, int n_tokens, hipStream_t stream);
 bool proj_tok_supported(int ggml_type);
 bool proj_tok_pair_supported(int first_type, int second_type);
 hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_type,

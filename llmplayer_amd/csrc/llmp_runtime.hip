@@ -7,6 +7,7 @@
 #include "gemv_kernels.h"
 #include "proj_tok_kernels.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -47,11 +48,17 @@ struct DevWeight {
     int rows = 0, cols = 0;
     void* mem = nullptr;
     gk::WPlanes planes{};
+    // The token-batched projections split fp32 and bf16 weights into fp16 parts: false when
+    // some weight reaches fp16's largest magnitude, 65504 (llmp_attn_block_batch then runs the
+    // tokens one by one, on the fp32 single-token kernels).
+    bool tok_ok = true;
 };
 
 struct LayerCfg {
     bool configured = false;
     int n_heads = 0;
+    int kgroup = 0;             // query heads per workgroup's KV head (kernel_group)
+    int krep = 1;               // virtual KV heads per cached KV head: n_heads / (Hkv * kgroup)
     int rope_type = 0;
     int rope_sel = LLMP_ROPE_SEL_GLOBAL;
     int window = 0;
@@ -126,9 +133,19 @@ struct KvHandle {
     float* vs(int layer) const {
         return reinterpret_cast<float*>(q8_layer(layer) + 2 * q8_quant_bytes() + q8_scale_bytes());
     }
-    size_t pool_bytes() const {
+    size_t rows_bytes() const {
         return q8() ? (size_t)n_layers * q8_layer_bytes()
                     : 2 * (size_t)n_layers * plane_floats * sizeof(float);
+    }
+    // Range exponents of the stored rows (dk::note_range), [layer][kv_head][K, V] int32, after
+    // the rows in the same allocation: zeroed with them, raised by every append and by
+    // llmp_kv_write / llmp_kv_write_q8.
+    int* range(int layer) const {
+        return reinterpret_cast<int*>(reinterpret_cast<char*>(pool) + rows_bytes()) +
+               (size_t)layer * 2 * (size_t)n_kv_heads;
+    }
+    size_t pool_bytes() const {
+        return rows_bytes() + pad256((size_t)n_layers * 2 * (size_t)n_kv_heads * sizeof(int));
     }
 };
 
@@ -270,7 +287,7 @@ int layer_window(const LayerCfg& c) { return (c.window > 0 && !c.is_global) ? c.
 Plan make_plan(const KvHandle* kv, const LayerCfg& c, int position, int splits_req) {
     const int window = layer_window(c);
     const StepPlan full = plan_step(position, window, 1);
-    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    const int D = kv->head_dim, Hkv = kv->n_kv_heads * c.krep, group = c.kgroup;
     const bool q8 = kv->q8();
     int s = splits_req, waves = 4;
     if (s <= 0)
@@ -311,9 +328,11 @@ int enqueue_decode(KvHandle* kv, int layer, int src_layer, int position, const i
     if (splits > kMaxSplits)
         return fail(LLMP_ERR_INVALID_ARG, "splits=%d above the maximum %d", splits, kMaxSplits);
 
-    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    // The grid runs over virtual KV heads: krep per cached KV head, kgroup query heads each.
+    const int D = kv->head_dim, Hkv = kv->n_kv_heads * c.krep, group = c.kgroup;
     const Plan plan = make_plan(kv, c, position, splits);
     DecodeArgs a{};
+    a.kv_rep = c.krep;
     a.q = reinterpret_cast<const float*>(q);
     a.k = reinterpret_cast<const float*>(k);
     a.v = reinterpret_cast<const float*>(v);
@@ -346,6 +365,7 @@ int enqueue_decode(KvHandle* kv, int layer, int src_layer, int position, const i
     a.part_o = kv->part_o;
     a.part_ml = kv->part_ml;
     a.d_pos = d_pos;
+    a.range = kv->range(kv_layer);
     a.head_stride = (long long)kv->max_seq * D;
     a.pos = position;
     a.max_seq = kv->max_seq;
@@ -708,6 +728,27 @@ int llmp_kv_read(uint64_t handle, int layer, int pos0, int n, float* host_k, flo
     return LLMP_OK;
 }
 
+// Raises the layer's range exponents to those of rows written from the host (ek / ev: one
+// per KV head): a read, a maximum and a write of the layer's 2 * n_kv_heads words.
+static int raise_range(KvHandle* kv, int layer, const std::vector<int>& ek, const std::vector<int>& ev) {
+    const size_t H = (size_t)kv->n_kv_heads;
+    bool any = false;
+    for (size_t h = 0; h < H; ++h) any = any || ek[h] > 0 || ev[h] > 0;
+    if (!any) return LLMP_OK;
+    std::vector<int> cur(2 * H);
+    LLMP_HIP_CHECK(hipMemcpyAsync(cur.data(), kv->range(layer), cur.size() * sizeof(int),
+                                  hipMemcpyDeviceToHost, G().stream), "hipMemcpyAsync(range)");
+    LLMP_HIP_CHECK(hipStreamSynchronize(G().stream), "hipStreamSynchronize");
+    for (size_t h = 0; h < H; ++h) {
+        cur[2 * h] = std::max(cur[2 * h], ek[h]);
+        cur[2 * h + 1] = std::max(cur[2 * h + 1], ev[h]);
+    }
+    LLMP_HIP_CHECK(hipMemcpyAsync(kv->range(layer), cur.data(), cur.size() * sizeof(int),
+                                  hipMemcpyHostToDevice, G().stream), "hipMemcpyAsync(range)");
+    LLMP_HIP_CHECK(hipStreamSynchronize(G().stream), "hipStreamSynchronize");
+    return LLMP_OK;
+}
+
 int llmp_kv_write(uint64_t handle, int layer, int pos0, int n, const float* host_k,
                   const float* host_v) {
     if (int rc = ensure_init()) return rc;
@@ -715,6 +756,12 @@ int llmp_kv_write(uint64_t handle, int layer, int pos0, int n, const float* host
     if (kv->q8()) return fail(LLMP_ERR_UNSUPPORTED, "llmp_kv_write: Q8_0 cache (use llmp_kv_write_q8)");
     if (int rc = check_rows(kv, layer, pos0, n)) return rc;
     if (n == 0) return LLMP_OK;
+    {
+        std::vector<int> ek((size_t)kv->n_kv_heads, 0), ev((size_t)kv->n_kv_heads, 0);
+        range_exp_rows(host_k, host_v, (size_t)kv->n_kv_heads, (size_t)n, (size_t)kv->head_dim,
+                       ek.data(), ev.data());
+        if (int rc = raise_range(kv, layer, ek, ev)) return rc;
+    }
     const size_t row = (size_t)kv->head_dim * sizeof(float);
     if (host_k)
         if (int rc = copy_plane(kv, kv->k_plane(layer), row, pos0, n, const_cast<float*>(host_k), false))
@@ -755,7 +802,24 @@ int llmp_kv_write_q8(uint64_t handle, int layer, int pos0, int n, const int8_t* 
     if (k_scales) if (int rc = cp(kv->ks(layer), srow, k_scales)) return rc;
     if (v_quants) if (int rc = cp(kv->vq(layer), qrow, v_quants)) return rc;
     if (v_scales) if (int rc = cp(kv->vs(layer), srow, v_scales)) return rc;
-    return LLMP_OK;
+    // Range exponents of the values the kernels now dequantise from these rows (quant * scale),
+    // read back whole so that a write of quants or scales alone is bounded too.
+    const size_t H = (size_t)kv->n_kv_heads;
+    std::vector<int> ek(H, 0), ev(H, 0);
+    std::vector<int8_t> qb((size_t)n * H * qrow);
+    std::vector<float> sb((size_t)n * H * qrow / 32);
+    for (int which = 0; which < 2; ++which) {
+        const bool k_side = which == 0;
+        if (k_side ? !(k_quants || k_scales) : !(v_quants || v_scales)) continue;
+        if (int rc = copy_plane(kv, k_side ? (void*)kv->kq(layer) : (void*)kv->vq(layer), qrow, pos0, n,
+                                qb.data(), true))
+            return rc;
+        if (int rc = copy_plane(kv, k_side ? (void*)kv->ks(layer) : (void*)kv->vs(layer), srow, pos0, n,
+                                sb.data(), true))
+            return rc;
+        range_exp_rows_q8(qb.data(), sb.data(), H, (size_t)n, qrow, k_side ? ek.data() : ev.data());
+    }
+    return raise_range(kv, layer, ek, ev);
 }
 
 int llmp_kv_layer_ptrs(uint64_t handle, int layer, uint64_t* k_plane, uint64_t* v_plane) {
@@ -905,7 +969,8 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
         return fail(LLMP_ERR_INVALID_ARG, "layer %d: n_heads=%d not a multiple of n_kv_heads=%d",
                     layer, n_heads, n_kv_heads);
     const int group = n_heads / n_kv_heads;
-    if (!decode_shape_supported(head_dim, group))
+    const int kgroup = kernel_group(head_dim, group);
+    if (kgroup == 0)
         return fail(LLMP_ERR_UNSUPPORTED, "layer %d: no decode kernel for head_dim=%d group=%d",
                     layer, head_dim, group);
     if (rope_type != LLMP_ROPE_NORMAL && rope_type != LLMP_ROPE_NEOX)
@@ -920,9 +985,23 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
     if ((qnorm_w == nullptr) != (knorm_w == nullptr))
         return fail(LLMP_ERR_INVALID_ARG, "layer %d: QK-norm needs both weights or neither", layer);
 
-    if ((size_t)kMaxSplits * (size_t)n_heads > kv->part_slots)   // guarded by group <= kMaxGroup
-        return fail(LLMP_ERR_UNSUPPORTED, "layer %d: %d query heads exceed the split workspace",
-                    layer, n_heads);
+    if ((size_t)kMaxSplits * (size_t)n_heads > kv->part_slots) {
+        // More query heads than llmp_kv_create sized the split workspace for (groups above
+        // kMaxGroup): it grows here, at set-up, so graphs captured before must be captured again.
+        const size_t slots = (size_t)kMaxSplits * (size_t)n_heads;
+        LLMP_HIP_CHECK(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        (void)hipFree(kv->part_o);
+        (void)hipFree(kv->part_ml);
+        kv->part_o = kv->part_ml = nullptr;
+        kv->part_slots = 0;
+        hipError_t ea = hipMalloc(&kv->part_o, slots * (size_t)head_dim * sizeof(float));
+        if (ea == hipSuccess) ea = hipMalloc(&kv->part_ml, slots * 2 * sizeof(float));
+        if (ea != hipSuccess)
+            return fail(ea == hipErrorOutOfMemory ? LLMP_ERR_OUT_OF_MEMORY : LLMP_ERR_HIP,
+                        "layer %d: split workspace for %d query heads: %s", layer, n_heads,
+                        hipGetErrorString(ea));
+        kv->part_slots = slots;
+    }
     LayerCfg& c = kv->layers[(size_t)layer];
     const size_t wbytes = (size_t)head_dim * sizeof(float);
     if (qnorm_w) {
@@ -940,6 +1019,8 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
         c.d_sinks = nullptr;
     }
     c.n_heads = n_heads;
+    c.kgroup = kgroup;
+    c.krep = group / kgroup;
     c.rope_type = rope_type;
     c.rope_sel = rope_sel;
     c.window = window;
@@ -1014,7 +1095,7 @@ int llmp_layer_norm_mode(uint64_t handle, int layer, int mode) {
 // Byte offsets of the token-batched block scratch: q, k, v, the attention output and the
 // output projection of kTokBatch tokens (each region 256-byte aligned).
 struct BatchLayout {
-    size_t q, k, v, attn, o, total;
+    size_t q, k, v, attn, o, sc, total;
 };
 static BatchLayout batch_layout(const KvHandle* kv, int qd, int kvd) {
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
@@ -1025,7 +1106,8 @@ static BatchLayout batch_layout(const KvHandle* kv, int qd, int kvd) {
     L.v = L.k + al((size_t)kTokBatch * kvd * sizeof(float));
     L.attn = L.v + al((size_t)kTokBatch * kvd * sizeof(float));
     L.o = L.attn + al((size_t)kTokBatch * qd * sizeof(float));
-    L.total = L.o + al((size_t)kTokBatch * dim * sizeof(float));
+    L.sc = L.o + al((size_t)kTokBatch * dim * sizeof(float));
+    L.total = L.sc + al((size_t)kTokBatch * 2 * sizeof(float));
     return L;
 }
 
@@ -1110,6 +1192,21 @@ int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int r
         return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_layer_weight: %zu bytes", packed.size());
     LLMP_HIP_CHECK(e, "hipMalloc(weight)");
     LLMP_HIP_CHECK(hipMemcpy(w.mem, packed.data(), packed.size(), hipMemcpyHostToDevice), "hipMemcpy(weight)");
+    if (!vec && (ggml_type == LLMP_GGML_F32 || ggml_type == LLMP_GGML_BF16)) {
+        const size_t n = (size_t)rows * cols;
+        for (size_t i = 0; i < n && w.tok_ok; ++i) {
+            float f;
+            if (ggml_type == LLMP_GGML_F32) {
+                std::memcpy(&f, static_cast<const char*>(data) + 4 * i, 4);
+            } else {
+                uint16_t b;
+                std::memcpy(&b, static_cast<const char*>(data) + 2 * i, 2);
+                const uint32_t u = (uint32_t)b << 16;
+                std::memcpy(&f, &u, 4);
+            }
+            if (!(std::fabs(f) < 65504.0f)) w.tok_ok = false;
+        }
+    }
     w.type = ggml_type;
     w.rows = rows;
     w.cols = cols;
@@ -1302,8 +1399,12 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
         return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: layer %d lacks projection weights", layer);
     if (!x || (x & 15)) return fail(LLMP_ERR_INVALID_ARG, "llmp_attn_block_batch: null or misaligned x");
     const int D = kv->head_dim, qd = c.n_heads * D, kvd = kv->n_kv_heads * D, dim = kv->blk_dim;
-    if (kv->blk_input == LLMP_INPUT_Q8_1 || prefill_tile_keys(D) <= 0) {
-        // the Q8_1 contract's int8 dot products, or a head size with decode kernels only
+    const bool w_ok = W[LLMP_W_O].tok_ok && (merged ? W[LLMP_W_QKV].tok_ok
+                                                     : W[LLMP_W_Q].tok_ok && W[LLMP_W_K].tok_ok &&
+                                                           W[LLMP_W_V].tok_ok);
+    if (kv->blk_input == LLMP_INPUT_Q8_1 || prefill_tile_keys(D) <= 0 || !w_ok) {
+        // the Q8_1 contract's int8 dot products, a head size with decode kernels only, or fp32 /
+        // bf16 weights beyond fp16's range
         for (int t = 0; t < n_tokens; ++t)
             if (int rc = enqueue_block(kv, layer, pos0 + t, 0, x + (uint64_t)t * dim * sizeof(float), 0,
                                        stream))
@@ -1326,6 +1427,7 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
     float* vb = reinterpret_cast<float*>(base + L.v);
     float* attn = reinterpret_cast<float*>(base + L.attn);
     float* ob = reinterpret_cast<float*>(base + L.o);
+    float* sc = reinterpret_cast<float*>(base + L.sc);
     hipStream_t st = pick_stream(stream);
     auto vecp = [&](int slot) -> const float* { return static_cast<const float*>(W[slot].mem); };
 
@@ -1363,7 +1465,10 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
     for (int t0 = 0; t0 < n_tokens; t0 += kTokBatch) {
         const int K = n_tokens - t0 < kTokBatch ? n_tokens - t0 : kTokBatch;
         float* xc = xp + (size_t)t0 * dim;
-        // 1-2. Pre-norm (folded into the projections) and the Q/K/V projections.
+        // 1-2. The tokens' pre-norm factors and input range exponents, then the Q/K/V
+        //      projections of the normalised inputs.
+        LLMP_HIP_CHECK(launch_tok_prep(xc, dim, dim, vecp(LLMP_W_ATTN_NORM), c.eps, sc, K, st),
+                       "batched block input prep launch");
         if (paired || t2 == -1) {
             tk::ProjTokArgs g{};
             for (int k = 0; k < 3; ++k) {
@@ -1377,6 +1482,7 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
             g.x = xc;
             g.x_pitch = dim;
             g.norm_w = vecp(LLMP_W_ATTN_NORM);
+            g.tok_sc = sc;
             g.eps = c.eps;
             LLMP_HIP_CHECK(launch_proj_tok(g, t1, paired ? t2 : -1, st), "batched block Q/K/V projection launch");
         } else {
@@ -1397,6 +1503,7 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
                 g.x = xc;
                 g.x_pitch = dim;
                 g.norm_w = vecp(LLMP_W_ATTN_NORM);
+                g.tok_sc = sc;
                 g.eps = c.eps;
                 LLMP_HIP_CHECK(launch_proj_tok(g, types[i], -1, st), "batched block Q/K/V projection launch");
                 i += n;
@@ -1418,6 +1525,8 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
         g.K = K;
         g.x = attn;
         g.x_pitch = qd;
+        g.in_range = kv->range(layer);   // |attention output| <= the largest stored |V|
+        g.in_range_n = kv->n_kv_heads;
         const float* post = vecp(LLMP_W_POST_ATTN_NORM);
         if (post) {
             g.seg[0].out = ob;
@@ -1565,8 +1674,9 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
         return fail(LLMP_ERR_INVALID_ARG,
                     "llmp_attn_prefill: misaligned q/k/v (%d B), gate (4 B) or out (16 B)",
                     in_f32 ? 4 : 2);
-    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.n_heads / Hkv;
+    const int D = kv->head_dim, Hkv = kv->n_kv_heads, group = c.kgroup;
     pk::PrefillArgs a{};
+    a.kv_rep = c.krep;
     a.q = reinterpret_cast<const void*>(q);
     a.k = reinterpret_cast<const void*>(k);
     a.v = reinterpret_cast<const void*>(v);
@@ -1584,6 +1694,7 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
     a.norm_seq = (c.norm_mode & LLMP_NORM_SEQUENTIAL) != 0;
     a.v_norm = (c.norm_mode & LLMP_NORM_V) != 0;
     a.head_stride = (long long)kv->max_seq * D;
+    a.range = kv->range(kv_layer);
     if (c.rope_sel != LLMP_ROPE_SEL_NONE) {
         const RopeTable& t = kv->rope[c.rope_sel];
         if (!t.d_cos)
@@ -1622,7 +1733,7 @@ static int enqueue_prefill(KvHandle* kv, int layer, int src_layer, int pos0, int
     const int kbeg_min = a.window > 0 ? std::max(0, pos0 - a.window + 1) : 0;
     const int tile0 = kbeg_min / TK, tile_last = (pos0 + n_tokens - 1) / TK;
     const int n_tiles = tile_last - tile0 + 1;
-    const int ksplit = prefill_key_splits(n_tokens, pos0, a.window, Hkv, group, D, G().n_cu);
+    const int ksplit = prefill_key_splits(n_tokens, pos0, a.window, Hkv * c.krep, group, D, G().n_cu);
     const size_t ws_bytes =
         ksplit == 1 ? (size_t)Hkv * (size_t)n_tiles * prefill_tile_bytes(D) : 0;
     const size_t part_bytes =

@@ -29,7 +29,7 @@ inline int prefill_nb(int P, int Hkv, int G, int n_cu) {
 template <int D, int G, int NB>
 hipError_t launch_attn_dgn(const pk::PrefillArgs& a, const uint4* ws, int tile0, int n_tiles,
                            int ksplit, int n_cu, hipStream_t stream) {
-    const int items = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv;
+    const int items = ((a.P + 16 * NB - 1) / (16 * NB)) * a.Hkv * a.kv_rep;
     if constexpr (D == 96) {   // fp32 caches only at head_dim 96
         if (a.kq != nullptr) return hipErrorInvalidValue;
     } else if (ksplit > 1 && a.kq != nullptr) {   // few query blocks: stage from the cache
@@ -59,7 +59,7 @@ hipError_t launch_attn_dg(const pk::PrefillArgs& a, const uint4* ws, int tile0, 
                           int n_cu, int ksplit, hipStream_t stream) {
     constexpr int NB = nb_big(G);
     if constexpr (NB > 1) {
-        if (prefill_items(a.P, a.Hkv, NB) < 2 * n_cu)
+        if (prefill_items(a.P, a.Hkv * a.kv_rep, NB) < 2 * n_cu)
             return launch_attn_dgn<D, G, NB / 2>(a, ws, tile0, n_tiles, ksplit, n_cu, stream);
     }
     return launch_attn_dgn<D, G, NB>(a, ws, tile0, n_tiles, ksplit, n_cu, stream);

@@ -62,6 +62,7 @@ struct PrefillArgs {
     signed char* vq;
     float* vs;
     long long head_stride;    // max_seq*D (elements of one KV head's rows)
+    int* range;               // range exponents of the layer's rows [Hkv][K, V] (dk::note_range)
     int q8_trunc;             // Q8_0 append: 1 = truncate (8-lane SIMD contract), 0 = round half up
     int norm_seq;             // 1: K-norm sums squares sequentially (RMSNorm.apply with offsets)
     int v_norm;               // 1: V rows RMS-normalised without weights before the append
@@ -75,6 +76,8 @@ struct PrefillArgs {
     float* part_o;            // split-K partials [ksplit][P][Hq][D] (ksplit > 1)
     float* part_ml;           // split-K (max, sum) [ksplit][P][Hq][2]
     int pos0, P, Hq, Hkv;
+    int kv_rep;               // virtual KV heads per cached KV head in the attention grid (groups of
+                              // more than 8 query heads run as kv_rep groups of Hq/(Hkv*kv_rep))
     int half_rope, rope_type;
     int window;               // > 0: attend to the last `window` rows (local layer)
     float eps;
@@ -139,6 +142,8 @@ void prefill_append_kernel(PrefillArgs a) {
             a.kc[off + i1] = k1;
             a.vc[off + i0] = v0;
             a.vc[off + i1] = v1;
+            dk::note_range(a.range, h, max(dk::abs_bits(k0), dk::abs_bits(k1)),
+                           max(dk::abs_bits(v0), dk::abs_bits(v1)));
         }
         return;
     }
@@ -172,6 +177,7 @@ void prefill_append_kernel(PrefillArgs a) {
             const long long off = (long long)h * a.head_stride + (long long)pos * D + d;
             a.kc[off] = s_k[e];
             a.vc[off] = s_v[e];
+            dk::note_range(a.range, h, dk::abs_bits(s_k[e]), dk::abs_bits(s_v[e]));
         }
         return;
     }
@@ -194,10 +200,13 @@ void prefill_append_kernel(PrefillArgs a) {
         const int e = 4 * (is_v ? w - kvd / 4 : w), h = e / D, d = e - h * D;
         const float* x = (is_v ? s_v : s_k) + e;
         const float inv = s_inv[(is_v ? nb : 0) + e / 32];
-        unsigned word = 0;
+        unsigned word = 0, xb = 0;   // the dequantised values stay within the fp32 rows' range
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) {
             word |= (unsigned)(dk::q8_code(x[j], inv, trunc) & 0xFF) << (8 * j);
+            xb = max(xb, dk::abs_bits(x[j]));
+        }
+        dk::note_range(a.range, h, is_v ? 0u : xb, is_v ? xb : 0u);
         *reinterpret_cast<unsigned*>((is_v ? a.vq : a.kq) + (long long)h * a.head_stride +
                                      (long long)pos * D + d) = word;
     }
@@ -309,6 +318,12 @@ __device__ __forceinline__ floatx4 load_chunk(const HeadRows& h, int r, int c4) 
         return reinterpret_cast<const floatx4*>(h.f + (long long)r * D)[c4];
     }
 }
+// 2^e as a float for -126 <= e <= 127, built from its exponent bits (integer operations, so a
+// uniform e stays in scalar registers): the range scale factors of dk::note_range.
+__device__ __forceinline__ float pow2i(int e) { return __uint_as_float((unsigned)(127 + e) << 23); }
+// 1 / f for f a power of two given by pow2i (exact).
+__device__ __forceinline__ float pow2_inv(float f) { return __uint_as_float(0x7F000000u - __float_as_uint(f)); }
+
 template <bool Q8>
 __device__ __forceinline__ floatx4 chunk_values(floatx4 x) {
     if constexpr (Q8) {
@@ -322,9 +337,10 @@ __device__ __forceinline__ floatx4 chunk_values(floatx4 x) {
 }
 
 // Image of keys [tau*TK, tau*TK + TK) of KV head blockIdx.y, tau = tile0 + blockIdx.x, at
-// ws[(kvh * n_tiles + blockIdx.x) * tile_img_u4<D>()], from fp32 or (Q8) dequantised Q8_0 rows.
-// Rows at or past row_end (never attended) repeat row row_end - 1 so that every staged value
-// is finite.
+// ws[(kvh * n_tiles + blockIdx.x) * tile_img_u4<D>()], from fp32 or (Q8) dequantised Q8_0 rows,
+// scaled by 2^-E of the head's range exponents (E = 0, no scaling, unless some stored value
+// reached 2^15) so that every split part is finite.  Rows at or past row_end (never attended)
+// repeat row row_end - 1 so that every staged value is finite.
 template <int D, int NTHR, bool Q8>
 __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4* ws, int tile0,
                                                             int n_tiles, int row_end) {
@@ -336,6 +352,7 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     const int tid = threadIdx.x, kvh = blockIdx.y;
     const int r0 = (tile0 + (int)blockIdx.x) * TK;
     const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);
+    const float fk = pow2i(-a.range[2 * kvh]), fv = pow2i(-a.range[2 * kvh + 1]);
     // K rows: work item (row r, dims 4*c4 .. 4*c4+3), c4 fastest across lanes, so the loads
     // are row-contiguous and the 8-byte stores of 16 lanes cover the 32 banks once.
     // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), rq fastest across lanes: each
@@ -364,7 +381,7 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     for (int i = 0; i < KI; ++i) {
         const int e = tid + i * NTHR;
         const int r = e / (D / 4), c4 = e - r * (D / 4);
-        const floatx4 x = chunk_values<Q8>(kx[i]);
+        const floatx4 x = chunk_values<Q8>(kx[i]) * fk;
         unsigned h0, l0, h1, l1;
         split_pair(x[0], x[1], h0, l0);
         split_pair(x[2], x[3], h1, l1);
@@ -376,8 +393,8 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     for (int i = 0; i < VI; ++i) {
         const int e = tid + i * NTHR;
         const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
-        const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]), chunk_values<Q8>(vx[i][1]),
-                               chunk_values<Q8>(vx[i][2]), chunk_values<Q8>(vx[i][3])};   // [key][dim]
+        const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]) * fv, chunk_values<Q8>(vx[i][1]) * fv,
+                               chunk_values<Q8>(vx[i][2]) * fv, chunk_values<Q8>(vx[i][3]) * fv};   // [key][dim]
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             unsigned h0, l0, h1, l1;
@@ -395,15 +412,25 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
 }
 
 // ---- 3. Double-buffered MFMA attention ------------------------------------------------------
+// Largest value of an int over the wave (prologue use only: lane exchanges through LDS).
+__device__ __forceinline__ int wave_max_int(int x) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) x = max(x, __shfl_xor(x, off));
+    return __builtin_amdgcn_readfirstlane(x);
+}
+
 // Query fragment of one lane for MFMA B operands: dims 32*s + 8*grp + j of query token qi
 // (clamped into range), head hq, as fp32 (or widened from bf16), QK-normed, rotated, scaled,
 // then split.  NEOX partners (d, d + half) usually sit in other lanes, so each element reads
 // its partner from the input and normalises it exactly as the partner's own lane does; any
-// rotated width (partial RoPE) works the same way.
+// rotated width (partial RoPE) works the same way.  The scaled queries of the wave are divided
+// by 2^eq before their split, eq the range exponent of the largest magnitude among them (0
+// below 2^15; wave-uniform, so the factor that restores the scores stays in scalar registers);
+// the scores are multiplied back.
 template <int D>
 __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int hq, int qpos,
                                                int grp, f16x8 (&qh)[D / 32],
-                                               f16x8 (&ql)[D / 32]) {
+                                               f16x8 (&ql)[D / 32], int& eq) {
     constexpr int KS = D / 32;
     float qf[KS][8];
     const long long q0 = (long long)qi * a.Hq * D + (long long)hq * D;
@@ -500,12 +527,22 @@ __device__ __forceinline__ void query_fragment(const PrefillArgs& a, int qi, int
                 }
         }
     }
+    float qmax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            qf[s][j] = qf[s][j] * a.qk_scale;
+            qmax = fmaxf(qmax, fabsf(qf[s][j]));
+        }
+    eq = wave_max_int(dk::range_exp_of_bits(dk::abs_bits(qmax)));
+    const float fq = pow2i(-eq);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         unsigned hh[4], ll[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            split_pair(qf[s][2 * j] * a.qk_scale, qf[s][2 * j + 1] * a.qk_scale, hh[j], ll[j]);
+            split_pair(qf[s][2 * j] * fq, qf[s][2 * j + 1] * fq, hh[j], ll[j]);
         qh[s] = __builtin_bit_cast(f16x8, make_uint4(hh[0], hh[1], hh[2], hh[3]));
         ql[s] = __builtin_bit_cast(f16x8, make_uint4(ll[0], ll[1], ll[2], ll[3]));
     }
@@ -573,9 +610,11 @@ __device__ __forceinline__ void raw_load(floatx4 (&kx)[KI], floatx4 (&vx)[VI][4]
     }
 }
 
+// The rows are scaled by fk (K) and fv (V), the head's 2^-E range factors (1 unless a stored
+// value reached 2^15), before the split.
 template <int D, int NTHR, int KI, int VI, bool Q8, int TK = direct_tile_keys<D>()>
 __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4 (&vx)[VI][4],
-                                          TileLds<D, TK>& t, int tid) {
+                                          TileLds<D, TK>& t, int tid, float fk, float fv) {
     using R = RawTile<D, NTHR, TK>;
     static_assert(KI == R::KI && VI == R::VI, "staging register counts");
     using T = TileLds<D, TK>;
@@ -584,7 +623,7 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
         const int e = tid + i * NTHR;
         if (i + 1 < R::KI || e < R::NK) {
             const int r = e / (D / 4), c4 = e - r * (D / 4);
-            const floatx4 x = chunk_values<Q8>(kx[i]);
+            const floatx4 x = chunk_values<Q8>(kx[i]) * fk;
             unsigned h0, l0, h1, l1;
             split_pair(x[0], x[1], h0, l0);
             split_pair(x[2], x[3], h1, l1);
@@ -597,8 +636,8 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
         const int e = tid + i * NTHR;
         if (i + 1 < R::VI || e < R::NV) {
             const int c4 = e / (TK / 4), rq = e - c4 * (TK / 4);
-            const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]), chunk_values<Q8>(vx[i][1]),
-                                   chunk_values<Q8>(vx[i][2]), chunk_values<Q8>(vx[i][3])};
+            const floatx4 vv[4] = {chunk_values<Q8>(vx[i][0]) * fv, chunk_values<Q8>(vx[i][1]) * fv,
+                                   chunk_values<Q8>(vx[i][2]) * fv, chunk_values<Q8>(vx[i][3]) * fv};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 unsigned h0, l0, h1, l1;
@@ -660,10 +699,14 @@ void prefill_attn2_kernel(PrefillArgs a,
     // of the item's key tiles (ksplit > 1 writes partials for prefill_combine_kernel).
     // With key halves a workgroup fills a CU alone: plain heaviest-first order, and the
     // dispatcher hands each freed CU the next item.
-    const int n_items = nblk * a.Hkv, L = (int)blockIdx.x, mid = (n_items + 1) / 2;
+    // Items run over virtual KV heads vkh (kv_rep per cached KV head kvh): the query heads
+    // are vkh's, the key rows and tiles kvh's.
+    const int hkv_v = a.Hkv * a.kv_rep;
+    const int n_items = nblk * hkv_v, L = (int)blockIdx.x, mid = (n_items + 1) / 2;
     const int rank = KH == 2 ? L : (L < mid ? L : n_items - 1 - (L - mid));
-    const int kvh = rank % a.Hkv;
-    const int blk = nblk - 1 - rank / a.Hkv;
+    const int vkh = rank % hkv_v;
+    const int kvh = vkh / a.kv_rep;
+    const int blk = nblk - 1 - rank / hkv_v;
     const int ks = blockIdx.y;
     const int i0 = blk * 16 * NB;
     const int sb = wave / HG, hg = wave - sb * HG;
@@ -690,9 +733,19 @@ void prefill_attn2_kernel(PrefillArgs a,
 
     const uint4* img = ws + (size_t)kvh * n_tiles * IMG;
     const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);   // DIRECT staging
+    // Range exponents of the head's rows: the tiles hold K * 2^-ek and V * 2^-ev (the images
+    // are built scaled; direct staging scales as it splits), restored on the scores and on the
+    // output.  Both are 0 unless a stored value reached 2^15.
+    const int ek = a.range[2 * kvh], ev = a.range[2 * kvh + 1];
+    const float fk = pow2i(-ek), fv = pow2i(-ev);
     using RT = RawTile<D, NTHR, T::TK>;
     u32x4 stage[DIRECT ? 1 : PER];
     floatx4 kx[RT::KI], vx[RT::VI][4];   // used by DIRECT staging only
+    // (Always multiplying measured fewer registers than a uniform branch between a scaled and
+    // an unscaled copy of the staging.)
+    auto stage_direct = [&](auto& dst) {   // generic: instantiated by DIRECT launches only
+        raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, dst, tid, fk, fv);
+    };
     floatx4 o[HPW][DT];
     float m[HPW], l[HPW];
 #pragma unroll
@@ -714,12 +767,21 @@ void prefill_attn2_kernel(PrefillArgs a,
             img_load<PER, NTHR, IMG>(stage, img + (size_t)(tb - tile0) * IMG, tid);
     }
     f16x8 qh[HPW][KS], ql[HPW][KS];
+    // Per query head of the wave: fs = 2^(ek + eq), the factor that restores the scores'
+    // scale.  The tiles' scores stay in units of fs (soft-capped ones are divided by it again)
+    // and fs is applied where the exponent's argument is formed and to the tile maximum: exact
+    // scalings by a power of two, so with ek = eq = 0 every value is bit for bit what it is
+    // without the range scaling.
+    float fs[HPW];
 #pragma unroll
-    for (int hh = 0; hh < HPW; ++hh)
-        query_fragment<D>(a, q_ok ? qi : a.P - 1, kvh * G + hg * HPW + hh, qpos, grp, qh[hh], ql[hh]);
+    for (int hh = 0; hh < HPW; ++hh) {
+        int eq;
+        query_fragment<D>(a, q_ok ? qi : a.P - 1, vkh * G + hg * HPW + hh, qpos, grp, qh[hh], ql[hh], eq);
+        fs[hh] = pow2i(min(ek + eq, 127));
+    }
     if (has_keys) {
         if constexpr (DIRECT) {
-            raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, hbuf[0], tid);
+            stage_direct(hbuf[0]);
             if (nh > 1)
                 raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (tb + 1) * TK, kend - 1, tid);
         } else {
@@ -759,12 +821,14 @@ void prefill_attn2_kernel(PrefillArgs a,
         // Soft-cap; causal/window/range mask only on tiles that cross a boundary of this wave.
         if (a.softcap > 0.0f) {
 #pragma unroll
-            for (int hh = 0; hh < HPW; ++hh)
+            for (int hh = 0; hh < HPW; ++hh) {
+                const float isc = a.inv_softcap * fs[hh], rfs = pow2_inv(fs[hh]);
 #pragma unroll
                 for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        st[hh][kt][j] = a.softcap_log2e * tanhf(st[hh][kt][j] * a.inv_softcap);
+                        st[hh][kt][j] = (a.softcap_log2e * tanhf(st[hh][kt][j] * isc)) * rfs;
+            }
         }
         const bool interior = w_full && t0 + TK - 1 <= w_lo && t0 >= w_start_max;
         if (!interior) {
@@ -788,6 +852,7 @@ void prefill_attn2_kernel(PrefillArgs a,
                 for (int j = 0; j < 4; ++j) mt = fmaxf(mt, st[hh][kt][j]);
             mt = dk::lane_step<16, true>(mt);
             mt = dk::lane_step<32, true>(mt);
+            mt = mt * fs[hh];
             // Rescaled on every tile, with no branch: alpha is exactly 1 where the running max
             // did not grow.  A branch on "some row grew" split the loop body into blocks the
             // scheduler could not interleave (C5 P = 2048: 86.2 -> 84.0 us per call; 16-token
@@ -805,7 +870,7 @@ void prefill_attn2_kernel(PrefillArgs a,
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float p = dk::fast_exp2(st[hh][kt][j] - mn);
+                    const float p = dk::fast_exp2(__builtin_fmaf(st[hh][kt][j], fs[hh], -mn));
                     l[hh] = l[hh] + p;
                     st[hh][kt][j] = p;
                 }
@@ -855,7 +920,7 @@ void prefill_attn2_kernel(PrefillArgs a,
         // buffer written here was last read before the previous iteration's barrier.
         if (it + 1 < nh) {
             if constexpr (DIRECT) {
-                raw_store<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, hbuf[(it + 1) & 1], tid);
+                stage_direct(hbuf[(it + 1) & 1]);
                 if (it + 2 < nh)
                     raw_load<D, NTHR, RT::KI, RT::VI, Q8, T::TK>(kx, vx, kr, vr, (tile + 2) * TK, kend - 1, tid);
             } else {
@@ -900,31 +965,33 @@ void prefill_attn2_kernel(PrefillArgs a,
             m[hh] = mn;
         }
     }
+    const float fvs = pow2i(ev);   // V's range factor, restored on the output (exact)
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
         float lt = dk::lane_step<16, false>(l[hh]);
         lt = dk::lane_step<32, false>(lt);
         if (q_ok && ksplit > 1) {
             // Unnormalised partial of split ks: o for this lane's dims, (max, sum) per row.
-            const int hq = kvh * G + hg * HPW + hh;
+            const int hq = vkh * G + hg * HPW + hh;
             const long long slot = ((long long)ks * a.P + qi) * a.Hq + hq;
 #pragma unroll
             for (int d = 0; d < DT; ++d)
                 *reinterpret_cast<float4*>(a.part_o + slot * D + d * 16 + 4 * grp) =
-                    make_float4(o[hh][d][0], o[hh][d][1], o[hh][d][2], o[hh][d][3]);
+                    make_float4(o[hh][d][0] * fvs, o[hh][d][1] * fvs, o[hh][d][2] * fvs,
+                                o[hh][d][3] * fvs);
             if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + 2 * slot) = make_float2(m[hh], lt);
         } else if (q_ok) {
-            const int hq = kvh * G + hg * HPW + hh;
+            const int hq = vkh * G + hg * HPW + hh;
             const long long row = (long long)qi * a.Hq * D + (long long)hq * D;
             float* op = a.out + row;
 #pragma unroll
             for (int d = 0; d < DT; ++d) {
                 const int d0 = d * 16 + 4 * grp;
                 float4 r;
-                r.x = dk::finish_output(m[hh], lt, o[hh][d][0], a.sinks, a.gate, hq, row + d0);
-                r.y = dk::finish_output(m[hh], lt, o[hh][d][1], a.sinks, a.gate, hq, row + d0 + 1);
-                r.z = dk::finish_output(m[hh], lt, o[hh][d][2], a.sinks, a.gate, hq, row + d0 + 2);
-                r.w = dk::finish_output(m[hh], lt, o[hh][d][3], a.sinks, a.gate, hq, row + d0 + 3);
+                r.x = dk::finish_output(m[hh], lt, o[hh][d][0], a.sinks, a.gate, hq, row + d0) * fvs;
+                r.y = dk::finish_output(m[hh], lt, o[hh][d][1], a.sinks, a.gate, hq, row + d0 + 1) * fvs;
+                r.z = dk::finish_output(m[hh], lt, o[hh][d][2], a.sinks, a.gate, hq, row + d0 + 2) * fvs;
+                r.w = dk::finish_output(m[hh], lt, o[hh][d][3], a.sinks, a.gate, hq, row + d0 + 3) * fvs;
                 reinterpret_cast<float4*>(op + d0)[0] = r;
             }
         }

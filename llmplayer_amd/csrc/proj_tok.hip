@@ -20,6 +20,15 @@ hipError_t launch_ff(const tk::ProjTokArgs& a, hipStream_t st) {
 
 }  // namespace
 
+hipError_t launch_tok_prep(const float* x, long long x_pitch, int cols, const float* norm_w, float eps,
+                           float* sc, int n_tokens, hipStream_t st) {
+    if (x == nullptr || sc == nullptr || cols <= 0 || n_tokens < 1 || n_tokens > tk::kTok)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(tk::tok_prep_kernel<tk::kPrepThreads>, dim3(n_tokens), dim3(tk::kPrepThreads), 0, st, x, x_pitch,
+                       cols, norm_w, eps, sc);
+    return hipGetLastError();
+}
+
 bool proj_tok_supported(int ggml_type) {
     switch (ggml_type) {
     case gk::kF32: case gk::kF16: case gk::kBF16: case gk::kQ8_0: case gk::kQ4_0: case gk::kQ4_K:
@@ -35,7 +44,7 @@ bool proj_tok_pair_supported(int first_type, int second_type) {
 }
 
 hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_type, hipStream_t st) {
-    if (a.cols <= 0 || a.cols % 32 || a.rows_total <= 0 || a.rows_total % 16 || a.K < 1 ||
+    if ((a.norm_w != nullptr && a.tok_sc == nullptr) || a.cols <= 0 || a.cols % 32 || a.rows_total <= 0 || a.rows_total % 16 || a.K < 1 ||
         a.K > tk::kTok || a.nseg < 1 || a.nseg > 3 || a.x == nullptr || (a.x_pitch & 3) ||
         (reinterpret_cast<uintptr_t>(a.x) & 15) || (reinterpret_cast<uintptr_t>(a.norm_w) & 15) ||
         a.cols > gk::kMaxGemvCols)

@@ -15,13 +15,18 @@
 //    BF16 weights are exact within fp16's normal range; F32 weights are two fp16 parts.
 //  - B (inputs): each fp32 input is split into two fp16 parts x = hi + lo, which holds x to
 //    ~2^-22 of its magnitude, so every product is fp32-accurate and the result matches the CPU
-//    path to the tolerance of a reordered fp32 sum.  Inputs must stay below 65504 (fp16's
-//    range; activations do).
+//    path to the tolerance of a reordered fp32 sum.  fp16 holds magnitudes below 65504, so the
+//    launch scales its inputs by 2^-E, E the range exponent of the largest input of its tokens
+//    (0 for inputs below 2^15), and its outputs by 2^E (exact scalings; E is uniform, so the
+//    factor stays in scalar registers, and with a norm it rides on the staged norm weights).
 //
-// The pre-attention RMSNorm is folded in: the kernel reads the raw fp32 inputs, multiplies them
-// by the norm weights, and accumulates each token's sum of squares from the same loads; the
-// token's factor r = 1/sqrt(sum/cols + eps) scales its outputs after the reduction
-// (W (r x*w) = r (W x*w), one rounding apart from the CPU path's (x*r)*w).
+// The pre-attention RMSNorm is folded in: a small first kernel (tok_prep_kernel) computes each
+// token's factor r = 1/sqrt(sum(x^2)/cols + eps) and the range exponent of its largest x*w; the
+// projection multiplies the raw inputs by the norm weights and its outputs by r after the
+// reduction (W (r x*w) = r (W x*w), one rounding apart from the CPU path's (x*r)*w).  Without
+// a norm the exponent comes from the same kernel (the raw residual of a layer with no pre-norm)
+// or from the layer's V range exponents (the output projection's input, the attention output,
+// is a convex combination of V rows).
 //
 // A workgroup owns 16 rows and all tokens; its 8 waves take 128-column chunks in turn and keep
 // the next chunk's weight and input loads in flight while they compute the current one; their
@@ -75,6 +80,13 @@ struct ProjTokArgs {
     const float* x;        // inputs [K][x_pitch] fp32 (16-byte aligned rows)
     long long x_pitch;
     const float* norm_w;   // pre-norm weights [cols] (RMSNorm of each input row), or nullptr
+    // Per token t (tok_prep_kernel): tok_sc[2t] = r, the RMSNorm factor applied to the outputs
+    // (with norm_w), and tok_sc[2t + 1] = e_t, the range exponent of its largest input (an
+    // integer in a float); E = max e_t.  When null, E is the largest V range exponent of
+    // in_range ([in_range_n][K, V] ints), or 0 when in_range is null too.
+    const float* tok_sc;
+    const int* in_range;
+    int in_range_n;
     float eps;
     float* resid;          // Wo epilogue: resid[t*resid_pitch + row] += rscale? * value
     long long resid_pitch;
@@ -337,6 +349,62 @@ struct PF32 {
     }
 };
 
+// ---- input range and pre-norm factors -------------------------------------------------------
+// The launch's input range exponent E (ProjTokArgs::tok_sc), uniform over the workgroup.
+__device__ __forceinline__ int input_exp(const ProjTokArgs& a) {
+    int e = 0;
+    if (a.tok_sc != nullptr) {
+        for (int t = 0; t < a.K; ++t) e = max(e, (int)a.tok_sc[2 * t + 1]);
+    } else if (a.in_range != nullptr) {
+        for (int h = 0; h < a.in_range_n; ++h) e = max(e, a.in_range[2 * h + 1]);
+    }
+    return __builtin_amdgcn_readfirstlane(e);
+}
+
+// One workgroup per token t: with norm weights w, r = 1/sqrt(sum(x^2)/cols + eps) (the factor
+// of RMSNorm.apply, RMSNorm.java:13-22) and e the range exponent (dk::range_exp_of_bits) of
+// max |x*w| (the values the projection splits); without, r = 1 and e from max |x|.  Writes
+// sc[2t] = r and sc[2t + 1] = e.
+constexpr int kPrepThreads = 256;
+template <int NTHR>
+__global__ __launch_bounds__(NTHR) void tok_prep_kernel(const float* x, long long x_pitch, int cols,
+                                                        const float* w, float eps, float* sc) {
+    constexpr int kPrepThreads = NTHR;
+    __shared__ float red[kPrepThreads / 64];
+    __shared__ unsigned redm[kPrepThreads / 64];
+    const int tid = threadIdx.x, t = blockIdx.x;
+    const float* xt = x + (long long)t * x_pitch;
+    float r = 1.0f;
+    if (w != nullptr) {
+        float ss = 0.0f;
+        for (int i = tid; i < cols; i += kPrepThreads) ss = __builtin_fmaf(xt[i], xt[i], ss);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss = ss + __shfl_xor(ss, off);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        float tot = red[0];
+#pragma unroll
+        for (int k = 1; k < kPrepThreads / 64; ++k) tot = tot + red[k];
+        float q = tot / (float)cols;
+        q = q + eps;
+        r = 1.0f / (float)__builtin_sqrt((double)q);
+    }
+    unsigned mb = 0;
+    for (int i = tid; i < cols; i += kPrepThreads)
+        mb = max(mb, dk::abs_bits(w != nullptr ? xt[i] * w[i] : xt[i]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mb = max(mb, (unsigned)__shfl_xor((int)mb, off));
+    if ((tid & 63) == 0) redm[tid >> 6] = mb;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned m = redm[0];
+#pragma unroll
+        for (int k = 1; k < kPrepThreads / 64; ++k) m = max(m, redm[k]);
+        sc[2 * t] = r;
+        sc[2 * t + 1] = (float)dk::range_exp_of_bits(m);
+    }
+}
+
 // ---- the projection kernel ------------------------------------------------------------------
 __device__ __forceinline__ const TokSeg& tok_seg(const ProjTokArgs& a, int row_g) {
     const bool in1 = a.nseg > 1 && row_g >= a.seg[1].out_off;
@@ -371,7 +439,7 @@ __device__ __forceinline__ void chunk_issue(ChunkRegs<F>& c, const ProjTokArgs& 
 }
 
 template <class F, bool NORM>
-__device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& acc, float& ss, float* tab,
+__device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& acc, float fin, float* tab,
                                               const float* s_nw, int ch, int ngroups, int lane) {
     const int m = lane & 15, kq = lane >> 4;
     const int ng = min(kGroups, ngroups - ch * kGroups);
@@ -383,16 +451,13 @@ __device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& ac
 #pragma unroll
     for (int gi = 0; gi < kGroups; ++gi) {
         if (gi >= ng) break;   // uniform: a partial last chunk
-        // lanes of tokens past K hold token K-1's inputs: finite, and their outputs, sums and
-        // norm factors are never stored
+        // lanes of tokens past K hold token K-1's inputs: finite, and their outputs are never
+        // stored.  Inputs times 2^-E: with the norm, the staged weights carry the factor.
         const float xv[8] = {c.x[gi][0].x, c.x[gi][0].y, c.x[gi][0].z, c.x[gi][0].w,
                              c.x[gi][1].x, c.x[gi][1].y, c.x[gi][1].z, c.x[gi][1].w};
         float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            ss = __builtin_fmaf(xv[e], xv[e], ss);
-            v[e] = xv[e];
-        }
+        for (int e = 0; e < 8; ++e) v[e] = NORM ? xv[e] : xv[e] * fin;
         if constexpr (NORM) {   // the norm weights of these 8 columns, from LDS
             const float4* wp = reinterpret_cast<const float4*>(s_nw + 32 * (ch * kGroups + gi) + 8 * kq);
             const float4 w0 = wp[0], w1 = wp[1];
@@ -453,7 +518,7 @@ __device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& ac
 // chunk's loads.
 template <class F, bool NORM>
 __device__ __forceinline__ void wave_rows(const ProjTokArgs& a, const WPlanes& w, int row, int wave,
-                                          int lane, f32x4_t& acc, float& ss, float* tab, float* s_nw) {
+                                          int lane, f32x4_t& acc, float fin, float* tab, float* s_nw) {
     const int ngroups = a.cols >> 5;
     const int nchunks = (ngroups + kGroups - 1) / kGroups;
     const int n = wave < nchunks ? (nchunks - wave + kWaves - 1) / kWaves : 0;
@@ -461,21 +526,25 @@ __device__ __forceinline__ void wave_rows(const ProjTokArgs& a, const WPlanes& w
     auto chunk = [&](int i) { return wave + min(i, n - 1) * kWaves; };
     ChunkRegs<F> ca, cb;
     if (n > 0) chunk_issue<F, NORM>(ca, a, w, row, chunk(0), ngroups, lane, tok_live);
-    if constexpr (NORM) {   // the norm weights to LDS once per workgroup, behind the first loads
+    if constexpr (NORM) {   // the norm weights times 2^-E to LDS once per workgroup, behind
+                            // the first loads ((x * w) * 2^-E = x * (w * 2^-E), exactly)
         const float4* src = reinterpret_cast<const float4*>(a.norm_w);
-        for (int c4 = wave * 64 + lane; c4 < (a.cols >> 2); c4 += kThreads)
-            reinterpret_cast<float4*>(s_nw)[c4] = src[c4];
+        for (int c4 = wave * 64 + lane; c4 < (a.cols >> 2); c4 += kThreads) {
+            const float4 wv = src[c4];
+            reinterpret_cast<float4*>(s_nw)[c4] =
+                make_float4(wv.x * fin, wv.y * fin, wv.z * fin, wv.w * fin);
+        }
         __syncthreads();
     }
     if (n == 0) return;
     int i = 0;
     for (; i + 1 < n; i += 2) {
         chunk_issue<F, NORM>(cb, a, w, row, chunk(i + 1), ngroups, lane, tok_live);
-        chunk_consume<F, NORM>(ca, acc, ss, tab, s_nw, chunk(i), ngroups, lane);
+        chunk_consume<F, NORM>(ca, acc, fin, tab, s_nw, chunk(i), ngroups, lane);
         chunk_issue<F, NORM>(ca, a, w, row, chunk(i + 2), ngroups, lane, tok_live);
-        chunk_consume<F, NORM>(cb, acc, ss, tab, s_nw, chunk(i + 1), ngroups, lane);
+        chunk_consume<F, NORM>(cb, acc, fin, tab, s_nw, chunk(i + 1), ngroups, lane);
     }
-    if (n & 1) chunk_consume<F, NORM>(ca, acc, ss, tab, s_nw, chunk(n - 1), ngroups, lane);
+    if (n & 1) chunk_consume<F, NORM>(ca, acc, fin, tab, s_nw, chunk(n - 1), ngroups, lane);
 }
 
 template <class F1, class F2>
@@ -491,28 +560,24 @@ constexpr int waves_per_eu() { return std::is_same<F1, PF32>::value ? 3 : 4; }
 template <class F1, class F2, bool NORM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_eu<F1, F2>())))
 void proj_tok_kernel(ProjTokArgs a) {
-    extern __shared__ float s_nw[];   // NORM: the pre-norm weights [cols]
+    extern __shared__ float s_nw[];   // NORM: the pre-norm weights [cols], times 2^-E
     __shared__ float s_tab[kWaves][16 * tab_floats<F1, F2>()];
     __shared__ f32x4_t s_red[kWaves][64];
-    __shared__ float s_ss[kWaves][16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = blockIdx.x * 16;
     const TokSeg& sg = tok_seg(a, row0);
     const int row = row0 - sg.out_off + (lane & 15);   // this lane's A row within its segment
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    float ss = 0.0f;
+    // The launch's input range factor 2^-E and output factor 2^E (scalar registers).
+    const int E = input_exp(a);
+    const float fin = __uint_as_float((unsigned)(127 - E) << 23);
     if (std::is_same<F1, F2>::value || sg.fmt == 0)
-        wave_rows<F1, NORM>(a, sg.w, row, wave, lane, acc, ss, s_tab[wave], s_nw);
+        wave_rows<F1, NORM>(a, sg.w, row, wave, lane, acc, fin, s_tab[wave], s_nw);
     else
-        wave_rows<F2, NORM>(a, sg.w, row, wave, lane, acc, ss, s_tab[wave], s_nw);
+        wave_rows<F2, NORM>(a, sg.w, row, wave, lane, acc, fin, s_tab[wave], s_nw);
 
     s_red[wave][lane] = acc;
-    if constexpr (NORM) {
-        ss = dk::lane_step<16, false>(ss);
-        ss = dk::lane_step<32, false>(ss);
-        if (lane < 16) s_ss[wave][lane] = ss;
-    }
     __syncthreads();
     // 256 outputs (16 rows x 16 tokens); thread o < 256 sums the waves' partials for (lane o%64,
     // element o/64).
@@ -523,15 +588,8 @@ void proj_tok_kernel(ProjTokArgs a) {
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) v = v + s_red[w][ln][i];
         if (tt < a.K) {
-            if constexpr (NORM) {   // RMSNorm.apply's factor, from the token's sum of squares
-                float tot = s_ss[0][tt];
-#pragma unroll
-                for (int w = 1; w < kWaves; ++w) tot = tot + s_ss[w][tt];
-                float q = tot / (float)a.cols;
-                q = q + a.eps;
-                const float r = 1.0f / (float)__builtin_sqrt((double)q);
-                v = v * r;
-            }
+            v = v * __uint_as_float((unsigned)(127 + E) << 23);   // the inputs were scaled by 2^-E
+            if constexpr (NORM) v = v * a.tok_sc[2 * tt];         // RMSNorm.apply's factor r
             const int r = row0 - sg.out_off + rr;
             if (sg.bias != nullptr) v = v + sg.bias[r];
             if (a.resid != nullptr) {

@@ -329,6 +329,21 @@ class TransformerLayerWeights:
     woBias: Optional[np.ndarray] = None
 
 
+def kernel_group(head_size: int, group: int) -> int:
+    """The GQA group the library's kernels run a layer with (llmp_runtime's kernel_group): the
+    group itself for head_dim 64/128/256/512 with groups 1-8, 96 with 1-4 (Phi-3) and 80 with 1-2
+    (Phi-2); a larger group runs as several groups of its largest such divisor per cached KV
+    head (GLM-4's 16 and 24 query heads per KV head as 2 and 3 groups of 8); 0 for a head size
+    with no kernel."""
+    limit = {64: 8, 128: 8, 256: 8, 512: 8, 96: 4, 80: 2}.get(head_size, 0)
+    if group < 1 or limit == 0:
+        return 0
+    for g in range(min(group, limit), 0, -1):
+        if group % g == 0:
+            return g
+    return 0
+
+
 class HipForwardPass:
     """Attention section of a GPU-resident forward pass on MI355X.
 
@@ -394,16 +409,7 @@ class HipForwardPass:
         if config.head_count % config.head_count_kv:
             return False
         group = config.head_count // config.head_count_kv
-        if config.head_size in (64, 128, 256):
-            if not 1 <= group <= 8:
-                return False
-        elif config.head_size == 96:         # fp32 caches, groups 1-4 (Phi-3)
-            if not 1 <= group <= 4:
-                return False
-        elif config.head_size == 80:         # fp32 caches, groups 1-2, decode only (Phi-2)
-            if not 1 <= group <= 2:
-                return False
-        else:
+        if kernel_group(config.head_size, group) == 0:
             return False
         rd = config.rope_dim_count or config.head_size
         return rd % 2 == 0 and rd <= config.head_size

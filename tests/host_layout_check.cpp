@@ -7,7 +7,12 @@
 //   plan POS WINDOW SPLITS            -> "start n rows_per_split splits"
 //   splits N HKV NCU PERCU Q8         -> "splits wide"
 //   cgroups D SPLITS THREADS BATCH    -> "column groups of the split combine"
+//   kgroup D G                        -> "kernel group" (kernel_group)
+//   range H N ROW K V QS              -> "ek0 .. ek(H-1) ev0 .. ev(H-1) eq0 .. eq(H-1)": range
+//                                        exponents of fp32 rows K, V ([N][H*ROW] floats) and of
+//                                        the Q8_0 rows QS (N*H*ROW int8 quants, then the scales)
 #include <cstdio>
+#include <cstring>
 #include <fstream>
 #include <iostream>
 #include <iterator>
@@ -71,6 +76,29 @@ int main() {
             bool wide = false;
             const int s = llmp::default_splits(n, hkv, ncu, per_cu, q8 != 0, &wide);
             std::printf("%d %d\n", s, wide ? 1 : 0);
+        } else if (cmd == "kgroup") {
+            int d, g;
+            in >> d >> g;
+            std::printf("%d\n", llmp::kernel_group(d, g));
+        } else if (cmd == "range") {
+            size_t H, n, row;
+            std::string ks, vs, qs;
+            in >> H >> n >> row >> ks >> vs >> qs;
+            std::vector<uint8_t> kb = read_file(ks), vb = read_file(vs), qb = read_file(qs);
+            std::vector<float> k(kb.size() / 4), v(vb.size() / 4);
+            std::memcpy(k.data(), kb.data(), kb.size());
+            std::memcpy(v.data(), vb.data(), vb.size());
+            const size_t nq = n * H * row;
+            std::vector<int8_t> q(nq);
+            std::vector<float> sc(nq / 32);
+            std::memcpy(q.data(), qb.data(), nq);
+            std::memcpy(sc.data(), qb.data() + nq, sc.size() * 4);
+            std::vector<int> ek(H, 0), ev(H, 0), eq(H, 0);
+            llmp::range_exp_rows(k.data(), v.data(), H, n, row, ek.data(), ev.data());
+            llmp::range_exp_rows_q8(q.data(), sc.data(), H, n, row, eq.data());
+            for (size_t h = 0; h < H; ++h) std::printf("%d ", ek[h]);
+            for (size_t h = 0; h < H; ++h) std::printf("%d ", ev[h]);
+            for (size_t h = 0; h < H; ++h) std::printf("%d%s", eq[h], h + 1 < H ? " " : "\n");
         } else if (!cmd.empty()) {
             std::printf("unknown command %s\n", cmd.c_str());
             return 2;

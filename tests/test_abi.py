@@ -116,9 +116,12 @@ def test_is_supported_for_attention():
     ok = hfp.ModelConfig(24, 8, 128, 28)
     assert hfp.HipForwardPass.isSupportedForAttention(ok)
     assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(24, 8, 128, 28, use_layer_norm=True))
-    for h, kv, d in ((24, 8, 96), (40, 8, 128), (28, 4, 128), (32, 32, 80), (16, 8, 80)):
+    # groups above the instantiated ones run as several groups per KV head: 9 (36/4) as 3 x 3,
+    # 6 at head_dim 96 as 2 x 3, 3 at head_dim 80 as 3 x 1, GLM-4's 16 and 24 as 2 and 3 x 8
+    for h, kv, d in ((24, 8, 96), (40, 8, 128), (28, 4, 128), (32, 32, 80), (16, 8, 80),
+                     (36, 4, 128), (24, 4, 96), (24, 8, 80), (32, 2, 128), (48, 2, 128)):
         assert hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(h, kv, d, 28)), (h, kv, d)
-    for h, kv, d in ((24, 7, 128), (36, 4, 128), (24, 4, 96), (24, 8, 80), (16, 4, 112)):
+    for h, kv, d in ((24, 7, 128), (16, 4, 112), (8, 8, 100)):
         assert not hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(h, kv, d, 28)), (h, kv, d)
 
 

@@ -193,8 +193,11 @@ def test_error_codes():
         hd = C.c_uint64()
         assert _lib.status("llmp_kv_create", 1, 16, 2, 112, 0, C.byref(hd)) == 6
         assert _lib.status("llmp_kv_create", 1, 16, 2, 96, 1, C.byref(hd)) == 6   # Q8_0 at 96
+        assert _lib.status("llmp_layer_config", h, 0, 9, 2, 64, 0, 0, 0, 1, 0.0, 0.0, 1e-5,
+                           None, None) == 1   # 9 query heads over 2 KV heads
+        # group 9 runs as 3 groups of 3 per KV head (any group has a divisor with a kernel)
         assert _lib.status("llmp_layer_config", h, 0, 18, 2, 64, 0, 0, 0, 1, 0.0, 0.0, 1e-5,
-                           None, None) == 6   # group 9 has no kernel
+                           None, None) == 0
         # an allocation beyond HBM is refused before touching the device
         assert _lib.status("llmp_kv_create", 4096, 1 << 20, 64, 128, 0, C.byref(hd)) == 5
 

@@ -208,6 +208,67 @@ def test_combine_column_groups(driver):
             assert cb == 8 or nc % (2 * cb) or nc // (2 * cb) < 4, (d, s, cb)
 
 
+def test_kernel_group_matches_the_python_mirror(driver):
+    """The group the kernels run a layer with (virtual KV heads for groups above the
+    instantiated ones): the library's rule and the host mirror's (HipForwardPass's
+    isSupportedForAttention) agree over head sizes and groups 0-64; GLM-4's groups 16 and 24
+    run as groups of 8, a prime group as groups of 1, and head_dim 112 has no kernel."""
+    from llmplayer_amd import hip_forward_pass as hfp
+    exe, _ = driver
+    cases = [(d, g) for d in (64, 80, 96, 112, 128, 256, 512) for g in range(0, 65)]
+    out = _run(exe, [f"kgroup {d} {g}" for d, g in cases])
+    got = [int(x) for x in out]
+    assert got == [hfp.kernel_group(d, g) for d, g in cases]
+    kg = dict(zip(cases, got))
+    assert kg[(128, 16)] == 8 and kg[(128, 24)] == 8 and kg[(128, 12)] == 6 and kg[(128, 11)] == 1
+    assert kg[(96, 6)] == 3 and kg[(80, 6)] == 2 and kg[(112, 1)] == 0 and kg[(64, 0)] == 0
+    for (d, g), k in kg.items():
+        if k:
+            assert g % k == 0 and k <= {80: 2, 96: 4}.get(d, 8)
+
+
+def _range_exp_ref(x):
+    """max(0, floor(log2|x|) - 14), 0 for x = 0: the smallest e with |x| * 2^-e < 2^15."""
+    x = np.abs(np.asarray(x, np.float64))
+    out = np.zeros(x.shape, np.int64)
+    nz = x > 0
+    out[nz] = np.maximum(0, np.floor(np.log2(x[nz])).astype(np.int64) - 14)
+    return out
+
+
+def test_range_exponents(driver):
+    """The host-side range exponents of rows written by llmp_kv_write / llmp_kv_write_q8 against
+    the closed form, per KV head: boundary values 2^15 - ulp / 2^15 / 65504, 1e5, the fp32
+    maximum, subnormals and zeros; and |x| * 2^-e < 2^15 for every value."""
+    exe, d = driver
+    rng = np.random.default_rng(11)
+    H, n, row = 3, 5, 64
+    k = rng.standard_normal((n, H * row)).astype(np.float32)
+    v = rng.standard_normal((n, H * row)).astype(np.float32)
+    special = np.array([np.nextafter(np.float32(32768), np.float32(0)), 32768, 65504, -1e5, 3.4e38,
+                        1e-45, -0.0, 1e-7, -65535.9], np.float32)
+    k[1, row:row + special.size] = special          # KV head 1
+    v[4, 2 * row + 5] = np.float32(-3e7)            # KV head 2
+    q = rng.integers(-128, 128, (n, H * row)).astype(np.int8)
+    sc = (rng.random((n, H * row // 32)) * 1e-2).astype(np.float32)
+    sc[2, 0] = np.float32(300.0)                    # KV head 0: 127 * 300 = 38100 -> e = 1
+    q[2, 0] = 127
+    (d / "k.bin").write_bytes(k.tobytes())
+    (d / "v.bin").write_bytes(v.tobytes())
+    (d / "q.bin").write_bytes(q.tobytes() + sc.tobytes())
+    out = _run(exe, [f"range {H} {n} {row} {d / 'k.bin'} {d / 'v.bin'} {d / 'q.bin'}"])
+    got = [int(t) for t in out[0].split()]
+    deq = (q.astype(np.float32) * np.repeat(sc, 32, axis=1)).astype(np.float32)
+    want = []
+    for arr in (k, v, deq):
+        want += [int(_range_exp_ref(arr.reshape(n, H, row)[:, h, :]).max()) for h in range(H)]
+    assert got == want, (got, want)
+    assert got[1] == 113 and got[H + 2] == 10 and got[2 * H] == 1
+    e = _range_exp_ref(special)
+    assert list(e) == [0, 1, 1, 2, 113, 0, 0, 0, 1]
+    assert (np.abs(special.astype(np.float64)) * 2.0 ** -e < 2 ** 15).all()
+
+
 def test_oracle_under_sanitizers(tmp_path):
     """tests/test_oracle.py and tests/test_block_oracle.py against the sanitized oracle build."""
     asan_dir = tmp_path / "asan"

@@ -1,9 +1,11 @@
 """GPU parity of the head shapes beyond the BASELINE configs, as the reference GPU's
 attention_full runs any headSize and kvMul (attention.cu:10-34): GQA groups 5 and 7
-(Qwen2.5-7B 28/4, 40/8), head_dim 96 (Phi-3-mini, 32/32, NEOX) and head_dim 80 (Phi-2, 32/32,
-NEOX over 32 of the 80 dims).  Decode against the oracle at fp32 (and Q8_0 for the groups),
-multi-token attention on fp32 projections, and the K-token attention half (at head_dim 80 its
-tokens run one by one: that head size has no prefill kernel).
+(Qwen2.5-7B 28/4, 40/8), groups 16 and 24 (GLM-4's 32 and 48 query heads over 2 KV heads,
+README.md:566, which run as 2 and 3 groups of 8 per cached KV head), head_dim 96 (Phi-3-mini,
+32/32, NEOX) and head_dim 80 (Phi-2, 32/32, NEOX over 32 of the 80 dims).  Decode against the
+oracle at fp32 (and Q8_0 for the groups), multi-token attention on fp32 projections, and the
+K-token attention half (at head_dim 80 its tokens run one by one: that head size has no prefill
+kernel).
 
 Bar: output max-abs <= 1e-4 (and <= 1e-4 + 1e-3*|ref|); every cache row bit-identical to the
 oracle's."""
@@ -27,6 +29,9 @@ SHAPES = {
     "24-8-96": dict(h=24, kv=8, d=96, arch=hfp.ARCH_LLAMA, theta=1e4),
     "phi2_32-32-80": dict(h=32, kv=32, d=80, arch="phi3", theta=1e4, rope_dim=32),
     "16-8-80": dict(h=16, kv=8, d=80, arch=hfp.ARCH_LLAMA, theta=1e4),
+    "glm4_32-2-128": dict(h=32, kv=2, d=128, arch=hfp.ARCH_LLAMA, theta=1e4),
+    "48-2-128": dict(h=48, kv=2, d=128, arch=hfp.ARCH_LLAMA, theta=1e4),
+    "36-4-64": dict(h=36, kv=4, d=64, arch=hfp.ARCH_LLAMA, theta=5e5),
 }
 
 
@@ -56,7 +61,8 @@ def test_decode_new_shapes(name, splits):
         dc.compare_cache(fp, 0, kc, vc, f"decode {name} cache", rows=(0, pos + 1))
 
 
-@pytest.mark.parametrize("name", ["qwen2.5-7b_28-4-128", "40-8-128", "14-2-64", "10-2-256"])
+@pytest.mark.parametrize("name", ["qwen2.5-7b_28-4-128", "40-8-128", "14-2-64", "10-2-256",
+                                  "glm4_32-2-128", "48-2-128", "36-4-64"])
 @pytest.mark.parametrize("mode", [_lib.LLMP_KV_Q8_0, _lib.LLMP_KV_Q8_0_TRUNC], ids=["round", "trunc"])
 def test_decode_groups_5_7_q8_0(name, mode):
     from oracle import oracle as orc
@@ -77,7 +83,9 @@ def test_decode_groups_5_7_q8_0(name, mode):
 
 @pytest.mark.parametrize("name,pos0,P", [("qwen2.5-7b_28-4-128", 100, 70), ("40-8-128", 0, 130),
                                          ("14-2-64", 3000, 4), ("10-2-256", 40, 33),
-                                         ("phi3-mini_32-32-96", 50, 90), ("24-8-96", 2000, 16)])
+                                         ("phi3-mini_32-32-96", 50, 90), ("24-8-96", 2000, 16),
+                                         ("glm4_32-2-128", 200, 40), ("48-2-128", 3000, 16),
+                                         ("36-4-64", 0, 300)])
 def test_prefill_f32_new_shapes(name, pos0, P):
     """Multi-token attention on fp32 projections (the split-K path for the short chunks after a
     long prefix), followed by decode steps."""
@@ -97,13 +105,21 @@ def test_head_dim_80_has_no_prefill_kernel():
 
 
 def test_unsupported_shapes_are_rejected():
-    for h, kv, d in ((24, 4, 80), (30, 5, 96), (18, 2, 64), (16, 16, 112)):
+    for h, kv, d in ((16, 16, 112), (8, 8, 100), (12, 5, 128)):
         c = hfp.ModelConfig(h, kv, d, 1)
         assert not hfp.HipForwardPass.isSupportedForAttention(c), (h, kv, d)
+    # groups beyond the instantiated ones run as several groups per KV head (group 9 at head_dim
+    # 64 as 3 of 3, 6 at head_dim 96 as 2 of 3, 6 at head_dim 80 as 3 of 2)
+    for h, kv, d in ((18, 2, 64), (30, 5, 96), (24, 4, 80), (32, 2, 128)):
+        assert hfp.HipForwardPass.isSupportedForAttention(hfp.ModelConfig(h, kv, d, 1)), (h, kv, d)
+    with hfp.HipForwardPass(hfp.ModelConfig(16, 16, 128, 1), 64) as fp:
+        h = fp.kv.handle
+        assert _lib.status("llmp_layer_config", h, 0, 16, 16, 112, 0, 0, 0, 1, 0.0, 0.0, 1e-6,
+                           None, None) != 0
 
 
 @pytest.mark.parametrize("name,dim", [("qwen2.5-7b_28-4-128", 3584), ("phi3-mini_32-32-96", 3072),
-                                      ("phi2_32-32-80", 2560)])
+                                      ("phi2_32-32-80", 2560), ("glm4_32-2-128", 4096)])
 def test_block_batch_new_shapes(name, dim):
     """The K-token attention half: 12 tokens after a 60-row prefix (head_dim 80 runs its tokens
     one by one through the decode kernel)."""
