@@ -722,6 +722,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     constexpr int NPART_LDS = WAVES * RPW;
     constexpr bool LDS_MERGE = NPART_LDS * G * D * 4 <= (D >= 256 && WAVES == 4 ? 65536 : 32768);
     constexpr int NPART = LDS_MERGE ? NPART_LDS : WAVES;
+    // The weight pass of the LDS merge gives one thread to each (partial, head) pair.
+    static_assert(!LDS_MERGE || NPART * G <= NTHR, "LDS merge needs a thread per partial and head");
     __shared__ float s_m[NPART * G];
     __shared__ float s_l[NPART * G];
     __shared__ float s_w[LDS_MERGE ? NPART * G : 1];

@@ -117,6 +117,21 @@ def test_every_supported_group_and_head_dim(hq, hkv, dim):
             _run(fp, c, 1200, d, 0, 999, splits, f"shape {hq}/{hkv}/{dim}")
 
 
+@pytest.mark.parametrize("hq,hkv,pos", [(64, 8, 991), (64, 8, 511), (16, 2, 250), (32, 8, 671),
+                                        (8, 8, 300)],
+                         ids=["g8-991", "g8-511", "g8-250", "g4-671", "g1-300"])
+def test_two_wave_workgroups_at_head_dim_64(hq, hkv, pos):
+    """The default plan at head_dim 64 over short splits (at most 32 rows) runs 2-wave
+    workgroups, whose LDS merge gives one thread to each of its 16 partials and G heads (128
+    pairs at G=8: every thread of the workgroup)."""
+    c = hfp.ModelConfig(hq, hkv, 64, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=5e5)
+    d = dc.make_layer(c, 1024, pos, seed=hq + pos)
+    with hfp.HipForwardPass(c, 1024) as fp:
+        plan = fp.decodePlan(0, pos)
+        assert plan["waves"] == 2 and plan["rows_per_split"] <= 32, plan
+        _run(fp, c, 1024, d, 0, pos, 0, f"2-wave {hq}/{hkv}/64 pos {pos} {plan}")
+
+
 # ------------------------------------------------------------------------------ edge cases
 def test_pos0_output_is_v0():
     c = hfp.ModelConfig(32, 8, 64, 1, rope_freq_base=500000.0)
