@@ -480,25 +480,36 @@ def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int, q8: bool = False
 
 
 def synthetic_gguf(t: int, rows: int, cols: int, rng) -> np.ndarray:
-    """Random GGUF-layout bytes of type t (Q4_K or Q6_K) with finite fp16 scale fields:
-    uniform quants and scale bytes, super-block scales 2^-10 (d) and 2^-12 (dmin)."""
+    """Random GGUF-layout bytes of type t (Q4_K, Q6_K, Q3_K or Q5_K) with finite fp16 scale
+    fields: uniform quants and scale bytes, super-block scales 2^-10 (d) and 2^-12 (dmin)."""
     ns = cols // 256
-    if t == 12:     # Q4_K: d, dmin (fp16), 12 scale bytes, 128 nibble bytes
-        b = rng.integers(0, 256, (rows, ns, 144), dtype=np.uint8)
-        b[:, :, 0:2] = np.frombuffer(np.float16(2.0 ** -10).tobytes(), np.uint8)
-        b[:, :, 2:4] = np.frombuffer(np.float16(2.0 ** -12).tobytes(), np.uint8)
-    else:           # Q6_K: ql, qh, 16 int8 scales, d (fp16) at byte 208
+    f16 = lambda v: np.frombuffer(np.float16(v).tobytes(), np.uint8)
+    if t in (12, 13):   # Q4_K (144 bytes) / Q5_K (176): d, dmin (fp16) first
+        b = rng.integers(0, 256, (rows, ns, 144 if t == 12 else 176), dtype=np.uint8)
+        b[:, :, 0:2] = f16(2.0 ** -10)
+        b[:, :, 2:4] = f16(2.0 ** -12)
+    elif t == 11:       # Q3_K: hmask, qs, 12 scale bytes, d (fp16) at byte 108
+        b = rng.integers(0, 256, (rows, ns, 110), dtype=np.uint8)
+        b[:, :, 108:110] = f16(2.0 ** -10)
+    else:               # Q6_K: ql, qh, 16 int8 scales, d (fp16) at byte 208
         b = rng.integers(0, 256, (rows, ns, 210), dtype=np.uint8)
-        b[:, :, 208:210] = np.frombuffer(np.float16(2.0 ** -12).tobytes(), np.uint8)
+        b[:, :, 208:210] = f16(2.0 ** -12)
     return b.reshape(-1)
 
 
-def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False) -> dict:
-    """The attention half of a C3 (Llama-3.2-3B, dim 3072) layer with the Q4_K_M weight mix
-    (Q4_K for q, k, o; Q6_K for v): pre-norm, projections, attention at ctx, output projection
-    and residual, as a graph replay over n_layers layers with their own weights and caches.
-    q8_input: the Q4_K projections on the Q8_1-quantised input (the reference GPU's int8
-    matvecs) instead of the fp32 input."""
+# GGUF weight mixes of the attention projections (q, k, v, o), as llama.cpp's quantiser assigns
+# them: Q4_K_M keeps Q6_K for v; Q3_K_L takes Q5_K for v and o.
+MIXES = {"q4_k_m": ((12, 12, 14, 12), "Q4_K_M mix (Q4_K q/k/o, Q6_K v)"),
+         "q3_k_l": ((11, 11, 13, 13), "Q3_K_L mix (Q3_K q/k, Q5_K v/o)")}
+
+
+def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
+              mix: str = "q4_k_m") -> dict:
+    """The attention half of a C3 (Llama-3.2-3B, dim 3072) layer with a GGUF weight mix (MIXES;
+    default Q4_K_M: Q4_K for q, k, o and Q6_K for v): pre-norm, projections, attention at ctx,
+    output projection and residual, as a graph replay over n_layers layers with their own
+    weights and caches.  q8_input: the Q4_K projections on the Q8_1-quantised input (the
+    reference GPU's int8 matvecs) instead of the fp32 input."""
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
     dim = 3072
@@ -512,10 +523,11 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False) 
             fp.kv.write(layer, 0, kc, vc)
         fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_Q8_1 if q8_input else _lib.LLMP_INPUT_F32)
         wbytes = 0
+        tq, tk, tv, to = MIXES[mix][0]
         for layer in range(n_layers):
             lw = hfp.TransformerLayerWeights(attnNorm=np.ones(dim, np.float32))
-            for name, t, rows, cols in (("wq", 12, c.q_dim, dim), ("wk", 12, c.kv_dim, dim),
-                                        ("wv", 14, c.kv_dim, dim), ("wo", 12, dim, c.q_dim)):
+            for name, t, rows, cols in (("wq", tq, c.q_dim, dim), ("wk", tk, c.kv_dim, dim),
+                                        ("wv", tv, c.kv_dim, dim), ("wo", to, dim, c.q_dim)):
                 data = synthetic_gguf(t, rows, cols, rng)
                 setattr(lw, name, hfp.GgufTensor(t, rows, cols, data))
                 if layer == 0:
@@ -534,7 +546,7 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False) 
     finally:
         fp.close()
     us = ms / steps * 1e3
-    return {"ctx": ctx, "weights": "Q4_K_M mix (Q4_K q/k/o, Q6_K v)", "dim": dim,
+    return {"ctx": ctx, "weights": MIXES[mix][1], "dim": dim,
             "input": "Q8_1 (int8 dot products for Q4_K)" if q8_input else "fp32",
             "us_per_layer_call": round(us, 2), "weight_bytes_per_layer": wbytes,
             "kv_bytes_per_layer": kv_bytes(ctx), "layers_rotated": n_layers}
@@ -790,6 +802,8 @@ def main() -> int:
                     help="skip the attention-block (projections + attention) measurement")
     ap.add_argument("--block-q8", action="store_true",
                     help="--profile-block: the Q8_1 input mode")
+    ap.add_argument("--block-mix", choices=sorted(MIXES), default="q4_k_m",
+                    help="--profile-block: the projection weight mix")
     ap.add_argument("--profile-block", action="store_true",
                     help="for rocprofv3: the attention-block graph at --ctx2 only, then exit")
     ap.add_argument("--profile-block-batch", type=int, default=0, metavar="K",
@@ -840,7 +854,7 @@ def main() -> int:
         log(f"[bench] profile prefill: P={args.profile_prefill}, {r}")
         return 0
     if args.profile_block:
-        r = block_run(args.ctx2 or 4096, args.steps, q8_input=args.block_q8)
+        r = block_run(args.ctx2 or 4096, args.steps, q8_input=args.block_q8, mix=args.block_mix)
         log(f"[bench] profile block: {r}")
         return 0
     if args.profile_block_batch:
@@ -898,7 +912,7 @@ def main() -> int:
                 f"kernel {r['attn_kernel_us']} us ({r['attn_kernel_causal_tflops']} causal TFLOP/s)")
             prefill.append(r)
 
-    block = block_q8 = block_batch = None
+    block = block_q8 = block_q3kl = block_batch = None
     if args.block:
         block = block_run(args.ctx2 or 4096, 200)
         if second is not None:
@@ -911,6 +925,13 @@ def main() -> int:
         log(f"[bench] attention block C3 Q4_K_M at ctx {block['ctx']}: {block['us_per_layer_call']} us/layer")
         block_q8 = block_run(args.ctx2 or 4096, 200, q8_input=True)
         log(f"[bench] attention block, Q8_1 input: {block_q8['us_per_layer_call']} us/layer")
+        block_q3kl = block_run(args.ctx2 or 4096, 200, mix="q3_k_l")
+        if second is not None:
+            block_q3kl["projections_us"] = round(block_q3kl["us_per_layer_call"] - second["us_per_layer_call"], 2)
+            if block_q3kl["projections_us"] > 0:
+                block_q3kl["projection_weight_gbps"] = round(
+                    block_q3kl["weight_bytes_per_layer"] / (block_q3kl["projections_us"] * 1e-6) / 1e9, 1)
+        log(f"[bench] attention block C3 Q3_K_L: {block_q3kl['us_per_layer_call']} us/layer")
         block_batch = []
         for ctx_b, K, nl in ((4096, 4, 28), (4096, 16, 28), (32768, 4, 8), (32768, 16, 8)):
             r = block_batch_run(ctx_b, K, 40, nl)
@@ -994,6 +1015,8 @@ def main() -> int:
         line["attn_block_c3_q4_k_m"] = block
     if block_q8 is not None:
         line["attn_block_c3_q4_k_m_q8_1_input"] = block_q8
+    if block_q3kl is not None:
+        line["attn_block_c3_q3_k_l"] = block_q3kl
     if block_batch:
         line["attn_block_batch_c3_q4_k_m"] = block_batch
     if q8_prefill is not None:

@@ -344,6 +344,12 @@ int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int 
 #define LLMP_GGML_Q4_K  12
 #define LLMP_GGML_Q6_K  14
 #define LLMP_GGML_BF16  30
+#define LLMP_GGML_Q5_0   6   /* split nibbles: element i low nibble of byte i, 16+i high      */
+#define LLMP_GGML_Q3_K  11
+#define LLMP_GGML_Q5_K  13
+#define LLMP_GGML_IQ4_NL 20  /* split nibbles, as Q5_0                                         */
+#define LLMP_GGML_IQ4_XS 23  /* split nibbles within each sub-block of 32 (its dot() order)   */
+#define LLMP_GGML_MXFP4 39   /* split nibbles; E8M0 exponent byte first                       */
 /* Weight slots of a layer (TransformerLayerWeights): matrices are [rows][cols] in GGUF row
  * order; vectors are fp32. */
 #define LLMP_W_ATTN_NORM      0  /* [dim] attnNorm RMSNorm weights; absent: x is copied (OLMo2) */

@@ -53,6 +53,25 @@ hipError_t launch_q4k_q6k(const gk::GemvArgs& a, hipStream_t st) {
     }
 }
 
+// Two formats of the K-quant mixes in one launch: F1 rows (GemvSeg::fmt 0) with NK1 rounds,
+// F2 rows (fmt 1) with at most 4 (Q3_K_L: Q3_K q and k with Q5_K v; Q5_K_M: Q5_K with Q6_K).
+template <class F1, int NK1, class F2>
+hipError_t launch_mix2(const gk::GemvArgs& a, hipStream_t st) {
+    switch (nk_for<F2>(a.cols)) {
+    case 2: return launch_nk<F1, NK1, F2, 2>(a, st);
+    case 3: return launch_nk<F1, NK1, F2, 3>(a, st);
+    default: return launch_nk<F1, NK1, F2, 4>(a, st);
+    }
+}
+template <class F1, class F2>
+hipError_t launch_mix(const gk::GemvArgs& a, hipStream_t st) {
+    switch (nk_for<F1>(a.cols)) {
+    case 2: return launch_mix2<F1, 2, F2>(a, st);
+    case 3: return launch_mix2<F1, 3, F2>(a, st);
+    default: return launch_mix2<F1, 4, F2>(a, st);
+    }
+}
+
 // The Q8_1-input Q4_K side holds at most 4 rounds next to Q6_K (more spills registers); its
 // rows need 4 rounds up to 4096 columns.
 template <class F1>
@@ -82,12 +101,21 @@ int gemv_unit(int ggml_type) {
     case gk::kQ4_0: return gk::FmtQ4_0::UNIT;
     case gk::kQ4_K: return gk::FmtQ4_K::UNIT;
     case gk::kQ6_K: return gk::FmtQ6_K::UNIT;
+    // block formats: the unit divides the block, so the host's whole-block check covers it
+    case gk::kQ5_0: return gk::FmtQ5_0::UNIT;
+    case gk::kQ3_K: return gk::FmtQ3_K::UNIT;
+    case gk::kQ5_K: return gk::FmtQ5_K::UNIT;
+    case gk::kIQ4_NL: return gk::FmtIQ4_NL::UNIT;
+    case gk::kIQ4_XS: return gk::FmtIQ4_XS::UNIT;
+    case gk::kMXFP4: return gk::FmtMXFP4::UNIT;
     default: return 0;
     }
 }
 
 bool gemv_pair_supported(int first_type, int second_type) {
-    return first_type == gk::kQ4_K && second_type == gk::kQ6_K;
+    return (first_type == gk::kQ4_K && second_type == gk::kQ6_K) ||
+           (first_type == gk::kQ3_K && second_type == gk::kQ5_K) ||
+           (first_type == gk::kQ5_K && second_type == gk::kQ6_K);
 }
 
 hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_type, bool q8_input,
@@ -96,6 +124,8 @@ hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_ty
     if (a.cols <= 0 || a.cols > gk::kMaxGemvCols || a.cols % 256 || a.rows_total <= 0 ||
         a.nseg < 1 || a.nseg > 3)
         return hipErrorInvalidValue;
+    if (first_type == gk::kQ3_K) return launch_mix<gk::FmtQ3_K, gk::FmtQ5_K>(a, st);
+    if (first_type == gk::kQ5_K) return launch_mix<gk::FmtQ5_K, gk::FmtQ6_K>(a, st);
     return q8_input ? launch_pair_f<gk::FmtQ4_KQ8>(a, st) : launch_pair_f<gk::FmtQ4_K>(a, st);
 }
 
@@ -114,6 +144,12 @@ hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipS
     case gk::kQ4_0: return launch_f<gk::FmtQ4_0>(a, st);
     case gk::kQ4_K: return launch_f<gk::FmtQ4_K>(a, st);
     case gk::kQ6_K: return launch_f<gk::FmtQ6_K>(a, st);
+    case gk::kQ5_0: return launch_f<gk::FmtQ5_0>(a, st);
+    case gk::kQ3_K: return launch_f<gk::FmtQ3_K>(a, st);
+    case gk::kQ5_K: return launch_f<gk::FmtQ5_K>(a, st);
+    case gk::kIQ4_NL: return launch_f<gk::FmtIQ4_NL>(a, st);
+    case gk::kIQ4_XS: return launch_f<gk::FmtIQ4_XS>(a, st);
+    case gk::kMXFP4: return launch_f<gk::FmtMXFP4>(a, st);
     default: return hipErrorInvalidValue;
     }
 }

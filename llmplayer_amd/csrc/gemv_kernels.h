@@ -21,6 +21,7 @@ namespace gk {
 
 // GGMLType ids (GGMLType.java:4-35) of the formats with a kernel here.
 constexpr int kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kBF16 = 30;
+constexpr int kQ5_0 = 6, kQ3_K = 11, kQ5_K = 13, kIQ4_NL = 20, kIQ4_XS = 23, kMXFP4 = 39;
 
 // One weight matrix on the device: up to four planes, each [rows][pitch bytes].
 struct WPlanes {
@@ -312,6 +313,251 @@ struct FmtQ6_K {
             const unsigned q = (nib | (((r.qh >> (2 * c)) & 0x03030303u) << 4)) ^ 0x20202020u;
             s = s + ds[c] * dot4(sx6(q, 0), sx6(q, 1), sx6(q, 2), sx6(q, 3),
                                  x4(st.xs, sb * 256 + 128 * h + 32 * c + l));
+        }
+        return s;
+    }
+};
+
+// ---- split-nibble formats ----------------------------------------------------------------------
+// Q5_0, IQ4_NL and MXFP4 blocks of 32, and each 32-weight sub-block of IQ4_XS, keep their codes
+// split: byte i of the block's 16 holds element i in its low nibble and element 16 + i in its
+// high nibble (the order of Q5_0FloatTensor, IQ4_NLFloatTensor, MXFP4FloatTensor and
+// IQ4_XSFloatTensor.dot).  Unit u: nibble bytes 4u .. 4u+3 of the row = bytes i0 .. i0+3 of
+// block u/4 (i0 = 4(u%4)), elements i0 .. i0+3 and 16+i0 .. 16+i0+3.
+__device__ __forceinline__ int split_x(int ub, int j) { return 8 * ub + 32 * (j >> 2) + 4 * (j & 3); }
+
+// Bit k (k < 4) of v moved to bit 0 of byte k (the four shifted copies land on distinct bits).
+__device__ __forceinline__ unsigned spread4(unsigned v) { return (v * 0x00204081u) & 0x01010101u; }
+
+// Four table bytes at once: byte k of the result is entry c_k (0..15) of the 16-byte table t,
+// c_k = byte k of `codes`.  Two byte permutes pick from entries 0-7 and 8-15, bit 3 selects.
+__device__ __forceinline__ unsigned lut16(unsigned codes, unsigned t0, unsigned t1, unsigned t2, unsigned t3) {
+    const unsigned sel = codes & 0x07070707u;
+    const unsigned a = __builtin_amdgcn_perm(t1, t0, sel);
+    const unsigned b = __builtin_amdgcn_perm(t3, t2, sel);
+    const unsigned m = ((codes >> 3) & 0x01010101u) * 0xFFu;
+    return (a & ~m) | (b & m);
+}
+// byte t of v as a signed integer, in float
+__device__ __forceinline__ float sbyte_f(unsigned v, int t) { return (float)((int)(v << (24 - 8 * t)) >> 24); }
+
+// The IQ4_NL codebook (IQ4_NLFloatTensor.KVALUES_IQ4NL) as int8, four entries per word.
+constexpr unsigned pack4(int a, int b, int c, int d) {
+    return (unsigned)(a & 0xFF) | ((unsigned)(b & 0xFF) << 8) | ((unsigned)(c & 0xFF) << 16) |
+           ((unsigned)(d & 0xFF) << 24);
+}
+constexpr unsigned kIq4[4] = {pack4(-127, -104, -83, -65), pack4(-49, -35, -22, -10), pack4(1, 13, 25, 38),
+                              pack4(53, 69, 89, 113)};
+// Twice MXFP4FloatTensor.FP4_TABLE (integers: 0, 1, 2, 3, 4, 6, 8, 12 and their negatives);
+// the block scale carries the factor 1/2.
+constexpr unsigned kFp4x2[4] = {pack4(0, 1, 2, 3), pack4(4, 6, 8, 12), pack4(0, -1, -2, -3),
+                                pack4(-4, -6, -8, -12)};
+
+// The dot of a split-nibble unit whose 8 values are the signed bytes of lo (elements i0..i0+3)
+// and hi (16+i0..), with the staged input.
+__device__ __forceinline__ float split_dot_s8(unsigned lo, unsigned hi, const Staged& st, int ub, int j) {
+    const int xi = split_x(ub, j);
+    return dot4(sbyte_f(lo, 0), sbyte_f(lo, 1), sbyte_f(lo, 2), sbyte_f(lo, 3), x4(st.xs, xi)) +
+           dot4(sbyte_f(hi, 0), sbyte_f(hi, 1), sbyte_f(hi, 2), sbyte_f(hi, 3), x4(st.xs, xi + 16));
+}
+
+// Q5_0: plane 0 = nibbles [rows][cols/2], plane 1 = the fifth bits of each block (uint32, bit i
+// = element i) [rows][cols/32], plane 2 = scales [rows][cols/32] fp16.  Values (q - 16) * d
+// (Q5_0FloatTensor.getFloat), summed as d * sum((q - 16) x).
+struct FmtQ5_0 {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false, Q8IN = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    struct Raw { unsigned q, qh; unsigned short d; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u),
+                   ldo<unsigned>(rp(w, 1, row), ((unsigned)u >> 2) * 4u),
+                   ldo<unsigned short>(rp(w, 2, row), ((unsigned)u >> 2) * 2u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned h = r.qh >> (4 * (j & 3));
+        // q ^ 16 as a 5-bit two's complement number is q - 16: flip bit 4, then sign-extend
+        const unsigned lo = ((r.q & 0x0F0F0F0Fu) | (spread4(h & 15u) << 4)) ^ 0x10101010u;
+        const unsigned hi = (((r.q >> 4) & 0x0F0F0F0Fu) | (spread4((h >> 16) & 15u) << 4)) ^ 0x10101010u;
+        auto s5 = [](unsigned v, int t) { return (float)((int)(v << (27 - 8 * t)) >> 27); };
+        const int xi = split_x(ub, j);
+        const float s = dot4(s5(lo, 0), s5(lo, 1), s5(lo, 2), s5(lo, 3), x4(st.xs, xi)) +
+                        dot4(s5(hi, 0), s5(hi, 1), s5(hi, 2), s5(hi, 3), x4(st.xs, xi + 16));
+        return h2f(r.d) * s;
+    }
+};
+
+// IQ4_NL: plane 0 = nibble codes [rows][cols/2], plane 1 = scales [rows][cols/32] fp16.
+// Values d * codebook[code] (IQ4_NLFloatTensor.dot), summed as d * sum(codebook x).
+struct FmtIQ4_NL {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false, Q8IN = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    struct Raw { unsigned q; unsigned short d; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u),
+                   ldo<unsigned short>(rp(w, 1, row), ((unsigned)u >> 2) * 2u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned lo = lut16(r.q & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        const unsigned hi = lut16((r.q >> 4) & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        return h2f(r.d) * split_dot_s8(lo, hi, st, ub, j);
+    }
+};
+
+// MXFP4: plane 0 = nibble codes [rows][cols/2], plane 1 = E8M0 exponent bytes [rows][cols/32].
+// Values FP4[code] * 2^(e - 127), 0 for e = 0 and e = 255 (MXFP4FloatTensor.dot), summed as
+// 2^(e - 128) * sum(2 FP4[code] x): both factors are exact, so each product is the same.
+__device__ __forceinline__ float e8m0_half(unsigned e) {
+    // 2^(e - 128): a normal float for e >= 2, the subnormal 2^-127 for e = 1
+    const float v = e >= 2u ? __uint_as_float((e - 1u) << 23) : __uint_as_float(0x00400000u);
+    return (e == 0u || e == 255u) ? 0.0f : v;
+}
+struct FmtMXFP4 {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false, Q8IN = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    struct Raw { unsigned q; unsigned char e; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u),
+                   ldo<unsigned char>(rp(w, 1, row), (unsigned)u >> 2)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned lo = lut16(r.q & 0x0F0F0F0Fu, kFp4x2[0], kFp4x2[1], kFp4x2[2], kFp4x2[3]);
+        const unsigned hi = lut16((r.q >> 4) & 0x0F0F0F0Fu, kFp4x2[0], kFp4x2[1], kFp4x2[2], kFp4x2[3]);
+        return e8m0_half(r.e) * split_dot_s8(lo, hi, st, ub, j);
+    }
+};
+
+// IQ4_XS: plane 0 = nibble codes [rows][cols/2] (sub-block ib of 32 at bytes 16ib .. 16ib+15
+// of its super-block, split), plane 1 = the sub-blocks' 6-bit scales decoded at upload to the
+// int8 ls - 32 [rows][cols/32], plane 2 = d [rows][cols/256] fp16.  Values
+// (d * (ls - 32)) * codebook[code] (IQ4_XSFloatTensor.dot).  Unit u: as the split-nibble
+// blocks, sub-block u/4.  Table: per super-block the 8 factors d * (ls - 32).
+struct FmtIQ4_XS {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 8;
+    static constexpr bool XSUM = false, Q8IN = false;
+    struct Row { uint2 sc; unsigned short d; };
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        const unsigned sb = (unsigned)min(j, (units >> 5) - 1);
+        return Row{ldo<uint2>(rp(w, 1, row), sb * 8u), ldo<unsigned short>(rp(w, 2, row), sb * 2u)};
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        if (j >= (units >> 5)) return;
+        const float d = h2f(r.d);
+        float4* t = reinterpret_cast<float4*>(tab + j * TAB);
+        t[0] = float4{d * sbyte_f(r.sc.x, 0), d * sbyte_f(r.sc.x, 1), d * sbyte_f(r.sc.x, 2), d * sbyte_f(r.sc.x, 3)};
+        t[1] = float4{d * sbyte_f(r.sc.y, 0), d * sbyte_f(r.sc.y, 1), d * sbyte_f(r.sc.y, 2), d * sbyte_f(r.sc.y, 3)};
+    }
+    struct Raw { unsigned q; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        // u = ub + j: sub-block (ub + j)/4 = 8 * (ub/32) + j/4 of the row's super-blocks
+        const float dl = st.tab[(ub >> 2) + (j >> 2)];
+        const unsigned lo = lut16(r.q & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        const unsigned hi = lut16((r.q >> 4) & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        return dl * split_dot_s8(lo, hi, st, ub, j);
+    }
+};
+
+// Q5_K: plane 0 = the low nibbles (Q4_K's plane 0 order), plane 1 = the 16-byte head (d, dmin,
+// 12 packed scale and min bytes: Q4_K's plane 1), plane 2 = the fifth bits qh (32 bytes per
+// super-block: bit 2g + s of byte l = element 64g + 32s + l).  Unit u as Q4_K's; value
+// d*sc*q - dmin*m (Q5_KFloatTensor.dot), summed as Q4_K's with the fifth bit or-ed in.
+struct FmtQ5_K {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 16;
+    static constexpr bool XSUM = true, Q8IN = false;
+    using Row = FmtQ4_K::Row;
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        return FmtQ4_K::head(w, row, j, units >> 5);
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        FmtQ4_K::build_tab_ns(r, tab, j, units >> 5);
+    }
+    struct Raw { unsigned q, qh; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        // qh bytes l .. l+3 of super-block u/32, l = 4(u%8)
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u),
+                   ldo<unsigned>(rp(w, 2, row), ((unsigned)u >> 5) * 32u + 4u * ((unsigned)u & 7u))};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const int g = (j >> 3) & 3;
+        const int i0 = 8 * ub + (j >> 5) * 256 + 64 * g + 4 * (j & 7), i1 = i0 + 32;
+        const float4& x0 = x4(st.xs, i0);
+        const float4& x1 = x4(st.xs, i1);
+        const float4 f = x4(st.tab, (ub >> 5) * TAB + (j >> 5) * TAB + 4 * g);
+        unsigned lo = (r.q & 0x0F0F0F0Fu) | (((r.qh >> (2 * g)) & 0x01010101u) << 4);
+        unsigned hi = ((r.q >> 4) & 0x0F0F0F0Fu) | (((r.qh >> (2 * g + 1)) & 0x01010101u) << 4);
+        asm("" : "+v"(lo), "+v"(hi));   // keep the byte conversions (see FmtQ4_K::dot)
+        const float p0 = dot4(byte_f(lo, 0), byte_f(lo, 1), byte_f(lo, 2), byte_f(lo, 3), x0);
+        const float p1 = dot4(byte_f(hi, 0), byte_f(hi, 1), byte_f(hi, 2), byte_f(hi, 3), x1);
+        return (f.x * p0 - f.y * st.xsum[i0 >> 2]) + (f.z * p1 - f.w * st.xsum[i1 >> 2]);
+    }
+};
+
+// Q3_K: plane 0 = the 2-bit quants qs (64 bytes per super-block), plane 1 = the high-bit mask
+// (32), plane 2 = the 16 sub-block scales decoded at upload to the int8 sc - 32, plane 3 = d
+// (fp16).  Element 128h + 32p + 16w + l: bits 2p..2p+1 of qs[32h + 16w + l], bit 4h + p of
+// hmask[16w + l], sub-block 8h + 2p + w; value (d * (sc - 32)) * (q - 4)
+// (Q3_KFloatTensor.dot).  Unit u: qs bytes 4u .. 4u+3 = super-block sb = u/16, h = (u%16)/8,
+// w = (u%8)/4, l = 4(u%4) .. +3, for the four p: 16 weights.  Table: per super-block the 16
+// factors d * (sc - 32) at (2h + w)*4 + p, so a unit's four factors are one 16-byte read.
+struct FmtQ3_K {
+    static constexpr int UNIT = 16, MAXU = 4, TAB = 16;
+    static constexpr bool XSUM = false, Q8IN = false;
+    struct Row { u32x4 sc; unsigned short d; };
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        const unsigned sb = (unsigned)min(j, (units >> 4) - 1);
+        return Row{ldo<u32x4>(rp(w, 2, row), sb * 16u), ldo<unsigned short>(rp(w, 3, row), sb * 2u)};
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        if (j >= (units >> 4)) return;
+        const float d = h2f(r.d);
+        float v[16];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int w = 0; w < 2; ++w)
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int k = 8 * h + 2 * p + w;
+                    v[(2 * h + w) * 4 + p] = d * sbyte_f(r.sc[k >> 2], k & 3);
+                }
+        float4* t = reinterpret_cast<float4*>(tab + j * TAB);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) t[g] = float4{v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]};
+    }
+    struct Raw { unsigned qs, hm; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        const unsigned sb = (unsigned)u >> 4, wv = ((unsigned)u >> 2) & 1u, l = 4u * ((unsigned)u & 3u);
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u),
+                   ldo<unsigned>(rp(w, 1, row), sb * 32u + 16u * wv + l)};
+    }
+    // the signed 3-bit field at bits 8t .. 8t+2 of v
+    static __device__ __forceinline__ float sx3(unsigned v, int t) {
+        return (float)((int)(v << (29 - 8 * t)) >> 29);
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const int h = (j >> 3) & 1, w = (j >> 2) & 1, l = 4 * (j & 3);
+        const int sb = (ub >> 4) + (j >> 4);
+        const float4 f = x4(st.tab, sb * TAB + (2 * h + w) * 4);
+        const float ds[4] = {f.x, f.y, f.z, f.w};
+        float s = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            // (q ^ 4) as a 3-bit two's complement number is q - 4
+            const unsigned q = (((r.qs >> (2 * p)) & 0x03030303u) | (((r.hm >> (4 * h + p)) & 0x01010101u) << 2)) ^
+                               0x04040404u;
+            s = s + ds[p] * dot4(sx3(q, 0), sx3(q, 1), sx3(q, 2), sx3(q, 3),
+                                 x4(st.xs, sb * 256 + 128 * h + 32 * p + 16 * w + l));
         }
         return s;
     }

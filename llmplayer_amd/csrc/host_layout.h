@@ -110,7 +110,36 @@ inline size_t ggml_row_bytes(int type, int cols) {
     case LLMP_GGML_Q4_0: return (size_t)(cols / 32) * 18;
     case LLMP_GGML_Q4_K: return (size_t)(cols / 256) * 144;
     case LLMP_GGML_Q6_K: return (size_t)(cols / 256) * 210;
+    case LLMP_GGML_Q5_0: return (size_t)(cols / 32) * 22;
+    case LLMP_GGML_Q3_K: return (size_t)(cols / 256) * 110;
+    case LLMP_GGML_Q5_K: return (size_t)(cols / 256) * 176;
+    case LLMP_GGML_IQ4_NL: return (size_t)(cols / 32) * 18;
+    case LLMP_GGML_IQ4_XS: return (size_t)(cols / 256) * 136;
+    case LLMP_GGML_MXFP4: return (size_t)(cols / 32) * 17;
     default: return 0;
+    }
+}
+
+// Q3_K's 16 six-bit sub-block scales from the 12 packed bytes at offset 96 of a super-block
+// (Q3_KFloatTensor.decodeAllScales, Q3_KFloatTensor.java:128-143): scale k has its low four
+// bits in byte k%8 (low nibble for k < 8, high nibble after) and its top two bits at bits
+// 2(k/4)..+1 of byte 8 + k%4.  Stored as the int8 sc - 32, the factor d multiplies.
+inline void q3k_scales(const uint8_t* raw, int8_t out[16]) {
+    for (int k = 0; k < 16; ++k) {
+        const int low = k < 8 ? (raw[k] & 15) : (raw[k - 8] >> 4);
+        const int top = (raw[8 + k % 4] >> (2 * (k / 4))) & 3;
+        out[k] = (int8_t)((low | (top << 4)) - 32);
+    }
+}
+// IQ4_XS's 8 six-bit sub-block scales from bytes 2..7 of a super-block (IQ4_XSFloatTensor.dot,
+// IQ4_XSFloatTensor.java:63-69): low four bits from scales_l (byte 4 + ib/2, low nibble for
+// even ib), top two bits from scales_h (uint16 at byte 2, bits 2ib..2ib+1); stored as ls - 32.
+inline void iq4xs_scales(const uint8_t* blk, int8_t out[8]) {
+    const int sh = blk[2] | (blk[3] << 8);
+    for (int ib = 0; ib < 8; ++ib) {
+        const int sl = blk[4 + ib / 2];
+        const int low = (ib & 1) ? (sl >> 4) : (sl & 15);
+        out[ib] = (int8_t)((low | (((sh >> (2 * ib)) & 3) << 4)) - 32);
     }
 }
 
@@ -158,6 +187,13 @@ inline void range_exp_rows_q8(const int8_t* q, const float* s, size_t H, size_t 
 //  - Q4_0: nibbles -> plane 0, fp16 scale -> plane 1;
 //  - Q4_K: d, dmin and the 12 packed scale bytes -> plane 1, nibbles -> plane 0;
 //  - Q6_K: low nibbles -> 0, high bit pairs -> 1, int8 scales -> 2, fp16 d -> 3;
+//  - Q5_0: nibbles -> 0, the 32 fifth bits (uint32) -> 1, fp16 scale -> 2;
+//  - Q3_K: 2-bit quants -> 0, high-bit mask -> 1, the 16 scales decoded to int8 sc - 32 -> 2,
+//    fp16 d -> 3;
+//  - Q5_K: nibbles -> 0, d, dmin and the 12 packed scale bytes -> 1, fifth bits -> 2;
+//  - IQ4_NL: nibble codes -> 0, fp16 scale -> 1;
+//  - IQ4_XS: nibble codes -> 0, the 8 scales decoded to int8 ls - 32 -> 1, fp16 d -> 2;
+//  - MXFP4: nibble codes -> 0, E8M0 exponent byte -> 1;
 //  - F32/F16/BF16: one plane, the rows unchanged.
 // Returns the plane count, or 0 for an unsupported type or a cols that is not a whole number
 // of blocks.
@@ -189,6 +225,28 @@ inline int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
         n = 4; bw = 256; blk_bytes = 210; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 4;
         pitch[2] = (size_t)cols / 16; pitch[3] = (size_t)cols / 256 * 2;
         set({{0, 0, 128}, {1, 128, 64}, {2, 192, 16}, {3, 208, 2}}); break;
+    case LLMP_GGML_Q5_0:
+        n = 3; bw = 32; blk_bytes = 22; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32 * 4;
+        pitch[2] = (size_t)cols / 32 * 2;
+        set({{2, 0, 2}, {1, 2, 4}, {0, 6, 16}}); break;
+    case LLMP_GGML_Q3_K:   // plane 2 (decoded scales) is written below
+        n = 4; bw = 256; blk_bytes = 110; pitch[0] = (size_t)cols / 4; pitch[1] = (size_t)cols / 8;
+        pitch[2] = (size_t)cols / 16; pitch[3] = (size_t)cols / 256 * 2;
+        set({{1, 0, 32}, {0, 32, 64}, {3, 108, 2}}); break;
+    case LLMP_GGML_Q5_K:
+        n = 3; bw = 256; blk_bytes = 176; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 256 * 16;
+        pitch[2] = (size_t)cols / 8;
+        set({{1, 0, 16}, {2, 16, 32}, {0, 48, 128}}); break;
+    case LLMP_GGML_IQ4_NL:
+        n = 2; bw = 32; blk_bytes = 18; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32 * 2;
+        set({{1, 0, 2}, {0, 2, 16}}); break;
+    case LLMP_GGML_IQ4_XS:   // plane 1 (decoded scales) is written below
+        n = 3; bw = 256; blk_bytes = 136; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32;
+        pitch[2] = (size_t)cols / 256 * 2;
+        set({{2, 0, 2}, {0, 8, 128}}); break;
+    case LLMP_GGML_MXFP4:
+        n = 2; bw = 32; blk_bytes = 17; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32;
+        set({{1, 0, 1}, {0, 1, 16}}); break;
     default: return 0;
     }
     if (bw && cols % (int)bw) return 0;
@@ -208,6 +266,10 @@ inline int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
                 std::memcpy(&dst[off[pc.plane] + (size_t)r * pitch[pc.plane] + b * pc.len],
                             blk + pc.src_off, pc.len);
             }
+            if (type == LLMP_GGML_Q3_K)
+                q3k_scales(blk + 96, reinterpret_cast<int8_t*>(&dst[off[2] + (size_t)r * pitch[2] + b * 16]));
+            else if (type == LLMP_GGML_IQ4_XS)
+                iq4xs_scales(blk, reinterpret_cast<int8_t*>(&dst[off[1] + (size_t)r * pitch[1] + b * 8]));
         }
     return n;
 }

@@ -32,7 +32,8 @@ hipError_t launch_tok_prep(const float* x, long long x_pitch, int cols, const fl
 bool proj_tok_supported(int ggml_type) {
     switch (ggml_type) {
     case gk::kF32: case gk::kF16: case gk::kBF16: case gk::kQ8_0: case gk::kQ4_0: case gk::kQ4_K:
-    case gk::kQ6_K:
+    case gk::kQ6_K: case gk::kQ5_0: case gk::kQ3_K: case gk::kQ5_K: case gk::kIQ4_NL: case gk::kIQ4_XS:
+    case gk::kMXFP4:
         return true;
     default:
         return false;
@@ -40,7 +41,9 @@ bool proj_tok_supported(int ggml_type) {
 }
 
 bool proj_tok_pair_supported(int first_type, int second_type) {
-    return first_type == gk::kQ4_K && second_type == gk::kQ6_K;
+    return (first_type == gk::kQ4_K && second_type == gk::kQ6_K) ||
+           (first_type == gk::kQ3_K && second_type == gk::kQ5_K) ||
+           (first_type == gk::kQ5_K && second_type == gk::kQ6_K);
 }
 
 hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_type, hipStream_t st) {
@@ -51,11 +54,15 @@ hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_
         return hipErrorInvalidValue;
     for (int i = 0; i < a.nseg; ++i)
         if (a.seg[i].rows % 16 || a.seg[i].out_off % 16) return hipErrorInvalidValue;
-    const bool kq = first_type == gk::kQ4_K || first_type == gk::kQ6_K || second_type == gk::kQ4_K ||
-                    second_type == gk::kQ6_K;
-    if (kq && a.cols % 256) return hipErrorInvalidValue;
+    // super-block formats need whole super-blocks of 256 columns
+    auto superblock = [](int t) {
+        return t == gk::kQ4_K || t == gk::kQ6_K || t == gk::kQ3_K || t == gk::kQ5_K || t == gk::kIQ4_XS;
+    };
+    if ((superblock(first_type) || superblock(second_type)) && a.cols % 256) return hipErrorInvalidValue;
     if (second_type >= 0) {
         if (!proj_tok_pair_supported(first_type, second_type)) return hipErrorInvalidValue;
+        if (first_type == gk::kQ3_K) return launch_ff<tk::PQ3K, tk::PQ5K>(a, st);
+        if (first_type == gk::kQ5_K) return launch_ff<tk::PQ5K, tk::PQ6K>(a, st);
         return launch_ff<tk::PQ4K, tk::PQ6K>(a, st);
     }
     switch (first_type) {
@@ -66,6 +73,12 @@ hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_
     case gk::kQ4_0: return launch_ff<tk::PQ4_0, tk::PQ4_0>(a, st);
     case gk::kQ4_K: return launch_ff<tk::PQ4K, tk::PQ4K>(a, st);
     case gk::kQ6_K: return launch_ff<tk::PQ6K, tk::PQ6K>(a, st);
+    case gk::kQ5_0: return launch_ff<tk::PQ5_0, tk::PQ5_0>(a, st);
+    case gk::kQ3_K: return launch_ff<tk::PQ3K, tk::PQ3K>(a, st);
+    case gk::kQ5_K: return launch_ff<tk::PQ5K, tk::PQ5K>(a, st);
+    case gk::kIQ4_NL: return launch_ff<tk::PIQ4_NL, tk::PIQ4_NL>(a, st);
+    case gk::kIQ4_XS: return launch_ff<tk::PIQ4_XS, tk::PIQ4_XS>(a, st);
+    case gk::kMXFP4: return launch_ff<tk::PMXFP4, tk::PMXFP4>(a, st);
     default: return hipErrorInvalidValue;
     }
 }

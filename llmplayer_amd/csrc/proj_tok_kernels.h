@@ -283,6 +283,208 @@ struct PQ4_0 {
     }
 };
 
+// Split-nibble 32-blocks (Q5_0, IQ4_NL, MXFP4; gemv_kernels.h): chunk = 4 blocks; lane kq
+// takes columns 8kq .. 8kq+7 of each, the low (kq < 2) or high (kq >= 2) nibbles of bytes
+// 8(kq%2) .. 8(kq%2)+7.  The nibble pair of those 8 bytes.
+__device__ __forceinline__ void split_codes(const uint2& q, int kq, unsigned& c0, unsigned& c1) {
+    const int sh = 4 * (kq >> 1);
+    c0 = (q.x >> sh) & 0x0F0F0F0Fu;
+    c1 = (q.y >> sh) & 0x0F0F0F0Fu;
+}
+// Eight signed bytes (int8 values, exact in fp16) -> one A operand.
+__device__ __forceinline__ uint4 f16x8_of_s8(unsigned c0, unsigned c1) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        v[e] = gk::sbyte_f(c0, e);
+        v[4 + e] = gk::sbyte_f(c1, e);
+    }
+    return f16x8_of(v);
+}
+
+// Q5_0: values q - 16 with the fifth bit of element e at bit e of the block's qh word (for
+// lane kq: bits 8kq .. 8kq+7, low or high nibbles alike).  Table: d of block kq.
+struct PQ5_0 {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 4;
+    static constexpr bool MIN = false, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    struct Raw { uint2 q[4]; unsigned qh[4]; unsigned short d; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int blk = ch * 4 + min(b, ng - 1);
+            r.q[b] = ldo<uint2>(rp(w, 0, row), (unsigned)(blk * 16 + 8 * (kq & 1)));
+            r.qh[b] = ldo<unsigned>(rp(w, 1, row), (unsigned)blk * 4u);
+        }
+        r.d = ldo<unsigned short>(rp(w, 2, row), (unsigned)(ch * 4 + min(kq, ng - 1)) * 2u);
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int) {
+        tab[m * TAB + kq] = h2f(r.d);
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        unsigned c0, c1;
+        split_codes(r.q[gi], kq, c0, c1);
+        const unsigned h = r.qh[gi] >> (8 * kq);
+        c0 = (c0 | (gk::spread4(h & 15u) << 4)) ^ 0x10101010u;          // q ^ 16: 5-bit q - 16
+        c1 = (c1 | (gk::spread4((h >> 4) & 15u) << 4)) ^ 0x10101010u;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = (float)((int)(c0 << (27 - 8 * e)) >> 27);
+            v[4 + e] = (float)((int)(c1 << (27 - 8 * e)) >> 27);
+        }
+        a[0] = f16x8_of(v);
+    }
+};
+
+// IQ4_NL: values codebook[code].  Table: d of block kq.
+struct PIQ4_NL {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 4;
+    static constexpr bool MIN = false, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    struct Raw { uint2 q[4]; unsigned short d; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            r.q[b] = ldo<uint2>(rp(w, 0, row), (unsigned)((ch * 4 + min(b, ng - 1)) * 16 + 8 * (kq & 1)));
+        r.d = ldo<unsigned short>(rp(w, 1, row), (unsigned)(ch * 4 + min(kq, ng - 1)) * 2u);
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int) {
+        tab[m * TAB + kq] = h2f(r.d);
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        unsigned c0, c1;
+        split_codes(r.q[gi], kq, c0, c1);
+        using gk::kIq4;
+        a[0] = f16x8_of_s8(gk::lut16(c0, kIq4[0], kIq4[1], kIq4[2], kIq4[3]),
+                           gk::lut16(c1, kIq4[0], kIq4[1], kIq4[2], kIq4[3]));
+    }
+};
+
+// MXFP4: values 2 FP4[code] (integers), table 2^(e - 128) of block kq.
+struct PMXFP4 {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 4;
+    static constexpr bool MIN = false, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    struct Raw { uint2 q[4]; unsigned char e; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            r.q[b] = ldo<uint2>(rp(w, 0, row), (unsigned)((ch * 4 + min(b, ng - 1)) * 16 + 8 * (kq & 1)));
+        r.e = ldo<unsigned char>(rp(w, 1, row), (unsigned)(ch * 4 + min(kq, ng - 1)));
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int) {
+        tab[m * TAB + kq] = gk::e8m0_half(r.e);
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        unsigned c0, c1;
+        split_codes(r.q[gi], kq, c0, c1);
+        using gk::kFp4x2;
+        a[0] = f16x8_of_s8(gk::lut16(c0, kFp4x2[0], kFp4x2[1], kFp4x2[2], kFp4x2[3]),
+                           gk::lut16(c1, kFp4x2[0], kFp4x2[1], kFp4x2[2], kFp4x2[3]));
+    }
+};
+
+// IQ4_XS: chunk = 4 sub-blocks of 32 (their nibbles are consecutive 16-byte runs, split as the
+// 32-blocks); values codebook[code], table d * (ls - 32) of sub-block kq.
+struct PIQ4_XS {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 4;
+    static constexpr bool MIN = false, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    struct Raw { uint2 q[4]; unsigned char sc; unsigned short d; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            r.q[b] = ldo<uint2>(rp(w, 0, row), (unsigned)((ch * 4 + min(b, ng - 1)) * 16 + 8 * (kq & 1)));
+        const int sbk = ch * 4 + min(kq, ng - 1);
+        r.sc = ldo<unsigned char>(rp(w, 1, row), (unsigned)sbk);
+        r.d = ldo<unsigned short>(rp(w, 2, row), (unsigned)(sbk >> 3) * 2u);
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int) {
+        tab[m * TAB + kq] = h2f(r.d) * (float)(int)(signed char)r.sc;
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        unsigned c0, c1;
+        split_codes(r.q[gi], kq, c0, c1);
+        using gk::kIq4;
+        a[0] = f16x8_of_s8(gk::lut16(c0, kIq4[0], kIq4[1], kIq4[2], kIq4[3]),
+                           gk::lut16(c1, kIq4[0], kIq4[1], kIq4[2], kIq4[3]));
+    }
+};
+
+// Q5_K: PQ4K's chunk with the fifth bits: qh bytes 8kq .. 8kq+7 of the super-block, bit 4h + gi
+// for group gi (sub-block 4h + gi) of chunk half h.
+struct PQ5K {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 8;
+    static constexpr bool MIN = true, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    struct Raw { PQ4K::Raw q4; uint2 qh; int h; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+        PQ4K::load(r.q4, w, row, ch, kq, ng);
+        r.qh = ldo<uint2>(rp(w, 2, row), (unsigned)((ch >> 1) * 32 + 8 * kq));
+        r.h = ch & 1;
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int ch) {
+        PQ4K::table(r.q4, tab, m, kq, ch);
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int) {
+        const uint2 q = r.q4.q[gi >> 1];
+        const int sh = 4 * (gi & 1), hb = 4 * r.h + gi;
+        const unsigned u0 = ((q.x >> sh) & 0x0F0F0F0Fu) | (((r.qh.x >> hb) & 0x01010101u) << 4);
+        const unsigned u1 = ((q.y >> sh) & 0x0F0F0F0Fu) | (((r.qh.y >> hb) & 0x01010101u) << 4);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = (float)((u0 >> (8 * e)) & 0xFF);
+            v[4 + e] = (float)((u1 >> (8 * e)) & 0xFF);
+        }
+        a[0] = f16x8_of(v);
+    }
+};
+
+// Q3_K: chunk = half h = ch%2 of a super-block, group gi = pair p (columns 32p .. 32p+31 of the
+// half): lane kq takes w = kq/2, l = 8(kq%2) .. +7, i.e. qs bytes 32h + 8kq .. +7 (bits 2p, 2p+1)
+// and hmask bytes 8kq .. +7 (bit 4h + p); values q - 4.  Columns 0-15 and 16-31 of a group are
+// sub-blocks 8h + 2p and 8h + 2p + 1, so the A operand goes out twice (as Q6_K's).  Table per
+// row: the decoded factors d * (sc - 32) of the chunk's 8 sub-blocks.
+struct PQ3K {
+    static constexpr int NA = 2, NPAIR = 4, TAB = 8;
+    static constexpr bool MIN = false, HALVES = true;
+    static constexpr PartPair pairs[4] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}};
+    struct Raw { uint2 qs, hm, sc; unsigned short d; int h; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int) {
+        const int sb = ch >> 1, h = ch & 1;
+        r.qs = ldo<uint2>(rp(w, 0, row), (unsigned)(sb * 64 + 32 * h + 8 * kq));
+        r.hm = ldo<uint2>(rp(w, 1, row), (unsigned)(sb * 32 + 8 * kq));
+        r.sc = ldo<uint2>(rp(w, 2, row), (unsigned)(sb * 16 + 8 * h));
+        r.d = ldo<unsigned short>(rp(w, 3, row), (unsigned)sb * 2u);
+        r.h = h;
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int) {
+        // entry kq: sub-blocks 8h + 2kq and 8h + 2kq + 1 (bytes 2kq, 2kq + 1 of the 8)
+        const float d = h2f(r.d);
+        const unsigned wv = kq < 2 ? r.sc.x : r.sc.y;
+        const int i0 = 2 * (kq & 1);
+        reinterpret_cast<float2*>(tab + m * TAB)[kq] =
+            make_float2(d * gk::sbyte_f(wv, i0), d * gk::sbyte_f(wv, i0 + 1));
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        const int hb = 4 * r.h + gi;
+        const unsigned q0 = (((r.qs.x >> (2 * gi)) & 0x03030303u) | (((r.hm.x >> hb) & 0x01010101u) << 2)) ^ 0x04040404u;
+        const unsigned q1 = (((r.qs.y >> (2 * gi)) & 0x03030303u) | (((r.hm.y >> hb) & 0x01010101u) << 2)) ^ 0x04040404u;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = (float)((int)(q0 << (29 - 8 * e)) >> 29);
+            v[4 + e] = (float)((int)(q1 << (29 - 8 * e)) >> 29);
+        }
+        const uint4 u = f16x8_of(v);
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        a[0] = kq < 2 ? u : z;   // columns 0-15: sub-block 8h + 2p
+        a[1] = kq < 2 ? z : u;   // columns 16-31: sub-block 8h + 2p + 1
+    }
+};
+
 // F16 rows: the 8 weights of a lane are its A operand as they are.
 struct PF16 {
     static constexpr int NA = 1, NPAIR = 2, TAB = 0;

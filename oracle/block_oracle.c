@@ -8,7 +8,8 @@
  * (TransformerBlock.java, attention half), and Attention.forward's Q/K/V projections, biases
  * and output projection (Attention.java:76-110, 232-238), over projection weights in the GGUF
  * block formats of the reference's tensor classes (the tensor package's FloatTensor classes):
- *   F32 (0), F16 (1), Q4_0 (2), Q8_0 (8), Q4_K (12), Q6_K (14), BF16 (30)  (GGMLType ids).
+ *   F32 (0), F16 (1), Q4_0 (2), Q5_0 (6), Q8_0 (8), Q3_K (11), Q4_K (12), Q5_K (13),
+ *   Q6_K (14), IQ4_NL (20), IQ4_XS (23), BF16 (30), MXFP4 (39)  (GGMLType ids).
  *
  * Dequantised weights are bit-identical to what each class's dot() stages (or getFloat()
  * returns); a row's dot follows the scalar classes of the java/ tree: F32 one
@@ -32,10 +33,34 @@
 #define ORC_GGML_F32 0
 #define ORC_GGML_F16 1
 #define ORC_GGML_Q4_0 2
+#define ORC_GGML_Q5_0 6
 #define ORC_GGML_Q8_0 8
+#define ORC_GGML_Q3_K 11
 #define ORC_GGML_Q4_K 12
+#define ORC_GGML_Q5_K 13
 #define ORC_GGML_Q6_K 14
+#define ORC_GGML_IQ4_NL 20
+#define ORC_GGML_IQ4_XS 23
 #define ORC_GGML_BF16 30
+#define ORC_GGML_MXFP4 39
+
+/* IQ4_NLFloatTensor.KVALUES_IQ4NL (IQ4_NLFloatTensor.java:25-28), shared by IQ4_XS. */
+static const float kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                        1,    13,   25,  38,  53,  69,  89,  113};
+/* MXFP4FloatTensor.FP4_TABLE (MXFP4FloatTensor.java:39-42): E2M1 values by nibble. */
+static const float fp4_e2m1[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                   -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
+
+/* MXFP4FloatTensor.e8m0ToFloat (MXFP4FloatTensor.java:104-110): 2^(e - 127), 0 for e = 0
+ * and e = 255. */
+static float e8m0_to_f32(int e)
+{
+    if (e == 0 || e == 255) return 0.0f;
+    uint32_t bits = (uint32_t)e << 23;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
 
 /* Float16.toFloat (Float16.java:11-34): sign, exponent and significand moved into float32,
  * subnormals normalised, infinities and NaNs kept. */
@@ -88,9 +113,15 @@ int orc_ggml_block(int type, int *bytes)
     case ORC_GGML_F16: *bytes = 2; return 1;
     case ORC_GGML_BF16: *bytes = 2; return 1;
     case ORC_GGML_Q4_0: *bytes = 18; return 32;
+    case ORC_GGML_Q5_0: *bytes = 22; return 32;
     case ORC_GGML_Q8_0: *bytes = 34; return 32;
+    case ORC_GGML_Q3_K: *bytes = 110; return 256;
     case ORC_GGML_Q4_K: *bytes = 144; return 256;
+    case ORC_GGML_Q5_K: *bytes = 176; return 256;
     case ORC_GGML_Q6_K: *bytes = 210; return 256;
+    case ORC_GGML_IQ4_NL: *bytes = 18; return 32;
+    case ORC_GGML_IQ4_XS: *bytes = 136; return 256;
+    case ORC_GGML_MXFP4: *bytes = 17; return 32;
     default: *bytes = 0; return 0;
     }
 }
@@ -159,6 +190,100 @@ static void dequant_block(int type, const uint8_t *b, float *out)
         }
         break;
     }
+    case ORC_GGML_Q5_0: {   /* Q5_0FloatTensor.getFloat: (quant - 16) * scale, split nibbles */
+        float scale = orc_f16_to_f32(le16(b));
+        uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+        for (int i = 0; i < 32; i++) {
+            int nib = i < 16 ? (b[6 + i] & 0x0F) : ((b[6 + i - 16] >> 4) & 0x0F);
+            int q = nib | (int)(((qh >> i) & 1u) << 4);
+            out[i] = (float)(q - 16) * scale;
+        }
+        break;
+    }
+    case ORC_GGML_Q3_K: {   /* Q3_KFloatTensor.dot: dl = d * (sc - 32), value dl * q */
+        const uint8_t *hm = b, *qs = b + 32, *raw = b + 96;
+        float d = orc_f16_to_f32(le16(b + 108));
+        int sc[16];
+        for (int i = 0; i < 8; i++) {
+            sc[i] = raw[i] & 0x0F;
+            sc[i + 8] = raw[i] >> 4;
+        }
+        for (int i = 0; i < 4; i++) {
+            int v = raw[8 + i];
+            sc[i] |= (v & 3) << 4;
+            sc[i + 4] |= ((v >> 2) & 3) << 4;
+            sc[i + 8] |= ((v >> 4) & 3) << 4;
+            sc[i + 12] |= ((v >> 6) & 3) << 4;
+        }
+        for (int half = 0; half < 2; half++)
+            for (int pair = 0; pair < 4; pair++)
+                for (int w16 = 0; w16 < 2; w16++) {
+                    float dl = d * (float)(sc[half * 8 + pair * 2 + w16] - 32);
+                    for (int l = 0; l < 16; l++) {
+                        int low = (qs[half * 32 + w16 * 16 + l] >> (2 * pair)) & 3;
+                        int hb = (hm[w16 * 16 + l] >> (half * 4 + pair)) & 1;
+                        out[half * 128 + pair * 32 + w16 * 16 + l] = dl * (float)((low | (hb << 2)) - 4);
+                    }
+                }
+        break;
+    }
+    case ORC_GGML_Q5_K: {   /* Q5_KFloatTensor.dot: ds * q - dm, q = nibble | qh bit << 4 */
+        float d = orc_f16_to_f32(le16(b)), dmin = orc_f16_to_f32(le16(b + 2));
+        const uint8_t *sb = b + 4, *qh = b + 16, *qs = b + 48;
+        int sc[8], mn[8];
+        for (int s = 0; s < 8; s++) {
+            if (s < 4) {
+                sc[s] = sb[s] & 0x3F;
+                mn[s] = sb[s + 4] & 0x3F;
+            } else {
+                sc[s] = (sb[s + 4] & 0x0F) | ((sb[s - 4] >> 6) << 4);
+                mn[s] = ((sb[s + 4] >> 4) & 0x0F) | ((sb[s] >> 6) << 4);
+            }
+        }
+        for (int g = 0; g < 4; g++) {
+            float ds0 = d * (float)sc[2 * g], dm0 = dmin * (float)mn[2 * g];
+            float ds1 = d * (float)sc[2 * g + 1], dm1 = dmin * (float)mn[2 * g + 1];
+            for (int l = 0; l < 32; l++) {
+                int q0 = (qs[g * 32 + l] & 0x0F) | (((qh[l] >> (2 * g)) & 1) << 4);
+                int q1 = ((qs[g * 32 + l] >> 4) & 0x0F) | (((qh[l] >> (2 * g + 1)) & 1) << 4);
+                out[g * 64 + l] = ds0 * (float)q0 - dm0;
+                out[g * 64 + 32 + l] = ds1 * (float)q1 - dm1;
+            }
+        }
+        break;
+    }
+    case ORC_GGML_IQ4_NL: {   /* IQ4_NLFloatTensor.dot: scale * KVALUES[nibble], split nibbles */
+        float scale = orc_f16_to_f32(le16(b));
+        for (int i = 0; i < 16; i++) {
+            out[i] = scale * kvalues_iq4nl[b[2 + i] & 0x0F];
+            out[i + 16] = scale * kvalues_iq4nl[(b[2 + i] >> 4) & 0x0F];
+        }
+        break;
+    }
+    case ORC_GGML_IQ4_XS: {   /* IQ4_XSFloatTensor.dot: dl = d * (ls - 32), split nibbles per 32 */
+        float d = orc_f16_to_f32(le16(b));
+        int scales_h = le16(b + 2);
+        for (int ib = 0; ib < 8; ib++) {
+            int sl = b[4 + ib / 2];
+            int low4 = (ib & 1) ? ((sl >> 4) & 0x0F) : (sl & 0x0F);
+            int ls = low4 | (((scales_h >> (2 * ib)) & 3) << 4);
+            float dl = d * (float)(ls - 32);
+            for (int i = 0; i < 16; i++) {
+                int p = b[8 + ib * 16 + i];
+                out[ib * 32 + i] = dl * kvalues_iq4nl[p & 0x0F];
+                out[ib * 32 + 16 + i] = dl * kvalues_iq4nl[(p >> 4) & 0x0F];
+            }
+        }
+        break;
+    }
+    case ORC_GGML_MXFP4: {   /* MXFP4FloatTensor.dot: FP4_TABLE[nibble] * 2^(e - 127), split */
+        float scale = e8m0_to_f32(b[0]);
+        for (int i = 0; i < 16; i++) {
+            out[i] = fp4_e2m1[b[1 + i] & 0x0F] * scale;
+            out[i + 16] = fp4_e2m1[(b[1 + i] >> 4) & 0x0F] * scale;
+        }
+        break;
+    }
     default: break;
     }
 }
@@ -198,6 +323,23 @@ static float row_dot(int type, const uint8_t *row, int cols, const float *x, flo
         return sum;
     }
     float result = 0.0f;                       /* block formats: result += dot(block) */
+    if (type == ORC_GGML_Q5_0) {              /* Q5_0FloatTensor.dot: scale * sequential sum */
+        for (int b = 0; b < cols / n; b++) {
+            const uint8_t *blk = row + (size_t)b * bytes;
+            float scale = orc_f16_to_f32(le16(blk));
+            uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                          ((uint32_t)blk[5] << 24);
+            float sum = 0.0f;
+            for (int j = 0; j < 16; j++) {
+                int q0 = (blk[6 + j] & 0x0F) | (int)(((qh >> j) & 1u) << 4);
+                int q1 = ((blk[6 + j] >> 4) & 0x0F) | (int)(((qh >> (j + 16)) & 1u) << 4);
+                sum += (float)(q0 - 16) * x[b * 32 + j];
+                sum += (float)(q1 - 16) * x[b * 32 + j + 16];
+            }
+            result += scale * sum;
+        }
+        return result;
+    }
     for (int b = 0; b < cols / n; b++) {
         dequant_block(type, row + (size_t)b * bytes, tmp);
         result += orc_dot(tmp, x + b * n, n);

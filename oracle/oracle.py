@@ -441,6 +441,7 @@ def forward_gemma4(cfg: OracleConfig, kcache, vcache, q, k, v, pos, is_swa, qnor
 
 # ---- attention half of a layer over GGUF-format projection weights ----------------------
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 14, 30
+GGML_Q5_0, GGML_Q3_K, GGML_Q5_K, GGML_IQ4_NL, GGML_IQ4_XS, GGML_MXFP4 = 6, 11, 13, 20, 23, 39
 
 
 def f16_to_f32(h: int) -> np.float32:

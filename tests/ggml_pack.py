@@ -4,13 +4,20 @@ the library's repacking), plus the exact float32 values each packed weight stand
 
 Every packer takes the format's fields (scales, mins, quants) and returns (bytes [rows,
 row_bytes] uint8, dequantised values [rows, cols] float32), the values computed in float32
-in the reference's operation order (Q8_0FloatTensor, Q4_0FloatTensor, Q4_KFloatTensor and
-Q6_KFloatTensor dot()).  Random fields give test weights whose dequantised values are known
+in the reference's operation order (the dot() of Q8_0FloatTensor, Q4_0FloatTensor,
+Q4_KFloatTensor, Q6_KFloatTensor, Q3_KFloatTensor, Q5_KFloatTensor, IQ4_NLFloatTensor,
+IQ4_XSFloatTensor and MXFP4FloatTensor; Q5_0FloatTensor.getFloat).  Random fields give test weights whose dequantised values are known
 without running the code under test."""
 import numpy as np
 
 F32 = np.float32
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 14, 30
+GGML_Q5_0, GGML_Q3_K, GGML_Q5_K, GGML_IQ4_NL, GGML_IQ4_XS, GGML_MXFP4 = 6, 11, 13, 20, 23, 39
+
+# the non-linear 4-bit codebook of IQ4_NL and IQ4_XS (GGUF's kvalues_iq4nl)
+IQ4NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], F32)
+# FP4 E2M1 by code: sign bit 3, exponent bits 2-1, mantissa bit 0 (OCP microscaling formats)
+FP4_VALUES = np.array([s * m for s in (1.0, -1.0) for m in (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)], F32)
 
 
 def _f16_bits(x):
@@ -119,6 +126,128 @@ def pack_q6_k(d_bits, sc, q):
     return out.reshape(rows, -1), vals.reshape(rows, -1)
 
 
+def _split_nibbles(idx):
+    """[..., 32] codes -> [..., 16] bytes: code i in the low nibble of byte i, code 16+i in its
+    high nibble (the split order of Q5_0, IQ4_NL, IQ4_XS sub-blocks and MXFP4)."""
+    idx = np.asarray(idx, np.uint8)
+    return (idx[..., :16] & 15) | ((idx[..., 16:] & 15) << 4)
+
+
+def pack_q5_0(d_bits, q):
+    """Blocks of 32 (22 bytes): d fp16, qh (uint32: bit i = bit 4 of element i), 16 bytes of
+    split nibbles.  q [rows, nb*32] in 0..31; value (q - 16) * d."""
+    rows, nb = d_bits.shape
+    qq = np.asarray(q, np.int64).reshape(rows, nb, 32)
+    out = np.zeros((rows, nb, 22), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, nb, 2)
+    qh = ((qq >> 4) & 1) << np.arange(32)
+    out[:, :, 2:6] = qh.sum(-1).astype(np.uint32)[..., None].view(np.uint8).reshape(rows, nb, 4)
+    out[:, :, 6:] = _split_nibbles(qq & 15)
+    vals = ((qq - 16).astype(F32) * _f16_val(d_bits)[..., None]).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_q3_k(d_bits, sc, q):
+    """Super-blocks of 256 (110 bytes): hmask[32], qs[64], 12 bytes of 6-bit scales, d fp16.
+    Element 128h + 32p + 16w + l (h < 2, p < 4, w < 2, l < 16) has its low two bits at bits
+    2p..2p+1 of qs[32h + 16w + l] and its third bit at bit 4h + p of hmask[16w + l]; its
+    sub-block is 8h + 2p + w.  Scale k: low four bits in byte k%8 (k < 8: low nibble, else
+    high), top two bits at bits 2(k/4)..+1 of byte 8 + k%4.  sc [rows, ns, 16] in 0..63, q
+    [rows, ns*256] in 0..7; value (d * (sc - 32)) * (q - 4)."""
+    rows, ns = d_bits.shape
+    qq = np.asarray(q, np.int64).reshape(rows, ns, 2, 4, 2, 16)     # [h][p][w][l]
+    out = np.zeros((rows, ns, 110), np.int64)
+    for h in range(2):
+        for p in range(4):
+            for w in range(2):
+                out[:, :, 32 + 32 * h + 16 * w:32 + 32 * h + 16 * w + 16] |= (qq[:, :, h, p, w] & 3) << (2 * p)
+                out[:, :, 16 * w:16 * w + 16] |= ((qq[:, :, h, p, w] >> 2) & 1) << (4 * h + p)
+    scv = np.asarray(sc, np.int64)
+    for k in range(16):
+        out[:, :, 96 + k % 8] |= (scv[:, :, k] & 15) << (0 if k < 8 else 4)
+        out[:, :, 104 + k % 4] |= ((scv[:, :, k] >> 4) & 3) << (2 * (k // 4))
+    out = out.astype(np.uint8)
+    out[:, :, 108:110] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    d = _f16_val(d_bits)
+    vals = np.zeros((rows, ns, 2, 4, 2, 16), F32)
+    for h in range(2):
+        for p in range(4):
+            for w in range(2):
+                dl = (d * (scv[:, :, 8 * h + 2 * p + w] - 32).astype(F32)).astype(F32)
+                vals[:, :, h, p, w] = (dl[..., None] * (qq[:, :, h, p, w] - 4).astype(F32)).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_q5_k(d_bits, dmin_bits, sc, mn, q):
+    """Super-blocks of 256 (176 bytes): d, dmin fp16, the 12 scale/min bytes of Q4_K, qh[32]
+    (bit 2g + s of byte l = bit 4 of element 64g + 32s + l), qs[128] (byte 32g + l: element
+    64g + l low, 64g + 32 + l high).  q [rows, ns*256] in 0..31; value d*sc*q - dmin*m."""
+    rows, ns = d_bits.shape
+    q5 = np.asarray(q, np.int64)
+    b4, _ = pack_q4_k(d_bits, dmin_bits, sc, mn, q5 & 15)
+    b4 = b4.reshape(rows, ns, 144)
+    out = np.zeros((rows, ns, 176), np.uint8)
+    out[:, :, 0:16] = b4[:, :, 0:16]
+    out[:, :, 48:176] = b4[:, :, 16:144]
+    qq = q5.reshape(rows, ns, 4, 2, 32)                              # [g][s][l]
+    qh = np.zeros((rows, ns, 32), np.int64)
+    for g in range(4):
+        for s_ in range(2):
+            qh |= ((qq[:, :, g, s_] >> 4) & 1) << (2 * g + s_)
+    out[:, :, 16:48] = qh.astype(np.uint8)
+    d = _f16_val(d_bits)[..., None, None, None]
+    dmin = _f16_val(dmin_bits)[..., None, None, None]
+    ds = (d * np.asarray(sc, np.int64).reshape(rows, ns, 4, 2).astype(F32)[..., None]).astype(F32)
+    dm = (dmin * np.asarray(mn, np.int64).reshape(rows, ns, 4, 2).astype(F32)[..., None]).astype(F32)
+    vals = ((ds * qq.astype(F32)).astype(F32) - dm).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_iq4_nl(d_bits, idx):
+    """Blocks of 32 (18 bytes): d fp16, 16 bytes of split nibble codes; value d * codebook."""
+    rows, nb = d_bits.shape
+    ii = np.asarray(idx, np.int64).reshape(rows, nb, 32)
+    out = np.zeros((rows, nb, 18), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, nb, 2)
+    out[:, :, 2:] = _split_nibbles(ii)
+    vals = (_f16_val(d_bits)[..., None] * IQ4NL_VALUES[ii]).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_iq4_xs(d_bits, ls, idx):
+    """Super-blocks of 256 (136 bytes): d fp16, scales_h (uint16: bits 2ib..2ib+1 = top bits of
+    sub-block ib's 6-bit scale), scales_l (4 bytes: low nibble of byte ib/2 for even ib, high
+    for odd), qs[128] (sub-block ib of 32: bytes 16ib .. 16ib+15, split nibbles).  ls [rows,
+    ns, 8] in 0..63; value (d * (ls - 32)) * codebook."""
+    rows, ns = d_bits.shape
+    lsv = np.asarray(ls, np.int64)
+    ii = np.asarray(idx, np.int64).reshape(rows, ns, 8, 32)
+    out = np.zeros((rows, ns, 136), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    sh = (((lsv >> 4) & 3) << (2 * np.arange(8))).sum(-1).astype(np.uint16)
+    out[:, :, 2:4] = sh[..., None].view(np.uint8).reshape(rows, ns, 2)
+    sl = (lsv[..., 0::2] & 15) | ((lsv[..., 1::2] & 15) << 4)
+    out[:, :, 4:8] = sl.astype(np.uint8)
+    out[:, :, 8:] = _split_nibbles(ii).reshape(rows, ns, 128)
+    dl = (_f16_val(d_bits)[..., None] * (lsv - 32).astype(F32)).astype(F32)     # [rows, ns, 8]
+    vals = (dl[..., None] * IQ4NL_VALUES[ii]).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_mxfp4(e, idx):
+    """Blocks of 32 (17 bytes): the E8M0 exponent byte e (scale 2^(e-127); 0 for e = 0 and
+    e = 255), 16 bytes of split FP4 codes; value FP4 * scale."""
+    rows, nb = e.shape
+    ii = np.asarray(idx, np.int64).reshape(rows, nb, 32)
+    ev = np.asarray(e, np.int64)
+    out = np.zeros((rows, nb, 17), np.uint8)
+    out[:, :, 0] = ev.astype(np.uint8)
+    out[:, :, 1:] = _split_nibbles(ii)
+    scale = np.where((ev == 0) | (ev == 255), 0.0, np.exp2((ev - 127).astype(np.float64))).astype(F32)
+    vals = (FP4_VALUES[ii] * scale[..., None]).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
 def random_weights(t, rows, cols, rng, scale=0.05):
     """Random weights of GGML type t with magnitudes around `scale`: (bytes, float32 values)."""
     if t == GGML_F32:
@@ -145,4 +274,29 @@ def random_weights(t, rows, cols, rng, scale=0.05):
         ns = cols // 256
         d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 1024)
         return pack_q6_k(d, rng.integers(-128, 128, (rows, ns, 16)), rng.integers(0, 64, (rows, cols)))
+    if t == GGML_Q5_0:
+        nb = cols // 32
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, nb)) * scale / 8)
+        return pack_q5_0(d, rng.integers(0, 32, (rows, cols)))
+    if t == GGML_Q3_K:
+        ns = cols // 256
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 64)
+        return pack_q3_k(d, rng.integers(0, 64, (rows, ns, 16)), rng.integers(0, 8, (rows, cols)))
+    if t == GGML_Q5_K:
+        ns = cols // 256
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 512)
+        dmin = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 64)
+        return pack_q5_k(d, dmin, rng.integers(0, 64, (rows, ns, 8)), rng.integers(0, 64, (rows, ns, 8)),
+                         rng.integers(0, 32, (rows, cols)))
+    if t == GGML_IQ4_NL:
+        nb = cols // 32
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, nb)) * scale / 64)
+        return pack_iq4_nl(d, rng.integers(0, 16, (rows, cols)))
+    if t == GGML_IQ4_XS:
+        ns = cols // 256
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 2048)
+        return pack_iq4_xs(d, rng.integers(0, 64, (rows, ns, 8)), rng.integers(0, 16, (rows, cols)))
+    if t == GGML_MXFP4:
+        nb = cols // 32
+        return pack_mxfp4(rng.integers(119, 124, (rows, nb)), rng.integers(0, 16, (rows, cols)))
     raise ValueError(t)

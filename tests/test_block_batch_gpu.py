@@ -12,6 +12,8 @@ same bar and no tighter one there); below |ref| = 13 the bar is the plain 1e-4. 
 drawn centred (_centered_q4_k) so the residual stays at a real model's scale.  The K appended
 K/V rows meet the standard bar; every other cache row is unchanged.  The oracle appends its own
 rows as it goes, so later tokens attend to the oracle's rows, as in the reference."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -67,9 +69,10 @@ def _compare_block(got, want, what):
 
 def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=False,
                post=False, pre=True, rscale=0.0, qk=None, q8=False, sinks=None, layer=0,
-               rounds=1):
+               rounds=1, batched=False):
     """`rounds` batched calls of K tokens each, from position pos0 on layer `layer` of c, each
-    token checked against sequential orc.attn_block calls."""
+    token checked against sequential orc.attn_block calls.  batched: also check that the calls
+    took the matrix-core path (no single-token decode launch: the profile counters)."""
     rng = np.random.default_rng(seed)
     lw, bw = _weights(c, dim, types, rng, merged, bias, post, pre)
     bw.residual_scale = rscale
@@ -88,6 +91,8 @@ def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=F
         fp.kv.write(layer, 0, kc, vc)
         fp.setBlockConfig(dim, rscale, _lib.LLMP_INPUT_Q8_1 if q8 else _lib.LLMP_INPUT_F32)
         fp.uploadLayerWeights(layer, lw)
+        if batched:
+            _lib.call("llmp_profile_enable", fp.kv.handle, 1)
         worst = 0.0
         p0 = pos0
         for r in range(rounds):
@@ -110,11 +115,16 @@ def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=F
             # continue from the device's rows
             kc[p0:p0 + K], vc[p0:p0 + K] = gk[p0:p0 + K], gv[p0:p0 + K]
             p0 += K
+        if batched:
+            n, ms = C.c_int(), C.c_double()
+            _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(n), C.byref(ms))
+            assert n.value == 0, f"{what}: {n.value} single-token decode launches"
+            _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_PREFILL_ATTN, C.byref(n), C.byref(ms))
+            assert n.value >= rounds, f"{what}: {n.value} multi-token attention launches"
         dc.log(f"[gpu] block batch {what}: ok, max abs err {worst:.2e}")
 
 
-TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
-         gp.GGML_Q6_K]
+TYPES = tbg.TYPES
 
 
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
@@ -122,7 +132,17 @@ def test_block_batch_every_weight_format(t):
     """Each format's matrix-core path: 5 tokens (a partial token tile) after a 40-row prefix,
     then 3 more."""
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
-    _run_batch(c, 1024, 64, 40, 5, (t, t, t, t), seed=1600 + t, what=NAMES[t], rounds=2)
+    _run_batch(c, 1024, 64, 40, 5, (t, t, t, t), seed=1600 + t, what=NAMES[t], rounds=2, batched=True)
+
+
+@pytest.mark.parametrize("mix", ["q3_k_l", "q5_k_m"])
+def test_block_batch_c3_q3_k_l_and_q5_k_m(mix):
+    """The C3 shape with the Q3_K_L mix (Q3_K q, k; Q5_K v, o) and the Q5_K_M mix (Q5_K q, k, o;
+    Q6_K v): their two-format launches on the matrix cores, 8 tokens after 4000 rows."""
+    types = {"q3_k_l": (gp.GGML_Q3_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_Q5_K),
+             "q5_k_m": (gp.GGML_Q5_K, gp.GGML_Q5_K, gp.GGML_Q6_K, gp.GGML_Q5_K)}[mix]
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    _run_batch(c, 3072, 4096, 4000, 8, types, seed=1650 + len(mix), what=f"C3 {mix}", batched=True)
 
 
 @pytest.mark.parametrize("K,ctx", [(4, 4096), (16, 4096), (4, 32768), (16, 32768)])

@@ -20,8 +20,10 @@ pytestmark = pytest.mark.gpu
 
 F32 = np.float32
 TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
-         gp.GGML_Q6_K]
-NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k"}
+         gp.GGML_Q6_K, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL, gp.GGML_IQ4_XS,
+         gp.GGML_MXFP4]
+NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k", 6: "q5_0",
+         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4"}
 
 
 def _tensor(t, rows, cols, rng, scale=0.05):
@@ -58,11 +60,13 @@ def _weights(c, dim, types, rng, merged=False, bias=False, post=False, pre=True)
 
 
 def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=False, post=False,
-         pre=True, rscale=0.0, qk=None, splits=0, devpos=False, q8=False, sinks=None, layer=0):
+         pre=True, rscale=0.0, qk=None, splits=0, devpos=False, q8=False, sinks=None, layer=0,
+         weights=None):
     """`steps` block calls at positions pos0.. on layer `layer` of c (its window, RoPE table
-    and sinks), each checked against orc.attn_block."""
+    and sinks), each checked against orc.attn_block.  weights: a prepared (layer weights, oracle
+    weights) pair in place of random ones of `types`."""
     rng = np.random.default_rng(seed)
-    lw, bw = _weights(c, dim, types, rng, merged, bias, post, pre)
+    lw, bw = weights if weights is not None else _weights(c, dim, types, rng, merged, bias, post, pre)
     bw.residual_scale = rscale
     bw.q8_1_input = q8
     kv = c.kv_dim
@@ -137,15 +141,45 @@ def test_block_every_weight_format(t):
     _run(c, 1024, 64, 40, 2, (t, t, t, t), seed=600 + t, what=NAMES[t])
 
 
-WIDE = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0]
+WIDE = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q5_0,
+        gp.GGML_IQ4_NL, gp.GGML_MXFP4, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS]
 
 
 @pytest.mark.parametrize("t", WIDE, ids=[NAMES[t] for t in WIDE])
 def test_block_weight_formats_at_width_4096(t):
     """Rows of 4096 columns: 8 unit rounds in registers and a second batch for the 4-weight
-    unit formats (F32, F16, BF16, Q8_0), 8 rounds for Q4_0."""
+    unit formats (F32, F16, BF16, Q8_0), 8 rounds for the 8-weight units (Q4_0, Q5_0, IQ4_NL,
+    MXFP4, Q5_K, IQ4_XS), 4 for Q3_K's 16-weight units."""
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
     _run(c, 4096, 64, 33, 1, (t, t, t, t), seed=900 + t, what=f"{NAMES[t]} width 4096")
+
+
+@pytest.mark.parametrize("dim", [2048, 3072, 8192])
+def test_block_c3_q3_k_l_and_q5_k_m_mixes(dim):
+    """The Q3_K_L mix (Q3_K q and k, Q5_K v and o; q, k and v in one two-format launch) and the
+    Q5_K_M mix (Q5_K q, k, o and Q6_K v), three steps after a 300-row prefix."""
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    _run(c, dim, 512, 300, 3, (gp.GGML_Q3_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_Q5_K),
+         seed=615 + dim // 1024, what=f"Q3_K_L dim {dim}")
+    _run(c, dim, 512, 300, 3, (gp.GGML_Q5_K, gp.GGML_Q5_K, gp.GGML_Q6_K, gp.GGML_Q5_K),
+         seed=625 + dim // 1024, what=f"Q5_K_M dim {dim}")
+
+
+def test_block_iq4_xs_with_q5_k_v_and_mxfp4_extreme_exponents():
+    """IQ4_XS q and k with a Q5_K v (the IQ4_XS mix at GQA 4 and above: two launches), and an
+    MXFP4 output projection whose block exponents include 0, 1 and 255."""
+    c = hfp.ModelConfig(16, 4, 128, 1, rope_freq_base=500000.0)
+    _run(c, 2048, 256, 100, 2, (gp.GGML_IQ4_XS, gp.GGML_IQ4_XS, gp.GGML_Q5_K, gp.GGML_IQ4_XS),
+         seed=670, what="IQ4_XS + Q5_K v")
+    rng = np.random.default_rng(671)
+    lw, bw = _weights(c, 1024, (gp.GGML_MXFP4,) * 4, rng)
+    e = rng.integers(119, 124, (1024, 2048 // 32))
+    e[0, :3] = (0, 1, 255)
+    e[5, 7] = 1
+    wb, _ = gp.pack_mxfp4(e, rng.integers(0, 16, (1024, 2048)))
+    lw.wo = hfp.GgufTensor(gp.GGML_MXFP4, 1024, 2048, wb.reshape(-1))
+    bw.wo = wb
+    _run(c, 1024, 64, 20, 2, None, seed=672, what="MXFP4 special exponents", weights=(lw, bw))
 
 
 def test_block_c3_llama3b_shape_q4_k_m_mix():

@@ -14,8 +14,10 @@ from tests import refmath as rm
 
 F32 = np.float32
 TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
-         gp.GGML_Q6_K]
-NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k"}
+         gp.GGML_Q6_K, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL, gp.GGML_IQ4_XS,
+         gp.GGML_MXFP4]
+NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k", 6: "q5_0",
+         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4"}
 
 
 def test_f16_conversion_matches_ieee_half_for_every_pattern():
@@ -71,6 +73,118 @@ def test_q6_k_quarters_take_their_own_scales():
         h, r = divmod(e, 128)
         c, l = divmod(r, 32)
         assert got[e] == sc[0, 0, 8 * h + l // 16 + 2 * c]
+
+
+def test_q5_0_split_nibbles_and_fifth_bit():
+    # element i < 16: low nibble of byte i; element 16 + i: its high nibble; bit 4 of element
+    # i is bit i of qh; value (q - 16) * d
+    q = np.full((1, 32), 16, np.int64)
+    q[0, 3] = 16 + 5                              # low nibble of byte 3, no fifth bit change
+    q[0, 20] = 1                                  # high nibble of byte 4, fifth bit clear
+    q[0, 31] = 31
+    wb, vals = gp.pack_q5_0(np.array([[0x3C00]], np.uint16), q)
+    assert wb[0, 6 + 3] == (5 | (0 << 4)) and wb[0, 6 + 4] == (0 | (1 << 4))
+    qh = int.from_bytes(bytes(wb[0, 2:6]), "little")
+    assert qh == (0xFFFFFFFF & ~(1 << 20)) & ~0
+    got = orc.dequant_rows(gp.GGML_Q5_0, wb, 1, 32)[0]
+    assert np.array_equal(got, vals[0])
+    want = np.zeros(32, np.float32)
+    want[3], want[20], want[31] = 5, -15, 15
+    assert np.array_equal(got, want)
+
+
+def test_q5_0_row_dot_is_scale_times_the_block_sum():
+    # Q5_0FloatTensor.dot: sum += (q0 - 16) * x[j]; sum += (q1 - 16) * x[j + 16] for j < 16,
+    # then result += scale * sum, block by block
+    rng = np.random.default_rng(7)
+    wb, vals = gp.random_weights(gp.GGML_Q5_0, 1, 64, rng)
+    x = rng.standard_normal(64).astype(F32)
+    blk = wb[0].reshape(2, 22)
+    res = F32(0)
+    for b_ in range(2):
+        d = np.frombuffer(bytes(blk[b_, 0:2]), np.float16)[0].astype(F32)
+        qh = int.from_bytes(bytes(blk[b_, 2:6]), "little")
+        s_ = F32(0)
+        for j in range(16):
+            q0 = (blk[b_, 6 + j] & 15) | (((qh >> j) & 1) << 4)
+            q1 = (blk[b_, 6 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4)
+            s_ = F32(s_ + F32(F32(int(q0) - 16) * x[32 * b_ + j]))
+            s_ = F32(s_ + F32(F32(int(q1) - 16) * x[32 * b_ + j + 16]))
+        res = F32(res + F32(d * s_))
+    assert orc.matmul(gp.GGML_Q5_0, wb, 1, 64, x)[0] == res
+
+
+def test_q3_k_sub_blocks_of_16_take_their_own_scales():
+    # 16 distinct scales, including top bits; code 5 = value +1, so each value is d*(sc-32)
+    sc = np.array([[[0, 1, 17, 30, 33, 40, 47, 48, 15, 16, 31, 32, 49, 55, 62, 63]]])
+    q = np.full((1, 256), 5, np.int64)
+    wb, vals = gp.pack_q3_k(np.array([[0x3C00]], np.uint16), sc, q)
+    got = orc.dequant_rows(gp.GGML_Q3_K, wb, 1, 256)[0]
+    assert np.array_equal(got, vals[0])
+    for j in range(256):
+        h, r = divmod(j, 128)
+        p_, r = divmod(r, 32)
+        w, _ = divmod(r, 16)
+        assert got[j] == sc[0, 0, 8 * h + 2 * p_ + w] - 32, j
+
+
+def test_q3_k_codes_place_their_bits():
+    # code c at element j: low bits at qs[32h + 16w + l] >> 2p, third bit at hmask[16w + l]
+    # bit 4h + p; value (c - 4) with scale 33 (d = 1)
+    sc = np.full((1, 1, 16), 33)
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 8, (1, 256))
+    wb, _ = gp.pack_q3_k(np.array([[0x3C00]], np.uint16), sc, q)
+    got = orc.dequant_rows(gp.GGML_Q3_K, wb, 1, 256)[0]
+    assert np.array_equal(got, (q[0] - 4).astype(F32))
+
+
+def test_q5_k_fifth_bits_and_scales():
+    sc = np.array([[[1, 2, 3, 4, 49, 50, 61, 63]]])
+    mn = np.zeros((1, 1, 8), np.int64)
+    rng = np.random.default_rng(4)
+    q = rng.integers(0, 32, (1, 256))
+    wb, vals = gp.pack_q5_k(np.array([[0x3C00]], np.uint16), np.array([[0x3800]], np.uint16), sc, mn, q)
+    got = orc.dequant_rows(gp.GGML_Q5_K, wb, 1, 256)[0]
+    assert np.array_equal(got, vals[0])
+    assert np.array_equal(got, (np.repeat(sc[0, 0], 32) * q[0]).astype(F32))
+
+
+def test_iq4_nl_codebook_and_split_nibbles():
+    idx = np.arange(32).reshape(1, 32) % 16
+    wb, vals = gp.pack_iq4_nl(np.array([[0x3C00]], np.uint16), idx)
+    got = orc.dequant_rows(gp.GGML_IQ4_NL, wb, 1, 32)[0]
+    assert np.array_equal(got, vals[0])
+    book = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    assert list(got[:16]) == book and list(got[16:]) == book
+    assert wb[0, 2] == (0 | (0 << 4)) and wb[0, 3] == (1 | (1 << 4))
+
+
+def test_iq4_xs_sub_block_scales_and_split_nibbles():
+    ls = np.array([[[0, 31, 32, 33, 47, 48, 62, 63]]])
+    idx = np.full((1, 256), 8)                   # codebook value +1
+    idx[0, 16] = 15                              # sub-block 0, high nibble of byte 0: +113
+    wb, vals = gp.pack_iq4_xs(np.array([[0x3C00]], np.uint16), ls, idx)
+    got = orc.dequant_rows(gp.GGML_IQ4_XS, wb, 1, 256)[0]
+    assert np.array_equal(got, vals[0])
+    for ib in range(8):
+        seg = got[32 * ib:32 * ib + 32]
+        want = np.full(32, ls[0, 0, ib] - 32, F32)
+        if ib == 0:
+            want[16] = (ls[0, 0, 0] - 32) * 113
+        assert np.array_equal(seg, want), ib
+    assert wb[0, 8] == (8 | (15 << 4))
+
+
+def test_mxfp4_scale_exponent_and_special_bytes():
+    idx = np.tile(np.arange(16), 2).reshape(1, 32)
+    for e, scale in ((127, 1.0), (130, 8.0), (120, 2.0 ** -7), (0, 0.0), (255, 0.0), (1, 2.0 ** -126)):
+        wb, vals = gp.pack_mxfp4(np.array([[e]]), idx)
+        got = orc.dequant_rows(gp.GGML_MXFP4, wb, 1, 32)[0]
+        assert np.array_equal(got.view(np.uint32), vals[0].view(np.uint32)), e
+        mags = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+        assert np.array_equal(np.abs(got[:8]), np.array(mags, F32) * F32(scale)), e
+        assert np.all(got[9:16] == -got[1:8]) and np.array_equal(got[16:], got[:16]), e
 
 
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])

@@ -57,7 +57,37 @@ BLOCKS = {
                    {"qs": 0, "d": 1, "dmin": 1, "scales": 1}),
     gp.GGML_Q6_K: (256, [("ql", 128), ("qh", 64), ("scales", 16), ("d", 2)],
                    {"ql": 0, "qh": 1, "scales": 2, "d": 3}),
+    gp.GGML_Q5_0: (32, [("d", 2), ("qh", 4), ("qs", 16)], {"qs": 0, "qh": 1, "d": 2}),
+    gp.GGML_Q3_K: (256, [("hmask", 32), ("qs", 64), ("scales", 12), ("d", 2)],
+                   {"qs": 0, "hmask": 1, "d": 3}),
+    gp.GGML_Q5_K: (256, [("d", 2), ("dmin", 2), ("scales", 12), ("qh", 32), ("qs", 128)],
+                   {"qs": 0, "d": 1, "dmin": 1, "scales": 1, "qh": 2}),
+    gp.GGML_IQ4_NL: (32, [("d", 2), ("qs", 16)], {"qs": 0, "d": 1}),
+    gp.GGML_IQ4_XS: (256, [("d", 2), ("scales_h", 2), ("scales_l", 4), ("qs", 128)], {"qs": 0, "d": 2}),
+    gp.GGML_MXFP4: (32, [("e", 1), ("qs", 16)], {"qs": 0, "e": 1}),
 }
+
+
+def _q3k_scales(parts):
+    # the 16 six-bit scales (low nibbles of bytes 0-7, then their high nibbles; top bit pairs
+    # of bytes 8-11, two bits per scale in groups of four) as the int8 sc - 32
+    raw = parts["scales"].astype(np.int64)
+    low = np.concatenate([raw[..., 0:8] & 15, raw[..., 0:8] >> 4], axis=-1)
+    top = np.concatenate([(raw[..., 8:12] >> (2 * j)) & 3 for j in range(4)], axis=-1)
+    return ((low | (top << 4)) - 32).astype(np.int8).view(np.uint8)
+
+
+def _iq4xs_scales(parts):
+    sh = parts["scales_h"].astype(np.int64)
+    sh = sh[..., 0] | (sh[..., 1] << 8)
+    sl = parts["scales_l"].astype(np.int64)
+    low = np.stack([sl[..., ib // 2] >> (4 * (ib % 2)) & 15 for ib in range(8)], axis=-1)
+    top = np.stack([(sh >> (2 * ib)) & 3 for ib in range(8)], axis=-1)
+    return ((low | (top << 4)) - 32).astype(np.int8).view(np.uint8)
+
+
+# planes computed from a block's fields rather than copied from it
+DERIVED = {gp.GGML_Q3_K: {2: _q3k_scales}, gp.GGML_IQ4_XS: {1: _iq4xs_scales}}
 DENSE = {gp.GGML_F32: 4, gp.GGML_F16: 2, gp.GGML_BF16: 2}
 
 
@@ -74,15 +104,21 @@ def _expected_planes(t, rows, cols, raw):
         parts[name] = blk[:, :, o:o + n]
         o += n
     planes = []
-    for p in range(max(plane_of.values()) + 1):
-        sel = [parts[name] for name, _ in fields if plane_of[name] == p]
+    derived = DERIVED.get(t, {})
+    for p in range(max(list(plane_of.values()) + list(derived)) + 1):
+        if p in derived:
+            planes.append(derived[p](parts).reshape(rows, -1))
+            continue
+        sel = [parts[name] for name, _ in fields if plane_of.get(name) == p]
         planes.append(np.concatenate(sel, axis=2).reshape(rows, -1))
     return planes
 
 
-CASES = [(t, rows, cols) for t in (gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0)
+CASES = [(t, rows, cols) for t in (gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0,
+                                  gp.GGML_Q5_0, gp.GGML_IQ4_NL, gp.GGML_MXFP4)
          for rows, cols in ((1, 32), (3, 96), (17, 2880))] + \
-        [(t, rows, cols) for t in (gp.GGML_Q4_K, gp.GGML_Q6_K) for rows, cols in ((1, 256), (5, 768), (33, 3072))]
+        [(t, rows, cols) for t in (gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS)
+         for rows, cols in ((1, 256), (5, 768), (33, 3072))]
 
 
 def test_repack_matches_the_gguf_block_layouts(driver):
