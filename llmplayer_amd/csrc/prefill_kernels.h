@@ -219,21 +219,47 @@ inline size_t prefill_append_lds(int Hkv, int D) {
 }
 
 // ---- LDS tile layout (also the workspace image of a tile) -------------------------------------
-// LDS tile: K hi/lo [TK keys][D + 8] fp16, V^T hi/lo [D][TK + 8] (row padding spreads banks).
-// Within each 32-key chunk of a V^T row the keys are stored in the order the P V MFMA takes
-// them (vt_group_pos): the 8 keys {4q..4q+3, 16+4q..16+4q+3} a lane group q feeds to one MFMA
-// are contiguous, so a lane reads its A operand with one 16-byte load.
+// LDS tile: K hi/lo [TK keys][D] fp16, V^T hi/lo [D][TK] fp16, then one flag word.  Within
+// each 32-key chunk of a V^T row the keys are stored in the order the P V MFMA takes them
+// (vt_group_pos): the 8 keys {4q..4q+3, 16+4q..16+4q+3} a lane group q feeds to one MFMA are
+// contiguous, so a lane reads its A operand with one 16-byte load.
+//
+// Bank conflicts.  The MFMA operand reads are ds_read_b128 of 16 rows x 4 consecutive 16-byte
+// chunks (lane l: row l%16, chunk 4s + l/16).  On gfx950 the LDS serves such a read in 4
+// cycles of 16 lanes over 64 four-byte banks; a cycle takes the lanes of one half-wave whose
+// 4-lane quad index (bits 2-4 of the lane) has a given parity (measured with
+// SQ_LDS_BANK_CONFLICT: lanes 0-3, 12-15, 20-23 and 24-27 share a cycle).  With 16-byte row
+// padding the 16 rows of a cycle collide in pairs (every read took 8 cycles instead of 4).
+// Instead the chunk index of a row is XOR-ed with the row (koff / voff): rows of 8 or more
+// chunks with r mod min(chunks, 16), the 4-chunk V^T rows of 32-key tiles with (r/2) mod 4,
+// which spreads each cycle's 16 reads over all 64 banks; no padding.  head_dim 96 (12 chunks, not
+// a power of two) keeps a padded pitch of 14 chunks, which is conflict-free as well.
 template <int D, int TKEYS = tile_keys<D>()>
 struct alignas(16) TileLds {
     static constexpr int TK = TKEYS;
-    static constexpr int KP = D + 8;   // K row pitch (fp16 elements; 16-byte multiple)
-    // V^T row pitch: TK + 8 fp16 = TK/2 + 4 dwords, 4 dwords past a multiple of 32 (TK is 32 or
-    // 64), so 8 consecutive dims' 16-byte reads cover the 32 banks once.
-    static constexpr int VP = TK + 8;
+    static constexpr int KCH = D / 8;                          // 16-byte chunks of a K row
+    static constexpr bool KSWZ = (KCH & (KCH - 1)) == 0;
+    static constexpr int KP = KSWZ ? D : D + 16;               // K row pitch (fp16 elements)
+    static constexpr int VCH = TK / 8;                         // 16-byte chunks of a V^T row
+    static constexpr int VP = TK;                              // V^T row pitch
     unsigned short kh[TK * KP];
     unsigned short kl[TK * KP];
     unsigned short vh[D * VP];
     unsigned short vl[D * VP];
+    // flag[0] (set by the image builder): nonzero when some V lo part of the tile exceeds
+    // 2^-24 in magnitude; the other words are unused.
+    unsigned flag[4];
+    // Offset (fp16 elements) of element e of K row r, and of element e of V^T row d.
+    static __device__ __forceinline__ int koff(int r, int e) {
+        if constexpr (KSWZ)
+            return r * KP + ((((e >> 3) ^ (r & (KCH >= 16 ? 15 : KCH - 1))) << 3) | (e & 7));
+        else
+            return r * KP + e;
+    }
+    static __device__ __forceinline__ int voff(int d, int e) {
+        const int sw = VCH >= 8 ? (d & 7) : ((d >> 1) & (VCH - 1));
+        return d * VP + ((((e >> 3) ^ sw) << 3) | (e & 7));
+    }
 };
 
 // ---- 2. Tile images ----------------------------------------------------------------------------
@@ -274,12 +300,9 @@ __device__ __forceinline__ int vt_keys_off(int rq) { return 32 * (rq >> 3) + vt_
 
 template <int D>
 constexpr int tile_img_u4() { return (int)(sizeof(TileLds<D>) / 16); }
-// A tile image carries one flag in the padding of its first K row (kh[D], never read as a
-// key): nonzero when some V lo part exceeds 2^-24 in magnitude.  Where it is zero the P V
-// product drops its V-lo MFMA: the terms it would add are below 2^-24 * sum(P) / l <= 2^-24
-// of the output.  16-byte chunk and dword of the flag within the image:
-template <int D>
-constexpr int vlo_flag_chunk() { return D / 8; }
+// A tile image carries one flag (TileLds::flag): nonzero when some V lo part exceeds 2^-24 in
+// magnitude.  Where it is zero the P V product drops its V-lo MFMA: the terms it would add are
+// below 2^-24 * sum(P) / l <= 2^-24 of the output.
 
 // One KV head's rows in the cache: fp32 rows (f), or Q8_0 quants (q) and block scales (s).
 struct HeadRows {
@@ -354,11 +377,11 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
     const HeadRows kr = k_rows<Q8>(a, kvh), vr = v_rows<Q8>(a, kvh);
     const float fk = pow2i(-a.range[2 * kvh]), fv = pow2i(-a.range[2 * kvh + 1]);
     // K rows: work item (row r, dims 4*c4 .. 4*c4+3), c4 fastest across lanes, so the loads
-    // are row-contiguous and the 8-byte stores of 16 lanes cover the 32 banks once.
+    // are row-contiguous and the 8-byte stores of 16 lanes fill one image row.
     // V^T: work item (keys 4*rq .. 4*rq+3, dims 4*c4 .. 4*c4+3), rq fastest across lanes: each
     // dim row gets the 4 keys as one 8-byte store, and the TK/4 lanes that share a dim chunk
-    // write one V^T row's TK keys together (no bank conflicts); a load instruction reads
-    // 64/(TK/4) consecutive 16-byte chunks of TK/4 rows.
+    // write one V^T row's TK keys together; a load instruction reads 64/(TK/4) consecutive
+    // 16-byte chunks of TK/4 rows.
     // Every global load of a thread is issued before any of its math (one memory round trip).
     constexpr int KI = TK * (D / 4) / NTHR, VI = (TK / 4) * (D / 4) / NTHR;
     static_assert(KI * NTHR == TK * (D / 4) && VI * NTHR == (TK / 4) * (D / 4),
@@ -385,8 +408,8 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
         unsigned h0, l0, h1, l1;
         split_pair(x[0], x[1], h0, l0);
         split_pair(x[2], x[3], h1, l1);
-        *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
-        *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
+        *reinterpret_cast<uint2*>(&t.kh[T::koff(r, 4 * c4)]) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(&t.kl[T::koff(r, 4 * c4)]) = make_uint2(l0, l1);
     }
     bool vlo = false;
 #pragma unroll
@@ -402,13 +425,12 @@ __global__ __launch_bounds__(NTHR) void prefill_tile_kernel(PrefillArgs a, uint4
             split_pair(vv[2][u], vv[3][u], h1, l1);
             vlo = vlo || lo_significant(l0) || lo_significant(l1);
             const int d = 4 * c4 + u;
-            *reinterpret_cast<uint2*>(&t.vh[d * T::VP + vt_keys_off(rq)]) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2*>(&t.vl[d * T::VP + vt_keys_off(rq)]) = make_uint2(l0, l1);
+            *reinterpret_cast<uint2*>(&t.vh[T::voff(d, vt_keys_off(rq))]) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(&t.vl[T::voff(d, vt_keys_off(rq))]) = make_uint2(l0, l1);
         }
     }
-    // The flag word sits in the padding of K row 0 (kh[D], kh[D + 1]), which no chunk covers.
     const unsigned any_vlo = __syncthreads_or(vlo ? 1 : 0) ? 1u : 0u;
-    if (tid == 0) reinterpret_cast<uint4*>(&t)[vlo_flag_chunk<D>()].x = any_vlo;
+    if (tid == 0) t.flag[0] = any_vlo;
 }
 
 // ---- 3. Double-buffered MFMA attention ------------------------------------------------------
@@ -627,8 +649,8 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
             unsigned h0, l0, h1, l1;
             split_pair(x[0], x[1], h0, l0);
             split_pair(x[2], x[3], h1, l1);
-            *reinterpret_cast<uint2*>(&t.kh[r * T::KP + 4 * c4]) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2*>(&t.kl[r * T::KP + 4 * c4]) = make_uint2(l0, l1);
+            *reinterpret_cast<uint2*>(&t.kh[T::koff(r, 4 * c4)]) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2*>(&t.kl[T::koff(r, 4 * c4)]) = make_uint2(l0, l1);
         }
     }
 #pragma unroll
@@ -644,8 +666,8 @@ __device__ __forceinline__ void raw_store(const floatx4 (&kx)[KI], const floatx4
                 split_pair(vv[0][u], vv[1][u], h0, l0);
                 split_pair(vv[2][u], vv[3][u], h1, l1);
                 const int d = 4 * c4 + u;
-                *reinterpret_cast<uint2*>(&t.vh[d * T::VP + vt_keys_off(rq)]) = make_uint2(h0, h1);
-                *reinterpret_cast<uint2*>(&t.vl[d * T::VP + vt_keys_off(rq)]) = make_uint2(l0, l1);
+                *reinterpret_cast<uint2*>(&t.vh[T::voff(d, vt_keys_off(rq))]) = make_uint2(h0, h1);
+                *reinterpret_cast<uint2*>(&t.vl[T::voff(d, vt_keys_off(rq))]) = make_uint2(l0, l1);
             }
         }
     }
@@ -806,8 +828,9 @@ void prefill_attn2_kernel(PrefillArgs a,
             const int krow = kt * 16 + col;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                const f16x8 kh = *reinterpret_cast<const f16x8*>(&t.kh[krow * T::KP + 32 * s + 8 * grp]);
-                const f16x8 kl = *reinterpret_cast<const f16x8*>(&t.kl[krow * T::KP + 32 * s + 8 * grp]);
+                const int ko = T::koff(krow, 32 * s + 8 * grp);
+                const f16x8 kh = *reinterpret_cast<const f16x8*>(&t.kh[ko]);
+                const f16x8 kl = *reinterpret_cast<const f16x8*>(&t.kl[ko]);
 #pragma unroll
                 for (int hh = 0; hh < HPW; ++hh) {
                     acc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[hh][s], acc[hh], 0, 0, 0);
@@ -879,7 +902,7 @@ void prefill_attn2_kernel(PrefillArgs a,
         // Tiles whose V lo parts are all within 2^-24 (rows written from bf16 inputs) skip the
         // V-lo MFMA and its LDS reads.  Direct staging does not flag its tiles.
         const bool tile_vlo =
-            DIRECT || __builtin_amdgcn_readfirstlane(*reinterpret_cast<const int*>(&t.kh[D])) != 0;
+            DIRECT || __builtin_amdgcn_readfirstlane(t.flag[0]) != 0;
         auto pv = [&](auto has_lo) {
             constexpr bool HL = decltype(has_lo)::value;
 #pragma unroll
@@ -899,14 +922,15 @@ void prefill_attn2_kernel(PrefillArgs a,
             for (int d = 0; d < DT; ++d) {
                 const int dim = d * 16 + col;
                 const int k0 = 32 * c + 8 * grp;   // keys {32c+4grp..+3, 32c+16+4grp..+3}
-                const f16x8 vh = *reinterpret_cast<const f16x8*>(&t.vh[dim * T::VP + k0]);
+                const int vo = T::voff(dim, k0);
+                const f16x8 vh = *reinterpret_cast<const f16x8*>(&t.vh[vo]);
 #pragma unroll
                 for (int hh = 0; hh < HPW; ++hh) {
                     o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[hh], o[hh][d], 0, 0, 0);
                     o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[hh], o[hh][d], 0, 0, 0);
                 }
                 if constexpr (HL) {
-                    const f16x8 vl = *reinterpret_cast<const f16x8*>(&t.vl[dim * T::VP + k0]);
+                    const f16x8 vl = *reinterpret_cast<const f16x8*>(&t.vl[vo]);
 #pragma unroll
                     for (int hh = 0; hh < HPW; ++hh)
                         o[hh][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[hh], o[hh][d], 0, 0, 0);
