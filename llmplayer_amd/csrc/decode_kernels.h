@@ -396,6 +396,7 @@ __device__ __forceinline__ void load_args_now(const DecodeArgs& a) {
                  "s"(a.kv_rep));
 }
 
+
 // 1/rms of D values in the order of RMSNorm.apply with offsets (RMSNorm.java:24-35, the
 // Gemma 4 engine's QK-norm and V-norm): one thread sums the squares sequentially, unfused,
 // then r = 1/(float)sqrt(ss/D + eps).
@@ -1059,8 +1060,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
 // ---- Q8_0 cache, scores on the matrix cores --------------------------------------------------
 // The same split-K decode over a Q8_0 cache (GQA groups of up to 4 query heads), with the
 // scores as int8 matrix products: per 16-key tile and 32-dim scale block, one
-// v_mfma_i32_16x16x32_i8 multiplies the tile's K quants (B operand, read straight from the
-// cache) by the query's int8 parts (A operand).  Each (query head, block) of the scaled query
+// v_mfma_i32_16x16x64_i8 multiplies the tile's K quants (B operand, read straight from the
+// cache) by the query's int8 parts (A operand).  Up to head_dim 128 the 64-deep product
+// covers two scale blocks of K (a lane's B operand is 16 contiguous quants: dims
+// 64p + 16(l/16) .. +15), and the A operand of block 2p carries the query parts in lane groups
+// 0-1 only, that of block 2p+1 in groups 2-3 only, so each product is one block's dot
+// product: the 16-byte loads halve the K load instructions of a tile against four 8-byte
+// pieces 32 bytes apart.  At head_dim 256 the two zero-padded operands per pair cost the
+// registers of an occupancy step, and a v_mfma_i32_16x16x32_i8 per block takes the 8-byte
+// pieces (dims 32b + 8(l/16) .. +7).  Each (query head, block) of the scaled query
 // is held as q = s * (Q1 + (Q2 + Q3/F)/F) with s = max|q|/127 and F = 254, Q1..Q3 int8, which
 // represents q to 2^-23 of the block maximum; the three integer dot products with the quants
 // are exact, so a score  sum_b ks_b * s_b * (D1 + (D2 + D3/F)/F)  rounds at the fp32 level of
@@ -1092,7 +1100,10 @@ struct Q8Tile {
     static constexpr int LPR = D / 16;    // V lanes per key (16 quants each)
     static constexpr int KPL = 64 / LPR;  // keys per wave-wide V load
     static constexpr int UV = 16 / KPL;   // V loads per tile
-    uint2 k[NB];   // K quants of key l%16, dims 32b + 8(l/16) .. +7 (MFMA B operand)
+    static constexpr int NP = D / 64;     // 64-dim pairs of scale blocks
+    static constexpr bool K64 = D <= 128; // 16x16x64 products (else one 16x16x32 per block)
+    uint4 k[K64 ? NP : 1];    // K64: quants of key l%16, dims 64p + 16(l/16) .. +15
+    uint2 k8[K64 ? 1 : NB];   // else: dims 32b + 8(l/16) .. +7
     float ks[NB];  // K block scales of key l%16
     uint4 v[UV];   // V quants of key u*KPL + l/LPR, dims 16(l%LPR) .. +15
     float vs[UV];  // its V block scale
@@ -1105,9 +1116,15 @@ __device__ __forceinline__ void q8_tile_load(Q8Tile<D>& t, const signed char* kq
                                              int last, int lane) {
     using T = Q8Tile<D>;
     const int kr = min(t0 + (lane & 15), last);
-    const signed char* krow = kq + (long long)kr * D + 8 * (lane >> 4);
+    if constexpr (T::K64) {
+        const signed char* krow = kq + (long long)kr * D + 16 * (lane >> 4);
 #pragma unroll
-    for (int b = 0; b < T::NB; ++b) t.k[b] = load_u2<NT>(reinterpret_cast<const uint2*>(krow + 32 * b));
+        for (int p = 0; p < T::NP; ++p) t.k[p] = load_u4<NT>(reinterpret_cast<const uint4*>(krow + 64 * p));
+    } else {
+        const signed char* krow = kq + (long long)kr * D + 8 * (lane >> 4);
+#pragma unroll
+        for (int b = 0; b < T::NB; ++b) t.k8[b] = load_u2<NT>(reinterpret_cast<const uint2*>(krow + 32 * b));
+    }
     const float* ksr = ks + (long long)kr * T::NB;
     if constexpr (T::NB % 4 == 0) {
 #pragma unroll
@@ -1167,11 +1184,26 @@ __device__ __forceinline__ void q8_query_split(const float* x, float qk_scale, s
     }
 }
 
-// The lane's A operands (one per 32-dim block): row l%16 = (head (l%16)/4, part l%4), dims
-// 32b + 8(l/16) .. +7.  Rows of absent heads and part 3 are zero.
+// The lane's A operands, row l%16 = (head (l%16)/4, part l%4); rows of absent heads and
+// part 3 are zero.  16x16x64 (D <= 128): two per 64-dim pair p, dims 64p + 16(l/16) .. +15,
+// held in aq0[p] by lane groups 0-1 (block 2p) and in aq1[p] by groups 2-3 (block 2p+1), zero
+// elsewhere.  16x16x32: one per block b in aq8[b], dims 32b + 8(l/16) .. +7.
 template <int D, int G>
 __device__ __forceinline__ void q8_query_operands(const signed char* parts, int lane,
-                                                  long (&aq)[D / 32]) {
+                                                  v4i_t (&aq0)[D / 64], v4i_t (&aq1)[D / 64]) {
+    const int row = lane & 15, h = row >> 2, part = row & 3, g = lane >> 4;
+    const bool live = h < G && part < 3;
+    const signed char* src = parts + (live ? part * G * D + h * D : 0) + 16 * g;
+    const v4i_t z = {0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < D / 64; ++p) {
+        const v4i_t w = *reinterpret_cast<const v4i_t*>(src + 64 * p);
+        aq0[p] = (live && g < 2) ? w : z;
+        aq1[p] = (live && g >= 2) ? w : z;
+    }
+}
+template <int D, int G>
+__device__ __forceinline__ void q8_query_operands8(const signed char* parts, int lane, long (&aq)[D / 32]) {
     const int row = lane & 15, h = row >> 2, part = row & 3;
     const bool live = h < G && part < 3;
     const signed char* src = parts + (live ? part * G * D + h * D : 0) + 8 * (lane >> 4);
@@ -1268,8 +1300,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
     prep_heads_lds<D, NTHR>(s_x, G, G, s_acc, s_r, hl, tid);
     q8_query_split<D, G, NTHR>(s_x, a.qk_scale, s_qp, s_qs, tid);
     __syncthreads();
-    long aq[NB];
-    q8_query_operands<D, G>(s_qp, lane, aq);
+    v4i_t aq0[T::K64 ? T::NP : 1], aq1[T::K64 ? T::NP : 1];
+    long aq8[T::K64 ? 1 : NB];
+    if constexpr (T::K64)
+        q8_query_operands<D, G>(s_qp, lane, aq0, aq1);
+    else
+        q8_query_operands8<D, G>(s_qp, lane, aq8);
     const int qh = lane >> 4;  // head of the lane's scores
     float sq[NB];
 #pragma unroll
@@ -1288,9 +1324,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
     auto consume = [&](const T& t, int base, int end) {
         float s = 0.0f;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                aq[b], __builtin_bit_cast(long, t.k[b]), v4i_t{0, 0, 0, 0}, 0, 0, 0);
+        for (int b = 0; b < NB; ++b) {   // blocks in order
+            v4i_t d;
+            if constexpr (T::K64)
+                d = __builtin_amdgcn_mfma_i32_16x16x64_i8((b & 1) ? aq1[b >> 1] : aq0[b >> 1],
+                                                          __builtin_bit_cast(v4i_t, t.k[b >> 1]),
+                                                          v4i_t{0, 0, 0, 0}, 0, 0, 0);
+            else
+                d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq8[b], __builtin_bit_cast(long, t.k8[b]),
+                                                          v4i_t{0, 0, 0, 0}, 0, 0, 0);
             const float f = (float)d[0] + ((float)d[1] + (float)d[2] * kQPartInvF) * kQPartInvF;
             s = __builtin_fmaf(f, t.ks[b] * sq[b], s);
         }
@@ -1366,12 +1408,19 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
         if (wave == 0) {
             T t;
             const bool k0 = (lane & 15) == 0;
+            if constexpr (T::K64) {
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                t.k[b] = k0 ? *reinterpret_cast<const uint2*>(s_kq + 32 * b + 8 * (lane >> 4))
-                            : make_uint2(0u, 0u);
-                t.ks[b] = k0 ? s_ks[b] : 0.0f;
+                for (int p = 0; p < T::NP; ++p)
+                    t.k[p] = k0 ? *reinterpret_cast<const uint4*>(s_kq + 64 * p + 16 * (lane >> 4))
+                                : make_uint4(0u, 0u, 0u, 0u);
+            } else {
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    t.k8[b] = k0 ? *reinterpret_cast<const uint2*>(s_kq + 32 * b + 8 * (lane >> 4))
+                                 : make_uint2(0u, 0u);
             }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) t.ks[b] = k0 ? s_ks[b] : 0.0f;
             const bool v0 = lane < LPR;
             t.v[0] = v0 ? *reinterpret_cast<const uint4*>(s_vq + 16 * lane) : make_uint4(0u, 0u, 0u, 0u);
             t.vs[0] = v0 ? s_vs[lane >> 1] : 0.0f;

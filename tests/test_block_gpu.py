@@ -314,7 +314,7 @@ def test_block_error_codes():
         assert _lib.status("llmp_attn_block", h, 0, 3, 0, x, 0, 0) == 1               # no weights yet
         w = np.zeros(512 * 512 * 4, np.uint8)
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 128, 512, w.ctypes.data, 128 * 512 * 4) == 1  # rows != q_dim
-        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 13, 512, 512, w.ctypes.data, 512 * 176 // 256 * 512) == 6  # Q5_K: no kernel
+        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 10, 512, 512, w.ctypes.data, 512 * 84 // 256 * 512) == 6  # Q2_K: no kernel
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 512, 512, w.ctypes.data, 100) == 1   # byte count
         assert _lib.status("llmp_layer_weight", h, 0, 11, 0, 1, 512, w.ctypes.data, 2048) == 1  # bad slot
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_ATTN_NORM, 8, 1, 512, w.ctypes.data, 2048) == 1  # vector not fp32
