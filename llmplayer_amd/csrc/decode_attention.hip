@@ -131,6 +131,16 @@ __global__ void copy_kernel(float4* __restrict__ dst, const float4* __restrict__
 
 bool decode_shape_supported(int head_dim, int group) { return decode_group_ok(head_dim, group); }
 
+// Measured on MI355X (graph replays, µs per layer-call, combine kernel -> merge in the split
+// kernel): C1 pos 511 (16 splits x 2 waves) 8.2 -> 7.2, C3 ctx 32768 (24 x 8) 45.5 -> 45.0,
+// but C2 ctx 1024 / 4096 (32 x 4) 8.3 -> 9.1 / 12.4 -> 12.6: with 4-wave workgroups the
+// combine kernel stays.
+bool decode_fused_merge(int head_dim, int group, int waves, int splits) {
+    const int nthr = waves * 64, nc = group * head_dim / 4;
+    const int np = nthr >= nc ? nthr / nc : 1;
+    return splits > 1 && waves != 4 && (splits + np - 1) / np <= dk::kMergeBatch;
+}
+
 int decode_split_waves(int head_dim, int group, int waves, bool q8) {
     return resolve_split(head_dim, group, waves, q8).waves;
 }

@@ -395,6 +395,157 @@ __device__ __forceinline__ void load_args_now(const DecodeArgs& a) {
     asm volatile("" ::"s"(a.softcap), "s"(a.softcap_log2e), "s"(a.inv_softcap), "s"(a.range),
                  "s"(a.kv_rep));
 }
+// The merge arguments too (the kernel instances that can merge their splits).
+__device__ __forceinline__ void load_merge_args_now(const DecodeArgs& a) {
+    asm volatile("" ::"s"(a.done), "s"(a.fused));
+}
+
+// ---- merge of the splits, in the split kernel ------------------------------------------------
+// A call with S > 1 splits leaves every workgroup's partial state (unnormalised o, max, sum)
+// of its G query heads in part_o / part_ml.  With DecodeArgs::fused the workgroup that
+// finishes last per virtual KV head merges them and writes the output (no second launch); the
+// host fuses only where that merge is one round of loads and measured faster than
+// decode_reduce_kernel's launch (decode_fused_merge): with more splits per thread group the
+// last workgroup's rounds of loads from the coherence point cost more (C3 at 4k, 16 splits
+// per group: 13.2 -> 15.5 us per layer-call; at 32k, 24 splits of 8-wave workgroups in 5
+// groups: 45.5 -> 45.0 us).  The workgroups of a KV head
+// may run on different XCDs, each with its own L2, so the partials move through the device's
+// coherence point: they are written and read with agent-scope relaxed atomic accesses (stores
+// and loads that bypass the non-coherent L2 state, 4 or 8 bytes each).  A workgroup waits for
+// its partial stores to complete before it counts itself done on the KV head's counter; the
+// one that brings the count to S has observed every other workgroup's count, issued after
+// their stores completed, so its loads see all partials.  It re-arms the counter for the next
+// call.  (A device-scope fence per workgroup instead would write back the whole L2 of each
+// workgroup's XCD: measured 13 -> 35 us per C3 layer-call at 4k.)
+//
+// The merge is the log-sum-exp combine of decode_reduce_kernel: per float4 column of the G
+// heads, the splits are taken in NP groups of threads (group p: splits p, p + NP, ..., the
+// first kMergeBatch of them loaded at once, any further merged online), and the groups' states
+// are merged through LDS.  `scratch`: LDS of at least combine_scratch_floats<NTHR>() floats that
+// the caller no longer reads.
+constexpr int kMergeBatch = 8;
+template <int NTHR>
+constexpr int combine_scratch_floats() { return 6 * NTHR; }   // float4 o + float2 (m, l) per thread
+
+__device__ __forceinline__ void store_partial(float* p, float v, int fused) {
+    if (fused)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+__device__ __forceinline__ float2 load_partial2(const float* p) {   // 8-byte aligned
+    const unsigned long long u = __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p),
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_bit_cast(float2, u);
+}
+
+template <int D, int G, int NTHR>
+__device__ __forceinline__ void combine_if_last(const DecodeArgs& a, int vkh, int S, int tid,
+                                                float* scratch) {
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this thread's partial stores completed
+    __syncthreads();
+    if (tid == 0) {
+        s_last = __hip_atomic_fetch_add(a.done + vkh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+        if (s_last) __hip_atomic_store(a.done + vkh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    constexpr int NC = G * D / 4;                      // float4 columns of the G heads
+    constexpr int NP = NTHR >= NC ? NTHR / NC : 1;     // split groups
+    const int h0 = vkh * G;
+    float4* s_o = reinterpret_cast<float4*>(scratch);                 // [NP][NC]
+    float2* s_ml = reinterpret_cast<float2*>(scratch + 4 * NTHR);     // [NP][NC]
+    // One column c over the splits p, p + NP, ...: (m, l, o).
+    auto merge_col = [&](int c, int p, float& m, float& l, float4& o) {
+        const int h = c / (D / 4), c4 = c - h * (D / 4);
+        const long long slot0 = (long long)vkh * S * G + h;   // split j: slot0 + j*G
+        m = kNegBig;
+        l = 0.0f;
+        o = make_float4(0.f, 0.f, 0.f, 0.f);
+        float2 mlj[kMergeBatch], oa[kMergeBatch], ob[kMergeBatch];
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const int jj = p + u * NP;
+            const long long slot = slot0 + (long long)(jj < S ? jj : 0) * G;
+            mlj[u] = load_partial2(a.part_ml + 2 * slot);
+            oa[u] = load_partial2(a.part_o + slot * D + 4 * c4);
+            ob[u] = load_partial2(a.part_o + slot * D + 4 * c4 + 2);
+        }
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) m = fmaxf(m, p + u * NP < S ? mlj[u].x : kNegBig);
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const float sj = p + u * NP < S ? fast_exp2(mlj[u].x - m) : 0.0f;
+            l = __builtin_fmaf(mlj[u].y, sj, l);
+            o.x = __builtin_fmaf(oa[u].x, sj, o.x);
+            o.y = __builtin_fmaf(oa[u].y, sj, o.y);
+            o.z = __builtin_fmaf(ob[u].x, sj, o.z);
+            o.w = __builtin_fmaf(ob[u].y, sj, o.w);
+        }
+        for (int jj = p + kMergeBatch * NP; jj < S; jj += NP) {
+            const long long slot = slot0 + (long long)jj * G;
+            const float2 mq = load_partial2(a.part_ml + 2 * slot);
+            const float2 qa = load_partial2(a.part_o + slot * D + 4 * c4);
+            const float2 qb = load_partial2(a.part_o + slot * D + 4 * c4 + 2);
+            const float mn = fmaxf(m, mq.x);
+            const float so = fast_exp2(m - mn), sq = fast_exp2(mq.x - mn);
+            l = __builtin_fmaf(l, so, mq.y * sq);
+            o.x = __builtin_fmaf(o.x, so, qa.x * sq);
+            o.y = __builtin_fmaf(o.y, so, qa.y * sq);
+            o.z = __builtin_fmaf(o.z, so, qb.x * sq);
+            o.w = __builtin_fmaf(o.w, so, qb.y * sq);
+            m = mn;
+        }
+    };
+    auto store_col = [&](int c, float M, float L, const float4& O) {
+        const int h = c / (D / 4), d0 = 4 * (c - h * (D / 4));
+        const long long row = (long long)(h0 + h) * D + d0;
+        float4 r;
+        r.x = finish_output(M, L, O.x, a.sinks, a.gate, h0 + h, row);
+        r.y = finish_output(M, L, O.y, a.sinks, a.gate, h0 + h, row + 1);
+        r.z = finish_output(M, L, O.z, a.sinks, a.gate, h0 + h, row + 2);
+        r.w = finish_output(M, L, O.w, a.sinks, a.gate, h0 + h, row + 3);
+        reinterpret_cast<float4*>(a.out + row)[0] = r;
+    };
+    if constexpr (NP == 1) {
+        for (int c = tid; c < NC; c += NTHR) {
+            float m, l;
+            float4 o;
+            merge_col(c, 0, m, l, o);
+            store_col(c, m, l, o);
+        }
+    } else {
+        const int c = tid % NC, p = tid / NC;
+        const bool act = p < NP;
+        float m, l;
+        float4 o;
+        merge_col(c, act ? p : 0, m, l, o);
+        if (act) {
+            s_o[p * NC + c] = o;
+            s_ml[p * NC + c] = make_float2(m, l);
+        }
+        __syncthreads();
+        if (p == 0) {
+            float M = s_ml[c].x;
+#pragma unroll
+            for (int q = 1; q < NP; ++q) M = fmaxf(M, s_ml[q * NC + c].x);
+            float L = 0.0f;
+            float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                const float sc = fast_exp2(s_ml[q * NC + c].x - M);
+                L = __builtin_fmaf(s_ml[q * NC + c].y, sc, L);
+                const float4 x = s_o[q * NC + c];
+                O.x = __builtin_fmaf(x.x, sc, O.x);
+                O.y = __builtin_fmaf(x.y, sc, O.y);
+                O.z = __builtin_fmaf(x.z, sc, O.z);
+                O.w = __builtin_fmaf(x.w, sc, O.w);
+            }
+            store_col(c, M, L, O);
+        }
+    }
+}
 
 
 // 1/rms of D values in the order of RMSNorm.apply with offsets (RMSNorm.java:24-35, the
@@ -730,6 +881,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     __shared__ float s_w[LDS_MERGE ? NPART * G : 1];
     __shared__ float s_ML[LDS_MERGE ? 2 * G : 1];
     __shared__ float s_o[NPART * G * D];
+    // The merge of the splits (combine_if_last), compiled into the 2- and 8-wave instances only
+    // (decode_fused_merge never picks it for 4-wave workgroups, whose code stays without it),
+    // reuses s_o when it is large enough.
+    constexpr bool CAN_FUSE = WAVES != 4;
+    constexpr bool CMB_ALIAS = NPART * G * D >= combine_scratch_floats<NTHR>();
+    __shared__ float s_cmb[(CMB_ALIAS || !CAN_FUSE) ? 1 : combine_scratch_floats<NTHR>()];
 
     const int tid = threadIdx.x;
     const int split = blockIdx.x;
@@ -743,6 +900,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
     // Step plan from the position (host value or device word).  A device position outside
     // the cache leaves everything untouched; splits beyond the rows of this step exit.
     load_args_now(a);
+    if constexpr (CAN_FUSE) load_merge_args_now(a);
     const int pos = step_position(a);
     if (pos < 0 || pos >= a.max_seq) return;
     const StepPlan sp = plan_step(pos, a.window, a.splits);
@@ -983,10 +1141,10 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
                     finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
             } else {
                 const long long slot = ((long long)vkh * sp.splits + split) * G + h;
-                a.part_o[slot * D + d] = O;
+                store_partial(a.part_o + slot * D + d, O, CAN_FUSE && a.fused);
                 if (d == 0) {
-                    a.part_ml[2 * slot] = M;
-                    a.part_ml[2 * slot + 1] = L;
+                    store_partial(a.part_ml + 2 * slot, M, CAN_FUSE && a.fused);
+                    store_partial(a.part_ml + 2 * slot + 1, L, CAN_FUSE && a.fused);
                 }
             }
         }
@@ -1047,13 +1205,16 @@ __global__ __launch_bounds__(WAVES * 64) void decode_split_kernel(DecodeArgs a) 
                     finish_output(M, L, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
             } else {
                 const long long slot = ((long long)vkh * sp.splits + split) * G + h;
-                a.part_o[slot * D + d] = O;
+                store_partial(a.part_o + slot * D + d, O, CAN_FUSE && a.fused);
                 if (d == 0) {
-                    a.part_ml[2 * slot] = M;
-                    a.part_ml[2 * slot + 1] = L;
+                    store_partial(a.part_ml + 2 * slot, M, CAN_FUSE && a.fused);
+                    store_partial(a.part_ml + 2 * slot + 1, L, CAN_FUSE && a.fused);
                 }
             }
         }
+    }
+    if constexpr (CAN_FUSE) {
+        if (sp.splits > 1 && a.fused) combine_if_last<D, G, NTHR>(a, vkh, sp.splits, tid, CMB_ALIAS ? s_o : s_cmb);
     }
 }
 
@@ -1239,6 +1400,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
     __shared__ float s_m[WAVES * G];
     __shared__ float s_l[WAVES * G];
     __shared__ float s_o[WAVES * G * D];
+    constexpr bool CAN_FUSE = WAVES != 4;   // as in decode_split_kernel
+    constexpr bool CMB_ALIAS = WAVES * G * D >= combine_scratch_floats<NTHR>();
+    __shared__ float s_cmb[(CMB_ALIAS || !CAN_FUSE) ? 1 : combine_scratch_floats<NTHR>()];
 
     const int tid = threadIdx.x;
     const int split = blockIdx.x;
@@ -1247,6 +1411,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
     const bool store = vkh == kvh * a.kv_rep;
     const int h0 = vkh * G;
     load_args_now(a);
+    if constexpr (CAN_FUSE) load_merge_args_now(a);
     const int pos = step_position(a);
     if (pos < 0 || pos >= a.max_seq) return;
     const StepPlan sp = plan_step(pos, a.window, a.splits);
@@ -1476,12 +1641,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_q8_mfma_kernel(DecodeArgs a
                 finish_output(Mx, Ls, O, a.sinks, a.gate, h0 + h, (long long)(h0 + h) * D + d);
         } else {
             const long long slot = ((long long)vkh * sp.splits + split) * G + h;
-            a.part_o[slot * D + d] = O;
+            store_partial(a.part_o + slot * D + d, O, CAN_FUSE && a.fused);
             if (d == 0) {
-                a.part_ml[2 * slot] = Mx;
-                a.part_ml[2 * slot + 1] = Ls;
+                store_partial(a.part_ml + 2 * slot, Mx, CAN_FUSE && a.fused);
+                store_partial(a.part_ml + 2 * slot + 1, Ls, CAN_FUSE && a.fused);
             }
         }
+    }
+    if constexpr (CAN_FUSE) {
+        if (sp.splits > 1 && a.fused) combine_if_last<D, G, NTHR>(a, vkh, sp.splits, tid, CMB_ALIAS ? s_o : s_cmb);
     }
 }
 

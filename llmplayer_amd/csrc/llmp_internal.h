@@ -43,6 +43,9 @@ struct DecodeArgs {
     const int* d_pos;      // device position (tokenParams[0]) or nullptr to use `pos`
     int* range;            // range exponents of the layer's rows [Hkv][K, V] (raised by the append)
     int kv_rep;            // virtual KV heads per cached KV head (grid y = n_kv_heads * kv_rep)
+    int* done;             // per virtual KV head: split workgroups of the current call that have
+                           // written their partials (zero between calls; dk::combine_if_last)
+    int fused;             // 1: the split kernel merges the splits itself (else decode_reduce_kernel)
     long long head_stride; // floats between consecutive KV heads of a plane (max_seq*D)
     int pos;               // position of the new token (row appended) when d_pos is null
     int max_seq;           // cache rows; a device position outside [0, max_seq) is a no-op
@@ -73,6 +76,10 @@ int decode_split_waves(int head_dim, int group, int waves, bool q8);
 // Workgroups of that kernel resident per CU at once (registers and LDS), 0 on error.
 int decode_split_blocks_per_cu(int head_dim, int group, int waves, bool q8);
 // Launches the log-sum-exp combine of the splits: one block per query head.
+// Whether a decode launch with `splits` splits of `waves`-wave workgroups merges its splits
+// inside the split kernel: when the last workgroup's merge takes one round of loads
+// (dk::combine_if_last with at most dk::kMergeBatch splits per thread group).
+bool decode_fused_merge(int head_dim, int group, int waves, int splits);
 hipError_t launch_decode_reduce(const DecodeArgs& a, int head_dim, int group, int n_heads,
                                 hipStream_t stream);
 // True when a decode kernel exists for (head_dim, group) (host_layout.h decode_group_ok; larger

@@ -96,6 +96,7 @@ struct KvHandle {
     size_t prefill_part_bytes = 0;
     float* part_o = nullptr;
     float* part_ml = nullptr;
+    int* done = nullptr;             // per virtual KV head: the decode split counters (zero between calls)
     int blk_dim = 0;                 // llmp_block_config: embedding length
     float blk_rscale = 0.0f;         // Granite residual scale, 0 = off
     int blk_input = LLMP_INPUT_F32;  // llmp_block_input_mode
@@ -216,6 +217,7 @@ void free_handle(KvHandle* kv) {
     if (kv->blkb_buf) (void)hipFree(kv->blkb_buf);
     if (kv->part_o) (void)hipFree(kv->part_o);
     if (kv->part_ml) (void)hipFree(kv->part_ml);
+    if (kv->done) (void)hipFree(kv->done);
     if (kv->prefill_ws) (void)hipFree(kv->prefill_ws);
     if (kv->prefill_part) (void)hipFree(kv->prefill_part);
     for (auto& v : kv->prof_pending)
@@ -364,6 +366,8 @@ int enqueue_decode(KvHandle* kv, int layer, int src_layer, int position, const i
     a.out = reinterpret_cast<float*>(out);
     a.part_o = kv->part_o;
     a.part_ml = kv->part_ml;
+    a.done = kv->done;
+    a.fused = decode_fused_merge(D, group, plan.waves, plan.splits) ? 1 : 0;
     a.d_pos = d_pos;
     a.range = kv->range(kv_layer);
     a.head_stride = (long long)kv->max_seq * D;
@@ -385,7 +389,7 @@ int enqueue_decode(KvHandle* kv, int layer, int src_layer, int position, const i
     }
 
     hipStream_t st = pick_stream(stream);
-    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
     if (kv->prof_on) {
         if (int rc = prof_event(kv, &e0)) return rc;
         if (int rc = prof_event(kv, &e1)) return rc;
@@ -397,16 +401,19 @@ int enqueue_decode(KvHandle* kv, int layer, int src_layer, int position, const i
         LLMP_HIP_CHECK(hipEventRecord(e1, st), "hipEventRecord");
         kv->prof_pending[LLMP_PROF_DECODE_SPLIT].push_back({e0, e1});
     }
-    if (plan.splits > 1) {
+    // Several splits: merged by the split kernel's last workgroup per KV head when that is one
+    // round of loads (a.fused), else by the combine kernel.
+    if (plan.splits > 1 && !a.fused) {
+        hipEvent_t e2 = nullptr, e3 = nullptr;
         if (kv->prof_on) {
             if (int rc = prof_event(kv, &e2)) return rc;
-            if (int rc = prof_event(kv, &e0)) return rc;
+            if (int rc = prof_event(kv, &e3)) return rc;
             LLMP_HIP_CHECK(hipEventRecord(e2, st), "hipEventRecord");
         }
         LLMP_HIP_CHECK(launch_decode_reduce(a, D, group, c.n_heads, st), "decode reduce launch");
         if (kv->prof_on) {
-            LLMP_HIP_CHECK(hipEventRecord(e0, st), "hipEventRecord");
-            kv->prof_pending[LLMP_PROF_DECODE_REDUCE].push_back({e2, e0});
+            LLMP_HIP_CHECK(hipEventRecord(e3, st), "hipEventRecord");
+            kv->prof_pending[LLMP_PROF_DECODE_REDUCE].push_back({e2, e3});
         }
     }
     if (kv->prof_on && kv->prof_pending[LLMP_PROF_DECODE_SPLIT].size() >= 4096) {
@@ -650,6 +657,8 @@ int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int 
     const size_t slots = (size_t)kMaxSplits * (size_t)kMaxGroup * (size_t)n_kv_heads;
     hipError_t ea = hipMalloc(&kv->part_o, slots * (size_t)head_dim * sizeof(float));
     if (ea == hipSuccess) ea = hipMalloc(&kv->part_ml, slots * 2 * sizeof(float));
+    // one split counter per query head bounds the virtual KV heads of any layer configuration
+    if (ea == hipSuccess) ea = hipMalloc(&kv->done, slots / kMaxSplits * sizeof(int));
     if (ea != hipSuccess) {
         free_handle(kv.get());
         return fail(ea == hipErrorOutOfMemory ? LLMP_ERR_OUT_OF_MEMORY : LLMP_ERR_HIP,
@@ -657,6 +666,7 @@ int llmp_kv_create(int n_layers, int max_seq, int n_kv_heads, int head_dim, int 
     }
     kv->part_slots = slots;
     hipError_t z = hipMemsetAsync(p, 0, bytes, G().stream);
+    if (z == hipSuccess) z = hipMemsetAsync(kv->done, 0, slots / kMaxSplits * sizeof(int), G().stream);
     if (z == hipSuccess) z = hipStreamSynchronize(G().stream);
     if (z != hipSuccess) {
         free_handle(kv.get());
@@ -992,10 +1002,14 @@ int llmp_layer_config(uint64_t handle, int layer, int n_heads, int n_kv_heads, i
         LLMP_HIP_CHECK(hipDeviceSynchronize(), "hipDeviceSynchronize");
         (void)hipFree(kv->part_o);
         (void)hipFree(kv->part_ml);
+        (void)hipFree(kv->done);
         kv->part_o = kv->part_ml = nullptr;
+        kv->done = nullptr;
         kv->part_slots = 0;
         hipError_t ea = hipMalloc(&kv->part_o, slots * (size_t)head_dim * sizeof(float));
         if (ea == hipSuccess) ea = hipMalloc(&kv->part_ml, slots * 2 * sizeof(float));
+        if (ea == hipSuccess) ea = hipMalloc(&kv->done, (size_t)n_heads * sizeof(int));
+        if (ea == hipSuccess) ea = hipMemset(kv->done, 0, (size_t)n_heads * sizeof(int));
         if (ea != hipSuccess)
             return fail(ea == hipErrorOutOfMemory ? LLMP_ERR_OUT_OF_MEMORY : LLMP_ERR_HIP,
                         "layer %d: split workspace for %d query heads: %s", layer, n_heads,

@@ -217,6 +217,27 @@ def test_error_codes():
         assert _lib.status("llmp_kv_create", 4096, 1 << 20, 64, 128, 0, C.byref(hd)) == 5
 
 
+def test_split_merge_in_the_split_kernel():
+    """Plans whose splits the split kernel merges itself (its last workgroup per KV head, through
+    agent-scope atomic partials and a per-head counter): C1 at pos 511 (16 splits of 2-wave
+    workgroups) and C3 at 32k (24 splits of 8 waves): no combine launch, the oracle's output,
+    and the counters re-armed (a second call, another layer, agrees too)."""
+    for c, n, seed in ((hfp.ModelConfig(32, 8, 64, 2, rope_freq_base=500000.0), 512, 41),
+                       (hfp.ModelConfig(24, 8, 128, 2, rope_freq_base=500000.0), 32768, 42)):
+        d = dc.make_layer(c, n, n - 1, seed=seed, k_scale=0.5)
+        with hfp.HipForwardPass(c, n) as fp:
+            plan = fp.decodePlan(0, n - 1)
+            assert plan["waves"] in (2, 8), plan
+            _lib.call("llmp_profile_enable", fp.kv.handle, 1)
+            out, kc, vc = dc.oracle_call(c, n, d, 0, n - 1)
+            for layer in (0, 1, 0):
+                _run(fp, c, n, d, layer, n - 1, 0, f"merged in the split kernel, layer {layer}",
+                     check_cache=False, oracle=(out, kc, vc))
+            cnt, ms = C.c_int(), C.c_double()
+            _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_REDUCE, C.byref(cnt), C.byref(ms))
+            assert cnt.value == 0
+
+
 def test_profile_counters_count_launches():
     c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
     d = dc.make_layer(c, 4096, 4095, seed=9, k_scale=0.5)
@@ -226,13 +247,17 @@ def test_profile_counters_count_launches():
         _lib.call("llmp_profile_enable", fp.kv.handle, 1)
         for _ in range(5):
             fp.forwardAttentionPart(0, 4095, 32)     # split kernel + combine kernel
+        for _ in range(2):
+            # 8 splits of 4-wave workgroups: the combine kernel too (the split kernel merges
+            # its splits itself only with 2- or 8-wave workgroups)
+            fp.forwardAttentionPart(0, 4095, 8)
         for _ in range(3):
             fp.forwardAttentionPart(0, 4095, 1)      # one split: no combine kernel
         cnt, ms = C.c_int(), C.c_double()
         _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(cnt), C.byref(ms))
-        assert cnt.value == 8 and ms.value > 0
+        assert cnt.value == 10 and ms.value > 0
         _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_REDUCE, C.byref(cnt), C.byref(ms))
-        assert cnt.value == 5
+        assert cnt.value == 7
         _lib.call("llmp_profile_reset", fp.kv.handle)
         _lib.call("llmp_profile_read", fp.kv.handle, 0, C.byref(cnt), C.byref(ms))
         assert cnt.value == 0
