@@ -22,7 +22,8 @@ hipError_t launch_ff(const tk::ProjTokArgs& a, hipStream_t st) {
 
 hipError_t launch_tok_prep(const float* x, long long x_pitch, int cols, const float* norm_w, float eps,
                            float* sc, int n_tokens, hipStream_t st) {
-    if (x == nullptr || sc == nullptr || cols <= 0 || n_tokens < 1 || n_tokens > tk::kTok)
+    if (x == nullptr || sc == nullptr || cols <= 0 || (cols & 3) || (x_pitch & 3) || n_tokens < 1 ||
+        n_tokens > tk::kTok || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(norm_w) & 15))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(tk::tok_prep_kernel<tk::kPrepThreads>, dim3(n_tokens), dim3(tk::kPrepThreads), 0, st, x, x_pitch,
                        cols, norm_w, eps, sc);
