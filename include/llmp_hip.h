@@ -409,8 +409,12 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
 
 /* ---- profiling (the reference's -Dcuda.profile section timers,
  *      CudaForwardPass.java:1646-1737, as HIP events around each kernel) ------------------ */
-#define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV) */
-#define LLMP_PROF_DECODE_REDUCE  1  /* log-sum-exp combine of the splits                    */
+#define LLMP_PROF_DECODE_SPLIT   0  /* split-K decode kernel (QK-norm, RoPE, append, QK/softmax/PV;
+                                        its last workgroup per KV head merges the splits where the
+                                        launch plan allows: the 2- and 8-wave plans whose partials
+                                        fit one batch of loads per thread)                      */
+#define LLMP_PROF_DECODE_REDUCE  1  /* log-sum-exp combine of the splits (no launch, so no count,
+                                        when one split or the split kernel merged them)          */
 #define LLMP_PROF_PREFILL_APPEND 2  /* prefill: exact K/V append of the prompt tokens       */
 #define LLMP_PROF_PREFILL_ATTN   3  /* prefill: key-tile images + MFMA causal attention      */
 #define LLMP_PROF_KINDS          4
