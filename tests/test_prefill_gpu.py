@@ -76,6 +76,15 @@ def test_c5_llama1b_prefill_then_128_decode_steps(P):
                       what=f"C5 prefill P={P}")
 
 
+# Long prompts in one round of workgroups: C5 at P = 1024 (16-token query blocks), P = 1100
+# (a ragged last block), 2048 after a 300-row prefix, and GQA group 2 at 2048.
+@pytest.mark.parametrize("hq,pos0,P", [(32, 0, 1024), (32, 0, 1100), (32, 300, 2048), (16, 0, 2048)])
+def test_prefill_long_prompts(hq, pos0, P):
+    c = hfp.ModelConfig(hq, 8, 64, 1, architecture=hfp.ARCH_LLAMA, rope_freq_base=500000.0)
+    _run_prefill_case(c, pos0 + P + 4, 0, pos0, P, seed=900 + P + pos0, decode_steps=2,
+                      what=f"long prefill {hq}/8/64 pos0={pos0} P={P}")
+
+
 SHAPES = [(8, 8, 64), (16, 8, 64), (24, 8, 64), (32, 8, 64), (48, 8, 64), (64, 8, 64),
           (8, 8, 128), (16, 8, 128), (24, 8, 128), (32, 8, 128), (48, 8, 128), (64, 8, 128),
           (4, 4, 256), (8, 4, 256), (12, 4, 256), (16, 4, 256), (24, 4, 256), (32, 4, 256),
