@@ -508,8 +508,8 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
     """The attention half of a C3 (Llama-3.2-3B, dim 3072) layer with a GGUF weight mix (MIXES;
     default Q4_K_M: Q4_K for q, k, o and Q6_K for v): pre-norm, projections, attention at ctx,
     output projection and residual, as a graph replay over n_layers layers with their own
-    weights and caches.  q8_input: the Q4_K projections on the Q8_1-quantised input (the
-    reference GPU's int8 matvecs) instead of the fp32 input."""
+    weights and caches.  q8_input: the projections the reference GPU runs on int8 (Q4_K, Q3_K,
+    Q5_K here; Q6_K stays fp32) on the Q8_1-quantised input instead of the fp32 input."""
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
     dim = 3072
@@ -547,7 +547,9 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
         fp.close()
     us = ms / steps * 1e3
     return {"ctx": ctx, "weights": MIXES[mix][1], "dim": dim,
-            "input": "Q8_1 (int8 dot products for Q4_K)" if q8_input else "fp32",
+            "input": ("Q8_1 (int8 dot products for "
+                      + ("Q4_K" if mix == "q4_k_m" else "Q3_K and Q5_K" if mix == "q3_k_l" else "Q5_K")
+                      + ")") if q8_input else "fp32",
             "us_per_layer_call": round(us, 2), "weight_bytes_per_layer": wbytes,
             "kv_bytes_per_layer": kv_bytes(ctx), "layers_rotated": n_layers}
 
@@ -912,7 +914,7 @@ def main() -> int:
                 f"kernel {r['attn_kernel_us']} us ({r['attn_kernel_causal_tflops']} causal TFLOP/s)")
             prefill.append(r)
 
-    block = block_q8 = block_q3kl = block_batch = None
+    block = block_q8 = block_q3kl = block_q3kl_q8 = block_batch = None
     if args.block:
         block = block_run(args.ctx2 or 4096, 200)
         if second is not None:
@@ -932,6 +934,8 @@ def main() -> int:
                 block_q3kl["projection_weight_gbps"] = round(
                     block_q3kl["weight_bytes_per_layer"] / (block_q3kl["projections_us"] * 1e-6) / 1e9, 1)
         log(f"[bench] attention block C3 Q3_K_L: {block_q3kl['us_per_layer_call']} us/layer")
+        block_q3kl_q8 = block_run(args.ctx2 or 4096, 200, q8_input=True, mix="q3_k_l")
+        log(f"[bench] attention block C3 Q3_K_L, Q8_1 input: {block_q3kl_q8['us_per_layer_call']} us/layer")
         block_batch = []
         for ctx_b, K, nl in ((4096, 4, 28), (4096, 16, 28), (32768, 4, 8), (32768, 16, 8)):
             r = block_batch_run(ctx_b, K, 40, nl)
@@ -1017,6 +1021,8 @@ def main() -> int:
         line["attn_block_c3_q4_k_m_q8_1_input"] = block_q8
     if block_q3kl is not None:
         line["attn_block_c3_q3_k_l"] = block_q3kl
+    if block_q3kl_q8 is not None:
+        line["attn_block_c3_q3_k_l_q8_1_input"] = block_q3kl_q8
     if block_batch:
         line["attn_block_batch_c3_q4_k_m"] = block_batch
     if q8_prefill is not None:

@@ -369,11 +369,11 @@ int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int 
 int llmp_block_config(uint64_t handle, int dim, float residual_scale);
 /* How the block's projections read their input.  LLMP_INPUT_F32 (the default): every type
  * takes the fp32 (normalised) input, the CPU engine's arithmetic (FloatTensor.matmul).
- * LLMP_INPUT_Q8_1: Q4_K and Q8_0 weights take a Q8_1 copy of the input (blocks of 32: scale
- * max|x|/127, int8 quants, block sum) and exact int8 dot products, the reference GPU's
- * default matvecs (CudaForwardPass.java:783-790 cuda.dp4a, :1998-2037; quantize_q8.cu,
- * rmsnorm_quantize.cu, matmul_q4_k_dp4a.cu, matmul_q8_0_dp4a.cu); other types keep the fp32
- * input, as there. */
+ * LLMP_INPUT_Q8_1: Q4_K, Q8_0, Q5_0, Q3_K, Q5_K, IQ4_NL and IQ4_XS weights take a Q8_1 copy
+ * of the input (blocks of 32: scale max|x|/127, int8 quants, block sum) and exact int8 dot
+ * products, the reference GPU's default matvecs (CudaForwardPass.java:783-790 cuda.dp4a,
+ * :216-226 and :1998-2090; quantize_q8.cu, rmsnorm_quantize.cu, matmul_<type>_dp4a*.cu); the
+ * other types (F32, F16, BF16, Q4_0, Q6_K, MXFP4) keep the fp32 input, as there. */
 #define LLMP_INPUT_F32   0
 #define LLMP_INPUT_Q8_1  1
 int llmp_block_input_mode(uint64_t handle, int mode);

@@ -25,12 +25,17 @@ int nk_for(int cols) {
     return nk > F::MAXU ? F::MAXU : nk;
 }
 
+// The largest instantiated round count of a format: nk_for never asks for more than MAXU, so
+// no instance above it is compiled.
+template <class F>
+constexpr int nk_cap(int nk) { return nk > F::MAXU ? F::MAXU : nk; }
+
 template <class F>
 hipError_t launch_f(const gk::GemvArgs& a, hipStream_t st) {
     switch (nk_for<F>(a.cols)) {
     case 2: return launch_nk<F, 2>(a, st);
-    case 3: return launch_nk<F, 3>(a, st);
-    case 4: return launch_nk<F, 4>(a, st);
+    case 3: return launch_nk<F, nk_cap<F>(3)>(a, st);
+    case 4: return launch_nk<F, nk_cap<F>(4)>(a, st);
     default:
         if constexpr (F::MAXU >= 8) {
             if (nk_for<F>(a.cols) == 6) return launch_nk<F, 6>(a, st);
@@ -59,16 +64,16 @@ template <class F1, int NK1, class F2>
 hipError_t launch_mix2(const gk::GemvArgs& a, hipStream_t st) {
     switch (nk_for<F2>(a.cols)) {
     case 2: return launch_nk<F1, NK1, F2, 2>(a, st);
-    case 3: return launch_nk<F1, NK1, F2, 3>(a, st);
-    default: return launch_nk<F1, NK1, F2, 4>(a, st);
+    case 3: return launch_nk<F1, NK1, F2, nk_cap<F2>(3)>(a, st);
+    default: return launch_nk<F1, NK1, F2, nk_cap<F2>(4)>(a, st);
     }
 }
 template <class F1, class F2>
 hipError_t launch_mix(const gk::GemvArgs& a, hipStream_t st) {
     switch (nk_for<F1>(a.cols)) {
     case 2: return launch_mix2<F1, 2, F2>(a, st);
-    case 3: return launch_mix2<F1, 3, F2>(a, st);
-    default: return launch_mix2<F1, 4, F2>(a, st);
+    case 3: return launch_mix2<F1, nk_cap<F1>(3), F2>(a, st);
+    default: return launch_mix2<F1, nk_cap<F1>(4), F2>(a, st);
     }
 }
 
@@ -124,8 +129,12 @@ hipError_t launch_gemv_pair(const gk::GemvArgs& a, int first_type, int second_ty
     if (a.cols <= 0 || a.cols > gk::kMaxGemvCols || a.cols % 256 || a.rows_total <= 0 ||
         a.nseg < 1 || a.nseg > 3)
         return hipErrorInvalidValue;
-    if (first_type == gk::kQ3_K) return launch_mix<gk::FmtQ3_K, gk::FmtQ5_K>(a, st);
-    if (first_type == gk::kQ5_K) return launch_mix<gk::FmtQ5_K, gk::FmtQ6_K>(a, st);
+    // The Q8_1 mode runs Q3_K, Q5_K and Q4_K on the int8 input; Q6_K stays on the fp32 one
+    // (its dp4a kernel is opt-in in the reference, CudaForwardPass.java:2031-2038).
+    if (first_type == gk::kQ3_K)
+        return q8_input ? launch_mix<gk::FmtQ3_KQ8, gk::FmtQ5_KQ8>(a, st) : launch_mix<gk::FmtQ3_K, gk::FmtQ5_K>(a, st);
+    if (first_type == gk::kQ5_K)
+        return q8_input ? launch_mix<gk::FmtQ5_KQ8, gk::FmtQ6_K>(a, st) : launch_mix<gk::FmtQ5_K, gk::FmtQ6_K>(a, st);
     return q8_input ? launch_pair_f<gk::FmtQ4_KQ8>(a, st) : launch_pair_f<gk::FmtQ4_K>(a, st);
 }
 
@@ -134,8 +143,18 @@ hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipS
         return hipErrorInvalidValue;
     const int unit = gemv_unit(ggml_type);
     if (unit == 0 || a.cols % unit) return hipErrorInvalidValue;
-    if (q8_input && ggml_type == gk::kQ4_K) return launch_f<gk::FmtQ4_KQ8>(a, st);
-    if (q8_input && ggml_type == gk::kQ8_0) return launch_f<gk::FmtQ8_0Q8>(a, st);
+    if (q8_input) {   // the formats the reference GPU runs on its Q8_1 input (dp4aType != 0, not Q6_K)
+        switch (ggml_type) {
+        case gk::kQ4_K: return launch_f<gk::FmtQ4_KQ8>(a, st);
+        case gk::kQ8_0: return launch_f<gk::FmtQ8_0Q8>(a, st);
+        case gk::kQ5_0: return launch_f<gk::FmtQ5_0Q8>(a, st);
+        case gk::kQ3_K: return launch_f<gk::FmtQ3_KQ8>(a, st);
+        case gk::kQ5_K: return launch_f<gk::FmtQ5_KQ8>(a, st);
+        case gk::kIQ4_NL: return launch_f<gk::FmtIQ4_NLQ8>(a, st);
+        case gk::kIQ4_XS: return launch_f<gk::FmtIQ4_XSQ8>(a, st);
+        default: break;
+        }
+    }
     switch (ggml_type) {
     case gk::kF32: return launch_f<gk::FmtF32>(a, st);
     case gk::kF16: return launch_f<gk::FmtHalf<false>>(a, st);

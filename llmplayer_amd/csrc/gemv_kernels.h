@@ -564,8 +564,8 @@ struct FmtQ3_K {
 };
 
 // ---- Q8_1 input: the reference GPU's int8 matvecs -------------------------------------------
-// CudaForwardPass runs its Q4_K and Q8_0 projections on a Q8_1 copy of the input by default
-// (CudaForwardPass.java:783-790, 1998-2037; rmsnorm_quantize.cu, quantize_q8.cu,
+// CudaForwardPass runs its Q4_K and Q8_0 projections (and the formats below) on a Q8_1 copy of
+// the input by default (CudaForwardPass.java:783-790, 1998-2037; rmsnorm_quantize.cu, quantize_q8.cu,
 // matmul_q4_k_dp4a.cu, matmul_q8_0_dp4a.cu): per 32 values d = max|x|/127, quants rint(x*127/
 // max|x|) clamped to +-127, s = sum(x); a block's dot is an exact int8 dot product scaled in
 // float.  Here the weights keep the planes of FmtQ4_K / FmtQ8_0; a unit is 8 weight bytes,
@@ -657,6 +657,149 @@ struct FmtQ8_0Q8 {
         const uint2 xa = *reinterpret_cast<const uint2*>(st.xq + i);
         const int dp = dot4_i8(r.q.y, xa.y, dot4_i8(r.q.x, xa.x, 0));
         return (h2f(r.d) * st.xd[i >> 5]) * (float)dp;
+    }
+};
+
+// The other formats CudaForwardPass runs on the Q8_1 input (:1998-2037: Q5_0, Q3_K, Q5_K, IQ4_NL,
+// IQ4_XS; matmul_q5_0_dp4a_smem.cu, matmul_q3_k_dp4a.cu, matmul_q5_k_dp4a.cu,
+// matmul_iq4_nl_dp4a.cu, matmul_iq4_xs_dp4a_mw.cu): the weights' integer values as int8, an
+// exact int8 dot with the input's quants, and the block's factors in the reference's order:
+// (scale * d_x) * dp, Q5_K minus (dmin * m) * s_x.  Units and planes are the fp32-input
+// formats'; a unit adds its share of a block's dot, so only the float sum's order differs.
+
+// Bytes holding 5-bit (3-bit) two's complement fields, sign-extended to int8 per byte.
+__device__ __forceinline__ unsigned sext5x4(unsigned v) { return v | ((v & 0x10101010u) * 0x0Eu); }
+__device__ __forceinline__ unsigned sext3x4(unsigned v) { return v | ((v & 0x04040404u) * 0x3Eu); }
+
+struct FmtQ5_0Q8 {
+    static constexpr int UNIT = FmtQ5_0::UNIT, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false, Q8IN = true;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    using Raw = FmtQ5_0::Raw;
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) { return FmtQ5_0::load(w, row, u); }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned h = r.qh >> (4 * (j & 3));
+        const unsigned lo = sext5x4(((r.q & 0x0F0F0F0Fu) | (spread4(h & 15u) << 4)) ^ 0x10101010u);
+        const unsigned hi = sext5x4((((r.q >> 4) & 0x0F0F0F0Fu) | (spread4((h >> 16) & 15u) << 4)) ^ 0x10101010u);
+        const int xi = split_x(ub, j);
+        const int dp = dot4_i8(hi, *reinterpret_cast<const unsigned*>(st.xq + xi + 16),
+                               dot4_i8(lo, *reinterpret_cast<const unsigned*>(st.xq + xi), 0));
+        return (h2f(r.d) * st.xd[xi >> 5]) * (float)dp;
+    }
+};
+
+struct FmtIQ4_NLQ8 {
+    static constexpr int UNIT = FmtIQ4_NL::UNIT, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = false, Q8IN = true;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    using Raw = FmtIQ4_NL::Raw;
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) { return FmtIQ4_NL::load(w, row, u); }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned lo = lut16(r.q & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        const unsigned hi = lut16((r.q >> 4) & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        const int xi = split_x(ub, j);
+        const int dp = dot4_i8(hi, *reinterpret_cast<const unsigned*>(st.xq + xi + 16),
+                               dot4_i8(lo, *reinterpret_cast<const unsigned*>(st.xq + xi), 0));
+        return (h2f(r.d) * st.xd[xi >> 5]) * (float)dp;
+    }
+};
+
+struct FmtIQ4_XSQ8 {
+    static constexpr int UNIT = FmtIQ4_XS::UNIT, MAXU = 8, TAB = FmtIQ4_XS::TAB;
+    static constexpr bool XSUM = false, Q8IN = true;
+    using Row = FmtIQ4_XS::Row;
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        return FmtIQ4_XS::load_row(w, row, j, units);
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        FmtIQ4_XS::build_tab(r, tab, j, units);
+    }
+    using Raw = FmtIQ4_XS::Raw;
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) { return FmtIQ4_XS::load(w, row, u); }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const float dl = st.tab[(ub >> 2) + (j >> 2)];   // d * (ls - 32) of sub-block (ub + j)/4
+        const unsigned lo = lut16(r.q & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        const unsigned hi = lut16((r.q >> 4) & 0x0F0F0F0Fu, kIq4[0], kIq4[1], kIq4[2], kIq4[3]);
+        const int xi = split_x(ub, j);
+        const int dp = dot4_i8(hi, *reinterpret_cast<const unsigned*>(st.xq + xi + 16),
+                               dot4_i8(lo, *reinterpret_cast<const unsigned*>(st.xq + xi), 0));
+        return (dl * st.xd[xi >> 5]) * (float)dp;
+    }
+};
+
+// Q5_K on the Q8_1 input: FmtQ4_KQ8's units (8 nibble bytes: elements 64g + l .. +7 of
+// sub-block 2g and 64g + 32 + l .. of sub-block 2g + 1, l = 8(u%4)) with the fifth bits of qh
+// bytes l .. l+7 (bit 2g, 2g + 1) or-ed in.
+struct FmtQ5_KQ8 {
+    // at most 3 rounds in registers: 4 spilled (the fifth-bit words take 2 more VGPRs a unit)
+    static constexpr int UNIT = 16, MAXU = 3, TAB = 16;
+    static constexpr bool XSUM = false, Q8IN = true;
+    using Row = FmtQ4_K::Row;
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        return FmtQ4_K::head(w, row, j, units >> 4);
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        FmtQ4_K::build_tab_ns(r, tab, j, units >> 4);
+    }
+    struct Raw { uint2 q, qh; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<uint2>(rp(w, 0, row), (unsigned)u * 8u),
+                   ldo<uint2>(rp(w, 2, row), ((unsigned)u >> 4) * 32u + 8u * ((unsigned)u & 3u))};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const int g = (j >> 2) & 3, sb = (ub >> 4) + (j >> 4);
+        const int i0 = sb * 256 + 64 * g + 8 * (j & 3);
+        const uint2 xa = *reinterpret_cast<const uint2*>(st.xq + i0);
+        const uint2 xb = *reinterpret_cast<const uint2*>(st.xq + i0 + 32);
+        auto q5 = [&](unsigned q, unsigned h, int s) {
+            return ((q >> (4 * s)) & 0x0F0F0F0Fu) | (((h >> (2 * g + s)) & 0x01010101u) << 4);
+        };
+        const int dp0 = dot4_i8(q5(r.q.y, r.qh.y, 0), xa.y, dot4_i8(q5(r.q.x, r.qh.x, 0), xa.x, 0));
+        const int dp1 = dot4_i8(q5(r.q.y, r.qh.y, 1), xb.y, dot4_i8(q5(r.q.x, r.qh.x, 1), xb.x, 0));
+        const float4 f = x4(st.tab, sb * TAB + 4 * g);   // (d*sc, dmin*m) of sub-blocks 2g, 2g+1
+        const int b0 = sb * 8 + 2 * g;
+        const float2 dx = *reinterpret_cast<const float2*>(st.xd + b0);
+        const float2 sx = *reinterpret_cast<const float2*>(st.xss + b0);
+        const float v = (f.x * dx.x) * (float)dp0 + (f.z * dx.y) * (float)dp1;
+        const float mt = (f.y * sx.x) + (f.w * sx.y);
+        return (j & 3) == 0 ? v - mt : v;
+    }
+};
+
+// Q3_K on the Q8_1 input: FmtQ3_K's units (the four 2-bit fields of 4 qs bytes: elements
+// 128h + 32p + 16w + l .. +3 for p = 0..3), each field (q - 4) as int8; per p the block
+// 8sb + 4h + p's factor (d * (sc - 32)) * d_x.
+struct FmtQ3_KQ8 {
+    static constexpr int UNIT = FmtQ3_K::UNIT, MAXU = 4, TAB = FmtQ3_K::TAB;
+    static constexpr bool XSUM = false, Q8IN = true;
+    using Row = FmtQ3_K::Row;
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        return FmtQ3_K::load_row(w, row, j, units);
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        FmtQ3_K::build_tab(r, tab, j, units);
+    }
+    using Raw = FmtQ3_K::Raw;
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) { return FmtQ3_K::load(w, row, u); }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const int h = (j >> 3) & 1, w = (j >> 2) & 1, l = 4 * (j & 3);
+        const int sb = (ub >> 4) + (j >> 4);
+        const float4 f = x4(st.tab, sb * TAB + (2 * h + w) * 4);
+        const float ds[4] = {f.x, f.y, f.z, f.w};
+        float s = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const unsigned q = sext3x4((((r.qs >> (2 * p)) & 0x03030303u) |
+                                        (((r.hm >> (4 * h + p)) & 0x01010101u) << 2)) ^ 0x04040404u);
+            const int xi = sb * 256 + 128 * h + 32 * p + 16 * w + l;
+            const int dp = dot4_i8(q, *reinterpret_cast<const unsigned*>(st.xq + xi), 0);
+            s = s + (ds[p] * st.xd[xi >> 5]) * (float)dp;
+        }
+        return s;
     }
 };
 

@@ -479,8 +479,9 @@ class HipForwardPass:
     def setBlockConfig(self, dim: int, residual_scale: float = 0.0,
                        input_mode: int = _lib.LLMP_INPUT_F32) -> None:
         """embeddingLength and Granite's residualScale (0 = off) for forwardAttentionBlock.
-        input_mode LLMP_INPUT_Q8_1: Q4_K / Q8_0 projections on a Q8_1 copy of the input with
-        int8 dot products (CudaForwardPass's default dp4a matvecs, CudaForwardPass.java:783-790);
+        input_mode LLMP_INPUT_Q8_1: Q4_K, Q8_0, Q5_0, Q3_K, Q5_K, IQ4_NL and IQ4_XS projections
+        on a Q8_1 copy of the input with int8 dot products (CudaForwardPass's default dp4a
+        matvecs, CudaForwardPass.java:783-790, 216-226);
         LLMP_INPUT_F32: the CPU engine's fp32 arithmetic."""
         call("llmp_block_config", self.kv.handle, dim, float(residual_scale))
         call("llmp_block_input_mode", self.kv.handle, int(input_mode))

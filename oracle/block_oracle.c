@@ -370,10 +370,11 @@ void orc_rmsnorm(float *out, const float *x, const float *w, int size, float eps
 }
 
 /* ---- the reference GPU's Q8_1 input (its default "dp4a" matvecs) ----------------------------
- * CudaForwardPass (CudaForwardPass.java:783-790: cuda.dp4a defaults to true; :1998-2037: Q4_K
- * and Q8_0 take the int8 kernels, Q6_K stays on the fp32 one) normalises x, quantises it to
- * Q8_1 blocks (rmsnorm_quantize.cu, quantize_q8.cu) and runs matmul_q4_k_dp4a.cu /
- * matmul_q8_0_dp4a.cu: exact int8 dot products per 32 values, scaled in float.  The
+ * CudaForwardPass (CudaForwardPass.java:783-790: cuda.dp4a defaults to true; :1998-2090: Q4_K,
+ * Q8_0, Q5_0, Q3_K, Q5_K, IQ4_NL and IQ4_XS take the int8 kernels, Q6_K stays on the fp32 one
+ * unless cuda.dp4a.q6 is set) normalises x, quantises it to Q8_1 blocks (rmsnorm_quantize.cu,
+ * quantize_q8.cu) and runs matmul_<type>_dp4a*.cu: exact int8 dot products per 32 values,
+ * scaled in float.  The
  * restatement fixes two reduction orders the reference leaves to its launch geometry (and to
  * CUDA's rsqrtf): the norm's sum of squares and each block's sum, both in the library's
  * staging order, so that the quantised bytes are the GPU's exactly. */
@@ -451,7 +452,13 @@ static void q4k_scale_min(const uint8_t *q, int j, int *sc, int *m)
 
 /* The int8 matvecs on a Q8_1 input (q [cols], d and s [cols/32]); out[row] += the row's dot:
  *   Q4_K (matmul_q4_k_dp4a.cu): per sub-block j of 32, ((d*sc_j)*d_x)*dp_j - (dmin*m_j)*s_x
+ *   Q5_K (matmul_q5_k_dp4a.cu:123-124): the same, q = nibble | fifth bit << 4
  *   Q8_0 (matmul_q8_0_dp4a.cu): per block, (d*d_x)*dp
+ *   Q5_0 (matmul_q5_0_dp4a_smem.cu:111): per block, (d*d_x)*dp, q = (nibble | bit << 4) - 16
+ *   IQ4_NL (matmul_iq4_nl_dp4a.cu:100): per block, (d*d_x)*dp, q = KVALUES[nibble]
+ *   IQ4_XS (matmul_iq4_xs_dp4a_mw.cu:115): per sub-block ib, (dl*d_x)*dp, dl = d*(ls - 32)
+ *   Q3_K (matmul_q3_k_dp4a.cu:142): per block of 32 (halves w = 0, 1 of 16 with scales dl_w =
+ *        d*(sc - 32)), (dl_0*d_x)*dp_0 + (dl_1*d_x)*dp_1, q = (2 bits | high bit << 2) - 4
  * with dp the exact integer dot of the block's weights with the input's quants, added over
  * the row's blocks in order (the reference adds per lane, then a warp tree).  -1 for other
  * types. */
@@ -484,6 +491,116 @@ int orc_matmul_q8_1(int type, const uint8_t *w, int rows, int cols, const int8_t
         }
         return 0;
     }
+    if (type == ORC_GGML_Q5_K) {
+        if (cols % 256) return -1;
+        const int ns = cols / 256;
+        for (int r = 0; r < rows; r++) {
+            float acc = 0.0f;
+            for (int b = 0; b < ns; b++) {
+                const uint8_t *blk = w + ((size_t)r * ns + b) * 176, *qh = blk + 16, *qs = blk + 48;
+                const float dd = orc_f16_to_f32(le16(blk)), dmin = orc_f16_to_f32(le16(blk + 2));
+                for (int g = 0; g < 4; g++)
+                    for (int h = 0; h < 2; h++) {   /* sub-block 2g + h: nibble h, qh bit 2g + h */
+                        const int j = 2 * g + h, xb = b * 8 + j;
+                        int dp = 0;
+                        for (int l = 0; l < 32; l++) {
+                            const int q5 = ((qs[32 * g + l] >> (4 * h)) & 15) | (((qh[l] >> j) & 1) << 4);
+                            dp += q5 * q[32 * xb + l];
+                        }
+                        int sc, mn;
+                        q4k_scale_min(blk + 4, j, &sc, &mn);
+                        acc += ((dd * (float)sc) * d[xb]) * (float)dp - (dmin * (float)mn) * s[xb];
+                    }
+            }
+            out[r] += acc;
+        }
+        return 0;
+    }
+    if (type == ORC_GGML_Q3_K) {
+        if (cols % 256) return -1;
+        const int ns = cols / 256;
+        for (int r = 0; r < rows; r++) {
+            float acc = 0.0f;
+            for (int b = 0; b < ns; b++) {
+                const uint8_t *blk = w + ((size_t)r * ns + b) * 110, *hm = blk, *qs = blk + 32, *raw = blk + 96;
+                const float dd = orc_f16_to_f32(le16(blk + 108));
+                for (int hf = 0; hf < 2; hf++)
+                    for (int pair = 0; pair < 4; pair++) {   /* Q8_1 block 8b + 4hf + pair */
+                        const int xb = b * 8 + hf * 4 + pair;
+                        float dl[2];
+                        int dp[2] = {0, 0};
+                        for (int w16 = 0; w16 < 2; w16++) {
+                            const int si = hf * 8 + pair * 2 + w16;   /* decodeQ3KScale */
+                            const int lo = si < 8 ? (raw[si & 7] & 15) : (raw[si & 7] >> 4);
+                            const int hi = (raw[8 + (si & 3)] >> ((si >> 2) * 2)) & 3;
+                            dl[w16] = dd * (float)((lo | (hi << 4)) - 32);
+                            for (int l = 0; l < 16; l++) {
+                                const int low = (qs[hf * 32 + w16 * 16 + l] >> (2 * pair)) & 3;
+                                const int hb = (hm[w16 * 16 + l] >> (hf * 4 + pair)) & 1;
+                                dp[w16] += ((low | (hb << 2)) - 4) * q[32 * xb + 16 * w16 + l];
+                            }
+                        }
+                        acc += (dl[0] * d[xb]) * (float)dp[0] + (dl[1] * d[xb]) * (float)dp[1];
+                    }
+            }
+            out[r] += acc;
+        }
+        return 0;
+    }
+    if (type == ORC_GGML_Q5_0 || type == ORC_GGML_IQ4_NL) {
+        if (cols % 32) return -1;
+        const int nb = cols / 32, bs = type == ORC_GGML_Q5_0 ? 22 : 18;
+        for (int r = 0; r < rows; r++) {
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *blk = w + ((size_t)r * nb + b) * bs;
+                const float dd = orc_f16_to_f32(le16(blk));
+                int dp = 0;
+                if (type == ORC_GGML_Q5_0) {
+                    const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) |
+                                        ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+                    for (int l = 0; l < 16; l++) {
+                        const int q0 = ((blk[6 + l] & 15) | (int)(((qh >> l) & 1u) << 4)) - 16;
+                        const int q1 = ((blk[6 + l] >> 4) | (int)(((qh >> (l + 16)) & 1u) << 4)) - 16;
+                        dp += q0 * q[32 * b + l] + q1 * q[32 * b + 16 + l];
+                    }
+                } else {
+                    for (int l = 0; l < 16; l++)
+                        dp += (int)kvalues_iq4nl[blk[2 + l] & 15] * q[32 * b + l] +
+                              (int)kvalues_iq4nl[blk[2 + l] >> 4] * q[32 * b + 16 + l];
+                }
+                acc += (dd * d[b]) * (float)dp;
+            }
+            out[r] += acc;
+        }
+        return 0;
+    }
+    if (type == ORC_GGML_IQ4_XS) {
+        if (cols % 256) return -1;
+        const int ns = cols / 256;
+        for (int r = 0; r < rows; r++) {
+            float acc = 0.0f;
+            for (int b = 0; b < ns; b++) {
+                const uint8_t *blk = w + ((size_t)r * ns + b) * 136;
+                const float dd = orc_f16_to_f32(le16(blk));
+                const uint32_t sh = le16(blk + 2);
+                const uint32_t sl = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) |
+                                    ((uint32_t)blk[7] << 24);
+                for (int ib = 0; ib < 8; ib++) {
+                    const int ls = (int)((sl >> (4 * ib)) & 15) | (int)(((sh >> (2 * ib)) & 3) << 4);
+                    const float dl = dd * (float)(ls - 32);
+                    const int xb = b * 8 + ib;
+                    int dp = 0;
+                    for (int l = 0; l < 16; l++)
+                        dp += (int)kvalues_iq4nl[blk[8 + 16 * ib + l] & 15] * q[32 * xb + l] +
+                              (int)kvalues_iq4nl[blk[8 + 16 * ib + l] >> 4] * q[32 * xb + 16 + l];
+                    acc += (dl * d[xb]) * (float)dp;
+                }
+            }
+            out[r] += acc;
+        }
+        return 0;
+    }
     if (type == ORC_GGML_Q8_0) {
         if (cols % 32) return -1;
         const int nb = cols / 32;
@@ -503,11 +620,20 @@ int orc_matmul_q8_1(int type, const uint8_t *w, int rows, int cols, const int8_t
     return -1;
 }
 
-/* One projection in the Q8_1 mode: the int8 matvec for Q4_K / Q8_0, else the fp32 one. */
+/* The types the reference GPU runs on its Q8_1 input (CudaForwardPass.java:216-226 with
+ * :2029-2038: Q6_K's int8 kernel is opt-in). */
+int orc_q8_1_routed(int type)
+{
+    return type == ORC_GGML_Q4_K || type == ORC_GGML_Q8_0 || type == ORC_GGML_Q5_0 ||
+           type == ORC_GGML_Q3_K || type == ORC_GGML_Q5_K || type == ORC_GGML_IQ4_NL ||
+           type == ORC_GGML_IQ4_XS;
+}
+
+/* One projection in the Q8_1 mode: the int8 matvec for the routed types, else the fp32 one. */
 static int matmul_mode(int q8, int type, const uint8_t *w, int rows, int cols, const float *x,
                        const int8_t *xq, const float *xd, const float *xs, float *out)
 {
-    if (q8 && (type == ORC_GGML_Q4_K || type == ORC_GGML_Q8_0))
+    if (q8 && orc_q8_1_routed(type))
         return orc_matmul_q8_1(type, w, rows, cols, xq, xd, xs, out);
     return orc_matmul(type, w, rows, cols, x, out);
 }

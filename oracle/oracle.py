@@ -155,6 +155,8 @@ def lib():
         L.orc_rmsnorm.argtypes = [_F, _F, _F, C.c_int, C.c_float]
         L.orc_rmsnorm_staged.argtypes = [_F, _F, _F, C.c_int, C.c_float]
         L.orc_quantize_q8_1.argtypes = [_F, C.c_int, C.POINTER(C.c_int8), _F, _F]
+        L.orc_q8_1_routed.restype = C.c_int
+        L.orc_q8_1_routed.argtypes = [C.c_int]
         L.orc_matmul_q8_1.restype = C.c_int
         L.orc_matmul_q8_1.argtypes = [C.c_int, _U8, C.c_int, C.c_int, C.POINTER(C.c_int8), _F, _F,
                                       _F]
@@ -518,9 +520,15 @@ def quantize_q8_1(x):
     return q, d, s
 
 
+def q8_1_routed(t: int) -> bool:
+    """Whether the reference GPU runs type t on its Q8_1 input (CudaForwardPass.java:216-226,
+    2029-2038)."""
+    return bool(lib().orc_q8_1_routed(int(t)))
+
+
 def matmul_q8_1(t: int, w: np.ndarray, rows: int, cols: int, q, d, s, out=None) -> np.ndarray:
-    """The reference GPU's int8 matvec (matmul_q4_k_dp4a.cu / matmul_q8_0_dp4a.cu) on a Q8_1
-    input: out[row] += dot."""
+    """The reference GPU's int8 matvec (matmul_<type>_dp4a*.cu: Q4_K, Q8_0, Q5_0, Q3_K, Q5_K,
+    IQ4_NL, IQ4_XS) on a Q8_1 input: out[row] += dot."""
     w = np.ascontiguousarray(w, np.uint8).reshape(-1)
     q = np.ascontiguousarray(q, np.int8)
     out = np.zeros(rows, np.float32) if out is None else f32(out).copy()
@@ -553,7 +561,7 @@ class BlockWeights:
     v_bias: Optional[np.ndarray] = None
     o_bias: Optional[np.ndarray] = None
     residual_scale: float = 0.0
-    q8_1_input: bool = False     # the reference GPU's Q8_1-input matvecs for Q4_K / Q8_0
+    q8_1_input: bool = False     # the reference GPU's Q8_1-input matvecs (q8_1_routed types)
 
     def c(self):
         keep = []

@@ -99,7 +99,7 @@ def _run(c, dim, max_seq, pos0, steps, types, seed, what, merged=False, bias=Fal
             assert np.array_equal(gk[:pos], kc[:pos]) and np.array_equal(gv[:pos], vc[:pos])
             dc.compare_out(gk[pos], kc[pos], f"block {what} appended K row")
             dc.compare_out(gv[pos], vc[pos], f"block {what} appended V row")
-            if q8 and bw.wo_type in (gp.GGML_Q4_K, gp.GGML_Q8_0):
+            if q8 and orc.q8_1_routed(bw.wo_type):
                 worst = max(worst, _compare_q8_output(got, want, attn, bw, rscale,
                                                       f"block {what} pos {pos}"))
             else:
@@ -238,13 +238,18 @@ def test_block_split_settings_agree():
              what=f"C3 q8_0 splits={splits}", splits=splits)
 
 
-# ---- the Q8_1 input mode (the reference GPU's int8 matvecs for Q4_K and Q8_0) ----------------
+# ---- the Q8_1 input mode (the reference GPU's int8 matvecs: Q4_K, Q8_0, Q5_0, Q3_K, Q5_K, ----
+# ---- IQ4_NL, IQ4_XS; the other formats on the fp32 input) ---------------------------------
 # The oracle quantises the same staged-norm floats, so the int8 operands are the GPU's; the
 # outputs differ by float summation order, and by a rare quantisation tie of the attention
 # output (computed in two orders) ahead of the output projection.
 
-@pytest.mark.parametrize("t", [gp.GGML_Q4_K, gp.GGML_Q8_0, gp.GGML_Q6_K, gp.GGML_F16],
-                         ids=["q4_k", "q8_0", "q6_k-fp32", "f16-fp32"])
+Q8_1_CASES = [gp.GGML_Q4_K, gp.GGML_Q8_0, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL,
+              gp.GGML_IQ4_XS, gp.GGML_Q6_K, gp.GGML_F16, gp.GGML_Q4_0, gp.GGML_MXFP4]
+
+
+@pytest.mark.parametrize("t", Q8_1_CASES,
+                         ids=[NAMES[t] + ("" if orc.q8_1_routed(t) else "-fp32") for t in Q8_1_CASES])
 def test_block_q8_1_input_formats(t):
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
     _run(c, 1024, 64, 40, 2, (t, t, t, t), seed=800 + t, what=f"q8_1 {NAMES[t]}", q8=True)
@@ -256,6 +261,18 @@ def test_block_q8_1_c3_llama3b_q4_k_m_mix():
     c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
     _run(c, 3072, 2048, 2000, 4, (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K),
          seed=810, what="q8_1 C3 Q4_K_M", q8=True)
+
+
+@pytest.mark.parametrize("dim", [2048, 3072, 8192])
+def test_block_q8_1_q3_k_l_and_q5_k_m_mixes(dim):
+    """The Q3_K_L mix (Q3_K and Q5_K rows both on the Q8_1 input in one launch; 8192 columns
+    take a second batch of the Q5_K side's 3 rounds) and the Q5_K_M mix (Q5_K on the Q8_1
+    input next to Q6_K on the fp32 one) in the Q8_1 mode."""
+    c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
+    _run(c, dim, 512, 300, 2, (gp.GGML_Q3_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_Q5_K),
+         seed=850 + dim // 1024, what=f"q8_1 Q3_K_L dim {dim}", q8=True)
+    _run(c, dim, 512, 300, 2, (gp.GGML_Q5_K, gp.GGML_Q5_K, gp.GGML_Q6_K, gp.GGML_Q5_K),
+         seed=860 + dim // 1024, what=f"q8_1 Q5_K_M dim {dim}", q8=True)
 
 
 @pytest.mark.parametrize("dim", [2048, 4096, 8192])

@@ -358,11 +358,17 @@ def test_staged_rmsnorm_matches_float64_and_the_plain_one():
     assert np.array_equal(got, c * F32(1.0 / np.sqrt(9.0)))
 
 
-@pytest.mark.parametrize("t", [gp.GGML_Q8_0, gp.GGML_Q4_K], ids=["q8_0", "q4_k"])
+Q8_1_TYPES = [gp.GGML_Q8_0, gp.GGML_Q4_K, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL,
+              gp.GGML_IQ4_XS]
+
+
+@pytest.mark.parametrize("t", Q8_1_TYPES, ids=[NAMES[t] for t in Q8_1_TYPES])
 def test_q8_1_matmul_equals_the_float_matmul_on_an_exactly_quantised_input(t):
     """On an input that Q8_1 represents exactly (x = d*q, with the block sum exact), the int8
-    matvec is the float matvec of the dequantised weights: the Q4_K min term enters through
-    the block sum, the scales through d."""
+    matvec is the float matvec of the dequantised weights (the independent packer's values):
+    the Q4_K / Q5_K min term enters through the block sum, the scales through d.  A wrong
+    nibble, bit or sign in a format's integer decode, or a scale on the wrong 16 or 32
+    values, moves it far off."""
     rng = np.random.default_rng(43 + t)
     rows, cols = 24, 1024
     wb, vals = gp.random_weights(t, rows, cols, rng)
@@ -400,11 +406,22 @@ def test_q8_1_matmul_integer_closed_form_and_min_term():
     np.testing.assert_allclose(a.astype(np.float64) - b, dmin * m3, rtol=1e-6, atol=1e-9)
 
 
-def test_attn_block_q8_1_mode_routes_only_q4_k_and_q8_0():
-    """Non-dp4a types (F16, Q6_K) take the fp32 path in the Q8_1 mode: the block then differs
-    from the fp32 mode only by the norm's summation order.  Q4_K / Q8_0 blocks move by the
-    input quantisation, within its bound."""
-    for t, tol in ((gp.GGML_F16, 2e-5), (gp.GGML_Q6_K, 2e-5), (gp.GGML_Q4_K, 3e-2), (gp.GGML_Q8_0, 3e-2)):
+def test_q8_1_routed_types_are_the_reference_gpus():
+    """The int8 kernels CudaForwardPass picks by default (dp4aType, CudaForwardPass.java:216-226;
+    Q6_K's is opt-in, :2029-2038)."""
+    routed = {t for t in NAMES if orc.q8_1_routed(t)}
+    assert routed == set(Q8_1_TYPES)
+
+
+def test_attn_block_q8_1_mode_routes_the_reference_gpus_int8_types():
+    """Non-dp4a types (F16, Q6_K, Q4_0, MXFP4) take the fp32 path in the Q8_1 mode: the block
+    then differs from the fp32 mode only by the norm's summation order.  The int8 types' blocks
+    move by the input quantisation (half a step of 1/127 of each block's maximum, times weights
+    whose integer values reach 31 with Q5_K's unsigned codes and their min term): a loose
+    bound that only shows the int8 path was taken; the exact-input test above pins it."""
+    cases = [(t, 2e-5) for t in (gp.GGML_F16, gp.GGML_Q6_K, gp.GGML_Q4_0, gp.GGML_MXFP4)]
+    cases += [(t, 6e-2) for t in Q8_1_TYPES]
+    for t, tol in cases:
         cfg, bw, _, kc, vc, x, pos, cs, sn = _block_setup(150 + t, t)
         kc2, vc2 = kc.copy(), vc.copy()
         a = orc.attn_block(cfg, bw, kc, vc, x, 0, pos, rope_cos=cs, rope_sin=sn)
