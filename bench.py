@@ -778,6 +778,9 @@ def roofline_of(row: dict, ctx: int, kernel: str) -> dict:
     if rp:
         r["rocprof_kernel_mean_us"] = rp
         r["frac_rocprof"] = round(B / (rp * 1e-6) / 1e9 / PEAK_GBPS, 4)
+    if row["plan"]["splits"] > 1 and not row.get("reduce_kernel_us"):
+        r["split_merge"] = ("in the kernel: its last workgroup per KV head merges the splits, "
+                            "so kernel_mean_us includes the merge and no combine kernel runs")
     return r
 
 
