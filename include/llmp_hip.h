@@ -350,6 +350,8 @@ int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int 
 #define LLMP_GGML_IQ4_NL 20  /* split nibbles, as Q5_0                                         */
 #define LLMP_GGML_IQ4_XS 23  /* split nibbles within each sub-block of 32 (its dot() order)   */
 #define LLMP_GGML_MXFP4 39   /* split nibbles; E8M0 exponent byte first                       */
+#define LLMP_GGML_Q5_1   7   /* split nibbles, as Q5_0; value q*d + m                           */
+#define LLMP_GGML_Q2_K  10   /* the reference's order: element j at bits 2(j%4) of qs byte j/4 */
 /* Weight slots of a layer (TransformerLayerWeights): matrices are [rows][cols] in GGUF row
  * order; vectors are fp32. */
 #define LLMP_W_ATTN_NORM      0  /* [dim] attnNorm RMSNorm weights; absent: x is copied (OLMo2) */

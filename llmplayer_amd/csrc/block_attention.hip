@@ -113,6 +113,8 @@ int gemv_unit(int ggml_type) {
     case gk::kIQ4_NL: return gk::FmtIQ4_NL::UNIT;
     case gk::kIQ4_XS: return gk::FmtIQ4_XS::UNIT;
     case gk::kMXFP4: return gk::FmtMXFP4::UNIT;
+    case gk::kQ5_1: return gk::FmtQ5_1::UNIT;
+    case gk::kQ2_K: return gk::FmtQ2_K::UNIT;
     default: return 0;
     }
 }
@@ -169,6 +171,8 @@ hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipS
     case gk::kIQ4_NL: return launch_f<gk::FmtIQ4_NL>(a, st);
     case gk::kIQ4_XS: return launch_f<gk::FmtIQ4_XS>(a, st);
     case gk::kMXFP4: return launch_f<gk::FmtMXFP4>(a, st);
+    case gk::kQ5_1: return launch_f<gk::FmtQ5_1>(a, st);
+    case gk::kQ2_K: return launch_f<gk::FmtQ2_K>(a, st);
     default: return hipErrorInvalidValue;
     }
 }

@@ -22,6 +22,7 @@ namespace gk {
 // GGMLType ids (GGMLType.java:4-35) of the formats with a kernel here.
 constexpr int kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kBF16 = 30;
 constexpr int kQ5_0 = 6, kQ3_K = 11, kQ5_K = 13, kIQ4_NL = 20, kIQ4_XS = 23, kMXFP4 = 39;
+constexpr int kQ5_1 = 7, kQ2_K = 10;
 
 // One weight matrix on the device: up to four planes, each [rows][pitch bytes].
 struct WPlanes {
@@ -560,6 +561,67 @@ struct FmtQ3_K {
                                  x4(st.xs, sb * 256 + 128 * h + 32 * p + 16 * w + l));
         }
         return s;
+    }
+};
+
+// Q5_1: plane 0 = nibbles [rows][cols/2], plane 1 = the fifth bits of each block (uint32),
+// planes 2 and 3 = d and m [rows][cols/32] fp16.  Values q * d + m (Q5_1FloatTensor.getFloat),
+// summed as d * sum(q x) + m * sum(x) (Q5_1FloatTensor.dot: scale * blockSum + min * otherSum).
+struct FmtQ5_1 {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = true, Q8IN = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    struct Raw { unsigned q, qh; unsigned short d, m; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        const unsigned b = (unsigned)u >> 2;
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u), ldo<unsigned>(rp(w, 1, row), b * 4u),
+                   ldo<unsigned short>(rp(w, 2, row), b * 2u), ldo<unsigned short>(rp(w, 3, row), b * 2u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned h = r.qh >> (4 * (j & 3));
+        unsigned lo = (r.q & 0x0F0F0F0Fu) | (spread4(h & 15u) << 4);
+        unsigned hi = ((r.q >> 4) & 0x0F0F0F0Fu) | (spread4((h >> 16) & 15u) << 4);
+        asm("" : "+v"(lo), "+v"(hi));   // keep the byte conversions (see FmtQ4_K::dot)
+        const int xi = split_x(ub, j);
+        const float s = dot4(byte_f(lo, 0), byte_f(lo, 1), byte_f(lo, 2), byte_f(lo, 3), x4(st.xs, xi)) +
+                        dot4(byte_f(hi, 0), byte_f(hi, 1), byte_f(hi, 2), byte_f(hi, 3), x4(st.xs, xi + 16));
+        return h2f(r.d) * s + h2f(r.m) * (st.xsum[xi >> 2] + st.xsum[(xi + 16) >> 2]);
+    }
+};
+
+// Q2_K in the reference's layout (Q2_KFloatTensor): element j of a super-block is bits
+// 2(j%4) .. +1 of quant byte j/4, sub-block j/16 takes scale byte j/16 (low nibble sc, high
+// nibble m).  Plane 0 = the 64 quant bytes [rows][cols/4], plane 1 = the 16 scale bytes
+// [rows][cols/16], planes 2 and 3 = d and dmin [rows][cols/256] fp16.  Values d*sc*q - dmin*m,
+// summed per sub-block as (d*sc) * sum(q x) - (dmin*m) * sum(x) (Q2_KFloatTensor.dotQ2KF32).
+// Unit u = 4 quant bytes = sub-block u (16 consecutive weights).
+struct FmtQ2_K {
+    static constexpr int UNIT = 16, MAXU = 8, TAB = 0;
+    static constexpr bool XSUM = true, Q8IN = false;
+    using Row = NoRow;
+    static __device__ __forceinline__ Row load_row(const WPlanes&, int, int, int) { return Row{}; }
+    static __device__ __forceinline__ void build_tab(const Row&, float*, int, int) {}
+    struct Raw { unsigned q; unsigned char sc; unsigned short d, dm; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        const unsigned sb = (unsigned)u >> 4;
+        return Raw{ldo<unsigned>(rp(w, 0, row), (unsigned)u * 4u), ldo<unsigned char>(rp(w, 1, row), (unsigned)u),
+                   ldo<unsigned short>(rp(w, 2, row), sb * 2u), ldo<unsigned short>(rp(w, 3, row), sb * 2u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const int i0 = 16 * (ub + j);   // the sub-block's first weight
+        const float4 x0 = x4(st.xs, i0), x1 = x4(st.xs, i0 + 4), x2 = x4(st.xs, i0 + 8), x3 = x4(st.xs, i0 + 12);
+        // field t of byte b is weight 4b + t: one masked word per t, its bytes the weights
+        // t, 4 + t, 8 + t, 12 + t
+        const unsigned m0 = r.q & 0x03030303u, m1 = (r.q >> 2) & 0x03030303u;
+        const unsigned m2 = (r.q >> 4) & 0x03030303u, m3 = (r.q >> 6) & 0x03030303u;
+        const float s = dot4(byte_f(m0, 0), byte_f(m0, 1), byte_f(m0, 2), byte_f(m0, 3), float4{x0.x, x1.x, x2.x, x3.x}) +
+                        dot4(byte_f(m1, 0), byte_f(m1, 1), byte_f(m1, 2), byte_f(m1, 3), float4{x0.y, x1.y, x2.y, x3.y}) +
+                        dot4(byte_f(m2, 0), byte_f(m2, 1), byte_f(m2, 2), byte_f(m2, 3), float4{x0.z, x1.z, x2.z, x3.z}) +
+                        dot4(byte_f(m3, 0), byte_f(m3, 1), byte_f(m3, 2), byte_f(m3, 3), float4{x0.w, x1.w, x2.w, x3.w});
+        const float xs = (st.xsum[i0 >> 2] + st.xsum[(i0 >> 2) + 1]) + (st.xsum[(i0 >> 2) + 2] + st.xsum[(i0 >> 2) + 3]);
+        return (h2f(r.d) * (float)(r.sc & 15u)) * s - (h2f(r.dm) * (float)(r.sc >> 4)) * xs;
     }
 };
 

@@ -116,6 +116,8 @@ inline size_t ggml_row_bytes(int type, int cols) {
     case LLMP_GGML_IQ4_NL: return (size_t)(cols / 32) * 18;
     case LLMP_GGML_IQ4_XS: return (size_t)(cols / 256) * 136;
     case LLMP_GGML_MXFP4: return (size_t)(cols / 32) * 17;
+    case LLMP_GGML_Q5_1: return (size_t)(cols / 32) * 24;
+    case LLMP_GGML_Q2_K: return (size_t)(cols / 256) * 84;
     default: return 0;
     }
 }
@@ -194,6 +196,8 @@ inline void range_exp_rows_q8(const int8_t* q, const float* s, size_t H, size_t 
 //  - IQ4_NL: nibble codes -> 0, fp16 scale -> 1;
 //  - IQ4_XS: nibble codes -> 0, the 8 scales decoded to int8 ls - 32 -> 1, fp16 d -> 2;
 //  - MXFP4: nibble codes -> 0, E8M0 exponent byte -> 1;
+//  - Q5_1: nibbles -> 0, the 32 fifth bits (uint32) -> 1, fp16 d -> 2, fp16 m -> 3;
+//  - Q2_K: the 64 quant bytes -> 0, the 16 scale/min bytes -> 1, fp16 d -> 2, fp16 dmin -> 3;
 //  - F32/F16/BF16: one plane, the rows unchanged.
 // Returns the plane count, or 0 for an unsupported type or a cols that is not a whole number
 // of blocks.
@@ -247,6 +251,14 @@ inline int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
     case LLMP_GGML_MXFP4:
         n = 2; bw = 32; blk_bytes = 17; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32;
         set({{1, 0, 1}, {0, 1, 16}}); break;
+    case LLMP_GGML_Q5_1:
+        n = 4; bw = 32; blk_bytes = 24; pitch[0] = (size_t)cols / 2; pitch[1] = (size_t)cols / 32 * 4;
+        pitch[2] = pitch[3] = (size_t)cols / 32 * 2;
+        set({{2, 0, 2}, {3, 2, 2}, {1, 4, 4}, {0, 8, 16}}); break;
+    case LLMP_GGML_Q2_K:
+        n = 4; bw = 256; blk_bytes = 84; pitch[0] = (size_t)cols / 4; pitch[1] = (size_t)cols / 16;
+        pitch[2] = pitch[3] = (size_t)cols / 256 * 2;
+        set({{1, 0, 16}, {0, 16, 64}, {2, 80, 2}, {3, 82, 2}}); break;
     default: return 0;
     }
     if (bw && cols % (int)bw) return 0;

@@ -49,8 +49,9 @@ struct DevWeight {
     void* mem = nullptr;
     gk::WPlanes planes{};
     // The token-batched projections split fp32 and bf16 weights into fp16 parts: false when
-    // some weight reaches fp16's largest magnitude, 65504 (llmp_attn_block_batch then runs the
-    // tokens one by one, on the fp32 single-token kernels).
+    // some weight reaches fp16's largest magnitude, 65504, or for a type without a
+    // token-batched kernel (Q2_K) (llmp_attn_block_batch then runs the tokens one by one, on
+    // the fp32 single-token kernels).
     bool tok_ok = true;
 };
 
@@ -1206,6 +1207,7 @@ int llmp_layer_weight(uint64_t handle, int layer, int slot, int ggml_type, int r
         return fail(LLMP_ERR_OUT_OF_MEMORY, "llmp_layer_weight: %zu bytes", packed.size());
     LLMP_HIP_CHECK(e, "hipMalloc(weight)");
     LLMP_HIP_CHECK(hipMemcpy(w.mem, packed.data(), packed.size(), hipMemcpyHostToDevice), "hipMemcpy(weight)");
+    w.tok_ok = vec || proj_tok_supported(ggml_type);
     if (!vec && (ggml_type == LLMP_GGML_F32 || ggml_type == LLMP_GGML_BF16)) {
         const size_t n = (size_t)rows * cols;
         for (size_t i = 0; i < n && w.tok_ok; ++i) {
@@ -1417,8 +1419,8 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
                                                      : W[LLMP_W_Q].tok_ok && W[LLMP_W_K].tok_ok &&
                                                            W[LLMP_W_V].tok_ok);
     if (kv->blk_input == LLMP_INPUT_Q8_1 || prefill_tile_keys(D) <= 0 || !w_ok) {
-        // the Q8_1 contract's int8 dot products, a head size with decode kernels only, or fp32 /
-        // bf16 weights beyond fp16's range
+        // the Q8_1 contract's int8 dot products, a head size with decode kernels only, fp32 /
+        // bf16 weights beyond fp16's range, or a type without a token-batched kernel
         for (int t = 0; t < n_tokens; ++t)
             if (int rc = enqueue_block(kv, layer, pos0 + t, 0, x + (uint64_t)t * dim * sizeof(float), 0,
                                        stream))

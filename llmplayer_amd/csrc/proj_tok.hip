@@ -34,7 +34,7 @@ bool proj_tok_supported(int ggml_type) {
     switch (ggml_type) {
     case gk::kF32: case gk::kF16: case gk::kBF16: case gk::kQ8_0: case gk::kQ4_0: case gk::kQ4_K:
     case gk::kQ6_K: case gk::kQ5_0: case gk::kQ3_K: case gk::kQ5_K: case gk::kIQ4_NL: case gk::kIQ4_XS:
-    case gk::kMXFP4:
+    case gk::kMXFP4: case gk::kQ5_1:
         return true;
     default:
         return false;
@@ -80,6 +80,7 @@ hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_
     case gk::kIQ4_NL: return launch_ff<tk::PIQ4_NL, tk::PIQ4_NL>(a, st);
     case gk::kIQ4_XS: return launch_ff<tk::PIQ4_XS, tk::PIQ4_XS>(a, st);
     case gk::kMXFP4: return launch_ff<tk::PMXFP4, tk::PMXFP4>(a, st);
+    case gk::kQ5_1: return launch_ff<tk::PQ5_1, tk::PQ5_1>(a, st);
     default: return hipErrorInvalidValue;
     }
 }

@@ -337,6 +337,43 @@ struct PQ5_0 {
     }
 };
 
+// Q5_1: values q (0..31) with the fifth bits as Q5_0's; value q * d + m, so the group's input
+// sum carries the min: table (d, -m) of block kq (the MIN path adds f.x * t0 - f.y * gs).
+struct PQ5_1 {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 8;
+    static constexpr bool MIN = true, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    struct Raw { uint2 q[4]; unsigned qh[4]; unsigned short d, m; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int blk = ch * 4 + min(b, ng - 1);
+            r.q[b] = ldo<uint2>(rp(w, 0, row), (unsigned)(blk * 16 + 8 * (kq & 1)));
+            r.qh[b] = ldo<unsigned>(rp(w, 1, row), (unsigned)blk * 4u);
+        }
+        const unsigned bk = (unsigned)(ch * 4 + min(kq, ng - 1)) * 2u;
+        r.d = ldo<unsigned short>(rp(w, 2, row), bk);
+        r.m = ldo<unsigned short>(rp(w, 3, row), bk);
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int) {
+        reinterpret_cast<float2*>(tab + m * TAB)[kq] = make_float2(h2f(r.d), -h2f(r.m));
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        unsigned c0, c1;
+        split_codes(r.q[gi], kq, c0, c1);
+        const unsigned h = r.qh[gi] >> (8 * kq);
+        c0 |= gk::spread4(h & 15u) << 4;
+        c1 |= gk::spread4((h >> 4) & 15u) << 4;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = (float)((c0 >> (8 * e)) & 0xFFu);
+            v[4 + e] = (float)((c1 >> (8 * e)) & 0xFFu);
+        }
+        a[0] = f16x8_of(v);
+    }
+};
+
 // IQ4_NL: values codebook[code].  Table: d of block kq.
 struct PIQ4_NL {
     static constexpr int NA = 1, NPAIR = 2, TAB = 4;

@@ -8,8 +8,8 @@
  * (TransformerBlock.java, attention half), and Attention.forward's Q/K/V projections, biases
  * and output projection (Attention.java:76-110, 232-238), over projection weights in the GGUF
  * block formats of the reference's tensor classes (the tensor package's FloatTensor classes):
- *   F32 (0), F16 (1), Q4_0 (2), Q5_0 (6), Q8_0 (8), Q3_K (11), Q4_K (12), Q5_K (13),
- *   Q6_K (14), IQ4_NL (20), IQ4_XS (23), BF16 (30), MXFP4 (39)  (GGMLType ids).
+ *   F32 (0), F16 (1), Q4_0 (2), Q5_0 (6), Q5_1 (7), Q8_0 (8), Q2_K (10), Q3_K (11), Q4_K (12),
+ *   Q5_K (13), Q6_K (14), IQ4_NL (20), IQ4_XS (23), BF16 (30), MXFP4 (39)  (GGMLType ids).
  *
  * Dequantised weights are bit-identical to what each class's dot() stages (or getFloat()
  * returns); a row's dot follows the scalar classes of the java/ tree: F32 one
@@ -34,6 +34,8 @@
 #define ORC_GGML_F16 1
 #define ORC_GGML_Q4_0 2
 #define ORC_GGML_Q5_0 6
+#define ORC_GGML_Q5_1 7
+#define ORC_GGML_Q2_K 10
 #define ORC_GGML_Q8_0 8
 #define ORC_GGML_Q3_K 11
 #define ORC_GGML_Q4_K 12
@@ -114,6 +116,8 @@ int orc_ggml_block(int type, int *bytes)
     case ORC_GGML_BF16: *bytes = 2; return 1;
     case ORC_GGML_Q4_0: *bytes = 18; return 32;
     case ORC_GGML_Q5_0: *bytes = 22; return 32;
+    case ORC_GGML_Q5_1: *bytes = 24; return 32;
+    case ORC_GGML_Q2_K: *bytes = 84; return 256;
     case ORC_GGML_Q8_0: *bytes = 34; return 32;
     case ORC_GGML_Q3_K: *bytes = 110; return 256;
     case ORC_GGML_Q4_K: *bytes = 144; return 256;
@@ -197,6 +201,26 @@ static void dequant_block(int type, const uint8_t *b, float *out)
             int nib = i < 16 ? (b[6 + i] & 0x0F) : ((b[6 + i - 16] >> 4) & 0x0F);
             int q = nib | (int)(((qh >> i) & 1u) << 4);
             out[i] = (float)(q - 16) * scale;
+        }
+        break;
+    }
+    case ORC_GGML_Q5_1: {   /* Q5_1FloatTensor.getFloat: quant * scale + min, split nibbles */
+        float scale = orc_f16_to_f32(le16(b)), mn = orc_f16_to_f32(le16(b + 2));
+        uint32_t qh = (uint32_t)b[4] | ((uint32_t)b[5] << 8) | ((uint32_t)b[6] << 16) | ((uint32_t)b[7] << 24);
+        for (int i = 0; i < 32; i++) {
+            int nib = i < 16 ? (b[8 + i] & 0x0F) : ((b[8 + i - 16] >> 4) & 0x0F);
+            int q = nib | (int)(((qh >> i) & 1u) << 4);
+            out[i] = (float)q * scale + mn;
+        }
+        break;
+    }
+    case ORC_GGML_Q2_K: {   /* Q2_KFloatTensor.getFloat: d * sc * q - dmin * m, element j at
+                               bits 2(j%4) of qs byte j/4, scale byte j/16 */
+        float d = orc_f16_to_f32(le16(b + 80)), dmin = orc_f16_to_f32(le16(b + 82));
+        for (int j = 0; j < 256; j++) {
+            int sc = b[j / 16] & 0x0F, m = b[j / 16] >> 4;
+            int q = (b[16 + j / 4] >> (2 * (j % 4))) & 3;
+            out[j] = d * (float)sc * (float)q - dmin * (float)m;
         }
         break;
     }
@@ -337,6 +361,43 @@ static float row_dot(int type, const uint8_t *row, int cols, const float *x, flo
                 sum += (float)(q1 - 16) * x[b * 32 + j + 16];
             }
             result += scale * sum;
+        }
+        return result;
+    }
+    if (type == ORC_GGML_Q5_1) {   /* Q5_1FloatTensor.dot: scale * blockSum + min * otherSum */
+        for (int b = 0; b < cols / n; b++) {
+            const uint8_t *blk = row + (size_t)b * bytes;
+            float scale = orc_f16_to_f32(le16(blk)), mn = orc_f16_to_f32(le16(blk + 2));
+            uint32_t qh = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) |
+                          ((uint32_t)blk[7] << 24);
+            float bsum = 0.0f, osum = 0.0f;
+            for (int j = 0; j < 16; j++) {
+                int q0 = (blk[8 + j] & 0x0F) | (int)(((qh >> j) & 1u) << 4);
+                int q1 = ((blk[8 + j] >> 4) & 0x0F) | (int)(((qh >> (j + 16)) & 1u) << 4);
+                bsum += (float)q0 * x[b * 32 + j];
+                bsum += (float)q1 * x[b * 32 + j + 16];
+                osum += x[b * 32 + j] + x[b * 32 + j + 16];
+            }
+            result += scale * bsum + mn * osum;
+        }
+        return result;
+    }
+    if (type == ORC_GGML_Q2_K) {   /* Q2_KFloatTensor.dotQ2KF32: per sub-block of 16 */
+        for (int b = 0; b < cols / n; b++) {
+            const uint8_t *blk = row + (size_t)b * bytes;
+            float d = orc_f16_to_f32(le16(blk + 80)), dmin = orc_f16_to_f32(le16(blk + 82));
+            for (int sb = 0; sb < 16; sb++) {
+                int sc = blk[sb] & 0x0F, m = blk[sb] >> 4;
+                float sum_q = 0.0f, sum_f = 0.0f;
+                for (int i = 0; i < 16; i++) {
+                    int j = sb * 16 + i;
+                    int q = (blk[16 + j / 4] >> (2 * (j % 4))) & 3;
+                    float f = x[b * 256 + j];
+                    sum_q += (float)q * f;
+                    sum_f += f;
+                }
+                result += d * (float)sc * sum_q - dmin * (float)m * sum_f;
+            }
         }
         return result;
     }

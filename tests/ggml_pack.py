@@ -13,6 +13,7 @@ import numpy as np
 F32 = np.float32
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 14, 30
 GGML_Q5_0, GGML_Q3_K, GGML_Q5_K, GGML_IQ4_NL, GGML_IQ4_XS, GGML_MXFP4 = 6, 11, 13, 20, 23, 39
+GGML_Q5_1, GGML_Q2_K = 7, 10
 
 # the non-linear 4-bit codebook of IQ4_NL and IQ4_XS (GGUF's kvalues_iq4nl)
 IQ4NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], F32)
@@ -144,6 +145,43 @@ def pack_q5_0(d_bits, q):
     out[:, :, 2:6] = qh.sum(-1).astype(np.uint32)[..., None].view(np.uint8).reshape(rows, nb, 4)
     out[:, :, 6:] = _split_nibbles(qq & 15)
     vals = ((qq - 16).astype(F32) * _f16_val(d_bits)[..., None]).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_q5_1(d_bits, m_bits, q):
+    """Blocks of 32 (24 bytes): d fp16, m fp16, qh (uint32: bit i = bit 4 of element i), 16 bytes
+    of split nibbles.  q [rows, nb*32] in 0..31; value q * d + m (two float roundings)."""
+    rows, nb = d_bits.shape
+    qq = np.asarray(q, np.int64).reshape(rows, nb, 32)
+    out = np.zeros((rows, nb, 24), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, nb, 2)
+    out[:, :, 2:4] = np.asarray(m_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, nb, 2)
+    qh = ((qq >> 4) & 1) << np.arange(32)
+    out[:, :, 4:8] = qh.sum(-1).astype(np.uint32)[..., None].view(np.uint8).reshape(rows, nb, 4)
+    out[:, :, 8:] = _split_nibbles(qq & 15)
+    prod = (qq.astype(F32) * _f16_val(d_bits)[..., None]).astype(F32)
+    vals = (prod + _f16_val(m_bits)[..., None]).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_q2_k(d_bits, dmin_bits, sc, mn, q):
+    """Super-blocks of 256 (84 bytes) in the reference's element order: 16 scale bytes (sub-block
+    s of 16: low nibble sc, high nibble m), 64 quant bytes (element j at bits 2(j%4)..+1 of byte
+    j/4), d fp16, dmin fp16.  sc, mn [rows, ns, 16] in 0..15, q [rows, ns*256] in 0..3; value
+    ((d*sc)*q) - (dmin*m)."""
+    rows, ns = d_bits.shape
+    qq = np.asarray(q, np.int64).reshape(rows, ns, 64, 4)
+    out = np.zeros((rows, ns, 84), np.uint8)
+    out[:, :, 0:16] = (np.asarray(sc, np.int64) | (np.asarray(mn, np.int64) << 4)).astype(np.uint8)
+    out[:, :, 16:80] = sum(qq[..., t] << (2 * t) for t in range(4)).astype(np.uint8)
+    out[:, :, 80:82] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    out[:, :, 82:84] = np.asarray(dmin_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    d = _f16_val(d_bits)[..., None]
+    dmin = _f16_val(dmin_bits)[..., None]
+    dsc = (d * np.asarray(sc, np.int64).astype(F32)).astype(F32)            # [rows, ns, 16]
+    dm = (dmin * np.asarray(mn, np.int64).astype(F32)).astype(F32)
+    qv = np.asarray(q, np.int64).reshape(rows, ns, 16, 16).astype(F32)
+    vals = ((dsc[..., None] * qv).astype(F32) - dm[..., None]).astype(F32)
     return out.reshape(rows, -1), vals.reshape(rows, -1)
 
 
@@ -299,4 +337,15 @@ def random_weights(t, rows, cols, rng, scale=0.05):
     if t == GGML_MXFP4:
         nb = cols // 32
         return pack_mxfp4(rng.integers(119, 124, (rows, nb)), rng.integers(0, 16, (rows, cols)))
+    if t == GGML_Q5_1:
+        nb = cols // 32
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, nb)) * scale / 8)
+        m = _f16_bits(-rng.uniform(0.5, 1.5, (rows, nb)) * scale * 2)   # centred: q*d + m around 0
+        return pack_q5_1(d, m, rng.integers(0, 32, (rows, cols)))
+    if t == GGML_Q2_K:
+        ns = cols // 256
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 8)
+        dmin = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 8)
+        return pack_q2_k(d, dmin, rng.integers(0, 16, (rows, ns, 16)), rng.integers(0, 16, (rows, ns, 16)),
+                         rng.integers(0, 4, (rows, cols)))
     raise ValueError(t)

@@ -69,9 +69,10 @@ def _compare_block(got, want, what):
 
 def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=False,
                post=False, pre=True, rscale=0.0, qk=None, q8=False, sinks=None, layer=0,
-               rounds=1, batched=False):
+               rounds=1, batched=False, per_token=False):
     """`rounds` batched calls of K tokens each, from position pos0 on layer `layer` of c, each
-    token checked against sequential orc.attn_block calls.  batched: also check that the calls
+    token checked against sequential orc.attn_block calls.  per_token: check that the calls ran
+    one single-token decode per token.  batched: also check that the calls
     took the matrix-core path (no single-token decode launch: the profile counters)."""
     rng = np.random.default_rng(seed)
     lw, bw = _weights(c, dim, types, rng, merged, bias, post, pre)
@@ -91,7 +92,7 @@ def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=F
         fp.kv.write(layer, 0, kc, vc)
         fp.setBlockConfig(dim, rscale, _lib.LLMP_INPUT_Q8_1 if q8 else _lib.LLMP_INPUT_F32)
         fp.uploadLayerWeights(layer, lw)
-        if batched:
+        if batched or per_token:
             _lib.call("llmp_profile_enable", fp.kv.handle, 1)
         worst = 0.0
         p0 = pos0
@@ -115,6 +116,10 @@ def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=F
             # continue from the device's rows
             kc[p0:p0 + K], vc[p0:p0 + K] = gk[p0:p0 + K], gv[p0:p0 + K]
             p0 += K
+        if per_token:
+            n, ms = C.c_int(), C.c_double()
+            _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(n), C.byref(ms))
+            assert n.value == rounds * K, f"{what}: {n.value} single-token decode launches"
         if batched:
             n, ms = C.c_int(), C.c_double()
             _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(n), C.byref(ms))
@@ -130,8 +135,13 @@ TYPES = tbg.TYPES
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
 def test_block_batch_every_weight_format(t):
     """Each format's matrix-core path: 5 tokens (a partial token tile) after a 40-row prefix,
-    then 3 more."""
+    then 5 more.  Q2_K has no token-batched kernel: its tokens run one by one (ten single-token
+    decode launches), with the same results."""
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    if t == gp.GGML_Q2_K:
+        _run_batch(c, 1024, 64, 40, 5, (t, t, t, t), seed=1600 + t, what=NAMES[t], rounds=2,
+                   per_token=True)
+        return
     _run_batch(c, 1024, 64, 40, 5, (t, t, t, t), seed=1600 + t, what=NAMES[t], rounds=2, batched=True)
 
 

@@ -21,9 +21,9 @@ pytestmark = pytest.mark.gpu
 F32 = np.float32
 TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
          gp.GGML_Q6_K, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL, gp.GGML_IQ4_XS,
-         gp.GGML_MXFP4]
+         gp.GGML_MXFP4, gp.GGML_Q5_1, gp.GGML_Q2_K]
 NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k", 6: "q5_0",
-         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4"}
+         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k"}
 
 
 def _tensor(t, rows, cols, rng, scale=0.05):
@@ -142,7 +142,8 @@ def test_block_every_weight_format(t):
 
 
 WIDE = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q5_0,
-        gp.GGML_IQ4_NL, gp.GGML_MXFP4, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS]
+        gp.GGML_IQ4_NL, gp.GGML_MXFP4, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS, gp.GGML_Q5_1,
+        gp.GGML_Q2_K]
 
 
 @pytest.mark.parametrize("t", WIDE, ids=[NAMES[t] for t in WIDE])
@@ -331,7 +332,7 @@ def test_block_error_codes():
         assert _lib.status("llmp_attn_block", h, 0, 3, 0, x, 0, 0) == 1               # no weights yet
         w = np.zeros(512 * 512 * 4, np.uint8)
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 128, 512, w.ctypes.data, 128 * 512 * 4) == 1  # rows != q_dim
-        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 10, 512, 512, w.ctypes.data, 512 * 84 // 256 * 512) == 6  # Q2_K: no kernel
+        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 22, 512, 512, w.ctypes.data, 512 * 82 // 256 * 512) == 6  # IQ2_S: no kernel
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 512, 512, w.ctypes.data, 100) == 1   # byte count
         assert _lib.status("llmp_layer_weight", h, 0, 11, 0, 1, 512, w.ctypes.data, 2048) == 1  # bad slot
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_ATTN_NORM, 8, 1, 512, w.ctypes.data, 2048) == 1  # vector not fp32

@@ -15,9 +15,9 @@ from tests import refmath as rm
 F32 = np.float32
 TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
          gp.GGML_Q6_K, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL, gp.GGML_IQ4_XS,
-         gp.GGML_MXFP4]
+         gp.GGML_MXFP4, gp.GGML_Q5_1, gp.GGML_Q2_K]
 NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k", 6: "q5_0",
-         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4"}
+         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k"}
 
 
 def test_f16_conversion_matches_ieee_half_for_every_pattern():
@@ -174,6 +174,82 @@ def test_iq4_xs_sub_block_scales_and_split_nibbles():
             want[16] = (ls[0, 0, 0] - 32) * 113
         assert np.array_equal(seg, want), ib
     assert wb[0, 8] == (8 | (15 << 4))
+
+
+def test_q5_1_split_nibbles_fifth_bit_and_min():
+    # element i < 16: low nibble of byte i; 16 + i: its high nibble; bit 4 from qh bit i;
+    # value q * d + m (Q5_1FloatTensor.getFloat), here d = 1, m = 0.5
+    q = np.zeros((1, 32), np.int64)
+    q[0, 3], q[0, 20], q[0, 31], q[0, 16] = 5, 17, 31, 16
+    wb, vals = gp.pack_q5_1(np.array([[0x3C00]], np.uint16), np.array([[0x3800]], np.uint16), q)
+    assert wb[0, 8 + 3] == 5 and wb[0, 8 + 4] == (1 << 4) and wb[0, 8 + 0] == 0
+    qh = int.from_bytes(bytes(wb[0, 4:8]), "little")
+    assert qh == (1 << 20) | (1 << 31) | (1 << 16)
+    got = orc.dequant_rows(gp.GGML_Q5_1, wb, 1, 32)[0]
+    want = q[0].astype(F32) + F32(0.5)
+    assert np.array_equal(got, want) and np.array_equal(got, vals[0])
+
+
+def test_q5_1_row_dot_restates_the_java_loop():
+    # Q5_1FloatTensor.dot: blockSum += q0*x[j]; blockSum += q1*x[j+16]; otherSum += x[j] +
+    # x[j+16] for j < 16, then result += scale*blockSum + min*otherSum, block by block
+    rng = np.random.default_rng(17)
+    wb, _ = gp.random_weights(gp.GGML_Q5_1, 1, 96, rng)
+    x = rng.standard_normal(96).astype(F32)
+    blk = wb[0].reshape(3, 24)
+    res = F32(0)
+    for b_ in range(3):
+        d = np.frombuffer(bytes(blk[b_, 0:2]), np.float16)[0].astype(F32)
+        m = np.frombuffer(bytes(blk[b_, 2:4]), np.float16)[0].astype(F32)
+        qh = int.from_bytes(bytes(blk[b_, 4:8]), "little")
+        bs = os_ = F32(0)
+        for j in range(16):
+            q0 = (blk[b_, 8 + j] & 15) | (((qh >> j) & 1) << 4)
+            q1 = (blk[b_, 8 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4)
+            bs = F32(bs + F32(F32(int(q0)) * x[32 * b_ + j]))
+            bs = F32(bs + F32(F32(int(q1)) * x[32 * b_ + j + 16]))
+            os_ = F32(os_ + F32(x[32 * b_ + j] + x[32 * b_ + j + 16]))
+        res = F32(res + F32(F32(d * bs) + F32(m * os_)))
+    assert orc.matmul(gp.GGML_Q5_1, wb, 1, 96, x)[0] == res
+
+
+def test_q2_k_reference_element_order_and_sub_block_scales():
+    # the reference's order (Q2_KFloatTensor.getFloat): element j at bits 2(j%4) of quant byte
+    # j/4 (not ggml's interleave of 32-element runs); scale byte j/16: low nibble sc, high m;
+    # value d*sc*q - dmin*m, here d = dmin = 1
+    rng = np.random.default_rng(21)
+    q = rng.integers(0, 4, (1, 256))
+    sc = rng.integers(0, 16, (1, 1, 16))
+    mn = rng.integers(0, 16, (1, 1, 16))
+    one = np.array([[0x3C00]], np.uint16)
+    wb, vals = gp.pack_q2_k(one, one, sc, mn, q)
+    for j in (0, 1, 5, 22, 255):
+        assert (wb[0, 16 + j // 4] >> (2 * (j % 4))) & 3 == q[0, j]
+    assert wb[0, 7] == sc[0, 0, 7] | (mn[0, 0, 7] << 4)
+    got = orc.dequant_rows(gp.GGML_Q2_K, wb, 1, 256)[0]
+    want = (np.repeat(sc[0, 0], 16) * q[0] - np.repeat(mn[0, 0], 16)).astype(F32)
+    assert np.array_equal(got, want) and np.array_equal(got, vals[0])
+
+
+def test_q2_k_row_dot_restates_dotq2kf32():
+    # per sub-block of 16: sumQ += q*f, sumF += f; result += d*sc*sumQ - dmin*m*sumF
+    rng = np.random.default_rng(22)
+    wb, _ = gp.random_weights(gp.GGML_Q2_K, 1, 256, rng)
+    x = rng.standard_normal(256).astype(F32)
+    blk = wb[0]
+    d = np.frombuffer(bytes(blk[80:82]), np.float16)[0].astype(F32)
+    dmin = np.frombuffer(bytes(blk[82:84]), np.float16)[0].astype(F32)
+    res = F32(0)
+    for sb in range(16):
+        sc, m = int(blk[sb] & 15), int(blk[sb] >> 4)
+        sq = sf = F32(0)
+        for i in range(16):
+            j = 16 * sb + i
+            q = (int(blk[16 + j // 4]) >> (2 * (j % 4))) & 3
+            sq = F32(sq + F32(F32(q) * x[j]))
+            sf = F32(sf + x[j])
+        res = F32(res + F32(F32(F32(d * F32(sc)) * sq) - F32(F32(dmin * F32(m)) * sf)))
+    assert orc.matmul(gp.GGML_Q2_K, wb, 1, 256, x)[0] == res
 
 
 def test_mxfp4_scale_exponent_and_special_bytes():

@@ -65,6 +65,9 @@ BLOCKS = {
     gp.GGML_IQ4_NL: (32, [("d", 2), ("qs", 16)], {"qs": 0, "d": 1}),
     gp.GGML_IQ4_XS: (256, [("d", 2), ("scales_h", 2), ("scales_l", 4), ("qs", 128)], {"qs": 0, "d": 2}),
     gp.GGML_MXFP4: (32, [("e", 1), ("qs", 16)], {"qs": 0, "e": 1}),
+    gp.GGML_Q5_1: (32, [("d", 2), ("m", 2), ("qh", 4), ("qs", 16)], {"qs": 0, "qh": 1, "d": 2, "m": 3}),
+    gp.GGML_Q2_K: (256, [("scales", 16), ("qs", 64), ("d", 2), ("dmin", 2)],
+                   {"qs": 0, "scales": 1, "d": 2, "dmin": 3}),
 }
 
 
@@ -115,9 +118,10 @@ def _expected_planes(t, rows, cols, raw):
 
 
 CASES = [(t, rows, cols) for t in (gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0,
-                                  gp.GGML_Q5_0, gp.GGML_IQ4_NL, gp.GGML_MXFP4)
+                                  gp.GGML_Q5_0, gp.GGML_IQ4_NL, gp.GGML_MXFP4, gp.GGML_Q5_1)
          for rows, cols in ((1, 32), (3, 96), (17, 2880))] + \
-        [(t, rows, cols) for t in (gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS)
+        [(t, rows, cols) for t in (gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS,
+                                  gp.GGML_Q2_K)
          for rows, cols in ((1, 256), (5, 768), (33, 3072))]
 
 
