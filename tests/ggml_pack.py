@@ -343,9 +343,10 @@ def random_weights(t, rows, cols, rng, scale=0.05):
         m = _f16_bits(-rng.uniform(0.5, 1.5, (rows, nb)) * scale * 2)   # centred: q*d + m around 0
         return pack_q5_1(d, m, rng.integers(0, 32, (rows, cols)))
     if t == GGML_Q2_K:
+        # centred, as a quantiser's are: dmin = d and m about 1.5 sc, the codes' mean
         ns = cols // 256
         d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 8)
-        dmin = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 8)
-        return pack_q2_k(d, dmin, rng.integers(0, 16, (rows, ns, 16)), rng.integers(0, 16, (rows, ns, 16)),
-                         rng.integers(0, 4, (rows, cols)))
+        sc = rng.integers(0, 11, (rows, ns, 16))
+        mn = np.clip(np.rint(1.5 * sc) + rng.integers(-1, 2, sc.shape), 0, 15).astype(np.int64)
+        return pack_q2_k(d, d, sc, mn, rng.integers(0, 4, (rows, cols)))
     raise ValueError(t)
