@@ -352,6 +352,9 @@ int llmp_attn_prefill_shared_f32(uint64_t handle, int layer, int src_layer, int 
 #define LLMP_GGML_MXFP4 39   /* split nibbles; E8M0 exponent byte first                       */
 #define LLMP_GGML_Q5_1   7   /* split nibbles, as Q5_0; value q*d + m                           */
 #define LLMP_GGML_Q2_K  10   /* the reference's order: element j at bits 2(j%4) of qs byte j/4 */
+#define LLMP_GGML_IQ3_XXS 18 /* codebook format (256 lattice words of 4 bytes)                 */
+#define LLMP_GGML_IQ3_S 21   /* codebook format; ninth index bits read as the reference does  */
+#define LLMP_GGML_IQ2_S 22   /* codebook format (1024 lattice words of 8 bytes)                */
 /* Weight slots of a layer (TransformerLayerWeights): matrices are [rows][cols] in GGUF row
  * order; vectors are fp32. */
 #define LLMP_W_ATTN_NORM      0  /* [dim] attnNorm RMSNorm weights; absent: x is copied (OLMo2) */
@@ -375,7 +378,8 @@ int llmp_block_config(uint64_t handle, int dim, float residual_scale);
  * of the input (blocks of 32: scale max|x|/127, int8 quants, block sum) and exact int8 dot
  * products, the reference GPU's default matvecs (CudaForwardPass.java:783-790 cuda.dp4a,
  * :216-226 and :1998-2090; quantize_q8.cu, rmsnorm_quantize.cu, matmul_<type>_dp4a*.cu); the
- * other types (F32, F16, BF16, Q4_0, Q6_K, MXFP4) keep the fp32 input, as there. */
+ * other types (F32, F16, BF16, Q4_0, Q5_1, Q2_K, Q6_K, MXFP4, IQ3_XXS, IQ3_S, IQ2_S) keep the
+ * fp32 input, as there. */
 #define LLMP_INPUT_F32   0
 #define LLMP_INPUT_Q8_1  1
 int llmp_block_input_mode(uint64_t handle, int mode);
@@ -402,8 +406,9 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
  * of two that brings the largest below 2^15 (a small first kernel computes it with each token's
  * RMSNorm factor), the outputs by its inverse.  The attention is llmp_attn_prefill_f32's (the
  * appended rows bit-identical to single-token appends of the same projections).  In the
- * LLMP_INPUT_Q8_1 mode, at head_dim 80 (no prefill kernel) and for layers whose fp32 or bf16
- * weights reach 65504, the tokens run one llmp_attn_block call each.  The call may grow the
+ * LLMP_INPUT_Q8_1 mode, at head_dim 80 (no prefill kernel), for layers whose fp32 or bf16
+ * weights reach 65504 and for Q2_K, IQ3_XXS, IQ3_S and IQ2_S weights (no token-batched
+ * kernel), the tokens run one llmp_attn_block call each.  The call may grow the
  * handle's prefill workspace, as llmp_attn_prefill_f32 does (not for use under graph capture
  * then). */
 int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t x,

@@ -29,6 +29,7 @@ LLMP_GGML_Q4_K, LLMP_GGML_Q6_K, LLMP_GGML_BF16 = 12, 14, 30
 LLMP_GGML_Q5_0, LLMP_GGML_Q3_K, LLMP_GGML_Q5_K = 6, 11, 13
 LLMP_GGML_IQ4_NL, LLMP_GGML_IQ4_XS, LLMP_GGML_MXFP4 = 20, 23, 39
 LLMP_GGML_Q5_1, LLMP_GGML_Q2_K = 7, 10
+LLMP_GGML_IQ3_XXS, LLMP_GGML_IQ3_S, LLMP_GGML_IQ2_S = 18, 21, 22
 (LLMP_W_ATTN_NORM, LLMP_W_Q, LLMP_W_K, LLMP_W_V, LLMP_W_QKV, LLMP_W_O, LLMP_W_Q_BIAS, LLMP_W_K_BIAS,
  LLMP_W_V_BIAS, LLMP_W_O_BIAS, LLMP_W_POST_ATTN_NORM) = range(11)
 LLMP_INPUT_F32, LLMP_INPUT_Q8_1 = 0, 1

@@ -40,6 +40,8 @@ hipError_t launch_f(const gk::GemvArgs& a, hipStream_t st) {
         if constexpr (F::MAXU >= 8) {
             if (nk_for<F>(a.cols) == 6) return launch_nk<F, 6>(a, st);
             return launch_nk<F, 8>(a, st);
+        } else if constexpr (F::MAXU >= 6) {
+            return launch_nk<F, 6>(a, st);
         } else {
             return hipErrorInvalidValue;
         }
@@ -115,6 +117,9 @@ int gemv_unit(int ggml_type) {
     case gk::kMXFP4: return gk::FmtMXFP4::UNIT;
     case gk::kQ5_1: return gk::FmtQ5_1::UNIT;
     case gk::kQ2_K: return gk::FmtQ2_K::UNIT;
+    case gk::kIQ3_XXS: return gk::FmtIQ3_XXS::UNIT;
+    case gk::kIQ3_S: return gk::FmtIQ3_S::UNIT;
+    case gk::kIQ2_S: return gk::FmtIQ2_S::UNIT;
     default: return 0;
     }
 }
@@ -173,6 +178,9 @@ hipError_t launch_gemv(const gk::GemvArgs& a, int ggml_type, bool q8_input, hipS
     case gk::kMXFP4: return launch_f<gk::FmtMXFP4>(a, st);
     case gk::kQ5_1: return launch_f<gk::FmtQ5_1>(a, st);
     case gk::kQ2_K: return launch_f<gk::FmtQ2_K>(a, st);
+    case gk::kIQ3_XXS: return launch_f<gk::FmtIQ3_XXS>(a, st);
+    case gk::kIQ3_S: return launch_f<gk::FmtIQ3_S>(a, st);
+    case gk::kIQ2_S: return launch_f<gk::FmtIQ2_S>(a, st);
     default: return hipErrorInvalidValue;
     }
 }

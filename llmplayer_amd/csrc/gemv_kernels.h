@@ -15,6 +15,7 @@
 #include <type_traits>
 
 #include "decode_kernels.h"
+#include "iq_grids.h"
 
 namespace llmp {
 namespace gk {
@@ -22,7 +23,7 @@ namespace gk {
 // GGMLType ids (GGMLType.java:4-35) of the formats with a kernel here.
 constexpr int kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kBF16 = 30;
 constexpr int kQ5_0 = 6, kQ3_K = 11, kQ5_K = 13, kIQ4_NL = 20, kIQ4_XS = 23, kMXFP4 = 39;
-constexpr int kQ5_1 = 7, kQ2_K = 10;
+constexpr int kQ5_1 = 7, kQ2_K = 10, kIQ3_XXS = 18, kIQ3_S = 21, kIQ2_S = 22;
 
 // One weight matrix on the device: up to four planes, each [rows][pitch bytes].
 struct WPlanes {
@@ -93,6 +94,20 @@ struct Staged {
     const unsigned char* xq;    // Q8IN formats: the input's Q8_1 quants [cols] (int8)
     const float* xd;            //   their block scales [cols/32]
     const float* xss;           //   and block sums [cols/32]
+    const void* grid;           // codebook formats: the format's codebook, copied to LDS
+};
+
+// A format's codebook (IQ3_XXS, IQ3_S, IQ2_S): GRID_BYTES and grid_src(), its table in device
+// memory, which each workgroup copies to LDS.  BYTES = 0 for the other formats.
+template <class F, class = void>
+struct FmtGrid {
+    static constexpr int BYTES = 0;
+    static __device__ __forceinline__ const void* src() { return nullptr; }
+};
+template <class F>
+struct FmtGrid<F, std::void_t<decltype(F::GRID_BYTES)>> {
+    static constexpr int BYTES = F::GRID_BYTES;
+    static __device__ __forceinline__ const void* src() { return F::grid_src(); }
 };
 
 __device__ __forceinline__ const float4& x4(const float* xs, int i) {
@@ -625,6 +640,148 @@ struct FmtQ2_K {
     }
 };
 
+// ---- codebook formats (IQ3_XXS, IQ3_S, IQ2_S) ------------------------------------------------
+// A unit is one 8-weight group: two 4-weight codebook entries (IQ3_XXS, IQ3_S) or one 8-weight
+// entry (IQ2_S), read from the LDS copy of the codebook, and eight sign bits.  Each weight is
+// (group scale * codebook byte), negated where its sign bit is set: the value the reference
+// classes stage (db * gv * sign; the negation is exact).  Units u = 32 sb + 4 g + l: super-
+// block sb, 32-group g, 8-weight group l.
+
+// byte t of the codebook word g times the group scale, its sign from bit t of s
+__device__ __forceinline__ float signed_gw(float db, unsigned g, int t, unsigned s) {
+    const float w = db * byte_f(g, t);
+    return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, w) ^ ((s << (31 - t)) & 0x80000000u));
+}
+// the 8 weights of unit u (codebook words lo, hi for weights 0-3, 4-7) against x[8u .. 8u+7]
+__device__ __forceinline__ float grid_dot8(float db, unsigned lo, unsigned hi, unsigned s, const Staged& st, int xi) {
+    const float4 x0 = x4(st.xs, xi), x1 = x4(st.xs, xi + 4);
+    return dot4(signed_gw(db, lo, 0, s), signed_gw(db, lo, 1, s), signed_gw(db, lo, 2, s), signed_gw(db, lo, 3, s), x0) +
+           dot4(signed_gw(db, hi, 0, s >> 4), signed_gw(db, hi, 1, s >> 4), signed_gw(db, hi, 2, s >> 4),
+                signed_gw(db, hi, 3, s >> 4), x1);
+}
+
+// IQ3_XXS (IQ3_XXSFloatTensor.dot, super-blocks of 256 in 98 bytes).  Plane 0 = the 64
+// codebook-index bytes [rows][cols/4] (unit u: bytes 2u, 2u+1); plane 1 = each unit's 8 sign
+// bits, its 7-bit pattern index expanded with the parity bit at upload (KSIGNS_IQ2XS)
+// [rows][cols/8]; plane 2 = per super-block 8 bytes: fp16 d, 2 pad bytes, the eight 4-bit
+// group scales (group g: nibble g%2 of byte 4 + g/2).  Table: per super-block the 8 factors
+// d * (0.5 + sc) * 0.5.
+struct FmtIQ3_XXS {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 8, GRID_BYTES = 256 * 4;
+    static constexpr bool XSUM = false, Q8IN = false;
+    static __device__ __forceinline__ const void* grid_src() { return kIq3xxsGrid; }
+    struct Row { uint2 h; };
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        const unsigned sb = (unsigned)min(j, (units >> 5) - 1);
+        return Row{ldo<uint2>(rp(w, 2, row), sb * 8u)};
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        if (j >= (units >> 5)) return;
+        const float d = h2f((unsigned short)(r.h.x & 0xFFFFu));
+        float v[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) v[g] = (d * (0.5f + (float)((r.h.y >> (4 * g)) & 15u))) * 0.5f;
+        float4* t = reinterpret_cast<float4*>(tab + j * TAB);
+        t[0] = float4{v[0], v[1], v[2], v[3]};
+        t[1] = float4{v[4], v[5], v[6], v[7]};
+    }
+    struct Raw { unsigned q, s; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        return Raw{ldo<unsigned short>(rp(w, 0, row), (unsigned)u * 2u), ldo<unsigned char>(rp(w, 1, row), (unsigned)u)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned* g = static_cast<const unsigned*>(st.grid);
+        const float db = st.tab[(ub >> 2) + (j >> 2)];
+        return grid_dot8(db, g[r.q & 0xFFu], g[r.q >> 8], r.s, st, 8 * ub + 8 * j);
+    }
+};
+
+// IQ3_S (IQ3_SFloatTensor.dot, super-blocks of 256 in 110 bytes).  Plane 0 = the low index
+// bytes qs [rows][cols/4] (unit u: bytes 2u, 2u+1); plane 1 = the sign bytes [rows][cols/8]
+// (unit u: byte u); plane 2 = per super-block 16 bytes: qh[8], scales[4], fp16 d, 2 pad.
+// Index 2l + h of group g has its ninth bit at bit 2l + h of qh[g/4 + g%2] (the reference's
+// OFF_QH + ib32/4, +1 for a pair's second group: IQ3_SFloatTensor.java:131, 145 and
+// matmul_iq3_s.cu:129, 158; ggml's own dequantiser reads qh[g]).  Table: per super-block the
+// 8 factors d * (1 + 2 sc) (exact: an 11-bit significand times at most 31).
+struct FmtIQ3_S {
+    // three registers per unit: 8 rounds would spill at the kernel's 5 waves per SIMD
+    static constexpr int UNIT = 8, MAXU = 6, TAB = 8, GRID_BYTES = 512 * 4;
+    static constexpr bool XSUM = false, Q8IN = false;
+    static __device__ __forceinline__ const void* grid_src() { return kIq3sGrid; }
+    struct Row { uint4 h; };
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        const unsigned sb = (unsigned)min(j, (units >> 5) - 1);
+        return Row{ldo<uint4>(rp(w, 2, row), sb * 16u)};
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        if (j >= (units >> 5)) return;
+        const float d = h2f((unsigned short)(r.h.w & 0xFFFFu));
+        float v[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) v[g] = d * (float)(1 + 2 * (int)((r.h.z >> (4 * g)) & 15u));
+        float4* t = reinterpret_cast<float4*>(tab + j * TAB);
+        t[0] = float4{v[0], v[1], v[2], v[3]};
+        t[1] = float4{v[4], v[5], v[6], v[7]};
+    }
+    struct Raw { unsigned q, s, h; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        const unsigned g = ((unsigned)u >> 2) & 7u;
+        const unsigned hb = ((unsigned)u >> 5) * 16u + (g >> 2) + (g & 1u);
+        return Raw{ldo<unsigned short>(rp(w, 0, row), (unsigned)u * 2u), ldo<unsigned char>(rp(w, 1, row), (unsigned)u),
+                   ldo<unsigned char>(rp(w, 2, row), hb)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const unsigned* g = static_cast<const unsigned*>(st.grid);
+        const unsigned l2 = 2u * ((unsigned)j & 3u);   // ub is a multiple of 64: l = j % 4
+        const unsigned i0 = (r.q & 0xFFu) | (((r.h >> l2) & 1u) << 8);
+        const unsigned i1 = (r.q >> 8) | (((r.h >> (l2 + 1u)) & 1u) << 8);
+        const float db = st.tab[(ub >> 2) + (j >> 2)];
+        return grid_dot8(db, g[i0], g[i1], r.s, st, 8 * ub + 8 * j);
+    }
+};
+
+// IQ2_S (IQ2_SFloatTensor.dot, super-blocks of 256 in 82 bytes).  Plane 0 = the low index
+// bytes qs [rows][cols/8] (unit u: byte u); plane 1 = the sign bytes [rows][cols/8]; plane 2 =
+// per super-block 24 bytes: scales[8], qh[8], fp16 d, 6 pad.  Unit u's index has bits 8-9 at
+// bits 2l..2l+1 of qh[g].  Table: per super-block the 16 factors d * (0.5 + sc) * 0.25 (low
+// nibble of scales[g] for groups l = 0, 1 of g, high nibble for l = 2, 3): entry u/2.
+struct FmtIQ2_S {
+    static constexpr int UNIT = 8, MAXU = 8, TAB = 16, GRID_BYTES = 1024 * 8;
+    static constexpr bool XSUM = false, Q8IN = false;
+    static __device__ __forceinline__ const void* grid_src() { return kIq2sGrid; }
+    struct Row { uint2 sc; unsigned short d; };
+    static __device__ __forceinline__ Row load_row(const WPlanes& w, int row, int j, int units) {
+        const unsigned sb = (unsigned)min(j, (units >> 5) - 1);
+        return Row{ldo<uint2>(rp(w, 2, row), sb * 24u), ldo<unsigned short>(rp(w, 2, row), sb * 24u + 16u)};
+    }
+    static __device__ __forceinline__ void build_tab(const Row& r, float* tab, int j, int units) {
+        if (j >= (units >> 5)) return;
+        const float d = h2f(r.d);
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const unsigned w = k < 8 ? r.sc.x : r.sc.y;
+            v[k] = (d * (0.5f + (float)((w >> (4 * (k & 7))) & 15u))) * 0.25f;
+        }
+        float4* t = reinterpret_cast<float4*>(tab + j * TAB);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t[c] = float4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+    }
+    struct Raw { unsigned q, s, h; };
+    static __device__ __forceinline__ Raw load(const WPlanes& w, int row, int u) {
+        const unsigned hb = ((unsigned)u >> 5) * 24u + 8u + (((unsigned)u >> 2) & 7u);
+        return Raw{ldo<unsigned char>(rp(w, 0, row), (unsigned)u), ldo<unsigned char>(rp(w, 1, row), (unsigned)u),
+                   ldo<unsigned char>(rp(w, 2, row), hb)};
+    }
+    static __device__ __forceinline__ float dot(const Raw& r, const Staged& st, int ub, int j) {
+        const uint2* g = static_cast<const uint2*>(st.grid);
+        const unsigned l2 = 2u * ((unsigned)j & 3u);
+        const uint2 e = g[r.q | (((r.h >> l2) & 3u) << 8)];
+        const float db = st.tab[(ub >> 1) + (j >> 1)];
+        return grid_dot8(db, e.x, e.y, r.s, st, 8 * ub + 8 * j);
+    }
+};
+
 // ---- Q8_1 input: the reference GPU's int8 matvecs -------------------------------------------
 // CudaForwardPass runs its Q4_K and Q8_0 projections (and the formats below) on a Q8_1 copy of
 // the input by default (CudaForwardPass.java:783-790, 1998-2037; rmsnorm_quantize.cu, quantize_q8.cu,
@@ -892,6 +1049,13 @@ struct GemvLds {
     static constexpr bool Q8X = F1::Q8IN || F2::Q8IN;      // some format reads the Q8_1 input
     static constexpr bool XSUM = F1::XSUM || F2::XSUM;
     static constexpr int TAB = F1::TAB > F2::TAB ? F1::TAB : F2::TAB;
+    // the codebook of a codebook format (a launch pairs no two of them)
+    static_assert(FmtGrid<F1>::BYTES == 0 || FmtGrid<F2>::BYTES == 0 || std::is_same<F1, F2>::value,
+                  "one codebook per launch");
+    static constexpr int GRID = FmtGrid<F1>::BYTES > 0 ? FmtGrid<F1>::BYTES : FmtGrid<F2>::BYTES;
+    static __device__ __forceinline__ const void* grid_src() {
+        return FmtGrid<F1>::BYTES > 0 ? FmtGrid<F1>::src() : FmtGrid<F2>::src();
+    }
     static __host__ __device__ constexpr int cols_padded(int cols) {
         return gemv_cols_padded<F1>(cols) > gemv_cols_padded<F2>(cols) ? gemv_cols_padded<F1>(cols)
                                                                         : gemv_cols_padded<F2>(cols);
@@ -902,9 +1066,13 @@ struct GemvLds {
     static __host__ __device__ constexpr int off_xd(int cp) { return off_xq(cp) + (Q8X ? cp / 4 : 0); }
     static __host__ __device__ constexpr int off_xss(int cp) { return off_xd(cp) + (Q8X ? cp / 32 : 0); }
     static __host__ __device__ constexpr int off_tab(int cp) { return off_xss(cp) + (Q8X ? cp / 32 : 0); }
+    // the codebook after the tables, 16-byte aligned
+    static __host__ __device__ constexpr int off_grid(int cp) {
+        return (off_tab(cp) + kGemvRowsPerGroup * (cp / 256) * TAB + 3) / 4 * 4;
+    }
     static __host__ __device__ constexpr size_t bytes(int cols) {
         const int cp = cols_padded(cols);
-        return sizeof(float) * ((size_t)off_tab(cp) + (size_t)kGemvRowsPerGroup * (size_t)(cp / 256) * TAB);
+        return sizeof(float) * (size_t)off_grid(cp) + (size_t)GRID;
     }
 };
 
@@ -1015,6 +1183,7 @@ void gemv_kernel(GemvArgs a) {
     float* xd = lds + L::off_xd(cp);
     float* xss = lds + L::off_xss(cp);
     float* tab = lds + L::off_tab(cp) + wave * (cp / 256) * L::TAB;
+    uint4* grid = reinterpret_cast<uint4*>(lds + L::off_grid(cp));
 
     // input chunks and norm weights (chunk c = tid + 256k, clamped to the last chunk)
     const bool norm = a.norm_w != nullptr;
@@ -1027,6 +1196,12 @@ void gemv_kernel(GemvArgs a) {
         xv[k] = x4g[c];
         wv[k] = w4g[c];
     }
+    // the codebook (codebook formats), 16 bytes per thread per trip, in flight with the input
+    constexpr int GRID_TRIPS = (L::GRID / 16 + kGemvThreads - 1) / kGemvThreads;
+    uint4 gv[GRID_TRIPS > 0 ? GRID_TRIPS : 1];
+#pragma unroll
+    for (int k = 0; k < GRID_TRIPS; ++k)
+        gv[k] = static_cast<const uint4*>(L::grid_src())[min(tid + k * kGemvThreads, L::GRID / 16 - 1)];
     __builtin_amdgcn_sched_barrier(0);   // keep the input loads ahead of the weight loads
     // the row's side data, then the weight units
     RowRegs<F1, NK1> r1;
@@ -1090,10 +1265,13 @@ void gemv_kernel(GemvArgs a) {
         put(c, norm ? scale4(x4g[c], r, w4g[c]) : x4g[c]);
     if (!second) F1::build_tab(r1.rw, tab, j, units1);
     else F2::build_tab(r2.rw, tab, j, units2);
+#pragma unroll
+    for (int k = 0; k < GRID_TRIPS; ++k)
+        if (tid + k * kGemvThreads < L::GRID / 16) grid[tid + k * kGemvThreads] = gv[k];
     __syncthreads();
     if (LATE_R && norm) r = rms_factor();
 
-    const Staged st{xs, xsum, tab, xq, xd, xss};
+    const Staged st{xs, xsum, tab, xq, xd, xss, grid};
     float acc = !second ? row_dot(r1, st, sg, row, j, units1) : row_dot(r2, st, sg, row, j, units2);
     acc = dk::row_group_sum<64>(acc);
     if (LATE_R) acc = acc * r;

@@ -118,6 +118,9 @@ inline size_t ggml_row_bytes(int type, int cols) {
     case LLMP_GGML_MXFP4: return (size_t)(cols / 32) * 17;
     case LLMP_GGML_Q5_1: return (size_t)(cols / 32) * 24;
     case LLMP_GGML_Q2_K: return (size_t)(cols / 256) * 84;
+    case LLMP_GGML_IQ3_XXS: return (size_t)(cols / 256) * 98;
+    case LLMP_GGML_IQ3_S: return (size_t)(cols / 256) * 110;
+    case LLMP_GGML_IQ2_S: return (size_t)(cols / 256) * 82;
     default: return 0;
     }
 }
@@ -142,6 +145,26 @@ inline void iq4xs_scales(const uint8_t* blk, int8_t out[8]) {
         const int sl = blk[4 + ib / 2];
         const int low = (ib & 1) ? (sl >> 4) : (sl & 15);
         out[ib] = (int8_t)((low | (((sh >> (2 * ib)) & 3) << 4)) - 32);
+    }
+}
+
+// IQ3_XXS's per-32-group words (bytes 66 + 4 ib32 of a super-block, little-endian; the
+// IQ3_XXSFloatTensor.dot fields): the four 7-bit sign-pattern indices at bits 7l expanded to
+// the 8-bit patterns (KSIGNS_IQ2XS: the eighth bit makes the count of set bits even) -> signs
+// [32] (8-weight group 4 ib32 + l), and the 4-bit scales at bits 28-31 -> nibble ib32%2 of
+// scales[ib32/2].
+inline void iq3xxs_signs_scales(const uint8_t* blk, uint8_t signs[32], uint8_t scales[4]) {
+    for (int i = 0; i < 4; ++i) scales[i] = 0;
+    for (int ib = 0; ib < 8; ++ib) {
+        const uint8_t* a = blk + 66 + 4 * ib;
+        const uint32_t aux = (uint32_t)a[0] | ((uint32_t)a[1] << 8) | ((uint32_t)a[2] << 16) | ((uint32_t)a[3] << 24);
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t i7 = (aux >> (7 * l)) & 0x7Fu;
+            uint32_t par = 0;
+            for (int k = 0; k < 7; ++k) par ^= (i7 >> k) & 1u;
+            signs[4 * ib + l] = (uint8_t)(i7 | (par << 7));
+        }
+        scales[ib / 2] = (uint8_t)(scales[ib / 2] | ((aux >> 28) << (4 * (ib & 1))));
     }
 }
 
@@ -198,6 +221,12 @@ inline void range_exp_rows_q8(const int8_t* q, const float* s, size_t H, size_t 
 //  - MXFP4: nibble codes -> 0, E8M0 exponent byte -> 1;
 //  - Q5_1: nibbles -> 0, the 32 fifth bits (uint32) -> 1, fp16 d -> 2, fp16 m -> 3;
 //  - Q2_K: the 64 quant bytes -> 0, the 16 scale/min bytes -> 1, fp16 d -> 2, fp16 dmin -> 3;
+//  - IQ3_XXS: the 64 codebook indices -> 0, the 32 sign patterns expanded to bytes -> 1,
+//    per super-block 8 bytes -> 2: fp16 d, 2 pad, the eight 4-bit scales;
+//  - IQ3_S: qs (64) -> 0, signs (32) -> 1, per super-block 16 bytes -> 2: qh[8], scales[4],
+//    fp16 d, 2 pad;
+//  - IQ2_S: qs (32) -> 0, signs (32) -> 1, per super-block 24 bytes -> 2: scales[8], qh[8],
+//    fp16 d, 6 pad;
 //  - F32/F16/BF16: one plane, the rows unchanged.
 // Returns the plane count, or 0 for an unsupported type or a cols that is not a whole number
 // of blocks.
@@ -206,8 +235,9 @@ inline int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
     const size_t rb = ggml_row_bytes(type, cols);
     if (rb == 0 || rows < 0 || cols <= 0) return 0;
     int n = 1;
-    struct Piece { int plane; size_t src_off, len; };   // per block: bytes [src_off, +len) -> plane
-    Piece pieces[4];
+    // per block: bytes [src_off, +len) -> plane, at dst_off in the block's pitch/blocks bytes
+    struct Piece { int plane; size_t src_off, len, dst_off; };
+    Piece pieces[6];
     int n_pieces = 0;
     size_t bw = 0, blk_bytes = 0;   // weights and bytes per GGUF block
     auto set = [&](std::initializer_list<Piece> l) {
@@ -259,6 +289,18 @@ inline int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
         n = 4; bw = 256; blk_bytes = 84; pitch[0] = (size_t)cols / 4; pitch[1] = (size_t)cols / 16;
         pitch[2] = pitch[3] = (size_t)cols / 256 * 2;
         set({{1, 0, 16}, {0, 16, 64}, {2, 80, 2}, {3, 82, 2}}); break;
+    case LLMP_GGML_IQ3_XXS:   // plane 1 and the scales of plane 2 are written below
+        n = 3; bw = 256; blk_bytes = 98; pitch[0] = (size_t)cols / 4; pitch[1] = (size_t)cols / 8;
+        pitch[2] = (size_t)cols / 256 * 8;
+        set({{0, 2, 64}, {2, 0, 2}}); break;
+    case LLMP_GGML_IQ3_S:
+        n = 3; bw = 256; blk_bytes = 110; pitch[0] = (size_t)cols / 4; pitch[1] = (size_t)cols / 8;
+        pitch[2] = (size_t)cols / 256 * 16;
+        set({{0, 2, 64}, {1, 74, 32}, {2, 66, 8, 0}, {2, 106, 4, 8}, {2, 0, 2, 12}}); break;
+    case LLMP_GGML_IQ2_S:
+        n = 3; bw = 256; blk_bytes = 82; pitch[0] = (size_t)cols / 8; pitch[1] = (size_t)cols / 8;
+        pitch[2] = (size_t)cols / 256 * 24;
+        set({{0, 2, 32}, {1, 34, 32}, {2, 74, 8, 0}, {2, 66, 8, 8}, {2, 0, 2, 16}}); break;
     default: return 0;
     }
     if (bw && cols % (int)bw) return 0;
@@ -275,13 +317,16 @@ inline int repack_weight(int type, int rows, int cols, const uint8_t* src, std::
             const uint8_t* blk = src + (size_t)r * rb + b * blk_bytes;
             for (int i = 0; i < n_pieces; ++i) {
                 const Piece& pc = pieces[i];
-                std::memcpy(&dst[off[pc.plane] + (size_t)r * pitch[pc.plane] + b * pc.len],
+                std::memcpy(&dst[off[pc.plane] + (size_t)r * pitch[pc.plane] + b * (pitch[pc.plane] / nb) + pc.dst_off],
                             blk + pc.src_off, pc.len);
             }
             if (type == LLMP_GGML_Q3_K)
                 q3k_scales(blk + 96, reinterpret_cast<int8_t*>(&dst[off[2] + (size_t)r * pitch[2] + b * 16]));
             else if (type == LLMP_GGML_IQ4_XS)
                 iq4xs_scales(blk, reinterpret_cast<int8_t*>(&dst[off[1] + (size_t)r * pitch[1] + b * 8]));
+            else if (type == LLMP_GGML_IQ3_XXS)
+                iq3xxs_signs_scales(blk, &dst[off[1] + (size_t)r * pitch[1] + b * 32],
+                                    &dst[off[2] + (size_t)r * pitch[2] + b * 8 + 4]);
         }
     return n;
 }

@@ -9,7 +9,8 @@
  * and output projection (Attention.java:76-110, 232-238), over projection weights in the GGUF
  * block formats of the reference's tensor classes (the tensor package's FloatTensor classes):
  *   F32 (0), F16 (1), Q4_0 (2), Q5_0 (6), Q5_1 (7), Q8_0 (8), Q2_K (10), Q3_K (11), Q4_K (12),
- *   Q5_K (13), Q6_K (14), IQ4_NL (20), IQ4_XS (23), BF16 (30), MXFP4 (39)  (GGMLType ids).
+ *   Q5_K (13), Q6_K (14), IQ3_XXS (18), IQ4_NL (20), IQ3_S (21), IQ2_S (22), IQ4_XS (23),
+ *   BF16 (30), MXFP4 (39)  (GGMLType ids).
  *
  * Dequantised weights are bit-identical to what each class's dot() stages (or getFloat()
  * returns); a row's dot follows the scalar classes of the java/ tree: F32 one
@@ -28,6 +29,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "iq_grids.h"
 #include "orc.h"
 
 #define ORC_GGML_F32 0
@@ -42,6 +44,9 @@
 #define ORC_GGML_Q5_K 13
 #define ORC_GGML_Q6_K 14
 #define ORC_GGML_IQ4_NL 20
+#define ORC_GGML_IQ3_XXS 18
+#define ORC_GGML_IQ3_S 21
+#define ORC_GGML_IQ2_S 22
 #define ORC_GGML_IQ4_XS 23
 #define ORC_GGML_BF16 30
 #define ORC_GGML_MXFP4 39
@@ -126,8 +131,30 @@ int orc_ggml_block(int type, int *bytes)
     case ORC_GGML_IQ4_NL: *bytes = 18; return 32;
     case ORC_GGML_IQ4_XS: *bytes = 136; return 256;
     case ORC_GGML_MXFP4: *bytes = 17; return 32;
+    case ORC_GGML_IQ3_XXS: *bytes = 98; return 256;
+    case ORC_GGML_IQ3_S: *bytes = 110; return 256;
+    case ORC_GGML_IQ2_S: *bytes = 82; return 256;
     default: *bytes = 0; return 0;
     }
+}
+
+/* IQ3_XXS sign patterns (IQGridTables.KSIGNS_IQ2XS): the 7-bit index with an eighth bit that
+ * makes the count of set bits even (the pattern's eighth sign is implied by parity). */
+static int orc_ksigns(int i)
+{
+    int p = 0;
+    for (int k = 0; k < 7; k++) p ^= (i >> k) & 1;
+    return i | (p << 7);
+}
+int orc_ksigns_entry(int i) { return orc_ksigns(i & 0x7F); }
+
+/* Codebook entry `i` of an IQ format's table (for the table checks of the tests); 0 past the end. */
+uint64_t orc_iq_grid(int type, int i)
+{
+    if (type == ORC_GGML_IQ3_XXS) return i >= 0 && i < 256 ? orc_iq3xxs_grid[i] : 0;
+    if (type == ORC_GGML_IQ3_S) return i >= 0 && i < 512 ? orc_iq3s_grid[i] : 0;
+    if (type == ORC_GGML_IQ2_S) return i >= 0 && i < 1024 ? orc_iq2s_grid[i] : 0;
+    return 0;
 }
 
 /* Dequantised values of one block (`n` weights) exactly as the class's dot() stages them. */
@@ -305,6 +332,70 @@ static void dequant_block(int type, const uint8_t *b, float *out)
         for (int i = 0; i < 16; i++) {
             out[i] = fp4_e2m1[b[1 + i] & 0x0F] * scale;
             out[i + 16] = fp4_e2m1[(b[1 + i] >> 4) & 0x0F] * scale;
+        }
+        break;
+    }
+    case ORC_GGML_IQ3_XXS: {   /* IQ3_XXSFloatTensor.dot (IQ3_XXSFloatTensor.java:77-113) */
+        /* 64 codebook indices at 2, then per 32 weights a little-endian word at 66 + 4*ib32:
+         * four 7-bit sign-pattern indices (bits 7l..7l+6) and the scale in bits 28..31 */
+        float d = orc_f16_to_f32(le16(b));
+        const uint8_t *qs = b + 2, *sas = b + 66;
+        for (int ib32 = 0; ib32 < 8; ib32++) {
+            uint32_t aux = (uint32_t)sas[4 * ib32] | ((uint32_t)sas[4 * ib32 + 1] << 8) |
+                           ((uint32_t)sas[4 * ib32 + 2] << 16) | ((uint32_t)sas[4 * ib32 + 3] << 24);
+            float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+            for (int l = 0; l < 4; l++) {
+                int signs = orc_ksigns((int)((aux >> (7 * l)) & 0x7F));
+                uint32_t g1 = orc_iq3xxs_grid[qs[ib32 * 8 + 2 * l]];
+                uint32_t g2 = orc_iq3xxs_grid[qs[ib32 * 8 + 2 * l + 1]];
+                for (int j = 0; j < 4; j++) {
+                    out[ib32 * 32 + l * 8 + j] = db * (float)((g1 >> (8 * j)) & 0xFF) * ((signs >> j) & 1 ? -1.0f : 1.0f);
+                    out[ib32 * 32 + l * 8 + 4 + j] =
+                        db * (float)((g2 >> (8 * j)) & 0xFF) * ((signs >> (j + 4)) & 1 ? -1.0f : 1.0f);
+                }
+            }
+        }
+        break;
+    }
+    case ORC_GGML_IQ3_S: {   /* IQ3_SFloatTensor.dot (IQ3_SFloatTensor.java:110-170) */
+        /* qs (low 8 index bits) at 2, qh (9th bits) at 66, sign bits at 74, 4-bit scales at 106.
+         * The 9th bits of 32-group g come from qh[(g >> 2) + (g & 1)]: the reference's
+         * OFF_QH + ib32/4 (+1 for the pair's second group), which its CUDA kernel
+         * (matmul_iq3_s.cu:129, 158) shares; ggml's dequantiser reads qh[g]. */
+        float d = orc_f16_to_f32(le16(b));
+        const uint8_t *qs = b + 2, *qh = b + 66, *sg = b + 74, *scl = b + 106;
+        for (int g = 0; g < 8; g++) {
+            int sb = scl[g / 2];
+            float db = d * (float)(1 + 2 * ((g & 1) ? (sb >> 4) & 0x0F : sb & 0x0F));
+            int h = qh[(g >> 2) + (g & 1)];
+            for (int l = 0; l < 4; l++) {
+                uint32_t g1 = orc_iq3s_grid[qs[g * 8 + 2 * l] | ((h << (8 - 2 * l)) & 256)];
+                uint32_t g2 = orc_iq3s_grid[qs[g * 8 + 2 * l + 1] | ((h << (7 - 2 * l)) & 256)];
+                int signs = sg[g * 4 + l];
+                for (int j = 0; j < 4; j++) {
+                    out[g * 32 + l * 8 + j] = db * (float)((g1 >> (8 * j)) & 0xFF) * ((signs >> j) & 1 ? -1.0f : 1.0f);
+                    out[g * 32 + l * 8 + 4 + j] =
+                        db * (float)((g2 >> (8 * j)) & 0xFF) * ((signs >> (j + 4)) & 1 ? -1.0f : 1.0f);
+                }
+            }
+        }
+        break;
+    }
+    case ORC_GGML_IQ2_S: {   /* IQ2_SFloatTensor.dot (IQ2_SFloatTensor.java:84-113) */
+        /* qs (low 8 index bits) at 2, sign bits at 34, qh (bits 8-9 of the 4 indices of a
+         * 32-group, two bits each) at 66, two 4-bit scales per 32-group at 74 */
+        float d = orc_f16_to_f32(le16(b));
+        const uint8_t *qs = b + 2, *sg = b + 34, *qh = b + 66, *scl = b + 74;
+        for (int ib32 = 0; ib32 < 8; ib32++) {
+            float db0 = d * (0.5f + (float)(scl[ib32] & 0x0F)) * 0.25f;
+            float db1 = d * (0.5f + (float)((scl[ib32] >> 4) & 0x0F)) * 0.25f;
+            for (int l = 0; l < 4; l++) {
+                float dl = l < 2 ? db0 : db1;
+                uint64_t gr = orc_iq2s_grid[qs[ib32 * 4 + l] | ((qh[ib32] << (8 - 2 * l)) & 0x300)];
+                int signs = sg[ib32 * 4 + l];
+                for (int j = 0; j < 8; j++)
+                    out[ib32 * 32 + l * 8 + j] = dl * (float)((gr >> (8 * j)) & 0xFF) * ((signs >> j) & 1 ? -1.0f : 1.0f);
+            }
         }
         break;
     }

@@ -157,6 +157,10 @@ def lib():
         L.orc_quantize_q8_1.argtypes = [_F, C.c_int, C.POINTER(C.c_int8), _F, _F]
         L.orc_q8_1_routed.restype = C.c_int
         L.orc_q8_1_routed.argtypes = [C.c_int]
+        L.orc_iq_grid.restype = C.c_uint64
+        L.orc_iq_grid.argtypes = [C.c_int, C.c_int]
+        L.orc_ksigns_entry.restype = C.c_int
+        L.orc_ksigns_entry.argtypes = [C.c_int]
         L.orc_matmul_q8_1.restype = C.c_int
         L.orc_matmul_q8_1.argtypes = [C.c_int, _U8, C.c_int, C.c_int, C.POINTER(C.c_int8), _F, _F,
                                       _F]
@@ -444,6 +448,7 @@ def forward_gemma4(cfg: OracleConfig, kcache, vcache, q, k, v, pos, is_swa, qnor
 # ---- attention half of a layer over GGUF-format projection weights ----------------------
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 14, 30
 GGML_Q5_0, GGML_Q3_K, GGML_Q5_K, GGML_IQ4_NL, GGML_IQ4_XS, GGML_MXFP4 = 6, 11, 13, 20, 23, 39
+GGML_IQ3_XXS, GGML_IQ3_S, GGML_IQ2_S = 18, 21, 22
 
 
 def f16_to_f32(h: int) -> np.float32:
@@ -458,6 +463,18 @@ def ggml_block(t: int):
     if n == 0:
         raise ValueError(f"unsupported GGML type {t}")
     return n, b.value
+
+
+def iq_grid(t: int) -> np.ndarray:
+    """The codebook of an IQ format (IQ3_XXS: 256 words, IQ3_S: 512, IQ2_S: 1024 of 8 bytes) as
+    the oracle holds it (IQGridTables.java:30-398)."""
+    n = {GGML_IQ3_XXS: 256, GGML_IQ3_S: 512, GGML_IQ2_S: 1024}[t]
+    return np.array([lib().orc_iq_grid(int(t), i) for i in range(n)], dtype=np.uint64)
+
+
+def ksigns(i: int) -> int:
+    """IQGridTables.KSIGNS_IQ2XS[i] as the oracle forms it (the 7-bit index plus a parity bit)."""
+    return int(lib().orc_ksigns_entry(int(i)))
 
 
 def ggml_row_bytes(t: int, cols: int) -> int:

@@ -6,14 +6,17 @@ Every packer takes the format's fields (scales, mins, quants) and returns (bytes
 row_bytes] uint8, dequantised values [rows, cols] float32), the values computed in float32
 in the reference's operation order (the dot() of Q8_0FloatTensor, Q4_0FloatTensor,
 Q4_KFloatTensor, Q6_KFloatTensor, Q3_KFloatTensor, Q5_KFloatTensor, IQ4_NLFloatTensor,
-IQ4_XSFloatTensor and MXFP4FloatTensor; Q5_0FloatTensor.getFloat).  Random fields give test weights whose dequantised values are known
-without running the code under test."""
+IQ4_XSFloatTensor and MXFP4FloatTensor; Q5_0FloatTensor.getFloat; the IQ3_XXS, IQ3_S and IQ2_S
+classes' getFloat, element by element).  Random fields give test weights whose dequantised
+values are known without running the code under test.  The IQ packers take their format's
+codebook as an argument (the tests pass the oracle's, which the table checks pin)."""
 import numpy as np
 
 F32 = np.float32
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = 0, 1, 2, 8, 12, 14, 30
 GGML_Q5_0, GGML_Q3_K, GGML_Q5_K, GGML_IQ4_NL, GGML_IQ4_XS, GGML_MXFP4 = 6, 11, 13, 20, 23, 39
 GGML_Q5_1, GGML_Q2_K = 7, 10
+GGML_IQ3_XXS, GGML_IQ3_S, GGML_IQ2_S = 18, 21, 22
 
 # the non-linear 4-bit codebook of IQ4_NL and IQ4_XS (GGUF's kvalues_iq4nl)
 IQ4NL_VALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], F32)
@@ -286,6 +289,105 @@ def pack_mxfp4(e, idx):
     return out.reshape(rows, -1), vals.reshape(rows, -1)
 
 
+def _parity_signs(i):
+    """KSIGNS_IQ2XS[i]: the 7-bit index with an eighth bit making the count of set bits even."""
+    i = np.asarray(i, np.int64)
+    par = np.zeros_like(i)
+    for k in range(7):
+        par ^= (i >> k) & 1
+    return i | (par << 7)
+
+
+def _grid_bytes(grid, idx, width):
+    """Byte j (j < width) of codebook entry idx: [..., width] as int64."""
+    g = np.asarray(grid, np.uint64)[np.asarray(idx, np.int64)]
+    return np.stack([((g >> np.uint64(8 * j)) & np.uint64(0xFF)).astype(np.int64) for j in range(width)], -1)
+
+
+def pack_iq3_xxs(d_bits, qs, sign_idx, sc, grid):
+    """Super-blocks of 256 (98 bytes): d fp16, 64 codebook indices (index 2l + h of 32-group
+    ib32 at byte 8 ib32 + 2l + h, h = the 4-weight half of 8-weight group l), then per
+    32-group a little-endian word: the 7-bit sign-pattern indices of its four 8-weight
+    groups at bits 7l.. and the scale in bits 28-31.  qs [rows, ns, 64] in 0..255, sign_idx
+    [rows, ns, 8, 4] in 0..127, sc [rows, ns, 8] in 0..15.  Element 32 ib32 + 8l + 4h + j is
+    (d * (0.5 + sc) * 0.5) * grid[qs].byte(j), negated where bit 4h + j of the pattern is set
+    (IQ3_XXSFloatTensor.getFloat)."""
+    rows, ns = d_bits.shape
+    qs = np.asarray(qs, np.int64)
+    si = np.asarray(sign_idx, np.int64)
+    sc = np.asarray(sc, np.int64)
+    out = np.zeros((rows, ns, 98), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    out[:, :, 2:66] = qs.astype(np.uint8)
+    aux = sum(si[..., l] << (7 * l) for l in range(4)) | (sc << 28)            # [rows, ns, 8]
+    out[:, :, 66:98] = aux.astype(np.uint32)[..., None].view(np.uint8).reshape(rows, ns, 32)
+    j = np.arange(256)
+    ib32, l, h, jj = j // 32, (j % 32) // 8, (j % 8) // 4, j % 4
+    d = _f16_val(d_bits)[..., None]
+    db = ((d * (F32(0.5) + sc[:, :, ib32].astype(F32))).astype(F32) * F32(0.5)).astype(F32)
+    gv = np.take_along_axis(_grid_bytes(grid, qs[:, :, ib32 * 8 + 2 * l + h], 4), jj[None, None, :, None], -1)[..., 0]
+    neg = (_parity_signs(si[:, :, ib32, l]) >> (4 * h + jj)) & 1
+    vals = (db * gv.astype(F32)).astype(F32)
+    vals = np.where(neg == 1, -vals, vals).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_iq3_s(d_bits, qs, qh, signs, sc, grid):
+    """Super-blocks of 256 (110 bytes): d fp16, qs[64] (low 8 bits of index 2l + h of 32-group
+    g at byte 8g + 2l + h), qh[8], signs[32] (one bit per weight: bit 4h + j of byte 4g + l),
+    scales[4] (32-group g: nibble g%2 of byte g/2).  The ninth index bit is bit 2l + h of
+    qh[g/4 + g%2]: IQ3_SFloatTensor.getFloat's OFF_QH + ib32/4 (+1 for the second group of a
+    pair), as its dot and its CUDA kernel read it.  qs [rows, ns, 64], qh [rows, ns, 8],
+    signs [rows, ns, 32] in 0..255, sc [rows, ns, 8] in 0..15.  Element 32g + 8l + 4h + j is
+    (d * (1 + 2 sc)) * grid[index].byte(j), negated where its sign bit is set."""
+    rows, ns = d_bits.shape
+    qs, qh, signs, sc = (np.asarray(a, np.int64) for a in (qs, qh, signs, sc))
+    out = np.zeros((rows, ns, 110), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    out[:, :, 2:66] = qs.astype(np.uint8)
+    out[:, :, 66:74] = qh.astype(np.uint8)
+    out[:, :, 74:106] = signs.astype(np.uint8)
+    out[:, :, 106:110] = (sc[:, :, 0::2] | (sc[:, :, 1::2] << 4)).astype(np.uint8)
+    j = np.arange(256)
+    g, l, h, jj = j // 32, (j % 32) // 8, (j % 8) // 4, j % 4
+    hi = (qh[:, :, g // 4 + g % 2] >> (2 * l + h)) & 1
+    idx = qs[:, :, 8 * g + 2 * l + h] | (hi << 8)
+    d = _f16_val(d_bits)[..., None]
+    db = (d * (1 + 2 * sc[:, :, g]).astype(F32)).astype(F32)
+    gv = np.take_along_axis(_grid_bytes(grid, idx, 4), jj[None, None, :, None], -1)[..., 0]
+    neg = (signs[:, :, 4 * g + l] >> (4 * h + jj)) & 1
+    vals = (db * gv.astype(F32)).astype(F32)
+    vals = np.where(neg == 1, -vals, vals).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
+def pack_iq2_s(d_bits, qs, qh, signs, sc, grid):
+    """Super-blocks of 256 (82 bytes): d fp16, qs[32] (low 8 bits of index l of 32-group ib32 at
+    byte 4 ib32 + l), signs[32] (bit j of byte 4 ib32 + l), qh[8] (index bits 8-9 at bits
+    2l..2l+1 of byte ib32), scales[8] (low nibble for the 32-group's first 16 weights, high
+    for the last 16).  qs, signs [rows, ns, 32], qh [rows, ns, 8] in 0..255, sc [rows, ns, 16]
+    in 0..15 (sc[2 ib32 + l/2]).  Element 32 ib32 + 8l + j is (d * (0.5 + sc) * 0.25) *
+    grid[index].byte(j), negated where its sign bit is set (IQ2_SFloatTensor.getFloat)."""
+    rows, ns = d_bits.shape
+    qs, qh, signs, sc = (np.asarray(a, np.int64) for a in (qs, qh, signs, sc))
+    out = np.zeros((rows, ns, 82), np.uint8)
+    out[:, :, 0:2] = np.asarray(d_bits, np.uint16)[..., None].view(np.uint8).reshape(rows, ns, 2)
+    out[:, :, 2:34] = qs.astype(np.uint8)
+    out[:, :, 34:66] = signs.astype(np.uint8)
+    out[:, :, 66:74] = qh.astype(np.uint8)
+    out[:, :, 74:82] = (sc[:, :, 0::2] | (sc[:, :, 1::2] << 4)).astype(np.uint8)
+    j = np.arange(256)
+    ib32, l, jj = j // 32, (j % 32) // 8, j % 8
+    idx = qs[:, :, 4 * ib32 + l] | (((qh[:, :, ib32] >> (2 * l)) & 3) << 8)
+    d = _f16_val(d_bits)[..., None]
+    dl = ((d * (F32(0.5) + sc[:, :, 2 * ib32 + l // 2].astype(F32))).astype(F32) * F32(0.25)).astype(F32)
+    gv = np.take_along_axis(_grid_bytes(grid, idx, 8), jj[None, None, :, None], -1)[..., 0]
+    neg = (signs[:, :, 4 * ib32 + l] >> jj) & 1
+    vals = (dl * gv.astype(F32)).astype(F32)
+    vals = np.where(neg == 1, -vals, vals).astype(F32)
+    return out.reshape(rows, -1), vals.reshape(rows, -1)
+
+
 def random_weights(t, rows, cols, rng, scale=0.05):
     """Random weights of GGML type t with magnitudes around `scale`: (bytes, float32 values)."""
     if t == GGML_F32:
@@ -349,4 +451,18 @@ def random_weights(t, rows, cols, rng, scale=0.05):
         sc = rng.integers(0, 11, (rows, ns, 16))
         mn = np.clip(np.rint(1.5 * sc) + rng.integers(-1, 2, sc.shape), 0, 15).astype(np.int64)
         return pack_q2_k(d, d, sc, mn, rng.integers(0, 4, (rows, cols)))
+    if t in (GGML_IQ3_XXS, GGML_IQ3_S, GGML_IQ2_S):
+        from oracle import oracle as orc   # the codebook
+        ns = cols // 256
+        grid = orc.iq_grid(t)
+        u8 = lambda *shape: rng.integers(0, 256, (rows, ns) + shape)
+        if t == GGML_IQ3_XXS:
+            d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 128)
+            return pack_iq3_xxs(d, u8(64), rng.integers(0, 128, (rows, ns, 8, 4)),
+                                rng.integers(0, 16, (rows, ns, 8)), grid)
+        if t == GGML_IQ3_S:
+            d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 128)
+            return pack_iq3_s(d, u8(64), u8(8), u8(32), rng.integers(0, 16, (rows, ns, 8)), grid)
+        d = _f16_bits(rng.uniform(0.5, 1.5, (rows, ns)) * scale / 50)
+        return pack_iq2_s(d, u8(32), u8(8), u8(32), rng.integers(0, 16, (rows, ns, 16)), grid)
     raise ValueError(t)

@@ -135,10 +135,11 @@ TYPES = tbg.TYPES
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
 def test_block_batch_every_weight_format(t):
     """Each format's matrix-core path: 5 tokens (a partial token tile) after a 40-row prefix,
-    then 5 more.  Q2_K has no token-batched kernel: its tokens run one by one (ten single-token
-    decode launches), with the same results."""
+    then 5 more.  Q2_K and the codebook formats (IQ3_XXS, IQ3_S, IQ2_S) have no token-batched
+    kernel: their tokens run one by one (ten single-token decode launches), with the same
+    results."""
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
-    if t == gp.GGML_Q2_K:
+    if t in tbg.PER_TOKEN:
         _run_batch(c, 1024, 64, 40, 5, (t, t, t, t), seed=1600 + t, what=NAMES[t], rounds=2,
                    per_token=True)
         return

@@ -21,9 +21,12 @@ pytestmark = pytest.mark.gpu
 F32 = np.float32
 TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
          gp.GGML_Q6_K, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL, gp.GGML_IQ4_XS,
-         gp.GGML_MXFP4, gp.GGML_Q5_1, gp.GGML_Q2_K]
+         gp.GGML_MXFP4, gp.GGML_Q5_1, gp.GGML_Q2_K, gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S]
 NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k", 6: "q5_0",
-         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k"}
+         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k",
+         18: "iq3_xxs", 21: "iq3_s", 22: "iq2_s"}
+# formats with no token-batched kernel: K-token calls run their tokens one by one
+PER_TOKEN = (gp.GGML_Q2_K, gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S)
 
 
 def _tensor(t, rows, cols, rng, scale=0.05):
@@ -143,14 +146,15 @@ def test_block_every_weight_format(t):
 
 WIDE = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q5_0,
         gp.GGML_IQ4_NL, gp.GGML_MXFP4, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS, gp.GGML_Q5_1,
-        gp.GGML_Q2_K]
+        gp.GGML_Q2_K, gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S]
 
 
 @pytest.mark.parametrize("t", WIDE, ids=[NAMES[t] for t in WIDE])
 def test_block_weight_formats_at_width_4096(t):
     """Rows of 4096 columns: 8 unit rounds in registers and a second batch for the 4-weight
     unit formats (F32, F16, BF16, Q8_0), 8 rounds for the 8-weight units (Q4_0, Q5_0, IQ4_NL,
-    MXFP4, Q5_K, IQ4_XS), 4 for Q3_K's 16-weight units."""
+    MXFP4, Q5_K, IQ4_XS, IQ3_XXS, IQ2_S), 6 and a second batch for IQ3_S, 4 for Q3_K's 16-weight
+    units."""
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
     _run(c, 4096, 64, 33, 1, (t, t, t, t), seed=900 + t, what=f"{NAMES[t]} width 4096")
 
@@ -246,7 +250,7 @@ def test_block_split_settings_agree():
 # output (computed in two orders) ahead of the output projection.
 
 Q8_1_CASES = [gp.GGML_Q4_K, gp.GGML_Q8_0, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL,
-              gp.GGML_IQ4_XS, gp.GGML_Q6_K, gp.GGML_F16, gp.GGML_Q4_0, gp.GGML_MXFP4]
+              gp.GGML_IQ4_XS, gp.GGML_Q6_K, gp.GGML_F16, gp.GGML_Q4_0, gp.GGML_MXFP4, gp.GGML_IQ3_S]
 
 
 @pytest.mark.parametrize("t", Q8_1_CASES,
@@ -332,7 +336,7 @@ def test_block_error_codes():
         assert _lib.status("llmp_attn_block", h, 0, 3, 0, x, 0, 0) == 1               # no weights yet
         w = np.zeros(512 * 512 * 4, np.uint8)
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 128, 512, w.ctypes.data, 128 * 512 * 4) == 1  # rows != q_dim
-        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 22, 512, 512, w.ctypes.data, 512 * 82 // 256 * 512) == 6  # IQ2_S: no kernel
+        assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 16, 512, 512, w.ctypes.data, 512 * 66 // 256 * 512) == 6  # IQ2_XXS: no kernel (the reference loads none either)
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_Q, 0, 512, 512, w.ctypes.data, 100) == 1   # byte count
         assert _lib.status("llmp_layer_weight", h, 0, 11, 0, 1, 512, w.ctypes.data, 2048) == 1  # bad slot
         assert _lib.status("llmp_layer_weight", h, 0, _lib.LLMP_W_ATTN_NORM, 8, 1, 512, w.ctypes.data, 2048) == 1  # vector not fp32

@@ -15,9 +15,11 @@ from tests import refmath as rm
 F32 = np.float32
 TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.GGML_Q4_K,
          gp.GGML_Q6_K, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL, gp.GGML_IQ4_XS,
-         gp.GGML_MXFP4, gp.GGML_Q5_1, gp.GGML_Q2_K]
+         gp.GGML_MXFP4, gp.GGML_Q5_1, gp.GGML_Q2_K, gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S]
 NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k", 6: "q5_0",
-         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k"}
+         11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k",
+         18: "iq3_xxs", 21: "iq3_s", 22: "iq2_s"}
+IQ_TYPES = [gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S]
 
 
 def test_f16_conversion_matches_ieee_half_for_every_pattern():
@@ -250,6 +252,122 @@ def test_q2_k_row_dot_restates_dotq2kf32():
             sf = F32(sf + x[j])
         res = F32(res + F32(F32(F32(d * F32(sc)) * sq) - F32(F32(dmin * F32(m)) * sf)))
     assert orc.matmul(gp.GGML_Q2_K, wb, 1, 256, x)[0] == res
+
+
+def _grid_levels(t):
+    # entries, bytes per entry and the lattice levels a byte may take: IQ3_XXS 8 levels
+    # (4, 12, .., 52 and 62: ggml's iq3xxs grid tops out at 62, not 60), IQ3_S the odd
+    # numbers 1..15, IQ2_S the three levels 8, 25, 43
+    return {gp.GGML_IQ3_XXS: (256, 4, [4, 12, 20, 28, 36, 44, 52, 62]),
+            gp.GGML_IQ3_S: (512, 4, list(range(1, 16, 2))),
+            gp.GGML_IQ2_S: (1024, 8, [8, 25, 43])}[t]
+
+
+@pytest.mark.parametrize("t", IQ_TYPES, ids=[NAMES[t] for t in IQ_TYPES])
+def test_iq_codebooks_are_ordered_lattice_tables(t):
+    # The codebooks are format constants (ggml's iq3xxs/iq3s/iq2s grids).  Each lists distinct
+    # lattice points in increasing order, every byte one of the format's levels, the first
+    # entry all at the lowest level: a mistyped or swapped entry breaks one of these.  The
+    # kernels' copy (llmplayer_amd/csrc/iq_grids.h) must hold the same values.
+    import pathlib
+    import re
+    n, width, levels = _grid_levels(t)
+    g = orc.iq_grid(t)
+    assert len(g) == n and np.all(g[1:] > g[:-1])
+    b = np.stack([(g >> np.uint64(8 * j)) & np.uint64(0xFF) for j in range(width)], -1).astype(np.int64)
+    assert set(np.unique(b)) == set(levels)
+    assert np.all(b[0] == levels[0])
+    # each byte level occurs in every position: no byte column was dropped or duplicated
+    for j in range(width):
+        assert set(np.unique(b[:, j])) == set(levels), j
+    src = (pathlib.Path(__file__).resolve().parents[1] / "llmplayer_amd" / "csrc" / "iq_grids.h").read_text()
+    name = {gp.GGML_IQ3_XXS: "kIq3xxsGrid", gp.GGML_IQ3_S: "kIq3sGrid", gp.GGML_IQ2_S: "kIq2sGrid"}[t]
+    body = re.search(name + r"\[\d+\][^=]*= \{(.*?)\};", src, re.S).group(1)
+    dev = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]+)", body)], np.uint64)
+    assert np.array_equal(dev, g)
+
+
+def test_iq3_xxs_sign_patterns_have_even_parity():
+    # KSIGNS_IQ2XS: entry i keeps the 7-bit index and sets bit 7 so that the byte has an even
+    # number of set bits (the eighth sign is implied); spot values from the reference table
+    got = [orc.ksigns(i) for i in range(128)]
+    assert all(v & 0x7F == i and bin(v).count("1") % 2 == 0 for i, v in enumerate(got))
+    assert (got[0], got[1], got[2], got[3], got[64], got[127]) == (0, 129, 130, 3, 192, 255)
+
+
+def test_iq3_xxs_word_fields_and_closed_form():
+    # one super-block, every index 0 (entry 0 = four 4s): weight 32 ib32 + 8l + j is
+    # (d * (0.5 + sc) * 0.5) * 4, negated by bit j of pattern ksigns(idx) of its 8-group
+    d = np.array([[0x3C00]], np.uint16)   # 1.0
+    rng = np.random.default_rng(31)
+    si = rng.integers(0, 128, (1, 1, 8, 4))
+    sc = rng.integers(0, 16, (1, 1, 8))
+    grid = orc.iq_grid(gp.GGML_IQ3_XXS)
+    wb, vals = gp.pack_iq3_xxs(d, np.zeros((1, 1, 64), np.int64), si, sc, grid)
+    aux = int.from_bytes(bytes(wb[0, 66 + 4 * 5:66 + 4 * 6]), "little")
+    assert aux >> 28 == sc[0, 0, 5] and (aux >> 14) & 0x7F == si[0, 0, 5, 2]
+    got = orc.dequant_rows(gp.GGML_IQ3_XXS, wb, 1, 256)[0]
+    for ib in range(8):
+        for l in range(4):
+            pat = orc.ksigns(int(si[0, 0, ib, l]))
+            mag = F32(F32(F32(1.0) * F32(0.5 + sc[0, 0, ib])) * F32(0.5)) * F32(4)
+            want = np.array([-mag if (pat >> j) & 1 else mag for j in range(8)], F32)
+            assert np.array_equal(got[32 * ib + 8 * l:32 * ib + 8 * l + 8], want), (ib, l)
+    assert np.array_equal(got, vals[0])
+
+
+def test_iq3_s_ninth_bits_follow_the_reference_not_ggml():
+    # The ninth index bit of 32-group g comes from qh[g/4 + g%2] (IQ3_SFloatTensor's
+    # OFF_QH + ib32/4, +1 for a pair's second group; its CUDA kernel reads the same bytes).
+    # With only qh[1] set, groups 1, 3, 4 and 6 take entries 256 + qs; ggml (qh[g]) would
+    # give that to group 1 alone.
+    d = np.array([[0x3C00]], np.uint16)
+    rng = np.random.default_rng(32)
+    qs = rng.integers(0, 256, (1, 1, 64))
+    qh = np.zeros((1, 1, 8), np.int64)
+    qh[0, 0, 1] = 0xFF
+    grid = orc.iq_grid(gp.GGML_IQ3_S)
+    sc = np.zeros((1, 1, 8), np.int64)        # db = d * 1
+    signs = np.zeros((1, 1, 32), np.int64)
+    wb, vals = gp.pack_iq3_s(d, qs, qh, signs, sc, grid)
+    got = orc.dequant_rows(gp.GGML_IQ3_S, wb, 1, 256)[0]
+    for g in range(8):
+        high = 256 if g in (1, 3, 4, 6) else 0
+        for k in range(8):   # the group's 8 indices, 4 weights each
+            e = int(grid[int(qs[0, 0, 8 * g + k]) + high])
+            want = np.array([(e >> (8 * j)) & 0xFF for j in range(4)], F32)
+            assert np.array_equal(got[32 * g + 4 * k:32 * g + 4 * k + 4], want), (g, k)
+    assert np.array_equal(got, vals[0])
+    # the scale nibbles: d * (1 + 2 sc), group g from byte g/2, low nibble first
+    sc = np.arange(8).reshape(1, 1, 8) * 2
+    wb, _ = gp.pack_iq3_s(d, qs, qh, signs, sc, grid)
+    got2 = orc.dequant_rows(gp.GGML_IQ3_S, wb, 1, 256)[0]
+    assert np.array_equal(got2, got * np.repeat(1 + 2 * sc[0, 0], 32).astype(F32))
+
+
+def test_iq2_s_high_bits_scale_halves_and_signs():
+    # index l of 32-group ib32: qs[4 ib32 + l] | bits 2l..2l+1 of qh[ib32] << 8; the low scale
+    # nibble covers l = 0, 1 and the high one l = 2, 3; sign bit j of byte 4 ib32 + l
+    d = np.array([[0x3C00]], np.uint16)
+    rng = np.random.default_rng(33)
+    qs = rng.integers(0, 256, (1, 1, 32))
+    qh = rng.integers(0, 256, (1, 1, 8))
+    signs = rng.integers(0, 256, (1, 1, 32))
+    sc = rng.integers(0, 16, (1, 1, 16))
+    grid = orc.iq_grid(gp.GGML_IQ2_S)
+    wb, vals = gp.pack_iq2_s(d, qs, qh, signs, sc, grid)
+    assert wb[0, 74 + 3] == sc[0, 0, 6] | (sc[0, 0, 7] << 4)
+    got = orc.dequant_rows(gp.GGML_IQ2_S, wb, 1, 256)[0]
+    for ib in range(8):
+        for l in range(4):
+            idx = int(qs[0, 0, 4 * ib + l]) | (((int(qh[0, 0, ib]) >> (2 * l)) & 3) << 8)
+            e = int(grid[idx])
+            dl = F32(F32(F32(1.0) * F32(0.5 + sc[0, 0, 2 * ib + l // 2])) * F32(0.25))
+            s = int(signs[0, 0, 4 * ib + l])
+            want = np.array([(-1 if (s >> j) & 1 else 1) * F32(dl * F32((e >> (8 * j)) & 0xFF))
+                             for j in range(8)], F32)
+            assert np.array_equal(got[32 * ib + 8 * l:32 * ib + 8 * l + 8], want), (ib, l)
+    assert np.array_equal(got, vals[0])
 
 
 def test_mxfp4_scale_exponent_and_special_bytes():

@@ -2,7 +2,7 @@
 llmp_attn_block_batch) against the oracle's block (orc.attn_block).
 
 Each case draws, from a fixed seed (so every run checks the same cases):
-- the projection formats: one of the 15 GGUF types for q, k, v and o, or a K-quant mix
+- the projection formats: one of the 18 GGUF types for q, k, v and o, or a K-quant mix
   (Q4_K_M, Q3_K_L, Q5_K_M);
 - a head shape: GQA group 1-8 or 16 over 1-4 KV heads, head_dim 64 or 128, and an embedding
   width of 1024-3072;
@@ -40,7 +40,7 @@ def _draw(rng):
         t = tbg.TYPES[int(rng.integers(len(tbg.TYPES)))]
         types, tname = (t,) * 4, tbg.NAMES[t]
     superblock = any(t in (gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS,
-                           gp.GGML_Q2_K) for t in types)
+                           gp.GGML_Q2_K, gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S) for t in types)
     while True:   # super-block formats need q_dim (the output projection's width) in whole 256s
         hkv = int(rng.choice([1, 2, 4]))
         group = int(rng.choice([1, 2, 3, 4, 5, 8, 16]))

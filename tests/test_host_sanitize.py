@@ -68,6 +68,11 @@ BLOCKS = {
     gp.GGML_Q5_1: (32, [("d", 2), ("m", 2), ("qh", 4), ("qs", 16)], {"qs": 0, "qh": 1, "d": 2, "m": 3}),
     gp.GGML_Q2_K: (256, [("scales", 16), ("qs", 64), ("d", 2), ("dmin", 2)],
                    {"qs": 0, "scales": 1, "d": 2, "dmin": 3}),
+    gp.GGML_IQ3_XXS: (256, [("d", 2), ("qs", 64), ("sas", 32)], {"qs": 0}),
+    gp.GGML_IQ3_S: (256, [("d", 2), ("qs", 64), ("qh", 8), ("signs", 32), ("scales", 4)],
+                    {"qs": 0, "signs": 1}),
+    gp.GGML_IQ2_S: (256, [("d", 2), ("qs", 32), ("signs", 32), ("qh", 8), ("scales", 8)],
+                    {"qs": 0, "signs": 1}),
 }
 
 
@@ -89,8 +94,42 @@ def _iq4xs_scales(parts):
     return ((low | (top << 4)) - 32).astype(np.int8).view(np.uint8)
 
 
+def _iq3xxs_aux(parts):
+    b = parts["sas"].astype(np.int64).reshape(parts["sas"].shape[:-1] + (8, 4))
+    return b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16) | (b[..., 3] << 24)   # [rows, nb, 8]
+
+
+def _iq3xxs_signs(parts):
+    # each 8-weight group's 7-bit pattern index (bits 7l of its 32-group's word) with the parity
+    # bit that makes the count of set bits even
+    aux = _iq3xxs_aux(parts)
+    idx = np.stack([(aux >> (7 * l)) & 0x7F for l in range(4)], axis=-1)        # [rows, nb, 8, 4]
+    par = sum((idx >> k) & 1 for k in range(7)) & 1
+    return (idx | (par << 7)).astype(np.uint8).reshape(aux.shape[:-1] + (32,))
+
+
+def _iq3xxs_side(parts):
+    # d, two zero bytes, the scales (bits 28-31 of each word) two per byte, low nibble first
+    sc = _iq3xxs_aux(parts) >> 28
+    packed = (sc[..., 0::2] | (sc[..., 1::2] << 4)).astype(np.uint8)
+    zero = np.zeros(sc.shape[:-1] + (2,), np.uint8)
+    return np.concatenate([parts["d"], zero, packed], axis=-1)
+
+
+def _iq3s_side(parts):
+    zero = np.zeros(parts["d"].shape, np.uint8)
+    return np.concatenate([parts["qh"], parts["scales"], parts["d"], zero], axis=-1)
+
+
+def _iq2s_side(parts):
+    zero = np.zeros(parts["d"].shape[:-1] + (6,), np.uint8)
+    return np.concatenate([parts["scales"], parts["qh"], parts["d"], zero], axis=-1)
+
+
 # planes computed from a block's fields rather than copied from it
-DERIVED = {gp.GGML_Q3_K: {2: _q3k_scales}, gp.GGML_IQ4_XS: {1: _iq4xs_scales}}
+DERIVED = {gp.GGML_Q3_K: {2: _q3k_scales}, gp.GGML_IQ4_XS: {1: _iq4xs_scales},
+           gp.GGML_IQ3_XXS: {1: _iq3xxs_signs, 2: _iq3xxs_side}, gp.GGML_IQ3_S: {2: _iq3s_side},
+           gp.GGML_IQ2_S: {2: _iq2s_side}}
 DENSE = {gp.GGML_F32: 4, gp.GGML_F16: 2, gp.GGML_BF16: 2}
 
 
@@ -121,7 +160,7 @@ CASES = [(t, rows, cols) for t in (gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GG
                                   gp.GGML_Q5_0, gp.GGML_IQ4_NL, gp.GGML_MXFP4, gp.GGML_Q5_1)
          for rows, cols in ((1, 32), (3, 96), (17, 2880))] + \
         [(t, rows, cols) for t in (gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_XS,
-                                  gp.GGML_Q2_K)
+                                  gp.GGML_Q2_K, gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S)
          for rows, cols in ((1, 256), (5, 768), (33, 3072))]
 
 
