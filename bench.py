@@ -479,21 +479,35 @@ def verify_run(ctx: int, K: int, steps: int, rotate_bytes: int, q8: bool = False
             "kv_read_gbps": round(kv_bytes(ctx - K, q8) / (us * 1e-6) / 1e9, 1)}
 
 
+# Per GGUF block type: (weights per block, bytes per block, byte offsets of its fp16 scale
+# fields) (GGMLType.java:4-35 and each tensor class's layout).
+GGUF_BLOCKS = {8: (32, 34, (0,)), 2: (32, 18, (0,)), 6: (32, 22, (0,)), 7: (32, 24, (0, 2)),
+               20: (32, 18, (0,)), 39: (32, 17, ()), 10: (256, 84, (80, 82)), 11: (256, 110, (108,)),
+               12: (256, 144, (0, 2)), 13: (256, 176, (0, 2)), 14: (256, 210, (208,)),
+               23: (256, 136, (0,)), 18: (256, 98, (0,)), 21: (256, 110, (0,)), 22: (256, 82, (0,))}
+GGUF_NAMES = {0: "F32", 1: "F16", 30: "BF16", 8: "Q8_0", 2: "Q4_0", 6: "Q5_0", 7: "Q5_1",
+              20: "IQ4_NL", 39: "MXFP4", 10: "Q2_K", 11: "Q3_K", 12: "Q4_K", 13: "Q5_K",
+              14: "Q6_K", 23: "IQ4_XS", 18: "IQ3_XXS", 21: "IQ3_S", 22: "IQ2_S"}
+
+
 def synthetic_gguf(t: int, rows: int, cols: int, rng) -> np.ndarray:
-    """Random GGUF-layout bytes of type t (Q4_K, Q6_K, Q3_K or Q5_K) with finite fp16 scale
-    fields: uniform quants and scale bytes, super-block scales 2^-10 (d) and 2^-12 (dmin)."""
-    ns = cols // 256
+    """Random GGUF-layout bytes of type t: uniform quant and sub-block scale bytes, fp16 block
+    scales 2^-10 (the second field, a min, 2^-12), MXFP4 exponents 2^-7; dense types normal
+    values times 0.02."""
+    if t in (0, 1, 30):
+        w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+        if t == 0:
+            return w.view(np.uint8).reshape(-1)
+        if t == 1:
+            return w.astype(np.float16).view(np.uint8).reshape(-1)
+        return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)
+    bw, bb, scales = GGUF_BLOCKS[t]
+    b = rng.integers(0, 256, (rows, cols // bw, bb), dtype=np.uint8)
     f16 = lambda v: np.frombuffer(np.float16(v).tobytes(), np.uint8)
-    if t in (12, 13):   # Q4_K (144 bytes) / Q5_K (176): d, dmin (fp16) first
-        b = rng.integers(0, 256, (rows, ns, 144 if t == 12 else 176), dtype=np.uint8)
-        b[:, :, 0:2] = f16(2.0 ** -10)
-        b[:, :, 2:4] = f16(2.0 ** -12)
-    elif t == 11:       # Q3_K: hmask, qs, 12 scale bytes, d (fp16) at byte 108
-        b = rng.integers(0, 256, (rows, ns, 110), dtype=np.uint8)
-        b[:, :, 108:110] = f16(2.0 ** -10)
-    else:               # Q6_K: ql, qh, 16 int8 scales, d (fp16) at byte 208
-        b = rng.integers(0, 256, (rows, ns, 210), dtype=np.uint8)
-        b[:, :, 208:210] = f16(2.0 ** -12)
+    for i, o in enumerate(scales):
+        b[:, :, o:o + 2] = f16(2.0 ** (-10 - 2 * i))
+    if t == 39:
+        b[:, :, 0] = 120
     return b.reshape(-1)
 
 
@@ -513,6 +527,7 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
     dim = 3072
+    types, label = MIXES[mix] if isinstance(mix, str) else (mix, "all " + GGUF_NAMES[mix[0]])
     c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=C3.theta)
     fp = hfp.HipForwardPass(c, ctx)
     try:
@@ -523,7 +538,7 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
             fp.kv.write(layer, 0, kc, vc)
         fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_Q8_1 if q8_input else _lib.LLMP_INPUT_F32)
         wbytes = 0
-        tq, tk, tv, to = MIXES[mix][0]
+        tq, tk, tv, to = types
         for layer in range(n_layers):
             lw = hfp.TransformerLayerWeights(attnNorm=np.ones(dim, np.float32))
             for name, t, rows, cols in (("wq", tq, c.q_dim, dim), ("wk", tk, c.kv_dim, dim),
@@ -546,7 +561,7 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
     finally:
         fp.close()
     us = ms / steps * 1e3
-    return {"ctx": ctx, "weights": MIXES[mix][1], "dim": dim,
+    return {"ctx": ctx, "weights": label, "dim": dim,
             "input": ("Q8_1 (int8 dot products for "
                       + ("Q4_K" if mix == "q4_k_m" else "Q3_K and Q5_K" if mix == "q3_k_l" else "Q5_K")
                       + ")") if q8_input else "fp32",
@@ -811,6 +826,11 @@ def main() -> int:
                     help="--profile-block: the projection weight mix")
     ap.add_argument("--profile-block", action="store_true",
                     help="for rocprofv3: the attention-block graph at --ctx2 only, then exit")
+    ap.add_argument("--profile-formats", action="store_true",
+                    help="for rocprofv3: the attention-block graph at --ctx2 with q, k, v and o "
+                         "in each GGUF type in turn, then exit")
+    ap.add_argument("--formats", default=None,
+                    help="--profile-formats: comma-separated type names (F32, Q8_0, IQ3_S, ...)")
     ap.add_argument("--profile-block-batch", type=int, default=0, metavar="K",
                     help="for rocprofv3: the K-token attention-block graph at --ctx2 only, then exit")
     ap.add_argument("--profile-workload", action="store_true",
@@ -861,6 +881,14 @@ def main() -> int:
     if args.profile_block:
         r = block_run(args.ctx2 or 4096, args.steps, q8_input=args.block_q8, mix=args.block_mix)
         log(f"[bench] profile block: {r}")
+        return 0
+    if args.profile_formats:
+        # projection formats (all, or the --formats list), q, k, v and o of one type each (28
+        # layers, graph replays)
+        pick = [t for t in GGUF_NAMES if args.formats is None or GGUF_NAMES[t] in args.formats.split(",")]
+        for t in pick:
+            r = block_run(args.ctx2 or 4096, args.steps, mix=(t, t, t, t))
+            log(f"[bench] profile formats: {GGUF_NAMES[t]} {r}")
         return 0
     if args.profile_block_batch:
         r = block_batch_run(args.ctx2 or 4096, args.profile_block_batch, args.steps)
