@@ -50,7 +50,7 @@ struct DevWeight {
     gk::WPlanes planes{};
     // The token-batched projections split fp32 and bf16 weights into fp16 parts: false when
     // some weight reaches fp16's largest magnitude, 65504, or for a type without a
-    // token-batched kernel (Q2_K, IQ3_XXS, IQ3_S, IQ2_S) (llmp_attn_block_batch then runs the tokens one by one, on
+    // token-batched kernel (Q2_K) (llmp_attn_block_batch then runs the tokens one by one, on
     // the fp32 single-token kernels).
     bool tok_ok = true;
 };

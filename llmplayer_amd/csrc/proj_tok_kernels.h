@@ -522,6 +522,129 @@ struct PQ3K {
     }
 };
 
+// ---- codebook formats (IQ3_XXS, IQ3_S, IQ2_S; planes and values as gemv_kernels.h) ---------
+// Lane kq of group gi takes unit u = 16 ch + 4 gi + kq (8 columns): 32-group g = 4 (ch%2) + gi
+// of super-block ch/2, 8-weight group l = kq.  A = the signed codebook bytes, exact in fp16
+// (at most 62); the group scale multiplies the product afterwards, and scale * byte is exact in
+// fp32 (an 11-bit d times at most 5 + 6 bits), so each term equals the reference's weight.
+// The workgroup copies the codebook to LDS once (wave_rows), as the single-token kernel does.
+template <int BYTES>
+__device__ __forceinline__ uint4* codebook_lds() {
+    __shared__ uint4 g[BYTES / 16];
+    return g;
+}
+// 8 signed codebook bytes (lo: weights 0-3, hi: 4-7; sign bit j of s negates weight j) as fp16
+__device__ __forceinline__ uint4 signed_grid8(unsigned lo, unsigned hi, unsigned s) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float a = gk::byte_f(lo, e), b = gk::byte_f(hi, e);
+        v[e] = (s >> e) & 1u ? -a : a;
+        v[4 + e] = (s >> (4 + e)) & 1u ? -b : b;
+    }
+    return f16x8_of(v);
+}
+
+// IQ3_XXS: per 32-group the factor d * (0.5 + sc) * 0.5.  Table per row: the chunk's 4.
+struct PIQ3_XXS {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 4, GRID_BYTES = 256 * 4;
+    static constexpr bool MIN = false, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    static __device__ __forceinline__ const void* grid_src() { return gk::kIq3xxsGrid; }
+    struct Raw { unsigned q[4], s[4]; uint2 h; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+            const unsigned u = (unsigned)(16 * ch + 4 * min(gi, ng - 1) + kq);
+            r.q[gi] = ldo<unsigned short>(rp(w, 0, row), 2u * u);
+            r.s[gi] = ldo<unsigned char>(rp(w, 1, row), u);
+        }
+        r.h = ldo<uint2>(rp(w, 2, row), (unsigned)(ch >> 1) * 8u);
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int ch) {
+        const int g = 4 * (ch & 1) + kq;
+        const float d = h2f((unsigned short)(r.h.x & 0xFFFFu));
+        tab[m * TAB + kq] = (d * (0.5f + (float)((r.h.y >> (4 * g)) & 15u))) * 0.5f;
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int) {
+        const unsigned* g = reinterpret_cast<const unsigned*>(codebook_lds<GRID_BYTES>());
+        a[0] = signed_grid8(g[r.q[gi] & 0xFFu], g[r.q[gi] >> 8], r.s[gi]);
+    }
+};
+
+// IQ3_S: ninth index bits from qh[g/4 + g%2] (the reference's reading); per 32-group the factor
+// d * (1 + 2 sc).  Table per row: the chunk's 4.
+struct PIQ3_S {
+    static constexpr int NA = 1, NPAIR = 2, TAB = 4, GRID_BYTES = 512 * 4;
+    static constexpr bool MIN = false, HALVES = false;
+    static constexpr PartPair pairs[2] = {{0, 0}, {0, 1}};
+    static __device__ __forceinline__ const void* grid_src() { return gk::kIq3sGrid; }
+    struct Raw { unsigned q[4], s[4]; uint4 side; int h; };   // side: qh[8], scales[4], d
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+            const unsigned u = (unsigned)(16 * ch + 4 * min(gi, ng - 1) + kq);
+            r.q[gi] = ldo<unsigned short>(rp(w, 0, row), 2u * u);
+            r.s[gi] = ldo<unsigned char>(rp(w, 1, row), u);
+        }
+        r.side = ldo<uint4>(rp(w, 2, row), (unsigned)(ch >> 1) * 16u);
+        r.h = ch & 1;
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int ch) {
+        const int g = 4 * (ch & 1) + kq;
+        const float d = h2f((unsigned short)(r.side.w & 0xFFFFu));
+        tab[m * TAB + kq] = d * (float)(1 + 2 * (int)((r.side.z >> (4 * g)) & 15u));
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        const unsigned* g = reinterpret_cast<const unsigned*>(codebook_lds<GRID_BYTES>());
+        // group g = 4h + gi reads qh[g/4 + g%2] = qh[h + gi%2], a byte of side.x
+        const unsigned qh = (r.side.x >> (8 * (r.h + (gi & 1)))) & 0xFFu;
+        const unsigned l2 = 2u * (unsigned)kq;
+        const unsigned i0 = (r.q[gi] & 0xFFu) | (((qh >> l2) & 1u) << 8);
+        const unsigned i1 = (r.q[gi] >> 8) | (((qh >> (l2 + 1u)) & 1u) << 8);
+        a[0] = signed_grid8(g[i0], g[i1], r.s[gi]);
+    }
+};
+
+// IQ2_S: index bits 8-9 from bits 2l..2l+1 of qh[g]; the 16-column halves of a 32-group have
+// their own factors d * (0.5 + sc) * 0.25, so the A operand goes out twice with the other half
+// zeroed (as Q6_K).  Table per row: the two factors of each of the chunk's 4 groups.
+struct PIQ2_S {
+    static constexpr int NA = 2, NPAIR = 4, TAB = 8, GRID_BYTES = 1024 * 8;
+    static constexpr bool MIN = false, HALVES = true;
+    static constexpr PartPair pairs[4] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}};
+    static __device__ __forceinline__ const void* grid_src() { return gk::kIq2sGrid; }
+    struct Raw { unsigned q[4], s[4]; uint4 side; unsigned short d; int h; };   // side: scales[8], qh[8]
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+        const unsigned sb = (unsigned)(ch >> 1);
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+            const unsigned u = (unsigned)(16 * ch + 4 * min(gi, ng - 1) + kq);
+            r.q[gi] = ldo<unsigned char>(rp(w, 0, row), u);
+            r.s[gi] = ldo<unsigned char>(rp(w, 1, row), u);
+        }
+        r.side = ldo<uint4>(rp(w, 2, row), sb * 24u);
+        r.d = ldo<unsigned short>(rp(w, 2, row), sb * 24u + 16u);
+        r.h = ch & 1;
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int ch) {
+        const int g = 4 * (ch & 1) + kq;
+        const unsigned b = ((g < 4 ? r.side.x : r.side.y) >> (8 * (g & 3))) & 0xFFu;
+        const float d = h2f(r.d);
+        reinterpret_cast<float2*>(tab + m * TAB)[kq] =
+            make_float2((d * (0.5f + (float)(b & 15u))) * 0.25f, (d * (0.5f + (float)(b >> 4))) * 0.25f);
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        const uint2* g = reinterpret_cast<const uint2*>(codebook_lds<GRID_BYTES>());
+        const unsigned qh = ((r.h ? r.side.w : r.side.z) >> (8 * gi)) & 0xFFu;   // qh[4h + gi]
+        const uint2 e = g[r.q[gi] | (((qh >> (2 * kq)) & 3u) << 8)];
+        const uint4 u = signed_grid8(e.x, e.y, r.s[gi]);
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        a[0] = kq < 2 ? u : z;   // columns 0-15: the low scale nibble
+        a[1] = kq < 2 ? z : u;   // columns 16-31: the high one
+    }
+};
+
 // F16 rows: the 8 weights of a lane are its A operand as they are.
 struct PF16 {
     static constexpr int NA = 1, NPAIR = 2, TAB = 0;
@@ -792,13 +915,20 @@ __device__ __forceinline__ void wave_rows(const ProjTokArgs& a, const WPlanes& w
     auto chunk = [&](int i) { return wave + min(i, n - 1) * kWaves; };
     ChunkRegs<F> ca, cb;
     if (n > 0) chunk_issue<F, NORM>(ca, a, w, row, chunk(0), ngroups, lane, tok_live);
-    if constexpr (NORM) {   // the norm weights times 2^-E to LDS once per workgroup, behind
-                            // the first loads ((x * w) * 2^-E = x * (w * 2^-E), exactly)
-        const float4* src = reinterpret_cast<const float4*>(a.norm_w);
-        for (int c4 = wave * 64 + lane; c4 < (a.cols >> 2); c4 += kThreads) {
-            const float4 wv = src[c4];
-            reinterpret_cast<float4*>(s_nw)[c4] =
-                make_float4(wv.x * fin, wv.y * fin, wv.z * fin, wv.w * fin);
+    constexpr int GRID = gk::FmtGrid<F>::BYTES;   // codebook formats: the codebook to LDS
+    if constexpr (NORM || GRID > 0) {
+        if constexpr (NORM) {   // the norm weights times 2^-E to LDS once per workgroup, behind
+                                // the first loads ((x * w) * 2^-E = x * (w * 2^-E), exactly)
+            const float4* src = reinterpret_cast<const float4*>(a.norm_w);
+            for (int c4 = wave * 64 + lane; c4 < (a.cols >> 2); c4 += kThreads) {
+                const float4 wv = src[c4];
+                reinterpret_cast<float4*>(s_nw)[c4] =
+                    make_float4(wv.x * fin, wv.y * fin, wv.z * fin, wv.w * fin);
+            }
+        }
+        if constexpr (GRID > 0) {
+            const uint4* src = static_cast<const uint4*>(gk::FmtGrid<F>::src());
+            for (int i = wave * 64 + lane; i < GRID / 16; i += kThreads) codebook_lds<GRID>()[i] = src[i];
         }
         __syncthreads();
     }
@@ -819,9 +949,12 @@ constexpr int tab_floats() { return F1::TAB > F2::TAB ? (F1::TAB > 0 ? F1::TAB :
 // Workgroup b: rows 16b .. 16b+15 (one segment, one format: segment sizes are multiples of 16),
 // all K tokens.
 // Waves per SIMD the kernel is compiled for: 4 (two workgroups per CU, so 256 CUs take 512
-// row tiles in one round), 3 for F32 rows (their raw chunk is twice as large).
+// row tiles in one round), 3 for F32 rows (their raw chunk is twice as large) and IQ2_S rows
+// (14 registers of raw bytes per chunk and two A operands: 4 waves spill with the norm).
 template <class F1, class F2>
-constexpr int waves_per_eu() { return std::is_same<F1, PF32>::value ? 3 : 4; }
+constexpr int waves_per_eu() {
+    return std::is_same<F1, PF32>::value || std::is_same<F1, PIQ2_S>::value ? 3 : 4;
+}
 
 template <class F1, class F2, bool NORM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(waves_per_eu<F1, F2>())))

@@ -26,7 +26,7 @@ NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "
          11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k",
          18: "iq3_xxs", 21: "iq3_s", 22: "iq2_s"}
 # formats with no token-batched kernel: K-token calls run their tokens one by one
-PER_TOKEN = (gp.GGML_Q2_K, gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S)
+PER_TOKEN = (gp.GGML_Q2_K,)
 
 
 def _tensor(t, rows, cols, rng, scale=0.05):
