@@ -49,9 +49,9 @@ struct DevWeight {
     void* mem = nullptr;
     gk::WPlanes planes{};
     // The token-batched projections split fp32 and bf16 weights into fp16 parts: false when
-    // some weight reaches fp16's largest magnitude, 65504, or for a type without a
-    // token-batched kernel (Q2_K) (llmp_attn_block_batch then runs the tokens one by one, on
-    // the fp32 single-token kernels).
+    // some weight reaches fp16's largest magnitude, 65504, or for a type proj_tok_supported
+    // rejects (llmp_attn_block_batch then runs the tokens one by one, on the fp32 single-token
+    // kernels).
     bool tok_ok = true;
 };
 

@@ -34,7 +34,7 @@ bool proj_tok_supported(int ggml_type) {
     switch (ggml_type) {
     case gk::kF32: case gk::kF16: case gk::kBF16: case gk::kQ8_0: case gk::kQ4_0: case gk::kQ4_K:
     case gk::kQ6_K: case gk::kQ5_0: case gk::kQ3_K: case gk::kQ5_K: case gk::kIQ4_NL: case gk::kIQ4_XS:
-    case gk::kMXFP4: case gk::kQ5_1: case gk::kIQ3_XXS: case gk::kIQ3_S: case gk::kIQ2_S:
+    case gk::kMXFP4: case gk::kQ5_1: case gk::kIQ3_XXS: case gk::kIQ3_S: case gk::kIQ2_S: case gk::kQ2_K:
         return true;
     default:
         return false;
@@ -58,7 +58,7 @@ hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_
     // super-block formats need whole super-blocks of 256 columns
     auto superblock = [](int t) {
         return t == gk::kQ4_K || t == gk::kQ6_K || t == gk::kQ3_K || t == gk::kQ5_K || t == gk::kIQ4_XS ||
-               t == gk::kIQ3_XXS || t == gk::kIQ3_S || t == gk::kIQ2_S;
+               t == gk::kIQ3_XXS || t == gk::kIQ3_S || t == gk::kIQ2_S || t == gk::kQ2_K;
     };
     if ((superblock(first_type) || superblock(second_type)) && a.cols % 256) return hipErrorInvalidValue;
     if (second_type >= 0) {
@@ -82,6 +82,7 @@ hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_
     case gk::kIQ4_XS: return launch_ff<tk::PIQ4_XS, tk::PIQ4_XS>(a, st);
     case gk::kMXFP4: return launch_ff<tk::PMXFP4, tk::PMXFP4>(a, st);
     case gk::kQ5_1: return launch_ff<tk::PQ5_1, tk::PQ5_1>(a, st);
+    case gk::kQ2_K: return launch_ff<tk::PQ2_K, tk::PQ2_K>(a, st);
     case gk::kIQ3_XXS: return launch_ff<tk::PIQ3_XXS, tk::PIQ3_XXS>(a, st);
     case gk::kIQ3_S: return launch_ff<tk::PIQ3_S, tk::PIQ3_S>(a, st);
     case gk::kIQ2_S: return launch_ff<tk::PIQ2_S, tk::PIQ2_S>(a, st);

@@ -522,6 +522,47 @@ struct PQ3K {
     }
 };
 
+// Q2_K (the reference's element order: element j of a super-block at bits 2(j%4) of quant byte
+// j/4; gemv_kernels.h): chunk = half h = ch%2 of a super-block, lane kq of group gi takes quant
+// bytes 32h + 8gi + 2kq, +1 (columns 8kq .. 8kq+7 of the group).  Each 16-column sub-block has
+// its own scale and min, so the A operand goes out twice with the other half zeroed (as Q6_K)
+// and the min term takes the input sums of both halves (as Q4_K's per 32).  Table per row:
+// (d*sc, dmin*m) of the group's two sub-blocks, for each of the chunk's 4 groups
+// (Q2_KFloatTensor.dotQ2KF32: d*sc*sumQ - dmin*m*sumF per sub-block of 16).
+struct PQ2_K {
+    static constexpr int NA = 2, NPAIR = 4, TAB = 16;
+    static constexpr bool MIN = true, HALVES = true;
+    static constexpr PartPair pairs[4] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}};
+    struct Raw { unsigned q[4]; uint2 sc; unsigned short d, dm; };
+    static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
+        const unsigned sb = (unsigned)(ch >> 1), h = (unsigned)(ch & 1);
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+            r.q[gi] = ldo<unsigned short>(rp(w, 0, row), sb * 64u + 32u * h + 8u * (unsigned)min(gi, ng - 1) + 2u * (unsigned)kq);
+        r.sc = ldo<uint2>(rp(w, 1, row), sb * 16u + 8u * h);
+        r.d = ldo<unsigned short>(rp(w, 2, row), sb * 2u);
+        r.dm = ldo<unsigned short>(rp(w, 3, row), sb * 2u);
+    }
+    static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int) {
+        // group kq: sub-blocks 2kq and 2kq + 1 of the chunk (scale bytes 2kq, 2kq + 1)
+        const unsigned wv = kq < 2 ? r.sc.x : r.sc.y;
+        const unsigned b0 = (wv >> (16 * (kq & 1))) & 0xFFu, b1 = (wv >> (16 * (kq & 1) + 8)) & 0xFFu;
+        const float d = h2f(r.d), dm = h2f(r.dm);
+        reinterpret_cast<float4*>(tab + m * TAB)[kq] =
+            make_float4(d * (float)(b0 & 15u), dm * (float)(b0 >> 4), d * (float)(b1 & 15u), dm * (float)(b1 >> 4));
+    }
+    static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
+        const unsigned q = r.q[gi];
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (float)((q >> (8 * (e >> 2) + 2 * (e & 3))) & 3u);
+        const uint4 u = f16x8_of(v);
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        a[0] = kq < 2 ? u : z;   // columns 0-15: sub-block 2gi
+        a[1] = kq < 2 ? z : u;   // columns 16-31: sub-block 2gi + 1
+    }
+};
+
 // ---- codebook formats (IQ3_XXS, IQ3_S, IQ2_S; planes and values as gemv_kernels.h) ---------
 // Lane kq of group gi takes unit u = 16 ch + 4 gi + kq (8 columns): 32-group g = 4 (ch%2) + gi
 // of super-block ch/2, 8-weight group l = kq.  A = the signed codebook bytes, exact in fp16
@@ -854,13 +895,22 @@ __device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& ac
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = v[e] * wv[e];
         }
-        float gs = 0.0f;   // the group's input sum for token l%16 (Q4_K's min term)
+        float gs = 0.0f, gs_hi = 0.0f;   // the group's input sum for token l%16 (the min term);
+                                          // per 16-column half (Q2_K): gs the first, gs_hi the second
         if constexpr (F::MIN) {
             gs = v[0];
 #pragma unroll
             for (int e = 1; e < 8; ++e) gs = gs + v[e];
-            gs = dk::lane_step<16, false>(gs);   // the group's 4 k-quads (lanes l ^ 16, l ^ 32)
-            gs = dk::lane_step<32, false>(gs);
+            gs = dk::lane_step<16, false>(gs);   // the k-quad pairs (lanes l ^ 16): half sums
+            if constexpr (F::HALVES) {
+                // lanes 0-31 hold the first half's sum, 32-63 the second's: both to every lane
+                const unsigned u = __builtin_bit_cast(unsigned, gs);
+                const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+                gs = __builtin_bit_cast(float, (unsigned)p[0]);
+                gs_hi = __builtin_bit_cast(float, (unsigned)p[1]);
+            } else {
+                gs = dk::lane_step<32, false>(gs);   // the group's 4 k-quads
+            }
         }
         uint4 b[2];
         split8(v, b[0], b[1]);
@@ -885,7 +935,10 @@ __device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& ac
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float* tr = tab + (4 * kq + i) * F::TAB;
-                if constexpr (F::MIN) {           // Q4_K: (d*sc, dmin*m) of sub-block gi
+                if constexpr (F::MIN && F::HALVES) {   // Q2_K: (d*sc, dmin*m) of both halves
+                    const float4 f = reinterpret_cast<const float4*>(tr)[gi];
+                    acc[i] = acc[i] + ((f.x * t0[i] - f.y * gs) + (f.z * t1[i] - f.w * gs_hi));
+                } else if constexpr (F::MIN) {    // Q4_K: (d*sc, dmin*m) of sub-block gi
                     const float2 f = reinterpret_cast<const float2*>(tr)[gi];
                     acc[i] = acc[i] + (f.x * t0[i] - f.y * gs);
                 } else if constexpr (F::HALVES) {  // Q6_K: d*sc of the two halves

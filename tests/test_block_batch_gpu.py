@@ -135,8 +135,7 @@ TYPES = tbg.TYPES
 @pytest.mark.parametrize("t", TYPES, ids=[NAMES[t] for t in TYPES])
 def test_block_batch_every_weight_format(t):
     """Each format's matrix-core path: 5 tokens (a partial token tile) after a 40-row prefix,
-    then 5 more.  Q2_K has no token-batched kernel: its tokens run one by one (ten single-token
-    decode launches), with the same results."""
+    then 5 more."""
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
     if t in tbg.PER_TOKEN:
         _run_batch(c, 1024, 64, 40, 5, (t, t, t, t), seed=1600 + t, what=NAMES[t], rounds=2,
@@ -155,10 +154,12 @@ def test_block_batch_c3_q3_k_l_and_q5_k_m(mix):
     _run_batch(c, 3072, 4096, 4000, 8, types, seed=1650 + len(mix), what=f"C3 {mix}", batched=True)
 
 
-@pytest.mark.parametrize("t", [gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S], ids=["iq3_xxs", "iq3_s", "iq2_s"])
-def test_block_batch_c3_codebook_formats(t):
-    """The C3 shape with q, k, v and o in a codebook format: 16 tokens after 1000 rows, each
-    wave over three 128-column chunks (both halves of the super-blocks), the codebook in LDS."""
+@pytest.mark.parametrize("t", [gp.GGML_IQ3_XXS, gp.GGML_IQ3_S, gp.GGML_IQ2_S, gp.GGML_Q2_K],
+                         ids=["iq3_xxs", "iq3_s", "iq2_s", "q2_k"])
+def test_block_batch_c3_codebook_formats_and_q2_k(t):
+    """The C3 shape with q, k, v and o in a codebook format (the codebook in LDS) or Q2_K (scale
+    and min per 16 columns): 16 tokens after 1000 rows, each wave over three 128-column chunks
+    (both halves of the super-blocks)."""
     c = hfp.ModelConfig(24, 8, 128, 1, rope_freq_base=500000.0)
     _run_batch(c, 3072, 1100, 1000, 16, (t, t, t, t), seed=1670 + t, what=f"C3 {NAMES[t]}", batched=True)
 

@@ -25,8 +25,8 @@ TYPES = [gp.GGML_F32, gp.GGML_F16, gp.GGML_BF16, gp.GGML_Q8_0, gp.GGML_Q4_0, gp.
 NAMES = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0", 2: "q4_0", 12: "q4_k", 14: "q6_k", 6: "q5_0",
          11: "q3_k", 13: "q5_k", 20: "iq4_nl", 23: "iq4_xs", 39: "mxfp4", 7: "q5_1", 10: "q2_k",
          18: "iq3_xxs", 21: "iq3_s", 22: "iq2_s"}
-# formats with no token-batched kernel: K-token calls run their tokens one by one
-PER_TOKEN = (gp.GGML_Q2_K,)
+# formats with no token-batched kernel, whose K-token calls run their tokens one by one: none
+PER_TOKEN = ()
 
 
 def _tensor(t, rows, cols, rng, scale=0.05):
