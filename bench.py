@@ -569,14 +569,16 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
             "kv_bytes_per_layer": kv_bytes(ctx), "layers_rotated": n_layers}
 
 
-def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28) -> dict:
-    """The attention half of a C3 Q4_K_M layer (as block_run) for K draft tokens at positions
-    ctx-K .. ctx-1 in one llmp_attn_block_batch call (projection weights read once for the K
-    tokens), against K single-token llmp_attn_block calls over the same layers; graph replays
-    over n_layers layers with their own weights and caches."""
+def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28, mix="q4_k_m") -> dict:
+    """The attention half of a C3 layer (as block_run; default the Q4_K_M mix, or a MIXES key,
+    or four GGML types) for K draft tokens at positions ctx-K .. ctx-1 in one
+    llmp_attn_block_batch call (projection weights read once for the K tokens), against K
+    single-token llmp_attn_block calls over the same layers; graph replays over n_layers
+    layers with their own weights and caches."""
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
     dim = 3072
+    types, label = MIXES[mix] if isinstance(mix, str) else (mix, "all " + GGUF_NAMES[mix[0]])
     c = hfp.ModelConfig(HQ, HKV, D, n_layers, architecture=hfp.ARCH_LLAMA, rope_freq_base=C3.theta)
     fp = hfp.HipForwardPass(c, ctx)
     try:
@@ -589,8 +591,8 @@ def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28) -> dict:
         wbytes = 0
         for layer in range(n_layers):
             lw = hfp.TransformerLayerWeights(attnNorm=np.ones(dim, np.float32))
-            for name, t, rows, cols in (("wq", 12, c.q_dim, dim), ("wk", 12, c.kv_dim, dim),
-                                        ("wv", 14, c.kv_dim, dim), ("wo", 12, dim, c.q_dim)):
+            for name, t, rows, cols in (("wq", types[0], c.q_dim, dim), ("wk", types[1], c.kv_dim, dim),
+                                        ("wv", types[2], c.kv_dim, dim), ("wo", types[3], dim, c.q_dim)):
                 data = synthetic_gguf(t, rows, cols, rng)
                 setattr(lw, name, hfp.GgufTensor(t, rows, cols, data))
                 if layer == 0:
@@ -619,7 +621,7 @@ def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28) -> dict:
         fp.close()
     us_b = ms_b / steps * 1e3
     us_s = ms_s / max(1, steps // 4) * 1e3
-    return {"K": K, "ctx": ctx, "weights": "Q4_K_M mix (Q4_K q/k/o, Q6_K v)", "dim": dim,
+    return {"K": K, "ctx": ctx, "weights": label, "dim": dim,
             "us_per_call": round(us_b, 2), "us_per_token": round(us_b / K, 2),
             "single_token_blocks_us": round(us_s, 2), "speedup_vs_single_token_blocks": round(us_s / us_b, 2),
             "weight_bytes_per_layer": wbytes, "kv_bytes_per_layer": kv_bytes(ctx - K),
@@ -884,10 +886,13 @@ def main() -> int:
         return 0
     if args.profile_formats:
         # projection formats (all, or the --formats list), q, k, v and o of one type each (28
-        # layers, graph replays)
+        # layers, graph replays); with --profile-block-batch K, K tokens per call
         pick = [t for t in GGUF_NAMES if args.formats is None or GGUF_NAMES[t] in args.formats.split(",")]
         for t in pick:
-            r = block_run(args.ctx2 or 4096, args.steps, mix=(t, t, t, t))
+            if args.profile_block_batch:
+                r = block_batch_run(args.ctx2 or 4096, args.profile_block_batch, args.steps, mix=(t, t, t, t))
+            else:
+                r = block_run(args.ctx2 or 4096, args.steps, mix=(t, t, t, t))
             log(f"[bench] profile formats: {GGUF_NAMES[t]} {r}")
         return 0
     if args.profile_block_batch:
