@@ -164,6 +164,14 @@ def test_block_batch_c3_codebook_formats_and_q2_k(t):
     _run_batch(c, 3072, 1100, 1000, 16, (t, t, t, t), seed=1670 + t, what=f"C3 {NAMES[t]}", batched=True)
 
 
+@pytest.mark.parametrize("t", [gp.GGML_Q4_K, gp.GGML_IQ2_S], ids=["q4_k", "iq2_s"])
+def test_block_batch_at_the_widest_embedding(t):
+    """dim 16384: the token-batched projections stage 64 KB of norm weights in LDS (with
+    IQ2_S's codebook and tables beside them)."""
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    _run_batch(c, 16384, 64, 40, 6, (t, t, t, t), seed=1690 + t, what=f"{NAMES[t]} width 16384", batched=True)
+
+
 @pytest.mark.parametrize("K,ctx", [(4, 4096), (16, 4096), (4, 32768), (16, 32768)])
 def test_block_batch_c3_q4_k_m(K, ctx):
     """C3 shape (24/8/128, dim 3072) with the Q4_K_M mix (Q4_K q, k, o; Q6_K v): K draft

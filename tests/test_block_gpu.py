@@ -34,19 +34,20 @@ def _tensor(t, rows, cols, rng, scale=0.05):
     return hfp.GgufTensor(t, rows, cols, wb.reshape(-1)), wb
 
 
-def _weights(c, dim, types, rng, merged=False, bias=False, post=False, pre=True):
-    """types: (tq, tk, tv, to).  Returns (TransformerLayerWeights, orc.BlockWeights)."""
+def _weights(c, dim, types, rng, merged=False, bias=False, post=False, pre=True, qkv_scale=0.05):
+    """types: (tq, tk, tv, to); qkv_scale: the Q/K/V weights' magnitude.  Returns
+    (TransformerLayerWeights, orc.BlockWeights)."""
     qd, kvd = c.q_dim, c.kv_dim
     tq, tk, tv, to = types
     lw = hfp.TransformerLayerWeights()
     bw = orc.BlockWeights(dim)
     if merged:
-        t, wb = _tensor(tq, qd + 2 * kvd, dim, rng)
+        t, wb = _tensor(tq, qd + 2 * kvd, dim, rng, qkv_scale)
         lw.wqkv, bw.wqkv, bw.wqkv_type = t, wb, tq
     else:
-        lw.wq, bw.wq = _tensor(tq, qd, dim, rng)
-        lw.wk, bw.wk = _tensor(tk, kvd, dim, rng)
-        lw.wv, bw.wv = _tensor(tv, kvd, dim, rng)
+        lw.wq, bw.wq = _tensor(tq, qd, dim, rng, qkv_scale)
+        lw.wk, bw.wk = _tensor(tk, kvd, dim, rng, qkv_scale)
+        lw.wv, bw.wv = _tensor(tv, kvd, dim, rng, qkv_scale)
         bw.wq_type, bw.wk_type, bw.wv_type = tq, tk, tv
     lw.wo, bw.wo = _tensor(to, dim, qd, rng)
     bw.wo_type = to
@@ -157,6 +158,19 @@ def test_block_weight_formats_at_width_4096(t):
     units."""
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
     _run(c, 4096, 64, 33, 1, (t, t, t, t), seed=900 + t, what=f"{NAMES[t]} width 4096")
+
+
+@pytest.mark.parametrize("t", [gp.GGML_F32, gp.GGML_Q8_0, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_IQ2_S],
+                         ids=["f32", "q8_0", "q4_k", "q6_k", "iq2_s"])
+def test_block_weight_formats_at_the_widest_embedding(t):
+    """dim 16384, the widest llmp_block_config accepts: the Q/K/V projections stage 64 KB of
+    input in LDS, plus the chunk sums (Q4_K), the per-row scale tables (Q4_K, Q6_K, IQ2_S) and
+    the codebook (IQ2_S); F32 and Q8_0 rows take several batches of unit rounds.  The Q/K/V weights are half the usual magnitude, so that
+    the 16384-term projections land at the magnitudes of the 4096-wide tests (and their fp32
+    reordering error with them)."""
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    w = _weights(c, 16384, (t, t, t, t), np.random.default_rng(950 + t), qkv_scale=0.025)
+    _run(c, 16384, 64, 33, 1, (t, t, t, t), seed=950 + t, what=f"{NAMES[t]} width 16384", weights=w)
 
 
 @pytest.mark.parametrize("dim", [2048, 3072, 8192])
