@@ -655,7 +655,7 @@ struct PIQ2_S {
     static constexpr bool MIN = false, HALVES = true;
     static constexpr PartPair pairs[4] = {{0, 0}, {0, 1}, {1, 0}, {1, 1}};
     static __device__ __forceinline__ const void* grid_src() { return gk::kIq2sGrid; }
-    struct Raw { unsigned q[4], s[4]; uint4 side; unsigned short d; int h; };   // side: scales[8], qh[8]
+    struct Raw { unsigned q[4], s[4]; uint2 sc, qh; unsigned short d; int h; };   // 24-byte stride: 8-byte loads
     static __device__ __forceinline__ void load(Raw& r, const WPlanes& w, int row, int ch, int kq, int ng) {
         const unsigned sb = (unsigned)(ch >> 1);
 #pragma unroll
@@ -664,20 +664,21 @@ struct PIQ2_S {
             r.q[gi] = ldo<unsigned char>(rp(w, 0, row), u);
             r.s[gi] = ldo<unsigned char>(rp(w, 1, row), u);
         }
-        r.side = ldo<uint4>(rp(w, 2, row), sb * 24u);
+        r.sc = ldo<uint2>(rp(w, 2, row), sb * 24u);
+        r.qh = ldo<uint2>(rp(w, 2, row), sb * 24u + 8u);
         r.d = ldo<unsigned short>(rp(w, 2, row), sb * 24u + 16u);
         r.h = ch & 1;
     }
     static __device__ __forceinline__ void table(const Raw& r, float* tab, int m, int kq, int ch) {
         const int g = 4 * (ch & 1) + kq;
-        const unsigned b = ((g < 4 ? r.side.x : r.side.y) >> (8 * (g & 3))) & 0xFFu;
+        const unsigned b = ((g < 4 ? r.sc.x : r.sc.y) >> (8 * (g & 3))) & 0xFFu;
         const float d = h2f(r.d);
         reinterpret_cast<float2*>(tab + m * TAB)[kq] =
             make_float2((d * (0.5f + (float)(b & 15u))) * 0.25f, (d * (0.5f + (float)(b >> 4))) * 0.25f);
     }
     static __device__ __forceinline__ void afrag(const Raw& r, int gi, uint4 (&a)[NA], int kq) {
         const uint2* g = reinterpret_cast<const uint2*>(codebook_lds<GRID_BYTES>());
-        const unsigned qh = ((r.h ? r.side.w : r.side.z) >> (8 * gi)) & 0xFFu;   // qh[4h + gi]
+        const unsigned qh = ((r.h ? r.qh.y : r.qh.x) >> (8 * gi)) & 0xFFu;   // qh[4h + gi]
         const uint2 e = g[r.q[gi] | (((qh >> (2 * kq)) & 3u) << 8)];
         const uint4 u = signed_grid8(e.x, e.y, r.s[gi]);
         const uint4 z = make_uint4(0u, 0u, 0u, 0u);
