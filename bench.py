@@ -569,12 +569,14 @@ def block_run(ctx: int, steps: int, n_layers: int = 28, q8_input: bool = False,
             "kv_bytes_per_layer": kv_bytes(ctx), "layers_rotated": n_layers}
 
 
-def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28, mix="q4_k_m") -> dict:
+def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28, mix="q4_k_m",
+                    q8_input: bool = False) -> dict:
     """The attention half of a C3 layer (as block_run; default the Q4_K_M mix, or a MIXES key,
     or four GGML types) for K draft tokens at positions ctx-K .. ctx-1 in one
     llmp_attn_block_batch call (projection weights read once for the K tokens), against K
     single-token llmp_attn_block calls over the same layers; graph replays over n_layers
-    layers with their own weights and caches."""
+    layers with their own weights and caches.  q8_input: the Q8_1 input mode (the reference
+    GPU's int8 matvecs for the routed types, in both the batched and the single-token calls)."""
     from llmplayer_amd import _lib
     from llmplayer_amd import hip_forward_pass as hfp
     dim = 3072
@@ -587,7 +589,7 @@ def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28, mix="q4_k_
         vc = rng.standard_normal((ctx - K, c.kv_dim), dtype=np.float32)
         for layer in range(n_layers):
             fp.kv.write(layer, 0, kc, vc)
-        fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_F32)
+        fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_Q8_1 if q8_input else _lib.LLMP_INPUT_F32)
         wbytes = 0
         for layer in range(n_layers):
             lw = hfp.TransformerLayerWeights(attnNorm=np.ones(dim, np.float32))
@@ -621,7 +623,7 @@ def block_batch_run(ctx: int, K: int, steps: int, n_layers: int = 28, mix="q4_k_
         fp.close()
     us_b = ms_b / steps * 1e3
     us_s = ms_s / max(1, steps // 4) * 1e3
-    return {"K": K, "ctx": ctx, "weights": label, "dim": dim,
+    return {"K": K, "ctx": ctx, "weights": label, "dim": dim, "input": "Q8_1" if q8_input else "fp32",
             "us_per_call": round(us_b, 2), "us_per_token": round(us_b / K, 2),
             "single_token_blocks_us": round(us_s, 2), "speedup_vs_single_token_blocks": round(us_s / us_b, 2),
             "weight_bytes_per_layer": wbytes, "kv_bytes_per_layer": kv_bytes(ctx - K),
@@ -896,7 +898,7 @@ def main() -> int:
             log(f"[bench] profile formats: {GGUF_NAMES[t]} {r}")
         return 0
     if args.profile_block_batch:
-        r = block_batch_run(args.ctx2 or 4096, args.profile_block_batch, args.steps)
+        r = block_batch_run(args.ctx2 or 4096, args.profile_block_batch, args.steps, q8_input=args.block_q8)
         log(f"[bench] profile block batch: {r}")
         return 0
     if args.profile_verify:
@@ -978,6 +980,10 @@ def main() -> int:
             log(f"[bench] attention block, {K} tokens at ctx {ctx_b}: {r['us_per_call']} us/call "
                 f"({r['single_token_blocks_us']} us as {K} single-token blocks)")
             block_batch.append(r)
+        r = block_batch_run(4096, 16, 40, 28, q8_input=True)
+        log(f"[bench] attention block, 16 tokens at ctx 4096, Q8_1 input: {r['us_per_call']} us/call "
+            f"({r['single_token_blocks_us']} us as 16 single-token blocks)")
+        block_batch.append(r)
 
     q8_prefill = q8_verify = None
     if args.q8 and args.prefill:

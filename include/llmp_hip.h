@@ -406,8 +406,10 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
  * of two that brings the largest below 2^15 (a small first kernel computes it with each token's
  * RMSNorm factor), the outputs by its inverse.  The attention is llmp_attn_prefill_f32's (the
  * appended rows bit-identical to single-token appends of the same projections).  In the
- * LLMP_INPUT_Q8_1 mode, at head_dim 80 (no prefill kernel), for layers whose fp32 or bf16
- * weights reach 65504, the tokens run one llmp_attn_block call each.  The call may grow the
+ * LLMP_INPUT_Q8_1 mode the routed types take each token's Q8_1 input as llmp_attn_block
+ * forms it (the same staged norm and quantiser) and exact integer block dots on the matrix
+ * cores, and Wo the quantised attention output.  At head_dim 80 (no prefill kernel) and for
+ * layers whose fp32 or bf16 weights reach 65504, the tokens run one llmp_attn_block call each.  The call may grow the
  * handle's prefill workspace, as llmp_attn_prefill_f32 does (not for use under graph capture
  * then). */
 int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, uint64_t x,

@@ -144,7 +144,16 @@ hipError_t launch_tok_prep(const float* x, long long x_pitch, int cols, const fl
                            float* sc, int n_tokens, hipStream_t stream);
 bool proj_tok_supported(int ggml_type);
 bool proj_tok_pair_supported(int first_type, int second_type);
-hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_type,
+// q8: the types the reference GPU runs on its Q8_1 input (proj_tok_q8_routed) take the staged
+// quants of a.q8b / q8d / q8s (launch_tok_q8); the others keep the fp32 input.
+hipError_t launch_proj_tok(const tk::ProjTokArgs& a, int first_type, int second_type, bool q8,
                            hipStream_t stream);
+bool proj_tok_q8_routed(int ggml_type);
+// The Q8_1 input of n_tokens rows for the int8 formats (tk::tok_q8_kernel): the single-token
+// kernel's staged norm and quantiser, written in the B-operand layout (q8b: cols/32 * 64
+// uint4, q8d and q8s: cols/32 * kTokBatch floats), kTokBatch slots (zeros past n_tokens); with
+// sc, also launch_tok_prep's per-token factors.
+hipError_t launch_tok_q8(const float* x, long long x_pitch, int cols, const float* norm_w, float eps,
+                         int n_tokens, void* q8b, float* q8d, float* q8s, float* sc, hipStream_t stream);
 
 }  // namespace llmp

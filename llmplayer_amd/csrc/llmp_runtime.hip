@@ -1110,7 +1110,7 @@ int llmp_layer_norm_mode(uint64_t handle, int layer, int mode) {
 // Byte offsets of the token-batched block scratch: q, k, v, the attention output and the
 // output projection of kTokBatch tokens (each region 256-byte aligned).
 struct BatchLayout {
-    size_t q, k, v, attn, o, sc, total;
+    size_t q, k, v, attn, o, sc, q8b, q8d, q8s, total;
 };
 static BatchLayout batch_layout(const KvHandle* kv, int qd, int kvd) {
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
@@ -1122,7 +1122,12 @@ static BatchLayout batch_layout(const KvHandle* kv, int qd, int kvd) {
     L.attn = L.v + al((size_t)kTokBatch * kvd * sizeof(float));
     L.o = L.attn + al((size_t)kTokBatch * qd * sizeof(float));
     L.sc = L.o + al((size_t)kTokBatch * dim * sizeof(float));
-    L.total = L.sc + al((size_t)kTokBatch * 2 * sizeof(float));
+    // the Q8_1 staging of the widest projection input (dim for Q/K/V, q_dim for Wo)
+    const size_t groups = (size_t)(dim > qd ? dim : qd) / 32;
+    L.q8b = L.sc + al((size_t)kTokBatch * 2 * sizeof(float));
+    L.q8d = L.q8b + al(groups * 64 * 16);
+    L.q8s = L.q8d + al(groups * kTokBatch * sizeof(float));
+    L.total = L.q8s + al(groups * kTokBatch * sizeof(float));
     return L;
 }
 
@@ -1418,9 +1423,10 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
     const bool w_ok = W[LLMP_W_O].tok_ok && (merged ? W[LLMP_W_QKV].tok_ok
                                                      : W[LLMP_W_Q].tok_ok && W[LLMP_W_K].tok_ok &&
                                                            W[LLMP_W_V].tok_ok);
-    if (kv->blk_input == LLMP_INPUT_Q8_1 || prefill_tile_keys(D) <= 0 || !w_ok) {
-        // the Q8_1 contract's int8 dot products, a head size with decode kernels only, fp32 /
-        // bf16 weights beyond fp16's range, or a type without a token-batched kernel
+    const bool q8 = kv->blk_input == LLMP_INPUT_Q8_1;
+    if (prefill_tile_keys(D) <= 0 || !w_ok) {
+        // a head size with decode kernels only, fp32 / bf16 weights beyond fp16's range, or a
+        // type without a token-batched kernel
         for (int t = 0; t < n_tokens; ++t)
             if (int rc = enqueue_block(kv, layer, pos0 + t, 0, x + (uint64_t)t * dim * sizeof(float), 0,
                                        stream))
@@ -1444,6 +1450,9 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
     float* attn = reinterpret_cast<float*>(base + L.attn);
     float* ob = reinterpret_cast<float*>(base + L.o);
     float* sc = reinterpret_cast<float*>(base + L.sc);
+    void* q8b = base + L.q8b;
+    float* q8d = reinterpret_cast<float*>(base + L.q8d);
+    float* q8s = reinterpret_cast<float*>(base + L.q8s);
     hipStream_t st = pick_stream(stream);
     auto vecp = [&](int slot) -> const float* { return static_cast<const float*>(W[slot].mem); };
 
@@ -1483,8 +1492,13 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
         float* xc = xp + (size_t)t0 * dim;
         // 1-2. The tokens' pre-norm factors and input range exponents, then the Q/K/V
         //      projections of the normalised inputs.
-        LLMP_HIP_CHECK(launch_tok_prep(xc, dim, dim, vecp(LLMP_W_ATTN_NORM), c.eps, sc, K, st),
-                       "batched block input prep launch");
+        // In the Q8_1 mode the tokens' quantised inputs come with the same factors.
+        if (q8)
+            LLMP_HIP_CHECK(launch_tok_q8(xc, dim, dim, vecp(LLMP_W_ATTN_NORM), c.eps, K, q8b, q8d, q8s, sc, st),
+                           "batched block Q8_1 input launch");
+        else
+            LLMP_HIP_CHECK(launch_tok_prep(xc, dim, dim, vecp(LLMP_W_ATTN_NORM), c.eps, sc, K, st),
+                           "batched block input prep launch");
         if (paired || t2 == -1) {
             tk::ProjTokArgs g{};
             for (int k = 0; k < 3; ++k) {
@@ -1500,7 +1514,10 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
             g.norm_w = vecp(LLMP_W_ATTN_NORM);
             g.tok_sc = sc;
             g.eps = c.eps;
-            LLMP_HIP_CHECK(launch_proj_tok(g, t1, paired ? t2 : -1, st), "batched block Q/K/V projection launch");
+            g.q8b = static_cast<const uint4*>(q8b);
+            g.q8d = q8d;
+            g.q8s = q8s;
+            LLMP_HIP_CHECK(launch_proj_tok(g, t1, paired ? t2 : -1, q8, st), "batched block Q/K/V projection launch");
         } else {
             for (int i = 0; i < 3;) {
                 int n = 1;
@@ -1521,7 +1538,10 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
                 g.norm_w = vecp(LLMP_W_ATTN_NORM);
                 g.tok_sc = sc;
                 g.eps = c.eps;
-                LLMP_HIP_CHECK(launch_proj_tok(g, types[i], -1, st), "batched block Q/K/V projection launch");
+                g.q8b = static_cast<const uint4*>(q8b);
+                g.q8d = q8d;
+                g.q8s = q8s;
+                LLMP_HIP_CHECK(launch_proj_tok(g, types[i], -1, q8, st), "batched block Q/K/V projection launch");
                 i += n;
             }
         }
@@ -1543,18 +1563,26 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
         g.x_pitch = qd;
         g.in_range = kv->range(layer);   // |attention output| <= the largest stored |V|
         g.in_range_n = kv->n_kv_heads;
+        const bool wo_q8 = q8 && proj_tok_q8_routed(W[LLMP_W_O].type);
+        if (wo_q8) {   // the attention output quantised, as the single-token kernel does
+            LLMP_HIP_CHECK(launch_tok_q8(attn, qd, qd, nullptr, 0.0f, K, q8b, q8d, q8s, nullptr, st),
+                           "batched block Q8_1 attention-output launch");
+            g.q8b = static_cast<const uint4*>(q8b);
+            g.q8d = q8d;
+            g.q8s = q8s;
+        }
         const float* post = vecp(LLMP_W_POST_ATTN_NORM);
         if (post) {
             g.seg[0].out = ob;
             g.seg[0].out_pitch = dim;
-            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, -1, st), "batched block output projection launch");
+            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, -1, wo_q8, st), "batched block output projection launch");
             LLMP_HIP_CHECK(launch_post_norm_residual(ob, post, c.eps, kv->blk_rscale, xc, dim, K, st),
                            "batched block post-norm launch");
         } else {
             g.resid = xc;
             g.resid_pitch = dim;
             g.rscale = kv->blk_rscale;
-            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, -1, st), "batched block output projection launch");
+            LLMP_HIP_CHECK(launch_proj_tok(g, W[LLMP_W_O].type, -1, wo_q8, st), "batched block output projection launch");
         }
     }
     return LLMP_OK;

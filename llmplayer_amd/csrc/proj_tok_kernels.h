@@ -91,6 +91,12 @@ struct ProjTokArgs {
     float* resid;          // Wo epilogue: resid[t*resid_pitch + row] += rscale? * value
     long long resid_pitch;
     float rscale;          // Granite residual scale, 0 = off
+    // The Q8_1 input of the int8 formats (Q8In<...>, tok_q8_kernel): per 32-column group g and
+    // lane l = 16 kq + t, q8b[64 g + l] = the 8 quants of token t at columns 32 g + 8 kq .. +7
+    // as fp16, q8d[16 g + t] / q8s[16 g + t] the block's scale and sum.
+    const uint4* q8b;
+    const float* q8d;
+    const float* q8s;
 };
 
 // Two fp32 values -> packed fp16, round to nearest even (v_cvt_pk_f16_f32).
@@ -130,6 +136,25 @@ __device__ __forceinline__ void split8(const float (&v)[8], uint4& hi, uint4& lo
 // from the table, for output rows 4*(l/16)+i.
 struct PartPair {
     int a, b;
+};
+
+// A format on the Q8_1 input (LLMP_INPUT_Q8_1: the reference GPU's int8 matvecs,
+// CudaForwardPass.java:216-226, 1998-2037): the same weight integers as its A operand, the
+// token's int8 quants (exact in fp16) as the B operand, one MFMA per A part giving the exact
+// integer dot of each 32-value block (16 for the halves formats), scaled as the reference's
+// dp4a kernels do: ((d*sc) * d_x) * dot - (dmin*m) * s_x per block (the min term for Q4_K and
+// Q5_K), (d_s * d_x) * dot per block or half otherwise.
+template <class P>
+struct Q8In : P {
+    static constexpr bool Q8B = true;
+};
+template <class F, class = void>
+struct IsQ8B {
+    static constexpr bool value = false;
+};
+template <class F>
+struct IsQ8B<F, std::void_t<decltype(F::Q8B)>> {
+    static constexpr bool value = F::Q8B;
 };
 
 // Q4_K: chunk = half a super-block (sub-blocks 4h..4h+3, h = ch%2): nibble bytes 64h + 32p +
@@ -836,6 +861,96 @@ __global__ __launch_bounds__(NTHR) void tok_prep_kernel(const float* x, long lon
     }
 }
 
+// The Q8_1 input of K tokens for the int8 formats (Q8In<...>), one workgroup per token slot
+// t < kTok.  Token t < n_tokens: with norm weights w, the staged RMSNorm of the single-token
+// projection kernel bit for bit (thread i sums the squares of chunks i, i + NTHR, ... with fmaf,
+// each wave's partials by row_group_sum, the waves' in order; r = 1/(float)sqrt((double)(sum/cols
+// + eps)); (x*r)*w per value), or x as it is without; then gk::put_q8 per block of 32 into LDS
+// (the single-token kernel's quantiser); then the quants as fp16 into q8b in the B-operand
+// layout, the block scales and sums into q8d and q8s.  Slots t >= n_tokens get zeros.  With sc,
+// also sc[2t] = r and sc[2t + 1] = the range exponent of max|x*w| (for the fp32-input rows of a
+// launch pairing an int8 format with Q6_K).  cols % 32 == 0, cols <= kMaxGemvCols.
+template <int NTHR>
+__global__ __launch_bounds__(NTHR) void tok_q8_kernel(const float* x, long long x_pitch, int cols,
+                                                      const float* w, float eps, int n_tokens,
+                                                      uint4* q8b, float* q8d, float* q8s, float* sc) {
+    static_assert(NTHR == 256, "the single-token kernel's staging: 4 waves of partial sums");
+    extern __shared__ unsigned char s_q[];             // the quants, cols bytes
+    __shared__ float s_d[gk::kMaxGemvCols / 32], s_s[gk::kMaxGemvCols / 32];
+    __shared__ float red[NTHR / 64];
+    __shared__ unsigned redm[NTHR / 64];
+    const int tid = threadIdx.x, t = blockIdx.x, lane = tid & 63;
+    const int n4 = cols >> 2, ng = cols >> 5;
+    if (t >= n_tokens) {
+        for (int i = tid; i < 4 * ng; i += NTHR) q8b[64 * (i >> 2) + 16 * (i & 3) + t] = make_uint4(0u, 0u, 0u, 0u);
+        for (int g = tid; g < ng; g += NTHR) {
+            q8d[16 * g + t] = 0.0f;
+            q8s[16 * g + t] = 0.0f;
+        }
+        return;
+    }
+    const float4* xt = reinterpret_cast<const float4*>(x + (long long)t * x_pitch);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    const bool norm = w != nullptr;
+    float ss = 0.0f;
+    unsigned mb = 0;
+    for (int c = tid; c < n4; c += NTHR) {
+        const float4 v = xt[c];
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+        const float4 b = norm ? w4[c] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        mb = max(mb, max(max(dk::abs_bits(v.x * b.x), dk::abs_bits(v.y * b.y)),
+                         max(dk::abs_bits(v.z * b.z), dk::abs_bits(v.w * b.w))));
+    }
+    ss = dk::row_group_sum<64>(ss);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mb = max(mb, (unsigned)__shfl_xor((int)mb, off));
+    if (lane == 0) {
+        red[tid >> 6] = ss;
+        redm[tid >> 6] = mb;
+    }
+    __syncthreads();
+    float r = 1.0f;
+    if (norm) {
+        float tot = red[0];
+#pragma unroll
+        for (int k = 1; k < NTHR / 64; ++k) tot = tot + red[k];
+        float q = tot / (float)cols;
+        q = q + eps;
+        r = 1.0f / (float)__builtin_sqrt((double)q);
+    }
+    if (sc != nullptr && tid == 0) {
+        unsigned m = redm[0];
+#pragma unroll
+        for (int k = 1; k < NTHR / 64; ++k) m = max(m, redm[k]);
+        sc[2 * t] = r;
+        sc[2 * t + 1] = (float)dk::range_exp_of_bits(m);
+    }
+    // quantise: the 8 lanes of a block call put_q8 together (cols % 32 == 0)
+    for (int c = tid; c < n4; c += NTHR) {
+        const float4 v = xt[c];
+        gk::put_q8(c, norm ? gk::scale4(v, r, w4[c]) : v, s_q, s_d, s_s);
+    }
+    __syncthreads();
+    // item i = 4 g + kq: the 8 quants at 32 g + 8 kq as fp16
+    for (int i = tid; i < 4 * ng; i += NTHR) {
+        const uint2 qb = *reinterpret_cast<const uint2*>(s_q + 8 * i);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = (float)(int)(signed char)((qb.x >> (8 * e)) & 0xFFu);
+            v[4 + e] = (float)(int)(signed char)((qb.y >> (8 * e)) & 0xFFu);
+        }
+        q8b[64 * (i >> 2) + 16 * (i & 3) + t] = f16x8_of(v);
+    }
+    for (int g = tid; g < ng; g += NTHR) {
+        q8d[16 * g + t] = s_d[g];
+        q8s[16 * g + t] = s_s[g];
+    }
+}
+
 // ---- the projection kernel ------------------------------------------------------------------
 __device__ __forceinline__ const TokSeg& tok_seg(const ProjTokArgs& a, int row_g) {
     const bool in1 = a.nseg > 1 && row_g >= a.seg[1].out_off;
@@ -845,10 +960,16 @@ __device__ __forceinline__ const TokSeg& tok_seg(const ProjTokArgs& a, int row_g
 
 // One wave's loads for one chunk: the raw weight bytes, and for each group the lane's 8 inputs
 // of token l%16 (columns 8*(l/16) .. +7 of the group) with their norm weights.
-template <class F>
+template <class F, bool Q8 = IsQ8B<F>::value>
 struct ChunkRegs {
     typename F::Raw raw;
     float4 x[kGroups][2];
+};
+template <class F>
+struct ChunkRegs<F, true> {   // the Q8_1 input: the quants as fp16, the block scales and sums
+    typename F::Raw raw;
+    uint4 b[kGroups];
+    float dx[kGroups], sx[kGroups];
 };
 
 template <class F, bool NORM>
@@ -858,14 +979,24 @@ __device__ __forceinline__ void chunk_issue(ChunkRegs<F>& c, const ProjTokArgs& 
     const int g0 = ch * kGroups;
     const int ng = min(kGroups, ngroups - g0);
     F::load(c.raw, w, row, ch, kq, ng);
-    // lanes of tokens past K load token K-1's row (no branch between the loads)
-    const float* xt = a.x + (long long)(tok_live ? t : a.K - 1) * a.x_pitch;
+    if constexpr (IsQ8B<F>::value) {   // token slots past K hold zeros (tok_q8_kernel)
 #pragma unroll
-    for (int gi = 0; gi < kGroups; ++gi) {
-        const int col = 32 * (g0 + min(gi, ng - 1)) + 8 * kq;
-        const float4* xp = reinterpret_cast<const float4*>(xt + col);
-        c.x[gi][0] = xp[0];
-        c.x[gi][1] = xp[1];
+        for (int gi = 0; gi < kGroups; ++gi) {
+            const int g = g0 + min(gi, ng - 1);
+            c.b[gi] = a.q8b[64 * g + lane];
+            c.dx[gi] = a.q8d[16 * g + t];
+            c.sx[gi] = a.q8s[16 * g + t];
+        }
+    } else {
+        // lanes of tokens past K load token K-1's row (no branch between the loads)
+        const float* xt = a.x + (long long)(tok_live ? t : a.K - 1) * a.x_pitch;
+#pragma unroll
+        for (int gi = 0; gi < kGroups; ++gi) {
+            const int col = 32 * (g0 + min(gi, ng - 1)) + 8 * kq;
+            const float4* xp = reinterpret_cast<const float4*>(xt + col);
+            c.x[gi][0] = xp[0];
+            c.x[gi][1] = xp[1];
+        }
     }
 }
 
@@ -882,6 +1013,31 @@ __device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& ac
 #pragma unroll
     for (int gi = 0; gi < kGroups; ++gi) {
         if (gi >= ng) break;   // uniform: a partial last chunk
+        if constexpr (IsQ8B<F>::value) {
+            static_assert(F::TAB > 0 && !(F::MIN && F::HALVES), "int8 formats carry a scale table");
+            uint4 af[F::NA];
+            F::afrag(c.raw, gi, af, kq);
+            const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+            const f32x4_t t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f8(af[0]), as_f8(c.b[gi]), z, 0, 0, 0);
+            f32x4_t t1 = z;
+            if constexpr (F::HALVES)
+                t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f8(af[1]), as_f8(c.b[gi]), z, 0, 0, 0);
+            const float dx = c.dx[gi], sx = c.sx[gi];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {   // output rows 4*kq + i, token lane%16
+                const float* tr = tab + (4 * kq + i) * F::TAB;
+                if constexpr (F::MIN) {            // Q4_K, Q5_K: (d*sc, dmin*m) of block gi
+                    const float2 f = reinterpret_cast<const float2*>(tr)[gi];
+                    acc[i] = acc[i] + ((f.x * dx) * t0[i] - f.y * sx);
+                } else if constexpr (F::HALVES) {  // Q3_K: d*(sc - 32) of the two halves
+                    const float2 f = reinterpret_cast<const float2*>(tr)[gi];
+                    acc[i] = acc[i] + ((f.x * dx) * t0[i] + (f.y * dx) * t1[i]);
+                } else {                           // Q8_0, Q5_0, IQ4_NL, IQ4_XS: the block's scale
+                    acc[i] = acc[i] + (tr[gi] * dx) * t0[i];
+                }
+            }
+            continue;
+        } else {
         // lanes of tokens past K hold token K-1's inputs: finite, and their outputs are never
         // stored.  Inputs times 2^-E: with the norm, the staged weights carry the factor.
         const float xv[8] = {c.x[gi][0].x, c.x[gi][0].y, c.x[gi][0].z, c.x[gi][0].w,
@@ -950,6 +1106,7 @@ __device__ __forceinline__ void chunk_consume(const ChunkRegs<F>& c, f32x4_t& ac
                 }
             }
         }
+        }
     }
     if constexpr (F::TAB > 0) __builtin_amdgcn_wave_barrier();   // table reads before its rewrite
 }
@@ -970,8 +1127,9 @@ __device__ __forceinline__ void wave_rows(const ProjTokArgs& a, const WPlanes& w
     ChunkRegs<F> ca, cb;
     if (n > 0) chunk_issue<F, NORM>(ca, a, w, row, chunk(0), ngroups, lane, tok_live);
     constexpr int GRID = gk::FmtGrid<F>::BYTES;   // codebook formats: the codebook to LDS
-    if constexpr (NORM || GRID > 0) {
-        if constexpr (NORM) {   // the norm weights times 2^-E to LDS once per workgroup, behind
+    constexpr bool STAGE_NW = NORM && !IsQ8B<F>::value;   // the Q8_1 input is normalised already
+    if constexpr (STAGE_NW || GRID > 0) {
+        if constexpr (STAGE_NW) {   // the norm weights times 2^-E to LDS once per workgroup, behind
                                 // the first loads ((x * w) * 2^-E = x * (w * 2^-E), exactly)
             const float4* src = reinterpret_cast<const float4*>(a.norm_w);
             for (int c4 = wave * 64 + lane; c4 < (a.cols >> 2); c4 += kThreads) {
@@ -1040,9 +1198,14 @@ void proj_tok_kernel(ProjTokArgs a) {
         float v = s_red[0][ln][i];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) v = v + s_red[w][ln][i];
+        // rows on the Q8_1 input carry its scales already (no 2^-E, normalised before quantising)
+        const bool first = std::is_same<F1, F2>::value || sg.fmt == 0;
+        const bool q8_rows = first ? IsQ8B<F1>::value : IsQ8B<F2>::value;
         if (tt < a.K) {
-            v = v * __uint_as_float((unsigned)(127 + E) << 23);   // the inputs were scaled by 2^-E
-            if constexpr (NORM) v = v * a.tok_sc[2 * tt];         // RMSNorm.apply's factor r
+            if (!q8_rows) {
+                v = v * __uint_as_float((unsigned)(127 + E) << 23);   // the inputs were scaled by 2^-E
+                if constexpr (NORM) v = v * a.tok_sc[2 * tt];         // RMSNorm.apply's factor r
+            }
             const int r = row0 - sg.out_off + rr;
             if (sg.bias != nullptr) v = v + sg.bias[r];
             if (a.resid != nullptr) {
