@@ -8,8 +8,8 @@ Each case draws, from a fixed seed (so every run checks the same cases):
   width of 1024-3072;
 - the architecture features: q/k/v/o biases, pre-norm or none, post-norm, merged QKV (one
   format), Granite's residual scale, per-head QK-norm (Qwen3, NEOX RoPE);
-- the call: single-token steps after a cached prefix, on the fp32 or the Q8_1 input, or one
-  K-token call of 1-20 tokens.
+- the call: single-token steps after a cached prefix or one K-token call of 1-20 tokens, on
+  the fp32 or the Q8_1 input.
 
 The combinations cross the projection kernels' format pairs and round counts, the input
 modes and the token-batched path with the decode and multi-token attention kernels.  The bars
@@ -59,7 +59,7 @@ def _draw(rng):
         "qk": bool(rng.random() < 0.3),
     }
     batched = bool(rng.random() < 0.4)
-    q8 = bool(not batched and rng.random() < 0.35)
+    q8 = bool(rng.random() < 0.35)
     pos0 = int(rng.integers(0, 300))
     k = int(rng.integers(1, 21))
     return types, tname, hkv * group, hkv, d, dim, flags, batched, q8, pos0, k
@@ -72,7 +72,7 @@ def _id(case):
     types, tname, hq, hkv, d, dim, flags, batched, q8, pos0, k = case
     on = "".join(c for c, f in (("b", flags["bias"]), ("p", flags["post"]), ("n", flags["pre"]),
                                 ("m", flags["merged"]), ("r", flags["rscale"] > 0), ("q", flags["qk"])) if f)
-    call = f"batch{k}" if batched else ("q8_1" if q8 else "tok")
+    call = (f"batch{k}" if batched else "tok") + ("-q8_1" if q8 else "")
     return f"{tname}-{hq}/{hkv}/{d}-dim{dim}-{on or 'none'}-{call}-p{pos0}"
 
 
@@ -91,6 +91,6 @@ def test_block_random(case):
     common = dict(merged=flags["merged"], bias=flags["bias"], post=flags["post"], pre=flags["pre"],
                   rscale=flags["rscale"], qk=qk)
     if batched:
-        tbb._run_batch(c, dim, pos0 + k + 8, pos0, k, types, seed=seed, what=_id(case), **common)
+        tbb._run_batch(c, dim, pos0 + k + 8, pos0, k, types, seed=seed, what=_id(case), q8=q8, **common)
     else:
         tbg._run(c, dim, pos0 + 10, pos0, 2, types, seed=seed, what=_id(case), q8=q8, **common)
