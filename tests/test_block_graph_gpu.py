@@ -5,7 +5,8 @@ replay, the state that the same call made eagerly on a twin handle leaves: the r
 and the cache rows bit for bit (the same kernels on the same inputs).  The single-token block
 reads its position from device memory (the reference's graph mode: CudaForwardPass.java:
 1760-1812, tokenParams updated between replays), so its replays step through positions; the
-K-token call repeats at a fixed position, its residual rows changing from replay to replay.
+K-token call (fp32 or Q8_1 input) repeats at a fixed position, its residual rows changing
+from replay to replay.
 Eager calls run between the replays, and every replay is checked."""
 import ctypes as C
 
@@ -22,8 +23,9 @@ pytestmark = pytest.mark.gpu
 F32 = np.float32
 
 
-def _twins(c, dim, max_seq, pos0, types, seed, K):
-    """Two handles with the same cache prefix, weights and residual rows."""
+def _twins(c, dim, max_seq, pos0, types, seed, K, q8=False):
+    """Two handles with the same cache prefix, weights and residual rows (q8: the Q8_1 input
+    mode)."""
     rng = np.random.default_rng(seed)
     lw, _ = tbg._weights(c, dim, types, rng, bias=True)
     kc = rng.standard_normal((pos0, c.kv_dim)).astype(F32)
@@ -33,7 +35,7 @@ def _twins(c, dim, max_seq, pos0, types, seed, K):
     for _ in range(2):
         fp = hfp.HipForwardPass(c, max_seq)
         fp.kv.write(0, 0, kc, vc)
-        fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_F32)
+        fp.setBlockConfig(dim, 0.0, _lib.LLMP_INPUT_Q8_1 if q8 else _lib.LLMP_INPUT_F32)
         fp.uploadLayerWeights(0, lw)
         fps.append(fp)
     return fps, x
@@ -81,13 +83,14 @@ def test_block_graph_at_device_positions_matches_eager_calls(types):
         eager.close()
 
 
-@pytest.mark.parametrize("types,K", [((gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K), 8),
-                                     ((gp.GGML_Q2_K,) * 4, 16), ((gp.GGML_F32,) * 4, 20)],
-                         ids=["q4_k_m-8", "q2_k-16", "f32-20"])
-def test_block_batch_graph_matches_eager_calls(types, K):
+@pytest.mark.parametrize("types,K,q8", [((gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K), 8, False),
+                                        ((gp.GGML_Q2_K,) * 4, 16, False), ((gp.GGML_F32,) * 4, 20, False),
+                                        ((gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K), 16, True)],
+                         ids=["q4_k_m-8", "q2_k-16", "f32-20", "q4_k_m-16-q8_1"])
+def test_block_batch_graph_matches_eager_calls(types, K, q8):
     c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
     pos0 = 150
-    (graphed, eager), x = _twins(c, 1024, 256, pos0, types, 43, K)
+    (graphed, eager), x = _twins(c, 1024, 256, pos0, types, 43, K, q8)
     try:
         for fp in (graphed, eager):
             fp.uploadXBatch(x)
