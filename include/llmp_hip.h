@@ -398,7 +398,8 @@ int llmp_attn_block(uint64_t handle, int layer, int position, uint64_t d_positio
 /* The attention half of n_tokens consecutive tokens (positions pos0 .. pos0+n_tokens-1) on the
  * device residual rows x (fp32 [n_tokens][dim], 16-byte aligned, updated in place): what
  * n_tokens llmp_attn_block calls compute, with each projection weight read once per group of
- * up to 16 tokens.  Replaces LLMEngine.forwardBatch's per-token attention halves
+ * up to 16 tokens (a group of one token runs the single-token call, which is faster for one
+ * token).  Replaces LLMEngine.forwardBatch's per-token attention halves
  * (LLMEngine.java:1019-1033), batched as docs/optimization/speculative-decoding.md:120-140
  * plans for the verification of K draft tokens.  The projections run on the matrix cores with
  * each fp32 input split into two fp16 parts (fp32-accurate products, fp32 sums in another order

@@ -1490,6 +1490,11 @@ int llmp_attn_block_batch(uint64_t handle, int layer, int pos0, int n_tokens, ui
     for (int t0 = 0; t0 < n_tokens; t0 += kTokBatch) {
         const int K = n_tokens - t0 < kTokBatch ? n_tokens - t0 : kTokBatch;
         float* xc = xp + (size_t)t0 * dim;
+        if (K == 1) {   // one token: the single-token launches are faster (27 against 49 µs at C3)
+            if (int rc = enqueue_block(kv, layer, pos0 + t0, 0, reinterpret_cast<uint64_t>(xc), 0, stream))
+                return rc;
+            continue;
+        }
         // 1-2. The tokens' pre-norm factors and input range exponents, then the Q/K/V
         //      projections of the normalised inputs.
         // In the Q8_1 mode the tokens' quantised inputs come with the same factors.

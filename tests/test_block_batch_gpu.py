@@ -69,7 +69,7 @@ def _compare_block(got, want, what):
 
 def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=False,
                post=False, pre=True, rscale=0.0, qk=None, q8=False, sinks=None, layer=0,
-               rounds=1, batched=False, per_token=False):
+               rounds=1, batched=False, per_token=False, single_tail=False):
     """`rounds` batched calls of K tokens each, from position pos0 on layer `layer` of c, each
     token checked against sequential orc.attn_block calls.  per_token: check that the calls ran
     one single-token decode per token.  batched: also check that the calls
@@ -92,7 +92,7 @@ def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=F
         fp.kv.write(layer, 0, kc, vc)
         fp.setBlockConfig(dim, rscale, _lib.LLMP_INPUT_Q8_1 if q8 else _lib.LLMP_INPUT_F32)
         fp.uploadLayerWeights(layer, lw)
-        if batched or per_token:
+        if batched or per_token or single_tail:
             _lib.call("llmp_profile_enable", fp.kv.handle, 1)
         worst = 0.0
         p0 = pos0
@@ -126,6 +126,12 @@ def _run_batch(c, dim, max_seq, pos0, K, types, seed, what, merged=False, bias=F
             n, ms = C.c_int(), C.c_double()
             _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(n), C.byref(ms))
             assert n.value == rounds * K, f"{what}: {n.value} single-token decode launches"
+        if single_tail:   # groups of 16 batched, a last group of one token single
+            n, ms = C.c_int(), C.c_double()
+            _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(n), C.byref(ms))
+            assert n.value == rounds * (K % 16 == 1), f"{what}: {n.value} single-token decode launches"
+            _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_PREFILL_ATTN, C.byref(n), C.byref(ms))
+            assert n.value >= rounds * (K // 16), f"{what}: {n.value} multi-token attention launches"
         if batched:
             n, ms = C.c_int(), C.c_double()
             _lib.call("llmp_profile_read", fp.kv.handle, _lib.LLMP_PROF_DECODE_SPLIT, C.byref(n), C.byref(ms))
@@ -234,6 +240,28 @@ def test_block_batch_qk_norm_qwen3():
     qk = (rng.uniform(0.5, 1.5, 128).astype(F32), rng.uniform(0.5, 1.5, 128).astype(F32))
     _run_batch(c, 1024, 128, 50, 9, (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K),
                seed=1760, what="qwen3 qk-norm", qk=qk)
+
+
+@pytest.mark.parametrize("q8", [False, True], ids=["fp32", "q8_1"])
+def test_block_batch_of_one_token_is_the_single_token_call(q8):
+    """A group of one token runs the single-token launches (faster than the batched ones for one
+    token): one-token llmp_attn_block_batch equals llmp_attn_block bit for bit, and 17 tokens
+    take one batched group of 16 and one single-token call."""
+    from tests.test_block_graph_gpu import _twins, _same
+    c = hfp.ModelConfig(8, 2, 128, 1, rope_freq_base=500000.0)
+    types = (gp.GGML_Q4_K, gp.GGML_Q4_K, gp.GGML_Q6_K, gp.GGML_Q4_K)
+    (a, b), x = _twins(c, 1024, 256, 100, types, 51, 1, q8)
+    try:
+        a.uploadXBatch(x)
+        a.forwardAttentionBlockBatch(0, 100, 1)
+        b.uploadX(x[0])
+        b.forwardAttentionBlock(0, 100)
+        _same(a, b, a.downloadXBatch(1)[0], b.downloadX(), 101, "one-token batch")
+    finally:
+        a.close()
+        b.close()
+    _run_batch(c, 1024, 256, 60, 17, types, seed=1790 + int(q8), what=f"17 tokens ({'q8_1' if q8 else 'fp32'})",
+               q8=q8, single_tail=True)
 
 
 Q8_1_BATCH = [gp.GGML_Q4_K, gp.GGML_Q8_0, gp.GGML_Q5_0, gp.GGML_Q3_K, gp.GGML_Q5_K, gp.GGML_IQ4_NL,
