@@ -1,5 +1,5 @@
-"""CPU checks of the Java (Panama FFM) binding a maintainer adds on the reference side, as
-INTEGRATION.md prints it: every `h("llmp_...", ...)` downcall descriptor against the prototype in
+"""CPU checks of the Java (Panama FFM) binding a maintainer adds on the reference side, as the
+repository's integration guide (DOC below) prints it: every `h("llmp_...", ...)` downcall descriptor against the prototype in
 include/llmp_hip.h, every `NAME.invokeExact(...)` call against its descriptor's arity, and the
 Java `kernelGroup` table against the Python mirror's.  No JDK is in this image, so the Java text
 itself is what is checked."""
